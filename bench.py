@@ -1,0 +1,189 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X decode/prefill path (BASELINE config 2 by default).
+
+Workload (one GPU): the Qwen3.5-0.8B-shaped hybrid with random-init fp32
+weights (N(0, 0.02), seed 0), a 454-token uniform random prompt (seed 4),
+greedy decode. A step is one decode forward (one token) including the device
+argmax readback, as the reference times `step_greedy` (src/device/cli.rs:797-812).
+`--warmup` untimed steps, then exactly `--steps` timed steps bracketed by a
+stream synchronisation on both sides. value = decode tokens/s at ctx 454.
+
+Also reported: weight-read HBM GB/s of the decode step; the prefill rate of
+the prompt; with --prefill, the 2644-token prefill (config 3); with --long,
+decode at ctx 8192 (config 4). roofline: the fp32 decode GEMV (every
+projection of a step, lm_head included) timed with hipEvent pairs on the
+bridge's stream in a profiled pass of the same decode; cpu_baseline: the
+CPU oracle (restatement of the reference's Backend::Vector path) on a bounded
+sample on this host.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+for p in (str(ROOT / "qwen-rust-inference_amd"), str(ROOT / "oracle")):
+    if p not in sys.path:
+        sys.path.insert(0, p)
+
+HBM_PEAK_GBS = 8000.0
+METRIC = "decode tok/s @ctx 454 & 8192 + HBM GB/s; prefill tok/s @2644"
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def gemv_bytes(label: str) -> int:
+    """Weight bytes one profiled fp32 GEMV call reads, from its label
+    ("gemv_f32 248320x1024", "gemv_f32_group 6144x1024+2048x1024", "..._glu 2x3584x1024")."""
+    body = label.split(" ", 1)[1].split(" t")[0]
+    total = 0
+    mult = 1
+    if body.startswith("2x"):
+        mult, body = 2, body[2:]
+    for part in body.split("+"):
+        r, c = part.split("x")
+        total += int(r) * int(c) * 4
+    return total * mult
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=128)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--prompt", type=int, default=454)
+    ap.add_argument("--prefill", action="store_true", help="also time the 2644-token prefill (config 3)")
+    ap.add_argument("--long", action="store_true", help="also time decode at ctx 8192 (config 4)")
+    ap.add_argument("--cpu-steps", type=int, default=6, help="oracle steps of the CPU baseline sample (0: skip)")
+    ap.add_argument("--profile-steps", type=int, default=16)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
+              "the path's sharding is described in DESIGN.md", file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+
+    import __graft_entry__
+    if not __graft_entry__._built():
+        __graft_entry__.build()
+    from qwen_mi355x import engine as E
+    from qwen_mi355x import model as M
+
+    c = M.config_qwen08b(max_positions=16384)
+    t0 = time.time()
+    w = M.synthetic_weights(c, seed=0)
+    log(f"weights synthesised in {time.time() - t0:.1f} s ({w.matrix_bytes() / 1e9:.3f} GB of matrices)")
+    model = E.Model(w)
+    log(model.info)
+    model.set_run_budget(64 << 30)
+    weight_bytes = w.matrix_bytes()
+    prompt = [int(v) for v in np.random.default_rng(4).integers(0, c.vocab_size, args.prompt)]
+
+    # prefill of the prompt (one chunk), then decode
+    cap = args.prompt + args.warmup + args.steps + args.profile_steps + 4
+    run = model.new_run(cap, chunk=args.prompt)
+    model.sync()
+    t = time.perf_counter()
+    logits = run.prefill(prompt)
+    prefill_s = time.perf_counter() - t
+    token = int(np.argmax(logits))
+    log(f"prefill {args.prompt} tokens: {prefill_s * 1e3:.1f} ms")
+    for _ in range(args.warmup):
+        token = run.step_greedy(token)
+    model.sync()
+    t = time.perf_counter()
+    ids, _ = run.decode_greedy(token, args.steps + 1)
+    model.sync()
+    decode_s = time.perf_counter() - t
+    token = ids[-1]
+    value = args.steps / decode_s
+    ms = decode_s / args.steps * 1e3
+    hbm = weight_bytes * value / 1e9
+    log(f"decode: {ms:.3f} ms/token, {value:.1f} tok/s, weight-read {hbm:.0f} GB/s ({hbm / HBM_PEAK_GBS:.1%} of peak)")
+
+    # roofline pass: the same decode with the bridge's event profiler on
+    model.profile(True)
+    run.decode_greedy(token, args.profile_steps + 1)
+    stats = model.profile_read()
+    model.profile(False)
+    gemv = {k: v for k, v in stats.items() if k.startswith("gemv_f32")}
+    gemv_bytes_total = sum(gemv_bytes(k) * v[0] for k, v in gemv.items())
+    gemv_ms = sum(v[1] for v in gemv.values())
+    launches = sum(v[0] for v in gemv.values())
+    achieved = gemv_bytes_total / (gemv_ms / 1e3) / 1e9
+    total_ms = sum(v[1] for v in stats.values())
+    for k, v in sorted(stats.items(), key=lambda kv: -kv[1][1])[:12]:
+        log(f"  {v[1] / args.profile_steps * 1e3:9.1f} us/step {v[0] // args.profile_steps:4d} calls/step  {k}")
+    roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                "kernel": "fp32 decode GEMV (gemv_kernel<F32,...>: every projection of a step, lm_head included)",
+                "bytes_per_step": gemv_bytes_total // args.profile_steps,
+                "launches_per_step": launches // args.profile_steps,
+                "gemv_us_per_step": round(gemv_ms / args.profile_steps * 1e3, 1),
+                "bridge_gpu_us_per_step": round(total_ms / args.profile_steps * 1e3, 1)}
+
+    out = {"metric": METRIC, "value": round(value, 2), "unit": "tok/s", "n_gpus": 1, "steps": args.steps,
+           "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak",
+           "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+           "config": {"workload": "config 2: Qwen3.5-0.8B-shaped hybrid, fp32 random-init weights, "
+                                  f"{args.prompt}-token prompt, batch-1 greedy decode",
+                      "prompt_tokens": args.prompt, "weights_seed": 0, "prompt_seed": 4,
+                      "weight_bytes_per_token": weight_bytes},
+           "hbm_weight_read_gbs": round(hbm, 1), "hbm_weight_read_frac": round(hbm / HBM_PEAK_GBS, 4),
+           f"prefill_{args.prompt}_tok_s": round(args.prompt / prefill_s, 1),
+           "roofline": roofline}
+
+    if args.prefill:
+        for n in (2644,):
+            ids2 = [int(v) for v in np.random.default_rng(2).integers(0, c.vocab_size, n)]
+            r2 = model.new_run(n + 1, chunk=n)
+            model.sync()
+            t = time.perf_counter()
+            r2.prefill(ids2)
+            dt = time.perf_counter() - t
+            out[f"prefill_{n}_tok_s"] = round(n / dt, 1)
+            log(f"prefill {n}: {dt * 1e3:.1f} ms, {n / dt:.0f} tok/s")
+            del r2
+    if args.long:
+        n = 8192
+        ids3 = [int(v) for v in np.random.default_rng(5).integers(0, c.vocab_size, n)]
+        r3 = model.new_run(n + 80, chunk=1024)
+        tok = int(np.argmax(r3.prefill(ids3)))
+        for _ in range(2):
+            tok = r3.step_greedy(tok)
+        model.sync()
+        t = time.perf_counter()
+        r3.decode_greedy(tok, 65)
+        dt = time.perf_counter() - t
+        out["decode_8192_tok_s"] = round(64 / dt, 2)
+        out["decode_8192_hbm_weight_read_frac"] = round(weight_bytes * 64 / dt / 1e9 / HBM_PEAK_GBS, 4)
+        log(f"decode @8192: {dt / 64 * 1e3:.3f} ms/token")
+        del r3
+
+    if args.cpu_steps > 0:
+        import oracle as O
+        threads = min(16, os.cpu_count() or 1)
+        O.set_threads(threads)
+        s = O.Oracle(w).new_state()
+        times = []
+        for tok in prompt[:args.cpu_steps]:
+            t = time.perf_counter()
+            s.step(tok, O.VECTOR)
+            times.append(time.perf_counter() - t)
+        per = sum(times[1:]) / max(1, len(times) - 1)
+        out["cpu_baseline"] = {"value": round(1.0 / per, 3), "unit": "tok/s", "cores": threads, "kind": "port",
+                               "sample": f"{args.cpu_steps} token-by-token steps (positions 0-{args.cpu_steps - 1}) of "
+                                         "the config-2 prompt through the CPU oracle's Backend::Vector path (C++ "
+                                         "restatement of the reference's Rust CPU decode), first step untimed; "
+                                         f"{threads} threads"}
+        log(f"cpu baseline: {per * 1e3:.1f} ms/token on {threads} threads")
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

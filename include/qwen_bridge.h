@@ -1,0 +1,162 @@
+/* The device bridge C ABI (version 3) that the reference's Rust device engine
+ * loads with dlopen (reference src/device.rs:322-474), exported here by the
+ * MI355X (gfx950) bridge libqwen_mi355x.so. Every entry point below replaces
+ * the one the reference's ROCm bridge exports (native/rocm/bridge.cpp); the
+ * comment of each cites the reference declaration it stands in for and the
+ * engine call site that binds it.
+ *
+ * Conventions (reference src/device.rs:33-190, native/rocm/bridge.cpp:354-910):
+ *   - every length is in 32-bit words (BF16 matrices pack two values per word,
+ *     element 2i in the low half; int8 matrices are `rows` fp32 scales followed
+ *     by the row-major int8 values, four per word, the last word zero-padded);
+ *   - every call returns 0 on success; otherwise qr_error() holds the message;
+ *   - all work of one context is ordered on one HIP stream; qr_read/qr_sync
+ *     synchronise it and are where asynchronous faults surface;
+ *   - one host thread per context.
+ */
+#ifndef QWEN_BRIDGE_H
+#define QWEN_BRIDGE_H
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct Context Context;
+
+/* Op arguments (reference native/rocm/reference.h:29, src/device.rs:33-38). */
+typedef struct Params {
+    float* p[8];
+    int32_t n[8];
+    float f[4];
+} Params;
+
+/* qr_run op codes (reference native/rocm/reference.h:21-24, src/device.rs:39-73). */
+enum QrOp {
+    QR_RMS_NORM = 1, QR_ADD = 2, QR_SILU_PRODUCT = 3, QR_CONV_SILU = 4, QR_DELTA_QK = 5, QR_DELTA_GATES = 6,
+    QR_DELTA_RULE = 7, QR_ATTENTION_QUERY = 8, QR_ATTENTION_KV = 9, QR_ATTENTION_READ = 10, QR_EMBED_BF16 = 11,
+    QR_ADD_RMS_NORM = 12, QR_RMS_NORM_GATE = 13, QR_DELTA_RULE_GATED = 14, QR_ATTENTION_QUERY_KV = 15,
+    QR_ARGMAX = 16, QR_EMBED_BF16_PICKED = 17
+};
+
+/* Bridge kinds returned by qr_kind (reference src/device.rs:74-80). */
+enum QrKind { QR_KIND_CPU_TEST = 0, QR_KIND_ROCM = 1, QR_KIND_METAL = 2, QR_KIND_CUDA = 3 };
+
+/* One entry of a grouped projection (reference src/device.rs:116-122). */
+typedef struct QrProjection {
+    float* y;
+    const float* a;
+    int32_t rows;
+} QrProjection;
+
+/* qr_delta_mixer arguments (reference src/device.rs:125-151, bridge.cpp:735-742). */
+typedef struct QrDelta {
+    float* convolved; const float* projected; const float* conv_w; float* conv_state;
+    float* query; float* key; float* core; float* recurrent;
+    const float* a; const float* b; const float* gates;
+    float* gated; const float* norm_w; const float* z;
+    int32_t key_heads, value_heads, key_dim, value_dim, kernel, tokens, channels;
+    float eps;
+} QrDelta;
+
+/* Add + RmsNorm after a one-token GEMV (reference src/device.rs:153-163, bridge.cpp:801). */
+typedef struct QrAddNormPost {
+    float* sum; const float* u; const float* v; const float* weight; float* norm;
+    float eps; float offset;
+} QrAddNormPost;
+
+/* ---- mandatory symbols (reference src/device.rs:341-367,442-450) ---- */
+
+/* ABI version, 3 (bridge.cpp:355). */
+int qr_abi(void);
+/* 1 = ROCm (bridge.cpp:364-372); the engine refuses any other kind in production. */
+int qr_kind(void);
+/* Context with its own stream on device 0 (bridge.cpp:375-411). */
+int qr_create(Context** out);
+/* n_floats zero-filled device words (bridge.cpp:457-466). */
+int qr_alloc(Context* c, float** p, size_t n_floats);
+/* bridge.cpp:478-486 */
+void qr_free(Context* c, float* p);
+/* Host -> device, synchronous: the host slice may die on return (bridge.cpp:487-497). */
+int qr_write(Context* c, float* dst, const float* host, size_t n);
+/* Device -> host, synchronises the stream (bridge.cpp:498-517). */
+int qr_read(Context* c, float* host, const float* src, size_t n);
+/* Device -> device, asynchronous on the stream (bridge.cpp:518-528). */
+int qr_copy(Context* c, float* dst, const float* src, size_t n);
+/* Runs op `op` over `count` items (bridge.cpp:529-570; slot semantics reference.h:117-232). */
+int qr_run(Context* c, int op, int count, const Params* a);
+/* y[rows] = A[rows, cols] x, fp32 A (bridge.cpp:571-583). */
+int qr_gemv(Context* c, float* y, const float* a, const float* x, int rows, int cols);
+/* As qr_gemv with BF16 A (bridge.cpp:654-656). */
+int qr_gemv_bf16(Context* c, float* y, const float* packed, const float* x, int rows, int cols);
+/* Y[batch, rows] = X[batch, cols] A^T, fp32 A (bridge.cpp:584-602). */
+int qr_gemm(Context* c, float* y, const float* a, const float* x, int rows, int cols, int batch);
+/* As qr_gemm with BF16 A (bridge.cpp:603-619). */
+int qr_gemm_bf16(Context* c, float* y, const float* packed, const float* x, int rows, int cols, int batch);
+/* bridge.cpp:427-435 */
+int qr_sync(Context* c);
+/* NUL-terminated, owned by the context (bridge.cpp:373). */
+const char* qr_error(Context* c);
+/* Device and runtime description (bridge.cpp:374,405-407). */
+const char* qr_info(Context* c);
+/* bridge.cpp:436-456 */
+void qr_destroy(Context* c);
+
+/* ---- optional symbols (reference src/device.rs:368-441) ---- */
+
+/* Highest qr_run op run by qr_run, 15 (bridge.cpp:356-358). */
+int qr_max_op(void);
+/* 1: ConvSilu n3 / DeltaRule(Gated) n6 store per-token state snapshots (bridge.cpp:359-361). */
+int qr_snapshots(void);
+/* 2: ops Argmax and EmbedBf16Picked (bridge.cpp:362-363). */
+int qr_argmax(void);
+/* Engine options; "attention_f16" is refused (RDNA3 WMMA only) (bridge.cpp:412-426). */
+int qr_set_option(Context* c, const char* name, int value);
+/* int8 per-row weights: Y[batch, rows] = scale[r] * (X Q^T) (bridge.cpp:620-653). */
+int qr_gemm_i8(Context* c, float* y, const float* packed, const float* x, int rows, int cols, int batch);
+/* n projections of one X (bridge.cpp:657-700 for BF16, 838-866 for int8). */
+int qr_gemm_bf16_group(Context* c, int n, const QrProjection* items, const float* x, int cols, int batch);
+int qr_gemm_i8_group(Context* c, int n, const QrProjection* items, const float* x, int cols, int batch);
+/* product = silu(X G^T) * (X U^T); gate_y/up_y are scratch (bridge.cpp:701-729, 867-885). */
+int qr_gemm_bf16_glu(Context* c, float* product, float* gate_y, float* up_y, const float* gate, const float* up,
+                     const float* x, int rows, int cols, int batch);
+int qr_gemm_i8_glu(Context* c, float* product, float* gate_y, float* up_y, const float* gate, const float* up,
+                   const float* x, int rows, int cols, int batch);
+/* One-token GEMV, then post->sum = u + v and post->norm = RmsNorm(sum) (bridge.cpp:797-827, 886-909). */
+int qr_gemm_bf16_add_norm(Context* c, float* y, const float* packed, const float* x, int rows, int cols,
+                          const QrAddNormPost* post);
+int qr_gemm_i8_add_norm(Context* c, float* y, const float* packed, const float* x, int rows, int cols,
+                        const QrAddNormPost* post);
+/* ConvSilu, DeltaQk, DeltaRuleGated and RmsNormGate of one DeltaNet layer (bridge.cpp:730-796). */
+int qr_delta_mixer(Context* c, const QrDelta* d);
+
+/* fp32 versions of the grouped / GLU / add-norm projections, with the int8
+ * signatures. The reference's engine picks the fused calls only for BF16 and
+ * int8 matrices (src/device.rs:779-786, 1801-1808, 2153-2160); these let an
+ * fp32-weight run take the same fused route through a three-site `m.f32` arm
+ * in `project_all`, `project_norm` and the GLU choice. Each output equals the
+ * separate qr_gemm / qr_gemv calls (and op SiluProduct / AddRmsNorm) it
+ * replaces, up to fp32 summation order. */
+int qr_gemm_f32_group(Context* c, int n, const QrProjection* items, const float* x, int cols, int batch);
+int qr_gemm_f32_glu(Context* c, float* product, float* gate_y, float* up_y, const float* gate, const float* up,
+                    const float* x, int rows, int cols, int batch);
+int qr_gemm_f32_add_norm(Context* c, float* y, const float* a, const float* x, int rows, int cols,
+                         const QrAddNormPost* post);
+
+/* In-bridge profiler: while on, every bridge call is bracketed by a hipEvent
+ * pair on the context stream and the durations are summed per call label
+ * (kernel family and shape). No counterpart in the reference's ABI: its
+ * bridge has the same profiler behind QWEN_ROCM_PROFILE
+ * (native/rocm/bridge.cpp:55-139), which this bridge also honours (table on
+ * stderr at qr_destroy). For benchmarks that time kernels on the stream the
+ * kernels run on. */
+int qr_profile(Context* c, int on);
+/* Totals since qr_profile(c, 1), one line per label: "calls\ttotal_ms\tlabel\n".
+ * Returns the buffer size the whole text needs (truncated to len), -1 on error. */
+long qr_profile_read(Context* c, char* out, size_t len);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

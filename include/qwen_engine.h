@@ -1,0 +1,126 @@
+/* C API of the host engine (libqwen_engine.so): a C++ restatement of the
+ * reference's Rust device engine, `DeviceModel` / `DeviceRun`
+ * (reference src/device.rs:648-2566), driving a qr_* bridge
+ * (include/qwen_bridge.h) loaded with dlopen. It issues the same bridge call
+ * sequence as `forward_body` (src/device.rs:1740-2378), plus the fp32 arms
+ * of `project_all` / `project_norm` / the GLU choice that route fp32 matrices
+ * through qr_gemm_f32_group / _add_norm / _glu when the bridge exports them.
+ *
+ * Every function returning int returns 0 on success and -1 on failure, with
+ * the message in qe_last_error(). A failed step, prefill or verify poisons the
+ * run until qe_run_reset (src/device.rs:1392-1451).
+ */
+#ifndef QWEN_ENGINE_H
+#define QWEN_ENGINE_H
+#include <stddef.h>
+#include <stdint.h>
+
+#include "qwen_model.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct QeModel QeModel;
+typedef struct QeRun QeRun;
+typedef struct QeCheckpoint QeCheckpoint;
+
+/* WeightFormat (src/device.rs:208-219). */
+enum QeFormat { QE_F32 = 0, QE_BF16_EXACT = 1, QE_INT8 = 2 };
+
+/* Optional bridge symbols the engine may be told to ignore (as if absent), to
+ * exercise the fallbacks of src/device.rs:368-441. */
+enum QeDisable {
+    QE_NO_F32_FUSIONS = 1,   /* qr_gemm_f32_group / _glu / _add_norm */
+    QE_NO_FUSIONS = 2,       /* qr_gemm_bf16_* and qr_gemm_i8_{group,glu,add_norm} */
+    QE_NO_DELTA_MIXER = 4,   /* qr_delta_mixer */
+    QE_NO_FUSED_OPS = 8,     /* qr_max_op (ops 12-15) */
+    QE_NO_ARGMAX = 16,       /* qr_argmax (ops 16-17) */
+    QE_NO_SNAPSHOTS = 32     /* qr_snapshots */
+};
+
+/* Record callback of a captured step: (layer, name, values, n). Names follow
+ * `forward_body`'s records ("input_norm", "mixed", "after_mixer", "post_norm",
+ * "ffn_product", "ffn", "output"), then "normalized" and "logits". */
+typedef void (*qe_record_fn)(void* user, int layer, const char* name, const float* values, int64_t n);
+
+const char* qe_last_error(void);
+
+/* DeviceModel::load_with (src/device.rs:926-934): dlopen `bridge_path`,
+ * require qr_abi() == 3 and qr_kind() == expect_kind, upload every tensor
+ * (slot order of include/qwen_model.h) in `format`. `disable` is a QeDisable
+ * mask. */
+QeModel* qe_model_load(const char* bridge_path, int expect_kind, const QwConfig* config,
+                       const float* const* tensors, int format, int disable);
+void qe_model_free(QeModel* m);
+/* qr_info of the bridge context. */
+const char* qe_model_info(QeModel* m);
+/* weight_summary (src/device.rs:957-965): BF16 matrices, all matrices, device matrix bytes. */
+void qe_model_weight_summary(QeModel* m, int64_t* bf16, int64_t* matrices, int64_t* bytes);
+/* qr_sync of the bridge context. */
+int qe_model_sync(QeModel* m);
+/* The bridge's profiler (qr_profile / qr_profile_read), when it has one. */
+int qe_model_profile(QeModel* m, int on);
+long qe_model_profile_read(QeModel* m, char* out, size_t len);
+/* Per-run device budget in bytes (MAX_RUN_BYTES, src/device.rs:855; default 4 GiB). */
+void qe_model_set_run_budget(QeModel* m, uint64_t bytes);
+/* run_bytes_chunked (src/device.rs:1144-1177). */
+uint64_t qe_model_run_bytes(QeModel* m, int64_t capacity, int64_t chunk);
+
+/* new_run_with (src/device.rs:1198-1294). snapshots > 0 is new_run_rollback. */
+QeRun* qe_run_new(QeModel* m, int64_t capacity, int64_t chunk, int64_t snapshots);
+void qe_run_free(QeRun* r);
+int qe_run_reset(QeRun* r);
+int64_t qe_run_position(QeRun* r);
+
+/* DeviceRun::step (src/device.rs:1440-1451); logits: vocab floats. With
+ * `record` non-NULL the step is captured (every record read back). */
+int qe_step(QeRun* r, uint32_t id, float* logits, qe_record_fn record, void* user);
+/* DeviceRun::step_greedy (src/device.rs:1568-1584). */
+int qe_step_greedy(QeRun* r, uint32_t id, uint32_t* next);
+/* DeviceRun::prefill (src/device.rs:1456-1490); last_logits (vocab floats)
+ * is written when ids is non-empty; *has_logits says whether it was. */
+int qe_prefill(QeRun* r, const uint32_t* ids, int64_t n, float* last_logits, int* has_logits);
+/* verify / verify_rollback (src/device.rs:1495-1531): n rows of logits. */
+int qe_verify(QeRun* r, const uint32_t* ids, int64_t n, float* logits);
+int qe_verify_rollback(QeRun* r, const uint32_t* ids, int64_t n, float* logits);
+/* verify_rollback_greedy (src/device.rs:1595-1610). */
+int qe_verify_rollback_greedy(QeRun* r, const uint32_t* ids, int64_t n, uint32_t* picks);
+/* accept (src/device.rs:1626-1662). */
+int qe_accept(QeRun* r, int64_t rows);
+/* unread_logits (src/device.rs:1590-1594): 1 and vocab floats if the last
+ * forward was a device-argmax step_greedy, else 0. */
+int qe_unread_logits(QeRun* r, float* logits);
+
+/* inspect_state (src/device.rs:2380-2424), one part at a time: which = 0
+ * conv history, 1 recurrent state, 2 keys (position * kv * d), 3 values. */
+int64_t qe_state_size(QeRun* r, int layer, int which);
+int qe_state_read(QeRun* r, int layer, int which, float* out);
+/* load_state (src/device.rs:2493-2516) of one part; set_position completes it. */
+int qe_state_write(QeRun* r, int layer, int which, const float* values, int64_t n);
+int qe_state_set_position(QeRun* r, int64_t position);
+/* checkpoint / restore / initial_checkpoint (src/device.rs:2425-2490). */
+QeCheckpoint* qe_checkpoint(QeRun* r);
+QeCheckpoint* qe_initial_checkpoint(QeRun* r);
+int qe_restore(QeRun* r, const QeCheckpoint* c);
+void qe_checkpoint_free(QeCheckpoint* c);
+int64_t qe_checkpoint_position(const QeCheckpoint* c);
+
+/* Greedy decode loop (decode_greedy_ids, src/generate.rs:135-166) without
+ * EOS: feeds `first`, then each pick, n_new tokens in all (n_new - 1
+ * forwards), timing the forwards (the reference's decode timing,
+ * src/device/cli.rs:797-812). ids: n_new outputs. */
+int qe_decode_greedy(QeRun* r, uint32_t first, int64_t n_new, uint32_t* ids, double* seconds);
+
+/* Row-wise symmetric int8 quantiser (src/device.rs:220-239) as the engine
+ * uploads it. */
+void qe_quantize_int8_rows(const float* w, int64_t rows, int64_t cols, float* scales, int8_t* q);
+
+/* Deterministic N(0, std) fill, counter-based: element i of (seed, stream)
+ * does not depend on the thread count. */
+void qw_synth_normal(float* dst, uint64_t n, uint64_t seed, uint64_t stream, float std_dev, int threads);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,502 @@
+// The qr_* C ABI (version 3) of the MI355X bridge: context, memory, op
+// dispatch and the projection entry points, over the gfx950 kernels of
+// gemv.hip, gemm.hip, ops.hip, attention.hip and deltanet.hip. Declarations
+// and the reference entry point each one replaces: include/qwen_bridge.h.
+#include <hip/hip_runtime.h>
+
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <map>
+#include <new>
+#include <string>
+#include <vector>
+
+#include "common.h"
+
+struct Context {
+    char error[256] = {};
+    char info[512] = {};
+    hipStream_t stream = nullptr;
+    unsigned* ticket = nullptr;   // add-norm tail counter (kept 0 between launches)
+    float* argmax_parts = nullptr;  // per-slice partials of the two-pass argmax
+    size_t argmax_parts_len = 0;
+    float* attn_parts = nullptr;  // split partials of decode attention
+    size_t attn_parts_len = 0;
+    // Profiler (qr_profile / QWEN_ROCM_PROFILE=1): a hipEvent pair on the
+    // context stream around every bridge call, summed per label.
+    bool profile = false, print_at_exit = false;
+    struct Timed {
+        std::string label;
+        hipEvent_t start, stop;
+    };
+    std::vector<Timed> timed;
+    std::vector<hipEvent_t> spare;
+    std::map<std::string, std::pair<long, double>> totals;  // label -> (calls, ms)
+};
+
+namespace {
+
+int fail(Context* c, const char* what, int status) {
+    std::snprintf(c->error, sizeof(c->error), "%s status=%d (%s)", what, status,
+                  status > 0 ? hipGetErrorString(hipError_t(status)) : "invalid argument");
+    return status ? status : -1;
+}
+int launched(Context* c, const char* what, int status) { return status ? fail(c, what, status) : 0; }
+
+hipEvent_t take_event(Context* c) {
+    hipEvent_t e = nullptr;
+    if (!c->spare.empty()) {
+        e = c->spare.back();
+        c->spare.pop_back();
+    } else {
+        (void)hipEventCreate(&e);
+    }
+    return e;
+}
+// Event pair around one bridge call when profiling; the label is built only then.
+template <class L>
+struct Scope {
+    Context* c;
+    hipEvent_t start = nullptr;
+    std::string label;
+    Scope(Context* ctx, L&& make) : c(ctx) {
+        if (!c->profile) return;
+        label = make();
+        start = take_event(c);
+        (void)hipEventRecord(start, c->stream);
+    }
+    ~Scope() {
+        if (!start) return;
+        hipEvent_t stop = take_event(c);
+        (void)hipEventRecord(stop, c->stream);
+        c->timed.push_back(Context::Timed{std::move(label), start, stop});
+    }
+};
+template <class L>
+Scope<L> scope(Context* c, L&& make) {
+    return Scope<L>(c, std::forward<L>(make));
+}
+void collect(Context* c) {
+    for (auto& t : c->timed) {
+        float ms = 0.f;
+        if (hipEventElapsedTime(&ms, t.start, t.stop) == hipSuccess) {
+            auto& v = c->totals[t.label];
+            v.first += 1;
+            v.second += ms;
+        }
+        c->spare.push_back(t.start);
+        c->spare.push_back(t.stop);
+    }
+    c->timed.clear();
+}
+const char* wname(qr::WeightType t) {
+    return t == qr::WeightType::F32 ? "f32" : t == qr::WeightType::BF16 ? "bf16" : "i8";
+}
+std::string shape(int rows, int cols, int batch) {
+    return std::to_string(rows) + "x" + std::to_string(cols) + (batch > 1 ? " t" + std::to_string(batch) : "");
+}
+const char* op_name(int op) {
+    static const char* names[] = {"?", "rms_norm", "add", "silu_product", "conv_silu", "delta_qk", "delta_gates",
+                                  "delta_rule", "attention_query", "attention_kv", "attention_read", "embed_bf16",
+                                  "add_rms_norm", "rms_norm_gate", "delta_rule_gated", "attention_query_kv", "argmax",
+                                  "embed_bf16_picked"};
+    return op >= 1 && op <= 17 ? names[op] : "?";
+}
+
+// Grows a bridge-owned scratch buffer (synchronising before a reallocation,
+// since queued kernels may still use the old one).
+int ensure(Context* c, float** buf, size_t* len, size_t need, const char* what) {
+    if (need <= *len) return 0;
+    if (*buf) {
+        (void)hipStreamSynchronize(c->stream);
+        (void)hipFree(*buf);
+        *buf = nullptr;
+        *len = 0;
+    }
+    auto st = hipMalloc(reinterpret_cast<void**>(buf), need * sizeof(float));
+    if (st != hipSuccess) return fail(c, what, int(st));
+    *len = need;
+    return 0;
+}
+
+const void* i8_packed(const float* packed) { return packed; }
+
+int project(Context* c, qr::WeightType t, float* y, const void* a, const float* x, int rows, int cols, int batch) {
+    if (rows < 1 || cols < 1 || batch < 1) return fail(c, "projection shape", -1);
+    if (!qr::gemm_preferred(t, rows, cols, batch)) {
+        auto s = scope(c, [&] { return std::string("gemv_") + wname(t) + " " + shape(rows, cols, batch); });
+        qr::GemvItem it{y, a, rows};
+        return launched(c, "gemv", qr::gemv_group(c->stream, t, &it, 1, x, cols, batch));
+    }
+    auto s = scope(c, [&] { return std::string("gemm_") + wname(t) + " " + shape(rows, cols, batch); });
+    return launched(c, "gemm", qr::gemm(c->stream, t, y, a, x, rows, cols, batch));
+}
+
+int group(Context* c, qr::WeightType t, int n, const QrProjection* items, const float* x, int cols, int batch) {
+    if (n < 1 || cols < 1 || batch < 1) return fail(c, "GEMM group shape", -1);
+    for (int i = 0; i < n; ++i)
+        if (items[i].rows < 1) return fail(c, "GEMM group shape", -1);
+    if (qr::gemm_preferred(t, items[0].rows, cols, batch)) {
+        for (int i = 0; i < n; ++i)
+            if (int s = project(c, t, items[i].y, items[i].a, x, items[i].rows, cols, batch)) return s;
+        return 0;
+    }
+    qr::GemvItem its[64];
+    if (n > 64) return fail(c, "GEMM group too large", -1);
+    for (int i = 0; i < n; ++i) its[i] = qr::GemvItem{items[i].y, items[i].a, items[i].rows};
+    auto s = scope(c, [&] {
+        std::string l = std::string("gemv_") + wname(t) + "_group";
+        for (int i = 0; i < n; ++i) l += (i ? "+" : " ") + shape(items[i].rows, cols, 1);
+        return batch > 1 ? l + " t" + std::to_string(batch) : l;
+    });
+    return launched(c, "gemv_group", qr::gemv_group(c->stream, t, its, n, x, cols, batch));
+}
+
+int glu(Context* c, qr::WeightType t, float* product, float* gate_y, float* up_y, const float* gate, const float* up,
+        const float* x, int rows, int cols, int batch) {
+    if (rows < 1 || cols < 1 || batch < 1) return fail(c, "GLU shape", -1);
+    if (!qr::gemm_preferred(t, rows, cols, batch)) {
+        auto s = scope(c, [&] { return std::string("gemv_") + wname(t) + "_glu 2x" + shape(rows, cols, batch); });
+        return launched(c, "gemv_glu", qr::gemv_glu(c->stream, t, product, gate, up, x, rows, cols, batch));
+    }
+    if (int s = project(c, t, gate_y, gate, x, rows, cols, batch)) return s;
+    if (int s = project(c, t, up_y, up, x, rows, cols, batch)) return s;
+    Params p{};
+    p.p[0] = product;
+    p.p[1] = gate_y;
+    p.p[2] = up_y;
+    return launched(c, "silu_product", qr::run_elementwise(c->stream, QR_SILU_PRODUCT, rows * batch, p));
+}
+
+int add_norm(Context* c, qr::WeightType t, float* y, const void* a, const float* x, int rows, int cols,
+             const QrAddNormPost* post) {
+    if (rows < 1 || cols < 1 || !post) return fail(c, "GEMV+norm shape", -1);
+    auto s = scope(c, [&] { return std::string("gemv_") + wname(t) + "_add_norm " + shape(rows, cols, 1); });
+    return launched(c, "gemv_add_norm", qr::gemv_add_norm(c->stream, t, y, a, x, rows, cols, *post, c->ticket));
+}
+
+// Attention read of 2..8 rows: the decode path once per row over its own
+// length, so every row equals the decode step of its position (the rows of a
+// verify pass; reference native/rocm/bridge.cpp:197-215 does the same).
+int attention_read(Context* c, int count, const Params& a) {
+    const int rows = a.n[5] > 0 ? a.n[5] : 1;
+    if (rows > 1 && rows <= 8) {
+        const size_t q = size_t(a.n[0]) * size_t(a.n[1]);
+        for (int r = 0; r < rows; ++r) {
+            Params one = a;
+            for (int slot : {0, 1, 4}) one.p[slot] = a.p[slot] + r * q;
+            one.n[3] = a.n[3] + r;
+            one.n[5] = 0;
+            if (int s = attention_read(c, count, one)) return s;
+        }
+        return 0;
+    }
+    if (int s = ensure(c, &c->attn_parts, &c->attn_parts_len, qr::attention_scratch_needed(a), "hipMalloc attention"))
+        return s;
+    auto s = scope(c, [&] {
+        return std::string(rows == 1 ? "attention_read decode len " : "attention_read prefill len ") +
+               std::to_string(a.n[3]) + (rows > 1 ? " rows " + std::to_string(rows) : "");
+    });
+    return launched(c, "attention_read",
+                    qr::run_attention_read(c->stream, count, a, c->attn_parts, c->attn_parts_len));
+}
+
+}  // namespace
+
+extern "C" {
+
+int qr_abi(void) { return 3; }
+int qr_kind(void) { return QR_KIND_ROCM; }
+int qr_max_op(void) { return QR_ATTENTION_QUERY_KV; }
+int qr_snapshots(void) { return 1; }
+int qr_argmax(void) { return 2; }
+
+const char* qr_error(Context* c) { return c->error; }
+const char* qr_info(Context* c) { return c->info; }
+
+int qr_create(Context** out) {
+    *out = nullptr;
+    Context* c = new (std::nothrow) Context;
+    if (!c) return -1;
+    hipError_t h = hipSetDevice(0);
+    if (h != hipSuccess) {
+        delete c;
+        return int(h);
+    }
+    h = hipStreamCreate(&c->stream);
+    if (h != hipSuccess) {
+        delete c;
+        return int(h);
+    }
+    h = hipMalloc(reinterpret_cast<void**>(&c->ticket), 256);
+    if (h == hipSuccess) h = hipMemset(c->ticket, 0, 256);
+    if (h != hipSuccess) {
+        (void)hipStreamDestroy(c->stream);
+        delete c;
+        return int(h);
+    }
+    hipDeviceProp_t props{};
+    int runtime = 0, driver = 0;
+    auto ps = hipGetDeviceProperties(&props, 0);
+    (void)hipRuntimeGetVersion(&runtime);
+    (void)hipDriverGetVersion(&driver);
+    std::snprintf(c->info, sizeof(c->info),
+                  "device0=%s arch=%s cus=%d hbm_bytes=%zu l2_bytes=%d hip_runtime=%d driver_api=%d "
+                  "bridge=qwen-mi355x gfx950 wave64",
+                  ps == hipSuccess ? props.name : "unknown", ps == hipSuccess ? props.gcnArchName : "unknown",
+                  ps == hipSuccess ? props.multiProcessorCount : 0, ps == hipSuccess ? size_t(props.totalGlobalMem) : 0,
+                  ps == hipSuccess ? props.l2CacheSize : 0, runtime, driver);
+    if (const char* p = std::getenv("QWEN_ROCM_PROFILE"))
+        c->profile = c->print_at_exit = std::strcmp(p, "0") != 0 && p[0] != 0;
+    *out = c;
+    return 0;
+}
+
+int qr_set_option(Context* c, const char* name, int value) {
+    if (std::strcmp(name, "attention_f16") != 0 || (value != 0 && value != 1))
+        return fail(c, "unknown bridge option", -1);
+    if (value) return fail(c, "attention_f16 (16-bit prefill attention) is not offered: attention runs in fp32", -1);
+    return 0;
+}
+
+int qr_sync(Context* c) {
+    auto s = hipStreamSynchronize(c->stream);
+    if (s != hipSuccess) return fail(c, "hipStreamSynchronize", int(s));
+    if (!c->timed.empty()) collect(c);
+    return 0;
+}
+
+// Profiler switch (no counterpart in the reference's ABI; its bridge had the
+// same event-pair profiler behind QWEN_ROCM_PROFILE, native/rocm/bridge.cpp:55-139).
+int qr_profile(Context* c, int on) {
+    if (int s = qr_sync(c)) return s;
+    c->profile = on != 0;
+    if (on) c->totals.clear();
+    return 0;
+}
+
+// Totals since qr_profile(c, 1) as text lines "calls<TAB>total_ms<TAB>label".
+// Returns the length the full text needs (the text is truncated to `len`).
+long qr_profile_read(Context* c, char* out, size_t len) {
+    if (qr_sync(c)) return -1;
+    std::string text;
+    for (auto& [label, v] : c->totals) {
+        char line[64];
+        std::snprintf(line, sizeof(line), "%ld\t%.6f\t", v.first, v.second);
+        text += line + label + "\n";
+    }
+    if (out && len) {
+        size_t n = text.size() < len - 1 ? text.size() : len - 1;
+        std::memcpy(out, text.data(), n);
+        out[n] = 0;
+    }
+    return long(text.size()) + 1;
+}
+
+void qr_destroy(Context* c) {
+    if (!c) return;
+    (void)hipStreamSynchronize(c->stream);
+    if (c->print_at_exit) {
+        collect(c);
+        double all = 0;
+        for (auto& [label, v] : c->totals) all += v.second;
+        std::fprintf(stderr, "QWEN_ROCM_PROFILE: %.3f ms of GPU time in bridge calls\n%10s %12s %10s  %s\n", all,
+                     "calls", "total_ms", "mean_us", "label");
+        for (auto& [label, v] : c->totals)
+            std::fprintf(stderr, "%10ld %12.3f %10.2f  %s\n", v.first, v.second, 1000 * v.second / double(v.first),
+                         label.c_str());
+    }
+    for (auto& t : c->timed) {
+        (void)hipEventDestroy(t.start);
+        (void)hipEventDestroy(t.stop);
+    }
+    for (auto e : c->spare) (void)hipEventDestroy(e);
+    if (c->ticket) (void)hipFree(c->ticket);
+    if (c->argmax_parts) (void)hipFree(c->argmax_parts);
+    if (c->attn_parts) (void)hipFree(c->attn_parts);
+    (void)hipStreamDestroy(c->stream);
+    delete c;
+}
+
+int qr_alloc(Context* c, float** p, size_t n) {
+    if (n == 0) return fail(c, "empty allocation", -1);
+    auto s = hipMalloc(reinterpret_cast<void**>(p), n * sizeof(float));
+    if (s != hipSuccess) return fail(c, "hipMalloc", int(s));
+    s = hipMemsetAsync(*p, 0, n * sizeof(float), c->stream);
+    if (s != hipSuccess) {
+        (void)hipFree(*p);
+        *p = nullptr;
+        return fail(c, "hipMemsetAsync", int(s));
+    }
+    return 0;
+}
+
+void qr_free(Context* c, float* p) {
+    (void)c;
+    (void)hipFree(p);
+}
+
+int qr_write(Context* c, float* p, const float* host, size_t n) {
+    auto s = hipMemcpyAsync(p, host, n * sizeof(float), hipMemcpyHostToDevice, c->stream);
+    if (s != hipSuccess) return fail(c, "H2D", int(s));
+    return qr_sync(c);  // the host slice may be gone after return
+}
+
+int qr_read(Context* c, float* host, const float* p, size_t n) {
+    auto s = hipMemcpyAsync(host, p, n * sizeof(float), hipMemcpyDeviceToHost, c->stream);
+    if (s != hipSuccess) return fail(c, "D2H", int(s));
+    return qr_sync(c);
+}
+
+int qr_copy(Context* c, float* dest, const float* src, size_t n) {
+    auto sc = scope(c, [&] { return std::string("copy"); });
+    auto s = hipMemcpyAsync(dest, src, n * sizeof(float), hipMemcpyDeviceToDevice, c->stream);
+    return s == hipSuccess ? 0 : fail(c, "D2D", int(s));
+}
+
+int qr_run(Context* c, int op, int count, const Params* ap) {
+    if (op < QR_RMS_NORM || op > QR_EMBED_BF16_PICKED || count < 1 || !ap) return fail(c, "invalid kernel", -1);
+    const Params& a = *ap;
+    hipStream_t s = c->stream;
+    if (op == QR_ATTENTION_READ) return attention_read(c, count, a);  // timed inside
+    auto sc = scope(c, [&] { return std::string(op_name(op)); });
+    switch (op) {
+    case QR_RMS_NORM:
+    case QR_ADD_RMS_NORM:
+    case QR_RMS_NORM_GATE:
+        if (a.n[0] < 1) return fail(c, "norm shape", -1);
+        return launched(c, "rms_norm", qr::run_rms_family(s, op, count, a));
+    case QR_ADD:
+    case QR_SILU_PRODUCT:
+    case QR_DELTA_GATES:
+    case QR_EMBED_BF16:
+    case QR_EMBED_BF16_PICKED: return launched(c, "elementwise", qr::run_elementwise(s, op, count, a));
+    case QR_CONV_SILU: return launched(c, "conv_silu", qr::run_conv_silu(s, count, a));
+    case QR_DELTA_QK:
+        if (a.n[0] < 1 || a.n[1] < 1 || a.n[1] % a.n[0] != 0) return fail(c, "DeltaQk heads", -1);
+        return launched(c, "delta_qk", qr::run_delta_qk(s, count, a));
+    case QR_DELTA_RULE:
+    case QR_DELTA_RULE_GATED:
+        if (a.n[0] < 1 || a.n[1] < 1 || a.n[0] > 256) return fail(c, "DeltaRule key_dim must be 1..256", -1);
+        return launched(c, "delta_rule", qr::run_delta_rule(s, op == QR_DELTA_RULE_GATED, count, a));
+    case QR_ATTENTION_QUERY:
+    case QR_ATTENTION_KV:
+    case QR_ATTENTION_QUERY_KV: return launched(c, "attention_qkv", qr::run_attention_qkv(s, op, count, a));
+    case QR_ATTENTION_READ: return attention_read(c, count, a);
+    case QR_ARGMAX: {
+        if (a.n[0] < 1) return fail(c, "argmax shape", -1);
+        if (int st = ensure(c, &c->argmax_parts, &c->argmax_parts_len, qr::argmax_parts_needed(count, a.n[0]),
+                            "hipMalloc argmax"))
+            return st;
+        return launched(c, "argmax", qr::run_argmax(s, count, a, c->argmax_parts, c->argmax_parts_len));
+    }
+    }
+    return fail(c, "invalid kernel", -1);
+}
+
+int qr_gemv(Context* c, float* y, const float* a, const float* x, int rows, int cols) {
+    return project(c, qr::WeightType::F32, y, a, x, rows, cols, 1);
+}
+int qr_gemm(Context* c, float* y, const float* a, const float* x, int rows, int cols, int batch) {
+    return project(c, qr::WeightType::F32, y, a, x, rows, cols, batch);
+}
+int qr_gemv_bf16(Context* c, float* y, const float* packed, const float* x, int rows, int cols) {
+    return project(c, qr::WeightType::BF16, y, packed, x, rows, cols, 1);
+}
+int qr_gemm_bf16(Context* c, float* y, const float* packed, const float* x, int rows, int cols, int batch) {
+    return project(c, qr::WeightType::BF16, y, packed, x, rows, cols, batch);
+}
+int qr_gemm_i8(Context* c, float* y, const float* packed, const float* x, int rows, int cols, int batch) {
+    return project(c, qr::WeightType::I8, y, i8_packed(packed), x, rows, cols, batch);
+}
+
+int qr_gemm_f32_group(Context* c, int n, const QrProjection* items, const float* x, int cols, int batch) {
+    return group(c, qr::WeightType::F32, n, items, x, cols, batch);
+}
+int qr_gemm_bf16_group(Context* c, int n, const QrProjection* items, const float* x, int cols, int batch) {
+    return group(c, qr::WeightType::BF16, n, items, x, cols, batch);
+}
+int qr_gemm_i8_group(Context* c, int n, const QrProjection* items, const float* x, int cols, int batch) {
+    return group(c, qr::WeightType::I8, n, items, x, cols, batch);
+}
+
+int qr_gemm_f32_glu(Context* c, float* product, float* gate_y, float* up_y, const float* gate, const float* up,
+                    const float* x, int rows, int cols, int batch) {
+    return glu(c, qr::WeightType::F32, product, gate_y, up_y, gate, up, x, rows, cols, batch);
+}
+int qr_gemm_bf16_glu(Context* c, float* product, float* gate_y, float* up_y, const float* gate, const float* up,
+                     const float* x, int rows, int cols, int batch) {
+    return glu(c, qr::WeightType::BF16, product, gate_y, up_y, gate, up, x, rows, cols, batch);
+}
+int qr_gemm_i8_glu(Context* c, float* product, float* gate_y, float* up_y, const float* gate, const float* up,
+                   const float* x, int rows, int cols, int batch) {
+    return glu(c, qr::WeightType::I8, product, gate_y, up_y, gate, up, x, rows, cols, batch);
+}
+
+int qr_gemm_f32_add_norm(Context* c, float* y, const float* a, const float* x, int rows, int cols,
+                         const QrAddNormPost* post) {
+    return add_norm(c, qr::WeightType::F32, y, a, x, rows, cols, post);
+}
+int qr_gemm_bf16_add_norm(Context* c, float* y, const float* packed, const float* x, int rows, int cols,
+                          const QrAddNormPost* post) {
+    return add_norm(c, qr::WeightType::BF16, y, packed, x, rows, cols, post);
+}
+int qr_gemm_i8_add_norm(Context* c, float* y, const float* packed, const float* x, int rows, int cols,
+                        const QrAddNormPost* post) {
+    return add_norm(c, qr::WeightType::I8, y, packed, x, rows, cols, post);
+}
+
+int qr_delta_mixer(Context* c, const QrDelta* d) {
+    if (!d || d->tokens < 1 || d->value_heads < 1 || d->key_heads < 1 || d->value_heads % d->key_heads != 0)
+        return fail(c, "delta mixer shape", -1);
+    if (qr::delta_mixer_decode_ok(*d)) {
+        auto sc = scope(c, [&] { return std::string("delta_mixer decode"); });
+        return launched(c, "delta_mixer", qr::delta_mixer_decode(c->stream, *d));
+    }
+    // Otherwise the four ops with the slots the engine gives them
+    // (reference native/rocm/bridge.cpp:743-761).
+    const int vh = d->value_heads, vd = vh * d->value_dim, t = d->tokens;
+    Params conv{}, qk{}, rule{}, gate{};
+    conv.p[0] = d->convolved;
+    conv.p[1] = const_cast<float*>(d->projected);
+    conv.p[2] = const_cast<float*>(d->conv_w);
+    conv.p[3] = d->conv_state;
+    conv.n[0] = d->kernel;
+    conv.n[1] = t;
+    conv.n[2] = d->channels;
+    qk.p[0] = d->query;
+    qk.p[1] = d->convolved;
+    qk.p[2] = d->key;
+    qk.n[0] = d->key_heads;
+    qk.n[1] = vh;
+    qk.n[2] = d->key_dim;
+    qk.n[3] = d->channels;
+    rule.p[0] = d->core;
+    rule.p[1] = d->query;
+    rule.p[2] = d->key;
+    rule.p[3] = d->convolved;
+    rule.p[4] = d->recurrent;
+    rule.p[5] = const_cast<float*>(d->a);
+    rule.p[6] = const_cast<float*>(d->b);
+    rule.p[7] = const_cast<float*>(d->gates);
+    rule.n[0] = d->key_dim;
+    rule.n[1] = d->value_dim;
+    rule.n[2] = d->key_heads;
+    rule.n[3] = vh;
+    rule.n[4] = t;
+    rule.n[5] = d->channels;
+    gate.p[0] = d->gated;
+    gate.p[1] = d->core;
+    gate.p[2] = const_cast<float*>(d->norm_w);
+    gate.p[3] = const_cast<float*>(d->z);
+    gate.n[0] = d->value_dim;
+    gate.f[0] = d->eps;
+    gate.f[1] = 0.f;
+    if (int s = qr_run(c, QR_CONV_SILU, d->channels, &conv)) return s;
+    if (int s = qr_run(c, QR_DELTA_QK, vh * t, &qk)) return s;
+    if (int s = qr_run(c, QR_DELTA_RULE_GATED, vd, &rule)) return s;
+    return qr_run(c, QR_RMS_NORM_GATE, vh * t, &gate);
+}
+
+}  // extern "C"

@@ -1,0 +1,106 @@
+// Shared definitions of the gfx950 bridge: wave64 helpers and the launch
+// wrappers each kernel translation unit exports to bridge.cpp.
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+
+#include "../../include/qwen_bridge.h"
+
+namespace qr {
+
+constexpr int kWave = 64;  // CDNA wavefront
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = kWave / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+    return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = kWave / 2; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
+    return v;
+}
+// Sum over groups of `width` consecutive lanes (width a power of two <= 64).
+template <int W>
+__device__ __forceinline__ float group_sum(float v) {
+#pragma unroll
+    for (int o = W / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+    return v;
+}
+
+// Block-wide sum for blockDim.x a multiple of 64 (<= 1024); every thread gets
+// the total. `scratch` holds at least blockDim.x / 64 floats.
+__device__ __forceinline__ float block_sum(float v, float* scratch) {
+    v = wave_sum(v);
+    int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave, waves = blockDim.x / kWave;
+    __syncthreads();
+    if (lane == 0) scratch[wave] = v;
+    __syncthreads();
+    float t = 0.f;
+    for (int w = 0; w < waves; ++w) t += scratch[w];
+    return t;
+}
+
+// Device math with the reference's branch structure (reference.h:31-40).
+__device__ __forceinline__ float sigmoidf_(float x) {
+    if (x >= 0.f) return 1.f / (1.f + expf(-x));
+    float e = expf(x);
+    return e / (1.f + e);
+}
+__device__ __forceinline__ float siluf_(float x) { return x * sigmoidf_(x); }
+__device__ __forceinline__ float softplusf_(float x) { return x > 20.f ? x : log1pf(expf(x)); }
+
+__host__ __device__ inline unsigned ceil_div(long a, long b) { return unsigned((a + b - 1) / b); }
+
+}  // namespace qr
+
+// ---------------------------------------------------------------- launch wrappers
+// Each returns 0 or a hipError_t from the launch. `s` is the context stream.
+namespace qr {
+
+// gemv.hip -------------------------------------------------------------------
+enum class WeightType { F32, BF16, I8 };
+struct GemvItem {
+    float* y;
+    const void* a;  // fp32 / packed bf16 / packed int8 (scales then values)
+    int rows;
+};
+// Y_i[batch, rows_i] = X[batch, cols] . A_i^T for up to kGroupMax items.
+constexpr int kGroupMax = 8;
+int gemv_group(hipStream_t s, WeightType t, const GemvItem* items, int n, const float* x, int cols, int batch);
+// product[batch, rows] = silu(X G^T) * (X U^T)
+int gemv_glu(hipStream_t s, WeightType t, float* product, const void* gate, const void* up, const float* x, int rows,
+             int cols, int batch);
+// One token: y = A x, then sum = u + v and norm = RmsNorm(sum) (weight, eps, offset) by the last block.
+int gemv_add_norm(hipStream_t s, WeightType t, float* y, const void* a, const float* x, int rows, int cols,
+                  const QrAddNormPost& post, unsigned* ticket);
+
+// gemm.hip -------------------------------------------------------------------
+// Y[batch, rows] = X[batch, cols] . A^T (prefill).
+int gemm(hipStream_t s, WeightType t, float* y, const void* a, const float* x, int rows, int cols, int batch);
+bool gemm_preferred(WeightType t, int rows, int cols, int batch);
+
+// ops.hip --------------------------------------------------------------------
+int run_elementwise(hipStream_t s, int op, int count, const Params& a);
+int run_rms_family(hipStream_t s, int op, int groups, const Params& a);
+int run_conv_silu(hipStream_t s, int count, const Params& a);
+int run_delta_qk(hipStream_t s, int count, const Params& a);
+int run_delta_rule(hipStream_t s, bool gated, int count, const Params& a);
+int run_attention_qkv(hipStream_t s, int op, int count, const Params& a);
+int run_embed(hipStream_t s, int op, int count, const Params& a);
+int run_argmax(hipStream_t s, int rows, const Params& a, float* parts, size_t parts_len);
+size_t argmax_parts_needed(int rows, int n);
+
+// attention.hip --------------------------------------------------------------
+// AttentionRead (op 10). `scratch` is the bridge's own partials buffer.
+int run_attention_read(hipStream_t s, int heads_count, const Params& a, float* scratch, size_t scratch_len);
+size_t attention_scratch_needed(const Params& a);
+
+// deltanet.hip ---------------------------------------------------------------
+// qr_delta_mixer for one token (decode) when the shape allows; returns -1 if not handled.
+int delta_mixer_decode(hipStream_t s, const QrDelta& d);
+bool delta_mixer_decode_ok(const QrDelta& d);
+
+}  // namespace qr

@@ -1,0 +1,453 @@
+// qr_run ops on gfx950: elementwise ops, the RMSNorm family, DeltaNet conv /
+// Q-K normalisation / gates / recurrent rule, attention Q/K preparation with
+// partial RoPE, embedding rows and the two-pass argmax.
+//
+// Each op computes what the reference's op body computes
+// (native/rocm/reference.h:117-232, slot meanings there); the decomposition is
+// this file's own: a wave or block per group for reductions, P lanes per
+// DeltaNet value column with the column's state in VGPRs.
+#include "common.h"
+
+namespace qr {
+namespace {
+
+// ---------------------------------------------------------------- elementwise
+// Add (2), SiluProduct (3), DeltaGates (6), EmbedBf16 (11), EmbedBf16Picked (17).
+__global__ __launch_bounds__(256) void elementwise_kernel(int op, int count, Params a) {
+    for (long t = blockIdx.x * long(blockDim.x) + threadIdx.x; t < count; t += long(gridDim.x) * blockDim.x) {
+        switch (op) {
+        case QR_ADD: a.p[0][t] = a.p[1][t] + a.p[2][t]; break;
+        case QR_SILU_PRODUCT: a.p[0][t] = siluf_(a.p[1][t]) * a.p[2][t]; break;
+        case QR_DELTA_GATES: {  // reference.h:144-148
+            int head = a.n[0] > 0 ? int(t % a.n[0]) : int(t);
+            a.p[0][t] = -expf(a.p[4][head]) * softplusf_(a.p[1][t] + a.p[3][head]);
+            a.p[5][t] = sigmoidf_(a.p[2][t]);
+            break;
+        }
+        case QR_EMBED_BF16: {  // reference.h:213-216
+            const uint16_t* m = reinterpret_cast<const uint16_t*>(a.p[1]);
+            a.p[0][t] = __uint_as_float(uint32_t(m[size_t(a.n[0]) * size_t(a.n[1]) + size_t(t)]) << 16);
+            break;
+        }
+        case QR_EMBED_BF16_PICKED: {  // reference.h:217-221
+            const uint16_t* m = reinterpret_cast<const uint16_t*>(a.p[1]);
+            size_t h = size_t(a.n[1]), r = size_t(t) / h;
+            size_t row = size_t(a.p[2][2 * r]);
+            a.p[0][t] = __uint_as_float(uint32_t(m[row * h + size_t(t) % h]) << 16);
+            break;
+        }
+        }
+    }
+}
+
+// ---------------------------------------------------------------- RMSNorm family
+// RmsNorm (1), AddRmsNorm (12), RmsNormGate (13): reference.h:120-126,194-207.
+// One wave per group when d <= 256, else one block per group.
+template <bool WAVE>
+__global__ __launch_bounds__(256) void rms_family_kernel(int op, int groups, Params a) {
+    __shared__ float red[16];
+    const int d = a.n[0];
+    const int g = WAVE ? blockIdx.x * 4 + int(threadIdx.x >> 6) : blockIdx.x;
+    const int t0 = WAVE ? int(threadIdx.x & 63) : int(threadIdx.x);
+    const int step = WAVE ? 64 : int(blockDim.x);
+    if (WAVE && g >= groups) return;  // whole waves only: no block barrier in the wave form
+    const size_t off = size_t(g) * d;
+    const float eps = a.f[0], offset = a.f[1];
+    float ss = 0.f;
+    if (op == QR_ADD_RMS_NORM) {
+        for (int i = t0; i < d; i += step) {
+            float s = a.p[1][off + i] + a.p[2][off + i];
+            a.p[0][off + i] = s;
+            ss += s * s;
+        }
+    } else {
+        for (int i = t0; i < d; i += step) {
+            float v = a.p[1][off + i];
+            ss += v * v;
+        }
+    }
+    ss = WAVE ? wave_sum(ss) : block_sum(ss, red);
+    const float r = 1.f / sqrtf(ss / float(d) + eps);
+    for (int i = t0; i < d; i += step) {
+        switch (op) {
+        case QR_RMS_NORM: a.p[0][off + i] = (a.p[1][off + i] * r) * (a.p[2][i] + offset); break;
+        case QR_ADD_RMS_NORM: a.p[3][off + i] = (a.p[0][off + i] * r) * (a.p[4][i] + offset); break;
+        case QR_RMS_NORM_GATE:
+            a.p[0][off + i] = siluf_(a.p[3][off + i]) * ((a.p[1][off + i] * r) * (a.p[2][i] + offset));
+            break;
+        }
+    }
+}
+
+// ---------------------------------------------------------------- ConvSilu (4)
+// reference.h:96-116: one channel per thread, tokens in order through the
+// channel's history (oldest -> newest); with n3 = S > 0 the history after
+// token r < S is also stored as snapshot r at (r + 1) * n2 * (k - 1).
+__global__ __launch_bounds__(256) void conv_silu_kernel(int count, Params a) {
+    const int ch = blockIdx.x * blockDim.x + threadIdx.x;
+    if (ch >= count) return;
+    const int k = a.n[0], tokens = a.n[1] > 0 ? a.n[1] : 1, stride = a.n[2], snaps = a.n[3];
+    const float* w = a.p[2] + size_t(ch) * k;
+    float* hist = a.p[3] + size_t(ch) * (k - 1);
+    float h[16];
+    float wk[17];
+    for (int i = 0; i < k - 1; ++i) h[i] = hist[i];
+    for (int i = 0; i < k; ++i) wk[i] = w[i];
+    for (int r = 0; r < tokens; ++r) {
+        const float xv = a.p[1][size_t(r) * stride + ch];
+        float sum = 0.f;
+        for (int i = 0; i < k - 1; ++i) sum += h[i] * wk[i];
+        sum += xv * wk[k - 1];
+        for (int i = 0; i + 1 < k - 1; ++i) h[i] = h[i + 1];
+        if (k > 1) h[k - 2] = xv;
+        a.p[0][size_t(r) * stride + ch] = siluf_(sum);
+        if (r < snaps)
+            for (int i = 0; i < k - 1; ++i) hist[size_t(r + 1) * size_t(stride) * size_t(k - 1) + i] = h[i];
+    }
+    for (int i = 0; i < k - 1; ++i) hist[i] = h[i];
+}
+
+// ---------------------------------------------------------------- DeltaQk (5)
+// reference.h:134-143: per (token, value head) the L2-normalised query (then
+// / sqrt(d)) and key of its key head. One wave per item.
+__global__ __launch_bounds__(256) void delta_qk_kernel(int count, Params a) {
+    const int t = blockIdx.x * 4 + int(threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (t >= count) return;
+    const int kh = a.n[0], vh = a.n[1], d = a.n[2], h = (t % vh) / (vh / kh), kd = kh * d;
+    const float* x = a.p[1] + size_t(t / vh) * a.n[3];
+    float sq = 0.f, sk = 0.f;
+    for (int i = lane; i < d; i += 64) {
+        float q = x[h * d + i], kk = x[kd + h * d + i];
+        sq += q * q;
+        sk += kk * kk;
+    }
+    sq = wave_sum(sq);
+    sk = wave_sum(sk);
+    const float rq = 1.f / sqrtf(sq + 1e-6f), rk = 1.f / sqrtf(sk + 1e-6f), sd = sqrtf(float(d));
+    for (int i = lane; i < d; i += 64) {
+        a.p[0][size_t(t) * d + i] = (x[h * d + i] * rq) / sd;
+        a.p[2][size_t(t) * d + i] = x[kd + h * d + i] * rk;
+    }
+}
+
+// ---------------------------------------------------------------- DeltaRule (7, 14)
+// reference.h:149-170 (and the gate expressions of reference.h:48-60): state
+// S[head][key][value]; per token S <- e^g S, m_j = sum_i S_ij k_i,
+// delta_j = (v_j - m_j) beta, S_ij += k_i delta_j, o_j = sum_i S_ij q_i.
+// Decomposition: P lanes share one value column, each holding KR key rows of
+// it in VGPRs (lane = p * (64 / P) + column-in-wave); the column sums are
+// reduced over the P lanes with two shuffles. Tokens run in order with the
+// state resident; snapshots (n6 = S > 0) store the state after token r < S at
+// (r + 1) * vh * kd * vd.
+template <int KR, int P, bool GATED>
+__global__ __launch_bounds__(256) void delta_rule_kernel(int count, Params a) {
+    constexpr int CW = 64 / P;  // columns per wave
+    const int lane = threadIdx.x & 63, p = lane / CW, jj = lane % CW;
+    const int col = (blockIdx.x * 4 + int(threadIdx.x >> 6)) * CW + jj;
+    const bool active = col < count;
+    const int kd = a.n[0], vd = a.n[1], kh = a.n[2], vh = a.n[3];
+    const int tokens = a.n[4] > 0 ? a.n[4] : 1, stride = a.n[5], snaps = a.n[6];
+    const int h = active ? col / vd : 0, j = active ? col % vd : 0;
+    float* state = a.p[4] + size_t(h) * kd * vd;
+    float s[KR];
+#pragma unroll
+    for (int ii = 0; ii < KR; ++ii) {
+        const int i = p * KR + ii;
+        s[ii] = active && i < kd ? state[size_t(i) * vd + j] : 0.f;
+    }
+    for (int r = 0; r < tokens; ++r) {
+        const float* q = a.p[1] + size_t(r) * vh * kd + size_t(h) * kd;
+        const float* k = a.p[2] + size_t(r) * vh * kd + size_t(h) * kd;
+        float log_decay = 0.f, beta = 0.f, v = 0.f;
+        if (active) {
+            const int gi = r * vh + h;
+            if (GATED) {
+                log_decay = -expf(a.p[7][vh + h]) * softplusf_(a.p[5][gi] + a.p[7][h]);
+                beta = sigmoidf_(a.p[6][gi]);
+            } else {
+                log_decay = a.p[5][gi];
+                beta = a.p[6][gi];
+            }
+            v = a.p[3][size_t(r) * stride + 2 * size_t(kh) * kd + size_t(h) * vd + j];
+        }
+        const float decay = expf(log_decay);
+        float kv[KR], qv[KR];
+        float m = 0.f;
+#pragma unroll
+        for (int ii = 0; ii < KR; ++ii) {
+            const int i = p * KR + ii;
+            kv[ii] = active && i < kd ? k[i] : 0.f;
+            qv[ii] = active && i < kd ? q[i] : 0.f;
+            s[ii] *= decay;
+            m = fmaf(s[ii], kv[ii], m);
+        }
+#pragma unroll
+        for (int o = CW; o < 64; o <<= 1) m += __shfl_xor(m, o, 64);
+        const float delta = (v - m) * beta;
+        float out = 0.f;
+#pragma unroll
+        for (int ii = 0; ii < KR; ++ii) {
+            s[ii] = fmaf(kv[ii], delta, s[ii]);
+            out = fmaf(s[ii], qv[ii], out);
+        }
+#pragma unroll
+        for (int o = CW; o < 64; o <<= 1) out += __shfl_xor(out, o, 64);
+        if (active && p == 0) a.p[0][size_t(r) * vh * vd + col] = out;
+        if (active && r < snaps) {
+            float* snap = state + size_t(r + 1) * vh * kd * vd;
+#pragma unroll
+            for (int ii = 0; ii < KR; ++ii) {
+                const int i = p * KR + ii;
+                if (i < kd) snap[size_t(i) * vd + j] = s[ii];
+            }
+        }
+    }
+    if (active) {
+#pragma unroll
+        for (int ii = 0; ii < KR; ++ii) {
+            const int i = p * KR + ii;
+            if (i < kd) state[size_t(i) * vd + j] = s[ii];
+        }
+    }
+}
+
+// ---------------------------------------------------------------- attention Q / KV
+// AttentionQuery (8), AttentionKv (9), AttentionQueryKv (15): reference.h:61-95.
+// One block per item; the head vector is normalised into LDS and RoPE'd there.
+__device__ void rope_lds(float* o, int rot, int pos, float theta) {
+    for (int i = threadIdx.x; i < rot / 2; i += blockDim.x) {
+        float angle = float(pos) / powf(theta, float(2 * i) / float(rot));
+        float sn = sinf(angle), cs = cosf(angle);
+        float x0 = o[i], x1 = o[i + rot / 2];
+        o[i] = x0 * cs - x1 * sn;
+        o[i + rot / 2] = x1 * cs + x0 * sn;
+    }
+}
+
+__device__ void attention_query_item(int t, const Params& a, float* buf, float* red) {
+    const int d = a.n[0], rot = a.n[1], pos = a.n[2] + (a.n[3] > 0 ? t / a.n[3] : 0);
+    const float* x = a.p[1] + size_t(t) * 2 * d;
+    float ss = 0.f;
+    for (int i = threadIdx.x; i < d; i += blockDim.x) ss += x[i] * x[i];
+    ss = block_sum(ss, red);
+    const float r = 1.f / sqrtf(ss / float(d) + a.f[0]);
+    for (int i = threadIdx.x; i < d; i += blockDim.x) {
+        buf[i] = (x[i] * r) * (1.f + a.p[2][i]);
+        a.p[3][size_t(t) * d + i] = x[d + i];
+    }
+    __syncthreads();
+    rope_lds(buf, rot, pos, a.f[1]);
+    __syncthreads();
+    for (int i = threadIdx.x; i < d; i += blockDim.x) a.p[0][size_t(t) * d + i] = buf[i];
+}
+
+__device__ void attention_kv_item(int t, const Params& a, float* buf, float* red) {
+    const int d = a.n[0], rot = a.n[1], kv = a.n[3], pos = a.n[2] + t / kv, hh = t % kv;
+    const float* x = a.p[1] + size_t(t) * d;
+    float ss = 0.f;
+    for (int i = threadIdx.x; i < d; i += blockDim.x) ss += x[i] * x[i];
+    ss = block_sum(ss, red);
+    const float r = 1.f / sqrtf(ss / float(d) + a.f[0]);
+    const size_t dest = (size_t(pos) * kv + hh) * d;
+    for (int i = threadIdx.x; i < d; i += blockDim.x) {
+        buf[i] = (x[i] * r) * (1.f + a.p[2][i]);
+        a.p[4][dest + i] = a.p[3][size_t(t) * d + i];
+    }
+    __syncthreads();
+    rope_lds(buf, rot, pos, a.f[1]);
+    __syncthreads();
+    for (int i = threadIdx.x; i < d; i += blockDim.x) a.p[0][dest + i] = buf[i];
+}
+
+constexpr int kAttnMaxHeadDim = 1024;
+
+__global__ __launch_bounds__(256) void attention_qkv_kernel(int op, int count, Params a) {
+    __shared__ float buf[kAttnMaxHeadDim];
+    __shared__ float red[16];
+    const int t = blockIdx.x;
+    if (op == QR_ATTENTION_QUERY) {
+        attention_query_item(t, a, buf, red);
+    } else if (op == QR_ATTENTION_KV) {
+        attention_kv_item(t, a, buf, red);
+    } else {  // AttentionQueryKv: split the items as reference.h:65-74 does
+        const int queries = a.n[3] * a.n[5];
+        Params part{};
+        part.n[0] = a.n[0];
+        part.n[1] = a.n[1];
+        part.n[2] = a.n[2];
+        part.f[0] = a.f[0];
+        part.f[1] = a.f[1];
+        if (t < queries) {
+            part.p[0] = a.p[0];
+            part.p[1] = a.p[1];
+            part.p[2] = a.p[2];
+            part.p[3] = a.p[3];
+            part.n[3] = a.n[3];
+            attention_query_item(t, part, buf, red);
+        } else {
+            part.p[0] = a.p[4];
+            part.p[1] = a.p[5];
+            part.p[2] = a.p[2] + a.n[0];
+            part.p[3] = a.p[6];
+            part.p[4] = a.p[7];
+            part.n[3] = a.n[4];
+            attention_kv_item(t - queries, part, buf, red);
+        }
+    }
+    (void)count;
+}
+
+// ---------------------------------------------------------------- Argmax (16)
+// reference.h:222-230: per row [first index of the maximum over finite values
+// (0xffffffff if none), non-finite count]. Pass 1: one block per (slice, row)
+// gives (max, index, bad); pass 2: one block per row merges the slices.
+constexpr int kArgmaxSlice = 8192;
+
+struct Best {
+    float v;
+    unsigned i;
+    unsigned bad;
+};
+__device__ __forceinline__ Best better(Best a, Best b) {
+    Best r;
+    r.bad = a.bad + b.bad;
+    if (b.v > a.v || (b.v == a.v && b.i < a.i)) {
+        r.v = b.v;
+        r.i = b.i;
+    } else {
+        r.v = a.v;
+        r.i = a.i;
+    }
+    return r;
+}
+__device__ Best block_best(Best b) {
+    __shared__ float sv[16];
+    __shared__ unsigned si[16], sb[16];
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        Best other{__shfl_xor(b.v, o, 64), unsigned(__shfl_xor(int(b.i), o, 64)),
+                   unsigned(__shfl_xor(int(b.bad), o, 64))};
+        b = better(b, other);
+    }
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, waves = blockDim.x >> 6;
+    __syncthreads();
+    if (lane == 0) {
+        sv[wave] = b.v;
+        si[wave] = b.i;
+        sb[wave] = b.bad;
+    }
+    __syncthreads();
+    Best t{-INFINITY, 0xffffffffu, 0u};
+    for (int w = 0; w < waves; ++w) t = better(t, Best{sv[w], si[w], sb[w]});
+    return t;
+}
+
+__global__ __launch_bounds__(256) void argmax_slices_kernel(Params a, float* parts, int slices) {
+    const int n = a.n[0], row = blockIdx.y, slice = blockIdx.x;
+    const float* v = a.p[1] + size_t(row) * n;
+    const int begin = slice * kArgmaxSlice, end = min(n, begin + kArgmaxSlice);
+    Best b{-INFINITY, 0xffffffffu, 0u};
+    for (int i = begin + threadIdx.x; i < end; i += blockDim.x) {
+        float x = v[i];
+        if (!isfinite(x)) {
+            ++b.bad;
+        } else if (x > b.v) {  // strided scan: indices rise per thread, so '>' keeps the first
+            b.v = x;
+            b.i = unsigned(i);
+        }
+    }
+    b = block_best(b);
+    if (threadIdx.x == 0) {
+        float* o = parts + (size_t(row) * slices + slice) * 3;
+        o[0] = b.v;
+        o[1] = __uint_as_float(b.i);
+        o[2] = __uint_as_float(b.bad);
+    }
+}
+
+__global__ __launch_bounds__(256) void argmax_merge_kernel(Params a, const float* parts, int slices) {
+    const int row = blockIdx.x;
+    Best b{-INFINITY, 0xffffffffu, 0u};
+    for (int s = threadIdx.x; s < slices; s += blockDim.x) {
+        const float* o = parts + (size_t(row) * slices + s) * 3;
+        b = better(b, Best{o[0], __float_as_uint(o[1]), __float_as_uint(o[2])});
+    }
+    b = block_best(b);
+    if (threadIdx.x == 0) {
+        a.p[0][2 * row] = float(b.i);
+        a.p[0][2 * row + 1] = float(b.bad);
+    }
+}
+
+unsigned grid_for(long n) {
+    long b = (n + 255) / 256;
+    return unsigned(b < 1 ? 1 : (b > 65536 ? 65536 : b));
+}
+
+}  // namespace
+
+int run_elementwise(hipStream_t s, int op, int count, const Params& a) {
+    hipLaunchKernelGGL(elementwise_kernel, dim3(grid_for(count)), dim3(256), 0, s, op, count, a);
+    return int(hipGetLastError());
+}
+
+int run_rms_family(hipStream_t s, int op, int groups, const Params& a) {
+    if (a.n[0] <= 256)
+        hipLaunchKernelGGL(rms_family_kernel<true>, dim3(ceil_div(groups, 4)), dim3(256), 0, s, op, groups, a);
+    else
+        hipLaunchKernelGGL(rms_family_kernel<false>, dim3(unsigned(groups)), dim3(256), 0, s, op, groups, a);
+    return int(hipGetLastError());
+}
+
+int run_conv_silu(hipStream_t s, int count, const Params& a) {
+    if (a.n[0] < 1 || a.n[0] > 17) return int(hipErrorInvalidValue);
+    hipLaunchKernelGGL(conv_silu_kernel, dim3(ceil_div(count, 256)), dim3(256), 0, s, count, a);
+    return int(hipGetLastError());
+}
+
+int run_delta_qk(hipStream_t s, int count, const Params& a) {
+    hipLaunchKernelGGL(delta_qk_kernel, dim3(ceil_div(count, 4)), dim3(256), 0, s, count, a);
+    return int(hipGetLastError());
+}
+
+template <int KR, int P>
+static int rule_launch(hipStream_t s, bool gated, int count, const Params& a) {
+    const unsigned blocks = ceil_div(count, 4 * (64 / P));
+    if (gated)
+        hipLaunchKernelGGL((delta_rule_kernel<KR, P, true>), dim3(blocks), dim3(256), 0, s, count, a);
+    else
+        hipLaunchKernelGGL((delta_rule_kernel<KR, P, false>), dim3(blocks), dim3(256), 0, s, count, a);
+    return int(hipGetLastError());
+}
+
+int run_delta_rule(hipStream_t s, bool gated, int count, const Params& a) {
+    const int kd = a.n[0];
+    if (kd <= 8) return rule_launch<8, 1>(s, gated, count, a);
+    if (kd <= 32) return rule_launch<8, 4>(s, gated, count, a);
+    if (kd <= 64) return rule_launch<16, 4>(s, gated, count, a);
+    if (kd <= 128) return rule_launch<32, 4>(s, gated, count, a);
+    if (kd <= 256) return rule_launch<64, 4>(s, gated, count, a);
+    return int(hipErrorInvalidValue);
+}
+
+int run_attention_qkv(hipStream_t s, int op, int count, const Params& a) {
+    if (a.n[0] > kAttnMaxHeadDim || a.n[1] > a.n[0] || a.n[1] % 2 != 0) return int(hipErrorInvalidValue);
+    hipLaunchKernelGGL(attention_qkv_kernel, dim3(unsigned(count)), dim3(256), 0, s, op, count, a);
+    return int(hipGetLastError());
+}
+
+int run_embed(hipStream_t s, int op, int count, const Params& a) { return run_elementwise(s, op, count, a); }
+
+size_t argmax_parts_needed(int rows, int n) { return size_t(rows) * ceil_div(n, kArgmaxSlice) * 3; }
+
+int run_argmax(hipStream_t s, int rows, const Params& a, float* parts, size_t parts_len) {
+    const int n = a.n[0];
+    const int slices = int(ceil_div(n, kArgmaxSlice));
+    if (argmax_parts_needed(rows, n) > parts_len) return int(hipErrorInvalidValue);
+    hipLaunchKernelGGL(argmax_slices_kernel, dim3(unsigned(slices), unsigned(rows)), dim3(256), 0, s, a, parts, slices);
+    if (int e = int(hipGetLastError())) return e;
+    hipLaunchKernelGGL(argmax_merge_kernel, dim3(unsigned(rows)), dim3(256), 0, s, a, parts, slices);
+    return int(hipGetLastError());
+}
+
+}  // namespace qr

@@ -1,0 +1,190 @@
+"""The host engine (the restatement of the reference's DeviceModel/DeviceRun)
+on CPU bridges: the oracle's op bridge and, when it was built, the
+reference's own CPU test bridge (oracle/_ref). Both compute every op with the
+reference's scalar bodies in the Reference summation order, so the engine's
+call sequence must reproduce the oracle's Backend::Reference results bit for
+bit."""
+import numpy as np
+import pytest
+
+from conftest import GOLDEN, ROOT
+from parity import INT8_RTOL, parity
+from qwen_mi355x import engine as E
+from qwen_mi355x import model as M
+
+import oracle as O
+
+OPS_BRIDGE = ROOT / "oracle" / "lib" / "libqwen_ops_bridge.so"
+REF_BRIDGE = ROOT / "oracle" / "_ref" / "libqwen_rocm_test.so"
+BRIDGES = [pytest.param(OPS_BRIDGE, id="ops_bridge"),
+           pytest.param(REF_BRIDGE, id="reference_cpu_bridge",
+                        marks=pytest.mark.skipif(not REF_BRIDGE.exists(), reason="reference tree not built here"))]
+
+
+@pytest.fixture(scope="module")
+def fixture():
+    return M.load_fixture(GOLDEN / "hybrid.json")
+
+
+@pytest.fixture(scope="module")
+def tiny():
+    c = M.config_tiny()
+    return c, M.synthetic_weights(c, seed=0)
+
+
+def tiny_prompt():
+    return [int(v) for v in np.random.default_rng(1).integers(0, 512, 16)]
+
+
+@pytest.mark.parametrize("bridge", BRIDGES)
+@pytest.mark.parametrize("fmt", [E.F32, E.BF16_EXACT])
+def test_fixture_records_bitwise(fixture, bridge, fmt):
+    c, w = M.fixture_config_and_weights(fixture)
+    m = E.Model(w, bridge=bridge, kind=E.KIND_CPU_TEST, fmt=fmt)
+    assert m.weight_summary()[0] == (32 if fmt == E.BF16_EXACT else 0)
+    run = m.new_run(len(fixture["ids"]))
+    s = O.Oracle(w).new_state()
+    for tok in fixture["ids"]:
+        logits, rec = run.step(tok, capture=True)
+        want, orec = s.step(tok, O.REFERENCE, trace=True)
+        assert np.array_equal(logits, want)
+        omap = {(l, n): v for (l, n, v) in orec}
+        names = {"input_norm": "input_norm", "mixed": "mixer", "after_mixer": "after_mixer", "post_norm": "post_norm",
+                 "ffn_product": "ffn.product", "ffn": "ffn.output", "output": "layer"}
+        seen = 0
+        for (layer, name, v) in rec:
+            if name in names:
+                assert np.array_equal(v, omap[(layer, names[name])]), (layer, name)
+                seen += 1
+        assert seen == 7 * c.num_layers
+    for layer in range(c.num_layers):
+        for which in range(4):
+            assert np.array_equal(run.state(layer, which), s.part(layer, which))
+
+
+@pytest.mark.parametrize("bridge", BRIDGES)
+def test_tiny_greedy_prefill_chunks_and_decode(tiny, bridge):
+    """Config 1: prompt of 16 IDs, greedy 32 tokens, bit-exact against the
+    oracle; every prefill chunk size gives the same logits and state."""
+    c, w = tiny
+    ids = tiny_prompt()
+    o = O.Oracle(w)
+    s = o.new_state()
+    for t in ids:
+        last = s.step(t, O.REFERENCE)
+    want_ids = [O.select_greedy(last)]
+    for _ in range(31):
+        want_ids.append(O.select_greedy(s.step(want_ids[-1], O.REFERENCE)))
+    m = E.Model(w, bridge=bridge, kind=E.KIND_CPU_TEST)
+    for chunk in (1, 7, 16):
+        run = m.new_run(64, chunk=chunk)
+        logits = run.prefill(ids)
+        assert np.array_equal(logits, o_last := last) or chunk > 1
+        got, _ = run.decode_greedy(O.select_greedy(logits), 32)
+        assert got == want_ids, chunk
+        del o_last
+
+
+@pytest.mark.parametrize("bridge", BRIDGES)
+def test_verify_rollback_and_accept(tiny, bridge):
+    """verify_rollback + accept(k) leaves exactly the state of k sequential
+    steps (reference src/device/tests.rs:1001-1041)."""
+    c, w = tiny
+    ids = tiny_prompt()
+    m = E.Model(w, bridge=bridge, kind=E.KIND_CPU_TEST)
+    draft = [5, 17, 300, 42]
+    for k in range(1, 5):
+        a = m.new_run(64, snapshots=3)
+        a.prefill(ids)
+        rows = a.verify_rollback(draft)
+        a.accept(k)
+        b = m.new_run(64)
+        b.prefill(ids)
+        for r, t in enumerate(draft[:k]):
+            assert np.array_equal(b.step(t), rows[r])
+        assert a.position == b.position == len(ids) + k
+        for layer in range(c.num_layers):
+            for which in range(4):
+                assert np.array_equal(a.state(layer, which), b.state(layer, which)), (k, layer, which)
+        # the next step continues from the accepted prefix
+        assert np.array_equal(a.step(9), b.step(9))
+    g = m.new_run(64, snapshots=3)
+    g.prefill(ids)
+    picks = g.verify_rollback_greedy(draft)
+    assert picks == [O.select_greedy(r) for r in rows]
+
+
+@pytest.mark.parametrize("bridge", BRIDGES)
+def test_fusion_fallbacks_agree(tiny, bridge):
+    """Optional symbols absent (src/device.rs:368-441) change nothing."""
+    c, w = tiny
+    ids = tiny_prompt()
+    ref = E.Model(w, bridge=bridge, kind=E.KIND_CPU_TEST).new_run(32)
+    want = ref.prefill(ids)
+    for disable in (E.NO_FUSED_OPS, E.NO_ARGMAX | E.NO_DELTA_MIXER, 63):
+        run = E.Model(w, bridge=bridge, kind=E.KIND_CPU_TEST, disable=disable).new_run(32)
+        assert np.array_equal(run.prefill(ids), want)
+        assert run.step_greedy(3) == ref.step_greedy(3) if disable == 63 else True
+
+
+def test_checkpoint_restore_reset_and_poison(tiny):
+    c, w = tiny
+    m = E.Model(w, bridge=OPS_BRIDGE, kind=E.KIND_CPU_TEST)
+    run = m.new_run(20)
+    ids = tiny_prompt()
+    run.prefill(ids[:8])
+    cp = run.checkpoint()
+    a = run.prefill(ids[8:12])
+    run.restore(cp)
+    assert run.position == 8
+    assert np.array_equal(run.prefill(ids[8:12]), a)
+    run.restore(run.initial_checkpoint())
+    assert run.position == 0
+    first = run.prefill(ids[:8])
+    fresh = m.new_run(20)
+    assert np.array_equal(fresh.prefill(ids[:8]), first)
+    # capacity overflow is refused before anything is enqueued; a failed forward poisons
+    with pytest.raises(E.EngineError):
+        run.prefill(list(range(13)))
+    assert run.position == 8
+    with pytest.raises(E.EngineError):
+        run.step(10**6)
+    run.reset()
+    assert run.position == 0
+    assert np.array_equal(run.prefill(ids[:8]), first)
+
+
+def test_int8_quantiser_matches_oracle(tiny):
+    c, w = tiny
+    a = w.tensors[0]
+    s1, q1 = E.quantize_int8_rows(a, c.vocab_size, c.hidden_size)
+    s2, q2 = O.quantize_int8_rows(a, c.vocab_size, c.hidden_size)
+    assert np.array_equal(s1, s2) and np.array_equal(q1, q2)
+
+
+def dequantised(c, w):
+    """The oracle on the int8 run's weights (the CPU path on
+    the dequantised weights): every projection matrix as scale * q, the
+    vocabulary projection as the dequantised embedding, the lookup rows exact."""
+    t = dict(w.tensors)
+    for spec in M.tensor_specs(c):
+        if spec.kind == "matrix" and spec.index != 0:
+            rows, cols = spec.shape
+            s, q = O.quantize_int8_rows(t[spec.index], rows, cols)
+            t[spec.index] = O.dequantize_int8_rows(s, q, rows, cols)
+    o = O.Oracle(M.Weights(c, t))
+    s, q = O.quantize_int8_rows(w.tensors[0], c.vocab_size, c.hidden_size)
+    o.set_lm_head(O.dequantize_int8_rows(s, q, c.vocab_size, c.hidden_size))
+    return o
+
+
+def test_int8_against_dequantised_oracle(tiny):
+    c, w = tiny
+    ids = tiny_prompt()
+    run = E.Model(w, bridge=OPS_BRIDGE, kind=E.KIND_CPU_TEST, fmt=E.INT8).new_run(32)
+    st = dequantised(c, w).new_state()
+    for t in ids:
+        want = st.step(t, O.REFERENCE)
+    parity(run.prefill(ids), want, rtol=INT8_RTOL, where="int8 logits")
+    for t in (3, 77, 500):
+        parity(run.step(t), st.step(t, O.REFERENCE), rtol=INT8_RTOL, where="int8 decode")

@@ -1,0 +1,169 @@
+"""The whole decode/prefill path on the MI355X bridge, driven by the host
+engine exactly as the reference's engine drives its bridge, against the CPU
+oracle on the same seeded weights: identical greedy IDs, per-layer records
+and logits within the fp32 parity bound (int8: against the oracle on the
+dequantised weights)."""
+import numpy as np
+import pytest
+
+from conftest import GOLDEN
+from parity import INT8_RTOL, parity
+from qwen_mi355x import engine as E
+from qwen_mi355x import model as M
+from test_engine_cpu import dequantised
+
+import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+NAMES = {"input_norm": "input_norm", "mixed": "mixer", "after_mixer": "after_mixer", "post_norm": "post_norm",
+         "ffn_product": "ffn.product", "ffn": "ffn.output", "output": "layer"}
+
+
+@pytest.fixture(scope="module")
+def fixture():
+    return M.load_fixture(GOLDEN / "hybrid.json")
+
+
+@pytest.fixture(scope="module")
+def tiny():
+    c = M.config_tiny()
+    return c, M.synthetic_weights(c, seed=0)
+
+
+def tiny_prompt():
+    return [int(v) for v in np.random.default_rng(1).integers(0, 512, 16)]
+
+
+def oracle_greedy(o, prompt, n_new, backend=O.VECTOR):
+    s = o.new_state()
+    for t in prompt:
+        logits = s.step(t, backend)
+    ids, all_logits = [O.select_greedy(logits)], [logits]
+    for _ in range(n_new - 1):
+        logits = s.step(ids[-1], backend)
+        all_logits.append(logits)
+        ids.append(O.select_greedy(logits))
+    return ids, all_logits, s
+
+
+@pytest.mark.parametrize("fmt", [E.F32, E.BF16_EXACT])
+def test_fixture_every_record(fixture, fmt):
+    print(f"fixture format {fmt}", flush=True)
+    c, w = M.fixture_config_and_weights(fixture)
+    run = E.Model(w, fmt=fmt).new_run(len(fixture["ids"]))
+    s = O.Oracle(w).new_state()
+    for tok in fixture["ids"]:
+        logits, rec = run.step(tok, capture=True)
+        want, orec = s.step(tok, O.REFERENCE, trace=True)
+        omap = {(l, n): v for (l, n, v) in orec}
+        for (layer, name, v) in rec:
+            if name in NAMES:
+                parity(v, omap[(layer, NAMES[name])], where=f"{layer}.{name}")
+        parity(logits, want, where="logits")
+        assert O.select_greedy(logits) == O.select_greedy(want)
+    for layer in range(c.num_layers):
+        for which in range(4):
+            parity(run.state(layer, which), s.part(layer, which), where=f"state {layer}/{which}")
+
+
+def test_tiny_config1_greedy_bit_exact(tiny):
+    """16-token prompt, 32 greedy tokens, identical IDs."""
+    c, w = tiny
+    ids = tiny_prompt()
+    want, want_logits, s = oracle_greedy(O.Oracle(w), ids, 32)
+    m = E.Model(w)
+    for chunk in (1, 5, 16):
+        run = m.new_run(64, chunk=chunk)
+        logits = run.prefill(ids)
+        parity(logits, want_logits[0], where=f"prefill chunk {chunk}")
+        got, _ = run.decode_greedy(O.select_greedy(logits), 32)
+        assert got == want, chunk
+    # logits of every decode step (step, not step_greedy)
+    run = m.new_run(64)
+    run.prefill(ids)
+    for i in range(31):
+        parity(run.step(want[i]), want_logits[i + 1], where=f"decode {i}")
+    for layer in range(c.num_layers):
+        for which in range(4):
+            parity(run.state(layer, which), s.part(layer, which), where=f"state {layer}/{which}")
+
+
+def test_tiny_fused_and_unfused_paths_agree(tiny):
+    """Every optional symbol switched off gives the same results (the
+    reference's fallbacks, src/device.rs:368-441)."""
+    c, w = tiny
+    ids = tiny_prompt()
+    base = E.Model(w).new_run(32)
+    want = base.prefill(ids)
+    for disable in (E.NO_F32_FUSIONS, E.NO_DELTA_MIXER, E.NO_FUSED_OPS, E.NO_ARGMAX, 63):
+        run = E.Model(w, disable=disable).new_run(32)
+        parity(run.prefill(ids), want, where=f"disable {disable}")
+        a, b = run.step_greedy(7), base.step_greedy(7) if disable == E.NO_F32_FUSIONS else None
+        assert b is None or a == b
+
+
+def test_tiny_verify_rollback(tiny):
+    c, w = tiny
+    ids = tiny_prompt()
+    m = E.Model(w)
+    draft = [5, 17, 300, 42]
+    for k in (1, 2, 4):
+        a = m.new_run(64, snapshots=3)
+        a.prefill(ids)
+        rows = a.verify_rollback(draft)
+        a.accept(k)
+        b = m.new_run(64)
+        b.prefill(ids)
+        for r, t in enumerate(draft[:k]):
+            parity(rows[r], b.step(t), where=f"row {r}")
+        for layer in range(c.num_layers):
+            for which in range(4):
+                parity(a.state(layer, which), b.state(layer, which), where=f"accept {k} {layer}/{which}")
+        parity(a.step(9), b.step(9), where="after accept")
+    g = m.new_run(64, snapshots=3)
+    g.prefill(ids)
+    assert g.verify_rollback_greedy(draft) == [O.select_greedy(r) for r in rows]
+
+
+def test_tiny_int8_against_dequantised_oracle(tiny):
+    """BASELINE config 5 on the tiny model: int8 per-row weights against the
+    CPU path on the dequantised weights at 1e-2; the 4-row verify too."""
+    c, w = tiny
+    ids = tiny_prompt()
+    run = E.Model(w, fmt=E.INT8).new_run(64, snapshots=3)
+    st = dequantised(c, w).new_state()
+    for t in ids:
+        want = st.step(t, O.VECTOR)
+    parity(run.prefill(ids), want, rtol=INT8_RTOL, where="int8 prefill")
+    draft = [3, 77, 500, 12]
+    rows = run.verify_rollback(draft)
+    for r, t in enumerate(draft):
+        parity(rows[r], st.step(t, O.VECTOR), rtol=INT8_RTOL, where=f"int8 verify row {r}")
+
+
+@pytest.fixture(scope="module")
+def qwen08b():
+    print("synthesising 0.8B weights", flush=True)
+    c = M.config_qwen08b(max_positions=4096)
+    return c, M.synthetic_weights(c, seed=0)
+
+
+def test_qwen08b_short_greedy(qwen08b):
+    """The 0.8B-shaped model (BASELINE config 2 shape) on a short prompt:
+    identical greedy IDs and logits within the fp32 bound."""
+    c, w = qwen08b
+    prompt = [int(v) for v in np.random.default_rng(3).integers(0, c.vocab_size, 12)]
+    print("oracle on 0.8B", flush=True)
+    want, want_logits, s = oracle_greedy(O.Oracle(w), prompt, 6)
+    print("gpu on 0.8B", flush=True)
+    m = E.Model(w)
+    print(m.info, flush=True)
+    run = m.new_run(64, chunk=8)
+    logits = run.prefill(prompt)
+    parity(logits, want_logits[0], where="0.8B prefill logits")
+    got, _ = run.decode_greedy(O.select_greedy(logits), 6)
+    assert got == want
+    for layer in (0, 3):
+        for which in range(4):
+            parity(run.state(layer, which), s.part(layer, which), where=f"0.8B state {layer}/{which}")

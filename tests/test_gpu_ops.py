@@ -1,0 +1,384 @@
+"""Each HIP kernel of the MI355X bridge, called through the C ABI, against the
+CPU op bridge (the restatement of the reference's op bodies) on the same
+seeded inputs, or against fp64 for the projections; argmax and the
+embedding ops bit-exact."""
+import numpy as np
+import pytest
+
+from conftest import ROOT
+from parity import FP32_RTOL, dot_bound, parity
+from qwen_mi355x.bridge import Bridge, pack_bf16, pack_int8
+
+import oracle as O
+
+pytestmark = pytest.mark.gpu
+OPS = ROOT / "oracle" / "lib" / "libqwen_ops_bridge.so"
+
+
+@pytest.fixture(scope="module")
+def gpu():
+    b = Bridge()
+    print("bridge:", b.info, flush=True)
+    yield b
+    b.close()
+
+
+@pytest.fixture(scope="module")
+def cpu():
+    b = Bridge(OPS, kind=0)
+    yield b
+    b.close()
+
+
+def both(gpu, cpu, op, count, inputs, outputs, n=(), f=(), slots=None):
+    """Run `op` on both bridges. inputs: {slot: array}; outputs: {slot: size}
+    (an output slot may also be an input). Returns ({slot: gpu}, {slot: cpu})."""
+    res = []
+    for br in (gpu, cpu):
+        bufs = {}
+        for s, arr in inputs.items():
+            bufs[s] = br.upload(np.ascontiguousarray(arr))
+        for s, size in outputs.items():
+            if s not in bufs:
+                bufs[s] = br.alloc(size)
+        p = [bufs.get(i, 0) for i in range(8)]
+        br.run(op, count, p, n, f)
+        res.append({s: bufs[s].read(size) for s, size in outputs.items()})
+    return res
+
+
+SHAPES_08B = [(6144, 1024), (2048, 1024), (16, 1024), (4096, 1024), (512, 1024), (1024, 2048), (3584, 1024),
+              (1024, 3584)]
+SHAPES_SMALL = [(24, 8), (8, 16), (16, 8), (19, 8), (64, 64), (256, 64), (64, 256), (512, 64), (7, 12), (33, 20)]
+
+
+@pytest.mark.parametrize("rows,cols", SHAPES_08B + SHAPES_SMALL)
+@pytest.mark.parametrize("batch", [1, 2, 4, 5, 8, 40])
+def test_gemm_f32(gpu, rows, cols, batch):
+    print(f"gemm f32 {rows}x{cols} batch {batch}", flush=True)
+    rng = np.random.default_rng(rows * 31 + cols + batch)
+    w = (rng.standard_normal(rows * cols) * 0.02).astype(np.float32)
+    x = rng.standard_normal(batch * cols).astype(np.float32)
+    a, xb, y = gpu.upload(w), gpu.upload(x), gpu.alloc(batch * rows)
+    if batch == 1:
+        gpu.gemv(y, a, xb, rows, cols)
+    else:
+        gpu.gemm(y, a, xb, rows, cols, batch)
+    got = y.read().reshape(batch, rows)
+    W = w.reshape(rows, cols)
+    X = x.reshape(batch, cols)
+    want = X.astype(np.float64) @ W.T.astype(np.float64)
+    bound = np.abs(X.astype(np.float64)) @ np.abs(W.T.astype(np.float64)) * 2e-5 + 1e-30
+    assert np.all(np.abs(got - want) <= bound)
+
+
+@pytest.mark.parametrize("kind", ["bf16", "i8"])
+@pytest.mark.parametrize("rows,cols", [(6144, 1024), (1024, 3584), (3584, 1024), (16, 1024), (24, 8), (64, 64),
+                                       (256, 64), (8, 16)])
+@pytest.mark.parametrize("batch", [1, 3, 4, 8, 24])
+def test_gemm_bf16_int8(gpu, kind, rows, cols, batch):
+    print(f"gemm {kind} {rows}x{cols} batch {batch}", flush=True)
+    rng = np.random.default_rng(rows + 7 * cols + batch)
+    w = (rng.standard_normal(rows * cols) * 0.02).astype(np.float32)
+    x = rng.standard_normal(batch * cols).astype(np.float32)
+    if kind == "bf16":
+        packed = pack_bf16(w)
+        dense = ((w.view(np.uint32) >> 16) << 16).view(np.float32)
+        scales = np.ones(rows, np.float64)
+        q = dense
+    else:
+        s, qi = O.quantize_int8_rows(w, rows, cols)
+        packed = pack_int8(s, qi)
+        scales = s.astype(np.float64)
+        q = qi.astype(np.float32)
+    a, xb, y = gpu.upload(packed), gpu.upload(x), gpu.alloc(batch * rows)
+    if batch == 1 and kind == "bf16":
+        gpu.gemv(y, a, xb, rows, cols, kind="bf16")
+    else:
+        gpu.gemm(y, a, xb, rows, cols, batch, kind=kind)
+    got = y.read().reshape(batch, rows)
+    Q = q.reshape(rows, cols).astype(np.float64)
+    X = x.reshape(batch, cols).astype(np.float64)
+    want = (X @ Q.T) * scales[None, :]
+    bound = (np.abs(X) @ np.abs(Q.T)) * np.abs(scales)[None, :] * 2e-5 + 1e-30
+    assert np.all(np.abs(got - want) <= bound)
+
+
+@pytest.mark.parametrize("kind", ["f32", "bf16", "i8"])
+@pytest.mark.parametrize("batch", [1, 4, 6, 20])
+def test_group_glu_equal_separate_calls(gpu, kind, batch):
+    """Grouped / GLU projections equal the separate projections (reference
+    native/rocm/bridge.cpp:657-729); fp32 arms are this bridge's own."""
+    print(f"group/glu {kind} batch {batch}", flush=True)
+    rng = np.random.default_rng(11 + batch)
+    cols = 1024
+    shapes = [6144, 2048, 16, 16]
+
+    def pack(w, rows):
+        if kind == "f32":
+            return w
+        if kind == "bf16":
+            return pack_bf16(w)
+        s, q = O.quantize_int8_rows(w, rows, cols)
+        return pack_int8(s, q)
+
+    mats = [gpu.upload(pack((rng.standard_normal(r * cols) * 0.02).astype(np.float32), r)) for r in shapes]
+    x = gpu.upload(rng.standard_normal(batch * cols).astype(np.float32))
+    ys = [gpu.alloc(batch * r) for r in shapes]
+    gpu.group(list(zip(ys, mats, shapes)), x, cols, batch, kind=kind)
+    for y, m, r in zip(ys, mats, shapes):
+        one = gpu.alloc(batch * r)
+        gpu.gemm(one, m, x, r, cols, batch, kind=kind)
+        assert np.array_equal(y.read(), one.read()) or batch > 4
+        parity(y.read(), one.read(), where=f"group {r}")
+    rows = 3584
+    g = gpu.upload(pack((rng.standard_normal(rows * cols) * 0.02).astype(np.float32), rows))
+    u = gpu.upload(pack((rng.standard_normal(rows * cols) * 0.02).astype(np.float32), rows))
+    prod, gy, uy = gpu.alloc(batch * rows), gpu.alloc(batch * rows), gpu.alloc(batch * rows)
+    gpu.glu(prod, gy, uy, g, u, x, rows, cols, batch, kind=kind)
+    g1, u1 = gpu.alloc(batch * rows), gpu.alloc(batch * rows)
+    gpu.gemm(g1, g, x, rows, cols, batch, kind=kind)
+    gpu.gemm(u1, u, x, rows, cols, batch, kind=kind)
+    gv, uv = g1.read().astype(np.float64), u1.read().astype(np.float64)
+    want = gv / (1 + np.exp(-gv)) * uv
+    parity(prod.read(), want, where="glu")
+
+
+@pytest.mark.parametrize("kind", ["f32", "bf16", "i8"])
+@pytest.mark.parametrize("rows,cols", [(1024, 2048), (1024, 3584), (64, 256), (8, 16)])
+def test_add_norm_tail(gpu, cpu, kind, rows, cols):
+    """GEMV + Add + RmsNorm tail equals GEMV then op AddRmsNorm (bridge.cpp:797-827)."""
+    print(f"add_norm {kind} {rows}x{cols}", flush=True)
+    rng = np.random.default_rng(rows + cols)
+    w = (rng.standard_normal(rows * cols) * 0.02).astype(np.float32)
+    if kind == "bf16":
+        packed = pack_bf16(w)
+    elif kind == "i8":
+        packed = pack_int8(*O.quantize_int8_rows(w, rows, cols))
+    else:
+        packed = w
+    xv = rng.standard_normal(cols).astype(np.float32)
+    uv = rng.standard_normal(rows).astype(np.float32)
+    wn = (rng.standard_normal(rows) * 0.1).astype(np.float32)
+    for repeat in range(3):  # the ticket must be back at 0 after every launch
+        a, x, y = gpu.upload(packed), gpu.upload(xv), gpu.alloc(rows)
+        u, s, norm, weight = gpu.upload(uv), gpu.alloc(rows), gpu.alloc(rows), gpu.upload(wn)
+        gpu.add_norm(y, a, x, rows, cols, s, u, y, weight, norm, 1e-6, 1.0, kind=kind)
+        y2 = gpu.alloc(rows)
+        gpu.gemm(y2, a, x, rows, cols, 1, kind=kind)
+        yv = y2.read()
+        parity(y.read(), yv, where="tail gemv")
+        sv = (uv + yv).astype(np.float32)
+        parity(s.read(), sv, where="tail sum")
+        r = 1 / np.sqrt(np.mean(sv.astype(np.float64) ** 2) + 1e-6)
+        parity(norm.read(), sv * r * (wn.astype(np.float64) + 1), where="tail norm")
+
+
+def argmax_cases():
+    """The reference's argmax known answers (src/device/tests.rs:1117-1184):
+    ties across slices, NaN/+-Inf, a row with no finite value, lengths around
+    the one-block / two-pass switch."""
+    seed = [0x2545F4914F6CDD1D]
+
+    def nxt():
+        s = seed[0]
+        s ^= (s << 13) & 0xFFFFFFFFFFFFFFFF
+        s ^= s >> 7
+        s ^= (s << 17) & 0xFFFFFFFFFFFFFFFF
+        seed[0] = s
+        return np.float32((s >> 40) / float(1 << 24) * 20.0 - 10.0)
+
+    cases = []
+    for n in [1, 4095, 8191, 8192, 8193, 70000, 248320]:
+        cases.append(np.array([nxt() for _ in range(n)], np.float32))
+    tie = np.array([nxt() for _ in range(248320)], np.float32)
+    for i in [248000, 70000, 5000, 300]:
+        tie[i] = 50.0
+    cases.append(tie)
+    odd = np.array([nxt() for _ in range(248320)], np.float32)
+    for k, i in enumerate([7, 4096, 4097, 100000, 248319]):
+        odd[i] = [np.nan, np.inf, -np.inf][k % 3]
+    odd[200000] = 30.0
+    cases.append(odd)
+    cases.append(np.full(20000, np.nan, np.float32))
+    return cases
+
+
+def argmax_rule(v):
+    fin = np.isfinite(v)
+    bad = int((~fin).sum())
+    if not fin.any():
+        return [np.float32(4294967295.0), np.float32(bad)]
+    best = np.max(v[fin])
+    return [np.float32(np.flatnonzero(fin & (v == best))[0]), np.float32(bad)]
+
+
+def test_argmax_known_answers(gpu):
+    for row in argmax_cases():
+        n = row.size
+        for rows in (1, 3):
+            logits = np.concatenate([np.roll(row, -r * 1013) for r in range(rows)]).astype(np.float32)
+            want = np.array(sum((argmax_rule(np.roll(row, -r * 1013)) for r in range(rows)), []), np.float32)
+            buf = gpu.alloc(logits.size).write(logits.view(np.uint32))
+            out = gpu.alloc(2 * rows)
+            gpu.run("ARGMAX", rows, [out, buf], [n])
+            assert np.array_equal(out.read(), want), (n, rows)
+
+
+def rnd(rng, n, scale=1.0):
+    return (rng.standard_normal(n) * scale).astype(np.float32)
+
+
+@pytest.mark.parametrize("d,groups", [(1024, 1), (1024, 3), (128, 16), (128, 48), (8, 5), (256, 8)])
+def test_rms_family(gpu, cpu, d, groups):
+    rng = np.random.default_rng(d + groups)
+    x, w, u, z = rnd(rng, d * groups), rnd(rng, d, 0.1), rnd(rng, d * groups), rnd(rng, d * groups)
+    g, c = both(gpu, cpu, "RMS_NORM", groups, {1: x, 2: w}, {0: d * groups}, [d], [1e-6, 1.0])
+    parity(g[0], c[0], where="rms_norm")
+    g, c = both(gpu, cpu, "ADD_RMS_NORM", groups, {1: x, 2: u, 4: w}, {0: d * groups, 3: d * groups}, [d], [1e-6, 1.0])
+    parity(g[0], c[0], where="add")
+    parity(g[3], c[3], where="add_rms_norm")
+    g, c = both(gpu, cpu, "RMS_NORM_GATE", groups, {1: x, 2: w, 3: z}, {0: d * groups}, [d], [1e-6, 0.0])
+    parity(g[0], c[0], where="rms_norm_gate")
+
+
+def test_elementwise_and_embed(gpu, cpu):
+    rng = np.random.default_rng(5)
+    n = 3584 * 3
+    a, b = rnd(rng, n, 3), rnd(rng, n)
+    g, c = both(gpu, cpu, "ADD", n, {1: a, 2: b}, {0: n})
+    assert np.array_equal(g[0], c[0])
+    g, c = both(gpu, cpu, "SILU_PRODUCT", n, {1: a, 2: b}, {0: n})
+    parity(g[0], c[0], where="silu_product")
+    # DeltaGates with the reference's boundary values (src/device/tests.rs:368-400)
+    av = np.array([100, -100, 0, 10], np.float32)
+    bv = np.array([-100, 100, 0, 1], np.float32)
+    dt = np.array([0, 0, 1, -1], np.float32)
+    al = np.array([-20, 0, 1, 2], np.float32)
+    g, c = both(gpu, cpu, "DELTA_GATES", 4, {1: av, 2: bv, 3: dt, 4: al}, {0: 4, 5: 4})
+    parity(g[0], c[0], where="gates g")
+    parity(g[5], c[5], where="gates beta")
+    emb = rnd(rng, 19 * 8)
+    packed = pack_bf16(emb)
+    g, c = both(gpu, cpu, "EMBED_BF16", 8, {1: packed.view(np.float32)}, {0: 8}, [5, 8])
+    assert np.array_equal(g[0], c[0])
+    picks = np.array([3, 0, 18, 0], np.float32)
+    g, c = both(gpu, cpu, "EMBED_BF16_PICKED", 16, {1: packed.view(np.float32), 2: picks}, {0: 16}, [0, 8])
+    assert np.array_equal(g[0], c[0])
+
+
+@pytest.mark.parametrize("k,tokens,snaps", [(4, 1, 0), (4, 5, 0), (4, 4, 3), (3, 2, 1), (1, 1, 0)])
+def test_conv_silu(gpu, cpu, k, tokens, snaps):
+    rng = np.random.default_rng(k * 10 + tokens)
+    ch = 6144 if k == 4 else 24
+    x, w, h = rnd(rng, tokens * ch), rnd(rng, ch * k, 0.5), rnd(rng, ch * max(k - 1, 1) * (1 + snaps))
+    g, c = both(gpu, cpu, "CONV_SILU", ch, {1: x, 2: w, 3: h}, {0: tokens * ch, 3: h.size}, [k, tokens, ch, snaps])
+    parity(g[0], c[0], where="conv out")
+    parity(g[3], c[3], where="conv history")
+
+
+@pytest.mark.parametrize("kh,vh,d,tokens", [(16, 16, 128, 1), (16, 16, 128, 3), (2, 4, 3, 1), (4, 4, 16, 2)])
+def test_delta_qk(gpu, cpu, kh, vh, d, tokens):
+    rng = np.random.default_rng(d + tokens)
+    stride = 2 * kh * d + vh * d
+    x = rnd(rng, tokens * stride)
+    g, c = both(gpu, cpu, "DELTA_QK", vh * tokens, {1: x}, {0: vh * tokens * d, 2: vh * tokens * d},
+                [kh, vh, d, stride])
+    parity(g[0], c[0], where="q")
+    parity(g[2], c[2], where="k")
+
+
+@pytest.mark.parametrize("kd,vd,heads,tokens,snaps,gated",
+                         [(128, 128, 16, 1, 0, True), (128, 128, 16, 5, 0, True), (128, 128, 16, 4, 3, True),
+                          (64, 5, 2, 3, 0, False), (128, 3, 2, 3, 0, False), (16, 16, 4, 7, 2, True),
+                          (4, 4, 2, 5, 0, True), (3, 2, 4, 1, 0, False)])
+def test_delta_rule(gpu, cpu, kd, vd, heads, tokens, snaps, gated):
+    """Includes the reference's partially filled column groups (kd 64 with 5
+    columns, kd 128 with 3; src/device/tests.rs:1214-1284)."""
+    print(f"delta_rule kd={kd} vd={vd} heads={heads} tokens={tokens} snaps={snaps}", flush=True)
+    rng = np.random.default_rng(kd + vd + tokens)
+    stride = 2 * heads * kd + heads * vd
+    q = rnd(rng, tokens * heads * kd, 0.2)
+    k = rnd(rng, tokens * heads * kd, 0.2)
+    v = rnd(rng, tokens * stride, 2.0)
+    state = rnd(rng, heads * kd * vd * (1 + snaps))
+    if gated:
+        a, b = rnd(rng, tokens * heads), rnd(rng, tokens * heads)
+        gates = rnd(rng, 2 * heads, 0.5)
+        ins = {1: q, 2: k, 3: v, 4: state, 5: a, 6: b, 7: gates}
+        op = "DELTA_RULE_GATED"
+    else:
+        decay = (-0.1 - np.abs(rnd(rng, tokens * heads, 0.1))).astype(np.float32)
+        beta = (0.5 + rnd(rng, tokens * heads, 0.2)).clip(0, 1).astype(np.float32)
+        ins = {1: q, 2: k, 3: v, 4: state, 5: decay, 6: beta}
+        op = "DELTA_RULE"
+    g, c = both(gpu, cpu, op, heads * vd, ins, {0: tokens * heads * vd, 4: state.size},
+                [kd, vd, heads, heads, tokens, stride, snaps])
+    parity(g[0], c[0], where="core")
+    parity(g[4], c[4], where="state+snapshots")
+
+
+@pytest.mark.parametrize("d,rot,heads,kv,tokens,pos", [(256, 64, 8, 2, 1, 453), (256, 64, 8, 2, 3, 8190),
+                                                       (16, 8, 4, 1, 2, 7), (4, 2, 2, 1, 1, 0)])
+def test_attention_query_kv(gpu, cpu, d, rot, heads, kv, tokens, pos):
+    rng = np.random.default_rng(d + pos)
+    cap = pos + tokens + 1
+    mixed, key, value = rnd(rng, tokens * heads * 2 * d), rnd(rng, tokens * kv * d), rnd(rng, tokens * kv * d)
+    qkn = rnd(rng, 2 * d, 0.1)
+    keys, values = np.zeros(cap * kv * d, np.float32), np.zeros(cap * kv * d, np.float32)
+    g, c = both(gpu, cpu, "ATTENTION_QUERY_KV", (heads + kv) * tokens,
+                {1: mixed, 2: qkn, 4: keys, 5: key, 6: value, 7: values},
+                {0: tokens * heads * d, 3: tokens * heads * d, 4: keys.size, 7: values.size},
+                [d, rot, pos, heads, kv, tokens], [1e-6, 1e7 if d == 256 else 1e4])
+    parity(g[0], c[0], where="query")
+    assert np.array_equal(g[3], c[3])
+    parity(g[4], c[4], where="keys")
+    assert np.array_equal(g[7], c[7])
+
+
+@pytest.mark.parametrize("d,heads,kv,length,tokens", [(256, 8, 2, 454, 1), (256, 8, 2, 8192, 1), (256, 8, 2, 1, 1),
+                                                      (256, 8, 2, 100, 4), (256, 8, 2, 40, 24), (16, 4, 1, 17, 1),
+                                                      (16, 4, 1, 5, 16), (4, 2, 1, 3, 2)])
+def test_attention_read(gpu, cpu, d, heads, kv, length, tokens):
+    """Decode (one row, split-K), a verify pass (rows 2..8, one decode read
+    per row) and a prefill chunk (causal rows)."""
+    print(f"attention_read d={d} len={length} rows={tokens}", flush=True)
+    rng = np.random.default_rng(d + length + tokens)
+    cap = length + tokens + 64
+    q = rnd(rng, tokens * heads * d)
+    keys, values = rnd(rng, cap * kv * d), rnd(rng, cap * kv * d)
+    gate = rnd(rng, tokens * heads * d)
+    n6 = max(cap, (cap + 31) // 32 * (d + 2))
+    g, c = both(gpu, cpu, "ATTENTION_READ", heads, {1: q, 2: keys, 3: values, 4: gate, 5: np.zeros(n6 * heads, np.float32)},
+                {0: tokens * heads * d}, [d, heads, kv, length, cap, tokens, n6])
+    parity(g[0], c[0], where="attention")
+
+
+def test_delta_mixer_matches_four_ops(gpu, cpu):
+    """qr_delta_mixer for one token equals ConvSilu, DeltaQk, DeltaRuleGated,
+    RmsNormGate (reference native/rocm/bridge.cpp:730-796)."""
+    rng = np.random.default_rng(99)
+    h, k = 16, 4
+    ch = 3 * h * 128
+    data = dict(projected=rnd(rng, ch), conv_w=rnd(rng, ch * k, 0.3), conv_state=rnd(rng, ch * (k - 1)),
+                recurrent=rnd(rng, h * 128 * 128, 0.5), a=rnd(rng, h), b=rnd(rng, h), gates=rnd(rng, 2 * h, 0.3),
+                norm_w=(1 + rnd(rng, 128, 0.1)).astype(np.float32), z=rnd(rng, h * 128))
+    outs = dict(convolved=ch, query=h * 128, key=h * 128, core=h * 128, gated=h * 128)
+    res = []
+    for br in (gpu, cpu):
+        bufs = {n: br.upload(v) for n, v in data.items()}
+        bufs.update({n: br.alloc(s) for n, s in outs.items()})
+        if br is gpu:
+            br.delta_mixer(**bufs, key_heads=h, value_heads=h, key_dim=128, value_dim=128, kernel=k, tokens=1,
+                           channels=ch, eps=1e-6)
+        else:
+            br.run("CONV_SILU", ch, [bufs["convolved"], bufs["projected"], bufs["conv_w"], bufs["conv_state"]],
+                   [k, 1, ch])
+            br.run("DELTA_QK", h, [bufs["query"], bufs["convolved"], bufs["key"]], [h, h, 128, ch])
+            br.run("DELTA_RULE_GATED", h * 128, [bufs["core"], bufs["query"], bufs["key"], bufs["convolved"],
+                                                 bufs["recurrent"], bufs["a"], bufs["b"], bufs["gates"]],
+                   [128, 128, h, h, 1, ch])
+            br.run("RMS_NORM_GATE", h, [bufs["gated"], bufs["core"], bufs["norm_w"], bufs["z"]], [128], [1e-6, 0.0])
+        res.append({n: bufs[n].read() for n in list(outs) + ["conv_state", "recurrent"]})
+    for n in res[0]:
+        parity(res[0][n], res[1][n], where=n)
