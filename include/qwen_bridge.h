@@ -144,6 +144,45 @@ int qr_gemm_f32_glu(Context* c, float* product, float* gate_y, float* up_y, cons
 int qr_gemm_f32_add_norm(Context* c, float* y, const float* a, const float* x, int rows, int cols,
                          const QrAddNormPost* post);
 
+/* One decode token in one launch (no counterpart in the reference's ABI; the
+ * engine calls it from `forward` when t == 1, nothing is captured, the
+ * matrices are fp32 and the bridge accepted the plan, instead of the op
+ * sequence of src/device.rs:1740-2378, which it computes identically up to
+ * fp32 summation order). The plan registers every weight, state and output
+ * buffer of one run once; each step embeds `token`, runs all layers at
+ * `position` (appending K/V there and advancing the DeltaNet states), writes
+ * the vocabulary logits to `logits` and [argmax index, non-finite count] to
+ * `picks` (op Argmax's output, reference.h:222-230). */
+typedef struct QrDecodeLayer {
+    int32_t attention;  /* 1 full attention, 0 Gated DeltaNet */
+    const float* input_norm; const float* post_norm;
+    const float* gate; const float* up; const float* down;
+    /* attention */
+    const float* q; const float* k; const float* v; const float* o;
+    const float* qk_norm;            /* [q_norm | k_norm] */
+    float* keys; float* values;      /* caches [capacity, kv_heads, head_dim] */
+    /* Gated DeltaNet */
+    const float* qkv; const float* z; const float* a; const float* b;
+    const float* conv_w; const float* gates; /* [dt | A_log] */ const float* norm_w; const float* out;
+    float* conv_state; float* recurrent;
+} QrDecodeLayer;
+typedef struct QrDecodeDesc {
+    int32_t hidden, intermediate, vocab, layers, heads, kv_heads, head_dim, rotary_dim;
+    int32_t key_heads, value_heads, key_dim, value_dim, conv_kernel, capacity;
+    float eps, theta;
+    const float* embedding;  /* [vocab, hidden]: the lookup rows */
+    const float* lm_head;    /* vocabulary projection, [vocab, hidden] */
+    const float* final_norm;
+    float* logits;           /* [vocab] */
+    float* picks;            /* [2] */
+    const QrDecodeLayer* layer;
+} QrDecodeDesc;
+typedef struct QrDecodePlan QrDecodePlan;
+/* Non-zero (with qr_error set) when this bridge has no one-launch decode for the shape. */
+int qr_decode_plan(Context* c, const QrDecodeDesc* d, QrDecodePlan** out);
+int qr_decode_step(Context* c, QrDecodePlan* p, int token, int position);
+void qr_decode_plan_free(Context* c, QrDecodePlan* p);
+
 /* In-bridge profiler: while on, every bridge call is bracketed by a hipEvent
  * pair on the context stream and the durations are summed per call label
  * (kernel family and shape). No counterpart in the reference's ABI: its

@@ -36,7 +36,8 @@ enum QeDisable {
     QE_NO_DELTA_MIXER = 4,   /* qr_delta_mixer */
     QE_NO_FUSED_OPS = 8,     /* qr_max_op (ops 12-15) */
     QE_NO_ARGMAX = 16,       /* qr_argmax (ops 16-17) */
-    QE_NO_SNAPSHOTS = 32     /* qr_snapshots */
+    QE_NO_SNAPSHOTS = 32,    /* qr_snapshots */
+    QE_NO_DECODE_STEP = 64   /* qr_decode_plan / qr_decode_step */
 };
 
 /* Record callback of a captured step: (layer, name, values, n). Names follow
@@ -72,6 +73,9 @@ QeRun* qe_run_new(QeModel* m, int64_t capacity, int64_t chunk, int64_t snapshots
 void qe_run_free(QeRun* r);
 int qe_run_reset(QeRun* r);
 int64_t qe_run_position(QeRun* r);
+/* 1 when uncaptured one-token steps of this run go through the bridge's
+ * one-launch decode (qr_decode_plan accepted the run), else 0. */
+int qe_run_decode_plan(QeRun* r);
 
 /* DeviceRun::step (src/device.rs:1440-1451); logits: vocab floats. With
  * `record` non-NULL the step is captured (every record read back). */

@@ -23,6 +23,8 @@ struct Context {
     size_t argmax_parts_len = 0;
     float* attn_parts = nullptr;  // split partials of decode attention
     size_t attn_parts_len = 0;
+    // RoPE denominators theta^(2i / rot) per (theta bits, rot), device copies.
+    std::map<std::pair<uint32_t, int>, float*> rope;
     // Profiler (qr_profile / QWEN_ROCM_PROFILE=1): a hipEvent pair on the
     // context stream around every bridge call, summed per label.
     bool profile = false, print_at_exit = false;
@@ -121,6 +123,31 @@ int ensure(Context* c, float** buf, size_t* len, size_t need, const char* what) 
 }
 
 const void* i8_packed(const float* packed) { return packed; }
+
+// The RoPE denominators of (theta, rot): powf(theta, float(2i) / float(rot)),
+// the expression of the reference's rotate (src/attention.rs:49-50 and
+// reference.h:41-47), evaluated by the host libm once per pair.
+int rope_table(Context* c, float theta, int rot, const float** out) {
+    uint32_t bits;
+    std::memcpy(&bits, &theta, 4);
+    auto key = std::make_pair(bits, rot);
+    auto it = c->rope.find(key);
+    if (it != c->rope.end()) {
+        *out = it->second;
+        return 0;
+    }
+    std::vector<float> host(size_t(rot / 2 > 0 ? rot / 2 : 1), 1.f);
+    for (int i = 0; i < rot / 2; ++i) host[size_t(i)] = powf(theta, float(2 * i) / float(rot));
+    float* dev = nullptr;
+    auto st = hipMalloc(reinterpret_cast<void**>(&dev), host.size() * sizeof(float));
+    if (st == hipSuccess)
+        st = hipMemcpyAsync(dev, host.data(), host.size() * sizeof(float), hipMemcpyHostToDevice, c->stream);
+    if (st == hipSuccess) st = hipStreamSynchronize(c->stream);
+    if (st != hipSuccess) return fail(c, "RoPE table", int(st));
+    c->rope[key] = dev;
+    *out = dev;
+    return 0;
+}
 
 int project(Context* c, qr::WeightType t, float* y, const void* a, const float* x, int rows, int cols, int batch) {
     if (rows < 1 || cols < 1 || batch < 1) return fail(c, "projection shape", -1);
@@ -312,6 +339,7 @@ void qr_destroy(Context* c) {
         (void)hipEventDestroy(t.stop);
     }
     for (auto e : c->spare) (void)hipEventDestroy(e);
+    for (auto& [key, dev] : c->rope) (void)hipFree(dev);
     if (c->ticket) (void)hipFree(c->ticket);
     if (c->argmax_parts) (void)hipFree(c->argmax_parts);
     if (c->attn_parts) (void)hipFree(c->attn_parts);
@@ -382,7 +410,11 @@ int qr_run(Context* c, int op, int count, const Params* ap) {
         return launched(c, "delta_rule", qr::run_delta_rule(s, op == QR_DELTA_RULE_GATED, count, a));
     case QR_ATTENTION_QUERY:
     case QR_ATTENTION_KV:
-    case QR_ATTENTION_QUERY_KV: return launched(c, "attention_qkv", qr::run_attention_qkv(s, op, count, a));
+    case QR_ATTENTION_QUERY_KV: {
+        const float* denom = nullptr;
+        if (int st = rope_table(c, a.f[1], a.n[1], &denom)) return st;
+        return launched(c, "attention_qkv", qr::run_attention_qkv(s, op, count, a, denom));
+    }
     case QR_ATTENTION_READ: return attention_read(c, count, a);
     case QR_ARGMAX: {
         if (a.n[0] < 1) return fail(c, "argmax shape", -1);
@@ -497,6 +529,27 @@ int qr_delta_mixer(Context* c, const QrDelta* d) {
     if (int s = qr_run(c, QR_DELTA_QK, vh * t, &qk)) return s;
     if (int s = qr_run(c, QR_DELTA_RULE_GATED, vd, &rule)) return s;
     return qr_run(c, QR_RMS_NORM_GATE, vh * t, &gate);
+}
+
+// One-launch decode (no counterpart in the reference's ABI).
+int qr_decode_plan(Context* c, const QrDecodeDesc* d, QrDecodePlan** out) {
+    if (!d || !out) return fail(c, "decode plan arguments", -1);
+    const char* why = nullptr;
+    int s = qr::decode_plan_create(*d, out, c->stream, &why);
+    if (s) {
+        std::snprintf(c->error, sizeof(c->error), "%s", why ? why : "one-launch decode unavailable");
+        return s;
+    }
+    return 0;
+}
+int qr_decode_step(Context* c, QrDecodePlan* p, int token, int position) {
+    if (!p) return fail(c, "decode step without a plan", -1);
+    auto sc = scope(c, [&] { return std::string("decode_step"); });
+    return launched(c, "decode step", qr::decode_step(p, token, position, c->stream));
+}
+void qr_decode_plan_free(Context* c, QrDecodePlan* p) {
+    if (c) (void)hipStreamSynchronize(c->stream);
+    qr::decode_plan_free(p);
 }
 
 }  // extern "C"

@@ -88,7 +88,8 @@ int run_rms_family(hipStream_t s, int op, int groups, const Params& a);
 int run_conv_silu(hipStream_t s, int count, const Params& a);
 int run_delta_qk(hipStream_t s, int count, const Params& a);
 int run_delta_rule(hipStream_t s, bool gated, int count, const Params& a);
-int run_attention_qkv(hipStream_t s, int op, int count, const Params& a);
+// `denom`: device table of theta^(2i / rot), i < rot / 2 (see rope_lds).
+int run_attention_qkv(hipStream_t s, int op, int count, const Params& a, const float* denom);
 int run_embed(hipStream_t s, int op, int count, const Params& a);
 int run_argmax(hipStream_t s, int rows, const Params& a, float* parts, size_t parts_len);
 size_t argmax_parts_needed(int rows, int n);
@@ -97,6 +98,13 @@ size_t argmax_parts_needed(int rows, int n);
 // AttentionRead (op 10). `scratch` is the bridge's own partials buffer.
 int run_attention_read(hipStream_t s, int heads_count, const Params& a, float* scratch, size_t scratch_len);
 size_t attention_scratch_needed(const Params& a);
+
+// decode.hip -----------------------------------------------------------------
+// One-launch decode step (qr_decode_plan / qr_decode_step).
+const char* decode_unsupported(const QrDecodeDesc& d);
+int decode_plan_create(const QrDecodeDesc& d, QrDecodePlan** out, hipStream_t s, const char** why);
+void decode_plan_free(QrDecodePlan* p);
+int decode_step(QrDecodePlan* p, int token, int position, hipStream_t s);
 
 // deltanet.hip ---------------------------------------------------------------
 // qr_delta_mixer for one token (decode) when the shape allows; returns -1 if not handled.

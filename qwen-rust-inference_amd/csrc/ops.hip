@@ -214,9 +214,13 @@ __global__ __launch_bounds__(256) void delta_rule_kernel(int count, Params a) {
 // ---------------------------------------------------------------- attention Q / KV
 // AttentionQuery (8), AttentionKv (9), AttentionQueryKv (15): reference.h:61-95.
 // One block per item; the head vector is normalised into LDS and RoPE'd there.
-__device__ void rope_lds(float* o, int rot, int pos, float theta) {
+// `denom[i]` = theta^(2i / rot), computed once on the host with the same libm
+// powf the CPU path calls, so the angle pos / denom[i] is the same correctly
+// rounded quotient on both sides (a one-ulp powf difference alone moves the
+// angle by ~5e-4 rad at position 8190).
+__device__ void rope_lds(float* o, int rot, int pos, const float* denom) {
     for (int i = threadIdx.x; i < rot / 2; i += blockDim.x) {
-        float angle = float(pos) / powf(theta, float(2 * i) / float(rot));
+        float angle = float(pos) / denom[i];
         float sn = sinf(angle), cs = cosf(angle);
         float x0 = o[i], x1 = o[i + rot / 2];
         o[i] = x0 * cs - x1 * sn;
@@ -224,7 +228,7 @@ __device__ void rope_lds(float* o, int rot, int pos, float theta) {
     }
 }
 
-__device__ void attention_query_item(int t, const Params& a, float* buf, float* red) {
+__device__ void attention_query_item(int t, const Params& a, const float* denom, float* buf, float* red) {
     const int d = a.n[0], rot = a.n[1], pos = a.n[2] + (a.n[3] > 0 ? t / a.n[3] : 0);
     const float* x = a.p[1] + size_t(t) * 2 * d;
     float ss = 0.f;
@@ -236,12 +240,12 @@ __device__ void attention_query_item(int t, const Params& a, float* buf, float* 
         a.p[3][size_t(t) * d + i] = x[d + i];
     }
     __syncthreads();
-    rope_lds(buf, rot, pos, a.f[1]);
+    rope_lds(buf, rot, pos, denom);
     __syncthreads();
     for (int i = threadIdx.x; i < d; i += blockDim.x) a.p[0][size_t(t) * d + i] = buf[i];
 }
 
-__device__ void attention_kv_item(int t, const Params& a, float* buf, float* red) {
+__device__ void attention_kv_item(int t, const Params& a, const float* denom, float* buf, float* red) {
     const int d = a.n[0], rot = a.n[1], kv = a.n[3], pos = a.n[2] + t / kv, hh = t % kv;
     const float* x = a.p[1] + size_t(t) * d;
     float ss = 0.f;
@@ -254,21 +258,21 @@ __device__ void attention_kv_item(int t, const Params& a, float* buf, float* red
         a.p[4][dest + i] = a.p[3][size_t(t) * d + i];
     }
     __syncthreads();
-    rope_lds(buf, rot, pos, a.f[1]);
+    rope_lds(buf, rot, pos, denom);
     __syncthreads();
     for (int i = threadIdx.x; i < d; i += blockDim.x) a.p[0][dest + i] = buf[i];
 }
 
 constexpr int kAttnMaxHeadDim = 1024;
 
-__global__ __launch_bounds__(256) void attention_qkv_kernel(int op, int count, Params a) {
+__global__ __launch_bounds__(256) void attention_qkv_kernel(int op, int count, Params a, const float* denom) {
     __shared__ float buf[kAttnMaxHeadDim];
     __shared__ float red[16];
     const int t = blockIdx.x;
     if (op == QR_ATTENTION_QUERY) {
-        attention_query_item(t, a, buf, red);
+        attention_query_item(t, a, denom, buf, red);
     } else if (op == QR_ATTENTION_KV) {
-        attention_kv_item(t, a, buf, red);
+        attention_kv_item(t, a, denom, buf, red);
     } else {  // AttentionQueryKv: split the items as reference.h:65-74 does
         const int queries = a.n[3] * a.n[5];
         Params part{};
@@ -283,7 +287,7 @@ __global__ __launch_bounds__(256) void attention_qkv_kernel(int op, int count, P
             part.p[2] = a.p[2];
             part.p[3] = a.p[3];
             part.n[3] = a.n[3];
-            attention_query_item(t, part, buf, red);
+            attention_query_item(t, part, denom, buf, red);
         } else {
             part.p[0] = a.p[4];
             part.p[1] = a.p[5];
@@ -291,7 +295,7 @@ __global__ __launch_bounds__(256) void attention_qkv_kernel(int op, int count, P
             part.p[3] = a.p[6];
             part.p[4] = a.p[7];
             part.n[3] = a.n[4];
-            attention_kv_item(t - queries, part, buf, red);
+            attention_kv_item(t - queries, part, denom, buf, red);
         }
     }
     (void)count;
@@ -430,9 +434,9 @@ int run_delta_rule(hipStream_t s, bool gated, int count, const Params& a) {
     return int(hipErrorInvalidValue);
 }
 
-int run_attention_qkv(hipStream_t s, int op, int count, const Params& a) {
+int run_attention_qkv(hipStream_t s, int op, int count, const Params& a, const float* denom) {
     if (a.n[0] > kAttnMaxHeadDim || a.n[1] > a.n[0] || a.n[1] % 2 != 0) return int(hipErrorInvalidValue);
-    hipLaunchKernelGGL(attention_qkv_kernel, dim3(unsigned(count)), dim3(256), 0, s, op, count, a);
+    hipLaunchKernelGGL(attention_qkv_kernel, dim3(unsigned(count)), dim3(256), 0, s, op, count, a, denom);
     return int(hipGetLastError());
 }
 

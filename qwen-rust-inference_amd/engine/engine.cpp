@@ -86,6 +86,9 @@ struct Api {
     Glu glu_bf16 = nullptr, glu_i8 = nullptr, glu_f32 = nullptr;
     AddNorm add_norm_bf16 = nullptr, add_norm_i8 = nullptr, add_norm_f32 = nullptr;
     int (*delta_mixer)(Context*, const QrDelta*) = nullptr;
+    int (*decode_plan)(Context*, const QrDecodeDesc*, QrDecodePlan**) = nullptr;
+    int (*decode_step)(Context*, QrDecodePlan*, int, int) = nullptr;
+    void (*decode_free)(Context*, QrDecodePlan*) = nullptr;
     int (*profile)(Context*, int) = nullptr;
     long (*profile_read)(Context*, char*, size_t) = nullptr;
     int (*sync_)(Context*) = nullptr;
@@ -150,6 +153,12 @@ struct Api {
             add_norm_f32 = symbol<AddNorm>("qr_gemm_f32_add_norm", false);
         }
         if (!(disable & QE_NO_DELTA_MIXER)) delta_mixer = symbol<decltype(delta_mixer)>("qr_delta_mixer", false);
+        if (!(disable & QE_NO_DECODE_STEP)) {
+            decode_plan = symbol<decltype(decode_plan)>("qr_decode_plan", false);
+            decode_step = symbol<decltype(decode_step)>("qr_decode_step", false);
+            decode_free = symbol<decltype(decode_free)>("qr_decode_plan_free", false);
+            if (!decode_plan || !decode_step || !decode_free) decode_plan = nullptr;
+        }
         profile = symbol<decltype(profile)>("qr_profile", false);
         profile_read = symbol<decltype(profile_read)>("qr_profile_read", false);
         if (!(disable & QE_NO_SNAPSHOTS)) {
@@ -463,8 +472,107 @@ struct QeRun {
     std::vector<uint32_t> picked;
     size_t pick_slot = 0;
     bool logits_unread = false;
+    // The bridge's one-launch decode step over this run's buffers (fp32
+    // matrices only), used by forward for uncaptured one-token steps.
+    QrDecodePlan* plan = nullptr;
 
     const Api* api() const { return model->api.get(); }
+    ~QeRun() { drop_plan(); }
+    void drop_plan() {
+        if (plan && model) api()->decode_free(api()->ctx, plan);
+        plan = nullptr;
+    }
+    // qr_decode_plan over the run's buffers; a bridge that declines the shape
+    // leaves the run on the op sequence.
+    void make_plan() {
+        drop_plan();
+        const Api* a = api();
+        const QwConfig& c = model->config;
+        if (!a->decode_plan || !model->embedding.f32() || !model->output().f32()) return;
+        std::vector<QrDecodeLayer> layers;
+        const DeviceBlock* attn = nullptr;
+        const DeviceBlock* delta = nullptr;
+        for (size_t l = 0; l < model->blocks.size(); ++l) {
+            const DeviceBlock& b = model->blocks[l];
+            MixerRun& m = mixers[l];
+            if (!b.gate.f32() || !b.up.f32() || !b.down.f32()) return;
+            QrDecodeLayer d{};
+            d.attention = b.attention ? 1 : 0;
+            d.input_norm = b.input.p;
+            d.post_norm = b.post.p;
+            d.gate = b.gate.buffer.p;
+            d.up = b.up.buffer.p;
+            d.down = b.down.buffer.p;
+            if (b.attention) {
+                if (!b.q.f32() || !b.k.f32() || !b.v.f32() || !b.o.f32()) return;
+                d.q = b.q.buffer.p;
+                d.k = b.k.buffer.p;
+                d.v = b.v.buffer.p;
+                d.o = b.o.buffer.p;
+                d.qk_norm = b.qkn.p;
+                d.keys = m.keys.p;
+                d.values = m.values.p;
+                attn = &b;
+            } else {
+                if (!b.qkv.f32() || !b.z.f32() || !b.a.f32() || !b.b.f32() || !b.out.f32()) return;
+                d.qkv = b.qkv.buffer.p;
+                d.z = b.z.buffer.p;
+                d.a = b.a.buffer.p;
+                d.b = b.b.buffer.p;
+                d.conv_w = b.conv.p;
+                d.gates = b.gates.p;
+                d.norm_w = b.norm.p;
+                d.out = b.out.buffer.p;
+                d.conv_state = m.conv_state.p;
+                d.recurrent = m.recurrent.p;
+                delta = &b;
+            }
+            layers.push_back(d);
+        }
+        QrDecodeDesc desc{};
+        desc.hidden = c.hidden_size;
+        desc.intermediate = c.intermediate_size;
+        desc.vocab = c.vocab_size;
+        desc.layers = int32(layers.size());
+        desc.heads = attn ? int32(attn->ac.heads) : c.num_heads;
+        desc.kv_heads = attn ? int32(attn->ac.kv_heads) : c.num_kv_heads;
+        desc.head_dim = attn ? int32(attn->ac.head_dim) : c.head_dim;
+        desc.rotary_dim = attn ? int32(attn->ac.rotary_dim) : c.rotary_dim;
+        desc.key_heads = delta ? int32(delta->dc.key_heads) : c.key_heads;
+        desc.value_heads = delta ? int32(delta->dc.value_heads) : c.value_heads;
+        desc.key_dim = delta ? int32(delta->dc.key_dim) : c.key_dim;
+        desc.value_dim = delta ? int32(delta->dc.value_dim) : c.value_dim;
+        desc.conv_kernel = delta ? int32(delta->dc.kernel) : c.conv_kernel;
+        desc.capacity = int32(capacity);
+        desc.eps = c.rms_norm_eps;
+        desc.theta = attn ? attn->ac.theta : c.rope_theta;
+        desc.embedding = model->embedding.buffer.p;
+        desc.lm_head = model->output().buffer.p;
+        desc.final_norm = model->norm.p;
+        desc.logits = logits.p;
+        desc.picks = picks.p;
+        desc.layer = layers.data();
+        QrDecodePlan* p = nullptr;
+        if (a->decode_plan(a->ctx, &desc, &p) == 0) plan = p;
+    }
+    // One uncaptured token through the plan (the work of forward_body for
+    // t == 1, logit_rows == 1): logits and [argmax, non-finite count] land in
+    // the run's logits / picks buffers.
+    std::vector<float> forward_planned(uint32_t id) {
+        const Api* a = api();
+        a->check(a->decode_step(a->ctx, plan, int(id), int(position)));
+        std::vector<float> out;
+        std::vector<float> pk(2);
+        a->check(a->read(a->ctx, pk.data(), picks.p, 2));
+        require(pk[1] < 1e30f, "one-launch decode step timed out at a stage barrier");
+        if (greedy_rows) {
+            picked = read_picks(0, 1);
+        } else {
+            out = logits.read(size_t(model->config.vocab_size));
+        }
+        position += 1;
+        return out;
+    }
 
     // new_run_with (src/device.rs:1198-1294)
     void build(size_t cap, size_t ch, size_t snaps) {
@@ -533,6 +641,7 @@ struct QeRun {
         picked.clear();
         pick_slot = 0;
         logits_unread = false;
+        make_plan();
     }
 
     // step (src/device.rs:1440-1451)
@@ -692,6 +801,11 @@ struct QeRun {
         require(t > 0 && t <= chunk && (!rec || t == 1) && (logit_rows <= 1 || logit_rows == t),
                 "device forward chunk/capture");
         const Api* a = api();
+        if (plan && t == 1 && !rec && logit_rows == 1 && snapshot_rows == 0 && pick_slot == 0) {
+            auto out = forward_planned(ids[0]);
+            logits_unread = greedy_rows;
+            return out;
+        }
         size_t h = size_t(model->config.hidden_size);
         for (size_t r = 0; r < t; ++r) {
             float* xr = x.at(r * h);
@@ -1038,6 +1152,8 @@ QeRun* qe_run_new(QeModel* m, int64_t capacity, int64_t chunk, int64_t snapshots
 }
 void qe_run_free(QeRun* r) { delete r; }
 
+int qe_run_decode_plan(QeRun* r) { return r && r->plan ? 1 : 0; }
+
 int qe_run_reset(QeRun* r) {
     return guarded([&] {
         QeRun fresh;
@@ -1054,6 +1170,9 @@ int qe_run_reset(QeRun* r) {
         r->ffn = std::move(fresh.ffn);
         r->logits = std::move(fresh.logits);
         r->picks = std::move(fresh.picks);
+        r->drop_plan();
+        r->plan = fresh.plan;  // over the buffers moved in above
+        fresh.plan = nullptr;
         r->position = 0;
         r->failed = false;
         r->pending.reset();

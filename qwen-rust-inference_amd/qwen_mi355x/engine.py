@@ -26,6 +26,7 @@ ENGINE = LIB_DIR / "libqwen_engine.so"
 KIND_CPU_TEST, KIND_ROCM = 0, 1
 F32, BF16_EXACT, INT8 = 0, 1, 2
 NO_F32_FUSIONS, NO_FUSIONS, NO_DELTA_MIXER, NO_FUSED_OPS, NO_ARGMAX, NO_SNAPSHOTS = 1, 2, 4, 8, 16, 32
+NO_DECODE_STEP = 64
 
 # Every entry point of include/qwen_bridge.h.
 BRIDGE_SYMBOLS = [
@@ -34,6 +35,7 @@ BRIDGE_SYMBOLS = [
     "qr_snapshots", "qr_argmax", "qr_set_option", "qr_gemm_i8", "qr_gemm_bf16_group", "qr_gemm_i8_group",
     "qr_gemm_bf16_glu", "qr_gemm_i8_glu", "qr_gemm_bf16_add_norm", "qr_gemm_i8_add_norm", "qr_delta_mixer",
     "qr_gemm_f32_group", "qr_gemm_f32_glu", "qr_gemm_f32_add_norm", "qr_profile", "qr_profile_read",
+    "qr_decode_plan", "qr_decode_step", "qr_decode_plan_free",
 ]
 
 _F = ctypes.POINTER(ctypes.c_float)
@@ -73,6 +75,7 @@ def lib():
         L.qe_run_reset.argtypes = [ctypes.c_void_p]
         L.qe_run_position.restype = ctypes.c_int64
         L.qe_run_position.argtypes = [ctypes.c_void_p]
+        L.qe_run_decode_plan.argtypes = [ctypes.c_void_p]
         L.qe_step.argtypes = [ctypes.c_void_p, ctypes.c_uint32, _F, RECORD_FN, ctypes.c_void_p]
         L.qe_step_greedy.argtypes = [ctypes.c_void_p, ctypes.c_uint32, _U32]
         L.qe_prefill.argtypes = [ctypes.c_void_p, _U32, ctypes.c_int64, _F, ctypes.POINTER(ctypes.c_int)]
@@ -229,6 +232,11 @@ class Run:
     @property
     def position(self) -> int:
         return lib().qe_run_position(self.ptr)
+
+    @property
+    def decode_plan(self) -> bool:
+        """True when uncaptured one-token steps run the bridge's one-launch decode."""
+        return bool(lib().qe_run_decode_plan(self.ptr))
 
     def reset(self):
         _check(lib().qe_run_reset(self.ptr))

@@ -145,8 +145,17 @@ def test_tiny_int8_against_dequantised_oracle(tiny):
 @pytest.fixture(scope="module")
 def qwen08b():
     print("synthesising 0.8B weights", flush=True)
-    c = M.config_qwen08b(max_positions=4096)
+    c = M.config_qwen08b(max_positions=16384)
     return c, M.synthetic_weights(c, seed=0)
+
+
+@pytest.fixture(scope="module")
+def qwen08b_models(qwen08b):
+    """The 0.8B model twice on the device: with the bridge's one-launch decode
+    step, and on the op sequence (the step's fallback and its reference)."""
+    c, w = qwen08b
+    print("loading 0.8B twice (one-launch decode / op sequence)", flush=True)
+    return E.Model(w), E.Model(w, disable=E.NO_DECODE_STEP)
 
 
 def test_qwen08b_short_greedy(qwen08b):
@@ -160,6 +169,7 @@ def test_qwen08b_short_greedy(qwen08b):
     m = E.Model(w)
     print(m.info, flush=True)
     run = m.new_run(64, chunk=8)
+    assert run.decode_plan, "0.8B fp32 steps should take the one-launch decode"
     logits = run.prefill(prompt)
     parity(logits, want_logits[0], where="0.8B prefill logits")
     got, _ = run.decode_greedy(O.select_greedy(logits), 6)
@@ -167,3 +177,74 @@ def test_qwen08b_short_greedy(qwen08b):
     for layer in (0, 3):
         for which in range(4):
             parity(run.state(layer, which), s.part(layer, which), where=f"0.8B state {layer}/{which}")
+
+
+def test_qwen08b_decode_step_logits_against_oracle(qwen08b, qwen08b_models):
+    """Each one-launch step's full logits against the oracle (fp32 bound)."""
+    c, w = qwen08b
+    fast, _ = qwen08b_models
+    prompt = [int(v) for v in np.random.default_rng(5).integers(0, c.vocab_size, 5)]
+    s = O.Oracle(w).new_state()
+    run = fast.new_run(32, chunk=8)
+    assert run.decode_plan
+    for i, t in enumerate(prompt):
+        print(f"one-launch step {i}", flush=True)
+        got = run.step(t)
+        parity(got, s.step(t, O.VECTOR), where=f"one-launch step {i}")
+
+
+def _random_states(c, run, position, seed):
+    """Seeded conv / recurrent states and K/V rows 0..position-1 on `run`."""
+    rng = np.random.default_rng(seed)
+    run.set_position(position)
+    parts = []
+    for layer in range(c.num_layers):
+        for which in range(4):
+            n = run.state(layer, which).size
+            if n:
+                scale = 0.05 if which == 1 else 1.0
+                parts.append((layer, which, (rng.standard_normal(n) * scale).astype(np.float32)))
+    return parts
+
+
+@pytest.mark.parametrize("position", [0, 1, 453, 8190, 8191, 8192, 10239])
+def test_qwen08b_one_launch_matches_op_sequence(qwen08b, qwen08b_models, position):
+    """The one-launch step against the op sequence on the same seeded state,
+    three tokens from `position`: logits within the fp32 bound, identical
+    greedy picks, and every state part after the steps. The positions cross
+    the attention span changes (8 positions per split up to 8192, longer
+    spans after)."""
+    c, w = qwen08b
+    fast, ops = qwen08b_models
+    cap = position + 8
+    a, b = fast.new_run(cap, chunk=8), ops.new_run(cap, chunk=8)
+    assert a.decode_plan and not b.decode_plan
+    parts = _random_states(c, a, position, seed=position)
+    b.set_position(position)
+    for (layer, which, v) in parts:
+        a.write_state(layer, which, v)
+        b.write_state(layer, which, v)
+    tokens = [int(v) for v in np.random.default_rng(position + 1).integers(0, c.vocab_size, 3)]
+    for i, t in enumerate(tokens):
+        print(f"position {position + i}: one-launch vs op sequence", flush=True)
+        got, want = a.step(t), b.step(t)
+        parity(got, want, where=f"logits at {position + i}")
+        assert O.select_greedy(got) == O.select_greedy(want)
+    for layer in range(c.num_layers):
+        for which in range(4):
+            parity(a.state(layer, which), b.state(layer, which), where=f"state {layer}/{which} at {position}")
+
+
+def test_qwen08b_one_launch_greedy_matches_op_sequence(qwen08b_models):
+    """BASELINE config 2's decode shape (a 454-token prompt) for 24 greedy
+    tokens: the one-launch path and the op sequence pick identical IDs."""
+    fast, ops = qwen08b_models
+    prompt = [int(v) for v in np.random.default_rng(4).integers(0, 248320, 454)]
+    got = []
+    for m in (fast, ops):
+        print(f"prefill 454 + 24 greedy, plan={m is fast}", flush=True)
+        run = m.new_run(512, chunk=512)
+        logits = run.prefill(prompt)
+        ids, _ = run.decode_greedy(O.select_greedy(logits), 24)
+        got.append(ids)
+    assert got[0] == got[1]
