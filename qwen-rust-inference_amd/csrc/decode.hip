@@ -3,12 +3,11 @@
 // sequence for one token computes (the engine's forward_body; arithmetic of
 // every step as in native/rocm/reference.h), with fp32 sums in its own order.
 //
-// Why one launch: at batch 1 the step is a chain of ~120 dependent stages
+// Why one launch: at batch 1 the step is a chain of ~130 dependent stages
 // (each projection needs the whole previous vector). As separate kernels each
 // stage pays a dispatch, a ramp-up and a drain (~2-5 us for the small
 // matrices) and the step cannot approach the HBM roofline. Here 256 blocks of
-// 8 waves stay resident (cooperative launch), and a stage boundary is a flag
-// barrier of ~1.5 us.
+// 8 waves stay resident (cooperative launch) and walk the stage list together.
 //
 // Structure:
 //   * The phase list: per DeltaNet layer in-proj + conv, mixer (+ z rows),
@@ -18,19 +17,25 @@
 //     (unit u = wave * 256 + block), so partial phases still use every CU.
 //   * A wave's share of any phase's weights (and DeltaNet state / KV rows,
 //     none of which depend on this token's activations) is at most 16 x 16
-//     bytes per lane. Right after a wave signals phase p it issues the loads
-//     of phase p + 1 into that register buffer, then waits for the barrier:
-//     HBM streams the next stage while the barrier resolves.
-//   * Every global access is a buffer instruction (one 32-bit lane offset, the
-//     base in SGPRs). Activations crossing blocks are written and read with
-//     the sc0 sc1 (system-coherent, write-through / cache-bypassing) policy;
-//     a barrier is s_waitcnt on the writer's stores, then a per-block flag
-//     (the last of the block's 8 waves publishes it), polled by wave 0 of each
-//     block and handed to the other waves through LDS. No L2 writeback or
-//     invalidate is needed and no atomic is contended.
-//   * Every wait is bounded by the 100 MHz real-time counter; on a time-out
-//     the wave records an error (picks[1] = 1e30, a non-finite count the
-//     engine refuses) and leaves, and every other wave leaves at its next wait.
+//     bytes per lane. Right after a wave finishes phase p it issues the loads
+//     of phase p + 1 into that register buffer, so HBM streams the next stage
+//     while the wave waits for that stage's inputs.
+//   * There is no grid barrier. Every activation crossing blocks is stored as
+//     a (value, tag) pair in ONE 8-byte system-coherent write (sc0 sc1,
+//     write-through), tag = (launch epoch, producing phase). A consumer polls
+//     the pairs it needs until every tag is the expected one: data and
+//     readiness arrive in the same read. Each buffer is rewritten only after
+//     every reader of its previous contents has produced something the writer
+//     transitively needs, so a consumer never sees a later phase's value.
+//     (The attention split partials are plain stores published by a tagged
+//     (max, sum) pair written after an s_waitcnt.)
+//   * Broadcast vectors are staged once per block in LDS (double-buffered by
+//     phase parity; one s_barrier per phase keeps the block's waves within a
+//     phase of each other, so a buffer is never rewritten while read).
+//   * Every poll is bounded by the 100 MHz real-time counter; on a time-out a
+//     lane records an error (picks[1] = 1e30, a non-finite count the engine
+//     refuses), the block's waves leave together after their next s_barrier,
+//     and blocks waiting on them time out in turn.
 #include <cstddef>
 #include <cstring>
 #include <vector>
@@ -63,22 +68,22 @@ static_assert(DIN_RPW * NW >= DIN_ROWS && GLU_RPW * NW >= I && AQKV_RPW * NW >= 
 static_assert(Z_RPW * (NW - MIX_WAVES) >= VD && COMB_WAVES <= NW && NKV * SMAX <= NW && SMAX % 64 == 0, "waves");
 static_assert(4 * DIN_RPW <= WBUF && 8 * GLU_RPW <= WBUF && 4 * AQKV_RPW <= WBUF && 4 * Z_RPW <= WBUF, "buffer");
 static_assert(I / 256 <= WBUF && VD / 256 <= WBUF && NH * HD / 256 <= WBUF && 8 <= WBUF, "buffer");
+static_assert(VD / 4 == THREADS && NH == WAVES, "one thread per 4 gated values, one wave per query head");
 
 enum : uint8_t { T_DIN, T_MIX, T_DOUT, T_GLU, T_DOWN, T_AQKV, T_ATTN, T_COMB, T_O, T_LM, T_ARG };
 
 typedef float f4 __attribute__((ext_vector_type(4)));
+typedef float f2 __attribute__((ext_vector_type(2)));
 
-// Cross-block activations of one step. pml / pacc: the attention splits'
-// (max score, exp sum) and weighted value sums per (query head, split).
+// Cross-block activations of one step, as (value, tag) pairs. pml: the
+// attention splits' (max score, tag), (exp sum, tag) per (query head, split);
+// pacc: their weighted value sums, plain floats published by the pml pair.
 struct Scratch {
-    float x[H], after[H], proj[CH], z[VD], ab[2 * VH], core[VD];
-    float mixed[QROWS], key[KVR], value[KVR], ctx[NH * HD], product[I];
-    float pml[NH * SMAX * 2];
+    f2 x[H], after[H], proj[CH], z[VD], ab[2 * VH], core[VD];
+    f2 mixed[QROWS], key[KVR], value[KVR], ctx[NH * HD], product[I];
+    f2 pml[NH * SMAX * 2];
     float pacc[NH * SMAX * HD];
-    float lmpart[NW * 3];
-};
-struct Sync {
-    unsigned flag[BLOCKS][16];
+    f2 lmpart[NW * 4];  // (max, index, non-finite count, unused) per wave
 };
 #define SOFF(field) unsigned(offsetof(::qr::dec::Scratch, field))
 
@@ -89,13 +94,12 @@ struct Args {
     const float* final_norm;
     float* logits;
     float* picks;
-    const float* rope_denom;
     Scratch* s;
-    Sync* sync;
     int token, pos, vocab, nphases;
     unsigned epoch;
     float eps;
-    uint32_t phase[MAXPH];  // type | layer << 8
+    float rope_cs[ROT / 2], rope_sn[ROT / 2];  // cos / sin of pos / theta^(2i / rot)
+    uint32_t phase[MAXPH];                     // type | layer << 8
 };
 __device__ __forceinline__ int ptype(const Args& a, int p) { return int(a.phase[p] & 255u); }
 __device__ __forceinline__ int player(const Args& a, int p) { return int(a.phase[p] >> 8); }
@@ -103,6 +107,8 @@ __device__ __forceinline__ int player(const Args& a, int p) { return int(a.phase
 // make scalar loads, so the weight pointers stay wave-uniform (in SGPRs).
 typedef const __attribute__((address_space(4))) QrDecodeLayer* LayerP;
 __device__ __forceinline__ LayerP layer(const Args& a, int L) { return (LayerP)(a.layers) + L; }
+// The tag of phase p's outputs in this launch.
+__device__ __forceinline__ unsigned tag(const Args& a, int p) { return (a.epoch << 10) | unsigned(p + 1); }
 
 // ---------------------------------------------------------------- memory helpers
 typedef __amdgpu_buffer_rsrc_t Rs;
@@ -118,24 +124,30 @@ constexpr int kSys = 1 | 16 | int(0x80000000u);
 // The typed LLVM buffer intrinsics (the clang builtins return integer
 // vectors, whose float reinterpretation can leave buffer entries in scratch).
 __device__ f4 buffer_load_f4(Rs r, unsigned voff, unsigned soff, int aux) __asm("llvm.amdgcn.raw.ptr.buffer.load.v4f32");
+__device__ f2 buffer_load_f2(Rs r, unsigned voff, unsigned soff, int aux) __asm("llvm.amdgcn.raw.ptr.buffer.load.v2f32");
 __device__ float buffer_load_f32(Rs r, unsigned voff, unsigned soff, int aux) __asm("llvm.amdgcn.raw.ptr.buffer.load.f32");
-__device__ unsigned buffer_load_u32(Rs r, unsigned voff, unsigned soff, int aux) __asm("llvm.amdgcn.raw.ptr.buffer.load.i32");
 __device__ void buffer_store_f32(float v, Rs r, unsigned voff, unsigned soff, int aux) __asm("llvm.amdgcn.raw.ptr.buffer.store.f32");
-__device__ void buffer_store_u32(unsigned v, Rs r, unsigned voff, unsigned soff, int aux) __asm("llvm.amdgcn.raw.ptr.buffer.store.i32");
+__device__ void buffer_store_f2(f2 v, Rs r, unsigned voff, unsigned soff, int aux) __asm("llvm.amdgcn.raw.ptr.buffer.store.v2f32");
+__device__ void buffer_store_f4(f4 v, Rs r, unsigned voff, unsigned soff, int aux) __asm("llvm.amdgcn.raw.ptr.buffer.store.v4f32");
 
 __device__ __forceinline__ f4 ldw(Rs r, unsigned off, unsigned soff) { return buffer_load_f4(r, off, soff, kNT); }
 __device__ __forceinline__ f4 ldp4(Rs r, unsigned off, unsigned soff) { return buffer_load_f4(r, off, soff, 0); }
 __device__ __forceinline__ float ldp(Rs r, unsigned off) { return buffer_load_f32(r, off, 0, 0); }
 __device__ __forceinline__ void stp(Rs r, unsigned off, float v) { buffer_store_f32(v, r, off, 0, 0); }
+__device__ __forceinline__ void stp4(Rs r, unsigned off, f4 v) { buffer_store_f4(v, r, off, 0, 0); }
 __device__ __forceinline__ f4 ldx4(Rs r, unsigned off) { return buffer_load_f4(r, off, 0, kSys); }
-__device__ __forceinline__ float ldx(Rs r, unsigned off) { return buffer_load_f32(r, off, 0, kSys); }
+__device__ __forceinline__ f2 ldx2(Rs r, unsigned off) { return buffer_load_f2(r, off, 0, kSys); }
 __device__ __forceinline__ void stx(Rs r, unsigned off, float v) { buffer_store_f32(v, r, off, 0, kSys); }
-__device__ __forceinline__ unsigned ldu(Rs r, unsigned off) { return buffer_load_u32(r, off, 0, kSys); }
-__device__ __forceinline__ void stu(Rs r, unsigned off, unsigned v) { buffer_store_u32(v, r, off, 0, kSys); }
+__device__ __forceinline__ void stx4(Rs r, unsigned off, f4 v) { buffer_store_f4(v, r, off, 0, kSys); }
+// A (value, tag) pair in one 8-byte write.
+__device__ __forceinline__ void stt(Rs r, unsigned off, float v, unsigned t) {
+    buffer_store_f2(f2{v, __uint_as_float(t)}, r, off, 0, kSys);
+}
 __device__ __forceinline__ float dot4(f4 a, f4 b) { return a.x * b.x + a.y * b.y + a.z * b.z + a.w * b.w; }
 __device__ __forceinline__ float fdot4(f4 a, f4 b, float acc) {
     return fmaf(a.x, b.x, fmaf(a.y, b.y, fmaf(a.z, b.z, fmaf(a.w, b.w, acc))));
 }
+__device__ __forceinline__ f4 lds4(const float* p) { return *reinterpret_cast<const f4*>(p); }
 __device__ __forceinline__ void compiler_fence() { __atomic_signal_fence(__ATOMIC_SEQ_CST); }
 // The lane index and the wave's unit index are re-materialised in every phase
 // (an empty asm makes them opaque): otherwise the compiler hoists each
@@ -151,104 +163,109 @@ __device__ __forceinline__ int opaque_uniform(int v) {
     return v;
 }
 
-// ---------------------------------------------------------------- barrier
+// ---------------------------------------------------------------- LDS, waits
 struct Lds {
-    alignas(16) float wave[WAVES][2 * HD + ROT];  // wave-private scratch
-    unsigned done[4];
-    unsigned seen;
-    unsigned fail;
+    alignas(16) float act[2][2 * VD];       // staged broadcast vector, by phase parity
+    alignas(16) float nw[2][H];             // staged (1 + w) norm weights, by phase parity
+    alignas(16) float wave[WAVES][2 * HD];  // wave-private scratch
+    int fail;  // the earliest phase in which a lane of the block timed out (kNoFail: none)
 };
+constexpr int kNoFail = 0x7fffffff;
 
 constexpr unsigned long long kTimeout = 50000000ull;  // 0.5 s at 100 MHz
 
-__device__ __forceinline__ unsigned tag(const Args& a, int p) { return (a.epoch << 10) | unsigned(p + 1); }
-__device__ __forceinline__ bool reached(unsigned flag, unsigned target) { return int(flag - target) >= 0; }
-
-__device__ void record_failure(const Args& a, Lds& l) {
+__device__ void record_failure(const Args& a, Lds& l, int p) {
     stx(rsrc(a.picks), 4, 1e30f);
-    __hip_atomic_store(&l.fail, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    __hip_atomic_fetch_min(&l.fail, p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
-
-// Phase p's outputs of this wave are written; count the wave in, and the last
-// of the block's waves publishes the block's flag.
-__device__ void signal(const Args& a, Lds& l, int p) {
-    compiler_fence();
-    __builtin_amdgcn_s_waitcnt(0);  // every store of this wave has completed
-    compiler_fence();
-    if (lane_id() == 0) {
-        unsigned old = __hip_atomic_fetch_add(&l.done[p & 3], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-        if (old + 1 == unsigned(WAVES)) {
-            __hip_atomic_store(&l.done[p & 3], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-            stu(rsrc(a.sync), unsigned(blockIdx.x) * 64u, tag(a, p));
+__device__ __forceinline__ int fail_phase(Lds& l) {
+    return __hip_atomic_load(&l.fail, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+__device__ __forceinline__ bool failed(Lds& l) { return fail_phase(l) != kNoFail; }
+// Polls the two pairs at `off` until both carry tag `want` (or time-out, or
+// the block has failed); returns the two values. `p`: the polling phase.
+__device__ f2 wait2(const Args& a, Rs r, unsigned off, unsigned want, Lds& l, unsigned long long start, int p) {
+    for (;;) {
+        const f4 v = ldx4(r, off);
+        if (__float_as_uint(v.y) == want && __float_as_uint(v.w) == want) return f2{v.x, v.z};
+        if (wall_clock64() - start > kTimeout || failed(l)) {
+            record_failure(a, l, p);
+            return f2{0.f, 0.f};
         }
+        __builtin_amdgcn_s_sleep(1);
     }
 }
-
-// Wait until phase p has completed in every block. Wave 0 of the block polls
-// the block flags (4 per lane) and passes the news on in LDS.
-__device__ bool wait_phase(const Args& a, Lds& l, int p, bool poller) {
-    const unsigned target = tag(a, p);
-    const unsigned long long start = wall_clock64();
-    if (poller) {
-        const Rs fl = rsrc(a.sync);
-        for (;;) {
-            bool ok = true;
-#pragma unroll
-            for (int k = 0; k < BLOCKS / 64; ++k) ok = ok && reached(ldu(fl, (lane_id() + 64u * k) * 64u), target);
-            if (__all(ok)) break;
-            if (wall_clock64() - start > kTimeout ||
-                __hip_atomic_load(&l.fail, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP)) {
-                record_failure(a, l);
-                return false;
-            }
+__device__ float wait1(const Args& a, Rs r, unsigned off, unsigned want, Lds& l, unsigned long long start, int p) {
+    for (;;) {
+        const f2 v = ldx2(r, off);
+        if (__float_as_uint(v.y) == want) return v.x;
+        if (wall_clock64() - start > kTimeout || failed(l)) {
+            record_failure(a, l, p);
+            return 0.f;
         }
-        if (lane_id() == 0) __hip_atomic_store(&l.seen, target, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-    } else {
-        while (!reached(__hip_atomic_load(&l.seen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP), target)) {
-            __builtin_amdgcn_s_sleep(2);
-            if (wall_clock64() - start > kTimeout ||
-                __hip_atomic_load(&l.fail, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP)) {
-                record_failure(a, l);
-                return false;
-            }
-        }
+        __builtin_amdgcn_s_sleep(1);
     }
+}
+// Block barrier of phase p without a memory fence: LDS writes done
+// (lgkmcnt(0)), then s_barrier; the outstanding prefetch loads stay in
+// flight. Every wave of the block calls it once per phase. False when a lane
+// of the block timed out in an earlier phase: every such record was made
+// before its wave reached this barrier, so the block's waves agree (a record
+// of phase p itself is acted on at the next barrier).
+__device__ __forceinline__ bool bsync(Lds& l, int p) {
     compiler_fence();
-    return true;
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0); vmcnt, expcnt not waited
+    __builtin_amdgcn_s_barrier();
+    compiler_fence();
+    return fail_phase(l) >= p;
 }
 
-// ---------------------------------------------------------------- phase helpers
+// ---------------------------------------------------------------- staging
 __device__ __forceinline__ float silu(float x) { return x * sigmoidf_(x); }
 
-// The layer's input residual in chunks (element 4(lane + 64v) .. +3 in xv[v]):
-// the embedding row of the token for layer 0, else the scratch x.
-__device__ __forceinline__ void load_input(const Args& a, Rs rs, int L, f4 (&xv)[4]) {
-    const unsigned lo = 16u * lane_id();
+// The block's 512 threads copy n (even) tagged values at scratch offset `off`
+// into dst, each pair polled until tagged `want`.
+__device__ void stage_tagged(const Args& a, Rs rs, unsigned off, int n, unsigned want, float* dst, Lds& l, int p) {
+    const unsigned long long start = wall_clock64();
+    for (int i = int(threadIdx.x); i < n / 2; i += THREADS)
+        *reinterpret_cast<f2*>(dst + 2 * i) = wait2(a, rs, off + 16u * unsigned(i), want, l, start, p);
+}
+// (1 + w) of an H-long norm weight into l.nw[par] (plain loads, issued before
+// the tagged polls so their latency overlaps).
+__device__ __forceinline__ void stage_norm(const float* w, int par, Lds& l) {
+    const int t = int(threadIdx.x);
+    if (t < H / 4) *reinterpret_cast<f4*>(&l.nw[par][4 * t]) = f4(1.f) + ldp4(rsrc(w), 16u * unsigned(t), 0);
+}
+// The layer's input residual into l.act[par]: the token's embedding row for
+// layer 0, else x as written by phase `producer`.
+__device__ __forceinline__ void stage_input(const Args& a, Rs rs, int L, int producer, int par, Lds& l, int p) {
     if (L == 0) {
-        const Rs re = rsrc(a.embedding);
-        const unsigned row = unsigned(a.token) * unsigned(H * 4);
-#pragma unroll
-        for (int v = 0; v < 4; ++v) xv[v] = ldp4(re, lo + 1024u * v, row);
+        const int t = int(threadIdx.x);
+        if (t < H / 4)
+            *reinterpret_cast<f4*>(&l.act[par][4 * t]) =
+                ldp4(rsrc(a.embedding), unsigned(a.token) * unsigned(H * 4) + 16u * unsigned(t), 0);
     } else {
-#pragma unroll
-        for (int v = 0; v < 4; ++v) xv[v] = ldx4(rs, SOFF(x) + lo + 1024u * v);
+        stage_tagged(a, rs, SOFF(x), H, tag(a, producer), l.act[par], l, p);
     }
 }
-__device__ __forceinline__ float input_at(const Args& a, Rs rs, int L, int i) {
+__device__ __forceinline__ float input_at(const Args& a, Rs rs, int L, int producer, int i, Lds& l, int p) {
     if (L == 0) return ldp(rsrc(a.embedding), (unsigned(a.token) * unsigned(H) + unsigned(i)) * 4u);
-    return ldx(rs, SOFF(x) + 4u * unsigned(i));
+    return wait1(a, rs, SOFF(x) + 8u * unsigned(i), tag(a, producer), l, wall_clock64(), p);
 }
-// RMSNorm of the H-long vector held in chunks, Qwen (1 + w) scale (reference.h:120-126).
-__device__ __forceinline__ void norm_chunks(f4 (&xv)[4], const float* w, float eps) {
-    const unsigned lo = 16u * lane_id();
-    const Rs rw = rsrc(w);
+// The staged H-vector in chunks (element 4(lane + 64v) .. +3 in xv[v]) times
+// its RMSNorm and the staged (1 + w) (reference.h:120-126).
+__device__ __forceinline__ void normed_chunks(const Lds& l, int par, float eps, f4 (&xv)[4]) {
+    const unsigned lane = lane_id();
     float ss = 0.f;
 #pragma unroll
-    for (int v = 0; v < 4; ++v) ss += dot4(xv[v], xv[v]);
+    for (int v = 0; v < 4; ++v) {
+        xv[v] = lds4(&l.act[par][4 * (lane + 64 * v)]);
+        ss += dot4(xv[v], xv[v]);
+    }
     ss = wave_sum(ss);
     const float r = 1.f / sqrtf(ss / float(H) + eps);
 #pragma unroll
-    for (int v = 0; v < 4; ++v) xv[v] = (xv[v] * r) * (f4(1.f) + ldp4(rw, lo + 1024u * v, 0));
+    for (int v = 0; v < 4; ++v) xv[v] = (xv[v] * r) * lds4(&l.nw[par][4 * (lane + 64 * v)]);
 }
 // Row `r` of an [rows, H] matrix into wb[AT .. AT + 3].
 template <int AT>
@@ -264,6 +281,20 @@ __device__ __forceinline__ float dot_row_h(const f4* wb, const f4 (&xv)[4]) {
     for (int v = 0; v < 4; ++v) acc = fdot4(wb[AT + v], xv[v], acc);
     return wave_sum(acc);
 }
+// Dot of a prefetched row of K * 256 columns with the staged vector.
+template <int K>
+__device__ __forceinline__ float dot_row_lds(const f4* wb, const float* act) {
+    const unsigned lane = lane_id();
+    float acc = 0.f;
+#pragma unroll
+    for (int v = 0; v < K; ++v) acc = fdot4(wb[v], lds4(act + 4 * (lane + 64 * v)), acc);
+    return wave_sum(acc);
+}
+
+// ---------------------------------------------------------------- phases
+// Each phase: every wave of the block stages (loads independent of this
+// token's activations first, then the tagged inputs), one bsync, then the
+// waves with work compute and store their tagged outputs. False: failed.
 
 // ---- T_DIN: qkv | a | b rows of a DeltaNet layer (z rows: phase T_MIX), then
 // the causal conv + SiLU of each qkv channel (reference.h:96-116): the wave
@@ -291,39 +322,50 @@ __device__ __forceinline__ void din_row(const f4* wb, const f4 (&xv)[4], int u, 
         if (lane_id() == R) mine = acc;
     }
 }
-__device__ void phase_din(const Args& a, Rs rs, LayerP w, int L, int u, const f4* wb) {
-    if (u * DIN_RPW >= DIN_ROWS) return;
+__device__ bool phase_din(const Args& a, Rs rs, LayerP w, int L, int p, int u, const f4* wb, Lds& l) {
+    const int par = p & 1;
+    const int lane = int(lane_id()), row = u * DIN_RPW + lane;
+    const bool conv = lane < DIN_RPW && row < CH;
+    float h0 = 0.f, h1 = 0.f, h2 = 0.f, c0 = 0.f, c1 = 0.f, c2 = 0.f, c3 = 0.f;
+    const Rs hs = rsrc(w->conv_state);
+    const unsigned ho = unsigned(row) * (CONVK - 1) * 4u;
+    if (conv) {  // this channel's history and weights
+        const Rs cw = rsrc(w->conv_w);
+        const unsigned co = unsigned(row) * CONVK * 4u;
+        h0 = ldp(hs, ho), h1 = ldp(hs, ho + 4), h2 = ldp(hs, ho + 8);
+        c0 = ldp(cw, co), c1 = ldp(cw, co + 4), c2 = ldp(cw, co + 8), c3 = ldp(cw, co + 12);
+    }
+    stage_norm(w->input_norm, par, l);
+    stage_input(a, rs, L, p - 1, par, l, p);
+    if (!bsync(l, p)) return false;
+    if (u * DIN_RPW >= DIN_ROWS) return true;
     f4 xv[4];
-    load_input(a, rs, L, xv);
-    norm_chunks(xv, w->input_norm, a.eps);
+    normed_chunks(l, par, a.eps, xv);
     float mine = 0.f;  // lane r: the dot product of row u * DIN_RPW + r
     din_row<0>(wb, xv, u, mine);
     din_row<1>(wb, xv, u, mine);
     din_row<2>(wb, xv, u, mine);
     din_row<3>(wb, xv, u, mine);
-    const int lane = int(lane_id()), row = u * DIN_RPW + lane;
-    if (lane < DIN_RPW && row < DIN_ROWS) {
-        if (row < CH) {
-            const Rs hs = rsrc(w->conv_state), cw = rsrc(w->conv_w);
-            const unsigned ho = unsigned(row) * (CONVK - 1) * 4u, co = unsigned(row) * CONVK * 4u;
-            const float h0 = ldp(hs, ho), h1 = ldp(hs, ho + 4), h2 = ldp(hs, ho + 8);
-            float sum = 0.f;
-            sum += h0 * ldp(cw, co);
-            sum += h1 * ldp(cw, co + 4);
-            sum += h2 * ldp(cw, co + 8);
-            sum += mine * ldp(cw, co + 12);
-            stp(hs, ho, h1);
-            stp(hs, ho + 4, h2);
-            stp(hs, ho + 8, mine);
-            stx(rs, SOFF(proj) + 4u * unsigned(row), silu(sum));
-        } else {
-            stx(rs, SOFF(ab) + 4u * unsigned(row - CH), mine);
-        }
+    const unsigned t = tag(a, p);
+    if (conv) {
+        float sum = 0.f;
+        sum += h0 * c0;
+        sum += h1 * c1;
+        sum += h2 * c2;
+        sum += mine * c3;
+        stp(hs, ho, h1);
+        stp(hs, ho + 4, h2);
+        stp(hs, ho + 8, mine);
+        stt(rs, SOFF(proj) + 8u * unsigned(row), silu(sum), t);
+    } else if (lane < DIN_RPW && row < DIN_ROWS) {
+        stt(rs, SOFF(ab) + 8u * unsigned(row - CH), mine, t);
     }
+    return true;
 }
 
 // ---- T_MIX: L2 q/k, gates and the gated delta rule for 16 value columns of
-// one head per wave (units 0..127); z = in_proj_z . n on the other units.
+// one head per wave (units 0..127); silu(z), z = in_proj_z . n, on the other
+// units (only silu(z) is used: the gated norm's gate, reference.h:201-207).
 template <int R>
 __device__ __forceinline__ void z_load(LayerP w, int u, f4* wb) {
     const int row = (u - MIX_WAVES) * Z_RPW + R;
@@ -347,31 +389,40 @@ __device__ __forceinline__ void prefetch_mix(LayerP w, int u, f4* wb) {
     }
 }
 template <int R>
-__device__ __forceinline__ void z_row(Rs rs, const f4* wb, const f4 (&xv)[4], int u) {
+__device__ __forceinline__ void z_row(Rs rs, const f4* wb, const f4 (&xv)[4], int u, unsigned t) {
     const int row = (u - MIX_WAVES) * Z_RPW + R;
     if (row < VD) {
         const float acc = dot_row_h<4 * R>(wb, xv);
-        if (lane_id() == 0) stx(rs, SOFF(z) + 4u * unsigned(row), acc);
+        if (lane_id() == 0) stt(rs, SOFF(z) + 8u * unsigned(row), silu(acc), t);
     }
 }
-__device__ void phase_mix(const Args& a, Rs rs, LayerP w, int L, int u, f4* wb, Lds& l) {
+__device__ bool phase_mix(const Args& a, Rs rs, LayerP w, int L, int p, int u, f4* wb, Lds& l) {
+    const int par = p & 1;
+    stage_norm(w->input_norm, par, l);
+    stage_input(a, rs, L, p - 2, par, l, p);
+    if (!bsync(l, p)) return false;
+    const unsigned t = tag(a, p);
     if (u >= MIX_WAVES) {
-        if ((u - MIX_WAVES) * Z_RPW >= VD) return;
+        if ((u - MIX_WAVES) * Z_RPW >= VD) return true;
         f4 xv[4];
-        load_input(a, rs, L, xv);
-        norm_chunks(xv, w->input_norm, a.eps);
-        z_row<0>(rs, wb, xv, u);
-        z_row<1>(rs, wb, xv, u);
-        return;
+        normed_chunks(l, par, a.eps, xv);
+        z_row<0>(rs, wb, xv, u, t);
+        z_row<1>(rs, wb, xv, u, t);
+        return true;
     }
     const unsigned lane = lane_id();
     const int wave = int(threadIdx.x >> 6);
-    const int h = u >> 3, cg = u & 7, p = int(lane >> 4), j = cg * 16 + int(lane & 15);
-    // convolved q and k of head h (lane: q[lane], q[lane + 64], k[lane], k[lane + 64])
-    const unsigned qo = SOFF(proj) + (unsigned(h) * DK + lane) * 4u, ko = qo + KD * 4u;
-    const float q0 = ldx(rs, qo), q1 = ldx(rs, qo + 256u), k0 = ldx(rs, ko), k1 = ldx(rs, ko + 256u);
-    const float v = ldx(rs, SOFF(proj) + unsigned(2 * KD + h * DV + j) * 4u);
-    const float av = ldx(rs, SOFF(ab) + 4u * unsigned(h)), bv = ldx(rs, SOFF(ab) + 4u * unsigned(VH + h));
+    const int h = u >> 3, cg = u & 7, pr = int(lane >> 4), j = cg * 16 + int(lane & 15);
+    const float dt = w->gates[h], alog = w->gates[VH + h];
+    // convolved q and k of head h (lane: q[lane], q[lane + 64], k[lane], k[lane + 64]), v of column j
+    const unsigned want = tag(a, p - 1);
+    const unsigned long long start = wall_clock64();
+    const unsigned qo = SOFF(proj) + (unsigned(h) * DK + lane) * 8u, ko = qo + KD * 8u;
+    const float q0 = wait1(a, rs, qo, want, l, start, p), q1 = wait1(a, rs, qo + 512u, want, l, start, p);
+    const float k0 = wait1(a, rs, ko, want, l, start, p), k1 = wait1(a, rs, ko + 512u, want, l, start, p);
+    const float v = wait1(a, rs, SOFF(proj) + unsigned(2 * KD + h * DV + j) * 8u, want, l, start, p);
+    const float av = wait1(a, rs, SOFF(ab) + 8u * unsigned(h), want, l, start, p);
+    const float bv = wait1(a, rs, SOFF(ab) + 8u * unsigned(VH + h), want, l, start, p);
     // L2 norms (reference.h:134-143), q / sqrt(dk)
     const float sq = wave_sum(q0 * q0 + q1 * q1);
     const float sk = wave_sum(k0 * k0 + k1 * k1);
@@ -382,19 +433,18 @@ __device__ void phase_mix(const Args& a, Rs rs, LayerP w, int L, int u, f4* wb, 
     lw[128 + lane] = k0 * rk;
     lw[192 + lane] = k1 * rk;
     compiler_fence();
-    const float* qq = lw + p * 32;        // this lane's 32 key rows of q / sqrt(dk)
-    const float* kk = lw + 128 + p * 32;  // and of k
+    const float* qq = lw + pr * 32;        // this lane's 32 key rows of q / sqrt(dk)
+    const float* kk = lw + 128 + pr * 32;  // and of k
     // gates (reference.h:48-60, 144-148)
-    const float log_decay = -expf(w->gates[VH + h]) * softplusf_(av + w->gates[h]);
+    const float log_decay = -expf(alog) * softplusf_(av + dt);
     const float beta = sigmoidf_(bv);
     const float decay = expf(log_decay);
-    // the rule (reference.h:149-170) on rows p*32 .. p*32+31 of column j, in place in wb[0..7]
+    // the rule (reference.h:149-170) on rows pr*32 .. pr*32+31 of column j, in place in wb[0..7]
     float m = 0.f;
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
         wb[k] *= decay;
-        const f4 kv = *reinterpret_cast<const f4*>(kk + 4 * k);
-        m = fdot4(wb[k], kv, m);
+        m = fdot4(wb[k], lds4(kk + 4 * k), m);
     }
     m += __shfl_xor(m, 16, 64);
     m += __shfl_xor(m, 32, 64);
@@ -402,14 +452,13 @@ __device__ void phase_mix(const Args& a, Rs rs, LayerP w, int L, int u, f4* wb, 
     float o = 0.f;
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
-        const f4 kv = *reinterpret_cast<const f4*>(kk + 4 * k), qv = *reinterpret_cast<const f4*>(qq + 4 * k);
-        wb[k] += kv * delta;
-        o = fdot4(wb[k], qv, o);
+        wb[k] += lds4(kk + 4 * k) * delta;
+        o = fdot4(wb[k], lds4(qq + 4 * k), o);
     }
     o += __shfl_xor(o, 16, 64);
     o += __shfl_xor(o, 32, 64);
     const Rs S = rsrc(w->recurrent);
-    const unsigned base = ((unsigned(h) * DK + unsigned(p) * 32u) * DV + unsigned(j)) * 4u;
+    const unsigned base = ((unsigned(h) * DK + unsigned(pr) * 32u) * DV + unsigned(j)) * 4u;
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
         const unsigned so = base + unsigned(4 * k) * DV * 4u;
@@ -418,10 +467,13 @@ __device__ void phase_mix(const Args& a, Rs rs, LayerP w, int L, int u, f4* wb, 
         stp(S, so + 2u * DV * 4u, wb[k].z);
         stp(S, so + 3u * DV * 4u, wb[k].w);
     }
-    if (p == 0) stx(rs, SOFF(core) + unsigned(h * DV + j) * 4u, o);
+    if (pr == 0) stt(rs, SOFF(core) + unsigned(h * DV + j) * 8u, o, t);
+    return true;
 }
 
-// ---- T_DOUT: gated RMSNorm of core with silu(z) (reference.h:201-207), then
+// ---- T_DOUT: the gated RMSNorm silu(z) * RmsNorm(core) (direct weight,
+// reference.h:201-207) is built once per block in LDS (thread t: elements
+// 4t .. 4t+3, its head's 32 threads reduce the sum of squares), then
 // out_proj row u plus the residual.
 template <int COLS>
 __device__ __forceinline__ void prefetch_row(const float* m, int row, int rows, f4* wb) {
@@ -431,22 +483,28 @@ __device__ __forceinline__ void prefetch_row(const float* m, int row, int rows, 
 #pragma unroll
     for (int v = 0; v < COLS / 256; ++v) wb[v] = ldw(r, lo + 1024u * v, ro);
 }
-__device__ void phase_dout(const Args& a, Rs rs, LayerP w, int L, int u, const f4* wb) {
-    if (u >= H) return;
-    const unsigned lane = lane_id();
-    const f4 nw = ldp4(rsrc(w->norm_w), 16u * (lane & 31), 0);  // element 4c % 128 of chunk c = lane + 64k
-    float acc = 0.f;
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-        const unsigned c = 16u * (lane + 64u * k);
-        const f4 core = ldx4(rs, SOFF(core) + c), zz = ldx4(rs, SOFF(z) + c);
-        const float ss = group_sum<32>(dot4(core, core));  // head 2k + lane / 32
+__device__ bool phase_dout(const Args& a, Rs rs, LayerP w, int L, int p, int u, const f4* wb, Lds& l) {
+    const int par = p & 1;
+    {
+        const unsigned th = threadIdx.x;
+        const f4 nw = ldp4(rsrc(w->norm_w), 16u * (th & 31), 0);
+        const unsigned want = tag(a, p - 1);
+        const unsigned long long start = wall_clock64();
+        const f2 c01 = wait2(a, rs, SOFF(core) + 32u * th, want, l, start, p);
+        const f2 c23 = wait2(a, rs, SOFF(core) + 32u * th + 16u, want, l, start, p);
+        const f2 z01 = wait2(a, rs, SOFF(z) + 32u * th, want, l, start, p);
+        const f2 z23 = wait2(a, rs, SOFF(z) + 32u * th + 16u, want, l, start, p);
+        const f4 core = f4{c01.x, c01.y, c23.x, c23.y}, sz = f4{z01.x, z01.y, z23.x, z23.y};
+        const float ss = group_sum<32>(dot4(core, core));
         const float r = 1.f / sqrtf(ss / float(DV) + a.eps);
-        const f4 g = f4{silu(zz.x), silu(zz.y), silu(zz.z), silu(zz.w)} * ((core * r) * nw);
-        acc = fdot4(wb[k], g, acc);
+        *reinterpret_cast<f4*>(&l.act[par][4 * th]) = sz * ((core * r) * nw);
     }
-    acc = wave_sum(acc);
-    if (lane == 0) stx(rs, SOFF(after) + 4u * unsigned(u), input_at(a, rs, L, u) + acc);
+    if (!bsync(l, p)) return false;
+    if (u >= H) return true;
+    const float acc = dot_row_lds<VD / 256>(wb, l.act[par]);
+    const float res = input_at(a, rs, L, p - 3, u, l, p);
+    if (lane_id() == 0) stt(rs, SOFF(after) + 8u * unsigned(u), res + acc, tag(a, p));
+    return true;
 }
 
 // ---- T_GLU: product = silu(gate . n) * (up . n), n = post RMSNorm of `after`
@@ -463,33 +521,36 @@ __device__ __forceinline__ void prefetch_glu(LayerP w, int u, f4* wb) {
     glu_load<1>(w, u, wb);
 }
 template <int R>
-__device__ __forceinline__ void glu_row(Rs rs, const f4* wb, const f4 (&xv)[4], int u) {
+__device__ __forceinline__ void glu_row(Rs rs, const f4* wb, const f4 (&xv)[4], int u, unsigned t) {
     const int row = u * GLU_RPW + R;
     if (row < I) {
         const float g = dot_row_h<8 * R>(wb, xv), up = dot_row_h<8 * R + 4>(wb, xv);
-        if (lane_id() == 0) stx(rs, SOFF(product) + 4u * unsigned(row), silu(g) * up);
+        if (lane_id() == 0) stt(rs, SOFF(product) + 8u * unsigned(row), silu(g) * up, t);
     }
 }
-__device__ void phase_glu(const Args& a, Rs rs, LayerP w, int u, const f4* wb) {
-    if (u * GLU_RPW >= I) return;
+__device__ bool phase_glu(const Args& a, Rs rs, LayerP w, int p, int u, const f4* wb, Lds& l) {
+    const int par = p & 1;
+    stage_norm(w->post_norm, par, l);
+    stage_tagged(a, rs, SOFF(after), H, tag(a, p - 1), l.act[par], l, p);
+    if (!bsync(l, p)) return false;
+    if (u * GLU_RPW >= I) return true;
     f4 xv[4];
-    const unsigned lo = 16u * lane_id();
-#pragma unroll
-    for (int v = 0; v < 4; ++v) xv[v] = ldx4(rs, SOFF(after) + lo + 1024u * v);
-    norm_chunks(xv, w->post_norm, a.eps);
-    glu_row<0>(rs, wb, xv, u);
-    glu_row<1>(rs, wb, xv, u);
+    normed_chunks(l, par, a.eps, xv);
+    glu_row<0>(rs, wb, xv, u, tag(a, p));
+    glu_row<1>(rs, wb, xv, u, tag(a, p));
+    return true;
 }
 
 // ---- T_DOWN: x = after + down . product
-__device__ void phase_down(Rs rs, int u, const f4* wb) {
-    if (u >= H) return;
-    const unsigned lo = 16u * lane_id();
-    float acc = 0.f;
-#pragma unroll
-    for (int v = 0; v < I / 256; ++v) acc = fdot4(wb[v], ldx4(rs, SOFF(product) + lo + 1024u * v), acc);
-    acc = wave_sum(acc);
-    if (lane_id() == 0) stx(rs, SOFF(x) + 4u * unsigned(u), ldx(rs, SOFF(after) + 4u * unsigned(u)) + acc);
+__device__ bool phase_down(const Args& a, Rs rs, int p, int u, const f4* wb, Lds& l) {
+    const int par = p & 1;
+    stage_tagged(a, rs, SOFF(product), I, tag(a, p - 1), l.act[par], l, p);
+    if (!bsync(l, p)) return false;
+    if (u >= H) return true;
+    const float acc = dot_row_lds<I / 256>(wb, l.act[par]);
+    const float res = wait1(a, rs, SOFF(after) + 8u * unsigned(u), tag(a, p - 2), l, wall_clock64(), p);
+    if (lane_id() == 0) stt(rs, SOFF(x) + 8u * unsigned(u), res + acc, tag(a, p));
+    return true;
 }
 
 // ---- T_AQKV: q ([Q | gate] per head), k, v rows of an attention layer
@@ -509,26 +570,30 @@ __device__ __forceinline__ void prefetch_aqkv(LayerP w, int u, f4* wb) {
     aqkv_load<2>(w, u, wb);
 }
 template <int R>
-__device__ __forceinline__ void aqkv_row(Rs rs, const f4* wb, const f4 (&xv)[4], int u) {
+__device__ __forceinline__ void aqkv_row(Rs rs, const f4* wb, const f4 (&xv)[4], int u, unsigned t) {
     const int row = u * AQKV_RPW + R;
     if (row < AQKV_ROWS) {
         const float acc = dot_row_h<4 * R>(wb, xv);
         if (lane_id() == 0) {
-            const unsigned dst = row < QROWS ? SOFF(mixed) + 4u * unsigned(row)
-                                 : row < QROWS + KVR ? SOFF(key) + 4u * unsigned(row - QROWS)
-                                                     : SOFF(value) + 4u * unsigned(row - QROWS - KVR);
-            stx(rs, dst, acc);
+            const unsigned dst = row < QROWS ? SOFF(mixed) + 8u * unsigned(row)
+                                 : row < QROWS + KVR ? SOFF(key) + 8u * unsigned(row - QROWS)
+                                                     : SOFF(value) + 8u * unsigned(row - QROWS - KVR);
+            stt(rs, dst, acc, t);
         }
     }
 }
-__device__ void phase_aqkv(const Args& a, Rs rs, LayerP w, int L, int u, const f4* wb) {
-    if (u * AQKV_RPW >= AQKV_ROWS) return;
+__device__ bool phase_aqkv(const Args& a, Rs rs, LayerP w, int L, int p, int u, const f4* wb, Lds& l) {
+    const int par = p & 1;
+    stage_norm(w->input_norm, par, l);
+    stage_input(a, rs, L, p - 1, par, l, p);
+    if (!bsync(l, p)) return false;
+    if (u * AQKV_RPW >= AQKV_ROWS) return true;
     f4 xv[4];
-    load_input(a, rs, L, xv);
-    norm_chunks(xv, w->input_norm, a.eps);
-    aqkv_row<0>(rs, wb, xv, u);
-    aqkv_row<1>(rs, wb, xv, u);
-    aqkv_row<2>(rs, wb, xv, u);
+    normed_chunks(l, par, a.eps, xv);
+    aqkv_row<0>(rs, wb, xv, u, tag(a, p));
+    aqkv_row<1>(rs, wb, xv, u, tag(a, p));
+    aqkv_row<2>(rs, wb, xv, u, tag(a, p));
+    return true;
 }
 
 // ---- T_ATTN: one wave per (KV head, span of positions); the 4 query heads of
@@ -556,16 +621,16 @@ __device__ __forceinline__ void load_kv_chunk(LayerP w, int kvh, int first, int 
     }
 }
 // The lanes whose position of the chunk at `first` is `pos` take the new
-// key / value (normalised, rotated) from the wave's LDS.
-__device__ __forceinline__ void patch_new(f4* buf, const float* lw, int first, int pos) {
+// key / value (normalised, rotated key) from LDS.
+__device__ __forceinline__ void patch_new(f4* buf, const float* kn, const float* vn, int first, int pos) {
     const unsigned lane = lane_id(), sub = lane & 15, slot = lane >> 4;
 #pragma unroll
     for (int step = 0; step < SPAN / 4; ++step) {
         if (first + 4 * step + int(slot) == pos) {
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                buf[step * 8 + e] = *reinterpret_cast<const f4*>(lw + sub * 16 + 4 * e);
-                buf[step * 8 + 4 + e] = *reinterpret_cast<const f4*>(lw + HD + sub * 16 + 4 * e);
+                buf[step * 8 + e] = lds4(kn + sub * 16 + 4 * e);
+                buf[step * 8 + 4 + e] = lds4(vn + sub * 16 + 4 * e);
             }
         }
     }
@@ -575,96 +640,91 @@ __device__ __forceinline__ void prefetch_attn(LayerP w, int u, int pos, f4* wb) 
     if (u >= NKV * splits) return;
     load_kv_chunk(w, u / splits, (u % splits) * span, pos, wb);
 }
-// cos / sin of the RoPE angles pos / theta^(2i / rot), i < rot / 2, one per
-// lane, into trig[0, 32) / trig[32, 64) (reference.h:41-47).
-__device__ __forceinline__ void rope_trig(float* trig, const float* denom, int pos) {
+// RMSNorm (1 + w) of one head's 256 dims held 4 per lane by a whole wave,
+// then rotate-half RoPE of the first 64 dims (the partner of dim d < 32 is
+// d + 32, on lane + 8), into LDS (reference.h:75-95, 41-47).
+__device__ __forceinline__ void norm_rope_head(f4 x, f4 wplus, const Args& a, float* out) {
     const unsigned lane = lane_id();
-    if (lane < ROT / 2) {
-        const float angle = float(pos) / denom[lane];
-        trig[lane] = cosf(angle);
-        trig[ROT / 2 + lane] = sinf(angle);
+    const float ss = wave_sum(dot4(x, x));
+    const float r = 1.f / sqrtf(ss / float(HD) + a.eps);
+    x = (x * r) * wplus;
+    f4 other;
+    other.x = __shfl_xor(x.x, 8, 64);
+    other.y = __shfl_xor(x.y, 8, 64);
+    other.z = __shfl_xor(x.z, 8, 64);
+    other.w = __shfl_xor(x.w, 8, 64);
+    if (lane < ROT / 4) {  // dims 4 lane .. 4 lane + 3 < 64
+        const int i = int(4 * (lane & 7));
+        const f4 cs = f4{a.rope_cs[i], a.rope_cs[i + 1], a.rope_cs[i + 2], a.rope_cs[i + 3]};
+        const f4 sn = f4{a.rope_sn[i], a.rope_sn[i + 1], a.rope_sn[i + 2], a.rope_sn[i + 3]};
+        x = lane < 8 ? x * cs - other * sn : x * cs + other * sn;
     }
-    compiler_fence();
+    *reinterpret_cast<f4*>(out + 4 * lane) = x;
 }
-// RMSNorm (1 + w) over the 256 dims spread as 16 per lane over 16 lanes, then
-// rotate-half RoPE of the first 64 dims (partner dims 32 apart live on
-// lane ^ 2). Reference: reference.h:75-95.
-__device__ __forceinline__ void norm_rope16(float (&x)[16], const float* w, const float* trig, float eps) {
-    const unsigned sub = lane_id() & 15;
-    float ss = 0.f;
-#pragma unroll
-    for (int e = 0; e < 16; ++e) ss += x[e] * x[e];
-    ss = group_sum<16>(ss);
-    const float r = 1.f / sqrtf(ss / float(HD) + eps);
-    const Rs rw = rsrc(w);
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        const f4 wv = ldp4(rw, 64u * sub + 16u * e, 0);
-        x[4 * e] = (x[4 * e] * r) * (1.f + wv.x);
-        x[4 * e + 1] = (x[4 * e + 1] * r) * (1.f + wv.y);
-        x[4 * e + 2] = (x[4 * e + 2] * r) * (1.f + wv.z);
-        x[4 * e + 3] = (x[4 * e + 3] * r) * (1.f + wv.w);
-    }
-#pragma unroll
-    for (int e = 0; e < 16; ++e) {
-        const float other = __shfl_xor(x[e], 2, 64);
-        if (sub < 4) {
-            const int i = int(sub & 1) * 16 + e;
-            const float cs = trig[i], sn = trig[ROT / 2 + i];
-            x[e] = sub < 2 ? x[e] * cs - other * sn : x[e] * cs + other * sn;
+__device__ bool phase_attn(const Args& a, Rs rs, LayerP w, int p, int u, f4* wb, Lds& l) {
+    const int par = p & 1;
+    const int pos = a.pos, len = pos + 1, span = attn_span(len), splits = (len + span - 1) / span;
+    const bool block_busy = int(blockIdx.x) < NKV * splits;  // wave 0 has the block's lowest unit
+    const int wave = int(threadIdx.x >> 6);
+    const unsigned want = tag(a, p - 1);
+    if (block_busy) {
+        // normalised, rotated q of the 8 heads (wave h: head h) and new k of the
+        // 2 KV heads (waves 0, 1) into LDS: q at act[h * HD], k at act[NH * HD + kvh * HD]
+        const unsigned lane = lane_id();
+        const Rs rn = rsrc(w->qk_norm);
+        const f4 wq = f4(1.f) + ldp4(rn, 16u * lane, 0), wk = f4(1.f) + ldp4(rn, HD * 4u + 16u * lane, 0);
+        const unsigned long long start = wall_clock64();
+        const unsigned qo = SOFF(mixed) + (unsigned(wave) * 2u * HD + 4u * lane) * 8u;
+        const f2 q01 = wait2(a, rs, qo, want, l, start, p), q23 = wait2(a, rs, qo + 16u, want, l, start, p);
+        norm_rope_head(f4{q01.x, q01.y, q23.x, q23.y}, wq, a, &l.act[par][wave * HD]);
+        if (wave < NKV) {
+            const unsigned ko = SOFF(key) + (unsigned(wave) * HD + 4u * lane) * 8u;
+            const f2 k01 = wait2(a, rs, ko, want, l, start, p), k23 = wait2(a, rs, ko + 16u, want, l, start, p);
+            norm_rope_head(f4{k01.x, k01.y, k23.x, k23.y}, wk, a, &l.act[par][NH * HD + wave * HD]);
         }
     }
-}
-__device__ void phase_attn(const Args& a, Rs rs, LayerP w, int u, f4* wb, Lds& l) {
-    const int pos = a.pos, len = pos + 1, span = attn_span(len), splits = (len + span - 1) / span;
-    if (u >= NKV * splits) return;
+    if (!bsync(l, p)) return false;
+    if (u >= NKV * splits) return true;
     const unsigned lane = lane_id(), sub = lane & 15, slot = lane >> 4;
-    const int wave = int(threadIdx.x >> 6);
     const int kvh = u / splits, sp = u % splits, begin = sp * span, end = min(len, begin + span);
-    float* lw = l.wave[wave];  // [0, HD): the new key, [HD, 2 HD): the new value
-    float* trig = lw + 2 * HD;
-    rope_trig(trig, a.rope_denom, pos);
+    const float* kn = &l.act[par][NH * HD + kvh * HD];
+    float* vn = l.wave[wave];  // the new value row
     const bool has_new = pos >= begin && pos < end;
     if (has_new) {
-        float kn[16];
-        const unsigned ko = SOFF(key) + (unsigned(kvh) * HD + sub * 16u) * 4u;
-#pragma unroll
-        for (int e = 0; e < 16; ++e) kn[e] = ldx(rs, ko + 4u * e);
-        norm_rope16(kn, w->qk_norm + HD, trig, a.eps);
         if (slot == 0) {
             const Rs rk = rsrc(w->keys), rv = rsrc(w->values);
             const unsigned co = ((unsigned(pos) * NKV + unsigned(kvh)) * HD + sub * 16u) * 4u;
-            const unsigned vo = SOFF(value) + (unsigned(kvh) * HD + sub * 16u) * 4u;
+            const unsigned vo = SOFF(value) + (unsigned(kvh) * HD + sub * 16u) * 8u;
+            const unsigned long long start = wall_clock64();
 #pragma unroll
-            for (int e = 0; e < 16; ++e) {
-                const float vv = ldx(rs, vo + 4u * e);
-                lw[sub * 16 + e] = kn[e];
-                lw[HD + sub * 16 + e] = vv;
-                stp(rk, co + 4u * e, kn[e]);
-                stp(rv, co + 4u * e, vv);
+            for (int e = 0; e < 4; ++e) {
+                const f2 v01 = wait2(a, rs, vo + 32u * e, want, l, start, p);
+                const f2 v23 = wait2(a, rs, vo + 32u * e + 16u, want, l, start, p);
+                const f4 vv = f4{v01.x, v01.y, v23.x, v23.y};
+                *reinterpret_cast<f4*>(vn + sub * 16 + 4 * e) = vv;
+                stp4(rk, co + 16u * e, lds4(kn + sub * 16 + 4 * e));
+                stp4(rv, co + 16u * e, vv);
             }
         }
         compiler_fence();
-        patch_new(wb, lw, begin, pos);
+        patch_new(wb, kn, vn, begin, pos);
     }
     const float scale = 1.f / 16.f;  // 1 / sqrt(256)
+    const unsigned t = tag(a, p);
     int held = begin;  // wb holds the K/V chunk starting here (prefetched: the first)
 #pragma unroll 1
     for (int g = 0; g < NH / NKV; ++g) {
         const int h = kvh * (NH / NKV) + g;
-        float q[16];
-        const unsigned qo = SOFF(mixed) + (unsigned(h) * 2u * HD + sub * 16u) * 4u;
+        f4 q[4];
 #pragma unroll
-        for (int e = 0; e < 16; ++e) q[e] = ldx(rs, qo + 4u * e);
-        norm_rope16(q, w->qk_norm, trig, a.eps);
-        float m = -INFINITY, lsum = 0.f, acc[16];
-#pragma unroll
-        for (int e = 0; e < 16; ++e) acc[e] = 0.f;
+        for (int e = 0; e < 4; ++e) q[e] = lds4(&l.act[par][h * HD + sub * 16 + 4 * e]);
+        float m = -INFINITY, lsum = 0.f;
+        f4 acc[4] = {f4(0.f), f4(0.f), f4(0.f), f4(0.f)};
 #pragma unroll 1
         for (int first = begin; first < end; first += SPAN) {
             if (first != held) {  // spans longer than one chunk (contexts over SPAN * SMAX)
                 load_kv_chunk(w, kvh, first, pos, wb);
-                if (has_new) patch_new(wb, lw, first, pos);
+                if (has_new) patch_new(wb, kn, vn, first, pos);
                 held = first;
             }
 #pragma unroll
@@ -672,13 +732,7 @@ __device__ void phase_attn(const Args& a, Rs rs, LayerP w, int u, f4* wb, Lds& l
                 const int pp = first + 4 * step + int(slot);
                 float sc = 0.f;
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const f4 kv4 = wb[step * 8 + e];
-                    sc = fmaf(q[4 * e], kv4.x, sc);
-                    sc = fmaf(q[4 * e + 1], kv4.y, sc);
-                    sc = fmaf(q[4 * e + 2], kv4.z, sc);
-                    sc = fmaf(q[4 * e + 3], kv4.w, sc);
-                }
+                for (int e = 0; e < 4; ++e) sc = fdot4(q[e], wb[step * 8 + e], sc);
                 sc = group_sum<16>(sc) * scale;
                 if (pp < end) {
                     const float mn = fmaxf(m, sc);
@@ -686,13 +740,7 @@ __device__ void phase_attn(const Args& a, Rs rs, LayerP w, int u, f4* wb, Lds& l
                     const float pw = expf(sc - mn);
                     lsum = lsum * corr + pw;
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        const f4 vv4 = wb[step * 8 + 4 + e];
-                        acc[4 * e] = acc[4 * e] * corr + pw * vv4.x;
-                        acc[4 * e + 1] = acc[4 * e + 1] * corr + pw * vv4.y;
-                        acc[4 * e + 2] = acc[4 * e + 2] * corr + pw * vv4.z;
-                        acc[4 * e + 3] = acc[4 * e + 3] * corr + pw * vv4.w;
-                    }
+                    for (int e = 0; e < 4; ++e) acc[e] = acc[e] * corr + wb[step * 8 + 4 + e] * pw;
                     m = mn;
                 }
             }
@@ -705,36 +753,56 @@ __device__ void phase_attn(const Args& a, Rs rs, LayerP w, int u, f4* wb, Lds& l
             const float c0 = m == -INFINITY ? 0.f : expf(m - mn), c1 = mo == -INFINITY ? 0.f : expf(mo - mn);
             lsum = lsum * c0 + lo * c1;
 #pragma unroll
-            for (int e = 0; e < 16; ++e) acc[e] = acc[e] * c0 + __shfl_xor(acc[e], o, 64) * c1;
+            for (int e = 0; e < 4; ++e) {
+                f4 other;
+                other.x = __shfl_xor(acc[e].x, o, 64);
+                other.y = __shfl_xor(acc[e].y, o, 64);
+                other.z = __shfl_xor(acc[e].z, o, 64);
+                other.w = __shfl_xor(acc[e].w, o, 64);
+                acc[e] = acc[e] * c0 + other * c1;
+            }
             m = mn;
         }
         const unsigned slotix = unsigned(h) * SMAX + unsigned(sp);
-        if (lane == 0) {
-            stx(rs, SOFF(pml) + slotix * 8u, m);
-            stx(rs, SOFF(pml) + slotix * 8u + 4u, lsum);
-        }
         if (slot == 0) {
             const unsigned ao = SOFF(pacc) + (slotix * HD + sub * 16u) * 4u;
 #pragma unroll
-            for (int e = 0; e < 16; ++e) stx(rs, ao + 4u * e, acc[e]);
+            for (int e = 0; e < 4; ++e) stx4(rs, ao + 16u * e, acc[e]);
+        }
+        // the sums are complete in memory before their (max, sum) pair is
+        __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
+        compiler_fence();
+        if (lane == 0) {
+            stt(rs, SOFF(pml) + slotix * 16u, m, t);
+            stt(rs, SOFF(pml) + slotix * 16u + 8u, lsum, t);
         }
     }
+    return true;
 }
 
 // ---- T_COMB: merge the splits (log-sum-exp) and apply the sigmoid gate
 // (reference.h:171-200); one wave per (head, 4 dims), lanes over splits.
 constexpr int COMB_PER_LANE = SMAX / 64;
-__device__ void phase_comb(const Args& a, Rs rs, int u) {
-    if (u >= COMB_WAVES) return;
+__device__ bool phase_comb(const Args& a, Rs rs, int p, int u, Lds& l) {
+    if (!bsync(l, p)) return false;
+    if (u >= COMB_WAVES) return true;
     const unsigned lane = lane_id();
     const int len = a.pos + 1, span = attn_span(len), splits = (len + span - 1) / span;
     const int h = u / (HD / 4), c4 = u % (HD / 4);
-    float mv[COMB_PER_LANE];
+    const unsigned want = tag(a, p - 1);
+    const unsigned long long start = wall_clock64();
+    float mv[COMB_PER_LANE], lv[COMB_PER_LANE];
     float mm = -INFINITY;
 #pragma unroll
     for (int k = 0; k < COMB_PER_LANE; ++k) {
         const int s = int(lane) + 64 * k;
-        mv[k] = s < splits ? ldx(rs, SOFF(pml) + (unsigned(h) * SMAX + unsigned(s)) * 8u) : -INFINITY;
+        mv[k] = -INFINITY;
+        lv[k] = 0.f;
+        if (s < splits) {
+            const f2 ml = wait2(a, rs, SOFF(pml) + (unsigned(h) * SMAX + unsigned(s)) * 16u, want, l, start, p);
+            mv[k] = ml.x;
+            lv[k] = ml.y;
+        }
         mm = fmaxf(mm, mv[k]);
     }
     mm = wave_max(mm);
@@ -746,7 +814,7 @@ __device__ void phase_comb(const Args& a, Rs rs, int u) {
         if (s < splits) {
             const unsigned ix = unsigned(h) * SMAX + unsigned(s);
             const float wgt = expf(mv[k] - mm);
-            den += ldx(rs, SOFF(pml) + ix * 8u + 4u) * wgt;
+            den += lv[k] * wgt;
             num += ldx4(rs, SOFF(pacc) + (ix * HD + unsigned(4 * c4)) * 4u) * wgt;
         }
     }
@@ -758,20 +826,22 @@ __device__ void phase_comb(const Args& a, Rs rs, int u) {
     if (lane < 4) {
         const float val = lane == 0 ? num.x : lane == 1 ? num.y : lane == 2 ? num.z : num.w;
         const int d = 4 * c4 + int(lane);
-        const float gate = ldx(rs, SOFF(mixed) + unsigned(h * 2 * HD + HD + d) * 4u);
-        stx(rs, SOFF(ctx) + unsigned(h * HD + d) * 4u, (val / den) * sigmoidf_(gate));
+        const float gate = wait1(a, rs, SOFF(mixed) + unsigned(h * 2 * HD + HD + d) * 8u, tag(a, p - 2), l, start, p);
+        stt(rs, SOFF(ctx) + unsigned(h * HD + d) * 8u, (val / den) * sigmoidf_(gate), tag(a, p));
     }
+    return true;
 }
 
 // ---- T_O: after = x + o . ctx
-__device__ void phase_o(const Args& a, Rs rs, int L, int u, const f4* wb) {
-    if (u >= H) return;
-    const unsigned lo = 16u * lane_id();
-    float acc = 0.f;
-#pragma unroll
-    for (int v = 0; v < NH * HD / 256; ++v) acc = fdot4(wb[v], ldx4(rs, SOFF(ctx) + lo + 1024u * v), acc);
-    acc = wave_sum(acc);
-    if (lane_id() == 0) stx(rs, SOFF(after) + 4u * unsigned(u), input_at(a, rs, L, u) + acc);
+__device__ bool phase_o(const Args& a, Rs rs, int L, int p, int u, const f4* wb, Lds& l) {
+    const int par = p & 1;
+    stage_tagged(a, rs, SOFF(ctx), NH * HD, tag(a, p - 1), l.act[par], l, p);
+    if (!bsync(l, p)) return false;
+    if (u >= H) return true;
+    const float acc = dot_row_lds<NH * HD / 256>(wb, l.act[par]);
+    const float res = input_at(a, rs, L, p - 4, u, l, p);
+    if (lane_id() == 0) stt(rs, SOFF(after) + 8u * unsigned(u), res + acc, tag(a, p));
+    return true;
 }
 
 // ---- T_LM: logits = lm_head . final RMSNorm(x); each wave streams its rows 4
@@ -812,12 +882,13 @@ __device__ __forceinline__ void prefetch_lm(const Args& a, int u, f4* wb) {
     const int rpw = lm_rows_per_wave(a.vocab), row0 = u * rpw, row_end = min(a.vocab, row0 + rpw);
     lm_load(rsrc(a.lm_head), row0, row_end, wb);
 }
-__device__ void phase_lm(const Args& a, Rs rs, int u, f4* wb) {
+__device__ bool phase_lm(const Args& a, Rs rs, int p, int u, f4* wb, Lds& l) {
+    const int par = p & 1;
+    stage_norm(a.final_norm, par, l);
+    stage_tagged(a, rs, SOFF(x), H, tag(a, p - 1), l.act[par], l, p);
+    if (!bsync(l, p)) return false;
     f4 xv[4];
-    const unsigned lo = 16u * lane_id();
-#pragma unroll
-    for (int v = 0; v < 4; ++v) xv[v] = ldx4(rs, SOFF(x) + lo + 1024u * v);
-    norm_chunks(xv, a.final_norm, a.eps);
+    normed_chunks(l, par, a.eps, xv);
     const int rpw = lm_rows_per_wave(a.vocab), row0 = u * rpw, row_end = min(a.vocab, row0 + rpw);
     const Rs lm = rsrc(a.lm_head), lg = rsrc(a.logits);
     float best = -INFINITY;
@@ -831,24 +902,28 @@ __device__ void phase_lm(const Args& a, Rs rs, int u, f4* wb) {
         lm_rows(lg, nb, xv, r + LM_G, row_end, best, at, bad);
     }
     if (lane_id() == 0) {
-        const unsigned o = SOFF(lmpart) + unsigned(u) * 12u;
-        stx(rs, o, best);
-        stx(rs, o + 4, __uint_as_float(at));
-        stx(rs, o + 8, __uint_as_float(bad));
+        const unsigned o = SOFF(lmpart) + unsigned(u) * 32u, t = tag(a, p);
+        stt(rs, o, best, t);
+        stt(rs, o + 8, __uint_as_float(at), t);
+        stt(rs, o + 16, __uint_as_float(bad), t);
     }
+    return true;
 }
 
-// ---- T_ARG: merge the per-wave maxima (first index of the maximum, non-finite
-// count; reference.h:222-230).
-__device__ void phase_arg(const Args& a, Rs rs) {
+// ---- T_ARG (block 0, wave 0): merge the per-wave maxima (first index of the
+// maximum, non-finite count; reference.h:222-230).
+__device__ void phase_arg(const Args& a, Rs rs, int p, Lds& l) {
     const unsigned lane = lane_id();
+    const unsigned want = tag(a, p - 1);
+    const unsigned long long start = wall_clock64();
     float best = -INFINITY;
     unsigned at = 0xffffffffu, bad = 0;
     for (int i = int(lane); i < NW; i += 64) {
-        const unsigned o = SOFF(lmpart) + unsigned(i) * 12u;
-        const float v = ldx(rs, o);
-        const unsigned idx = __float_as_uint(ldx(rs, o + 4));
-        bad += __float_as_uint(ldx(rs, o + 8));
+        const unsigned o = SOFF(lmpart) + unsigned(i) * 32u;
+        const f2 vi = wait2(a, rs, o, want, l, start, p);
+        const float v = vi.x;
+        const unsigned idx = __float_as_uint(vi.y);
+        bad += __float_as_uint(wait1(a, rs, o + 16, want, l, start, p));
         if (v > best || (v == best && idx < at)) {
             best = v;
             at = idx;
@@ -864,7 +939,7 @@ __device__ void phase_arg(const Args& a, Rs rs) {
             at = oi;
         }
     }
-    if (lane == 0) {
+    if (lane == 0 && !failed(l)) {
         const Rs pk = rsrc(a.picks);
         stp(pk, 0, float(at));
         stp(pk, 4, float(bad));
@@ -895,40 +970,35 @@ __global__ __launch_bounds__(THREADS, 1) void decode_kernel(Args a) {
     // descriptors derived from it in SGPRs)
     const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x >> 6));
     const int unit = wave * BLOCKS + int(blockIdx.x);  // rows spread wave-major over blocks
-    if (threadIdx.x == 0) {
-        for (int i = 0; i < 4; ++i) l.done[i] = 0;
-        l.seen = 0;
-        l.fail = 0;
-    }
+    if (threadIdx.x == 0) l.fail = kNoFail;
     __syncthreads();
-    const bool poller = wave == 0;
     const Rs rs = rsrc(a.s);
     f4 wb[WBUF];
     prefetch(a, 0, unit, wb);
     for (int p = 0; p < a.nphases; ++p) {
         const int t = ptype(a, p);
         if (t == T_ARG) {
-            if (blockIdx.x == 0 && wave == 0 && wait_phase(a, l, p - 1, true)) phase_arg(a, rs);
+            if (blockIdx.x == 0 && wave == 0) phase_arg(a, rs, p, l);
             return;
         }
-        if (p > 0 && !wait_phase(a, l, p - 1, poller)) return;
         const int L = player(a, p);
         const LayerP w = layer(a, L);
         const int u = opaque_uniform(unit);
+        bool ok = true;
         switch (t) {
-        case T_DIN: phase_din(a, rs, w, L, u, wb); break;
-        case T_MIX: phase_mix(a, rs, w, L, u, wb, l); break;
-        case T_DOUT: phase_dout(a, rs, w, L, u, wb); break;
-        case T_GLU: phase_glu(a, rs, w, u, wb); break;
-        case T_DOWN: phase_down(rs, u, wb); break;
-        case T_AQKV: phase_aqkv(a, rs, w, L, u, wb); break;
-        case T_ATTN: phase_attn(a, rs, w, u, wb, l); break;
-        case T_COMB: phase_comb(a, rs, u); break;
-        case T_O: phase_o(a, rs, L, u, wb); break;
-        case T_LM: phase_lm(a, rs, u, wb); break;
+        case T_DIN: ok = phase_din(a, rs, w, L, p, u, wb, l); break;
+        case T_MIX: ok = phase_mix(a, rs, w, L, p, u, wb, l); break;
+        case T_DOUT: ok = phase_dout(a, rs, w, L, p, u, wb, l); break;
+        case T_GLU: ok = phase_glu(a, rs, w, p, u, wb, l); break;
+        case T_DOWN: ok = phase_down(a, rs, p, u, wb, l); break;
+        case T_AQKV: ok = phase_aqkv(a, rs, w, L, p, u, wb, l); break;
+        case T_ATTN: ok = phase_attn(a, rs, w, p, u, wb, l); break;
+        case T_COMB: ok = phase_comb(a, rs, p, u, l); break;
+        case T_O: ok = phase_o(a, rs, L, p, u, wb, l); break;
+        case T_LM: ok = phase_lm(a, rs, p, u, wb, l); break;
         default: break;
         }
-        signal(a, l, p);
+        if (!ok) return;
         prefetch(a, p + 1, opaque_uniform(unit), wb);
     }
 }
@@ -941,8 +1011,7 @@ struct QrDecodePlan {
     qr::dec::Args args;
     QrDecodeLayer* layers = nullptr;
     qr::dec::Scratch* scratch = nullptr;
-    qr::dec::Sync* sync = nullptr;
-    float* denom = nullptr;
+    std::vector<float> host_denom;  // theta^(2i / rot) by the host libm
     int capacity = 0;
 };
 
@@ -985,17 +1054,13 @@ int decode_plan_create(const QrDecodeDesc& d, QrDecodePlan** out, hipStream_t s,
     p->capacity = d.capacity;
     hipError_t e = hipMalloc(reinterpret_cast<void**>(&p->layers), sizeof(QrDecodeLayer) * size_t(d.layers));
     if (e == hipSuccess) e = hipMalloc(reinterpret_cast<void**>(&p->scratch), sizeof(Scratch));
-    if (e == hipSuccess) e = hipMalloc(reinterpret_cast<void**>(&p->sync), sizeof(Sync));
-    if (e == hipSuccess) e = hipMalloc(reinterpret_cast<void**>(&p->denom), sizeof(float) * ROT / 2);
     // RoPE denominators theta^(2i / rot) by the host libm (the reference's
     // expression, src/attention.rs:49-50), as the op path's table
-    std::vector<float> denom(ROT / 2);
-    for (int i = 0; i < ROT / 2; ++i) denom[size_t(i)] = powf(d.theta, float(2 * i) / float(ROT));
+    p->host_denom.resize(ROT / 2);
+    for (int i = 0; i < ROT / 2; ++i) p->host_denom[size_t(i)] = powf(d.theta, float(2 * i) / float(ROT));
     if (e == hipSuccess)
         e = hipMemcpyAsync(p->layers, d.layer, sizeof(QrDecodeLayer) * size_t(d.layers), hipMemcpyHostToDevice, s);
-    if (e == hipSuccess) e = hipMemcpyAsync(p->denom, denom.data(), sizeof(float) * ROT / 2, hipMemcpyHostToDevice, s);
-    if (e == hipSuccess) e = hipMemsetAsync(p->sync, 0, sizeof(Sync), s);
-    if (e == hipSuccess) e = hipMemsetAsync(p->scratch, 0, sizeof(Scratch), s);
+    if (e == hipSuccess) e = hipMemsetAsync(p->scratch, 0, sizeof(Scratch), s);  // tag 0: never expected
     if (e == hipSuccess) e = hipStreamSynchronize(s);
     if (e != hipSuccess) {
         decode_plan_free(p);
@@ -1009,9 +1074,7 @@ int decode_plan_create(const QrDecodeDesc& d, QrDecodePlan** out, hipStream_t s,
     a.final_norm = d.final_norm;
     a.logits = d.logits;
     a.picks = d.picks;
-    a.rope_denom = p->denom;
     a.s = p->scratch;
-    a.sync = p->sync;
     a.vocab = d.vocab;
     a.eps = d.eps;
     a.epoch = 0;
@@ -1034,8 +1097,6 @@ void decode_plan_free(QrDecodePlan* p) {
     if (!p) return;
     if (p->layers) (void)hipFree(p->layers);
     if (p->scratch) (void)hipFree(p->scratch);
-    if (p->sync) (void)hipFree(p->sync);
-    if (p->denom) (void)hipFree(p->denom);
     delete p;
 }
 
@@ -1045,8 +1106,18 @@ int decode_step(QrDecodePlan* p, int token, int position, hipStream_t s) {
     if (token < 0 || token >= a.vocab || position < 0 || position >= p->capacity) return int(hipErrorInvalidValue);
     a.token = token;
     a.pos = position;
+    // RoPE angle pos / theta^(2i / rot) and its cos / sin on the host
+    // (reference: src/attention.rs:49-55, the same f32 expressions)
+    for (int i = 0; i < ROT / 2; ++i) {
+        const float angle = float(position) / p->host_denom[size_t(i)];
+        a.rope_cs[i] = cosf(angle);
+        a.rope_sn[i] = sinf(angle);
+    }
     a.epoch = (a.epoch + 1) & 0x3fffffu;
-    if (a.epoch == 0) a.epoch = 1;
+    if (a.epoch == 0) {  // tags repeat after 2^22 steps: clear every pair first
+        a.epoch = 1;
+        if (hipError_t e = hipMemsetAsync(p->scratch, 0, sizeof(Scratch), s)) return int(e);
+    }
     void* args[] = {&a};
     return int(hipLaunchCooperativeKernel(reinterpret_cast<const void*>(decode_kernel), dim3(BLOCKS), dim3(THREADS),
                                           args, 0, s));
