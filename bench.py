@@ -76,6 +76,9 @@ def main():
     ap.add_argument("--long", action="store_true", help="also time decode at ctx 8192 (config 4)")
     ap.add_argument("--cpu-steps", type=int, default=6, help="oracle steps of the CPU baseline sample (0: skip)")
     ap.add_argument("--profile-steps", type=int, default=16)
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="also run one device copy of MIB MiB (a plain copy kernel of known size, the scale "
+                         "for rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
@@ -204,6 +207,17 @@ def main():
         out["decode_8192_hbm_frac"] = round(long_bytes * 64 / dt / 1e9 / HBM_PEAK_GBS, 4)
         log(f"decode @8192: {dt / 64 * 1e3:.3f} ms/token, {long_bytes * 64 / dt / 1e9:.0f} GB/s algorithmic")
         del r3
+
+    if args.copy_calibration > 0:
+        from qwen_mi355x.bridge import Bridge
+        br = Bridge()
+        n = args.copy_calibration << 18  # floats
+        src, dst = br.alloc(n), br.alloc(n)
+        br.copy(dst, src, n)
+        br.sync()
+        out["copy_calibration_bytes"] = n * 4
+        del src, dst
+        br.close()
 
     if args.cpu_steps > 0:
         import oracle as O

@@ -127,6 +127,10 @@ class Bridge:
     def sync(self):
         self._check(self.L.qr_sync(self.ctx))
 
+    def copy(self, dst: Buffer, src: Buffer, n: int):
+        """qr_copy: n floats device to device, on the context stream."""
+        self._check(self.L.qr_copy(self.ctx, ctypes.c_void_p(dst.ptr), ctypes.c_void_p(src.ptr), ctypes.c_size_t(n)))
+
     def run(self, op, count: int, p=(), n=(), f=()):
         a = Params()
         for i, v in enumerate(p):
