@@ -1,14 +1,114 @@
 // Prefill projections Y[batch, rows] = X[batch, cols] . A^T (batch >= 5) on
 // gfx950, fp32 / BF16 / int8-per-row weights, fp32 accumulation.
 //
-// LDS-tiled kernel: a 64 (tokens) x 64 (rows) output tile per 256-thread
-// block, K in steps of 16 staged transposed in LDS, 4 x 4 outputs per thread.
-// int8 rows are scaled after the sum (scale * sum(q x), as the reference's
-// qr_gemm_i8, native/rocm/bridge.cpp:620-653).
+// fp32 weights (the prefill of every config): FP32 MFMA
+// (v_mfma_f32_32x32x2_f32). A 128 (tokens) x 128 (rows) output tile per
+// 256-thread block, 2 x 2 waves of 64 x 64 (2 x 2 MFMA tiles each); K in
+// steps of 16 through LDS, k-major ([k][m], [k][n]) so each MFMA operand is
+// one conflict-free ds_read_b32 per lane; the next K step's global loads are
+// in flight (registers) while the current one is multiplied.
+// BF16 / int8 weights: the LDS-tiled FMA kernel below (64 x 64 tile, 4 x 4
+// outputs per thread). int8 rows are scaled after the sum (scale * sum(q x),
+// as the reference's qr_gemm_i8, native/rocm/bridge.cpp:620-653).
 #include "common.h"
 
 namespace qr {
 namespace {
+
+typedef float f16v __attribute__((ext_vector_type(16)));
+typedef float f4v __attribute__((ext_vector_type(4)));
+
+constexpr int MM = 128, MN = 128, MK = 16, MPAD = 4;
+
+// One 16-deep K step of a [128, cols] row block of a row-major matrix into
+// registers: thread t loads rows t / 4 and 64 + t / 4, 4 consecutive k at
+// (t % 4) * 4 (zero outside the matrix).
+__device__ __forceinline__ void mfma_load(const float* m, int rows, int cols, int r0, int k0, f4v (&v)[2]) {
+    const int t = threadIdx.x, kq = (t & 3) * 4;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int r = r0 + (t >> 2) + 64 * i;
+        if (r < rows && k0 + kq + 3 < cols) {
+            v[i] = *reinterpret_cast<const f4v*>(m + size_t(r) * cols + k0 + kq);
+        } else {
+            f4v z = {0.f, 0.f, 0.f, 0.f};
+            for (int e = 0; e < 4; ++e)
+                if (r < rows && k0 + kq + e < cols) z[e] = m[size_t(r) * cols + k0 + kq + e];
+            v[i] = z;
+        }
+    }
+}
+__device__ __forceinline__ void mfma_store(float (*lds)[MM + MPAD], const f4v (&v)[2]) {
+    const int t = threadIdx.x, kq = (t & 3) * 4;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int r = (t >> 2) + 64 * i;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) lds[kq + e][r] = v[i][e];
+    }
+}
+
+__global__ __launch_bounds__(256) void gemm_mfma_kernel(float* y, const float* a, const float* x, int rows, int cols,
+                                                        int batch) {
+    __shared__ float xs[2][MK][MM + MPAD];
+    __shared__ float ws[2][MK][MN + MPAD];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;  // the wave's 64 x 64 sub-tile
+    const int m0 = blockIdx.y * MM, n0 = blockIdx.x * MN;
+    f16v acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+    f4v xv[2], wv[2];
+    mfma_load(x, batch, cols, m0, 0, xv);
+    mfma_load(a, rows, cols, n0, 0, wv);
+    mfma_store(xs[0], xv);
+    mfma_store(ws[0], wv);
+    __syncthreads();
+    int buf = 0;
+    for (int k0 = 0; k0 < cols; k0 += MK) {
+        const bool more = k0 + MK < cols;
+        if (more) {  // next K step in flight while this one is multiplied
+            mfma_load(x, batch, cols, m0, k0 + MK, xv);
+            mfma_load(a, rows, cols, n0, k0 + MK, wv);
+        }
+#pragma unroll
+        for (int kk = 0; kk < MK; kk += 2) {
+            const int k = kk + (lane >> 5);  // A[i = lane % 32][k], B[k][j = lane % 32]
+            float av[2], bv[2];
+#pragma unroll
+            for (int i = 0; i < 2; ++i) av[i] = xs[buf][k][wm + 32 * i + (lane & 31)];
+#pragma unroll
+            for (int j = 0; j < 2; ++j) bv[j] = ws[buf][k][wn + 32 * j + (lane & 31)];
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i], bv[j], acc[i][j], 0, 0, 0);
+        }
+        if (more) {
+            mfma_store(xs[buf ^ 1], xv);
+            mfma_store(ws[buf ^ 1], wv);
+        }
+        __syncthreads();
+        buf ^= 1;
+    }
+    // D[i][j]: lane l, register r holds row 8 (r / 4) + 4 (l / 32) + r % 4, column l % 32
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int n = n0 + wn + 32 * j + (lane & 31);
+            if (n >= rows) continue;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int m = m0 + wm + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                if (m < batch) y[size_t(m) * rows + n] = acc[i][j][r];
+            }
+        }
+}
 
 constexpr int BM = 64, BN = 64, BK = 16;
 
@@ -77,6 +177,12 @@ int gemm(hipStream_t s, WeightType t, float* y, const void* a, const float* x, i
     dim3 grid(ceil_div(rows, BN), ceil_div(batch, BM));
     switch (t) {
     case WeightType::F32:
+        // 16-byte aligned rows for the vector loads
+        if (cols % 4 == 0 && (reinterpret_cast<uintptr_t>(a) | reinterpret_cast<uintptr_t>(x)) % 16 == 0) {
+            hipLaunchKernelGGL(gemm_mfma_kernel, dim3(ceil_div(rows, MN), ceil_div(batch, MM)), dim3(256), 0, s, y,
+                               static_cast<const float*>(a), x, rows, cols, batch);
+            break;
+        }
         hipLaunchKernelGGL(gemm_tiled_kernel<WeightType::F32>, grid, dim3(256), 0, s, y, a, x, rows, cols, batch);
         break;
     case WeightType::BF16:

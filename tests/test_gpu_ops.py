@@ -72,6 +72,13 @@ def test_gemm_f32(gpu, rows, cols, batch):
     assert np.all(np.abs(got - want) <= bound)
 
 
+@pytest.mark.parametrize("rows,cols", SHAPES_08B + [(33, 20), (7, 12)])
+@pytest.mark.parametrize("batch", [127, 130, 257])
+def test_gemm_f32_prefill_tiles(gpu, rows, cols, batch):
+    """Prefill batches across the 128-token MFMA tile edge (and odd widths on the FMA kernel)."""
+    test_gemm_f32(gpu, rows, cols, batch)
+
+
 @pytest.mark.parametrize("kind", ["bf16", "i8"])
 @pytest.mark.parametrize("rows,cols", [(6144, 1024), (1024, 3584), (3584, 1024), (16, 1024), (24, 8), (64, 64),
                                        (256, 64), (8, 16)])
