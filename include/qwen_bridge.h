@@ -183,6 +183,15 @@ int qr_decode_plan(Context* c, const QrDecodeDesc* d, QrDecodePlan** out);
 int qr_decode_step(Context* c, QrDecodePlan* p, int token, int position);
 void qr_decode_plan_free(Context* c, QrDecodePlan* p);
 
+/* Embedding rows of a prefill chunk in one call: dst[r, 0..width) = row
+ * ids[r] of `table` for r < n (ids on the host, each checked against
+ * table_rows; bf16 != 0: `table` is packed BF16 and the rows are widened).
+ * Replaces the per-token qr_copy (fp32) or EmbedBf16 op (BF16) of the
+ * reference's DeviceRun::forward (src/device.rs:1716-1732) with the same
+ * result; no counterpart in the reference's ABI. */
+int qr_embed_rows(Context* c, float* dst, const float* table, int table_rows, int width, int bf16,
+                  const int32_t* ids, int n);
+
 /* In-bridge profiler: while on, every bridge call is bracketed by a hipEvent
  * pair on the context stream and the durations are summed per call label
  * (kernel family and shape). No counterpart in the reference's ABI: its

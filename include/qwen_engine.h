@@ -37,7 +37,8 @@ enum QeDisable {
     QE_NO_FUSED_OPS = 8,     /* qr_max_op (ops 12-15) */
     QE_NO_ARGMAX = 16,       /* qr_argmax (ops 16-17) */
     QE_NO_SNAPSHOTS = 32,    /* qr_snapshots */
-    QE_NO_DECODE_STEP = 64   /* qr_decode_plan / qr_decode_step */
+    QE_NO_DECODE_STEP = 64,  /* qr_decode_plan / qr_decode_step */
+    QE_NO_EMBED_ROWS = 128   /* qr_embed_rows */
 };
 
 /* Record callback of a captured step: (layer, name, values, n). Names follow

@@ -23,6 +23,8 @@ struct Context {
     size_t argmax_parts_len = 0;
     float* attn_parts = nullptr;  // split partials of decode attention
     size_t attn_parts_len = 0;
+    float* rule_chunks = nullptr;  // per-(chunk, head) records of the chunked DeltaRule
+    size_t rule_chunks_len = 0;
     // RoPE denominators theta^(2i / rot) per (theta bits, rot), device copies.
     std::map<std::pair<uint32_t, int>, float*> rope;
     // Profiler (qr_profile / QWEN_ROCM_PROFILE=1): a hipEvent pair on the
@@ -343,6 +345,7 @@ void qr_destroy(Context* c) {
     if (c->ticket) (void)hipFree(c->ticket);
     if (c->argmax_parts) (void)hipFree(c->argmax_parts);
     if (c->attn_parts) (void)hipFree(c->attn_parts);
+    if (c->rule_chunks) (void)hipFree(c->rule_chunks);
     (void)hipStreamDestroy(c->stream);
     delete c;
 }
@@ -407,6 +410,13 @@ int qr_run(Context* c, int op, int count, const Params* ap) {
     case QR_DELTA_RULE:
     case QR_DELTA_RULE_GATED:
         if (a.n[0] < 1 || a.n[1] < 1 || a.n[0] > 256) return fail(c, "DeltaRule key_dim must be 1..256", -1);
+        if (qr::delta_rule_chunked_ok(a, count)) {
+            if (int st = ensure(c, &c->rule_chunks, &c->rule_chunks_len, qr::delta_rule_chunked_scratch(a),
+                                "hipMalloc delta rule chunks"))
+                return st;
+            return launched(c, "delta_rule_chunked", qr::run_delta_rule_chunked(s, op == QR_DELTA_RULE_GATED, a,
+                                                                                  c->rule_chunks, c->rule_chunks_len));
+        }
         return launched(c, "delta_rule", qr::run_delta_rule(s, op == QR_DELTA_RULE_GATED, count, a));
     case QR_ATTENTION_QUERY:
     case QR_ATTENTION_KV:
@@ -550,6 +560,15 @@ int qr_decode_step(Context* c, QrDecodePlan* p, int token, int position) {
 void qr_decode_plan_free(Context* c, QrDecodePlan* p) {
     if (c) (void)hipStreamSynchronize(c->stream);
     qr::decode_plan_free(p);
+}
+
+int qr_embed_rows(Context* c, float* dst, const float* table, int table_rows, int width, int bf16,
+                  const int32_t* ids, int n) {
+    if (!dst || !table || !ids || width < 1 || n < 1) return fail(c, "embed_rows shape", -1);
+    for (int r = 0; r < n; ++r)
+        if (ids[r] < 0 || ids[r] >= table_rows) return fail(c, "embed_rows id out of range", -1);
+    auto sc = scope(c, [&] { return std::string(bf16 ? "embed_rows bf16" : "embed_rows f32"); });
+    return launched(c, "embed rows", qr::run_embed_rows(c->stream, dst, table, width, bf16 != 0, ids, n));
 }
 
 }  // extern "C"

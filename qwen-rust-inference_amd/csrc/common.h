@@ -91,6 +91,8 @@ int run_delta_rule(hipStream_t s, bool gated, int count, const Params& a);
 // `denom`: device table of theta^(2i / rot), i < rot / 2 (see rope_lds).
 int run_attention_qkv(hipStream_t s, int op, int count, const Params& a, const float* denom);
 int run_embed(hipStream_t s, int op, int count, const Params& a);
+// dst[r] = table row ids[r] (fp32, or packed BF16 widened), r < n; ids on the host.
+int run_embed_rows(hipStream_t s, float* dst, const void* table, int width, bool bf16, const int32_t* ids, int n);
 int run_argmax(hipStream_t s, int rows, const Params& a, float* parts, size_t parts_len);
 size_t argmax_parts_needed(int rows, int n);
 
@@ -105,6 +107,14 @@ const char* decode_unsupported(const QrDecodeDesc& d);
 int decode_plan_create(const QrDecodeDesc& d, QrDecodePlan** out, hipStream_t s, const char** why);
 void decode_plan_free(QrDecodePlan* p);
 int decode_step(QrDecodePlan* p, int token, int position, hipStream_t s);
+
+// delta_chunk.hip ------------------------------------------------------------
+// DeltaRule / DeltaRuleGated over a prefill chunk in the WY form (key_dim ==
+// value_dim == 128, no snapshots, at least kChunkMinTokens tokens).
+constexpr int kChunkMinTokens = 16;
+bool delta_rule_chunked_ok(const Params& a, int count);
+size_t delta_rule_chunked_scratch(const Params& a);  // floats
+int run_delta_rule_chunked(hipStream_t s, bool gated, const Params& a, float* scratch, size_t len);
 
 // deltanet.hip ---------------------------------------------------------------
 // qr_delta_mixer for one token (decode) when the shape allows; returns -1 if not handled.

@@ -7,6 +7,7 @@
 // steps of 16 through LDS, k-major ([k][m], [k][n]) so each MFMA operand is
 // one conflict-free ds_read_b32 per lane; the next K step's global loads are
 // in flight (registers) while the current one is multiplied.
+// fp32 weights with at most 16 rows: gemm_skinny_kernel (lanes over columns).
 // BF16 / int8 weights: the LDS-tiled FMA kernel below (64 x 64 tile, 4 x 4
 // outputs per thread). int8 rows are scaled after the sum (scale * sum(q x),
 // as the reference's qr_gemm_i8, native/rocm/bridge.cpp:620-653).
@@ -169,6 +170,44 @@ __global__ __launch_bounds__(256) void gemm_tiled_kernel(float* y, const void* a
     }
 }
 
+// fp32 weights with few rows (<= 16: the DeltaNet a / b projections) over many
+// tokens: a 128-row MFMA tile would be mostly empty, so each wave takes 4
+// tokens, its lanes stride the columns with coalesced float4 loads of x and
+// of every weight row, and the 4 x 16 per-lane partial dots are summed over
+// the 64 lanes through LDS (one (token, row) output per lane).
+constexpr int SK_ROWS = 16, SK_TOK = 4;
+__global__ __launch_bounds__(256) void gemm_skinny_kernel(float* y, const float* a, const float* x, int rows, int cols,
+                                                          int batch) {
+    __shared__ float part[4][64][SK_ROWS * SK_TOK + 1];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int m0 = (int(blockIdx.x) * 4 + wave) * SK_TOK;
+    float acc[SK_TOK][SK_ROWS] = {};
+    for (int c = lane * 4; c < cols; c += 256) {
+        f4v xv[SK_TOK];
+#pragma unroll
+        for (int t = 0; t < SK_TOK; ++t)
+            xv[t] = m0 + t < batch ? *reinterpret_cast<const f4v*>(x + size_t(m0 + t) * cols + c) : f4v{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int r = 0; r < SK_ROWS; ++r) {
+            if (r >= rows) break;
+            const f4v av = *reinterpret_cast<const f4v*>(a + size_t(r) * cols + c);
+#pragma unroll
+            for (int t = 0; t < SK_TOK; ++t)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) acc[t][r] = fmaf(xv[t][e], av[e], acc[t][r]);
+        }
+    }
+#pragma unroll
+    for (int t = 0; t < SK_TOK; ++t)
+#pragma unroll
+        for (int r = 0; r < SK_ROWS; ++r) part[wave][lane][t * SK_ROWS + r] = acc[t][r];
+    __syncthreads();
+    const int t = lane / SK_ROWS, r = lane % SK_ROWS;
+    float sum = 0.f;
+    for (int j = 0; j < 64; ++j) sum += part[wave][j][lane];
+    if (m0 + t < batch && r < rows) y[size_t(m0 + t) * rows + r] = sum;
+}
+
 }  // namespace
 
 bool gemm_preferred(WeightType, int, int, int batch) { return batch > 4; }
@@ -179,6 +218,11 @@ int gemm(hipStream_t s, WeightType t, float* y, const void* a, const float* x, i
     case WeightType::F32:
         // 16-byte aligned rows for the vector loads
         if (cols % 4 == 0 && (reinterpret_cast<uintptr_t>(a) | reinterpret_cast<uintptr_t>(x)) % 16 == 0) {
+            if (rows <= SK_ROWS) {
+                hipLaunchKernelGGL(gemm_skinny_kernel, dim3(ceil_div(batch, 4 * SK_TOK)), dim3(256), 0, s, y,
+                                   static_cast<const float*>(a), x, rows, cols, batch);
+                break;
+            }
             hipLaunchKernelGGL(gemm_mfma_kernel, dim3(ceil_div(rows, MN), ceil_div(batch, MM)), dim3(256), 0, s, y,
                                static_cast<const float*>(a), x, rows, cols, batch);
             break;

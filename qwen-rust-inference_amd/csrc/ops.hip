@@ -107,6 +107,39 @@ __global__ __launch_bounds__(256) void conv_silu_kernel(int count, Params a) {
     for (int i = 0; i < k - 1; ++i) hist[i] = h[i];
 }
 
+// Prefill form of ConvSilu: one thread per (token, channel); the input at
+// relative position j < 0 is history[k - 1 + j]. Same sums as above
+// (history terms oldest first, then the new input). Snapshot slot r + 1 gets
+// the history after token r (r < snaps). The live history is rewritten by
+// conv_history_kernel afterwards, once every token has read it.
+__global__ __launch_bounds__(256) void conv_silu_tokens_kernel(int count, Params a) {
+    const int ch = blockIdx.x * blockDim.x + threadIdx.x, r = blockIdx.y;
+    if (ch >= count) return;
+    const int k = a.n[0], stride = a.n[2], snaps = a.n[3];
+    const float* w = a.p[2] + size_t(ch) * k;
+    const float* hist = a.p[3] + size_t(ch) * (k - 1);
+    auto input = [&](int j) { return j >= 0 ? a.p[1][size_t(j) * stride + ch] : hist[k - 1 + j]; };
+    float sum = 0.f;
+    for (int i = 0; i < k - 1; ++i) sum += input(r - (k - 1) + i) * w[i];
+    sum += input(r) * w[k - 1];
+    a.p[0][size_t(r) * stride + ch] = siluf_(sum);
+    if (r < snaps)
+        for (int i = 0; i < k - 1; ++i)
+            a.p[3][size_t(r + 1) * size_t(stride) * size_t(k - 1) + size_t(ch) * (k - 1) + i] = input(r - (k - 2) + i);
+}
+__global__ __launch_bounds__(256) void conv_history_kernel(int count, Params a) {
+    const int ch = blockIdx.x * blockDim.x + threadIdx.x;
+    if (ch >= count) return;
+    const int k = a.n[0], tokens = a.n[1], stride = a.n[2];
+    float* hist = a.p[3] + size_t(ch) * (k - 1);
+    float h[16];
+    for (int i = 0; i < k - 1; ++i) {
+        const int j = tokens - (k - 1) + i;
+        h[i] = j >= 0 ? a.p[1][size_t(j) * stride + ch] : hist[k - 1 + j];
+    }
+    for (int i = 0; i < k - 1; ++i) hist[i] = h[i];
+}
+
 // ---------------------------------------------------------------- DeltaQk (5)
 // reference.h:134-143: per (token, value head) the L2-normalised query (then
 // / sqrt(d)) and key of its key head. One wave per item.
@@ -405,7 +438,14 @@ int run_rms_family(hipStream_t s, int op, int groups, const Params& a) {
 
 int run_conv_silu(hipStream_t s, int count, const Params& a) {
     if (a.n[0] < 1 || a.n[0] > 17) return int(hipErrorInvalidValue);
-    hipLaunchKernelGGL(conv_silu_kernel, dim3(ceil_div(count, 256)), dim3(256), 0, s, count, a);
+    const int tokens = a.n[1] > 0 ? a.n[1] : 1;
+    if (tokens <= 4) {  // decode and short verify chunks: one thread walks the tokens of its channel
+        hipLaunchKernelGGL(conv_silu_kernel, dim3(ceil_div(count, 256)), dim3(256), 0, s, count, a);
+        return int(hipGetLastError());
+    }
+    hipLaunchKernelGGL(conv_silu_tokens_kernel, dim3(ceil_div(count, 256), unsigned(tokens)), dim3(256), 0, s, count, a);
+    if (hipError_t e = hipGetLastError()) return int(e);
+    hipLaunchKernelGGL(conv_history_kernel, dim3(ceil_div(count, 256)), dim3(256), 0, s, count, a);
     return int(hipGetLastError());
 }
 
@@ -441,6 +481,38 @@ int run_attention_qkv(hipStream_t s, int op, int count, const Params& a, const f
 }
 
 int run_embed(hipStream_t s, int op, int count, const Params& a) { return run_elementwise(s, op, count, a); }
+
+// Embedding rows of a prefill chunk: the ids ride in the kernel arguments,
+// kEmbedIds per launch (one block per row), so no host-to-device copy is
+// queued. BF16 rows widen as EmbedBf16 does (reference.h:213-216).
+constexpr int kEmbedIds = 480;
+struct EmbedIds {
+    int ids[kEmbedIds];
+};
+__global__ __launch_bounds__(256) void embed_rows_kernel(float* dst, const void* table, int width, int bf16,
+                                                         EmbedIds b) {
+    const size_t id = size_t(b.ids[blockIdx.x]);
+    float* out = dst + size_t(blockIdx.x) * width;
+    if (bf16) {
+        const uint16_t* row = static_cast<const uint16_t*>(table) + id * width;
+        for (int i = threadIdx.x; i < width; i += 256) out[i] = __uint_as_float(uint32_t(row[i]) << 16);
+    } else {
+        const float* row = static_cast<const float*>(table) + id * width;
+        for (int i = threadIdx.x; i < width; i += 256) out[i] = row[i];
+    }
+}
+
+int run_embed_rows(hipStream_t s, float* dst, const void* table, int width, bool bf16, const int32_t* ids, int n) {
+    for (int r0 = 0; r0 < n; r0 += kEmbedIds) {
+        const int m = n - r0 < kEmbedIds ? n - r0 : kEmbedIds;
+        EmbedIds b{};
+        for (int r = 0; r < m; ++r) b.ids[r] = ids[r0 + r];
+        hipLaunchKernelGGL(embed_rows_kernel, dim3(unsigned(m)), dim3(256), 0, s, dst + size_t(r0) * width, table,
+                           width, bf16 ? 1 : 0, b);
+        if (hipError_t e = hipGetLastError()) return int(e);
+    }
+    return 0;
+}
 
 size_t argmax_parts_needed(int rows, int n) { return size_t(rows) * ceil_div(n, kArgmaxSlice) * 3; }
 

@@ -89,6 +89,7 @@ struct Api {
     int (*decode_plan)(Context*, const QrDecodeDesc*, QrDecodePlan**) = nullptr;
     int (*decode_step)(Context*, QrDecodePlan*, int, int) = nullptr;
     void (*decode_free)(Context*, QrDecodePlan*) = nullptr;
+    int (*embed_rows)(Context*, float*, const float*, int, int, int, const int32_t*, int) = nullptr;
     int (*profile)(Context*, int) = nullptr;
     long (*profile_read)(Context*, char*, size_t) = nullptr;
     int (*sync_)(Context*) = nullptr;
@@ -159,6 +160,7 @@ struct Api {
             decode_free = symbol<decltype(decode_free)>("qr_decode_plan_free", false);
             if (!decode_plan || !decode_step || !decode_free) decode_plan = nullptr;
         }
+        if (!(disable & QE_NO_EMBED_ROWS)) embed_rows = symbol<decltype(embed_rows)>("qr_embed_rows", false);
         profile = symbol<decltype(profile)>("qr_profile", false);
         profile_read = symbol<decltype(profile_read)>("qr_profile_read", false);
         if (!(disable & QE_NO_SNAPSHOTS)) {
@@ -807,7 +809,12 @@ struct QeRun {
             return out;
         }
         size_t h = size_t(model->config.hidden_size);
-        for (size_t r = 0; r < t; ++r) {
+        if (a->embed_rows && t > 1) {  // the whole chunk in one call
+            std::vector<int32_t> rows(ids, ids + t);
+            a->check(a->embed_rows(a->ctx, x.at(0), model->embedding.buffer.p, int(model->config.vocab_size), int(h),
+                                   model->embedding.bf16 ? 1 : 0, rows.data(), int(t)));
+        }
+        for (size_t r = 0; r < t && !(a->embed_rows && t > 1); ++r) {
             float* xr = x.at(r * h);
             if (model->embedding.bf16) {
                 a->op(EmbedBf16, h, {xr, model->embedding.buffer.p}, {size_t(ids[r]), h}, {});

@@ -131,6 +131,13 @@ class Bridge:
         """qr_copy: n floats device to device, on the context stream."""
         self._check(self.L.qr_copy(self.ctx, ctypes.c_void_p(dst.ptr), ctypes.c_void_p(src.ptr), ctypes.c_size_t(n)))
 
+    def embed_rows(self, dst: Buffer, table: Buffer, table_rows: int, width: int, ids, bf16: bool = False):
+        """qr_embed_rows: dst[r] = row ids[r] of the (fp32 or packed BF16) table."""
+        v = np.ascontiguousarray(ids, dtype=np.int32)
+        self._check(self.L.qr_embed_rows(self.ctx, ctypes.c_void_p(dst.ptr), ctypes.c_void_p(table.ptr), table_rows,
+                                         width, int(bf16), v.ctypes.data_as(ctypes.POINTER(ctypes.c_int32)),
+                                         int(v.size)))
+
     def run(self, op, count: int, p=(), n=(), f=()):
         a = Params()
         for i, v in enumerate(p):

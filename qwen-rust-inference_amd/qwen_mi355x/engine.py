@@ -27,6 +27,7 @@ KIND_CPU_TEST, KIND_ROCM = 0, 1
 F32, BF16_EXACT, INT8 = 0, 1, 2
 NO_F32_FUSIONS, NO_FUSIONS, NO_DELTA_MIXER, NO_FUSED_OPS, NO_ARGMAX, NO_SNAPSHOTS = 1, 2, 4, 8, 16, 32
 NO_DECODE_STEP = 64
+NO_EMBED_ROWS = 128
 
 # Every entry point of include/qwen_bridge.h.
 BRIDGE_SYMBOLS = [
@@ -35,7 +36,7 @@ BRIDGE_SYMBOLS = [
     "qr_snapshots", "qr_argmax", "qr_set_option", "qr_gemm_i8", "qr_gemm_bf16_group", "qr_gemm_i8_group",
     "qr_gemm_bf16_glu", "qr_gemm_i8_glu", "qr_gemm_bf16_add_norm", "qr_gemm_i8_add_norm", "qr_delta_mixer",
     "qr_gemm_f32_group", "qr_gemm_f32_glu", "qr_gemm_f32_add_norm", "qr_profile", "qr_profile_read",
-    "qr_decode_plan", "qr_decode_step", "qr_decode_plan_free",
+    "qr_decode_plan", "qr_decode_step", "qr_decode_plan_free", "qr_embed_rows",
 ]
 
 _F = ctypes.POINTER(ctypes.c_float)

@@ -96,7 +96,7 @@ def test_tiny_fused_and_unfused_paths_agree(tiny):
     ids = tiny_prompt()
     base = E.Model(w).new_run(32)
     want = base.prefill(ids)
-    for disable in (E.NO_F32_FUSIONS, E.NO_DELTA_MIXER, E.NO_FUSED_OPS, E.NO_ARGMAX, 63):
+    for disable in (E.NO_F32_FUSIONS, E.NO_DELTA_MIXER, E.NO_FUSED_OPS, E.NO_ARGMAX, E.NO_EMBED_ROWS, 255):
         run = E.Model(w, disable=disable).new_run(32)
         parity(run.prefill(ids), want, where=f"disable {disable}")
         a, b = run.step_greedy(7), base.step_greedy(7) if disable == E.NO_F32_FUSIONS else None
@@ -140,6 +140,32 @@ def test_tiny_int8_against_dequantised_oracle(tiny):
     rows = run.verify_rollback(draft)
     for r, t in enumerate(draft):
         parity(rows[r], st.step(t, O.VECTOR), rtol=INT8_RTOL, where=f"int8 verify row {r}")
+
+
+@pytest.mark.parametrize("chunk", [300, 130])
+def test_mid_prefill_against_oracle(chunk):
+    """Prefill chunks long enough for every prefill kernel: the chunked
+    DeltaRule (dk = dv = 128, one key head feeding two value heads, ragged
+    last chunk), the token-parallel conv, the MFMA and few-row GEMMs, prefill
+    attention and the one-call embedding. 300 prompt tokens in one chunk, or
+    as 130 + 130 + 40; logits of the last row, every state, then greedy
+    decode, against the token-by-token oracle."""
+    c = M.make_config(hidden=256, intermediate=512, vocab=1024,
+                      layer_types=["linear_attention"] * 3 + ["full_attention"], heads=2, kv_heads=1, head_dim=64,
+                      rotary_dim=16, key_heads=1, value_heads=2, key_dim=128, value_dim=128, conv_kernel=4,
+                      max_positions=1024, eps=1e-6, theta=1e6)
+    w = M.synthetic_weights(c, seed=5)
+    prompt = [int(v) for v in np.random.default_rng(11).integers(0, c.vocab_size, 300)]
+    print(f"oracle on the mid config, chunk {chunk}", flush=True)
+    want, want_logits, s = oracle_greedy(O.Oracle(w), prompt, 8)
+    run = E.Model(w).new_run(320, chunk=chunk)
+    logits = run.prefill(prompt)
+    parity(logits, want_logits[0], where="prefill logits")
+    got, _ = run.decode_greedy(O.select_greedy(logits), 8)
+    assert got == want
+    for layer in range(c.num_layers):
+        for which in range(4):
+            parity(run.state(layer, which), s.part(layer, which), where=f"state {layer}/{which}")
 
 
 @pytest.fixture(scope="module")

@@ -72,7 +72,7 @@ def test_gemm_f32(gpu, rows, cols, batch):
     assert np.all(np.abs(got - want) <= bound)
 
 
-@pytest.mark.parametrize("rows,cols", SHAPES_08B + [(33, 20), (7, 12)])
+@pytest.mark.parametrize("rows,cols", SHAPES_08B + [(33, 20), (7, 12), (3, 260)])
 @pytest.mark.parametrize("batch", [127, 130, 257])
 def test_gemm_f32_prefill_tiles(gpu, rows, cols, batch):
     """Prefill batches across the 128-token MFMA tile edge (and odd widths on the FMA kernel)."""
@@ -274,7 +274,29 @@ def test_elementwise_and_embed(gpu, cpu):
     assert np.array_equal(g[0], c[0])
 
 
-@pytest.mark.parametrize("k,tokens,snaps", [(4, 1, 0), (4, 5, 0), (4, 4, 3), (3, 2, 1), (1, 1, 0)])
+@pytest.mark.parametrize("width,n", [(1024, 1000), (1000, 3), (8, 481)])
+def test_embed_rows(gpu, width, n):
+    """qr_embed_rows (several launches past 480 ids) equals the per-row gather,
+    bit for bit, for fp32 and packed BF16 tables; a bad id is refused before
+    anything is queued."""
+    rng = np.random.default_rng(width + n)
+    rows = 300
+    table = rnd(rng, rows * width)
+    ids = rng.integers(0, rows, n).astype(np.int32)
+    ids[0], ids[-1] = 0, rows - 1
+    dst = gpu.alloc(n * width)
+    gpu.embed_rows(dst, gpu.upload(table), rows, width, ids)
+    assert np.array_equal(dst.read().reshape(n, width), table.reshape(rows, width)[ids])
+    packed = gpu.upload(pack_bf16(table).view(np.float32))
+    gpu.embed_rows(dst, packed, rows, width, ids, bf16=True)
+    widened = ((table.view(np.uint32) >> 16) << 16).view(np.float32).reshape(rows, width)
+    assert np.array_equal(dst.read().reshape(n, width), widened[ids])
+    with pytest.raises(Exception, match="out of range"):
+        gpu.embed_rows(dst, packed, rows, width, np.array([0, rows], np.int32), bf16=True)
+
+
+@pytest.mark.parametrize("k,tokens,snaps", [(4, 1, 0), (4, 5, 0), (4, 4, 3), (3, 2, 1), (1, 1, 0),
+                                             (4, 37, 5), (4, 130, 0), (3, 9, 8), (1, 7, 2), (17, 6, 2)])
 def test_conv_silu(gpu, cpu, k, tokens, snaps):
     rng = np.random.default_rng(k * 10 + tokens)
     ch = 6144 if k == 4 else 24
@@ -323,6 +345,45 @@ def test_delta_rule(gpu, cpu, kd, vd, heads, tokens, snaps, gated):
                 [kd, vd, heads, heads, tokens, stride, snaps])
     parity(g[0], c[0], where="core")
     parity(g[4], c[4], where="state+snapshots")
+
+
+def _unit_rows(rng, rows, d, scale=1.0):
+    x = rng.standard_normal((rows, d))
+    return (x / np.linalg.norm(x, axis=1, keepdims=True) * scale).astype(np.float32).ravel()
+
+
+@pytest.mark.parametrize("tokens,gated,a_log", [(16, True, 0.0), (63, True, 0.0), (64, True, 0.0), (65, False, 0.0),
+                                                (130, True, 0.0), (300, False, 0.0), (200, True, 3.0),
+                                                (64 * 64 + 37, True, 0.0)])
+def test_delta_rule_chunked(gpu, cpu, tokens, gated, a_log):
+    """Prefill lengths take the chunked (WY form, MFMA) path: 64-token chunks,
+    ragged last chunks, one more chunk than a prep/scan group holds, and
+    heavy decay (A_log 3: g ~ -14 per token). q and k are unit rows (q also
+    / sqrt(dk)) as DeltaQk hands them to the rule; the CPU side is the
+    token-by-token recurrence."""
+    kd = vd = 128
+    heads = 16
+    print(f"delta_rule_chunked tokens={tokens} gated={gated} a_log={a_log}", flush=True)
+    rng = np.random.default_rng(tokens + 7 * gated)
+    stride = 2 * heads * kd + heads * vd
+    q = _unit_rows(rng, tokens * heads, kd, 1 / np.sqrt(kd))
+    k = _unit_rows(rng, tokens * heads, kd)
+    v = rnd(rng, tokens * stride, 1.0)
+    state = rnd(rng, heads * kd * vd, 0.5)
+    if gated:
+        a, b = rnd(rng, tokens * heads), rnd(rng, tokens * heads)
+        gates = np.concatenate([rnd(rng, heads, 0.5), np.full(heads, a_log, np.float32) + rnd(rng, heads, 0.5)])
+        ins = {1: q, 2: k, 3: v, 4: state, 5: a, 6: b, 7: gates}
+        op = "DELTA_RULE_GATED"
+    else:
+        decay = (-0.05 - np.abs(rnd(rng, tokens * heads, 0.1))).astype(np.float32)
+        beta = (0.5 + rnd(rng, tokens * heads, 0.2)).clip(0, 1).astype(np.float32)
+        ins = {1: q, 2: k, 3: v, 4: state, 5: decay, 6: beta}
+        op = "DELTA_RULE"
+    g, c = both(gpu, cpu, op, heads * vd, ins, {0: tokens * heads * vd, 4: state.size},
+                [kd, vd, heads, heads, tokens, stride, 0])
+    parity(g[0], c[0], where="core")
+    parity(g[4], c[4], where="state")
 
 
 @pytest.mark.parametrize("d,rot,heads,kv,tokens,pos", [(256, 64, 8, 2, 1, 453), (256, 64, 8, 2, 3, 8190),
