@@ -9,8 +9,9 @@ argmax readback, as the reference times `step_greedy` (src/device/cli.rs:797-812
 stream synchronisation on both sides. value = decode tokens/s at ctx 454.
 
 Also reported: weight-read HBM GB/s of the decode step; the prefill rate of
-the prompt; with --prefill, the 2644-token prefill (config 3); with --long,
-decode at ctx 8192 (config 4). roofline: the one-launch decode kernel
+the prompt; the 2644- and 10,240-token prefills (config 3: median of timed
+runs, tok/s and FLOP rate against the fp32 MFMA peak; --no-prefill skips);
+decode at ctx 8192 (config 4; --no-long skips). roofline: the one-launch decode kernel
 (decode_kernel: every layer, lm_head and argmax of a step), timed with a
 hipEvent pair around each launch on the bridge's stream in a profiled pass of
 the same decode; achieved = the step's algorithmic HBM bytes (every matrix
@@ -32,6 +33,7 @@ for p in (str(ROOT / "qwen-rust-inference_amd"), str(ROOT / "oracle")):
         sys.path.insert(0, p)
 
 HBM_PEAK_GBS = 8000.0
+MFMA_F32_PEAK_TFLOPS = 157.3
 METRIC = "decode tok/s @ctx 454 & 8192 + HBM GB/s; prefill tok/s @2644"
 
 
@@ -66,14 +68,31 @@ def step_bytes(c, weight_bytes: int, length: int) -> int:
     return (weight_bytes + delta * 2 * (recurrent + conv) + attn * length * kv_row + c.vocab_size * 4)
 
 
+def prefill_flops(c, n: int, weight_params: int) -> float:
+    """Algorithmic FLOPs of an n-token prefill: every projection but lm_head
+    on n rows, lm_head on the last row, causal attention (QK^T and PV,
+    n(n+1)/2 pairs per head), and the chunked DeltaRule (per chunk and head:
+    the Gram products, the triangular solve, U / W, and the three scan
+    products)."""
+    vocab_params = c.vocab_size * c.hidden_size
+    proj = 2.0 * (weight_params - vocab_params) * n + 2.0 * vocab_params
+    attn_layers = sum(1 for t in c.layer_types if t == "full_attention")
+    attn = attn_layers * c.num_heads * 4.0 * c.head_dim * n * (n + 1) / 2
+    dk, dv, ch = c.key_dim, c.value_dim, 64
+    per_chunk = 2.0 * (2 * ch * ch * dk + ch * ch * (dk + dv) / 2 + 2 * ch * dk * dv + ch * ch * dv + dk * ch * dv)
+    rule = (len(c.layer_types) - attn_layers) * c.value_heads * -(-n // ch) * per_chunk
+    return proj + attn + rule
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=128)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--prompt", type=int, default=454)
-    ap.add_argument("--prefill", action="store_true", help="also time the 2644-token prefill (config 3)")
-    ap.add_argument("--long", action="store_true", help="also time decode at ctx 8192 (config 4)")
+    ap.add_argument("--no-prefill", dest="prefill", action="store_false",
+                    help="skip the 2644- and 10,240-token prefills (config 3)")
+    ap.add_argument("--no-long", dest="long", action="store_false", help="skip decode at ctx 8192 (config 4)")
     ap.add_argument("--cpu-steps", type=int, default=6, help="oracle steps of the CPU baseline sample (0: skip)")
     ap.add_argument("--profile-steps", type=int, default=16)
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
@@ -171,16 +190,30 @@ def main():
            "roofline": roofline}
 
     if args.prefill:
-        for n in (2644,):
+        # Config 3: one chunk of n uniform random IDs (seed 2) into a fresh run,
+        # timed from the call to the last-row logits on the host (as the
+        # reference times prefill, src/device/cli.rs:775-791); one untimed run,
+        # then the median of `reps`.
+        for n, reps in ((2644, 5), (10240, 3)):
             ids2 = [int(v) for v in np.random.default_rng(2).integers(0, c.vocab_size, n)]
-            r2 = model.new_run(n + 1, chunk=n)
-            model.sync()
-            t = time.perf_counter()
-            r2.prefill(ids2)
-            dt = time.perf_counter() - t
+            times = []
+            for rep in range(reps + 1):
+                r2 = model.new_run(n + 1, chunk=n)
+                model.sync()
+                t = time.perf_counter()
+                r2.prefill(ids2)
+                dt = time.perf_counter() - t
+                if rep:
+                    times.append(dt)
+                del r2
+            dt = float(np.median(times))
+            tflops = prefill_flops(c, n, weight_bytes // 4) / dt / 1e12
             out[f"prefill_{n}_tok_s"] = round(n / dt, 1)
-            log(f"prefill {n}: {dt * 1e3:.1f} ms, {n / dt:.0f} tok/s")
-            del r2
+            out[f"prefill_{n}_ms"] = round(dt * 1e3, 2)
+            out[f"prefill_{n}_tflops"] = round(tflops, 2)
+            out[f"prefill_{n}_mfma_frac"] = round(tflops / MFMA_F32_PEAK_TFLOPS, 4)
+            log(f"prefill {n}: {dt * 1e3:.1f} ms (median of {reps}), {n / dt:.0f} tok/s, "
+                f"{tflops:.1f} TFLOP/s algorithmic ({tflops / MFMA_F32_PEAK_TFLOPS:.1%} of fp32 MFMA peak)")
     if args.long:
         # Decode at ctx 8192 (config 4): the context's DeltaNet states and
         # K/V rows are seeded synthetic state written into the run (a decode

@@ -174,6 +174,188 @@ __global__ __launch_bounds__(256) void attention_combine_kernel(ReadArgs a) {
     a.out[o] = (num / den) * sigmoidf_(a.gate[o]);
 }
 
+// ---------------------------------------------------------------- prefill
+// Prefill rows (flash attention on fp32 MFMA, v_mfma_f32_32x32x2_f32): a block
+// owns 32 consecutive query rows and one KV head; wave w serves query head
+// kv * G + w, so each K / V tile staged in LDS feeds the whole GQA group.
+// Per tile of 32 positions a wave forms S^T = K Q^T (32 positions x 32
+// queries: lane l holds 16 scores of query l % 32), keeps the online softmax
+// per query in registers (the two lane halves of a query combine with one
+// shuffle), and accumulates O^T += V^T P^T, whose B operand is the score
+// accumulator itself (step st of the product uses the position that score
+// register st holds). Q^T stays in registers (D / 2 per lane), O^T in
+// accumulators (D / 2 per lane). The next tile's K / V are loaded into
+// registers while the current one is multiplied. Positions past the block's
+// last visible one are zero-filled; scores past a row's own length are -inf.
+template <int D>
+struct PrefillShape {
+    static constexpr int DH = D / 2;                    // score steps (dims hl * DH + st)
+    static constexpr int SKEW = DH % 64 == 0 ? 32 : 0;  // upper dim half 32 banks over
+    static constexpr int KS = D + 33;                   // K row stride (= 33 mod 64)
+    static constexpr int VS = D + 8;                    // V row stride (4 rows = 32 banks)
+    static constexpr int DT = D / 32;                   // output dim tiles
+};
+
+typedef float f16v __attribute__((ext_vector_type(16)));
+typedef float f4v __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ int acc_row(int r, int hl) { return 8 * (r >> 2) + 4 * hl + (r & 3); }
+
+// Scheduling of a run of N MFMAs, each with one LDS operand read: four reads
+// ahead, then one read per MFMA, so the reads are neither serialised behind
+// their MFMAs nor all hoisted (which would hold N operands in registers).
+template <int N>
+__device__ __forceinline__ void pipeline_ds_mfma() {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+#pragma unroll
+    for (int i = 0; i < N - 4; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+}
+
+// (D, G) with the prefill kernel: at most 8 float4 of K (and of V) per thread
+// per tile, and, at 512 threads (a 256-register budget), D <= 128.
+constexpr bool prefill_shape_ok(int d, int g) { return d / (8 * g) <= 8 && (g < 8 || d <= 128); }
+
+template <int D, int G>
+__global__ __launch_bounds__(64 * G) void attention_prefill_kernel(ReadArgs a) {
+    using S = PrefillShape<D>;
+    constexpr int T = 64 * G, F4 = 32 * D / 4 / T;  // float4 of K (and of V) per thread per tile
+    static_assert(F4 >= 1 && (32 * D / 4) % T == 0, "tile load split");
+    __shared__ float ks[2][32 * S::KS], vs[2][32 * S::VS];
+    const int qtiles = (a.rows + 31) / 32;
+    const int q0 = (qtiles - 1 - int(blockIdx.x)) * 32, kvh = blockIdx.y;  // longest rows first
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, lc = lane & 31, hl = lane >> 5;
+    const int head = kvh * G + w, qrow = q0 + lc;
+    const int len = a.length0 + qrow;  // positions [0, len) visible to this lane's query
+    const int len_max = a.length0 + min(a.rows, q0 + 32) - 1;
+    const int tiles = (len_max + 31) / 32;
+    const float scale = 1.f / sqrtf(float(D));
+    const size_t rowstride = size_t(a.kv) * D;
+    float qv[S::DH];
+    {
+        const float* qp = a.query + (size_t(qrow) * a.heads + head) * D + hl * S::DH;
+#pragma unroll
+        for (int e = 0; e < S::DH; e += 4) {
+            const f4v v = qrow < a.rows ? *reinterpret_cast<const f4v*>(qp + e) : f4v{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) qv[e + j] = v[j];
+        }
+    }
+    f4v kp[F4], vp[F4];
+    auto fetch = [&](int t) {
+#pragma unroll
+        for (int i = 0; i < F4; ++i) {
+            const int e = int(threadIdx.x) + T * i, pos = t * 32 + e / (D / 4), c = (e % (D / 4)) * 4;
+            const size_t off = size_t(pos) * rowstride + size_t(kvh) * D + c;
+            const bool live = pos < len_max;
+            kp[i] = live ? *reinterpret_cast<const f4v*>(a.keys + off) : f4v{0.f, 0.f, 0.f, 0.f};
+            vp[i] = live ? *reinterpret_cast<const f4v*>(a.values + off) : f4v{0.f, 0.f, 0.f, 0.f};
+        }
+    };
+    auto stage = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < F4; ++i) {
+            const int e = int(threadIdx.x) + T * i, pr = e / (D / 4), c = (e % (D / 4)) * 4;
+            float* kd = &ks[buf][pr * S::KS + c + (c >= S::DH ? S::SKEW : 0)];
+            float* vd = &vs[buf][pr * S::VS + c];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                kd[j] = kp[i][j];
+                vd[j] = vp[i][j];
+            }
+        }
+    };
+    fetch(0);
+    stage(0);
+    __syncthreads();
+    f16v o[S::DT];
+#pragma unroll
+    for (int dt = 0; dt < S::DT; ++dt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[dt][r] = 0.f;
+    float m = -INFINITY, l = 0.f;
+    for (int t = 0; t < tiles; ++t) {
+        const int buf = t & 1;
+        if (t + 1 < tiles) fetch(t + 1);
+        const float* kt = &ks[buf][lc * S::KS + hl * (S::DH + S::SKEW)];
+        f16v sc;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) sc[r] = 0.f;
+#pragma unroll
+        for (int st = 0; st < S::DH; ++st) sc = __builtin_amdgcn_mfma_f32_32x32x2f32(kt[st], qv[st], sc, 0, 0, 0);
+        pipeline_ds_mfma<S::DH>();
+        float mx = -INFINITY;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const float v = t * 32 + acc_row(r, hl) < len ? sc[r] * scale : -INFINITY;
+            sc[r] = v;
+            mx = fmaxf(mx, v);
+        }
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        const float mn = fmaxf(m, mx);  // finite: position 0 is visible to every row
+        const float corr = expf(m - mn);
+        m = mn;
+        float ps = 0.f;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const float p = expf(sc[r] - mn);
+            sc[r] = p;
+            ps += p;
+        }
+        l = l * corr + ps;
+        const float* vt = &vs[buf][lc];
+#pragma unroll
+        for (int dt = 0; dt < S::DT; ++dt) {
+            o[dt] *= corr;
+#pragma unroll
+            for (int st = 0; st < 16; ++st)
+                o[dt] = __builtin_amdgcn_mfma_f32_32x32x2f32(vt[acc_row(st, hl) * S::VS + dt * 32], sc[st], o[dt], 0,
+                                                             0, 0);
+        }
+        pipeline_ds_mfma<16 * S::DT>();
+        if (t + 1 < tiles) stage(buf ^ 1);
+        __syncthreads();
+    }
+    if (qrow < a.rows) {
+        const float den = l + __shfl_xor(l, 32, 64);
+        const size_t base = (size_t(qrow) * a.heads + head) * D;
+#pragma unroll
+        for (int dt = 0; dt < S::DT; ++dt)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const size_t idx = base + dt * 32 + acc_row(r, hl);
+                a.out[idx] = (o[dt][r] / den) * sigmoidf_(a.gate[idx]);
+            }
+    } else {
+        (void)__shfl_xor(l, 32, 64);
+    }
+}
+
+template <int D, int G>
+int launch_prefill_g(hipStream_t s, const ReadArgs& a) {
+    if constexpr (prefill_shape_ok(D, G)) {
+        hipLaunchKernelGGL((attention_prefill_kernel<D, G>), dim3(ceil_div(a.rows, 32), unsigned(a.kv)), dim3(64 * G),
+                           0, s, a);
+        return int(hipGetLastError());
+    }
+    return int(hipErrorInvalidValue);
+}
+template <int D>
+int launch_prefill(hipStream_t s, const ReadArgs& a, int group) {
+    switch (group) {
+    case 1: return launch_prefill_g<D, 1>(s, a);
+    case 2: return launch_prefill_g<D, 2>(s, a);
+    case 4: return launch_prefill_g<D, 4>(s, a);
+    case 8: return launch_prefill_g<D, 8>(s, a);
+    }
+    return int(hipErrorInvalidValue);
+}
+
 template <int D>
 int launch_d(hipStream_t s, const ReadArgs& a, int group) {
     dim3 grid(unsigned(a.splits), unsigned(a.kv), unsigned(a.rows));
@@ -197,6 +379,8 @@ int decode_splits(int length, int kv, int& span) {
     span = s;
     return (length + s - 1) / s;
 }
+
+constexpr int kPrefillMinRows = 8;  // fewer rows (decode, verify): attention_read_kernel
 
 }  // namespace
 
@@ -231,6 +415,14 @@ int run_attention_read(hipStream_t s, int heads_count, const Params& p, float* s
     } else {
         a.splits = 1;
         a.span = a.length0 + a.rows;  // row r reads its own length inside the span
+    }
+    if (a.rows >= kPrefillMinRows && (a.d == 64 || a.d == 128 || a.d == 256) &&
+        (group == 1 || group == 2 || group == 4 || group == 8) && prefill_shape_ok(a.d, group)) {
+        switch (a.d) {
+        case 64: return launch_prefill<64>(s, a, group);
+        case 128: return launch_prefill<128>(s, a, group);
+        default: return launch_prefill<256>(s, a, group);
+        }
     }
     int e;
     switch (a.d) {

@@ -206,6 +206,35 @@ __device__ float wait1(const Args& a, Rs r, unsigned off, unsigned want, Lds& l,
         __builtin_amdgcn_s_sleep(1);
     }
 }
+// Several polls at once: every load is issued before any tag is checked, so
+// one round trip serves all of them when their producers are done; an entry
+// not yet tagged `want` falls back to its own poll. live[k] false: skipped.
+template <int N>
+__device__ __forceinline__ void wait2n(const Args& a, Rs r, const unsigned (&off)[N], const bool (&live)[N],
+                                       unsigned want, f2 (&out)[N], Lds& l, unsigned long long start, int p) {
+    f4 v[N];
+#pragma unroll
+    for (int k = 0; k < N; ++k)
+        if (live[k]) v[k] = ldx4(r, off[k]);
+#pragma unroll
+    for (int k = 0; k < N; ++k) {
+        if (!live[k]) continue;
+        if (__float_as_uint(v[k].y) == want && __float_as_uint(v[k].w) == want)
+            out[k] = f2{v[k].x, v[k].z};
+        else
+            out[k] = wait2(a, r, off[k], want, l, start, p);
+    }
+}
+template <int N>
+__device__ __forceinline__ void wait1n(const Args& a, Rs r, const unsigned (&off)[N], unsigned want, float (&out)[N],
+                                       Lds& l, unsigned long long start, int p) {
+    f2 v[N];
+#pragma unroll
+    for (int k = 0; k < N; ++k) v[k] = ldx2(r, off[k]);
+#pragma unroll
+    for (int k = 0; k < N; ++k)
+        out[k] = __float_as_uint(v[k].y) == want ? v[k].x : wait1(a, r, off[k], want, l, start, p);
+}
 // Block barrier of phase p without a memory fence: LDS writes done
 // (lgkmcnt(0)), then s_barrier; the outstanding prefetch loads stay in
 // flight. Every wave of the block calls it once per phase. False when a lane
@@ -223,12 +252,27 @@ __device__ __forceinline__ bool bsync(Lds& l, int p) {
 // ---------------------------------------------------------------- staging
 __device__ __forceinline__ float silu(float x) { return x * sigmoidf_(x); }
 
-// The block's 512 threads copy n (even) tagged values at scratch offset `off`
-// into dst, each pair polled until tagged `want`.
-__device__ void stage_tagged(const Args& a, Rs rs, unsigned off, int n, unsigned want, float* dst, Lds& l, int p) {
+// The block's 512 threads copy N (even) tagged values at scratch offset `off`
+// into dst, each pair polled until tagged `want` (all of a thread's polls in
+// flight together).
+template <int N>
+__device__ __forceinline__ void stage_tagged(const Args& a, Rs rs, unsigned off, unsigned want, float* dst, Lds& l,
+                                             int p) {
+    constexpr int PAIRS = N / 2, K = (PAIRS + THREADS - 1) / THREADS;
     const unsigned long long start = wall_clock64();
-    for (int i = int(threadIdx.x); i < n / 2; i += THREADS)
-        *reinterpret_cast<f2*>(dst + 2 * i) = wait2(a, rs, off + 16u * unsigned(i), want, l, start, p);
+    unsigned o[K];
+    bool live[K];
+    f2 v[K];
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+        const int i = int(threadIdx.x) + THREADS * k;
+        live[k] = i < PAIRS;
+        o[k] = off + 16u * unsigned(i);
+    }
+    wait2n<K>(a, rs, o, live, want, v, l, start, p);
+#pragma unroll
+    for (int k = 0; k < K; ++k)
+        if (live[k]) *reinterpret_cast<f2*>(dst + 2 * (int(threadIdx.x) + THREADS * k)) = v[k];
 }
 // (1 + w) of an H-long norm weight into l.nw[par] (plain loads, issued before
 // the tagged polls so their latency overlaps).
@@ -245,7 +289,7 @@ __device__ __forceinline__ void stage_input(const Args& a, Rs rs, int L, int pro
             *reinterpret_cast<f4*>(&l.act[par][4 * t]) =
                 ldp4(rsrc(a.embedding), unsigned(a.token) * unsigned(H * 4) + 16u * unsigned(t), 0);
     } else {
-        stage_tagged(a, rs, SOFF(x), H, tag(a, producer), l.act[par], l, p);
+        stage_tagged<H>(a, rs, SOFF(x), tag(a, producer), l.act[par], l, p);
     }
 }
 __device__ __forceinline__ float input_at(const Args& a, Rs rs, int L, int producer, int i, Lds& l, int p) {
@@ -322,7 +366,7 @@ __device__ __forceinline__ void din_row(const f4* wb, const f4 (&xv)[4], int u, 
         if (lane_id() == R) mine = acc;
     }
 }
-__device__ bool phase_din(const Args& a, Rs rs, LayerP w, int L, int p, int u, const f4* wb, Lds& l) {
+__device__ __forceinline__ bool phase_din(const Args& a, Rs rs, LayerP w, int L, int p, int u, const f4* wb, Lds& l) {
     const int par = p & 1;
     const int lane = int(lane_id()), row = u * DIN_RPW + lane;
     const bool conv = lane < DIN_RPW && row < CH;
@@ -396,7 +440,7 @@ __device__ __forceinline__ void z_row(Rs rs, const f4* wb, const f4 (&xv)[4], in
         if (lane_id() == 0) stt(rs, SOFF(z) + 8u * unsigned(row), silu(acc), t);
     }
 }
-__device__ bool phase_mix(const Args& a, Rs rs, LayerP w, int L, int p, int u, f4* wb, Lds& l) {
+__device__ __forceinline__ bool phase_mix(const Args& a, Rs rs, LayerP w, int L, int p, int u, f4* wb, Lds& l) {
     const int par = p & 1;
     stage_norm(w->input_norm, par, l);
     stage_input(a, rs, L, p - 2, par, l, p);
@@ -418,11 +462,11 @@ __device__ bool phase_mix(const Args& a, Rs rs, LayerP w, int L, int p, int u, f
     const unsigned want = tag(a, p - 1);
     const unsigned long long start = wall_clock64();
     const unsigned qo = SOFF(proj) + (unsigned(h) * DK + lane) * 8u, ko = qo + KD * 8u;
-    const float q0 = wait1(a, rs, qo, want, l, start, p), q1 = wait1(a, rs, qo + 512u, want, l, start, p);
-    const float k0 = wait1(a, rs, ko, want, l, start, p), k1 = wait1(a, rs, ko + 512u, want, l, start, p);
-    const float v = wait1(a, rs, SOFF(proj) + unsigned(2 * KD + h * DV + j) * 8u, want, l, start, p);
-    const float av = wait1(a, rs, SOFF(ab) + 8u * unsigned(h), want, l, start, p);
-    const float bv = wait1(a, rs, SOFF(ab) + 8u * unsigned(VH + h), want, l, start, p);
+    const unsigned mo[7] = {qo, qo + 512u, ko, ko + 512u, SOFF(proj) + unsigned(2 * KD + h * DV + j) * 8u,
+                            SOFF(ab) + 8u * unsigned(h), SOFF(ab) + 8u * unsigned(VH + h)};
+    float mv[7];
+    wait1n<7>(a, rs, mo, want, mv, l, start, p);
+    const float q0 = mv[0], q1 = mv[1], k0 = mv[2], k1 = mv[3], v = mv[4], av = mv[5], bv = mv[6];
     // L2 norms (reference.h:134-143), q / sqrt(dk)
     const float sq = wave_sum(q0 * q0 + q1 * q1);
     const float sk = wave_sum(k0 * k0 + k1 * k1);
@@ -483,17 +527,19 @@ __device__ __forceinline__ void prefetch_row(const float* m, int row, int rows, 
 #pragma unroll
     for (int v = 0; v < COLS / 256; ++v) wb[v] = ldw(r, lo + 1024u * v, ro);
 }
-__device__ bool phase_dout(const Args& a, Rs rs, LayerP w, int L, int p, int u, const f4* wb, Lds& l) {
+__device__ __forceinline__ bool phase_dout(const Args& a, Rs rs, LayerP w, int L, int p, int u, const f4* wb, Lds& l) {
     const int par = p & 1;
     {
         const unsigned th = threadIdx.x;
         const f4 nw = ldp4(rsrc(w->norm_w), 16u * (th & 31), 0);
         const unsigned want = tag(a, p - 1);
         const unsigned long long start = wall_clock64();
-        const f2 c01 = wait2(a, rs, SOFF(core) + 32u * th, want, l, start, p);
-        const f2 c23 = wait2(a, rs, SOFF(core) + 32u * th + 16u, want, l, start, p);
-        const f2 z01 = wait2(a, rs, SOFF(z) + 32u * th, want, l, start, p);
-        const f2 z23 = wait2(a, rs, SOFF(z) + 32u * th + 16u, want, l, start, p);
+        const unsigned co[4] = {SOFF(core) + 32u * th, SOFF(core) + 32u * th + 16u, SOFF(z) + 32u * th,
+                                SOFF(z) + 32u * th + 16u};
+        const bool all[4] = {true, true, true, true};
+        f2 cz[4];
+        wait2n<4>(a, rs, co, all, want, cz, l, start, p);
+        const f2 c01 = cz[0], c23 = cz[1], z01 = cz[2], z23 = cz[3];
         const f4 core = f4{c01.x, c01.y, c23.x, c23.y}, sz = f4{z01.x, z01.y, z23.x, z23.y};
         const float ss = group_sum<32>(dot4(core, core));
         const float r = 1.f / sqrtf(ss / float(DV) + a.eps);
@@ -528,10 +574,10 @@ __device__ __forceinline__ void glu_row(Rs rs, const f4* wb, const f4 (&xv)[4], 
         if (lane_id() == 0) stt(rs, SOFF(product) + 8u * unsigned(row), silu(g) * up, t);
     }
 }
-__device__ bool phase_glu(const Args& a, Rs rs, LayerP w, int p, int u, const f4* wb, Lds& l) {
+__device__ __forceinline__ bool phase_glu(const Args& a, Rs rs, LayerP w, int p, int u, const f4* wb, Lds& l) {
     const int par = p & 1;
     stage_norm(w->post_norm, par, l);
-    stage_tagged(a, rs, SOFF(after), H, tag(a, p - 1), l.act[par], l, p);
+    stage_tagged<H>(a, rs, SOFF(after), tag(a, p - 1), l.act[par], l, p);
     if (!bsync(l, p)) return false;
     if (u * GLU_RPW >= I) return true;
     f4 xv[4];
@@ -542,9 +588,9 @@ __device__ bool phase_glu(const Args& a, Rs rs, LayerP w, int p, int u, const f4
 }
 
 // ---- T_DOWN: x = after + down . product
-__device__ bool phase_down(const Args& a, Rs rs, int p, int u, const f4* wb, Lds& l) {
+__device__ __forceinline__ bool phase_down(const Args& a, Rs rs, int p, int u, const f4* wb, Lds& l) {
     const int par = p & 1;
-    stage_tagged(a, rs, SOFF(product), I, tag(a, p - 1), l.act[par], l, p);
+    stage_tagged<I>(a, rs, SOFF(product), tag(a, p - 1), l.act[par], l, p);
     if (!bsync(l, p)) return false;
     if (u >= H) return true;
     const float acc = dot_row_lds<I / 256>(wb, l.act[par]);
@@ -582,7 +628,7 @@ __device__ __forceinline__ void aqkv_row(Rs rs, const f4* wb, const f4 (&xv)[4],
         }
     }
 }
-__device__ bool phase_aqkv(const Args& a, Rs rs, LayerP w, int L, int p, int u, const f4* wb, Lds& l) {
+__device__ __forceinline__ bool phase_aqkv(const Args& a, Rs rs, LayerP w, int L, int p, int u, const f4* wb, Lds& l) {
     const int par = p & 1;
     stage_norm(w->input_norm, par, l);
     stage_input(a, rs, L, p - 1, par, l, p);
@@ -598,7 +644,8 @@ __device__ bool phase_aqkv(const Args& a, Rs rs, LayerP w, int L, int p, int u, 
 
 // ---- T_ATTN: one wave per (KV head, span of positions); the 4 query heads of
 // the group share every K/V read. Lane: sub = lane % 16 holds dims
-// 16 sub .. 16 sub + 15, slot = lane / 16 one of 4 positions per step.
+// 64 e + 4 sub .. +3 (e < 4), slot = lane / 16 one of 4 positions per step, so
+// each K / V load instruction reads 256 contiguous bytes of 4 rows.
 // Caches are [capacity, kv_heads, head_dim].
 __device__ __forceinline__ int attn_span(int len) {
     const int chunks = (len + SPAN * SMAX - 1) / (SPAN * SMAX);
@@ -611,11 +658,11 @@ __device__ __forceinline__ void load_kv_chunk(LayerP w, int kvh, int first, int 
     for (int step = 0; step < SPAN / 4; ++step) {
         const int pp = first + 4 * step + int(slot);
         if (pp < pos) {  // position pos is this step's own: patched in from LDS
-            const unsigned o = ((unsigned(pp) * NKV + unsigned(kvh)) * HD + sub * 16u) * 4u;
+            const unsigned o = ((unsigned(pp) * NKV + unsigned(kvh)) * HD + sub * 4u) * 4u;
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                buf[step * 8 + e] = ldw(rk, o + 16u * e, 0);
-                buf[step * 8 + 4 + e] = ldw(rv, o + 16u * e, 0);
+                buf[step * 8 + e] = ldp4(rk, o + 256u * e, 0);
+                buf[step * 8 + 4 + e] = ldp4(rv, o + 256u * e, 0);
             }
         }
     }
@@ -629,8 +676,8 @@ __device__ __forceinline__ void patch_new(f4* buf, const float* kn, const float*
         if (first + 4 * step + int(slot) == pos) {
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                buf[step * 8 + e] = lds4(kn + sub * 16 + 4 * e);
-                buf[step * 8 + 4 + e] = lds4(vn + sub * 16 + 4 * e);
+                buf[step * 8 + e] = lds4(kn + sub * 4 + 64 * e);
+                buf[step * 8 + 4 + e] = lds4(vn + sub * 4 + 64 * e);
             }
         }
     }
@@ -661,7 +708,7 @@ __device__ __forceinline__ void norm_rope_head(f4 x, f4 wplus, const Args& a, fl
     }
     *reinterpret_cast<f4*>(out + 4 * lane) = x;
 }
-__device__ bool phase_attn(const Args& a, Rs rs, LayerP w, int p, int u, f4* wb, Lds& l) {
+__device__ __forceinline__ bool phase_attn(const Args& a, Rs rs, LayerP w, int p, int u, f4* wb, Lds& l) {
     const int par = p & 1;
     const int pos = a.pos, len = pos + 1, span = attn_span(len), splits = (len + span - 1) / span;
     const bool block_busy = int(blockIdx.x) < NKV * splits;  // wave 0 has the block's lowest unit
@@ -675,13 +722,13 @@ __device__ bool phase_attn(const Args& a, Rs rs, LayerP w, int p, int u, f4* wb,
         const f4 wq = f4(1.f) + ldp4(rn, 16u * lane, 0), wk = f4(1.f) + ldp4(rn, HD * 4u + 16u * lane, 0);
         const unsigned long long start = wall_clock64();
         const unsigned qo = SOFF(mixed) + (unsigned(wave) * 2u * HD + 4u * lane) * 8u;
-        const f2 q01 = wait2(a, rs, qo, want, l, start, p), q23 = wait2(a, rs, qo + 16u, want, l, start, p);
-        norm_rope_head(f4{q01.x, q01.y, q23.x, q23.y}, wq, a, &l.act[par][wave * HD]);
-        if (wave < NKV) {
-            const unsigned ko = SOFF(key) + (unsigned(wave) * HD + 4u * lane) * 8u;
-            const f2 k01 = wait2(a, rs, ko, want, l, start, p), k23 = wait2(a, rs, ko + 16u, want, l, start, p);
-            norm_rope_head(f4{k01.x, k01.y, k23.x, k23.y}, wk, a, &l.act[par][NH * HD + wave * HD]);
-        }
+        const unsigned ko = SOFF(key) + (unsigned(wave < NKV ? wave : 0) * HD + 4u * lane) * 8u;
+        const unsigned qk[4] = {qo, qo + 16u, ko, ko + 16u};
+        const bool hask = wave < NKV, live[4] = {true, true, hask, hask};
+        f2 qkv[4];
+        wait2n<4>(a, rs, qk, live, want, qkv, l, start, p);
+        norm_rope_head(f4{qkv[0].x, qkv[0].y, qkv[1].x, qkv[1].y}, wq, a, &l.act[par][wave * HD]);
+        if (hask) norm_rope_head(f4{qkv[2].x, qkv[2].y, qkv[3].x, qkv[3].y}, wk, a, &l.act[par][NH * HD + wave * HD]);
     }
     if (!bsync(l, p)) return false;
     if (u >= NKV * splits) return true;
@@ -693,17 +740,24 @@ __device__ bool phase_attn(const Args& a, Rs rs, LayerP w, int p, int u, f4* wb,
     if (has_new) {
         if (slot == 0) {
             const Rs rk = rsrc(w->keys), rv = rsrc(w->values);
-            const unsigned co = ((unsigned(pos) * NKV + unsigned(kvh)) * HD + sub * 16u) * 4u;
-            const unsigned vo = SOFF(value) + (unsigned(kvh) * HD + sub * 16u) * 8u;
+            const unsigned co = ((unsigned(pos) * NKV + unsigned(kvh)) * HD + sub * 4u) * 4u;
+            const unsigned vo = SOFF(value) + (unsigned(kvh) * HD + sub * 4u) * 8u;
             const unsigned long long start = wall_clock64();
+            unsigned vof[8];
+            bool all[8];
+            f2 vpair[8];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {  // dims 64 (k / 2) + 4 sub + 2 (k % 2) .. +1
+                vof[k] = vo + 512u * unsigned(k >> 1) + 16u * unsigned(k & 1);
+                all[k] = true;
+            }
+            wait2n<8>(a, rs, vof, all, want, vpair, l, start, p);
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                const f2 v01 = wait2(a, rs, vo + 32u * e, want, l, start, p);
-                const f2 v23 = wait2(a, rs, vo + 32u * e + 16u, want, l, start, p);
-                const f4 vv = f4{v01.x, v01.y, v23.x, v23.y};
-                *reinterpret_cast<f4*>(vn + sub * 16 + 4 * e) = vv;
-                stp4(rk, co + 16u * e, lds4(kn + sub * 16 + 4 * e));
-                stp4(rv, co + 16u * e, vv);
+                const f4 vv = f4{vpair[2 * e].x, vpair[2 * e].y, vpair[2 * e + 1].x, vpair[2 * e + 1].y};
+                *reinterpret_cast<f4*>(vn + sub * 4 + 64 * e) = vv;
+                stp4(rk, co + 256u * e, lds4(kn + sub * 4 + 64 * e));
+                stp4(rv, co + 256u * e, vv);
             }
         }
         compiler_fence();
@@ -711,13 +765,14 @@ __device__ bool phase_attn(const Args& a, Rs rs, LayerP w, int p, int u, f4* wb,
     }
     const float scale = 1.f / 16.f;  // 1 / sqrt(256)
     const unsigned t = tag(a, p);
+    float* gml = l.wave[wave] + HD;  // each head's (max, sum), published after all the heads' sums
     int held = begin;  // wb holds the K/V chunk starting here (prefetched: the first)
 #pragma unroll 1
     for (int g = 0; g < NH / NKV; ++g) {
         const int h = kvh * (NH / NKV) + g;
         f4 q[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) q[e] = lds4(&l.act[par][h * HD + sub * 16 + 4 * e]);
+        for (int e = 0; e < 4; ++e) q[e] = lds4(&l.act[par][h * HD + sub * 4 + 64 * e]);
         float m = -INFINITY, lsum = 0.f;
         f4 acc[4] = {f4(0.f), f4(0.f), f4(0.f), f4(0.f)};
 #pragma unroll 1
@@ -765,16 +820,24 @@ __device__ bool phase_attn(const Args& a, Rs rs, LayerP w, int p, int u, f4* wb,
         }
         const unsigned slotix = unsigned(h) * SMAX + unsigned(sp);
         if (slot == 0) {
-            const unsigned ao = SOFF(pacc) + (slotix * HD + sub * 16u) * 4u;
+            const unsigned ao = SOFF(pacc) + (slotix * HD + sub * 4u) * 4u;
 #pragma unroll
-            for (int e = 0; e < 4; ++e) stx4(rs, ao + 16u * e, acc[e]);
+            for (int e = 0; e < 4; ++e) stx4(rs, ao + 256u * e, acc[e]);
         }
-        // the sums are complete in memory before their (max, sum) pair is
-        __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
-        compiler_fence();
         if (lane == 0) {
-            stt(rs, SOFF(pml) + slotix * 16u, m, t);
-            stt(rs, SOFF(pml) + slotix * 16u + 8u, lsum, t);
+            gml[2 * g] = m;
+            gml[2 * g + 1] = lsum;
+        }
+    }
+    // every head's sums are complete in memory before any (max, sum) pair is
+    __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
+    compiler_fence();
+    if (lane == 0) {
+#pragma unroll
+        for (int g = 0; g < NH / NKV; ++g) {
+            const unsigned slotix = unsigned(kvh * (NH / NKV) + g) * SMAX + unsigned(sp);
+            stt(rs, SOFF(pml) + slotix * 16u, gml[2 * g], t);
+            stt(rs, SOFF(pml) + slotix * 16u + 8u, gml[2 * g + 1], t);
         }
     }
     return true;
@@ -783,7 +846,7 @@ __device__ bool phase_attn(const Args& a, Rs rs, LayerP w, int p, int u, f4* wb,
 // ---- T_COMB: merge the splits (log-sum-exp) and apply the sigmoid gate
 // (reference.h:171-200); one wave per (head, 4 dims), lanes over splits.
 constexpr int COMB_PER_LANE = SMAX / 64;
-__device__ bool phase_comb(const Args& a, Rs rs, int p, int u, Lds& l) {
+__device__ __forceinline__ bool phase_comb(const Args& a, Rs rs, int p, int u, Lds& l) {
     if (!bsync(l, p)) return false;
     if (u >= COMB_WAVES) return true;
     const unsigned lane = lane_id();
@@ -793,17 +856,23 @@ __device__ bool phase_comb(const Args& a, Rs rs, int p, int u, Lds& l) {
     const unsigned long long start = wall_clock64();
     float mv[COMB_PER_LANE], lv[COMB_PER_LANE];
     float mm = -INFINITY;
+    {
+        unsigned po[COMB_PER_LANE];
+        bool live[COMB_PER_LANE];
+        f2 ml[COMB_PER_LANE];
 #pragma unroll
-    for (int k = 0; k < COMB_PER_LANE; ++k) {
-        const int s = int(lane) + 64 * k;
-        mv[k] = -INFINITY;
-        lv[k] = 0.f;
-        if (s < splits) {
-            const f2 ml = wait2(a, rs, SOFF(pml) + (unsigned(h) * SMAX + unsigned(s)) * 16u, want, l, start, p);
-            mv[k] = ml.x;
-            lv[k] = ml.y;
+        for (int k = 0; k < COMB_PER_LANE; ++k) {
+            const int s = int(lane) + 64 * k;
+            live[k] = s < splits;
+            po[k] = SOFF(pml) + (unsigned(h) * SMAX + unsigned(s)) * 16u;
         }
-        mm = fmaxf(mm, mv[k]);
+        wait2n<COMB_PER_LANE>(a, rs, po, live, want, ml, l, start, p);
+#pragma unroll
+        for (int k = 0; k < COMB_PER_LANE; ++k) {
+            mv[k] = live[k] ? ml[k].x : -INFINITY;
+            lv[k] = live[k] ? ml[k].y : 0.f;
+            mm = fmaxf(mm, mv[k]);
+        }
     }
     mm = wave_max(mm);
     float den = 0.f;
@@ -833,9 +902,9 @@ __device__ bool phase_comb(const Args& a, Rs rs, int p, int u, Lds& l) {
 }
 
 // ---- T_O: after = x + o . ctx
-__device__ bool phase_o(const Args& a, Rs rs, int L, int p, int u, const f4* wb, Lds& l) {
+__device__ __forceinline__ bool phase_o(const Args& a, Rs rs, int L, int p, int u, const f4* wb, Lds& l) {
     const int par = p & 1;
-    stage_tagged(a, rs, SOFF(ctx), NH * HD, tag(a, p - 1), l.act[par], l, p);
+    stage_tagged<NH * HD>(a, rs, SOFF(ctx), tag(a, p - 1), l.act[par], l, p);
     if (!bsync(l, p)) return false;
     if (u >= H) return true;
     const float acc = dot_row_lds<NH * HD / 256>(wb, l.act[par]);
@@ -882,10 +951,10 @@ __device__ __forceinline__ void prefetch_lm(const Args& a, int u, f4* wb) {
     const int rpw = lm_rows_per_wave(a.vocab), row0 = u * rpw, row_end = min(a.vocab, row0 + rpw);
     lm_load(rsrc(a.lm_head), row0, row_end, wb);
 }
-__device__ bool phase_lm(const Args& a, Rs rs, int p, int u, f4* wb, Lds& l) {
+__device__ __forceinline__ bool phase_lm(const Args& a, Rs rs, int p, int u, f4* wb, Lds& l) {
     const int par = p & 1;
     stage_norm(a.final_norm, par, l);
-    stage_tagged(a, rs, SOFF(x), H, tag(a, p - 1), l.act[par], l, p);
+    stage_tagged<H>(a, rs, SOFF(x), tag(a, p - 1), l.act[par], l, p);
     if (!bsync(l, p)) return false;
     f4 xv[4];
     normed_chunks(l, par, a.eps, xv);
@@ -910,20 +979,33 @@ __device__ bool phase_lm(const Args& a, Rs rs, int p, int u, f4* wb, Lds& l) {
     return true;
 }
 
-// ---- T_ARG (block 0, wave 0): merge the per-wave maxima (first index of the
-// maximum, non-finite count; reference.h:222-230).
-__device__ void phase_arg(const Args& a, Rs rs, int p, Lds& l) {
-    const unsigned lane = lane_id();
+// ---- T_ARG (block 0): merge the per-wave maxima (first index of the
+// maximum, non-finite count; reference.h:222-230). Each of the block's
+// threads polls NW / THREADS parts at once; the waves' results meet in LDS.
+__device__ __forceinline__ void phase_arg(const Args& a, Rs rs, int p, Lds& l) {
+    constexpr int K = NW / THREADS;
+    static_assert(NW % THREADS == 0, "argmax parts per thread");
+    const unsigned lane = lane_id(), wave = threadIdx.x >> 6;
     const unsigned want = tag(a, p - 1);
     const unsigned long long start = wall_clock64();
+    unsigned po[K];
+    bool live[K];
+    f2 vi[K], b2[K];
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+        po[k] = SOFF(lmpart) + unsigned(int(threadIdx.x) + THREADS * k) * 32u;
+        live[k] = true;
+        b2[k] = ldx2(rs, po[k] + 16u);
+    }
+    wait2n<K>(a, rs, po, live, want, vi, l, start, p);
     float best = -INFINITY;
     unsigned at = 0xffffffffu, bad = 0;
-    for (int i = int(lane); i < NW; i += 64) {
-        const unsigned o = SOFF(lmpart) + unsigned(i) * 32u;
-        const f2 vi = wait2(a, rs, o, want, l, start, p);
-        const float v = vi.x;
-        const unsigned idx = __float_as_uint(vi.y);
-        bad += __float_as_uint(wait1(a, rs, o + 16, want, l, start, p));
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+        const float bk = __float_as_uint(b2[k].y) == want ? b2[k].x : wait1(a, rs, po[k] + 16u, want, l, start, p);
+        bad += __float_as_uint(bk);
+        const float v = vi[k].x;
+        const unsigned idx = __float_as_uint(vi[k].y);
         if (v > best || (v == best && idx < at)) {
             best = v;
             at = idx;
@@ -939,7 +1021,22 @@ __device__ void phase_arg(const Args& a, Rs rs, int p, Lds& l) {
             at = oi;
         }
     }
-    if (lane == 0 && !failed(l)) {
+    if (lane == 0) {
+        l.wave[wave][0] = best;
+        l.wave[wave][1] = __uint_as_float(at);
+        l.wave[wave][2] = __uint_as_float(bad);
+    }
+    if (!bsync(l, p + 1) || threadIdx.x != 0) return;
+    for (int w = 1; w < WAVES; ++w) {
+        const float ov = l.wave[w][0];
+        const unsigned oi = __float_as_uint(l.wave[w][1]);
+        bad += __float_as_uint(l.wave[w][2]);
+        if (ov > best || (ov == best && oi < at)) {
+            best = ov;
+            at = oi;
+        }
+    }
+    if (!failed(l)) {
         const Rs pk = rsrc(a.picks);
         stp(pk, 0, float(at));
         stp(pk, 4, float(bad));
@@ -978,7 +1075,7 @@ __global__ __launch_bounds__(THREADS, 1) void decode_kernel(Args a) {
     for (int p = 0; p < a.nphases; ++p) {
         const int t = ptype(a, p);
         if (t == T_ARG) {
-            if (blockIdx.x == 0 && wave == 0) phase_arg(a, rs, p, l);
+            if (blockIdx.x == 0) phase_arg(a, rs, p, l);
             return;
         }
         const int L = player(a, p);
@@ -999,7 +1096,11 @@ __global__ __launch_bounds__(THREADS, 1) void decode_kernel(Args a) {
         default: break;
         }
         if (!ok) return;
-        prefetch(a, p + 1, opaque_uniform(unit), wb);
+        // T_COMB reads no weights: the rows of the phase after it are fetched
+        // before it (at the end of T_ATTN) instead of after it.
+        if (t == T_COMB) continue;
+        const int q = p + 1 < a.nphases && ptype(a, p + 1) == T_COMB ? p + 2 : p + 1;
+        prefetch(a, q, opaque_uniform(unit), wb);
     }
 }
 

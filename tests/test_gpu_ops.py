@@ -406,10 +406,15 @@ def test_attention_query_kv(gpu, cpu, d, rot, heads, kv, tokens, pos):
 
 @pytest.mark.parametrize("d,heads,kv,length,tokens", [(256, 8, 2, 454, 1), (256, 8, 2, 8192, 1), (256, 8, 2, 1, 1),
                                                       (256, 8, 2, 100, 4), (256, 8, 2, 40, 24), (16, 4, 1, 17, 1),
-                                                      (16, 4, 1, 5, 16), (4, 2, 1, 3, 2)])
+                                                      (16, 4, 1, 5, 16), (4, 2, 1, 3, 2), (256, 8, 2, 1, 700),
+                                                      (256, 8, 2, 77, 33), (128, 8, 2, 1, 64), (128, 4, 2, 10, 100),
+                                                      (128, 8, 1, 3, 40), (64, 2, 2, 1, 65), (64, 8, 1, 5, 129),
+                                                      (256, 16, 2, 1, 40), (256, 8, 2, 1, 8)])
 def test_attention_read(gpu, cpu, d, heads, kv, length, tokens):
     """Decode (one row, split-K), a verify pass (rows 2..8, one decode read
-    per row) and a prefill chunk (causal rows)."""
+    per row) and prefill chunks (causal rows: the MFMA flash kernel for head
+    dims 64 / 128 / 256 and GQA groups 1, 2, 4, 8, ragged 32-row tiles, a
+    cached prefix before the chunk; the per-row kernel for the rest)."""
     print(f"attention_read d={d} len={length} rows={tokens}", flush=True)
     rng = np.random.default_rng(d + length + tokens)
     cap = length + tokens + 64
