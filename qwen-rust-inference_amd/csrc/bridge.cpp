@@ -25,6 +25,8 @@ struct Context {
     size_t attn_parts_len = 0;
     float* rule_chunks = nullptr;  // per-(chunk, head) records of the chunked DeltaRule
     size_t rule_chunks_len = 0;
+    float* gemm_work = nullptr;  // K-split partial sums of prefill GEMMs
+    size_t gemm_work_len = 0;
     // RoPE denominators theta^(2i / rot) per (theta bits, rot), device copies.
     std::map<std::pair<uint32_t, int>, float*> rope;
     // Profiler (qr_profile / QWEN_ROCM_PROFILE=1): a hipEvent pair on the
@@ -158,8 +160,11 @@ int project(Context* c, qr::WeightType t, float* y, const void* a, const float* 
         qr::GemvItem it{y, a, rows};
         return launched(c, "gemv", qr::gemv_group(c->stream, t, &it, 1, x, cols, batch));
     }
+    if (int st = ensure(c, &c->gemm_work, &c->gemm_work_len, qr::gemm_scratch(t, rows, cols, batch),
+                        "hipMalloc GEMM split"))
+        return st;
     auto s = scope(c, [&] { return std::string("gemm_") + wname(t) + " " + shape(rows, cols, batch); });
-    return launched(c, "gemm", qr::gemm(c->stream, t, y, a, x, rows, cols, batch));
+    return launched(c, "gemm", qr::gemm(c->stream, t, y, a, x, rows, cols, batch, c->gemm_work, c->gemm_work_len));
 }
 
 int group(Context* c, qr::WeightType t, int n, const QrProjection* items, const float* x, int cols, int batch) {
@@ -188,6 +193,11 @@ int glu(Context* c, qr::WeightType t, float* product, float* gate_y, float* up_y
     if (!qr::gemm_preferred(t, rows, cols, batch)) {
         auto s = scope(c, [&] { return std::string("gemv_") + wname(t) + "_glu 2x" + shape(rows, cols, batch); });
         return launched(c, "gemv_glu", qr::gemv_glu(c->stream, t, product, gate, up, x, rows, cols, batch));
+    }
+    if (qr::gemm_glu_fused(t, gate, up, x, rows, cols, batch)) {  // gate_y / up_y untouched, as the reference's fused GLU
+        auto s = scope(c, [&] { return std::string("gemm_") + wname(t) + "_glu 2x" + shape(rows, cols, batch); });
+        return launched(c, "gemm_glu", qr::gemm_glu(c->stream, product, static_cast<const float*>(gate),
+                                                    static_cast<const float*>(up), x, rows, cols, batch));
     }
     if (int s = project(c, t, gate_y, gate, x, rows, cols, batch)) return s;
     if (int s = project(c, t, up_y, up, x, rows, cols, batch)) return s;
@@ -346,6 +356,7 @@ void qr_destroy(Context* c) {
     if (c->argmax_parts) (void)hipFree(c->argmax_parts);
     if (c->attn_parts) (void)hipFree(c->attn_parts);
     if (c->rule_chunks) (void)hipFree(c->rule_chunks);
+    if (c->gemm_work) (void)hipFree(c->gemm_work);
     (void)hipStreamDestroy(c->stream);
     delete c;
 }

@@ -78,9 +78,16 @@ int gemv_add_norm(hipStream_t s, WeightType t, float* y, const void* a, const fl
                   const QrAddNormPost& post, unsigned* ticket);
 
 // gemm.hip -------------------------------------------------------------------
-// Y[batch, rows] = X[batch, cols] . A^T (prefill).
-int gemm(hipStream_t s, WeightType t, float* y, const void* a, const float* x, int rows, int cols, int batch);
+// Y[batch, rows] = X[batch, cols] . A^T (prefill). `work`: bridge scratch of
+// at least gemm_scratch(...) floats (K-split partials).
+int gemm(hipStream_t s, WeightType t, float* y, const void* a, const float* x, int rows, int cols, int batch,
+         float* work, size_t work_len);
+size_t gemm_scratch(WeightType t, int rows, int cols, int batch);
 bool gemm_preferred(WeightType t, int rows, int cols, int batch);
+// product[batch, rows] = silu(X G^T) * (X U^T) in one kernel (prefill, fp32 weights).
+bool gemm_glu_fused(WeightType t, const void* gate, const void* up, const float* x, int rows, int cols, int batch);
+int gemm_glu(hipStream_t s, float* product, const float* gate, const float* up, const float* x, int rows, int cols,
+             int batch);
 
 // ops.hip --------------------------------------------------------------------
 int run_elementwise(hipStream_t s, int op, int count, const Params& a);

@@ -111,8 +111,28 @@ def test_gemm_bf16_int8(gpu, kind, rows, cols, batch):
     assert np.all(np.abs(got - want) <= bound)
 
 
+@pytest.mark.parametrize("rows,cols,batch", [(100, 64, 37), (64, 1024, 129), (3584, 1024, 130), (8, 12, 5)])
+def test_glu_f32_fused_edges(gpu, rows, cols, batch):
+    """The fused fp32 GLU kernel (64-row gate/up tiles, silu in the epilogue)
+    at ragged row, token and K edges, against fp64."""
+    print(f"glu f32 {rows}x{cols} batch {batch}", flush=True)
+    rng = np.random.default_rng(rows + cols + batch)
+    gw = (rng.standard_normal(rows * cols) * 0.05).astype(np.float32)
+    uw = (rng.standard_normal(rows * cols) * 0.05).astype(np.float32)
+    x = rng.standard_normal(batch * cols).astype(np.float32)
+    prod, gy, uy = gpu.alloc(batch * rows), gpu.alloc(batch * rows), gpu.alloc(batch * rows)
+    gpu.glu(prod, gy, uy, gpu.upload(gw), gpu.upload(uw), gpu.upload(x), rows, cols, batch)
+    X = x.reshape(batch, cols).astype(np.float64)
+    G, U = X @ gw.reshape(rows, cols).astype(np.float64).T, X @ uw.reshape(rows, cols).astype(np.float64).T
+    want = G / (1 + np.exp(-G)) * U
+    bound = dot_bound(gw.reshape(rows, cols), X.T).T * (np.abs(U) + 1) + dot_bound(uw.reshape(rows, cols), X.T).T * \
+        (np.abs(G) + 1)
+    got = prod.read().reshape(batch, rows)
+    assert np.all(np.abs(got - want) <= bound + 1e-6 * np.abs(want)), np.max(np.abs(got - want) - bound)
+
+
 @pytest.mark.parametrize("kind", ["f32", "bf16", "i8"])
-@pytest.mark.parametrize("batch", [1, 4, 6, 20])
+@pytest.mark.parametrize("batch", [1, 4, 6, 20, 130])
 def test_group_glu_equal_separate_calls(gpu, kind, batch):
     """Grouped / GLU projections equal the separate projections (reference
     native/rocm/bridge.cpp:657-729); fp32 arms are this bridge's own."""
