@@ -187,6 +187,10 @@ __global__ __launch_bounds__(256) void attention_combine_kernel(ReadArgs a) {
 // accumulators (D / 2 per lane). The next tile's K / V are loaded into
 // registers while the current one is multiplied. Positions past the block's
 // last visible one are zero-filled; scores past a row's own length are -inf.
+// KV split (blockIdx.z of a.splits): when there are too few (query tile, KV
+// head) blocks to fill the CUs, each block takes an equal share of its tile's
+// K / V tiles and writes (max, sum, unnormalised context) partials that
+// attention_combine_kernel merges, as for a decode row.
 template <int D>
 struct PrefillShape {
     static constexpr int DH = D / 2;                    // score steps (dims hl * DH + st)
@@ -233,7 +237,15 @@ __global__ __launch_bounds__(64 * G) void attention_prefill_kernel(ReadArgs a) {
     const int head = kvh * G + w, qrow = q0 + lc;
     const int len = a.length0 + qrow;  // positions [0, len) visible to this lane's query
     const int len_max = a.length0 + min(a.rows, q0 + 32) - 1;
-    const int tiles = (len_max + 31) / 32;
+    const int all_tiles = (len_max + 31) / 32, share = (all_tiles + a.splits - 1) / a.splits;
+    const int t_begin = int(blockIdx.z) * share, t_end = min(all_tiles, t_begin + share);
+    if (t_begin >= t_end) {  // an empty share (early query tiles): a neutral partial
+        if (qrow < a.rows) {
+            float* part = a.parts + ((size_t(qrow) * a.heads + head) * a.splits + blockIdx.z) * (D + 2);
+            for (int i = hl; i < D + 2; i += 2) part[i] = i == 0 ? -INFINITY : 0.f;
+        }
+        return;
+    }
     const float scale = 1.f / sqrtf(float(D));
     const size_t rowstride = size_t(a.kv) * D;
     float qv[S::DH];
@@ -270,8 +282,8 @@ __global__ __launch_bounds__(64 * G) void attention_prefill_kernel(ReadArgs a) {
             }
         }
     };
-    fetch(0);
-    stage(0);
+    fetch(t_begin);
+    stage(t_begin & 1);
     __syncthreads();
     f16v o[S::DT];
 #pragma unroll
@@ -279,9 +291,9 @@ __global__ __launch_bounds__(64 * G) void attention_prefill_kernel(ReadArgs a) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) o[dt][r] = 0.f;
     float m = -INFINITY, l = 0.f;
-    for (int t = 0; t < tiles; ++t) {
+    for (int t = t_begin; t < t_end; ++t) {
         const int buf = t & 1;
-        if (t + 1 < tiles) fetch(t + 1);
+        if (t + 1 < t_end) fetch(t + 1);
         const float* kt = &ks[buf][lc * S::KS + hl * (S::DH + S::SKEW)];
         f16v sc;
 #pragma unroll
@@ -297,13 +309,14 @@ __global__ __launch_bounds__(64 * G) void attention_prefill_kernel(ReadArgs a) {
             mx = fmaxf(mx, v);
         }
         mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-        const float mn = fmaxf(m, mx);  // finite: position 0 is visible to every row
-        const float corr = expf(m - mn);
+        // -inf while a row has seen no visible position (a KV share past its length)
+        const float mn = fmaxf(m, mx), mref = mn == -INFINITY ? 0.f : mn;
+        const float corr = expf(m - mref);
         m = mn;
         float ps = 0.f;
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-            const float p = expf(sc[r] - mn);
+            const float p = expf(sc[r] - mref);
             sc[r] = p;
             ps += p;
         }
@@ -318,11 +331,11 @@ __global__ __launch_bounds__(64 * G) void attention_prefill_kernel(ReadArgs a) {
                                                              0, 0);
         }
         pipeline_ds_mfma<16 * S::DT>();
-        if (t + 1 < tiles) stage(buf ^ 1);
+        if (t + 1 < t_end) stage(buf ^ 1);
         __syncthreads();
     }
-    if (qrow < a.rows) {
-        const float den = l + __shfl_xor(l, 32, 64);
+    const float den = l + __shfl_xor(l, 32, 64);
+    if (qrow < a.rows && a.splits == 1) {
         const size_t base = (size_t(qrow) * a.heads + head) * D;
 #pragma unroll
         for (int dt = 0; dt < S::DT; ++dt)
@@ -331,16 +344,28 @@ __global__ __launch_bounds__(64 * G) void attention_prefill_kernel(ReadArgs a) {
                 const size_t idx = base + dt * 32 + acc_row(r, hl);
                 a.out[idx] = (o[dt][r] / den) * sigmoidf_(a.gate[idx]);
             }
-    } else {
-        (void)__shfl_xor(l, 32, 64);
+    } else if (qrow < a.rows) {
+        float* part = a.parts + ((size_t(qrow) * a.heads + head) * a.splits + blockIdx.z) * (D + 2);
+        if (hl == 0) {
+            part[0] = m;
+            part[1] = den;
+        }
+#pragma unroll
+        for (int dt = 0; dt < S::DT; ++dt)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) part[2 + dt * 32 + acc_row(r, hl)] = o[dt][r];
     }
 }
 
 template <int D, int G>
 int launch_prefill_g(hipStream_t s, const ReadArgs& a) {
     if constexpr (prefill_shape_ok(D, G)) {
-        hipLaunchKernelGGL((attention_prefill_kernel<D, G>), dim3(ceil_div(a.rows, 32), unsigned(a.kv)), dim3(64 * G),
-                           0, s, a);
+        hipLaunchKernelGGL((attention_prefill_kernel<D, G>),
+                           dim3(ceil_div(a.rows, 32), unsigned(a.kv), unsigned(a.splits)), dim3(64 * G), 0, s, a);
+        if (a.splits == 1) return int(hipGetLastError());
+        if (hipError_t e = hipGetLastError()) return int(e);
+        const long total = long(a.rows) * a.heads * a.d;
+        hipLaunchKernelGGL(attention_combine_kernel, dim3(ceil_div(total, 256)), dim3(256), 0, s, a);
         return int(hipGetLastError());
     }
     return int(hipErrorInvalidValue);
@@ -382,11 +407,27 @@ int decode_splits(int length, int kv, int& span) {
 
 constexpr int kPrefillMinRows = 8;  // fewer rows (decode, verify): attention_read_kernel
 
+bool prefill_path(int d, int group, int rows) {
+    return rows >= kPrefillMinRows && (d == 64 || d == 128 || d == 256) &&
+           (group == 1 || group == 2 || group == 4 || group == 8) && prefill_shape_ok(d, group);
+}
+// KV splits of a prefill chunk: about 512 blocks, at most 8 shares per tile.
+int prefill_splits(int rows, int kv) {
+    const long blocks = long(ceil_div(rows, 32)) * (kv > 0 ? kv : 1);
+    long s = (512 + blocks - 1) / blocks;
+    return int(s < 1 ? 1 : s > 8 ? 8 : s);
+}
+
 }  // namespace
 
 size_t attention_scratch_needed(const Params& a) {
     const int tokens = a.n[5] > 0 ? a.n[5] : 1;
-    if (tokens != 1) return 0;
+    const int group = a.n[2] > 0 ? a.n[1] / a.n[2] : 0;
+    if (tokens > 1) {
+        if (!prefill_path(a.n[0], group, tokens)) return 0;
+        const int splits = prefill_splits(tokens, a.n[2]);
+        return splits > 1 ? size_t(tokens) * a.n[1] * splits * (a.n[0] + 2) : 0;
+    }
     int span;
     const int splits = decode_splits(a.n[3], a.n[2], span);
     return splits > 1 ? size_t(a.n[1]) * splits * (a.n[0] + 2) : 0;
@@ -416,8 +457,12 @@ int run_attention_read(hipStream_t s, int heads_count, const Params& p, float* s
         a.splits = 1;
         a.span = a.length0 + a.rows;  // row r reads its own length inside the span
     }
-    if (a.rows >= kPrefillMinRows && (a.d == 64 || a.d == 128 || a.d == 256) &&
-        (group == 1 || group == 2 || group == 4 || group == 8) && prefill_shape_ok(a.d, group)) {
+    if (prefill_path(a.d, group, a.rows)) {
+        a.splits = prefill_splits(a.rows, a.kv);
+        if (a.splits > 1) {
+            if (size_t(a.rows) * a.heads * a.splits * (a.d + 2) > scratch_len) return int(hipErrorInvalidValue);
+            a.parts = scratch;
+        }
         switch (a.d) {
         case 64: return launch_prefill<64>(s, a, group);
         case 128: return launch_prefill<128>(s, a, group);
