@@ -1,7 +1,7 @@
 // Chunked DeltaRule / DeltaRuleGated (ops 7 and 14) for prefill on gfx950:
 // the recurrence of reference.h:149-170 (gates of reference.h:48-60),
 // evaluated 64 tokens at a time in the WY / UT form so that the dense products
-// run on fp32 MFMA (v_mfma_f32_32x32x2_f32) instead of one token per step.
+// run on fp32 MFMA (v_mfma_f32_16x16x4_f32) instead of one token per step.
 //
 // Per head, tokens t = 0..63 of a chunk, state S0 (dk x dv) entering it, log
 // decay g_t, beta_t, and G_t = g_0 + ... + g_t:
@@ -15,7 +15,7 @@
 // rule_chunk_prep_kernel builds U, -W, e^G Q, (e^{G_63-G} K)^T and L for all
 // (chunk, head) pairs at once (the triangular solve is a forward substitution,
 // one column per thread); rule_chunk_scan_kernel then walks the chunks in
-// order, one block per (head, 32-column slice of S) with the slice in LDS.
+// order, one block per (head, 16-column slice of S) with the slice in LDS.
 // Tokens past the end of the last chunk are zero with g = 0 and beta = 0,
 // which leaves D, O and S unchanged. G is summed in double so that
 // G_t - G_s keeps its precision when G itself is large.
@@ -26,51 +26,37 @@ namespace {
 
 constexpr int kC = 64;     // tokens per chunk
 constexpr int kD = 128;    // key_dim == value_dim
-constexpr int kSlice = 32; // value columns per scan block
+constexpr int kSlice = 16; // value columns per scan block
 constexpr int kSlices = kD / kSlice;
 // One (chunk, head) record, in floats: -W, U, e^G Q, (e^{G_63-G} K)^T, L, e^{G_63}.
 constexpr int kW = 0, kU = kW + kC * kD, kQ = kU + kC * kD, kK = kQ + kC * kD, kL = kK + kD * kC,
               kG = kL + kC * kC, kRec = kG + 64;
 constexpr int kGroupChunks = 64;  // chunks per prep + scan pair
 
-typedef float f16v __attribute__((ext_vector_type(16)));
 typedef float f4v __attribute__((ext_vector_type(4)));
 
-// A operand order of v_mfma_f32_32x32x2_f32 for a (32 x tiles) x (2 KH)
-// matrix: in row tile `tile`, lane l feeds row l % 32 from the k-half l / 32,
-// and step kk of the product uses k = (l / 32) KH + kk. float4 m of every
-// lane (kk = 4m .. 4m+3) is stored as one contiguous 1 KiB run per wave.
-template <int KH>
-__device__ __forceinline__ int a_slot(int row, int k) {
-    const int tile = row >> 5, l = (k / KH) * 32 + (row & 31), kk = k % KH;
-    return tile * 64 * KH + (kk >> 2) * 256 + l * 4 + (kk & 3);
-}
-// Accumulator order of a 64 x 128 matrix in 32 x 32 tiles (row tile, column
-// slice): register r of lane l holds row 8 (r / 4) + 4 (l / 32) + r % 4 and
-// column l % 32; registers 4q .. 4q+3 of every lane are one 1 KiB run.
-__device__ __forceinline__ int d_slot(int row, int col) {
-    const int tile = row >> 5, lr = row & 31, q = lr >> 3, hl = (lr >> 2) & 1, e = lr & 3;
-    const int js = col >> 5, l = hl * 32 + (col & 31);
-    return ((tile * kSlices + js) * 4 + q) * 256 + l * 4 + e;
-}
-// Row of accumulator register r in lane half hl.
-__device__ __forceinline__ int d_row(int r, int hl) { return 8 * (r >> 2) + 4 * hl + (r & 3); }
-
-// LDS slots of the S slice (128 x 32) and of the D slice (64 x 32): the upper
-// k-half is shifted by 32 banks, so the two lane halves of a B-operand read
-// (rows kk and kk + KH) never meet in a bank.
-__device__ __forceinline__ int s_lds(int row, int col) { return row * kSlice + col + (row >> 6) * kSlice; }
-__device__ __forceinline__ int d_lds(int row, int col) { return row * kSlice + col + (row >> 5) * kSlice; }
+// Record layouts, for v_mfma_f32_16x16x4_f32 (lane l: A[i = l % 16][k = l / 16],
+// B[k = l / 16][j = l % 16], accumulator register r: row 4 (l / 16) + r,
+// column l % 16). Step s of a product over K uses k = 4 s + (l / 16), so the
+// B rows a step reads are 4 consecutive rows (conflict-free in a [rows][16]
+// LDS array).
+// A operand of a (16 x tiles) x K matrix: float4 m of lane l in row tile
+// `tile` holds row 16 tile + l % 16 at k = 16 m + l / 16 + 4 e (e = 0..3),
+// every lane's float4 m one contiguous 1 KiB run. f4 index of (tile, m, l):
+// tile * K + m * 64 + l.
+// U in accumulator order: f4 (tile, js, l) holds rows 16 tile + 4 (l / 16) + e
+// of column 16 js + l % 16; f4 index (tile * kSlices + js) * 64 + l.
 
 __global__ __launch_bounds__(256) void rule_chunk_prep_kernel(Params a, int gated, int c0, float* scratch) {
     __shared__ float ks[kC][kD + 1], qs[kC][kD + 1];
-    __shared__ float am[kC][kC + 4];
+    __shared__ float am[kC][kC + 4], lm[kC][kC + 4];
     __shared__ double gd[kC];
     __shared__ float bs[kC], eg[kC], el[kC];
     const int tid = threadIdx.x, h = blockIdx.y, c = c0 + int(blockIdx.x);
     const int kh = a.n[2], vh = a.n[3], tokens = a.n[4] > 0 ? a.n[4] : 1, stride = a.n[5];
     const int t0 = c * kC, n = min(kC, tokens - t0);
     float* rec = scratch + (size_t(blockIdx.x) * vh + h) * kRec;
+    f4v* rec4 = reinterpret_cast<f4v*>(rec);
     for (int e = tid; e < kC * kD; e += 256) {
         const int r = e / kD, i = e % kD;
         const size_t off = size_t(t0 + r) * vh * kD + size_t(h) * kD + i;
@@ -128,14 +114,27 @@ __global__ __launch_bounds__(256) void rule_chunk_prep_kernel(Params a, int gate
                 const int t = tr + x, s = sc + y;
                 const float e = s <= t ? expf(float(gd[t] - gd[s])) : 0.f;
                 am[t][s] = s < t ? bs[t] * e * kk[x][y] : 0.f;
-                rec[kL + a_slot<32>(t, s)] = e * qk[x][y];
+                lm[t][s] = e * qk[x][y];
             }
     }
     __syncthreads();
-    for (int e = tid; e < kC * kD; e += 256) {
-        const int t = e / kD, i = e % kD;
-        rec[kQ + a_slot<64>(t, i)] = eg[t] * qs[t][i];
-        rec[kK + a_slot<32>(i, t)] = el[t] * ks[t][i];
+    // e^G Q, (e^{G_63-G} K)^T and L into the record, one float4 of the
+    // destination per thread step (contiguous stores)
+    for (int d = tid; d < kC * kD / 4; d += 256) {
+        const int l = d & 63, lr = l & 15, q = l >> 4;
+        {  // e^G Q: 4 tiles of 16 rows, K = 128 (8 float4 per lane)
+            const int tile = d >> 9, m = (d >> 6) & 7, t = tile * 16 + lr, k = 16 * m + q;
+            rec4[kQ / 4 + d] = f4v{qs[t][k], qs[t][k + 4], qs[t][k + 8], qs[t][k + 12]} * eg[t];
+        }
+        {  // (e^{G_63-G} K)^T: 8 tiles of 16 key dims, K = 64 tokens (4 float4 per lane)
+            const int tile = d >> 8, m = (d >> 6) & 3, i = tile * 16 + lr, t = 16 * m + q;
+            rec4[kK / 4 + d] = f4v{el[t] * ks[t][i], el[t + 4] * ks[t + 4][i], el[t + 8] * ks[t + 8][i],
+                                   el[t + 12] * ks[t + 12][i]};
+        }
+        if (d < kC * kC / 4) {  // L: 4 tiles of 16 tokens, K = 64 tokens
+            const int tile = d >> 8, m = (d >> 6) & 3, t = tile * 16 + lr, k = 16 * m + q;
+            rec4[kL / 4 + d] = f4v{lm[t][k], lm[t][k + 4], lm[t][k + 8], lm[t][k + 12]};
+        }
     }
     __syncthreads();
     // right-hand sides: beta e^G K in ks, beta V in qs
@@ -145,121 +144,126 @@ __global__ __launch_bounds__(256) void rule_chunk_prep_kernel(Params a, int gate
         qs[t][i] = t < n ? bs[t] * a.p[3][size_t(t0 + t) * stride + 2 * size_t(kh) * kD + size_t(h) * kD + i] : 0.f;
     }
     __syncthreads();
-    {  // forward substitution (I + A) X = B, one column per thread: W (threads 0..127), U (128..255)
+    {  // forward substitution (I + A) X = B, one column per thread: W (threads 0..127), U (128..255),
+       // two partial sums per row; the solution replaces its right-hand side in LDS
         const int col = tid & (kD - 1);
-        const float* rhs = tid < kD ? &ks[0][col] : &qs[0][col];
+        float* rhs = tid < kD ? &ks[0][col] : &qs[0][col];
         float x[kC];
 #pragma unroll
         for (int t = 0; t < kC; ++t) {
-            float r = rhs[t * (kD + 1)];
+            float r0 = rhs[t * (kD + 1)], r1 = 0.f;
 #pragma unroll
-            for (int s = 0; s < t; ++s) r = fmaf(-am[t][s], x[s], r);
-            x[t] = r;
+            for (int s = 0; s + 1 < t; s += 2) {
+                r0 = fmaf(-am[t][s], x[s], r0);
+                r1 = fmaf(-am[t][s + 1], x[s + 1], r1);
+            }
+            if (t & 1) r0 = fmaf(-am[t][t - 1], x[t - 1], r0);
+            x[t] = r0 + r1;
             asm volatile("" ::: "memory");  // keep each row's LDS reads with its row
         }
-        if (tid < kD) {
 #pragma unroll
-            for (int t = 0; t < kC; ++t) rec[kW + a_slot<64>(t, col)] = -x[t];
-        } else {
-#pragma unroll
-            for (int t = 0; t < kC; ++t) rec[kU + d_slot(t, col)] = x[t];
+        for (int t = 0; t < kC; ++t) rhs[t * (kD + 1)] = x[t];
+    }
+    __syncthreads();
+    for (int d = tid; d < kC * kD / 4; d += 256) {
+        const int l = d & 63, lr = l & 15, q = l >> 4;
+        {  // -W, as e^G Q
+            const int tile = d >> 9, m = (d >> 6) & 7, t = tile * 16 + lr, k = 16 * m + q;
+            rec4[kW / 4 + d] = -f4v{ks[t][k], ks[t][k + 4], ks[t][k + 8], ks[t][k + 12]};
+        }
+        {  // U in accumulator order
+            const int js = (d >> 6) & (kSlices - 1), tile = d >> 9, t = tile * 16 + 4 * q, col = js * 16 + lr;
+            rec4[kU / 4 + d] = f4v{qs[t][col], qs[t + 1][col], qs[t + 2][col], qs[t + 3][col]};
         }
     }
     if (tid == 0) rec[kG] = eg[kC - 1];
 }
 
-__device__ __forceinline__ f16v mfma32(float x, float y, f16v acc) {
-    return __builtin_amdgcn_mfma_f32_32x32x2f32(x, y, acc, 0, 0, 0);
+__device__ __forceinline__ f4v mfma16(float x, float y, f4v acc) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(x, y, acc, 0, 0, 0);
 }
 
-// One block per (head, 32-column slice of S); waves 0, 1 own the D row tiles
-// and waves 2, 3 the O row tiles of a chunk, and wave w updates S rows
-// 32w .. 32w+31. Operands of the next chunk's first product are loaded while
-// the current chunk's second product runs.
+// One block per (head, 16-column slice of S), 4 waves. Wave w: rows 16w..16w+15
+// of D and of O (phase 1: D = U - W S0 and O = e^G Q S0, sharing every S0
+// read), then O += L D over the tokens up to its rows and S rows of tiles w
+// and w + 4 (phase 2: one D read feeds all three products). The next chunk's
+// phase-1 operands are loaded while phase 2 runs.
 __global__ __launch_bounds__(256) void rule_chunk_scan_kernel(Params a, int c0, int chunks, const float* scratch) {
-    __shared__ float sl[kD * kSlice + kSlice];
-    __shared__ float dl[kC * kSlice + kSlice];
+    __shared__ float sl[kD][kSlice];
+    __shared__ float dl[kC][kSlice];
     const int h = int(blockIdx.x) / kSlices, js = int(blockIdx.x) % kSlices;
-    const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, lc = l & 31, hl = l >> 5;
+    const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, lc = l & 15, q = l >> 4;
     const int vh = a.n[3], tokens = a.n[4] > 0 ? a.n[4] : 1;
     float* state = a.p[4] + size_t(h) * kD * kD + js * kSlice;
-    for (int e = tid; e < kD * kSlice; e += 256) {
-        const int r = e / kSlice, cc = e % kSlice;
-        sl[s_lds(r, cc)] = state[size_t(r) * kD + cc];
-    }
-    // phase-1 operands of chunk c: -W (waves 0, 1) or e^G Q (waves 2, 3) rows of
-    // tile w & 1, and U (waves 0, 1) in accumulator order
-    const int first = w < 2 ? kW : kQ;
-    auto load1 = [&](int c, f4v (&av)[16], f4v (&uv)[4]) {
+    for (int e = tid; e < kD * kSlice; e += 256) sl[e / kSlice][e % kSlice] = state[size_t(e / kSlice) * kD + e % kSlice];
+    auto load1 = [&](int c, f4v (&wv)[8], f4v (&qv)[8], f4v& uv) {
         const float* rec = scratch + (size_t(c) * vh + h) * kRec;
-        const f4v* A = reinterpret_cast<const f4v*>(rec + first + (w & 1) * 4096) + l;
+        const f4v* W = reinterpret_cast<const f4v*>(rec + kW) + w * 512 + l;
+        const f4v* Q = reinterpret_cast<const f4v*>(rec + kQ) + w * 512 + l;
 #pragma unroll
-        for (int m = 0; m < 16; ++m) av[m] = A[m * 64];
-        const f4v* U = reinterpret_cast<const f4v*>(rec + kU + ((w & 1) * kSlices + js) * 1024) + l;
-#pragma unroll
-        for (int q = 0; q < 4; ++q) uv[q] = w < 2 ? U[q * 64] : f4v{0.f, 0.f, 0.f, 0.f};
+        for (int m = 0; m < 8; ++m) {
+            wv[m] = W[m * 64];
+            qv[m] = Q[m * 64];
+        }
+        uv = reinterpret_cast<const f4v*>(rec + kU)[(w * kSlices + js) * 64 + l];
     };
-    f4v av[16], uv[4];
-    load1(0, av, uv);
+    f4v wv[8], qv[8], uv;
+    load1(0, wv, qv, uv);
     __syncthreads();
     for (int c = 0; c < chunks; ++c) {
         const float* rec = scratch + (size_t(c) * vh + h) * kRec;
         const int t0 = (c0 + c) * kC;
-        // phase-2 operands: L rows of tile w & 1 (waves 2, 3), (e^{G_63-G} K)^T rows of tile w
-        f4v lv[8], kv[8];
+        f4v lv[4], k0[4], k1[4];  // phase-2 operands: L rows of tile w, K^T rows of tiles w and w + 4
         {
-            const f4v* Lm = reinterpret_cast<const f4v*>(rec + kL + (w & 1) * 2048) + l;
-            const f4v* K = reinterpret_cast<const f4v*>(rec + kK + w * 2048) + l;
+            const f4v* Lp = reinterpret_cast<const f4v*>(rec + kL) + w * 256 + l;
+            const f4v* Kp = reinterpret_cast<const f4v*>(rec + kK) + l;
 #pragma unroll
-            for (int m = 0; m < 8; ++m) {
-                lv[m] = w >= 2 ? Lm[m * 64] : f4v{0.f, 0.f, 0.f, 0.f};
-                kv[m] = K[m * 64];
+            for (int m = 0; m < 4; ++m) {
+                lv[m] = Lp[m * 64];
+                k0[m] = Kp[w * 256 + m * 64];
+                k1[m] = Kp[(w + 4) * 256 + m * 64];
             }
         }
         const float decay = rec[kG];
-        // phase 1: D = U - W S0 (waves 0, 1) or O = e^G Q S0 (waves 2, 3)
-        f16v acc;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) acc[r] = uv[r >> 2][r & 3];
-#pragma unroll
-        for (int m = 0; m < 16; ++m)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) acc = mfma32(av[m][e], sl[s_lds(hl * 64 + 4 * m + e, lc)], acc);
-        const int R = (w & 1) * 32;
-        if (w < 2) {
-#pragma unroll
-            for (int r = 0; r < 16; ++r) dl[d_lds(R + d_row(r, hl), lc)] = acc[r];
-        }
-        __syncthreads();
-        if (c + 1 < chunks) load1(c + 1, av, uv);
-        // phase 2: O += L D (waves 2, 3); S rows 32w.. = e^{G_63} S0 + (e^{G_63-G} K)^T D
-        if (w >= 2) {
-#pragma unroll
-            for (int m = 0; m < 8; ++m)
-#pragma unroll
-                for (int e = 0; e < 4; ++e) acc = mfma32(lv[m][e], dl[d_lds(hl * 32 + 4 * m + e, lc)], acc);
-            float* out = a.p[0] + size_t(h) * kD + js * kSlice + lc;
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int t = t0 + R + d_row(r, hl);
-                if (t < tokens) out[size_t(t) * vh * kD] = acc[r];
-            }
-        }
-        f16v sacc;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) sacc[r] = decay * sl[s_lds(32 * w + d_row(r, hl), lc)];
+        f4v dacc = uv, oacc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int m = 0; m < 8; ++m)
 #pragma unroll
-            for (int e = 0; e < 4; ++e) sacc = mfma32(kv[m][e], dl[d_lds(hl * 32 + 4 * m + e, lc)], sacc);
+            for (int e = 0; e < 4; ++e) {
+                const float b = sl[16 * m + 4 * e + q][lc];  // k = 4 (4m + e) + q
+                dacc = mfma16(wv[m][e], b, dacc);
+                oacc = mfma16(qv[m][e], b, oacc);
+            }
 #pragma unroll
-        for (int r = 0; r < 16; ++r) sl[s_lds(32 * w + d_row(r, hl), lc)] = sacc[r];
+        for (int r = 0; r < 4; ++r) dl[16 * w + 4 * q + r][lc] = dacc[r];
+        __syncthreads();
+        if (c + 1 < chunks) load1(c + 1, wv, qv, uv);
+        f4v s0, s1;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            s0[r] = decay * sl[16 * w + 4 * q + r][lc];
+            s1[r] = decay * sl[16 * (w + 4) + 4 * q + r][lc];
+        }
+#pragma unroll
+        for (int m = 0; m < 4; ++m)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float b = dl[16 * m + 4 * e + q][lc];
+                if (m <= w) oacc = mfma16(lv[m][e], b, oacc);  // L is zero past the tile's last token
+                s0 = mfma16(k0[m][e], b, s0);
+                s1 = mfma16(k1[m][e], b, s1);
+            }
+        float* out = a.p[0] + size_t(h) * kD + js * kSlice + lc;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int t = t0 + 16 * w + 4 * q + r;
+            if (t < tokens) out[size_t(t) * vh * kD] = oacc[r];
+            sl[16 * w + 4 * q + r][lc] = s0[r];
+            sl[16 * (w + 4) + 4 * q + r][lc] = s1[r];
+        }
         __syncthreads();
     }
-    for (int e = tid; e < kD * kSlice; e += 256) {
-        const int r = e / kSlice, cc = e % kSlice;
-        state[size_t(r) * kD + cc] = sl[s_lds(r, cc)];
-    }
+    for (int e = tid; e < kD * kSlice; e += 256) state[size_t(e / kSlice) * kD + e % kSlice] = sl[e / kSlice][e % kSlice];
 }
 
 }  // namespace
