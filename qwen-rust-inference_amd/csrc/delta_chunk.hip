@@ -48,7 +48,9 @@ typedef float f4v __attribute__((ext_vector_type(4)));
 // of column 16 js + l % 16; f4 index (tile * kSlices + js) * 64 + l.
 
 __global__ __launch_bounds__(256) void rule_chunk_prep_kernel(Params a, int gated, int c0, float* scratch) {
-    __shared__ float ks[kC][kD + 1], qs[kC][kD + 1];
+    // row stride 132 (4 mod 64 banks): the Gram products' MFMA operand reads
+    // (16 rows x 4 interleaved k per step) hit 64 distinct banks
+    __shared__ float ks[kC][kD + 4], qs[kC][kD + 4];
     __shared__ float am[kC][kC + 4], lm[kC][kC + 4];
     __shared__ double gd[kC];
     __shared__ float bs[kC], eg[kC], el[kC];
@@ -57,11 +59,22 @@ __global__ __launch_bounds__(256) void rule_chunk_prep_kernel(Params a, int gate
     const int t0 = c * kC, n = min(kC, tokens - t0);
     float* rec = scratch + (size_t(blockIdx.x) * vh + h) * kRec;
     f4v* rec4 = reinterpret_cast<f4v*>(rec);
-    for (int e = tid; e < kC * kD; e += 256) {
-        const int r = e / kD, i = e % kD;
-        const size_t off = size_t(t0 + r) * vh * kD + size_t(h) * kD + i;
-        ks[r][i] = r < n ? a.p[2][off] : 0.f;
-        qs[r][i] = r < n ? a.p[1][off] : 0.f;
+    {  // q and k rows: every thread's 8 + 8 float4 loads in flight together
+        f4v kv[8], qv[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int e = tid + 256 * j, r = e >> 5, i = (e & 31) * 4;
+            const size_t off = size_t(t0 + r) * vh * kD + size_t(h) * kD + i;
+            const f4v z = {0.f, 0.f, 0.f, 0.f};
+            kv[j] = r < n ? *reinterpret_cast<const f4v*>(a.p[2] + off) : z;
+            qv[j] = r < n ? *reinterpret_cast<const f4v*>(a.p[1] + off) : z;
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int e = tid + 256 * j, r = e >> 5, i = (e & 31) * 4;
+            *reinterpret_cast<f4v*>(&ks[r][i]) = kv[j];
+            *reinterpret_cast<f4v*>(&qs[r][i]) = qv[j];
+        }
     }
     if (tid < kC) {  // wave 0: gates and the inclusive prefix of g
         float g = 0.f, b = 0.f;
@@ -88,34 +101,34 @@ __global__ __launch_bounds__(256) void rule_chunk_prep_kernel(Params a, int gate
         el[tid] = expf(float(last - G));
     }
     __syncthreads();
-    {  // Gram products: a 4 x 4 block of K K^T and Q K^T per thread
-        const int tr = (tid >> 4) * 4, sc = (tid & 15) * 4;
-        float kk[4][4] = {}, qk[4][4] = {};
-        for (int i = 0; i < kD; ++i) {
-            float kt[4], qt[4], kc[4];
-#pragma unroll
-            for (int x = 0; x < 4; ++x) {
-                kt[x] = ks[tr + x][i];
-                qt[x] = qs[tr + x][i];
-                kc[x] = ks[sc + x][i];
-            }
-#pragma unroll
-            for (int x = 0; x < 4; ++x)
-#pragma unroll
-                for (int y = 0; y < 4; ++y) {
-                    kk[x][y] = fmaf(kt[x], kc[y], kk[x][y]);
-                    qk[x][y] = fmaf(qt[x], kc[y], qk[x][y]);
-                }
+    {  // Gram products K K^T and Q K^T on MFMA, the 10 lower 16 x 16 tiles (sj <= ti);
+       // a tile's two products share the B operand (rows of K)
+        const int w = tid >> 6, l = tid & 63, lc = l & 15, q = l >> 4;
+        for (int e = tid; e < 6 * 256; e += 256) {  // the upper tiles are zero
+            const int tile = e >> 8, ti = tile < 3 ? 0 : tile < 5 ? 1 : 2, sj = tile < 3 ? tile + 1 : tile < 5 ? tile - 1 : 3;
+            const int t = 16 * ti + ((e >> 4) & 15), s2 = 16 * sj + (e & 15);
+            am[t][s2] = 0.f;
+            lm[t][s2] = 0.f;
         }
-#pragma unroll
-        for (int x = 0; x < 4; ++x)
-#pragma unroll
-            for (int y = 0; y < 4; ++y) {
-                const int t = tr + x, s = sc + y;
-                const float e = s <= t ? expf(float(gd[t] - gd[s])) : 0.f;
-                am[t][s] = s < t ? bs[t] * e * kk[x][y] : 0.f;
-                lm[t][s] = e * qk[x][y];
+        // wave w: tiles w, w + 4, w + 8 of the list (ti, sj) = (0,0) (1,0) (1,1) (2,0) ... (3,3)
+        for (int j = w; j < 10; j += 4) {
+            const int ti = j < 1 ? 0 : j < 3 ? 1 : j < 6 ? 2 : 3, sj = j - ti * (ti + 1) / 2;
+            f4v kk = {0.f, 0.f, 0.f, 0.f}, qk = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll 8
+            for (int st = 0; st < kD / 4; ++st) {
+                const int k = 4 * st + q;
+                const float b = ks[16 * sj + lc][k];
+                kk = __builtin_amdgcn_mfma_f32_16x16x4f32(ks[16 * ti + lc][k], b, kk, 0, 0, 0);
+                qk = __builtin_amdgcn_mfma_f32_16x16x4f32(qs[16 * ti + lc][k], b, qk, 0, 0, 0);
             }
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int t = 16 * ti + 4 * q + r, s2 = 16 * sj + lc;
+                const float e = s2 <= t ? expf(float(gd[t] - gd[s2])) : 0.f;
+                am[t][s2] = s2 < t ? bs[t] * e * kk[r] : 0.f;
+                lm[t][s2] = e * qk[r];
+            }
+        }
     }
     __syncthreads();
     // e^G Q, (e^{G_63-G} K)^T and L into the record, one float4 of the
@@ -137,21 +150,34 @@ __global__ __launch_bounds__(256) void rule_chunk_prep_kernel(Params a, int gate
         }
     }
     __syncthreads();
-    // right-hand sides: beta e^G K in ks, beta V in qs
-    for (int e = tid; e < kC * kD; e += 256) {
-        const int t = e / kD, i = e % kD;
-        ks[t][i] *= bs[t] * eg[t];
-        qs[t][i] = t < n ? bs[t] * a.p[3][size_t(t0 + t) * stride + 2 * size_t(kh) * kD + size_t(h) * kD + i] : 0.f;
+    {  // right-hand sides: beta e^G K in ks, beta V in qs (the V loads all in flight together)
+        f4v vv[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int e = tid + 256 * j, t = e >> 5, i = (e & 31) * 4;
+            const f4v z = {0.f, 0.f, 0.f, 0.f};
+            vv[j] = t < n ? *reinterpret_cast<const f4v*>(a.p[3] + size_t(t0 + t) * stride + 2 * size_t(kh) * kD +
+                                                          size_t(h) * kD + i)
+                          : z;
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int e = tid + 256 * j, t = e >> 5, i = (e & 31) * 4;
+            f4v* kr = reinterpret_cast<f4v*>(&ks[t][i]);
+            *kr = *kr * (bs[t] * eg[t]);
+            *reinterpret_cast<f4v*>(&qs[t][i]) = vv[j] * bs[t];
+        }
     }
     __syncthreads();
     {  // forward substitution (I + A) X = B, one column per thread: W (threads 0..127), U (128..255),
        // two partial sums per row; the solution replaces its right-hand side in LDS
         const int col = tid & (kD - 1);
         float* rhs = tid < kD ? &ks[0][col] : &qs[0][col];
+        constexpr int RS = kD + 4;  // row stride of ks / qs
         float x[kC];
 #pragma unroll
         for (int t = 0; t < kC; ++t) {
-            float r0 = rhs[t * (kD + 1)], r1 = 0.f;
+            float r0 = rhs[t * RS], r1 = 0.f;
 #pragma unroll
             for (int s = 0; s + 1 < t; s += 2) {
                 r0 = fmaf(-am[t][s], x[s], r0);
@@ -162,7 +188,7 @@ __global__ __launch_bounds__(256) void rule_chunk_prep_kernel(Params a, int gate
             asm volatile("" ::: "memory");  // keep each row's LDS reads with its row
         }
 #pragma unroll
-        for (int t = 0; t < kC; ++t) rhs[t * (kD + 1)] = x[t];
+        for (int t = 0; t < kC; ++t) rhs[t * RS] = x[t];
     }
     __syncthreads();
     for (int d = tid; d < kC * kD / 4; d += 256) {
@@ -270,8 +296,10 @@ __global__ __launch_bounds__(256) void rule_chunk_scan_kernel(Params a, int c0, 
 
 bool delta_rule_chunked_ok(const Params& a, int count) {
     const int tokens = a.n[4] > 0 ? a.n[4] : 1;
+    const uintptr_t vec = reinterpret_cast<uintptr_t>(a.p[1]) | reinterpret_cast<uintptr_t>(a.p[2]) |
+                          reinterpret_cast<uintptr_t>(a.p[3]);  // float4 loads of q, k, v rows
     return a.n[0] == kD && a.n[1] == kD && a.n[3] >= 1 && count == a.n[3] * kD && a.n[6] <= 0 &&
-           tokens >= kChunkMinTokens;
+           tokens >= kChunkMinTokens && vec % 16 == 0 && a.n[5] % 4 == 0 && a.n[2] >= 0;
 }
 
 size_t delta_rule_chunked_scratch(const Params& a) {
