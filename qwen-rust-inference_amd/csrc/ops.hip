@@ -127,6 +127,38 @@ __global__ __launch_bounds__(256) void conv_silu_tokens_kernel(int count, Params
         for (int i = 0; i < k - 1; ++i)
             a.p[3][size_t(r + 1) * size_t(stride) * size_t(k - 1) + size_t(ch) * (k - 1) + i] = input(r - (k - 2) + i);
 }
+// The same for kernel size K, CT tokens per thread: the window of the CT
+// tokens' inputs (plus the K - 1 before them) is loaded once, all loads in
+// flight together, and slid in registers.
+template <int K, int CT>
+__global__ __launch_bounds__(256) void conv_silu_window_kernel(int count, Params a) {
+    const int ch = blockIdx.x * blockDim.x + threadIdx.x, r0 = int(blockIdx.y) * CT;
+    if (ch >= count) return;
+    const int tokens = a.n[1], stride = a.n[2], snaps = a.n[3];
+    float w[K], win[CT + K - 1];
+#pragma unroll
+    for (int i = 0; i < K; ++i) w[i] = a.p[2][size_t(ch) * K + i];
+    const float* hist = a.p[3] + size_t(ch) * (K - 1);
+#pragma unroll
+    for (int i = 0; i < CT + K - 1; ++i) {
+        const int j = r0 - (K - 1) + i;
+        win[i] = j < 0 ? hist[K - 1 + j] : j < tokens ? a.p[1][size_t(j) * stride + ch] : 0.f;
+    }
+#pragma unroll
+    for (int c = 0; c < CT; ++c) {
+        const int r = r0 + c;
+        if (r >= tokens) break;
+        float sum = 0.f;
+#pragma unroll
+        for (int i = 0; i < K - 1; ++i) sum += win[c + i] * w[i];
+        sum += win[c + K - 1] * w[K - 1];
+        a.p[0][size_t(r) * stride + ch] = siluf_(sum);
+        if (r < snaps)
+#pragma unroll
+            for (int i = 0; i < K - 1; ++i)
+                a.p[3][size_t(r + 1) * size_t(stride) * (K - 1) + size_t(ch) * (K - 1) + i] = win[c + 1 + i];
+    }
+}
 __global__ __launch_bounds__(256) void conv_history_kernel(int count, Params a) {
     const int ch = blockIdx.x * blockDim.x + threadIdx.x;
     if (ch >= count) return;
@@ -443,7 +475,12 @@ int run_conv_silu(hipStream_t s, int count, const Params& a) {
         hipLaunchKernelGGL(conv_silu_kernel, dim3(ceil_div(count, 256)), dim3(256), 0, s, count, a);
         return int(hipGetLastError());
     }
-    hipLaunchKernelGGL(conv_silu_tokens_kernel, dim3(ceil_div(count, 256), unsigned(tokens)), dim3(256), 0, s, count, a);
+    if (a.n[0] == 4)
+        hipLaunchKernelGGL((conv_silu_window_kernel<4, 16>), dim3(ceil_div(count, 256), ceil_div(tokens, 16)), dim3(256),
+                           0, s, count, a);
+    else
+        hipLaunchKernelGGL(conv_silu_tokens_kernel, dim3(ceil_div(count, 256), unsigned(tokens)), dim3(256), 0, s, count,
+                           a);
     if (hipError_t e = hipGetLastError()) return int(e);
     hipLaunchKernelGGL(conv_history_kernel, dim3(ceil_div(count, 256)), dim3(256), 0, s, count, a);
     return int(hipGetLastError());

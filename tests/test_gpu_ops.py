@@ -316,7 +316,7 @@ def test_embed_rows(gpu, width, n):
 
 
 @pytest.mark.parametrize("k,tokens,snaps", [(4, 1, 0), (4, 5, 0), (4, 4, 3), (3, 2, 1), (1, 1, 0),
-                                             (4, 37, 5), (4, 130, 0), (3, 9, 8), (1, 7, 2), (17, 6, 2)])
+                                             (4, 37, 5), (4, 130, 0), (3, 9, 8), (1, 7, 2), (17, 6, 2), (4, 33, 33)])
 def test_conv_silu(gpu, cpu, k, tokens, snaps):
     rng = np.random.default_rng(k * 10 + tokens)
     ch = 6144 if k == 4 else 24
