@@ -22,6 +22,9 @@ namespace {
 typedef float f16v __attribute__((ext_vector_type(16)));
 typedef float f4v __attribute__((ext_vector_type(4)));
 
+// LDS rows of 132 floats: the two lane halves of an MFMA operand read take
+// rows k and k + 8 (8 * 132 = 32 banks apart), and the four k-quads a wave
+// stores land 16 banks apart, so neither side has bank conflicts.
 constexpr int MM = 128, MN = 128, MK = 16, MPAD = 4;
 
 // One 16-deep K step of two 64-row blocks into registers: thread t loads row
@@ -95,8 +98,8 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(float* y, const float* a
             mfma_load(a, n0, wbot, wbot_r0, rows, cols, k0 + MK, kend, wv);
         }
 #pragma unroll
-        for (int kk = 0; kk < MK; kk += 2) {
-            const int k = kk + (lane >> 5);  // A[i = lane % 32][k], B[k][j = lane % 32]
+        for (int kk = 0; kk < MK / 2; ++kk) {
+            const int k = kk + (MK / 2) * (lane >> 5);  // A[i = lane % 32][k], B[k][j = lane % 32]
             float av[2], bv[2];
 #pragma unroll
             for (int i = 0; i < 2; ++i) av[i] = xs[buf][k][wm + 32 * i + (lane & 31)];
