@@ -98,6 +98,8 @@ def main():
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="also run one device copy of MIB MiB (a plain copy kernel of known size, the scale "
                          "for rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")
+    ap.add_argument("--only-prefill", type=int, default=0, metavar="N",
+                    help="profiling mode: only two N-token prefills (one chunk, fresh runs) and a one-line summary")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
@@ -120,6 +122,20 @@ def main():
     log(model.info)
     model.set_run_budget(64 << 30)
     weight_bytes = w.matrix_bytes()
+    if args.only_prefill > 0:
+        n = args.only_prefill
+        ids2 = [int(v) for v in np.random.default_rng(2).integers(0, c.vocab_size, n)]
+        times = []
+        for rep in range(2):
+            r2 = model.new_run(n + 1, chunk=n)
+            model.sync()
+            t = time.perf_counter()
+            r2.prefill(ids2)
+            times.append(time.perf_counter() - t)
+            del r2
+        print(json.dumps({"mode": "only-prefill", "tokens": n, "prefill_ms": [round(x * 1e3, 2) for x in times]}),
+              flush=True)
+        return
     prompt = [int(v) for v in np.random.default_rng(4).integers(0, c.vocab_size, args.prompt)]
 
     # prefill of the prompt (one chunk), then decode
