@@ -11,7 +11,8 @@ stream synchronisation on both sides. value = decode tokens/s at ctx 454.
 Also reported: weight-read HBM GB/s of the decode step; the prefill rate of
 the prompt; the 2644- and 10,240-token prefills (config 3: median of timed
 runs, tok/s and FLOP rate against the fp32 MFMA peak; --no-prefill skips);
-decode at ctx 8192 (config 4; --no-long skips). roofline: the one-launch decode kernel
+decode at ctx 8192 (config 4; --no-long skips); int8 decode at ctx 454 and
+a 4-row verify with snapshots (config 5; --no-int8 skips). roofline: the one-launch decode kernel
 (decode_kernel: every layer, lm_head and argmax of a step), timed with a
 hipEvent pair around each launch on the bridge's stream in a profiled pass of
 the same decode; achieved = the step's algorithmic HBM bytes (every matrix
@@ -93,6 +94,8 @@ def main():
     ap.add_argument("--no-prefill", dest="prefill", action="store_false",
                     help="skip the 2644- and 10,240-token prefills (config 3)")
     ap.add_argument("--no-long", dest="long", action="store_false", help="skip decode at ctx 8192 (config 4)")
+    ap.add_argument("--no-int8", dest="int8", action="store_false",
+                    help="skip the int8 decode and 4-row verify at ctx 454 (config 5)")
     ap.add_argument("--cpu-steps", type=int, default=6, help="oracle steps of the CPU baseline sample (0: skip)")
     ap.add_argument("--profile-steps", type=int, default=16)
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
@@ -256,6 +259,42 @@ def main():
         out["decode_8192_hbm_frac"] = round(long_bytes * 64 / dt / 1e9 / HBM_PEAK_GBS, 4)
         log(f"decode @8192: {dt / 64 * 1e3:.3f} ms/token, {long_bytes * 64 / dt / 1e9:.0f} GB/s algorithmic")
         del r3
+
+    if args.int8:
+        # Config 5: int8 per-row weights (quantised on the host by the engine, as the
+        # reference's upload_int8), decode at ctx 454 on the op path and a 4-row
+        # verify with per-row DeltaNet snapshots (verify_rollback_greedy + accept).
+        specs = [sp for sp in M.tensor_specs(c) if sp.kind == "matrix"]
+        int8_bytes = sum(sp.shape[0] * sp.shape[1] + 4 * sp.shape[0] for sp in specs)
+        m8 = E.Model(w, fmt=E.INT8)
+        m8.set_run_budget(64 << 30)
+        r8 = m8.new_run(args.prompt + 160, chunk=args.prompt, snapshots=3)
+        tok = int(np.argmax(r8.prefill(prompt)))
+        for _ in range(2):
+            tok = r8.step_greedy(tok)
+        m8.sync()
+        t = time.perf_counter()
+        ids8, _ = r8.decode_greedy(tok, 65)
+        dt = time.perf_counter() - t
+        out["int8_decode_454_tok_s"] = round(64 / dt, 2)
+        out["int8_weight_bytes_per_token"] = int8_bytes
+        out["int8_hbm_weight_read_frac"] = round(int8_bytes * 64 / dt / 1e9 / HBM_PEAK_GBS, 4)
+        log(f"int8 decode @454: {dt / 64 * 1e3:.3f} ms/token, {int8_bytes * 64 / dt / 1e9:.0f} GB/s of int8 weights")
+        tok = ids8[-1]
+        draft = [int(v) for v in np.random.default_rng(6).integers(0, c.vocab_size, 4)]
+        r8.verify_rollback_greedy(draft)
+        r8.accept(1)
+        m8.sync()
+        reps = 16
+        t = time.perf_counter()
+        for _ in range(reps):
+            r8.verify_rollback_greedy(draft)
+            r8.accept(1)
+        m8.sync()
+        dt = (time.perf_counter() - t) / reps
+        out["int8_verify4_ms"] = round(dt * 1e3, 3)
+        log(f"int8 4-row verify with snapshots + accept(1): {dt * 1e3:.3f} ms")
+        del r8, m8
 
     if args.copy_calibration > 0:
         from qwen_mi355x.bridge import Bridge
