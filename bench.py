@@ -34,6 +34,9 @@ for p in (str(ROOT / "qwen-rust-inference_amd"), str(ROOT / "oracle")):
         sys.path.insert(0, p)
 
 HBM_PEAK_GBS = 8000.0
+# HBM bytes per decode_kernel launch at ctx ~590 from the rocprofv3 FETCH_SIZE / WRITE_SIZE passes
+# (calibrated on a 512 MiB copy; profiles/decode_kernel_config2.md).
+DECODE_TRAFFIC_BYTES = 3_164_000_000
 MFMA_F32_PEAK_TFLOPS = 157.3
 METRIC = "decode tok/s @ctx 454 & 8192 + HBM GB/s; prefill tok/s @2644"
 
@@ -178,7 +181,7 @@ def main():
         bytes_total = sum(step_bytes(c, weight_bytes, p + 1) for p in range(pos0, pos0 + calls))
         achieved = bytes_total / (step_ms / 1e3) / 1e9
         roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                    "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                    "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": DECODE_TRAFFIC_BYTES,
                     "kernel": "decode_kernel (one-launch decode step: 24 layers, lm_head, argmax)",
                     "bytes_per_launch": bytes_total // calls, "launch_us": round(step_ms / calls * 1e3, 2),
                     "launches": calls, "context": [pos0 + 1, pos0 + calls],
