@@ -265,8 +265,9 @@ def main():
 
     if args.int8:
         # Config 5: int8 per-row weights (quantised on the host by the engine, as the
-        # reference's upload_int8), decode at ctx 454 on the op path and a 4-row
-        # verify with per-row DeltaNet snapshots (verify_rollback_greedy + accept).
+        # reference's upload_int8), decode at ctx 454 (the one-launch step when the
+        # bridge accepts the int8 plan, else the op sequence) and a 4-row verify
+        # with per-row DeltaNet snapshots (verify_rollback_greedy + accept).
         specs = [sp for sp in M.tensor_specs(c) if sp.kind == "matrix"]
         int8_bytes = sum(sp.shape[0] * sp.shape[1] + 4 * sp.shape[0] for sp in specs)
         m8 = E.Model(w, fmt=E.INT8)
@@ -280,6 +281,7 @@ def main():
         ids8, _ = r8.decode_greedy(tok, 65)
         dt = time.perf_counter() - t
         out["int8_decode_454_tok_s"] = round(64 / dt, 2)
+        out["int8_decode_one_launch"] = bool(r8.decode_plan)
         out["int8_weight_bytes_per_token"] = int8_bytes
         out["int8_hbm_weight_read_frac"] = round(int8_bytes * 64 / dt / 1e9 / HBM_PEAK_GBS, 4)
         log(f"int8 decode @454: {dt / 64 * 1e3:.3f} ms/token, {int8_bytes * 64 / dt / 1e9:.0f} GB/s of int8 weights")

@@ -146,9 +146,9 @@ int qr_gemm_f32_add_norm(Context* c, float* y, const float* a, const float* x, i
 
 /* One decode token in one launch (no counterpart in the reference's ABI; the
  * engine calls it from `forward` when t == 1, nothing is captured, the
- * matrices are fp32 and the bridge accepted the plan, instead of the op
- * sequence of src/device.rs:1740-2378, which it computes identically up to
- * fp32 summation order). The plan registers every weight, state and output
+ * matrices are all fp32 or all int8 and the bridge accepted the plan, instead
+ * of the op sequence of src/device.rs:1740-2378, which it computes identically
+ * up to fp32 summation order). The plan registers every weight, state and output
  * buffer of one run once; each step embeds `token`, runs all layers at
  * `position` (appending K/V there and advancing the DeltaNet states), writes
  * the vocabulary logits to `logits` and [argmax index, non-finite count] to
@@ -176,7 +176,13 @@ typedef struct QrDecodeDesc {
     float* logits;           /* [vocab] */
     float* picks;            /* [2] */
     const QrDecodeLayer* layer;
+    /* Matrix format of every layer matrix and of lm_head: QR_DECODE_F32 or
+     * QR_DECODE_INT8 (the reference's upload_int8 packing, src/device.rs:550-561:
+     * rows fp32 scales, then the int8 values row-major, four to a word). */
+    int32_t weights;
+    int32_t embedding_bf16;  /* embedding is packed BF16 (element 2i in the low half of word i) */
 } QrDecodeDesc;
+enum { QR_DECODE_F32 = 0, QR_DECODE_INT8 = 2 };
 typedef struct QrDecodePlan QrDecodePlan;
 /* Non-zero (with qr_error set) when this bridge has no one-launch decode for the shape. */
 int qr_decode_plan(Context* c, const QrDecodeDesc* d, QrDecodePlan** out);

@@ -96,6 +96,7 @@ struct Args {
     float* picks;
     Scratch* s;
     int token, pos, vocab, nphases;
+    int emb_bf16;  // the embedding table is packed BF16 (two per word, element 2i low)
     unsigned epoch;
     float eps;
     float rope_cs[ROT / 2], rope_sn[ROT / 2];  // cos / sin of pos / theta^(2i / rot)
@@ -281,55 +282,115 @@ __device__ __forceinline__ void stage_norm(const float* w, int par, Lds& l) {
     if (t < H / 4) *reinterpret_cast<f4*>(&l.nw[par][4 * t]) = f4(1.f) + ldp4(rsrc(w), 16u * unsigned(t), 0);
 }
 // The layer's input residual into l.act[par]: the token's embedding row for
-// layer 0, else x as written by phase `producer`.
+// layer 0 (BF16 tables only with int8 matrices, as the reference's int8
+// upload keeps the embedding BF16), else x as written by phase `producer`.
+template <bool Q8>
 __device__ __forceinline__ void stage_input(const Args& a, Rs rs, int L, int producer, int par, Lds& l, int p) {
     if (L == 0) {
         const int t = int(threadIdx.x);
-        if (t < H / 4)
+        if (Q8 && a.emb_bf16) {
+            if (t < H / 8) {
+                const f4 wv = ldp4(rsrc(a.embedding), unsigned(a.token) * unsigned(H * 2) + 16u * unsigned(t), 0);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const unsigned w = __float_as_uint(wv[j]);
+                    l.act[par][8 * t + 2 * j] = __uint_as_float(w << 16);
+                    l.act[par][8 * t + 2 * j + 1] = __uint_as_float(w & 0xffff0000u);
+                }
+            }
+        } else if (t < H / 4) {
             *reinterpret_cast<f4*>(&l.act[par][4 * t]) =
                 ldp4(rsrc(a.embedding), unsigned(a.token) * unsigned(H * 4) + 16u * unsigned(t), 0);
+        }
     } else {
         stage_tagged<H>(a, rs, SOFF(x), tag(a, producer), l.act[par], l, p);
     }
 }
+template <bool Q8>
 __device__ __forceinline__ float input_at(const Args& a, Rs rs, int L, int producer, int i, Lds& l, int p) {
-    if (L == 0) return ldp(rsrc(a.embedding), (unsigned(a.token) * unsigned(H) + unsigned(i)) * 4u);
+    if (L == 0) {
+        if (Q8 && a.emb_bf16) {
+            const unsigned e = unsigned(a.token) * unsigned(H) + unsigned(i);
+            const unsigned w = __float_as_uint(ldp(rsrc(a.embedding), e / 2u * 4u));
+            return __uint_as_float((i & 1) ? (w & 0xffff0000u) : (w << 16));
+        }
+        return ldp(rsrc(a.embedding), (unsigned(a.token) * unsigned(H) + unsigned(i)) * 4u);
+    }
     return wait1(a, rs, SOFF(x) + 8u * unsigned(i), tag(a, producer), l, wall_clock64(), p);
 }
-// The staged H-vector in chunks (element 4(lane + 64v) .. +3 in xv[v]) times
-// its RMSNorm and the staged (1 + w) (reference.h:120-126).
+// The staged H-vector in chunks times its RMSNorm and the staged (1 + w)
+// (reference.h:120-126). fp32 rows: xv[v] holds elements 4 (lane + 64 v) .. +3;
+// int8 rows: elements 16 lane + 4 v .. +3 (the 16 columns of the lane's
+// 16-byte weight entry).
+template <bool Q8>
 __device__ __forceinline__ void normed_chunks(const Lds& l, int par, float eps, f4 (&xv)[4]) {
     const unsigned lane = lane_id();
     float ss = 0.f;
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
-        xv[v] = lds4(&l.act[par][4 * (lane + 64 * v)]);
+        xv[v] = lds4(&l.act[par][Q8 ? 16 * lane + 4 * v : 4 * (lane + 64 * v)]);
         ss += dot4(xv[v], xv[v]);
     }
     ss = wave_sum(ss);
     const float r = 1.f / sqrtf(ss / float(H) + eps);
 #pragma unroll
-    for (int v = 0; v < 4; ++v) xv[v] = (xv[v] * r) * lds4(&l.nw[par][4 * (lane + 64 * v)]);
+    for (int v = 0; v < 4; ++v) xv[v] = (xv[v] * r) * lds4(&l.nw[par][Q8 ? 16 * lane + 4 * v : 4 * (lane + 64 * v)]);
 }
-// Row `r` of an [rows, H] matrix into wb[AT .. AT + 3].
-template <int AT>
-__device__ __forceinline__ void load_row_h(f4* wb, Rs m, int r) {
-    const unsigned lo = 16u * lane_id(), row = unsigned(r) * unsigned(H * 4);
+// Value e (0..3) of a word of packed int8.
+__device__ __forceinline__ float q8v(unsigned w, int e) { return float(int(w << (24 - 8 * e)) >> 24); }
+// 16 int8 weights (one 16-byte entry) times 16 activations.
+__device__ __forceinline__ float q8dot(f4 w, const f4 (&x)[4], float acc) {
 #pragma unroll
-    for (int v = 0; v < 4; ++v) wb[AT + v] = ldw(m, lo + 1024u * v, row);
+    for (int j = 0; j < 4; ++j) {
+        const unsigned wj = __float_as_uint(w[j]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc = fmaf(q8v(wj, e), x[j][e], acc);
+    }
+    return acc;
 }
-template <int AT>
+// Row `r` of an [rows, H] matrix into wb[AT .. AT + 3]. int8 (packed as the
+// reference's upload_int8, src/device.rs:550-561: `rows` fp32 scales, then the
+// values row-major): the row's 1 KiB in wb[AT] (columns 16 lane .. +15) and
+// its scale in wb[AT + 1].x.
+template <bool Q8, int AT>
+__device__ __forceinline__ void load_row_h(f4* wb, Rs m, int r, int rows) {
+    const unsigned lo = 16u * lane_id();
+    if constexpr (Q8) {
+        wb[AT] = ldw(m, lo, unsigned(rows) * 4u + unsigned(r) * unsigned(H));
+        wb[AT + 1] = f4{ldp(m, unsigned(r) * 4u), 0.f, 0.f, 0.f};
+    } else {
+        const unsigned row = unsigned(r) * unsigned(H * 4);
+#pragma unroll
+        for (int v = 0; v < 4; ++v) wb[AT + v] = ldw(m, lo + 1024u * v, row);
+    }
+}
+// int8: scale * sum(q x), the scale after the sum (reference bridge.cpp:620-653).
+template <bool Q8, int AT>
 __device__ __forceinline__ float dot_row_h(const f4* wb, const f4 (&xv)[4]) {
     float acc = 0.f;
+    if constexpr (Q8) return wb[AT + 1].x * wave_sum(q8dot(wb[AT], xv, acc));
 #pragma unroll
     for (int v = 0; v < 4; ++v) acc = fdot4(wb[AT + v], xv[v], acc);
     return wave_sum(acc);
 }
-// Dot of a prefetched row of K * 256 columns with the staged vector.
-template <int K>
+// Dot of a prefetched row of K * 256 columns with the staged vector (int8: the
+// row in ceil(K / 4) entries of 16 columns per lane, its scale after them).
+template <bool Q8, int K>
 __device__ __forceinline__ float dot_row_lds(const f4* wb, const float* act) {
     const unsigned lane = lane_id();
     float acc = 0.f;
+    if constexpr (Q8) {
+        constexpr int NV = (K + 3) / 4;
+#pragma unroll
+        for (int v = 0; v < NV; ++v) {
+            const unsigned c0 = 1024u * v + 16u * lane;
+            if (c0 < unsigned(K * 256)) {
+                const f4 x[4] = {lds4(act + c0), lds4(act + c0 + 4), lds4(act + c0 + 8), lds4(act + c0 + 12)};
+                acc = q8dot(wb[v], x, acc);
+            }
+        }
+        return wb[NV].x * wave_sum(acc);
+    }
 #pragma unroll
     for (int v = 0; v < K; ++v) acc = fdot4(wb[v], lds4(act + 4 * (lane + 64 * v)), acc);
     return wave_sum(acc);
@@ -343,29 +404,31 @@ __device__ __forceinline__ float dot_row_lds(const f4* wb, const float* act) {
 // ---- T_DIN: qkv | a | b rows of a DeltaNet layer (z rows: phase T_MIX), then
 // the causal conv + SiLU of each qkv channel (reference.h:96-116): the wave
 // computing a channel's row is the only one touching its history.
-template <int R>
+template <bool Q8, int R>
 __device__ __forceinline__ void din_load(LayerP w, int u, f4* wb) {
     const int row = u * DIN_RPW + R;
     if (row < CH)
-        load_row_h<4 * R>(wb, rsrc(w->qkv), row);
+        load_row_h<Q8, 4 * R>(wb, rsrc(w->qkv), row, CH);
     else if (row < CH + VH)
-        load_row_h<4 * R>(wb, rsrc(w->a), row - CH);
+        load_row_h<Q8, 4 * R>(wb, rsrc(w->a), row - CH, VH);
     else if (row < DIN_ROWS)
-        load_row_h<4 * R>(wb, rsrc(w->b), row - CH - VH);
+        load_row_h<Q8, 4 * R>(wb, rsrc(w->b), row - CH - VH, VH);
 }
+template <bool Q8>
 __device__ __forceinline__ void prefetch_din(LayerP w, int u, f4* wb) {
-    din_load<0>(w, u, wb);
-    din_load<1>(w, u, wb);
-    din_load<2>(w, u, wb);
-    din_load<3>(w, u, wb);
+    din_load<Q8, 0>(w, u, wb);
+    din_load<Q8, 1>(w, u, wb);
+    din_load<Q8, 2>(w, u, wb);
+    din_load<Q8, 3>(w, u, wb);
 }
-template <int R>
+template <bool Q8, int R>
 __device__ __forceinline__ void din_row(const f4* wb, const f4 (&xv)[4], int u, float& mine) {
     if (u * DIN_RPW + R < DIN_ROWS) {
-        const float acc = dot_row_h<4 * R>(wb, xv);
+        const float acc = dot_row_h<Q8, 4 * R>(wb, xv);
         if (lane_id() == R) mine = acc;
     }
 }
+template <bool Q8>
 __device__ __forceinline__ bool phase_din(const Args& a, Rs rs, LayerP w, int L, int p, int u, const f4* wb, Lds& l) {
     const int par = p & 1;
     const int lane = int(lane_id()), row = u * DIN_RPW + lane;
@@ -380,16 +443,16 @@ __device__ __forceinline__ bool phase_din(const Args& a, Rs rs, LayerP w, int L,
         c0 = ldp(cw, co), c1 = ldp(cw, co + 4), c2 = ldp(cw, co + 8), c3 = ldp(cw, co + 12);
     }
     stage_norm(w->input_norm, par, l);
-    stage_input(a, rs, L, p - 1, par, l, p);
+    stage_input<Q8>(a, rs, L, p - 1, par, l, p);
     if (!bsync(l, p)) return false;
     if (u * DIN_RPW >= DIN_ROWS) return true;
     f4 xv[4];
-    normed_chunks(l, par, a.eps, xv);
+    normed_chunks<Q8>(l, par, a.eps, xv);
     float mine = 0.f;  // lane r: the dot product of row u * DIN_RPW + r
-    din_row<0>(wb, xv, u, mine);
-    din_row<1>(wb, xv, u, mine);
-    din_row<2>(wb, xv, u, mine);
-    din_row<3>(wb, xv, u, mine);
+    din_row<Q8, 0>(wb, xv, u, mine);
+    din_row<Q8, 1>(wb, xv, u, mine);
+    din_row<Q8, 2>(wb, xv, u, mine);
+    din_row<Q8, 3>(wb, xv, u, mine);
     const unsigned t = tag(a, p);
     if (conv) {
         float sum = 0.f;
@@ -410,15 +473,16 @@ __device__ __forceinline__ bool phase_din(const Args& a, Rs rs, LayerP w, int L,
 // ---- T_MIX: L2 q/k, gates and the gated delta rule for 16 value columns of
 // one head per wave (units 0..127); silu(z), z = in_proj_z . n, on the other
 // units (only silu(z) is used: the gated norm's gate, reference.h:201-207).
-template <int R>
+template <bool Q8, int R>
 __device__ __forceinline__ void z_load(LayerP w, int u, f4* wb) {
     const int row = (u - MIX_WAVES) * Z_RPW + R;
-    if (row < VD) load_row_h<4 * R>(wb, rsrc(w->z), row);
+    if (row < VD) load_row_h<Q8, 4 * R>(wb, rsrc(w->z), row, VD);
 }
+template <bool Q8>
 __device__ __forceinline__ void prefetch_mix(LayerP w, int u, f4* wb) {
     if (u >= MIX_WAVES) {
-        z_load<0>(w, u, wb);
-        z_load<1>(w, u, wb);
+        z_load<Q8, 0>(w, u, wb);
+        z_load<Q8, 1>(w, u, wb);
         return;
     }
     // state S[h][i][j] (key row i, value column j), rows p*32 .. p*32+31 of column j
@@ -432,26 +496,27 @@ __device__ __forceinline__ void prefetch_mix(LayerP w, int u, f4* wb) {
         wb[k] = f4{ldp(S, o), ldp(S, o + DV * 4u), ldp(S, o + 2u * DV * 4u), ldp(S, o + 3u * DV * 4u)};
     }
 }
-template <int R>
+template <bool Q8, int R>
 __device__ __forceinline__ void z_row(Rs rs, const f4* wb, const f4 (&xv)[4], int u, unsigned t) {
     const int row = (u - MIX_WAVES) * Z_RPW + R;
     if (row < VD) {
-        const float acc = dot_row_h<4 * R>(wb, xv);
+        const float acc = dot_row_h<Q8, 4 * R>(wb, xv);
         if (lane_id() == 0) stt(rs, SOFF(z) + 8u * unsigned(row), silu(acc), t);
     }
 }
+template <bool Q8>
 __device__ __forceinline__ bool phase_mix(const Args& a, Rs rs, LayerP w, int L, int p, int u, f4* wb, Lds& l) {
     const int par = p & 1;
     stage_norm(w->input_norm, par, l);
-    stage_input(a, rs, L, p - 2, par, l, p);
+    stage_input<Q8>(a, rs, L, p - 2, par, l, p);
     if (!bsync(l, p)) return false;
     const unsigned t = tag(a, p);
     if (u >= MIX_WAVES) {
         if ((u - MIX_WAVES) * Z_RPW >= VD) return true;
         f4 xv[4];
-        normed_chunks(l, par, a.eps, xv);
-        z_row<0>(rs, wb, xv, u, t);
-        z_row<1>(rs, wb, xv, u, t);
+        normed_chunks<Q8>(l, par, a.eps, xv);
+        z_row<Q8, 0>(rs, wb, xv, u, t);
+        z_row<Q8, 1>(rs, wb, xv, u, t);
         return true;
     }
     const unsigned lane = lane_id();
@@ -519,14 +584,25 @@ __device__ __forceinline__ bool phase_mix(const Args& a, Rs rs, LayerP w, int L,
 // reference.h:201-207) is built once per block in LDS (thread t: elements
 // 4t .. 4t+3, its head's 32 threads reduce the sum of squares), then
 // out_proj row u plus the residual.
-template <int COLS>
+template <bool Q8, int COLS>
 __device__ __forceinline__ void prefetch_row(const float* m, int row, int rows, f4* wb) {
     if (row >= rows) return;
     const Rs r = rsrc(m);
-    const unsigned lo = 16u * lane_id(), ro = unsigned(row) * unsigned(COLS * 4);
+    const unsigned lo = 16u * lane_id();
+    if constexpr (Q8) {
+        constexpr int NV = (COLS + 1023) / 1024;
+        const unsigned ro = unsigned(rows) * 4u + unsigned(row) * unsigned(COLS);
 #pragma unroll
-    for (int v = 0; v < COLS / 256; ++v) wb[v] = ldw(r, lo + 1024u * v, ro);
+        for (int v = 0; v < NV; ++v)
+            if (lo + 1024u * v < unsigned(COLS)) wb[v] = ldw(r, lo + 1024u * v, ro);
+        wb[NV] = f4{ldp(r, unsigned(row) * 4u), 0.f, 0.f, 0.f};
+    } else {
+        const unsigned ro = unsigned(row) * unsigned(COLS * 4);
+#pragma unroll
+        for (int v = 0; v < COLS / 256; ++v) wb[v] = ldw(r, lo + 1024u * v, ro);
+    }
 }
+template <bool Q8>
 __device__ __forceinline__ bool phase_dout(const Args& a, Rs rs, LayerP w, int L, int p, int u, const f4* wb, Lds& l) {
     const int par = p & 1;
     {
@@ -547,33 +623,35 @@ __device__ __forceinline__ bool phase_dout(const Args& a, Rs rs, LayerP w, int L
     }
     if (!bsync(l, p)) return false;
     if (u >= H) return true;
-    const float acc = dot_row_lds<VD / 256>(wb, l.act[par]);
-    const float res = input_at(a, rs, L, p - 3, u, l, p);
+    const float acc = dot_row_lds<Q8, VD / 256>(wb, l.act[par]);
+    const float res = input_at<Q8>(a, rs, L, p - 3, u, l, p);
     if (lane_id() == 0) stt(rs, SOFF(after) + 8u * unsigned(u), res + acc, tag(a, p));
     return true;
 }
 
 // ---- T_GLU: product = silu(gate . n) * (up . n), n = post RMSNorm of `after`
-template <int R>
+template <bool Q8, int R>
 __device__ __forceinline__ void glu_load(LayerP w, int u, f4* wb) {
     const int row = u * GLU_RPW + R;
     if (row < I) {
-        load_row_h<8 * R>(wb, rsrc(w->gate), row);
-        load_row_h<8 * R + 4>(wb, rsrc(w->up), row);
+        load_row_h<Q8, 8 * R>(wb, rsrc(w->gate), row, I);
+        load_row_h<Q8, 8 * R + 4>(wb, rsrc(w->up), row, I);
     }
 }
+template <bool Q8>
 __device__ __forceinline__ void prefetch_glu(LayerP w, int u, f4* wb) {
-    glu_load<0>(w, u, wb);
-    glu_load<1>(w, u, wb);
+    glu_load<Q8, 0>(w, u, wb);
+    glu_load<Q8, 1>(w, u, wb);
 }
-template <int R>
+template <bool Q8, int R>
 __device__ __forceinline__ void glu_row(Rs rs, const f4* wb, const f4 (&xv)[4], int u, unsigned t) {
     const int row = u * GLU_RPW + R;
     if (row < I) {
-        const float g = dot_row_h<8 * R>(wb, xv), up = dot_row_h<8 * R + 4>(wb, xv);
+        const float g = dot_row_h<Q8, 8 * R>(wb, xv), up = dot_row_h<Q8, 8 * R + 4>(wb, xv);
         if (lane_id() == 0) stt(rs, SOFF(product) + 8u * unsigned(row), silu(g) * up, t);
     }
 }
+template <bool Q8>
 __device__ __forceinline__ bool phase_glu(const Args& a, Rs rs, LayerP w, int p, int u, const f4* wb, Lds& l) {
     const int par = p & 1;
     stage_norm(w->post_norm, par, l);
@@ -581,45 +659,47 @@ __device__ __forceinline__ bool phase_glu(const Args& a, Rs rs, LayerP w, int p,
     if (!bsync(l, p)) return false;
     if (u * GLU_RPW >= I) return true;
     f4 xv[4];
-    normed_chunks(l, par, a.eps, xv);
-    glu_row<0>(rs, wb, xv, u, tag(a, p));
-    glu_row<1>(rs, wb, xv, u, tag(a, p));
+    normed_chunks<Q8>(l, par, a.eps, xv);
+    glu_row<Q8, 0>(rs, wb, xv, u, tag(a, p));
+    glu_row<Q8, 1>(rs, wb, xv, u, tag(a, p));
     return true;
 }
 
 // ---- T_DOWN: x = after + down . product
+template <bool Q8>
 __device__ __forceinline__ bool phase_down(const Args& a, Rs rs, int p, int u, const f4* wb, Lds& l) {
     const int par = p & 1;
     stage_tagged<I>(a, rs, SOFF(product), tag(a, p - 1), l.act[par], l, p);
     if (!bsync(l, p)) return false;
     if (u >= H) return true;
-    const float acc = dot_row_lds<I / 256>(wb, l.act[par]);
+    const float acc = dot_row_lds<Q8, I / 256>(wb, l.act[par]);
     const float res = wait1(a, rs, SOFF(after) + 8u * unsigned(u), tag(a, p - 2), l, wall_clock64(), p);
     if (lane_id() == 0) stt(rs, SOFF(x) + 8u * unsigned(u), res + acc, tag(a, p));
     return true;
 }
 
 // ---- T_AQKV: q ([Q | gate] per head), k, v rows of an attention layer
-template <int R>
+template <bool Q8, int R>
 __device__ __forceinline__ void aqkv_load(LayerP w, int u, f4* wb) {
     const int row = u * AQKV_RPW + R;
     if (row < QROWS)
-        load_row_h<4 * R>(wb, rsrc(w->q), row);
+        load_row_h<Q8, 4 * R>(wb, rsrc(w->q), row, QROWS);
     else if (row < QROWS + KVR)
-        load_row_h<4 * R>(wb, rsrc(w->k), row - QROWS);
+        load_row_h<Q8, 4 * R>(wb, rsrc(w->k), row - QROWS, KVR);
     else if (row < AQKV_ROWS)
-        load_row_h<4 * R>(wb, rsrc(w->v), row - QROWS - KVR);
+        load_row_h<Q8, 4 * R>(wb, rsrc(w->v), row - QROWS - KVR, KVR);
 }
+template <bool Q8>
 __device__ __forceinline__ void prefetch_aqkv(LayerP w, int u, f4* wb) {
-    aqkv_load<0>(w, u, wb);
-    aqkv_load<1>(w, u, wb);
-    aqkv_load<2>(w, u, wb);
+    aqkv_load<Q8, 0>(w, u, wb);
+    aqkv_load<Q8, 1>(w, u, wb);
+    aqkv_load<Q8, 2>(w, u, wb);
 }
-template <int R>
+template <bool Q8, int R>
 __device__ __forceinline__ void aqkv_row(Rs rs, const f4* wb, const f4 (&xv)[4], int u, unsigned t) {
     const int row = u * AQKV_RPW + R;
     if (row < AQKV_ROWS) {
-        const float acc = dot_row_h<4 * R>(wb, xv);
+        const float acc = dot_row_h<Q8, 4 * R>(wb, xv);
         if (lane_id() == 0) {
             const unsigned dst = row < QROWS ? SOFF(mixed) + 8u * unsigned(row)
                                  : row < QROWS + KVR ? SOFF(key) + 8u * unsigned(row - QROWS)
@@ -628,17 +708,18 @@ __device__ __forceinline__ void aqkv_row(Rs rs, const f4* wb, const f4 (&xv)[4],
         }
     }
 }
+template <bool Q8>
 __device__ __forceinline__ bool phase_aqkv(const Args& a, Rs rs, LayerP w, int L, int p, int u, const f4* wb, Lds& l) {
     const int par = p & 1;
     stage_norm(w->input_norm, par, l);
-    stage_input(a, rs, L, p - 1, par, l, p);
+    stage_input<Q8>(a, rs, L, p - 1, par, l, p);
     if (!bsync(l, p)) return false;
     if (u * AQKV_RPW >= AQKV_ROWS) return true;
     f4 xv[4];
-    normed_chunks(l, par, a.eps, xv);
-    aqkv_row<0>(rs, wb, xv, u, tag(a, p));
-    aqkv_row<1>(rs, wb, xv, u, tag(a, p));
-    aqkv_row<2>(rs, wb, xv, u, tag(a, p));
+    normed_chunks<Q8>(l, par, a.eps, xv);
+    aqkv_row<Q8, 0>(rs, wb, xv, u, tag(a, p));
+    aqkv_row<Q8, 1>(rs, wb, xv, u, tag(a, p));
+    aqkv_row<Q8, 2>(rs, wb, xv, u, tag(a, p));
     return true;
 }
 
@@ -902,13 +983,14 @@ __device__ __forceinline__ bool phase_comb(const Args& a, Rs rs, int p, int u, L
 }
 
 // ---- T_O: after = x + o . ctx
+template <bool Q8>
 __device__ __forceinline__ bool phase_o(const Args& a, Rs rs, int L, int p, int u, const f4* wb, Lds& l) {
     const int par = p & 1;
     stage_tagged<NH * HD>(a, rs, SOFF(ctx), tag(a, p - 1), l.act[par], l, p);
     if (!bsync(l, p)) return false;
     if (u >= H) return true;
-    const float acc = dot_row_lds<NH * HD / 256>(wb, l.act[par]);
-    const float res = input_at(a, rs, L, p - 4, u, l, p);
+    const float acc = dot_row_lds<Q8, NH * HD / 256>(wb, l.act[par]);
+    const float res = input_at<Q8>(a, rs, L, p - 4, u, l, p);
     if (lane_id() == 0) stt(rs, SOFF(after) + 8u * unsigned(u), res + acc, tag(a, p));
     return true;
 }
@@ -918,15 +1000,22 @@ __device__ __forceinline__ bool phase_o(const Args& a, Rs rs, int L, int p, int 
 // non-finite count).
 constexpr int LM_G = 4;
 __device__ __forceinline__ int lm_rows_per_wave(int vocab) { return (vocab + NW - 1) / NW; }
-__device__ __forceinline__ void lm_load(Rs lm, int row0, int row_end, f4* buf) {
+template <bool Q8>
+__device__ __forceinline__ void lm_load(Rs lm, int row0, int row_end, int vocab, f4* buf) {
 #pragma unroll
     for (int r = 0; r < LM_G; ++r)
         if (row0 + r < row_end) {
-            const unsigned lo = 16u * lane_id(), ro = unsigned(row0 + r) * unsigned(H * 4);
+            if constexpr (Q8) {
+                buf[r * 4] = ldw(lm, 16u * lane_id(), unsigned(vocab) * 4u + unsigned(row0 + r) * unsigned(H));
+                buf[r * 4 + 1] = f4{ldp(lm, unsigned(row0 + r) * 4u), 0.f, 0.f, 0.f};
+            } else {
+                const unsigned lo = 16u * lane_id(), ro = unsigned(row0 + r) * unsigned(H * 4);
 #pragma unroll
-            for (int v = 0; v < 4; ++v) buf[r * 4 + v] = ldw(lm, lo + 1024u * v, ro);
+                for (int v = 0; v < 4; ++v) buf[r * 4 + v] = ldw(lm, lo + 1024u * v, ro);
+            }
         }
 }
+template <bool Q8>
 __device__ __forceinline__ void lm_rows(Rs lg, const f4* buf, const f4 (&xv)[4], int row0, int row_end, float& best,
                                         unsigned& at, unsigned& bad) {
 #pragma unroll
@@ -934,9 +1023,13 @@ __device__ __forceinline__ void lm_rows(Rs lg, const f4* buf, const f4 (&xv)[4],
         const int row = row0 + r;
         if (row < row_end) {
             float acc = 0.f;
+            if constexpr (Q8) {
+                acc = buf[r * 4 + 1].x * wave_sum(q8dot(buf[r * 4], xv, acc));
+            } else {
 #pragma unroll
-            for (int v = 0; v < 4; ++v) acc = fdot4(buf[r * 4 + v], xv[v], acc);
-            acc = wave_sum(acc);
+                for (int v = 0; v < 4; ++v) acc = fdot4(buf[r * 4 + v], xv[v], acc);
+                acc = wave_sum(acc);
+            }
             if (lane_id() == 0) stp(lg, 4u * unsigned(row), acc);
             if (!isfinite(acc)) {
                 ++bad;
@@ -947,28 +1040,30 @@ __device__ __forceinline__ void lm_rows(Rs lg, const f4* buf, const f4 (&xv)[4],
         }
     }
 }
+template <bool Q8>
 __device__ __forceinline__ void prefetch_lm(const Args& a, int u, f4* wb) {
     const int rpw = lm_rows_per_wave(a.vocab), row0 = u * rpw, row_end = min(a.vocab, row0 + rpw);
-    lm_load(rsrc(a.lm_head), row0, row_end, wb);
+    lm_load<Q8>(rsrc(a.lm_head), row0, row_end, a.vocab, wb);
 }
+template <bool Q8>
 __device__ __forceinline__ bool phase_lm(const Args& a, Rs rs, int p, int u, f4* wb, Lds& l) {
     const int par = p & 1;
     stage_norm(a.final_norm, par, l);
     stage_tagged<H>(a, rs, SOFF(x), tag(a, p - 1), l.act[par], l, p);
     if (!bsync(l, p)) return false;
     f4 xv[4];
-    normed_chunks(l, par, a.eps, xv);
+    normed_chunks<Q8>(l, par, a.eps, xv);
     const int rpw = lm_rows_per_wave(a.vocab), row0 = u * rpw, row_end = min(a.vocab, row0 + rpw);
     const Rs lm = rsrc(a.lm_head), lg = rsrc(a.logits);
     float best = -INFINITY;
     unsigned at = 0xffffffffu, bad = 0;
     f4 nb[4 * LM_G];
     for (int r = row0; r < row_end; r += 2 * LM_G) {
-        lm_load(lm, r + LM_G, row_end, nb);
-        lm_rows(lg, wb, xv, r, row_end, best, at, bad);
+        lm_load<Q8>(lm, r + LM_G, row_end, a.vocab, nb);
+        lm_rows<Q8>(lg, wb, xv, r, row_end, best, at, bad);
         if (r + LM_G >= row_end) break;
-        lm_load(lm, r + 2 * LM_G, row_end, wb);
-        lm_rows(lg, nb, xv, r + LM_G, row_end, best, at, bad);
+        lm_load<Q8>(lm, r + 2 * LM_G, row_end, a.vocab, wb);
+        lm_rows<Q8>(lg, nb, xv, r + LM_G, row_end, best, at, bad);
     }
     if (lane_id() == 0) {
         const unsigned o = SOFF(lmpart) + unsigned(u) * 32u, t = tag(a, p);
@@ -1044,23 +1139,25 @@ __device__ __forceinline__ void phase_arg(const Args& a, Rs rs, int p, Lds& l) {
 }
 
 // ---------------------------------------------------------------- the kernel
+template <bool Q8>
 __device__ __forceinline__ void prefetch(const Args& a, int q, int u, f4* wb) {
     if (q >= a.nphases) return;
     const LayerP w = layer(a, player(a, q));
     switch (ptype(a, q)) {
-    case T_DIN: prefetch_din(w, u, wb); break;
-    case T_MIX: prefetch_mix(w, u, wb); break;
-    case T_DOUT: prefetch_row<VD>(w->out, u, H, wb); break;
-    case T_GLU: prefetch_glu(w, u, wb); break;
-    case T_DOWN: prefetch_row<I>(w->down, u, H, wb); break;
-    case T_AQKV: prefetch_aqkv(w, u, wb); break;
+    case T_DIN: prefetch_din<Q8>(w, u, wb); break;
+    case T_MIX: prefetch_mix<Q8>(w, u, wb); break;
+    case T_DOUT: prefetch_row<Q8, VD>(w->out, u, H, wb); break;
+    case T_GLU: prefetch_glu<Q8>(w, u, wb); break;
+    case T_DOWN: prefetch_row<Q8, I>(w->down, u, H, wb); break;
+    case T_AQKV: prefetch_aqkv<Q8>(w, u, wb); break;
     case T_ATTN: prefetch_attn(w, u, a.pos, wb); break;
-    case T_O: prefetch_row<NH * HD>(w->o, u, H, wb); break;
-    case T_LM: prefetch_lm(a, u, wb); break;
+    case T_O: prefetch_row<Q8, NH * HD>(w->o, u, H, wb); break;
+    case T_LM: prefetch_lm<Q8>(a, u, wb); break;
     default: break;
     }
 }
 
+template <bool Q8>
 __global__ __launch_bounds__(THREADS, 1) void decode_kernel(Args a) {
     __shared__ Lds l;
     // wave-uniform (readfirstlane lets the compiler keep indices and buffer
@@ -1071,7 +1168,7 @@ __global__ __launch_bounds__(THREADS, 1) void decode_kernel(Args a) {
     __syncthreads();
     const Rs rs = rsrc(a.s);
     f4 wb[WBUF];
-    prefetch(a, 0, unit, wb);
+    prefetch<Q8>(a, 0, unit, wb);
     for (int p = 0; p < a.nphases; ++p) {
         const int t = ptype(a, p);
         if (t == T_ARG) {
@@ -1083,16 +1180,16 @@ __global__ __launch_bounds__(THREADS, 1) void decode_kernel(Args a) {
         const int u = opaque_uniform(unit);
         bool ok = true;
         switch (t) {
-        case T_DIN: ok = phase_din(a, rs, w, L, p, u, wb, l); break;
-        case T_MIX: ok = phase_mix(a, rs, w, L, p, u, wb, l); break;
-        case T_DOUT: ok = phase_dout(a, rs, w, L, p, u, wb, l); break;
-        case T_GLU: ok = phase_glu(a, rs, w, p, u, wb, l); break;
-        case T_DOWN: ok = phase_down(a, rs, p, u, wb, l); break;
-        case T_AQKV: ok = phase_aqkv(a, rs, w, L, p, u, wb, l); break;
+        case T_DIN: ok = phase_din<Q8>(a, rs, w, L, p, u, wb, l); break;
+        case T_MIX: ok = phase_mix<Q8>(a, rs, w, L, p, u, wb, l); break;
+        case T_DOUT: ok = phase_dout<Q8>(a, rs, w, L, p, u, wb, l); break;
+        case T_GLU: ok = phase_glu<Q8>(a, rs, w, p, u, wb, l); break;
+        case T_DOWN: ok = phase_down<Q8>(a, rs, p, u, wb, l); break;
+        case T_AQKV: ok = phase_aqkv<Q8>(a, rs, w, L, p, u, wb, l); break;
         case T_ATTN: ok = phase_attn(a, rs, w, p, u, wb, l); break;
         case T_COMB: ok = phase_comb(a, rs, p, u, l); break;
-        case T_O: ok = phase_o(a, rs, L, p, u, wb, l); break;
-        case T_LM: ok = phase_lm(a, rs, p, u, wb, l); break;
+        case T_O: ok = phase_o<Q8>(a, rs, L, p, u, wb, l); break;
+        case T_LM: ok = phase_lm<Q8>(a, rs, p, u, wb, l); break;
         default: break;
         }
         if (!ok) return;
@@ -1100,7 +1197,7 @@ __global__ __launch_bounds__(THREADS, 1) void decode_kernel(Args a) {
         // before it (at the end of T_ATTN) instead of after it.
         if (t == T_COMB) continue;
         const int q = p + 1 < a.nphases && ptype(a, p + 1) == T_COMB ? p + 2 : p + 1;
-        prefetch(a, q, opaque_uniform(unit), wb);
+        prefetch<Q8>(a, q, opaque_uniform(unit), wb);
     }
 }
 
@@ -1114,6 +1211,7 @@ struct QrDecodePlan {
     qr::dec::Scratch* scratch = nullptr;
     std::vector<float> host_denom;  // theta^(2i / rot) by the host libm
     int capacity = 0;
+    bool q8 = false;  // int8 matrices and LM head: decode_kernel<true>
 };
 
 namespace qr {
@@ -1131,6 +1229,9 @@ const char* decode_unsupported(const QrDecodeDesc& d) {
         return "one-launch decode: vocabulary or capacity beyond 32-bit offsets";
     if (!d.embedding || !d.final_norm || !d.logits || !d.picks || !d.layer)
         return "one-launch decode: missing buffer";
+    if (d.weights != QR_DECODE_F32 && d.weights != QR_DECODE_INT8)
+        return "one-launch decode: matrices must be all fp32 or all int8";
+    if (d.weights == QR_DECODE_INT8 && !d.lm_head) return "one-launch decode: int8 needs its own int8 LM head";
     int phases = 2;
     for (int l = 0; l < d.layers; ++l) phases += d.layer[l].attention ? 6 : 5;
     if (phases > MAXPH || phases >= 1023) return "one-launch decode: too many phases";
@@ -1145,7 +1246,10 @@ int decode_plan_create(const QrDecodeDesc& d, QrDecodePlan** out, hipStream_t s,
     (void)hipGetDevice(&dev);
     (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
     (void)hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, dev);
-    if (!coop || hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, decode_kernel, THREADS, 0) != hipSuccess ||
+    const bool q8 = d.weights == QR_DECODE_INT8;
+    if (!coop ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, q8 ? decode_kernel<true> : decode_kernel<false>,
+                                                     THREADS, 0) != hipSuccess ||
         per_cu * cus < BLOCKS) {
         *why = "one-launch decode: 256 co-resident blocks do not fit this device";
         return -1;
@@ -1153,6 +1257,7 @@ int decode_plan_create(const QrDecodeDesc& d, QrDecodePlan** out, hipStream_t s,
     auto* p = new QrDecodePlan;
     std::memset(&p->args, 0, sizeof(p->args));
     p->capacity = d.capacity;
+    p->q8 = q8;
     hipError_t e = hipMalloc(reinterpret_cast<void**>(&p->layers), sizeof(QrDecodeLayer) * size_t(d.layers));
     if (e == hipSuccess) e = hipMalloc(reinterpret_cast<void**>(&p->scratch), sizeof(Scratch));
     // RoPE denominators theta^(2i / rot) by the host libm (the reference's
@@ -1177,6 +1282,7 @@ int decode_plan_create(const QrDecodeDesc& d, QrDecodePlan** out, hipStream_t s,
     a.picks = d.picks;
     a.s = p->scratch;
     a.vocab = d.vocab;
+    a.emb_bf16 = d.embedding_bf16 ? 1 : 0;
     a.eps = d.eps;
     a.epoch = 0;
     static const uint8_t delta[5] = {T_DIN, T_MIX, T_DOUT, T_GLU, T_DOWN};
@@ -1220,8 +1326,9 @@ int decode_step(QrDecodePlan* p, int token, int position, hipStream_t s) {
         if (hipError_t e = hipMemsetAsync(p->scratch, 0, sizeof(Scratch), s)) return int(e);
     }
     void* args[] = {&a};
-    return int(hipLaunchCooperativeKernel(reinterpret_cast<const void*>(decode_kernel), dim3(BLOCKS), dim3(THREADS),
-                                          args, 0, s));
+    const void* k = p->q8 ? reinterpret_cast<const void*>(decode_kernel<true>)
+                          : reinterpret_cast<const void*>(decode_kernel<false>);
+    return int(hipLaunchCooperativeKernel(k, dim3(BLOCKS), dim3(THREADS), args, 0, s));
 }
 
 }  // namespace qr

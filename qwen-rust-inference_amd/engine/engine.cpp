@@ -490,14 +490,18 @@ struct QeRun {
         drop_plan();
         const Api* a = api();
         const QwConfig& c = model->config;
-        if (!a->decode_plan || !model->embedding.f32() || !model->output().f32()) return;
+        if (!a->decode_plan || model->embedding.int8) return;
+        // all matrices fp32, or all int8 (the int8 model's LM head is int8 too)
+        const bool q8 = model->output().int8;
+        auto ok = [q8](const DeviceMatrix& m) { return q8 ? m.int8 : m.f32(); };
+        if (!ok(model->output())) return;
         std::vector<QrDecodeLayer> layers;
         const DeviceBlock* attn = nullptr;
         const DeviceBlock* delta = nullptr;
         for (size_t l = 0; l < model->blocks.size(); ++l) {
             const DeviceBlock& b = model->blocks[l];
             MixerRun& m = mixers[l];
-            if (!b.gate.f32() || !b.up.f32() || !b.down.f32()) return;
+            if (!ok(b.gate) || !ok(b.up) || !ok(b.down)) return;
             QrDecodeLayer d{};
             d.attention = b.attention ? 1 : 0;
             d.input_norm = b.input.p;
@@ -506,7 +510,7 @@ struct QeRun {
             d.up = b.up.buffer.p;
             d.down = b.down.buffer.p;
             if (b.attention) {
-                if (!b.q.f32() || !b.k.f32() || !b.v.f32() || !b.o.f32()) return;
+                if (!ok(b.q) || !ok(b.k) || !ok(b.v) || !ok(b.o)) return;
                 d.q = b.q.buffer.p;
                 d.k = b.k.buffer.p;
                 d.v = b.v.buffer.p;
@@ -516,7 +520,7 @@ struct QeRun {
                 d.values = m.values.p;
                 attn = &b;
             } else {
-                if (!b.qkv.f32() || !b.z.f32() || !b.a.f32() || !b.b.f32() || !b.out.f32()) return;
+                if (!ok(b.qkv) || !ok(b.z) || !ok(b.a) || !ok(b.b) || !ok(b.out)) return;
                 d.qkv = b.qkv.buffer.p;
                 d.z = b.z.buffer.p;
                 d.a = b.a.buffer.p;
@@ -554,6 +558,8 @@ struct QeRun {
         desc.logits = logits.p;
         desc.picks = picks.p;
         desc.layer = layers.data();
+        desc.weights = q8 ? QR_DECODE_INT8 : QR_DECODE_F32;
+        desc.embedding_bf16 = model->embedding.bf16 ? 1 : 0;
         QrDecodePlan* p = nullptr;
         if (a->decode_plan(a->ctx, &desc, &p) == 0) plan = p;
     }

@@ -274,3 +274,76 @@ def test_qwen08b_one_launch_greedy_matches_op_sequence(qwen08b_models):
         ids, _ = run.decode_greedy(O.select_greedy(logits), 24)
         got.append(ids)
     assert got[0] == got[1]
+
+
+def _bf16_embedding(w):
+    """The weights with the embedding table rounded (truncated) to BF16, so the
+    int8 upload keeps the lookup rows BF16 as the reference's does for a
+    BF16 checkpoint (src/device.rs:978-1042)."""
+    t = dict(w.tensors)
+    t[0] = (t[0].view(np.uint32) & np.uint32(0xFFFF0000)).view(np.float32)
+    return M.Weights(w.config, t)
+
+
+@pytest.fixture(scope="module")
+def qwen08b_int8_models(qwen08b):
+    """The 0.8B model with int8 matrices (BASELINE config 5's format) and a
+    BF16 embedding: one-launch decode step and op sequence."""
+    c, w = qwen08b
+    wb = _bf16_embedding(w)
+    print("loading 0.8B int8 twice (one-launch decode / op sequence)", flush=True)
+    return E.Model(wb, fmt=E.INT8), E.Model(wb, fmt=E.INT8, disable=E.NO_DECODE_STEP)
+
+
+@pytest.mark.parametrize("position", [0, 453, 8191])
+def test_qwen08b_int8_one_launch_matches_op_sequence(qwen08b, qwen08b_int8_models, position):
+    """int8 weights: the one-launch step against the op sequence on the same
+    seeded state. Both read the same int8 rows and scales and differ only in
+    fp32 summation order, so the fp32 bound applies (tighter than config 5's
+    1e-2); greedy picks identical."""
+    c, _ = qwen08b
+    fast, ops = qwen08b_int8_models
+    cap = position + 8
+    a, b = fast.new_run(cap, chunk=8), ops.new_run(cap, chunk=8)
+    assert a.decode_plan and not b.decode_plan
+    parts = _random_states(c, a, position, seed=position + 7)
+    b.set_position(position)
+    for (layer, which, v) in parts:
+        a.write_state(layer, which, v)
+        b.write_state(layer, which, v)
+    tokens = [int(v) for v in np.random.default_rng(position + 2).integers(0, c.vocab_size, 3)]
+    for i, t in enumerate(tokens):
+        print(f"int8 position {position + i}: one-launch vs op sequence", flush=True)
+        got, want = a.step(t), b.step(t)
+        parity(got, want, where=f"int8 logits at {position + i}")
+        assert O.select_greedy(got) == O.select_greedy(want)
+    for layer in range(c.num_layers):
+        for which in range(4):
+            parity(a.state(layer, which), b.state(layer, which), where=f"int8 state {layer}/{which} at {position}")
+
+
+def test_qwen08b_int8_one_launch_greedy_matches_op_sequence(qwen08b_int8_models):
+    """Config 5's decode shape (a 454-token prompt, int8 weights) for 24
+    greedy tokens: identical IDs on the one-launch path and the op sequence."""
+    fast, ops = qwen08b_int8_models
+    prompt = [int(v) for v in np.random.default_rng(4).integers(0, 248320, 454)]
+    got = []
+    for m in (fast, ops):
+        print(f"int8 prefill 454 + 24 greedy, plan={m is fast}", flush=True)
+        run = m.new_run(512, chunk=512)
+        logits = run.prefill(prompt)
+        ids, _ = run.decode_greedy(O.select_greedy(logits), 24)
+        got.append(ids)
+    assert got[0] == got[1]
+
+
+def test_qwen08b_int8_one_launch_against_dequantised_oracle(qwen08b):
+    """Config 5's bar on the one-launch path: int8 steps (fp32 embedding rows)
+    against the CPU path on the dequantised weights at 1e-2."""
+    c, w = qwen08b
+    run = E.Model(w, fmt=E.INT8).new_run(16, chunk=8)
+    assert run.decode_plan
+    st = dequantised(c, w).new_state()
+    for i, t in enumerate([int(v) for v in np.random.default_rng(6).integers(0, c.vocab_size, 4)]):
+        print(f"int8 one-launch step {i} against the dequantised oracle", flush=True)
+        parity(run.step(t), st.step(t, O.VECTOR), rtol=INT8_RTOL, where=f"int8 one-launch step {i}")
