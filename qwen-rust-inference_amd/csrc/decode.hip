@@ -164,6 +164,58 @@ __device__ __forceinline__ int opaque_uniform(int v) {
     return v;
 }
 
+// ---------------------------------------------------------------- cross-lane steps
+// DPP moves within 16-lane rows and the gfx950 row / half swaps
+// (v_permlane16_swap, v_permlane32_swap): one VALU op per step, where
+// __shfl_xor is a ds_bpermute through the LDS crossbar (~100+ cycles each, six
+// in a row per wave sum). Each sum step adds the same pair on both lanes, so
+// every lane ends with a bitwise-identical result. Whole-wave control flow
+// only (a DPP read of a masked-off lane returns its stale register).
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+constexpr int kQuadXor1 = 0xB1, kQuadXor2 = 0x4E, kRowHalfMirror = 0x141, kRowMirror = 0x140, kRowRor8 = 0x128;
+// The value of lane ^ 16 (O = 16) or lane ^ 32 (O = 32).
+template <int O>
+__device__ __forceinline__ float lane_xor(float v) {
+    static_assert(O == 16 || O == 32, "row or half swap");
+    const unsigned x = __float_as_uint(v);
+    const auto r = O == 16 ? __builtin_amdgcn_permlane16_swap(x, x, false, false)
+                           : __builtin_amdgcn_permlane32_swap(x, x, false, false);
+    // swapped: lanes of odd rows (halves) hold the partner in r[0], the others in r[1]
+    return __uint_as_float((threadIdx.x & O) ? r[0] : r[1]);
+}
+template <int O>
+__device__ __forceinline__ float xor_sum(float v) {
+    const unsigned x = __float_as_uint(v);
+    const auto r = O == 16 ? __builtin_amdgcn_permlane16_swap(x, x, false, false)
+                           : __builtin_amdgcn_permlane32_swap(x, x, false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);  // (even, odd) on both lanes
+}
+// Sum over aligned groups of W lanes (W = 16, 32 or 64).
+template <int W>
+__device__ __forceinline__ float lanes_sum(float v) {
+    v += dpp<kQuadXor1>(v);
+    v += dpp<kQuadXor2>(v);
+    v += dpp<kRowHalfMirror>(v);
+    v += dpp<kRowMirror>(v);
+    if constexpr (W >= 32) v = xor_sum<16>(v);
+    if constexpr (W >= 64) v = xor_sum<32>(v);
+    return v;
+}
+__device__ __forceinline__ float wave_total(float v) { return lanes_sum<64>(v); }
+// Sum over the four lanes of equal lane % 16.
+__device__ __forceinline__ float column_sum(float v) { return xor_sum<32>(xor_sum<16>(v)); }
+__device__ __forceinline__ float wave_maximum(float v) {
+    v = fmaxf(v, dpp<kQuadXor1>(v));
+    v = fmaxf(v, dpp<kQuadXor2>(v));
+    v = fmaxf(v, dpp<kRowHalfMirror>(v));
+    v = fmaxf(v, dpp<kRowMirror>(v));
+    v = fmaxf(v, lane_xor<16>(v));
+    return fmaxf(v, lane_xor<32>(v));
+}
+
 // ---------------------------------------------------------------- LDS, waits
 struct Lds {
     alignas(16) float act[2][2 * VD];       // staged broadcast vector, by phase parity
@@ -331,7 +383,7 @@ __device__ __forceinline__ void normed_chunks(const Lds& l, int par, float eps, 
         xv[v] = lds4(&l.act[par][Q8 ? 16 * lane + 4 * v : 4 * (lane + 64 * v)]);
         ss += dot4(xv[v], xv[v]);
     }
-    ss = wave_sum(ss);
+    ss = wave_total(ss);
     const float r = 1.f / sqrtf(ss / float(H) + eps);
 #pragma unroll
     for (int v = 0; v < 4; ++v) xv[v] = (xv[v] * r) * lds4(&l.nw[par][Q8 ? 16 * lane + 4 * v : 4 * (lane + 64 * v)]);
@@ -368,10 +420,10 @@ __device__ __forceinline__ void load_row_h(f4* wb, Rs m, int r, int rows) {
 template <bool Q8, int AT>
 __device__ __forceinline__ float dot_row_h(const f4* wb, const f4 (&xv)[4]) {
     float acc = 0.f;
-    if constexpr (Q8) return wb[AT + 1].x * wave_sum(q8dot(wb[AT], xv, acc));
+    if constexpr (Q8) return wb[AT + 1].x * wave_total(q8dot(wb[AT], xv, acc));
 #pragma unroll
     for (int v = 0; v < 4; ++v) acc = fdot4(wb[AT + v], xv[v], acc);
-    return wave_sum(acc);
+    return wave_total(acc);
 }
 // Dot of a prefetched row of K * 256 columns with the staged vector (int8: the
 // row in ceil(K / 4) entries of 16 columns per lane, its scale after them).
@@ -389,11 +441,11 @@ __device__ __forceinline__ float dot_row_lds(const f4* wb, const float* act) {
                 acc = q8dot(wb[v], x, acc);
             }
         }
-        return wb[NV].x * wave_sum(acc);
+        return wb[NV].x * wave_total(acc);
     }
 #pragma unroll
     for (int v = 0; v < K; ++v) acc = fdot4(wb[v], lds4(act + 4 * (lane + 64 * v)), acc);
-    return wave_sum(acc);
+    return wave_total(acc);
 }
 
 // ---------------------------------------------------------------- phases
@@ -533,8 +585,8 @@ __device__ __forceinline__ bool phase_mix(const Args& a, Rs rs, LayerP w, int L,
     wait1n<7>(a, rs, mo, want, mv, l, start, p);
     const float q0 = mv[0], q1 = mv[1], k0 = mv[2], k1 = mv[3], v = mv[4], av = mv[5], bv = mv[6];
     // L2 norms (reference.h:134-143), q / sqrt(dk)
-    const float sq = wave_sum(q0 * q0 + q1 * q1);
-    const float sk = wave_sum(k0 * k0 + k1 * k1);
+    const float sq = wave_total(q0 * q0 + q1 * q1);
+    const float sk = wave_total(k0 * k0 + k1 * k1);
     const float rq = 1.f / sqrtf(sq + 1e-6f), rk = 1.f / sqrtf(sk + 1e-6f), sd = sqrtf(float(DK));
     float* lw = l.wave[wave];
     lw[lane] = (q0 * rq) / sd;
@@ -555,8 +607,7 @@ __device__ __forceinline__ bool phase_mix(const Args& a, Rs rs, LayerP w, int L,
         wb[k] *= decay;
         m = fdot4(wb[k], lds4(kk + 4 * k), m);
     }
-    m += __shfl_xor(m, 16, 64);
-    m += __shfl_xor(m, 32, 64);
+    m = column_sum(m);
     const float delta = (v - m) * beta;
     float o = 0.f;
 #pragma unroll
@@ -564,8 +615,7 @@ __device__ __forceinline__ bool phase_mix(const Args& a, Rs rs, LayerP w, int L,
         wb[k] += lds4(kk + 4 * k) * delta;
         o = fdot4(wb[k], lds4(qq + 4 * k), o);
     }
-    o += __shfl_xor(o, 16, 64);
-    o += __shfl_xor(o, 32, 64);
+    o = column_sum(o);
     const Rs S = rsrc(w->recurrent);
     const unsigned base = ((unsigned(h) * DK + unsigned(pr) * 32u) * DV + unsigned(j)) * 4u;
 #pragma unroll
@@ -617,7 +667,7 @@ __device__ __forceinline__ bool phase_dout(const Args& a, Rs rs, LayerP w, int L
         wait2n<4>(a, rs, co, all, want, cz, l, start, p);
         const f2 c01 = cz[0], c23 = cz[1], z01 = cz[2], z23 = cz[3];
         const f4 core = f4{c01.x, c01.y, c23.x, c23.y}, sz = f4{z01.x, z01.y, z23.x, z23.y};
-        const float ss = group_sum<32>(dot4(core, core));
+        const float ss = lanes_sum<32>(dot4(core, core));
         const float r = 1.f / sqrtf(ss / float(DV) + a.eps);
         *reinterpret_cast<f4*>(&l.act[par][4 * th]) = sz * ((core * r) * nw);
     }
@@ -773,14 +823,14 @@ __device__ __forceinline__ void prefetch_attn(LayerP w, int u, int pos, f4* wb) 
 // d + 32, on lane + 8), into LDS (reference.h:75-95, 41-47).
 __device__ __forceinline__ void norm_rope_head(f4 x, f4 wplus, const Args& a, float* out) {
     const unsigned lane = lane_id();
-    const float ss = wave_sum(dot4(x, x));
+    const float ss = wave_total(dot4(x, x));
     const float r = 1.f / sqrtf(ss / float(HD) + a.eps);
     x = (x * r) * wplus;
-    f4 other;
-    other.x = __shfl_xor(x.x, 8, 64);
-    other.y = __shfl_xor(x.y, 8, 64);
-    other.z = __shfl_xor(x.z, 8, 64);
-    other.w = __shfl_xor(x.w, 8, 64);
+    f4 other;  // lane ^ 8: a rotation by 8 within the 16-lane row
+    other.x = dpp<kRowRor8>(x.x);
+    other.y = dpp<kRowRor8>(x.y);
+    other.z = dpp<kRowRor8>(x.z);
+    other.w = dpp<kRowRor8>(x.w);
     if (lane < ROT / 4) {  // dims 4 lane .. 4 lane + 3 < 64
         const int i = int(4 * (lane & 7));
         const f4 cs = f4{a.rope_cs[i], a.rope_cs[i + 1], a.rope_cs[i + 2], a.rope_cs[i + 3]};
@@ -869,7 +919,7 @@ __device__ __forceinline__ bool phase_attn(const Args& a, Rs rs, LayerP w, int p
                 float sc = 0.f;
 #pragma unroll
                 for (int e = 0; e < 4; ++e) sc = fdot4(q[e], wb[step * 8 + e], sc);
-                sc = group_sum<16>(sc) * scale;
+                sc = lanes_sum<16>(sc) * scale;
                 if (pp < end) {
                     const float mn = fmaxf(m, sc);
                     const float corr = expf(m - mn);
@@ -884,17 +934,18 @@ __device__ __forceinline__ bool phase_attn(const Args& a, Rs rs, LayerP w, int p
         // merge the 4 position slots
 #pragma unroll
         for (int o = 16; o < 64; o <<= 1) {
-            const float mo = __shfl_xor(m, o, 64), lo = __shfl_xor(lsum, o, 64);
+            auto exch = [o](float v) { return o == 16 ? lane_xor<16>(v) : lane_xor<32>(v); };
+            const float mo = exch(m), lo = exch(lsum);
             const float mn = fmaxf(m, mo);
             const float c0 = m == -INFINITY ? 0.f : expf(m - mn), c1 = mo == -INFINITY ? 0.f : expf(mo - mn);
             lsum = lsum * c0 + lo * c1;
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 f4 other;
-                other.x = __shfl_xor(acc[e].x, o, 64);
-                other.y = __shfl_xor(acc[e].y, o, 64);
-                other.z = __shfl_xor(acc[e].z, o, 64);
-                other.w = __shfl_xor(acc[e].w, o, 64);
+                other.x = exch(acc[e].x);
+                other.y = exch(acc[e].y);
+                other.z = exch(acc[e].z);
+                other.w = exch(acc[e].w);
                 acc[e] = acc[e] * c0 + other * c1;
             }
             m = mn;
@@ -955,7 +1006,7 @@ __device__ __forceinline__ bool phase_comb(const Args& a, Rs rs, int p, int u, L
             mm = fmaxf(mm, mv[k]);
         }
     }
-    mm = wave_max(mm);
+    mm = wave_maximum(mm);
     float den = 0.f;
     f4 num = f4(0.f);
 #pragma unroll
@@ -968,11 +1019,11 @@ __device__ __forceinline__ bool phase_comb(const Args& a, Rs rs, int p, int u, L
             num += ldx4(rs, SOFF(pacc) + (ix * HD + unsigned(4 * c4)) * 4u) * wgt;
         }
     }
-    den = wave_sum(den);
-    num.x = wave_sum(num.x);
-    num.y = wave_sum(num.y);
-    num.z = wave_sum(num.z);
-    num.w = wave_sum(num.w);
+    den = wave_total(den);
+    num.x = wave_total(num.x);
+    num.y = wave_total(num.y);
+    num.z = wave_total(num.z);
+    num.w = wave_total(num.w);
     if (lane < 4) {
         const float val = lane == 0 ? num.x : lane == 1 ? num.y : lane == 2 ? num.z : num.w;
         const int d = 4 * c4 + int(lane);
@@ -1024,11 +1075,11 @@ __device__ __forceinline__ void lm_rows(Rs lg, const f4* buf, const f4 (&xv)[4],
         if (row < row_end) {
             float acc = 0.f;
             if constexpr (Q8) {
-                acc = buf[r * 4 + 1].x * wave_sum(q8dot(buf[r * 4], xv, acc));
+                acc = buf[r * 4 + 1].x * wave_total(q8dot(buf[r * 4], xv, acc));
             } else {
 #pragma unroll
                 for (int v = 0; v < 4; ++v) acc = fdot4(buf[r * 4 + v], xv[v], acc);
-                acc = wave_sum(acc);
+                acc = wave_total(acc);
             }
             if (lane_id() == 0) stp(lg, 4u * unsigned(row), acc);
             if (!isfinite(acc)) {
