@@ -38,6 +38,8 @@
 //     and blocks waiting on them time out in turn.
 #include <cstddef>
 #include <cstring>
+#include <mutex>
+#include <utility>
 #include <vector>
 
 #include "common.h"
@@ -1259,7 +1261,8 @@ __global__ __launch_bounds__(THREADS, 1) void decode_kernel(Args a) {
 struct QrDecodePlan {
     qr::dec::Args args;
     QrDecodeLayer* layers = nullptr;
-    qr::dec::Scratch* scratch = nullptr;
+    qr::dec::Scratch* scratch = nullptr;  // from the device's pool
+    int device = 0;
     std::vector<float> host_denom;  // theta^(2i / rot) by the host libm
     int capacity = 0;
     bool q8 = false;  // int8 matrices and LM head: decode_kernel<true>
@@ -1289,6 +1292,51 @@ const char* decode_unsupported(const QrDecodeDesc& d) {
     return nullptr;
 }
 
+// Scratch buffers are uncached device memory (hipDeviceMallocUncached): every
+// access to them is a cross-block hand-off that bypasses the L2s anyway, and on
+// uncached pages a 1024-pair broadcast to all 256 blocks settles in ~1.7 us
+// instead of ~2.8 us. Uncached memory that kernels have read is never handed
+// back to HIP while the process runs (freeing it has been seen to corrupt
+// later allocations on this platform): plans take buffers from a per-device
+// pool and return them with their last launch epoch, which the next plan on
+// the buffer continues, so no stale pair ever carries a tag a later launch
+// expects.
+namespace {
+struct PooledScratch {
+    qr::dec::Scratch* p;
+    unsigned epoch;
+};
+std::mutex g_pool_mutex;
+std::vector<std::pair<int, PooledScratch>> g_pool;  // (device, buffer) not in use
+
+hipError_t scratch_acquire(int dev, hipStream_t s, qr::dec::Scratch** out, unsigned* epoch) {
+    {
+        std::lock_guard<std::mutex> lock(g_pool_mutex);
+        for (size_t i = 0; i < g_pool.size(); ++i)
+            if (g_pool[i].first == dev) {
+                *out = g_pool[i].second.p;
+                *epoch = g_pool[i].second.epoch;
+                g_pool.erase(g_pool.begin() + long(i));
+                return hipSuccess;
+            }
+    }
+    hipError_t e = hipExtMallocWithFlags(reinterpret_cast<void**>(out), sizeof(qr::dec::Scratch),
+                                         hipDeviceMallocUncached);
+    if (e != hipSuccess) {
+        *out = nullptr;
+        return e;
+    }
+    *epoch = 0;
+    e = hipMemsetAsync(*out, 0, sizeof(qr::dec::Scratch), s);  // tag 0: never expected
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    return e;
+}
+void scratch_release(int dev, qr::dec::Scratch* p, unsigned epoch) {
+    std::lock_guard<std::mutex> lock(g_pool_mutex);
+    g_pool.push_back({dev, PooledScratch{p, epoch}});
+}
+}  // namespace
+
 int decode_plan_create(const QrDecodeDesc& d, QrDecodePlan** out, hipStream_t s, const char** why) {
     using namespace dec;
     *out = nullptr;
@@ -1309,15 +1357,17 @@ int decode_plan_create(const QrDecodeDesc& d, QrDecodePlan** out, hipStream_t s,
     std::memset(&p->args, 0, sizeof(p->args));
     p->capacity = d.capacity;
     p->q8 = q8;
+    p->device = dev;
+    unsigned epoch = 0;
     hipError_t e = hipMalloc(reinterpret_cast<void**>(&p->layers), sizeof(QrDecodeLayer) * size_t(d.layers));
-    if (e == hipSuccess) e = hipMalloc(reinterpret_cast<void**>(&p->scratch), sizeof(Scratch));
+    if (e == hipSuccess) e = scratch_acquire(dev, s, &p->scratch, &epoch);
+    p->args.epoch = epoch;  // what decode_plan_free hands back with the buffer
     // RoPE denominators theta^(2i / rot) by the host libm (the reference's
     // expression, src/attention.rs:49-50), as the op path's table
     p->host_denom.resize(ROT / 2);
     for (int i = 0; i < ROT / 2; ++i) p->host_denom[size_t(i)] = powf(d.theta, float(2 * i) / float(ROT));
     if (e == hipSuccess)
         e = hipMemcpyAsync(p->layers, d.layer, sizeof(QrDecodeLayer) * size_t(d.layers), hipMemcpyHostToDevice, s);
-    if (e == hipSuccess) e = hipMemsetAsync(p->scratch, 0, sizeof(Scratch), s);  // tag 0: never expected
     if (e == hipSuccess) e = hipStreamSynchronize(s);
     if (e != hipSuccess) {
         decode_plan_free(p);
@@ -1335,7 +1385,7 @@ int decode_plan_create(const QrDecodeDesc& d, QrDecodePlan** out, hipStream_t s,
     a.vocab = d.vocab;
     a.emb_bf16 = d.embedding_bf16 ? 1 : 0;
     a.eps = d.eps;
-    a.epoch = 0;
+    a.epoch = epoch;
     static const uint8_t delta[5] = {T_DIN, T_MIX, T_DOUT, T_GLU, T_DOWN};
     static const uint8_t attn[6] = {T_AQKV, T_ATTN, T_COMB, T_O, T_GLU, T_DOWN};
     int n = 0;
@@ -1354,7 +1404,7 @@ int decode_plan_create(const QrDecodeDesc& d, QrDecodePlan** out, hipStream_t s,
 void decode_plan_free(QrDecodePlan* p) {
     if (!p) return;
     if (p->layers) (void)hipFree(p->layers);
-    if (p->scratch) (void)hipFree(p->scratch);
+    if (p->scratch) scratch_release(p->device, p->scratch, p->args.epoch);
     delete p;
 }
 
