@@ -54,6 +54,10 @@ const char* qe_last_error(void);
  * mask. */
 QeModel* qe_model_load(const char* bridge_path, int expect_kind, const QwConfig* config,
                        const float* const* tensors, int format, int disable);
+/* Releases the model once no run of it is left. The reference's DeviceRun
+ * borrows its DeviceModel (src/device.rs:1333-1334), so the model outlives its
+ * runs by construction; across a C ABI the free order is the caller's, so runs
+ * hold their model and models and runs may be freed in any order. */
 void qe_model_free(QeModel* m);
 /* qr_info of the bridge context. */
 const char* qe_model_info(QeModel* m);

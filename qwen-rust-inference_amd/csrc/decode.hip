@@ -61,15 +61,18 @@ constexpr int BLOCKS = 256, WAVES = 8, THREADS = 64 * WAVES;
 constexpr int NW = BLOCKS * WAVES;  // 2048 waves
 constexpr int WBUF = 16;            // prefetch buffer, 16-byte entries per lane
 constexpr int SPAN = 8;             // attention positions per K/V chunk (2 steps of 4)
-constexpr int SMAX = 1024;          // attention splits per KV head
+constexpr int KVE = 2 * SPAN;       // 16-byte entries per lane of one K/V chunk
+constexpr int SMAX = 256;           // attention splits per KV head
+constexpr int QPG = NH / NKV;       // query heads per KV head: the waves of one attention slot
 constexpr int MAXPH = 6 * 64 + 2;
 constexpr int DIN_RPW = 4, GLU_RPW = 2, AQKV_RPW = 3, Z_RPW = 2;
 constexpr int MIX_WAVES = VH * 8;  // 16 value columns per wave
 constexpr int COMB_WAVES = NH * (HD / 4);
 static_assert(DIN_RPW * NW >= DIN_ROWS && GLU_RPW * NW >= I && AQKV_RPW * NW >= AQKV_ROWS, "rows per wave");
-static_assert(Z_RPW * (NW - MIX_WAVES) >= VD && COMB_WAVES <= NW && NKV * SMAX <= NW && SMAX % 64 == 0, "waves");
+static_assert(Z_RPW * (NW - MIX_WAVES) >= VD && COMB_WAVES <= NW && NKV * SMAX * QPG <= NW && SMAX % 64 == 0, "waves");
+static_assert(WAVES % QPG == 0 && NKV * SMAX <= BLOCKS * (WAVES / QPG), "attention slots: QPG waves of one block each");
 static_assert(4 * DIN_RPW <= WBUF && 8 * GLU_RPW <= WBUF && 4 * AQKV_RPW <= WBUF && 4 * Z_RPW <= WBUF, "buffer");
-static_assert(I / 256 <= WBUF && VD / 256 <= WBUF && NH * HD / 256 <= WBUF && 8 <= WBUF, "buffer");
+static_assert(I / 256 <= WBUF && VD / 256 <= WBUF && NH * HD / 256 <= WBUF && 8 <= WBUF && KVE <= WBUF, "buffer");
 static_assert(VD / 4 == THREADS && NH == WAVES, "one thread per 4 gated values, one wave per query head");
 
 enum : uint8_t { T_DIN, T_MIX, T_DOUT, T_GLU, T_DOWN, T_AQKV, T_ATTN, T_COMB, T_O, T_LM, T_ARG };
@@ -775,14 +778,25 @@ __device__ __forceinline__ bool phase_aqkv(const Args& a, Rs rs, LayerP w, int L
     return true;
 }
 
-// ---- T_ATTN: one wave per (KV head, span of positions); the 4 query heads of
-// the group share every K/V read. Lane: sub = lane % 16 holds dims
-// 64 e + 4 sub .. +3 (e < 4), slot = lane / 16 one of 4 positions per step, so
-// each K / V load instruction reads 256 contiguous bytes of 4 rows.
-// Caches are [capacity, kv_heads, head_dim].
+// ---- T_ATTN: one wave per (KV head, span of positions, query head of the
+// group). The QPG waves of one (KV head, span) slot sit in one block (waves
+// QPG k .. QPG k + QPG - 1 of block b take slot b + BLOCKS k), so the K/V
+// chunk they all read comes from HBM once and from the CU's caches for the
+// others. Lane: sub = lane % 16 holds dims 64 e + 4 sub .. +3 (e < 4),
+// slot = lane / 16 one of 4 positions per step, so each K / V load
+// instruction reads 256 contiguous bytes of 4 rows. Caches are
+// [capacity, kv_heads, head_dim].
 __device__ __forceinline__ int attn_span(int len) {
     const int chunks = (len + SPAN * SMAX - 1) / (SPAN * SMAX);
     return SPAN * chunks;
+}
+struct AttnUnit {
+    int kvh, sp, g;
+    bool busy;
+};
+__device__ __forceinline__ AttnUnit attn_unit(int u, int splits) {
+    const int block = u % BLOCKS, wave = u / BLOCKS, slot = block + BLOCKS * (wave / QPG);
+    return AttnUnit{slot / splits, slot % splits, wave % QPG, slot < NKV * splits};
 }
 __device__ __forceinline__ void load_kv_chunk(LayerP w, int kvh, int first, int pos, f4* buf) {
     const unsigned lane = lane_id(), sub = lane & 15, slot = lane >> 4;
@@ -817,8 +831,8 @@ __device__ __forceinline__ void patch_new(f4* buf, const float* kn, const float*
 }
 __device__ __forceinline__ void prefetch_attn(LayerP w, int u, int pos, f4* wb) {
     const int len = pos + 1, span = attn_span(len), splits = (len + span - 1) / span;
-    if (u >= NKV * splits) return;
-    load_kv_chunk(w, u / splits, (u % splits) * span, pos, wb);
+    const AttnUnit au = attn_unit(u, splits);
+    if (au.busy) load_kv_chunk(w, au.kvh, au.sp * span, pos, wb);
 }
 // RMSNorm (1 + w) of one head's 256 dims held 4 per lane by a whole wave,
 // then rotate-half RoPE of the first 64 dims (the partner of dim d < 32 is
@@ -841,10 +855,44 @@ __device__ __forceinline__ void norm_rope_head(f4 x, f4 wplus, const Args& a, fl
     }
     *reinterpret_cast<f4*>(out + 4 * lane) = x;
 }
+// One K/V chunk (SPAN positions from `first`, positions >= end masked) into
+// the lane's running (max, sum, weighted values): both steps' scores first,
+// then one rescale (reference.h:171-190, online form).
+__device__ __forceinline__ void attn_chunk(const f4* kv, const f4 (&q)[4], int first, int end, float& m, float& lsum,
+                                           f4 (&acc)[4]) {
+    const float scale = 1.f / 16.f;  // 1 / sqrt(256)
+    const int slot = int(lane_id() >> 4);
+    float sc[SPAN / 4];
+    bool ok[SPAN / 4];
+    float mn = m;
+#pragma unroll
+    for (int step = 0; step < SPAN / 4; ++step) {
+        float d = 0.f;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) d = fdot4(q[e], kv[step * 8 + e], d);
+        sc[step] = lanes_sum<16>(d) * scale;
+        ok[step] = first + 4 * step + slot < end;
+        if (ok[step]) mn = fmaxf(mn, sc[step]);
+    }
+    const float corr = m == -INFINITY ? 0.f : expf(m - mn);
+    lsum *= corr;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) acc[e] *= corr;
+#pragma unroll
+    for (int step = 0; step < SPAN / 4; ++step) {
+        if (ok[step]) {  // a masked lane's entries hold stale registers (any bit pattern): never read
+            const float pw = expf(sc[step] - mn);
+            lsum += pw;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) acc[e] += kv[step * 8 + 4 + e] * pw;
+        }
+    }
+    m = mn;
+}
 __device__ __forceinline__ bool phase_attn(const Args& a, Rs rs, LayerP w, int p, int u, f4* wb, Lds& l) {
     const int par = p & 1;
     const int pos = a.pos, len = pos + 1, span = attn_span(len), splits = (len + span - 1) / span;
-    const bool block_busy = int(blockIdx.x) < NKV * splits;  // wave 0 has the block's lowest unit
+    const bool block_busy = int(blockIdx.x) < NKV * splits;  // waves 0 .. QPG-1 hold the block's first slot
     const int wave = int(threadIdx.x >> 6);
     const unsigned want = tag(a, p - 1);
     if (block_busy) {
@@ -864,16 +912,15 @@ __device__ __forceinline__ bool phase_attn(const Args& a, Rs rs, LayerP w, int p
         if (hask) norm_rope_head(f4{qkv[2].x, qkv[2].y, qkv[3].x, qkv[3].y}, wk, a, &l.act[par][NH * HD + wave * HD]);
     }
     if (!bsync(l, p)) return false;
-    if (u >= NKV * splits) return true;
+    const AttnUnit au = attn_unit(u, splits);
+    if (!au.busy) return true;
     const unsigned lane = lane_id(), sub = lane & 15, slot = lane >> 4;
-    const int kvh = u / splits, sp = u % splits, begin = sp * span, end = min(len, begin + span);
+    const int kvh = au.kvh, sp = au.sp, h = kvh * QPG + au.g, begin = sp * span, end = min(len, begin + span);
     const float* kn = &l.act[par][NH * HD + kvh * HD];
     float* vn = l.wave[wave];  // the new value row
     const bool has_new = pos >= begin && pos < end;
     if (has_new) {
         if (slot == 0) {
-            const Rs rk = rsrc(w->keys), rv = rsrc(w->values);
-            const unsigned co = ((unsigned(pos) * NKV + unsigned(kvh)) * HD + sub * 4u) * 4u;
             const unsigned vo = SOFF(value) + (unsigned(kvh) * HD + sub * 4u) * 8u;
             const unsigned long long start = wall_clock64();
             unsigned vof[8];
@@ -885,94 +932,66 @@ __device__ __forceinline__ bool phase_attn(const Args& a, Rs rs, LayerP w, int p
                 all[k] = true;
             }
             wait2n<8>(a, rs, vof, all, want, vpair, l, start, p);
+            const Rs rk = rsrc(w->keys), rv = rsrc(w->values);
+            const unsigned co = ((unsigned(pos) * NKV + unsigned(kvh)) * HD + sub * 4u) * 4u;
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const f4 vv = f4{vpair[2 * e].x, vpair[2 * e].y, vpair[2 * e + 1].x, vpair[2 * e + 1].y};
                 *reinterpret_cast<f4*>(vn + sub * 4 + 64 * e) = vv;
-                stp4(rk, co + 256u * e, lds4(kn + sub * 4 + 64 * e));
-                stp4(rv, co + 256u * e, vv);
+                if (au.g == 0) {  // one wave of the slot appends the row to the caches
+                    stp4(rk, co + 256u * e, lds4(kn + sub * 4 + 64 * e));
+                    stp4(rv, co + 256u * e, vv);
+                }
             }
         }
         compiler_fence();
         patch_new(wb, kn, vn, begin, pos);
     }
-    const float scale = 1.f / 16.f;  // 1 / sqrt(256)
-    const unsigned t = tag(a, p);
-    float* gml = l.wave[wave] + HD;  // each head's (max, sum), published after all the heads' sums
-    int held = begin;  // wb holds the K/V chunk starting here (prefetched: the first)
+    f4 q[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) q[e] = lds4(&l.act[par][h * HD + sub * 4 + 64 * e]);
+    float m = -INFINITY, lsum = 0.f;
+    f4 acc[4] = {f4(0.f), f4(0.f), f4(0.f), f4(0.f)};
 #pragma unroll 1
-    for (int g = 0; g < NH / NKV; ++g) {
-        const int h = kvh * (NH / NKV) + g;
-        f4 q[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) q[e] = lds4(&l.act[par][h * HD + sub * 4 + 64 * e]);
-        float m = -INFINITY, lsum = 0.f;
-        f4 acc[4] = {f4(0.f), f4(0.f), f4(0.f), f4(0.f)};
-#pragma unroll 1
-        for (int first = begin; first < end; first += SPAN) {
-            if (first != held) {  // spans longer than one chunk (contexts over SPAN * SMAX)
-                load_kv_chunk(w, kvh, first, pos, wb);
-                if (has_new) patch_new(wb, kn, vn, first, pos);
-                held = first;
-            }
-#pragma unroll
-            for (int step = 0; step < SPAN / 4; ++step) {
-                const int pp = first + 4 * step + int(slot);
-                float sc = 0.f;
-#pragma unroll
-                for (int e = 0; e < 4; ++e) sc = fdot4(q[e], wb[step * 8 + e], sc);
-                sc = lanes_sum<16>(sc) * scale;
-                if (pp < end) {
-                    const float mn = fmaxf(m, sc);
-                    const float corr = expf(m - mn);
-                    const float pw = expf(sc - mn);
-                    lsum = lsum * corr + pw;
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) acc[e] = acc[e] * corr + wb[step * 8 + 4 + e] * pw;
-                    m = mn;
-                }
-            }
+    for (int first = begin; first < end; first += SPAN) {
+        if (first != begin) {
+            load_kv_chunk(w, kvh, first, pos, wb);
+            if (has_new) patch_new(wb, kn, vn, first, pos);
         }
-        // merge the 4 position slots
-#pragma unroll
-        for (int o = 16; o < 64; o <<= 1) {
-            auto exch = [o](float v) { return o == 16 ? lane_xor<16>(v) : lane_xor<32>(v); };
-            const float mo = exch(m), lo = exch(lsum);
-            const float mn = fmaxf(m, mo);
-            const float c0 = m == -INFINITY ? 0.f : expf(m - mn), c1 = mo == -INFINITY ? 0.f : expf(mo - mn);
-            lsum = lsum * c0 + lo * c1;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                f4 other;
-                other.x = exch(acc[e].x);
-                other.y = exch(acc[e].y);
-                other.z = exch(acc[e].z);
-                other.w = exch(acc[e].w);
-                acc[e] = acc[e] * c0 + other * c1;
-            }
-            m = mn;
-        }
-        const unsigned slotix = unsigned(h) * SMAX + unsigned(sp);
-        if (slot == 0) {
-            const unsigned ao = SOFF(pacc) + (slotix * HD + sub * 4u) * 4u;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) stx4(rs, ao + 256u * e, acc[e]);
-        }
-        if (lane == 0) {
-            gml[2 * g] = m;
-            gml[2 * g + 1] = lsum;
-        }
+        attn_chunk(wb, q, first, end, m, lsum, acc);
     }
-    // every head's sums are complete in memory before any (max, sum) pair is
+    // merge the 4 position slots
+#pragma unroll
+    for (int o = 16; o < 64; o <<= 1) {
+        auto exch = [o](float v) { return o == 16 ? lane_xor<16>(v) : lane_xor<32>(v); };
+        const float mo = exch(m), lo = exch(lsum);
+        const float mn = fmaxf(m, mo);
+        const float c0 = m == -INFINITY ? 0.f : expf(m - mn), c1 = mo == -INFINITY ? 0.f : expf(mo - mn);
+        lsum = lsum * c0 + lo * c1;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            f4 other;
+            other.x = exch(acc[e].x);
+            other.y = exch(acc[e].y);
+            other.z = exch(acc[e].z);
+            other.w = exch(acc[e].w);
+            acc[e] = acc[e] * c0 + other * c1;
+        }
+        m = mn;
+    }
+    const unsigned slotix = unsigned(h) * SMAX + unsigned(sp);
+    if (slot == 0) {
+        const unsigned ao = SOFF(pacc) + (slotix * HD + sub * 4u) * 4u;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) stx4(rs, ao + 256u * e, acc[e]);
+    }
+    // the weighted sums are complete in memory before their (max, sum) pair is
     __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
     compiler_fence();
     if (lane == 0) {
-#pragma unroll
-        for (int g = 0; g < NH / NKV; ++g) {
-            const unsigned slotix = unsigned(kvh * (NH / NKV) + g) * SMAX + unsigned(sp);
-            stt(rs, SOFF(pml) + slotix * 16u, gml[2 * g], t);
-            stt(rs, SOFF(pml) + slotix * 16u + 8u, gml[2 * g + 1], t);
-        }
+        const unsigned t = tag(a, p);
+        stt(rs, SOFF(pml) + slotix * 16u, m, t);
+        stt(rs, SOFF(pml) + slotix * 16u + 8u, lsum, t);
     }
     return true;
 }
@@ -988,11 +1007,14 @@ __device__ __forceinline__ bool phase_comb(const Args& a, Rs rs, int p, int u, L
     const int h = u / (HD / 4), c4 = u % (HD / 4);
     const unsigned want = tag(a, p - 1);
     const unsigned long long start = wall_clock64();
+    // the gate (q_proj's second half, written two phases back) in flight with the polls
+    const unsigned go = SOFF(mixed) + unsigned(h * 2 * HD + HD + 4 * c4 + int(lane & 3)) * 8u;
+    const f2 gpair = ldx2(rs, go);
     float mv[COMB_PER_LANE], lv[COMB_PER_LANE];
     float mm = -INFINITY;
+    bool live[COMB_PER_LANE];
     {
         unsigned po[COMB_PER_LANE];
-        bool live[COMB_PER_LANE];
         f2 ml[COMB_PER_LANE];
 #pragma unroll
         for (int k = 0; k < COMB_PER_LANE; ++k) {
@@ -1009,17 +1031,20 @@ __device__ __forceinline__ bool phase_comb(const Args& a, Rs rs, int p, int u, L
         }
     }
     mm = wave_maximum(mm);
+    // every split's weighted sums in flight at once (dead lanes read split 0)
+    f4 pv[COMB_PER_LANE];
+#pragma unroll
+    for (int k = 0; k < COMB_PER_LANE; ++k) {
+        const unsigned ix = unsigned(h) * SMAX + (live[k] ? unsigned(lane) + 64u * k : 0u);
+        pv[k] = ldx4(rs, SOFF(pacc) + (ix * HD + unsigned(4 * c4)) * 4u);
+    }
     float den = 0.f;
     f4 num = f4(0.f);
 #pragma unroll
     for (int k = 0; k < COMB_PER_LANE; ++k) {
-        const int s = int(lane) + 64 * k;
-        if (s < splits) {
-            const unsigned ix = unsigned(h) * SMAX + unsigned(s);
-            const float wgt = expf(mv[k] - mm);
-            den += lv[k] * wgt;
-            num += ldx4(rs, SOFF(pacc) + (ix * HD + unsigned(4 * c4)) * 4u) * wgt;
-        }
+        const float wgt = live[k] ? expf(mv[k] - mm) : 0.f;
+        den += lv[k] * wgt;
+        num += pv[k] * wgt;
     }
     den = wave_total(den);
     num.x = wave_total(num.x);
@@ -1029,7 +1054,7 @@ __device__ __forceinline__ bool phase_comb(const Args& a, Rs rs, int p, int u, L
     if (lane < 4) {
         const float val = lane == 0 ? num.x : lane == 1 ? num.y : lane == 2 ? num.z : num.w;
         const int d = 4 * c4 + int(lane);
-        const float gate = wait1(a, rs, SOFF(mixed) + unsigned(h * 2 * HD + HD + d) * 8u, tag(a, p - 2), l, start, p);
+        const float gate = __float_as_uint(gpair.y) == tag(a, p - 2) ? gpair.x : wait1(a, rs, go, tag(a, p - 2), l, start, p);
         stt(rs, SOFF(ctx) + unsigned(h * HD + d) * 8u, (val / den) * sigmoidf_(gate), tag(a, p));
     }
     return true;

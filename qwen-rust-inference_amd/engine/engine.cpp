@@ -4,6 +4,7 @@
 // reference's own Rust engine binds the same bridge unchanged.
 #include <dlfcn.h>
 
+#include <atomic>
 #include <chrono>
 #include <cmath>
 #include <cstdio>
@@ -408,6 +409,10 @@ struct QeModel {
     std::vector<DeviceBlock> blocks;
     uint64_t run_budget = uint64_t(4) << 30;  // MAX_RUN_BYTES
     std::string info;
+    // Runs hold the model (the reference's DeviceRun borrows it, so it
+    // outlives them): qe_model_free marks it, the last run's free releases it.
+    std::atomic<int> runs{0};
+    bool released = false;
 
     const DeviceMatrix& output() const { return lm_head ? *lm_head : embedding; }
 
@@ -1095,14 +1100,18 @@ QeModel* qe_model_load(const char* bridge_path, int expect_kind, const QwConfig*
     return out;
 }
 
-void qe_model_free(QeModel* m) {
-    if (!m) return;
+static void destroy_model(QeModel* m) {
     // Buffers free through the api: release them before the context goes.
     m->blocks.clear();
     m->embedding = DeviceMatrix{};
     m->lm_head.reset();
     m->norm = Buffer{};
     delete m;
+}
+void qe_model_free(QeModel* m) {
+    if (!m) return;
+    m->released = true;
+    if (m->runs.load() == 0) destroy_model(m);
 }
 
 const char* qe_model_info(QeModel* m) { return m->info.c_str(); }
@@ -1160,10 +1169,16 @@ QeRun* qe_run_new(QeModel* m, int64_t capacity, int64_t chunk, int64_t snapshots
         r->model = m;
         r->build(size_t(capacity), size_t(chunk), size_t(snapshots));
         out = r.release();
+        ++m->runs;
     });
     return out;
 }
-void qe_run_free(QeRun* r) { delete r; }
+void qe_run_free(QeRun* r) {
+    if (!r) return;
+    QeModel* m = r->model;
+    delete r;  // its buffers go back through the model's bridge first
+    if (m && --m->runs == 0 && m->released) destroy_model(m);
+}
 
 int qe_run_decode_plan(QeRun* r) { return r && r->plan ? 1 : 0; }
 
