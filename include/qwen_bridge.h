@@ -187,6 +187,15 @@ typedef struct QrDecodePlan QrDecodePlan;
 /* Non-zero (with qr_error set) when this bridge has no one-launch decode for the shape. */
 int qr_decode_plan(Context* c, const QrDecodeDesc* d, QrDecodePlan** out);
 int qr_decode_step(Context* c, QrDecodePlan* p, int token, int position);
+/* n greedy one-launch steps queued back to back: step k runs at position + k
+ * on first_token (k = 0) or on step k-1's argmax, which the kernel reads from
+ * the device, so the host does not wait between steps. ids[k] = step k's
+ * argmax (-1 where the step failed); *bad = 0 when every step's logits were
+ * finite, else the largest non-finite count (1e30 when a step did not finish).
+ * No counterpart in the reference's ABI: its step_greedy reads each argmax
+ * back before the next step (src/device.rs:1568-1584); the tokens are the
+ * same. */
+int qr_decode_steps(Context* c, QrDecodePlan* p, int first_token, int position, int n, int32_t* ids, float* bad);
 void qr_decode_plan_free(Context* c, QrDecodePlan* p);
 
 /* Embedding rows of a prefill chunk in one call: dst[r, 0..width) = row

@@ -566,7 +566,30 @@ int qr_decode_plan(Context* c, const QrDecodeDesc* d, QrDecodePlan** out) {
 int qr_decode_step(Context* c, QrDecodePlan* p, int token, int position) {
     if (!p) return fail(c, "decode step without a plan", -1);
     auto sc = scope(c, [&] { return std::string("decode_step"); });
-    return launched(c, "decode step", qr::decode_step(p, token, position, c->stream));
+    if (token < 0) return fail(c, "decode step token", -1);
+    return launched(c, "decode step", qr::decode_step(p, token, position, -1, c->stream));
+}
+int qr_decode_steps(Context* c, QrDecodePlan* p, int first_token, int position, int n, int32_t* ids, float* bad) {
+    if (!p || !ids || !bad || n < 1 || first_token < 0 || position < 0) return fail(c, "decode steps shape", -1);
+    int e = qr::decode_history_clear(p, n, c->stream);
+    if (e) return launched(c, "decode steps", e);
+    for (int k = 0; k < n; ++k) {
+        auto sc = scope(c, [&] { return std::string("decode_step"); });
+        e = qr::decode_step(p, k == 0 ? first_token : -1, position + k, k, c->stream);
+        if (e) return launched(c, "decode steps", e);
+    }
+    std::vector<float> h(2 * size_t(n));
+    e = qr::decode_history_read(p, n, h.data(), c->stream);
+    if (e) return launched(c, "decode steps", e);
+    float worst = 0.f;
+    for (int k = 0; k < n; ++k) {
+        const float idx = h[2 * size_t(k)], b = h[2 * size_t(k) + 1];
+        const bool ok = b == 0.f && idx >= 0.f && idx < 2147483648.f;  // NaN: the step never wrote its slot
+        ids[k] = ok ? int32_t(idx) : -1;
+        if (!ok) worst = b == b && b > 0.f ? (b > worst ? b : worst) : 1e30f;
+    }
+    *bad = worst;
+    return 0;
 }
 void qr_decode_plan_free(Context* c, QrDecodePlan* p) {
     if (c) (void)hipStreamSynchronize(c->stream);

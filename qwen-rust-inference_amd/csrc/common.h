@@ -113,7 +113,11 @@ size_t attention_scratch_needed(const Params& a);
 const char* decode_unsupported(const QrDecodeDesc& d);
 int decode_plan_create(const QrDecodeDesc& d, QrDecodePlan** out, hipStream_t s, const char** why);
 void decode_plan_free(QrDecodePlan* p);
-int decode_step(QrDecodePlan* p, int token, int position, hipStream_t s);
+// token -1: the previous launch's argmax (read on the device). slot >= 0: the
+// step's [argmax, non-finite count] also goes to history slot `slot`.
+int decode_step(QrDecodePlan* p, int token, int position, int slot, hipStream_t s);
+int decode_history_clear(QrDecodePlan* p, int n, hipStream_t s);
+int decode_history_read(QrDecodePlan* p, int n, float* out, hipStream_t s);
 
 // delta_chunk.hip ------------------------------------------------------------
 // DeltaRule / DeltaRuleGated over a prefill chunk in the WY form (key_dim ==

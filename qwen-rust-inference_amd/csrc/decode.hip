@@ -102,6 +102,8 @@ struct Args {
     Scratch* s;
     int token, pos, vocab, nphases;
     int emb_bf16;  // the embedding table is packed BF16 (two per word, element 2i low)
+    int chain;     // 1: the token is the previous launch's argmax (picks[0]), not `token`
+    float* hist;   // when set: this launch's [argmax, non-finite count] also lands here
     unsigned epoch;
     float eps;
     float rope_cs[ROT / 2], rope_sn[ROT / 2];  // cos / sin of pos / theta^(2i / rot)
@@ -227,6 +229,7 @@ struct Lds {
     alignas(16) float nw[2][H];             // staged (1 + w) norm weights, by phase parity
     alignas(16) float wave[WAVES][2 * HD];  // wave-private scratch
     int fail;  // the earliest phase in which a lane of the block timed out (kNoFail: none)
+    int token;  // this launch's token
 };
 constexpr int kNoFail = 0x7fffffff;
 
@@ -347,7 +350,7 @@ __device__ __forceinline__ void stage_input(const Args& a, Rs rs, int L, int pro
         const int t = int(threadIdx.x);
         if (Q8 && a.emb_bf16) {
             if (t < H / 8) {
-                const f4 wv = ldp4(rsrc(a.embedding), unsigned(a.token) * unsigned(H * 2) + 16u * unsigned(t), 0);
+                const f4 wv = ldp4(rsrc(a.embedding), unsigned(l.token) * unsigned(H * 2) + 16u * unsigned(t), 0);
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
                     const unsigned w = __float_as_uint(wv[j]);
@@ -357,7 +360,7 @@ __device__ __forceinline__ void stage_input(const Args& a, Rs rs, int L, int pro
             }
         } else if (t < H / 4) {
             *reinterpret_cast<f4*>(&l.act[par][4 * t]) =
-                ldp4(rsrc(a.embedding), unsigned(a.token) * unsigned(H * 4) + 16u * unsigned(t), 0);
+                ldp4(rsrc(a.embedding), unsigned(l.token) * unsigned(H * 4) + 16u * unsigned(t), 0);
         }
     } else {
         stage_tagged<H>(a, rs, SOFF(x), tag(a, producer), l.act[par], l, p);
@@ -367,11 +370,11 @@ template <bool Q8>
 __device__ __forceinline__ float input_at(const Args& a, Rs rs, int L, int producer, int i, Lds& l, int p) {
     if (L == 0) {
         if (Q8 && a.emb_bf16) {
-            const unsigned e = unsigned(a.token) * unsigned(H) + unsigned(i);
+            const unsigned e = unsigned(l.token) * unsigned(H) + unsigned(i);
             const unsigned w = __float_as_uint(ldp(rsrc(a.embedding), e / 2u * 4u));
             return __uint_as_float((i & 1) ? (w & 0xffff0000u) : (w << 16));
         }
-        return ldp(rsrc(a.embedding), (unsigned(a.token) * unsigned(H) + unsigned(i)) * 4u);
+        return ldp(rsrc(a.embedding), (unsigned(l.token) * unsigned(H) + unsigned(i)) * 4u);
     }
     return wait1(a, rs, SOFF(x) + 8u * unsigned(i), tag(a, producer), l, wall_clock64(), p);
 }
@@ -1213,6 +1216,11 @@ __device__ __forceinline__ void phase_arg(const Args& a, Rs rs, int p, Lds& l) {
         const Rs pk = rsrc(a.picks);
         stp(pk, 0, float(at));
         stp(pk, 4, float(bad));
+        if (a.hist) {
+            const Rs hs = rsrc(a.hist);
+            stp(hs, 0, float(at));
+            stp(hs, 4, float(bad));
+        }
     }
 }
 
@@ -1242,7 +1250,15 @@ __global__ __launch_bounds__(THREADS, 1) void decode_kernel(Args a) {
     // descriptors derived from it in SGPRs)
     const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x >> 6));
     const int unit = wave * BLOCKS + int(blockIdx.x);  // rows spread wave-major over blocks
-    if (threadIdx.x == 0) l.fail = kNoFail;
+    if (threadIdx.x == 0) {
+        l.fail = kNoFail;
+        int tok = a.token;
+        if (a.chain) {  // the previous launch's argmax (kernel boundary: its stores are visible)
+            const float f = ldp(rsrc(a.picks), 0);
+            tok = f >= 0.f && f < float(a.vocab) ? int(f) : 0;  // a bad step is reported by its own slot
+        }
+        l.token = tok;
+    }
     __syncthreads();
     const Rs rs = rsrc(a.s);
     f4 wb[WBUF];
@@ -1291,6 +1307,7 @@ struct QrDecodePlan {
     std::vector<float> host_denom;  // theta^(2i / rot) by the host libm
     int capacity = 0;
     bool q8 = false;  // int8 matrices and LM head: decode_kernel<true>
+    float* hist = nullptr;  // [capacity][argmax, non-finite count] of chained steps
 };
 
 namespace qr {
@@ -1386,6 +1403,7 @@ int decode_plan_create(const QrDecodeDesc& d, QrDecodePlan** out, hipStream_t s,
     unsigned epoch = 0;
     hipError_t e = hipMalloc(reinterpret_cast<void**>(&p->layers), sizeof(QrDecodeLayer) * size_t(d.layers));
     if (e == hipSuccess) e = scratch_acquire(dev, s, &p->scratch, &epoch);
+    if (e == hipSuccess) e = hipMalloc(reinterpret_cast<void**>(&p->hist), sizeof(float) * 2 * size_t(d.capacity));
     p->args.epoch = epoch;  // what decode_plan_free hands back with the buffer
     // RoPE denominators theta^(2i / rot) by the host libm (the reference's
     // expression, src/attention.rs:49-50), as the op path's table
@@ -1429,15 +1447,19 @@ int decode_plan_create(const QrDecodeDesc& d, QrDecodePlan** out, hipStream_t s,
 void decode_plan_free(QrDecodePlan* p) {
     if (!p) return;
     if (p->layers) (void)hipFree(p->layers);
+    if (p->hist) (void)hipFree(p->hist);
     if (p->scratch) scratch_release(p->device, p->scratch, p->args.epoch);
     delete p;
 }
 
-int decode_step(QrDecodePlan* p, int token, int position, hipStream_t s) {
+int decode_step(QrDecodePlan* p, int token, int position, int slot, hipStream_t s) {
     using namespace dec;
     Args& a = p->args;
-    if (token < 0 || token >= a.vocab || position < 0 || position >= p->capacity) return int(hipErrorInvalidValue);
-    a.token = token;
+    if (token < -1 || token >= a.vocab || position < 0 || position >= p->capacity || slot >= p->capacity)
+        return int(hipErrorInvalidValue);
+    a.chain = token < 0 ? 1 : 0;
+    a.token = token < 0 ? 0 : token;
+    a.hist = slot < 0 ? nullptr : p->hist + 2 * slot;
     a.pos = position;
     // RoPE angle pos / theta^(2i / rot) and its cos / sin on the host
     // (reference: src/attention.rs:49-55, the same f32 expressions)
@@ -1455,6 +1477,16 @@ int decode_step(QrDecodePlan* p, int token, int position, hipStream_t s) {
     const void* k = p->q8 ? reinterpret_cast<const void*>(decode_kernel<true>)
                           : reinterpret_cast<const void*>(decode_kernel<false>);
     return int(hipLaunchCooperativeKernel(k, dim3(BLOCKS), dim3(THREADS), args, 0, s));
+}
+int decode_history_clear(QrDecodePlan* p, int n, hipStream_t s) {
+    if (n < 1 || n > p->capacity) return int(hipErrorInvalidValue);
+    return int(hipMemsetAsync(p->hist, 0xff, sizeof(float) * 2 * size_t(n), s));  // NaN: slot never written
+}
+int decode_history_read(QrDecodePlan* p, int n, float* out, hipStream_t s) {
+    if (n < 1 || n > p->capacity) return int(hipErrorInvalidValue);
+    hipError_t e = hipMemcpyAsync(out, p->hist, sizeof(float) * 2 * size_t(n), hipMemcpyDeviceToHost, s);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    return int(e);
 }
 
 }  // namespace qr

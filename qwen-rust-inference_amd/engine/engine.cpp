@@ -89,6 +89,7 @@ struct Api {
     int (*delta_mixer)(Context*, const QrDelta*) = nullptr;
     int (*decode_plan)(Context*, const QrDecodeDesc*, QrDecodePlan**) = nullptr;
     int (*decode_step)(Context*, QrDecodePlan*, int, int) = nullptr;
+    int (*decode_steps)(Context*, QrDecodePlan*, int, int, int, int32_t*, float*) = nullptr;
     void (*decode_free)(Context*, QrDecodePlan*) = nullptr;
     int (*embed_rows)(Context*, float*, const float*, int, int, int, const int32_t*, int) = nullptr;
     int (*profile)(Context*, int) = nullptr;
@@ -159,6 +160,7 @@ struct Api {
             decode_plan = symbol<decltype(decode_plan)>("qr_decode_plan", false);
             decode_step = symbol<decltype(decode_step)>("qr_decode_step", false);
             decode_free = symbol<decltype(decode_free)>("qr_decode_plan_free", false);
+            decode_steps = symbol<decltype(decode_steps)>("qr_decode_steps", false);
             if (!decode_plan || !decode_step || !decode_free) decode_plan = nullptr;
         }
         if (!(disable & QE_NO_EMBED_ROWS)) embed_rows = symbol<decltype(embed_rows)>("qr_embed_rows", false);
@@ -1352,6 +1354,31 @@ int qe_decode_greedy(QeRun* r, uint32_t first, int64_t n_new, uint32_t* ids, dou
     return guarded([&] {
         double total = 0;
         uint32_t token = first;
+        // the planned steps of step_greedy (forward's one-launch conditions),
+        // queued back to back with one read-back
+        if (n_new > 1 && r->plan && r->api()->decode_steps && r->snapshot_rows == 0 && r->pick_slot == 0) {
+            const Api* a = r->api();
+            require(!r->failed, "device run failed; reset required");
+            require(first < uint32_t(r->model->config.vocab_size) && r->position + size_t(n_new - 1) <= r->capacity,
+                    "device token/capacity out of bounds");
+            std::vector<int32_t> got(size_t(n_new - 1));
+            float bad = 0.f;
+            r->pending.reset();
+            auto t0 = std::chrono::steady_clock::now();
+            const int st = a->decode_steps(a->ctx, r->plan, int(first), int(r->position), int(n_new - 1), got.data(), &bad);
+            total = std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
+            r->position += size_t(n_new - 1);
+            r->logits_unread = true;
+            if (st != 0 || bad != 0.f) r->failed = true;
+            a->check(st);
+            require(bad < 1e30f, "one-launch decode step timed out at a stage barrier");
+            require(bad == 0.f, "non-finite logits");
+            ids[0] = first;
+            for (size_t i = 0; i < got.size(); ++i) ids[i + 1] = uint32_t(got[i]);
+            r->picked = {ids[n_new - 1]};
+            if (seconds) *seconds = total;
+            return;
+        }
         for (int64_t i = 0; i < n_new; ++i) {
             ids[i] = token;
             if (i + 1 == n_new) break;

@@ -347,3 +347,23 @@ def test_qwen08b_int8_one_launch_against_dequantised_oracle(qwen08b):
     for i, t in enumerate([int(v) for v in np.random.default_rng(6).integers(0, c.vocab_size, 4)]):
         print(f"int8 one-launch step {i} against the dequantised oracle", flush=True)
         parity(run.step(t), st.step(t, O.VECTOR), rtol=INT8_RTOL, where=f"int8 one-launch step {i}")
+
+
+def test_qwen08b_chained_greedy_equals_stepwise(qwen08b_models):
+    """decode_greedy queues its one-launch steps back to back, each kernel
+    reading the previous step's argmax on the device (qr_decode_steps): the
+    same IDs and bitwise the same states as one step_greedy call per token."""
+    fast, _ = qwen08b_models
+    prompt = [int(v) for v in np.random.default_rng(8).integers(0, 248320, 40)]
+    runs = [fast.new_run(96, chunk=64) for _ in range(2)]
+    first = [O.select_greedy(r.prefill(prompt)) for r in runs]
+    assert first[0] == first[1]
+    chained, _ = runs[0].decode_greedy(first[0], 17)
+    stepped = [first[1]]
+    for _ in range(16):
+        stepped.append(runs[1].step_greedy(stepped[-1]))
+    assert chained == stepped
+    assert runs[0].position == runs[1].position == 40 + 16
+    for layer in (0, 3, 23):
+        for which in range(4):
+            assert np.array_equal(runs[0].state(layer, which), runs[1].state(layer, which)), (layer, which)
