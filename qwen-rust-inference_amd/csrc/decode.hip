@@ -520,10 +520,12 @@ __device__ __forceinline__ bool phase_din(const Args& a, Rs rs, LayerP w, int L,
         sum += h1 * c1;
         sum += h2 * c2;
         sum += mine * c3;
+        // the tagged output first: stores leave in order, and a wave's stores
+        // queue behind the memory traffic of its CU
+        stt(rs, SOFF(proj) + 8u * unsigned(row), silu(sum), t);
         stp(hs, ho, h1);
         stp(hs, ho + 4, h2);
         stp(hs, ho + 8, mine);
-        stt(rs, SOFF(proj) + 8u * unsigned(row), silu(sum), t);
     } else if (lane < DIN_RPW && row < DIN_ROWS) {
         stt(rs, SOFF(ab) + 8u * unsigned(row - CH), mine, t);
     }
@@ -582,15 +584,26 @@ __device__ __forceinline__ bool phase_mix(const Args& a, Rs rs, LayerP w, int L,
     const unsigned lane = lane_id();
     const int wave = int(threadIdx.x >> 6);
     const int h = u >> 3, cg = u & 7, pr = int(lane >> 4), j = cg * 16 + int(lane & 15);
-    const float dt = w->gates[h], alog = w->gates[VH + h];
     // convolved q and k of head h (lane: q[lane], q[lane + 64], k[lane], k[lane + 64]), v of column j
     const unsigned want = tag(a, p - 1);
     const unsigned long long start = wall_clock64();
     const unsigned qo = SOFF(proj) + (unsigned(h) * DK + lane) * 8u, ko = qo + KD * 8u;
     const unsigned mo[7] = {qo, qo + 512u, ko, ko + 512u, SOFF(proj) + unsigned(2 * KD + h * DV + j) * 8u,
                             SOFF(ab) + 8u * unsigned(h), SOFF(ab) + 8u * unsigned(VH + h)};
+    f2 raw[7];
+#pragma unroll
+    for (int k = 0; k < 7; ++k) raw[k] = ldx2(rs, mo[k]);
+    // the gate parameters while the polls are in flight
+    float dt = w->gates[h], alog = w->gates[VH + h];
+    asm volatile("" : "+v"(dt), "+v"(alog));
     float mv[7];
-    wait1n<7>(a, rs, mo, want, mv, l, start, p);
+    bool ready = true;
+#pragma unroll
+    for (int k = 0; k < 7; ++k) {
+        mv[k] = raw[k].x;
+        ready = ready && __float_as_uint(raw[k].y) == want;
+    }
+    if (!ready) wait1n<7>(a, rs, mo, want, mv, l, start, p);
     const float q0 = mv[0], q1 = mv[1], k0 = mv[2], k1 = mv[3], v = mv[4], av = mv[5], bv = mv[6];
     // L2 norms (reference.h:134-143), q / sqrt(dk)
     const float sq = wave_total(q0 * q0 + q1 * q1);
@@ -624,6 +637,7 @@ __device__ __forceinline__ bool phase_mix(const Args& a, Rs rs, LayerP w, int L,
         o = fdot4(wb[k], lds4(qq + 4 * k), o);
     }
     o = column_sum(o);
+    if (pr == 0) stt(rs, SOFF(core) + unsigned(h * DV + j) * 8u, o, t);  // the consumers' value first
     const Rs S = rsrc(w->recurrent);
     const unsigned base = ((unsigned(h) * DK + unsigned(pr) * 32u) * DV + unsigned(j)) * 4u;
 #pragma unroll
@@ -634,7 +648,6 @@ __device__ __forceinline__ bool phase_mix(const Args& a, Rs rs, LayerP w, int L,
         stp(S, so + 2u * DV * 4u, wb[k].z);
         stp(S, so + 3u * DV * 4u, wb[k].w);
     }
-    if (pr == 0) stt(rs, SOFF(core) + unsigned(h * DV + j) * 8u, o, t);
     return true;
 }
 
