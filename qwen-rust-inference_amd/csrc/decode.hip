@@ -1300,6 +1300,12 @@ __global__ __launch_bounds__(THREADS, 1) void decode_kernel(Args a) {
         default: break;
         }
         if (!ok) return;
+        // every wave of the block has issued its outputs before any issues the
+        // next phase's loads, which would otherwise queue ahead of a late
+        // wave's output stores in the CU's memory pipeline
+        compiler_fence();
+        __builtin_amdgcn_s_barrier();
+        compiler_fence();
         // T_COMB reads no weights: the rows of the phase after it are fetched
         // before it (at the end of T_ATTN) instead of after it.
         if (t == T_COMB) continue;
