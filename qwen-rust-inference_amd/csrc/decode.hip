@@ -270,6 +270,21 @@ __device__ float wait1(const Args& a, Rs r, unsigned off, unsigned want, Lds& l,
 // Several polls at once: every load is issued before any tag is checked, so
 // one round trip serves all of them when their producers are done; an entry
 // not yet tagged `want` falls back to its own poll. live[k] false: skipped.
+// The same, from first reads already issued into v (other loads may have been
+// issued after them: they stay in flight while these are checked).
+template <int N>
+__device__ __forceinline__ void wait2n_from(const Args& a, Rs r, const unsigned (&off)[N], const bool (&live)[N],
+                                            unsigned want, const f4 (&v)[N], f2 (&out)[N], Lds& l,
+                                            unsigned long long start, int p) {
+#pragma unroll
+    for (int k = 0; k < N; ++k) {
+        if (!live[k]) continue;
+        if (__float_as_uint(v[k].y) == want && __float_as_uint(v[k].w) == want)
+            out[k] = f2{v[k].x, v[k].z};
+        else
+            out[k] = wait2(a, r, off[k], want, l, start, p);
+    }
+}
 template <int N>
 __device__ __forceinline__ void wait2n(const Args& a, Rs r, const unsigned (&off)[N], const bool (&live)[N],
                                        unsigned want, f2 (&out)[N], Lds& l, unsigned long long start, int p) {
@@ -316,21 +331,31 @@ __device__ __forceinline__ float silu(float x) { return x * sigmoidf_(x); }
 // The block's 512 threads copy N (even) tagged values at scratch offset `off`
 // into dst, each pair polled until tagged `want` (all of a thread's polls in
 // flight together).
-template <int N>
+// `mid` runs between the first reads and their check: loads it issues (the
+// second half of this phase's weights) queue behind the polls, not ahead.
+struct NoMid {
+    __device__ void operator()() const {}
+};
+template <int N, class Mid = NoMid>
 __device__ __forceinline__ void stage_tagged(const Args& a, Rs rs, unsigned off, unsigned want, float* dst, Lds& l,
-                                             int p) {
+                                             int p, Mid&& mid = Mid()) {
     constexpr int PAIRS = N / 2, K = (PAIRS + THREADS - 1) / THREADS;
     const unsigned long long start = wall_clock64();
     unsigned o[K];
     bool live[K];
+    f4 first[K];
     f2 v[K];
 #pragma unroll
     for (int k = 0; k < K; ++k) {
         const int i = int(threadIdx.x) + THREADS * k;
         live[k] = i < PAIRS;
         o[k] = off + 16u * unsigned(i);
+        if (live[k]) first[k] = ldx4(rs, o[k]);
     }
-    wait2n<K>(a, rs, o, live, want, v, l, start, p);
+    mid();
+    // keep mid's loads ahead of the first check (which waits for the polls)
+    asm volatile("" ::: "memory");
+    wait2n_from<K>(a, rs, o, live, want, first, v, l, start, p);
 #pragma unroll
     for (int k = 0; k < K; ++k)
         if (live[k]) *reinterpret_cast<f2*>(dst + 2 * (int(threadIdx.x) + THREADS * k)) = v[k];
@@ -344,9 +369,11 @@ __device__ __forceinline__ void stage_norm(const float* w, int par, Lds& l) {
 // The layer's input residual into l.act[par]: the token's embedding row for
 // layer 0 (BF16 tables only with int8 matrices, as the reference's int8
 // upload keeps the embedding BF16), else x as written by phase `producer`.
-template <bool Q8>
-__device__ __forceinline__ void stage_input(const Args& a, Rs rs, int L, int producer, int par, Lds& l, int p) {
+template <bool Q8, class Mid = NoMid>
+__device__ __forceinline__ void stage_input(const Args& a, Rs rs, int L, int producer, int par, Lds& l, int p,
+                                            Mid&& mid = Mid()) {
     if (L == 0) {
+        mid();
         const int t = int(threadIdx.x);
         if (Q8 && a.emb_bf16) {
             if (t < H / 8) {
@@ -363,7 +390,7 @@ __device__ __forceinline__ void stage_input(const Args& a, Rs rs, int L, int pro
                 ldp4(rsrc(a.embedding), unsigned(l.token) * unsigned(H * 4) + 16u * unsigned(t), 0);
         }
     } else {
-        stage_tagged<H>(a, rs, SOFF(x), tag(a, producer), l.act[par], l, p);
+        stage_tagged<H>(a, rs, SOFF(x), tag(a, producer), l.act[par], l, p, mid);
     }
 }
 template <bool Q8>
@@ -474,12 +501,18 @@ __device__ __forceinline__ void din_load(LayerP w, int u, f4* wb) {
     else if (row < DIN_ROWS)
         load_row_h<Q8, 4 * R>(wb, rsrc(w->b), row - CH - VH, VH);
 }
+// Weights of the heavier phases are fetched in two parts: part 0 after the
+// previous phase, part 1 after the phase's own first polls (so the polls are
+// not queued behind all of it).
 template <bool Q8>
-__device__ __forceinline__ void prefetch_din(LayerP w, int u, f4* wb) {
-    din_load<Q8, 0>(w, u, wb);
-    din_load<Q8, 1>(w, u, wb);
-    din_load<Q8, 2>(w, u, wb);
-    din_load<Q8, 3>(w, u, wb);
+__device__ __forceinline__ void prefetch_din(LayerP w, int u, f4* wb, int part) {
+    if (part == 0) {
+        din_load<Q8, 0>(w, u, wb);
+        din_load<Q8, 1>(w, u, wb);
+    } else {
+        din_load<Q8, 2>(w, u, wb);
+        din_load<Q8, 3>(w, u, wb);
+    }
 }
 template <bool Q8, int R>
 __device__ __forceinline__ void din_row(const f4* wb, const f4 (&xv)[4], int u, float& mine) {
@@ -489,7 +522,7 @@ __device__ __forceinline__ void din_row(const f4* wb, const f4 (&xv)[4], int u, 
     }
 }
 template <bool Q8>
-__device__ __forceinline__ bool phase_din(const Args& a, Rs rs, LayerP w, int L, int p, int u, const f4* wb, Lds& l) {
+__device__ __forceinline__ bool phase_din(const Args& a, Rs rs, LayerP w, int L, int p, int u, f4* wb, Lds& l) {
     const int par = p & 1;
     const int lane = int(lane_id()), row = u * DIN_RPW + lane;
     const bool conv = lane < DIN_RPW && row < CH;
@@ -503,7 +536,7 @@ __device__ __forceinline__ bool phase_din(const Args& a, Rs rs, LayerP w, int L,
         c0 = ldp(cw, co), c1 = ldp(cw, co + 4), c2 = ldp(cw, co + 8), c3 = ldp(cw, co + 12);
     }
     stage_norm(w->input_norm, par, l);
-    stage_input<Q8>(a, rs, L, p - 1, par, l, p);
+    stage_input<Q8>(a, rs, L, p - 1, par, l, p, [&] { prefetch_din<Q8>(w, u, wb, 1); });
     if (!bsync(l, p)) return false;
     if (u * DIN_RPW >= DIN_ROWS) return true;
     f4 xv[4];
@@ -655,12 +688,15 @@ __device__ __forceinline__ bool phase_mix(const Args& a, Rs rs, LayerP w, int L,
 // reference.h:201-207) is built once per block in LDS (thread t: elements
 // 4t .. 4t+3, its head's 32 threads reduce the sum of squares), then
 // out_proj row u plus the residual.
-template <bool Q8, int COLS>
+// PART -1: the whole row; 0 / 1: the first / second half of an fp32 row
+// (int8: part 0 is the whole row).
+template <bool Q8, int COLS, int PART = -1>
 __device__ __forceinline__ void prefetch_row(const float* m, int row, int rows, f4* wb) {
     if (row >= rows) return;
     const Rs r = rsrc(m);
     const unsigned lo = 16u * lane_id();
     if constexpr (Q8) {
+        if (PART == 1) return;
         constexpr int NV = (COLS + 1023) / 1024;
         const unsigned ro = unsigned(rows) * 4u + unsigned(row) * unsigned(COLS);
 #pragma unroll
@@ -669,8 +705,9 @@ __device__ __forceinline__ void prefetch_row(const float* m, int row, int rows, 
         wb[NV] = f4{ldp(r, unsigned(row) * 4u), 0.f, 0.f, 0.f};
     } else {
         const unsigned ro = unsigned(row) * unsigned(COLS * 4);
+        constexpr int K = COLS / 256, V0 = PART == 1 ? K / 2 : 0, V1 = PART == 0 ? K / 2 : K;
 #pragma unroll
-        for (int v = 0; v < COLS / 256; ++v) wb[v] = ldw(r, lo + 1024u * v, ro);
+        for (int v = V0; v < V1; ++v) wb[v] = ldw(r, lo + 1024u * v, ro);
     }
 }
 template <bool Q8>
@@ -710,9 +747,11 @@ __device__ __forceinline__ void glu_load(LayerP w, int u, f4* wb) {
     }
 }
 template <bool Q8>
-__device__ __forceinline__ void prefetch_glu(LayerP w, int u, f4* wb) {
-    glu_load<Q8, 0>(w, u, wb);
-    glu_load<Q8, 1>(w, u, wb);
+__device__ __forceinline__ void prefetch_glu(LayerP w, int u, f4* wb, int part) {
+    if (part == 0)
+        glu_load<Q8, 0>(w, u, wb);
+    else
+        glu_load<Q8, 1>(w, u, wb);
 }
 template <bool Q8, int R>
 __device__ __forceinline__ void glu_row(Rs rs, const f4* wb, const f4 (&xv)[4], int u, unsigned t) {
@@ -723,10 +762,10 @@ __device__ __forceinline__ void glu_row(Rs rs, const f4* wb, const f4 (&xv)[4], 
     }
 }
 template <bool Q8>
-__device__ __forceinline__ bool phase_glu(const Args& a, Rs rs, LayerP w, int p, int u, const f4* wb, Lds& l) {
+__device__ __forceinline__ bool phase_glu(const Args& a, Rs rs, LayerP w, int p, int u, f4* wb, Lds& l) {
     const int par = p & 1;
     stage_norm(w->post_norm, par, l);
-    stage_tagged<H>(a, rs, SOFF(after), tag(a, p - 1), l.act[par], l, p);
+    stage_tagged<H>(a, rs, SOFF(after), tag(a, p - 1), l.act[par], l, p, [&] { prefetch_glu<Q8>(w, u, wb, 1); });
     if (!bsync(l, p)) return false;
     if (u * GLU_RPW >= I) return true;
     f4 xv[4];
@@ -738,9 +777,10 @@ __device__ __forceinline__ bool phase_glu(const Args& a, Rs rs, LayerP w, int p,
 
 // ---- T_DOWN: x = after + down . product
 template <bool Q8>
-__device__ __forceinline__ bool phase_down(const Args& a, Rs rs, int p, int u, const f4* wb, Lds& l) {
+__device__ __forceinline__ bool phase_down(const Args& a, Rs rs, LayerP w, int p, int u, f4* wb, Lds& l) {
     const int par = p & 1;
-    stage_tagged<I>(a, rs, SOFF(product), tag(a, p - 1), l.act[par], l, p);
+    stage_tagged<I>(a, rs, SOFF(product), tag(a, p - 1), l.act[par], l, p,
+                    [&] { prefetch_row<Q8, I, 1>(w->down, u, H, wb); });
     if (!bsync(l, p)) return false;
     if (u >= H) return true;
     const float acc = dot_row_lds<Q8, I / 256>(wb, l.act[par]);
@@ -761,10 +801,13 @@ __device__ __forceinline__ void aqkv_load(LayerP w, int u, f4* wb) {
         load_row_h<Q8, 4 * R>(wb, rsrc(w->v), row - QROWS - KVR, KVR);
 }
 template <bool Q8>
-__device__ __forceinline__ void prefetch_aqkv(LayerP w, int u, f4* wb) {
-    aqkv_load<Q8, 0>(w, u, wb);
-    aqkv_load<Q8, 1>(w, u, wb);
-    aqkv_load<Q8, 2>(w, u, wb);
+__device__ __forceinline__ void prefetch_aqkv(LayerP w, int u, f4* wb, int part) {
+    if (part == 0) {
+        aqkv_load<Q8, 0>(w, u, wb);
+        aqkv_load<Q8, 1>(w, u, wb);
+    } else {
+        aqkv_load<Q8, 2>(w, u, wb);
+    }
 }
 template <bool Q8, int R>
 __device__ __forceinline__ void aqkv_row(Rs rs, const f4* wb, const f4 (&xv)[4], int u, unsigned t) {
@@ -780,10 +823,10 @@ __device__ __forceinline__ void aqkv_row(Rs rs, const f4* wb, const f4 (&xv)[4],
     }
 }
 template <bool Q8>
-__device__ __forceinline__ bool phase_aqkv(const Args& a, Rs rs, LayerP w, int L, int p, int u, const f4* wb, Lds& l) {
+__device__ __forceinline__ bool phase_aqkv(const Args& a, Rs rs, LayerP w, int L, int p, int u, f4* wb, Lds& l) {
     const int par = p & 1;
     stage_norm(w->input_norm, par, l);
-    stage_input<Q8>(a, rs, L, p - 1, par, l, p);
+    stage_input<Q8>(a, rs, L, p - 1, par, l, p, [&] { prefetch_aqkv<Q8>(w, u, wb, 1); });
     if (!bsync(l, p)) return false;
     if (u * AQKV_RPW >= AQKV_ROWS) return true;
     f4 xv[4];
@@ -1243,12 +1286,12 @@ __device__ __forceinline__ void prefetch(const Args& a, int q, int u, f4* wb) {
     if (q >= a.nphases) return;
     const LayerP w = layer(a, player(a, q));
     switch (ptype(a, q)) {
-    case T_DIN: prefetch_din<Q8>(w, u, wb); break;
+    case T_DIN: prefetch_din<Q8>(w, u, wb, 0); break;
     case T_MIX: prefetch_mix<Q8>(w, u, wb); break;
     case T_DOUT: prefetch_row<Q8, VD>(w->out, u, H, wb); break;
-    case T_GLU: prefetch_glu<Q8>(w, u, wb); break;
-    case T_DOWN: prefetch_row<Q8, I>(w->down, u, H, wb); break;
-    case T_AQKV: prefetch_aqkv<Q8>(w, u, wb); break;
+    case T_GLU: prefetch_glu<Q8>(w, u, wb, 0); break;
+    case T_DOWN: prefetch_row<Q8, I, 0>(w->down, u, H, wb); break;
+    case T_AQKV: prefetch_aqkv<Q8>(w, u, wb, 0); break;
     case T_ATTN: prefetch_attn(w, u, a.pos, wb); break;
     case T_O: prefetch_row<Q8, NH * HD>(w->o, u, H, wb); break;
     case T_LM: prefetch_lm<Q8>(a, u, wb); break;
@@ -1291,7 +1334,7 @@ __global__ __launch_bounds__(THREADS, 1) void decode_kernel(Args a) {
         case T_MIX: ok = phase_mix<Q8>(a, rs, w, L, p, u, wb, l); break;
         case T_DOUT: ok = phase_dout<Q8>(a, rs, w, L, p, u, wb, l); break;
         case T_GLU: ok = phase_glu<Q8>(a, rs, w, p, u, wb, l); break;
-        case T_DOWN: ok = phase_down<Q8>(a, rs, p, u, wb, l); break;
+        case T_DOWN: ok = phase_down<Q8>(a, rs, w, p, u, wb, l); break;
         case T_AQKV: ok = phase_aqkv<Q8>(a, rs, w, L, p, u, wb, l); break;
         case T_ATTN: ok = phase_attn(a, rs, w, p, u, wb, l); break;
         case T_COMB: ok = phase_comb(a, rs, p, u, l); break;
