@@ -100,17 +100,14 @@ struct Args {
     float* logits;
     float* picks;
     Scratch* s;
-    int token, pos, vocab, nphases;
+    int token, pos, vocab, nlayers;
     int emb_bf16;  // the embedding table is packed BF16 (two per word, element 2i low)
     int chain;     // 1: the token is the previous launch's argmax (picks[0]), not `token`
     float* hist;   // when set: this launch's [argmax, non-finite count] also lands here
     unsigned epoch;
     float eps;
     float rope_cs[ROT / 2], rope_sn[ROT / 2];  // cos / sin of pos / theta^(2i / rot)
-    uint32_t phase[MAXPH];                     // type | layer << 8
 };
-__device__ __forceinline__ int ptype(const Args& a, int p) { return int(a.phase[p] & 255u); }
-__device__ __forceinline__ int player(const Args& a, int p) { return int(a.phase[p] >> 8); }
 // The layer table read through the constant address space: uniform indices
 // make scalar loads, so the weight pointers stay wave-uniform (in SGPRs).
 typedef const __attribute__((address_space(4))) QrDecodeLayer* LayerP;
@@ -1281,24 +1278,33 @@ __device__ __forceinline__ void phase_arg(const Args& a, Rs rs, int p, Lds& l) {
 }
 
 // ---------------------------------------------------------------- the kernel
+// Every wave of the block has issued its outputs before any issues the next
+// phase's loads, which would otherwise queue ahead of a late wave's output
+// stores in the CU's memory pipeline.
+__device__ __forceinline__ void out_barrier() {
+    compiler_fence();
+    __builtin_amdgcn_s_barrier();
+    compiler_fence();
+}
+// Part 0 of the first phase of layer L, or the LM head's first rows after the
+// last layer.
 template <bool Q8>
-__device__ __forceinline__ void prefetch(const Args& a, int q, int u, f4* wb) {
-    if (q >= a.nphases) return;
-    const LayerP w = layer(a, player(a, q));
-    switch (ptype(a, q)) {
-    case T_DIN: prefetch_din<Q8>(w, u, wb, 0); break;
-    case T_MIX: prefetch_mix<Q8>(w, u, wb); break;
-    case T_DOUT: prefetch_row<Q8, VD>(w->out, u, H, wb); break;
-    case T_GLU: prefetch_glu<Q8>(w, u, wb, 0); break;
-    case T_DOWN: prefetch_row<Q8, I, 0>(w->down, u, H, wb); break;
-    case T_AQKV: prefetch_aqkv<Q8>(w, u, wb, 0); break;
-    case T_ATTN: prefetch_attn(w, u, a.pos, wb); break;
-    case T_O: prefetch_row<Q8, NH * HD>(w->o, u, H, wb); break;
-    case T_LM: prefetch_lm<Q8>(a, u, wb); break;
-    default: break;
+__device__ __forceinline__ void prefetch_layer(const Args& a, int L, int u, f4* wb) {
+    if (L >= a.nlayers) {
+        prefetch_lm<Q8>(a, u, wb);
+        return;
     }
+    const LayerP w = layer(a, L);
+    if (w->attention)
+        prefetch_aqkv<Q8>(w, u, wb, 0);
+    else
+        prefetch_din<Q8>(w, u, wb, 0);
 }
 
+// Phase p (the tag index) runs, per DeltaNet layer, DIN MIX DOUT GLU DOWN and,
+// per attention layer, AQKV ATTN COMB O GLU DOWN, then LM and ARG: per layer
+// straight-line code, so the prefetch buffer flows from each phase into the
+// next without a dispatch between them.
 template <bool Q8>
 __global__ __launch_bounds__(THREADS, 1) void decode_kernel(Args a) {
     __shared__ Lds l;
@@ -1318,43 +1324,49 @@ __global__ __launch_bounds__(THREADS, 1) void decode_kernel(Args a) {
     __syncthreads();
     const Rs rs = rsrc(a.s);
     f4 wb[WBUF];
-    prefetch<Q8>(a, 0, unit, wb);
-    for (int p = 0; p < a.nphases; ++p) {
-        const int t = ptype(a, p);
-        if (t == T_ARG) {
-            if (blockIdx.x == 0) phase_arg(a, rs, p, l);
-            return;
-        }
-        const int L = player(a, p);
+    prefetch_layer<Q8>(a, 0, unit, wb);
+    int p = 0;
+    for (int L = 0; L < a.nlayers; ++L) {
         const LayerP w = layer(a, L);
-        const int u = opaque_uniform(unit);
-        bool ok = true;
-        switch (t) {
-        case T_DIN: ok = phase_din<Q8>(a, rs, w, L, p, u, wb, l); break;
-        case T_MIX: ok = phase_mix<Q8>(a, rs, w, L, p, u, wb, l); break;
-        case T_DOUT: ok = phase_dout<Q8>(a, rs, w, L, p, u, wb, l); break;
-        case T_GLU: ok = phase_glu<Q8>(a, rs, w, p, u, wb, l); break;
-        case T_DOWN: ok = phase_down<Q8>(a, rs, w, p, u, wb, l); break;
-        case T_AQKV: ok = phase_aqkv<Q8>(a, rs, w, L, p, u, wb, l); break;
-        case T_ATTN: ok = phase_attn(a, rs, w, p, u, wb, l); break;
-        case T_COMB: ok = phase_comb(a, rs, p, u, l); break;
-        case T_O: ok = phase_o<Q8>(a, rs, L, p, u, wb, l); break;
-        case T_LM: ok = phase_lm<Q8>(a, rs, p, u, wb, l); break;
-        default: break;
+        if (w->attention) {
+            if (!phase_aqkv<Q8>(a, rs, w, L, p, opaque_uniform(unit), wb, l)) return;
+            out_barrier();
+            prefetch_attn(w, opaque_uniform(unit), a.pos, wb);
+            ++p;
+            if (!phase_attn(a, rs, w, p, opaque_uniform(unit), wb, l)) return;
+            out_barrier();
+            prefetch_row<Q8, NH * HD>(w->o, opaque_uniform(unit), H, wb);  // T_COMB reads no weights
+            ++p;
+            if (!phase_comb(a, rs, p, opaque_uniform(unit), l)) return;
+            out_barrier();
+            ++p;
+            if (!phase_o<Q8>(a, rs, L, p, opaque_uniform(unit), wb, l)) return;
+        } else {
+            if (!phase_din<Q8>(a, rs, w, L, p, opaque_uniform(unit), wb, l)) return;
+            out_barrier();
+            prefetch_mix<Q8>(w, opaque_uniform(unit), wb);
+            ++p;
+            if (!phase_mix<Q8>(a, rs, w, L, p, opaque_uniform(unit), wb, l)) return;
+            out_barrier();
+            prefetch_row<Q8, VD>(w->out, opaque_uniform(unit), H, wb);
+            ++p;
+            if (!phase_dout<Q8>(a, rs, w, L, p, opaque_uniform(unit), wb, l)) return;
         }
-        if (!ok) return;
-        // every wave of the block has issued its outputs before any issues the
-        // next phase's loads, which would otherwise queue ahead of a late
-        // wave's output stores in the CU's memory pipeline
-        compiler_fence();
-        __builtin_amdgcn_s_barrier();
-        compiler_fence();
-        // T_COMB reads no weights: the rows of the phase after it are fetched
-        // before it (at the end of T_ATTN) instead of after it.
-        if (t == T_COMB) continue;
-        const int q = p + 1 < a.nphases && ptype(a, p + 1) == T_COMB ? p + 2 : p + 1;
-        prefetch<Q8>(a, q, opaque_uniform(unit), wb);
+        out_barrier();
+        prefetch_glu<Q8>(w, opaque_uniform(unit), wb, 0);
+        ++p;
+        if (!phase_glu<Q8>(a, rs, w, p, opaque_uniform(unit), wb, l)) return;
+        out_barrier();
+        prefetch_row<Q8, I, 0>(w->down, opaque_uniform(unit), H, wb);
+        ++p;
+        if (!phase_down<Q8>(a, rs, w, p, opaque_uniform(unit), wb, l)) return;
+        out_barrier();
+        prefetch_layer<Q8>(a, L + 1, opaque_uniform(unit), wb);
+        ++p;
     }
+    if (!phase_lm<Q8>(a, rs, p, opaque_uniform(unit), wb, l)) return;
+    ++p;
+    if (blockIdx.x == 0) phase_arg(a, rs, p, l);
 }
 
 }  // namespace dec
@@ -1491,17 +1503,10 @@ int decode_plan_create(const QrDecodeDesc& d, QrDecodePlan** out, hipStream_t s,
     a.emb_bf16 = d.embedding_bf16 ? 1 : 0;
     a.eps = d.eps;
     a.epoch = epoch;
-    static const uint8_t delta[5] = {T_DIN, T_MIX, T_DOUT, T_GLU, T_DOWN};
-    static const uint8_t attn[6] = {T_AQKV, T_ATTN, T_COMB, T_O, T_GLU, T_DOWN};
-    int n = 0;
-    for (int l = 0; l < d.layers; ++l) {
-        const uint8_t* seq = d.layer[l].attention ? attn : delta;
-        const int cnt = d.layer[l].attention ? 6 : 5;
-        for (int k = 0; k < cnt; ++k) a.phase[n++] = uint32_t(seq[k]) | uint32_t(l) << 8;
-    }
-    a.phase[n++] = T_LM;
-    a.phase[n++] = T_ARG;
-    a.nphases = n;
+    // the phase list the kernel walks (tags are phase indices): per DeltaNet
+    // layer DIN MIX DOUT GLU DOWN, per attention layer AQKV ATTN COMB O GLU
+    // DOWN, then LM and ARG
+    a.nlayers = d.layers;
     *out = p;
     return 0;
 }
