@@ -36,7 +36,7 @@ for p in (str(ROOT / "qwen-rust-inference_amd"), str(ROOT / "oracle")):
 HBM_PEAK_GBS = 8000.0
 # HBM bytes per decode_kernel launch at ctx ~590 from the rocprofv3 FETCH_SIZE / WRITE_SIZE passes
 # (calibrated on a 512 MiB copy; profiles/decode_kernel_config2.md).
-DECODE_TRAFFIC_BYTES = 3_164_000_000
+DECODE_TRAFFIC_BYTES = 3_153_000_000
 MFMA_F32_PEAK_TFLOPS = 157.3
 METRIC = "decode tok/s @ctx 454 & 8192 + HBM GB/s; prefill tok/s @2644"
 
