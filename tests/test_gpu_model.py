@@ -367,3 +367,19 @@ def test_qwen08b_chained_greedy_equals_stepwise(qwen08b_models):
     for layer in (0, 3, 23):
         for which in range(4):
             assert np.array_equal(runs[0].state(layer, which), runs[1].state(layer, which)), (layer, which)
+
+
+def test_qwen08b_chained_greedy_bounds(qwen08b_models):
+    """Chained greedy decoding refuses to run past the run's capacity or from an
+    out-of-range token (checked on the host, before any launch), and leaves the
+    run usable."""
+    fast, _ = qwen08b_models
+    run = fast.new_run(12, chunk=8)
+    run.prefill([1, 2, 3, 4])
+    with pytest.raises(E.EngineError):
+        run.decode_greedy(5, 10)  # 9 steps from position 4 > capacity 12
+    with pytest.raises(E.EngineError):
+        run.decode_greedy(248320, 3)  # token id == vocab
+    assert run.position == 4
+    ids, _ = run.decode_greedy(5, 4)
+    assert len(ids) == 4 and run.position == 7
