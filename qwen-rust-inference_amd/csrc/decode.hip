@@ -952,20 +952,27 @@ __device__ __forceinline__ bool phase_attn(const Args& a, Rs rs, LayerP w, int p
     const int wave = int(threadIdx.x >> 6);
     const unsigned want = tag(a, p - 1);
     if (block_busy) {
-        // normalised, rotated q of the 8 heads (wave h: head h) and new k of the
-        // 2 KV heads (waves 0, 1) into LDS: q at act[h * HD], k at act[NH * HD + kvh * HD]
+        // normalised, rotated q of the 8 heads (wave h: head h), new k of the 2
+        // KV heads (waves 0, 1) and their new v (waves 2, 3) into LDS: q at
+        // act[h * HD], k at act[NH * HD + kvh * HD], v at act[(NH + NKV) * HD + kvh * HD]
         const unsigned lane = lane_id();
         const Rs rn = rsrc(w->qk_norm);
         const f4 wq = f4(1.f) + ldp4(rn, 16u * lane, 0), wk = f4(1.f) + ldp4(rn, HD * 4u + 16u * lane, 0);
         const unsigned long long start = wall_clock64();
+        const bool hask = wave < NKV, hasv = wave >= NKV && wave < 2 * NKV;
         const unsigned qo = SOFF(mixed) + (unsigned(wave) * 2u * HD + 4u * lane) * 8u;
-        const unsigned ko = SOFF(key) + (unsigned(wave < NKV ? wave : 0) * HD + 4u * lane) * 8u;
+        const unsigned ko = hask   ? SOFF(key) + (unsigned(wave) * HD + 4u * lane) * 8u
+                            : hasv ? SOFF(value) + (unsigned(wave - NKV) * HD + 4u * lane) * 8u
+                                   : qo;
         const unsigned qk[4] = {qo, qo + 16u, ko, ko + 16u};
-        const bool hask = wave < NKV, live[4] = {true, true, hask, hask};
+        const bool live[4] = {true, true, hask || hasv, hask || hasv};
         f2 qkv[4];
         wait2n<4>(a, rs, qk, live, want, qkv, l, start, p);
         norm_rope_head(f4{qkv[0].x, qkv[0].y, qkv[1].x, qkv[1].y}, wq, a, &l.act[par][wave * HD]);
         if (hask) norm_rope_head(f4{qkv[2].x, qkv[2].y, qkv[3].x, qkv[3].y}, wk, a, &l.act[par][NH * HD + wave * HD]);
+        if (hasv)
+            *reinterpret_cast<f4*>(&l.act[par][(NH + NKV) * HD + (wave - NKV) * HD + 4 * int(lane)]) =
+                f4{qkv[2].x, qkv[2].y, qkv[3].x, qkv[3].y};
     }
     if (!bsync(l, p)) return false;
     const AttnUnit au = attn_unit(u, splits);
@@ -973,34 +980,18 @@ __device__ __forceinline__ bool phase_attn(const Args& a, Rs rs, LayerP w, int p
     const unsigned lane = lane_id(), sub = lane & 15, slot = lane >> 4;
     const int kvh = au.kvh, sp = au.sp, h = kvh * QPG + au.g, begin = sp * span, end = min(len, begin + span);
     const float* kn = &l.act[par][NH * HD + kvh * HD];
-    float* vn = l.wave[wave];  // the new value row
+    const float* vn = &l.act[par][(NH + NKV) * HD + kvh * HD];
     const bool has_new = pos >= begin && pos < end;
     if (has_new) {
-        if (slot == 0) {
-            const unsigned vo = SOFF(value) + (unsigned(kvh) * HD + sub * 4u) * 8u;
-            const unsigned long long start = wall_clock64();
-            unsigned vof[8];
-            bool all[8];
-            f2 vpair[8];
-#pragma unroll
-            for (int k = 0; k < 8; ++k) {  // dims 64 (k / 2) + 4 sub + 2 (k % 2) .. +1
-                vof[k] = vo + 512u * unsigned(k >> 1) + 16u * unsigned(k & 1);
-                all[k] = true;
-            }
-            wait2n<8>(a, rs, vof, all, want, vpair, l, start, p);
+        if (slot == 0 && au.g == 0) {  // one wave of the slot appends the row to the caches
             const Rs rk = rsrc(w->keys), rv = rsrc(w->values);
             const unsigned co = ((unsigned(pos) * NKV + unsigned(kvh)) * HD + sub * 4u) * 4u;
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                const f4 vv = f4{vpair[2 * e].x, vpair[2 * e].y, vpair[2 * e + 1].x, vpair[2 * e + 1].y};
-                *reinterpret_cast<f4*>(vn + sub * 4 + 64 * e) = vv;
-                if (au.g == 0) {  // one wave of the slot appends the row to the caches
-                    stp4(rk, co + 256u * e, lds4(kn + sub * 4 + 64 * e));
-                    stp4(rv, co + 256u * e, vv);
-                }
+                stp4(rk, co + 256u * e, lds4(kn + sub * 4 + 64 * e));
+                stp4(rv, co + 256u * e, lds4(vn + sub * 4 + 64 * e));
             }
         }
-        compiler_fence();
         patch_new(wb, kn, vn, begin, pos);
     }
     f4 q[4];
@@ -1133,21 +1124,34 @@ __device__ __forceinline__ bool phase_o(const Args& a, Rs rs, int L, int p, int 
 // at a time with the next 4 in flight; per-wave (max, first index,
 // non-finite count).
 constexpr int LM_G = 4;
+// The first LM_KEEP rows of each wave's lm_head slice are read with
+// allocating loads, every other weight with non-temporal ones: that part of
+// the head (fp32: 201 MB of the 256 MB memory-side cache) stays there from
+// one step to the next (measured: 24 rows beat 16; 40 thrash; int8 likewise).
+constexpr int LM_KEEP = 24;
 __device__ __forceinline__ int lm_rows_per_wave(int vocab) { return (vocab + NW - 1) / NW; }
-template <bool Q8>
-__device__ __forceinline__ void lm_load(Rs lm, int row0, int row_end, int vocab, f4* buf) {
+template <bool Q8, int AUX>
+__device__ __forceinline__ void lm_load_as(Rs lm, int row0, int row_end, int vocab, f4* buf) {
 #pragma unroll
     for (int r = 0; r < LM_G; ++r)
         if (row0 + r < row_end) {
             if constexpr (Q8) {
-                buf[r * 4] = ldw(lm, 16u * lane_id(), unsigned(vocab) * 4u + unsigned(row0 + r) * unsigned(H));
+                buf[r * 4] = buffer_load_f4(lm, 16u * lane_id(), unsigned(vocab) * 4u + unsigned(row0 + r) * unsigned(H), AUX);
                 buf[r * 4 + 1] = f4{ldp(lm, unsigned(row0 + r) * 4u), 0.f, 0.f, 0.f};
             } else {
                 const unsigned lo = 16u * lane_id(), ro = unsigned(row0 + r) * unsigned(H * 4);
 #pragma unroll
-                for (int v = 0; v < 4; ++v) buf[r * 4 + v] = ldw(lm, lo + 1024u * v, ro);
+                for (int v = 0; v < 4; ++v) buf[r * 4 + v] = buffer_load_f4(lm, lo + 1024u * v, ro, AUX);
             }
         }
+}
+// rows row0 .. row0 + LM_G - 1 (below row_end) of a slice starting at first
+template <bool Q8>
+__device__ __forceinline__ void lm_load(Rs lm, int first, int row0, int row_end, int vocab, f4* buf) {
+    if (row0 - first < LM_KEEP)
+        lm_load_as<Q8, 0>(lm, row0, row_end, vocab, buf);
+    else
+        lm_load_as<Q8, kNT>(lm, row0, row_end, vocab, buf);
 }
 template <bool Q8>
 __device__ __forceinline__ void lm_rows(Rs lg, const f4* buf, const f4 (&xv)[4], int row0, int row_end, float& best,
@@ -1177,7 +1181,7 @@ __device__ __forceinline__ void lm_rows(Rs lg, const f4* buf, const f4 (&xv)[4],
 template <bool Q8>
 __device__ __forceinline__ void prefetch_lm(const Args& a, int u, f4* wb) {
     const int rpw = lm_rows_per_wave(a.vocab), row0 = u * rpw, row_end = min(a.vocab, row0 + rpw);
-    lm_load<Q8>(rsrc(a.lm_head), row0, row_end, a.vocab, wb);
+    lm_load<Q8>(rsrc(a.lm_head), row0, row0, row_end, a.vocab, wb);
 }
 template <bool Q8>
 __device__ __forceinline__ bool phase_lm(const Args& a, Rs rs, int p, int u, f4* wb, Lds& l) {
@@ -1193,10 +1197,10 @@ __device__ __forceinline__ bool phase_lm(const Args& a, Rs rs, int p, int u, f4*
     unsigned at = 0xffffffffu, bad = 0;
     f4 nb[4 * LM_G];
     for (int r = row0; r < row_end; r += 2 * LM_G) {
-        lm_load<Q8>(lm, r + LM_G, row_end, a.vocab, nb);
+        lm_load<Q8>(lm, row0, r + LM_G, row_end, a.vocab, nb);
         lm_rows<Q8>(lg, wb, xv, r, row_end, best, at, bad);
         if (r + LM_G >= row_end) break;
-        lm_load<Q8>(lm, r + 2 * LM_G, row_end, a.vocab, wb);
+        lm_load<Q8>(lm, row0, r + 2 * LM_G, row_end, a.vocab, wb);
         lm_rows<Q8>(lg, nb, xv, r + LM_G, row_end, best, at, bad);
     }
     if (lane_id() == 0) {
