@@ -436,16 +436,16 @@ __device__ __forceinline__ float q8dot(f4 w, const f4 (&x)[4], float acc) {
 // reference's upload_int8, src/device.rs:550-561: `rows` fp32 scales, then the
 // values row-major): the row's 1 KiB in wb[AT] (columns 16 lane .. +15) and
 // its scale in wb[AT + 1].x.
-template <bool Q8, int AT>
+template <bool Q8, int AT, int AUX = kNT>
 __device__ __forceinline__ void load_row_h(f4* wb, Rs m, int r, int rows) {
     const unsigned lo = 16u * lane_id();
     if constexpr (Q8) {
-        wb[AT] = ldw(m, lo, unsigned(rows) * 4u + unsigned(r) * unsigned(H));
+        wb[AT] = buffer_load_f4(m, lo, unsigned(rows) * 4u + unsigned(r) * unsigned(H), AUX);
         wb[AT + 1] = f4{ldp(m, unsigned(r) * 4u), 0.f, 0.f, 0.f};
     } else {
         const unsigned row = unsigned(r) * unsigned(H * 4);
 #pragma unroll
-        for (int v = 0; v < 4; ++v) wb[AT + v] = ldw(m, lo + 1024u * v, row);
+        for (int v = 0; v < 4; ++v) wb[AT + v] = buffer_load_f4(m, lo + 1024u * v, row, AUX);
     }
 }
 // int8: scale * sum(q x), the scale after the sum (reference bridge.cpp:620-653).
@@ -488,24 +488,24 @@ __device__ __forceinline__ float dot_row_lds(const f4* wb, const float* act) {
 // ---- T_DIN: qkv | a | b rows of a DeltaNet layer (z rows: phase T_MIX), then
 // the causal conv + SiLU of each qkv channel (reference.h:96-116): the wave
 // computing a channel's row is the only one touching its history.
-template <bool Q8, int R>
+template <bool Q8, int R, int AUX = kNT>
 __device__ __forceinline__ void din_load(LayerP w, int u, f4* wb) {
     const int row = u * DIN_RPW + R;
     if (row < CH)
-        load_row_h<Q8, 4 * R>(wb, rsrc(w->qkv), row, CH);
+        load_row_h<Q8, 4 * R, AUX>(wb, rsrc(w->qkv), row, CH);
     else if (row < CH + VH)
-        load_row_h<Q8, 4 * R>(wb, rsrc(w->a), row - CH, VH);
+        load_row_h<Q8, 4 * R, AUX>(wb, rsrc(w->a), row - CH, VH);
     else if (row < DIN_ROWS)
-        load_row_h<Q8, 4 * R>(wb, rsrc(w->b), row - CH - VH, VH);
+        load_row_h<Q8, 4 * R, AUX>(wb, rsrc(w->b), row - CH - VH, VH);
 }
 // Weights of the heavier phases are fetched in two parts: part 0 after the
 // previous phase, part 1 after the phase's own first polls (so the polls are
 // not queued behind all of it).
-template <bool Q8>
+template <bool Q8, int AUX = kNT>
 __device__ __forceinline__ void prefetch_din(LayerP w, int u, f4* wb, int part) {
     if (part == 0) {
-        din_load<Q8, 0>(w, u, wb);
-        din_load<Q8, 1>(w, u, wb);
+        din_load<Q8, 0, AUX>(w, u, wb);
+        din_load<Q8, 1, AUX>(w, u, wb);
     } else {
         din_load<Q8, 2>(w, u, wb);
         din_load<Q8, 3>(w, u, wb);
@@ -687,7 +687,7 @@ __device__ __forceinline__ bool phase_mix(const Args& a, Rs rs, LayerP w, int L,
 // out_proj row u plus the residual.
 // PART -1: the whole row; 0 / 1: the first / second half of an fp32 row
 // (int8: part 0 is the whole row).
-template <bool Q8, int COLS, int PART = -1>
+template <bool Q8, int COLS, int PART = -1, int AUX = kNT>
 __device__ __forceinline__ void prefetch_row(const float* m, int row, int rows, f4* wb) {
     if (row >= rows) return;
     const Rs r = rsrc(m);
@@ -698,13 +698,13 @@ __device__ __forceinline__ void prefetch_row(const float* m, int row, int rows, 
         const unsigned ro = unsigned(rows) * 4u + unsigned(row) * unsigned(COLS);
 #pragma unroll
         for (int v = 0; v < NV; ++v)
-            if (lo + 1024u * v < unsigned(COLS)) wb[v] = ldw(r, lo + 1024u * v, ro);
+            if (lo + 1024u * v < unsigned(COLS)) wb[v] = buffer_load_f4(r, lo + 1024u * v, ro, AUX);
         wb[NV] = f4{ldp(r, unsigned(row) * 4u), 0.f, 0.f, 0.f};
     } else {
         const unsigned ro = unsigned(row) * unsigned(COLS * 4);
         constexpr int K = COLS / 256, V0 = PART == 1 ? K / 2 : 0, V1 = PART == 0 ? K / 2 : K;
 #pragma unroll
-        for (int v = V0; v < V1; ++v) wb[v] = ldw(r, lo + 1024u * v, ro);
+        for (int v = V0; v < V1; ++v) wb[v] = buffer_load_f4(r, lo + 1024u * v, ro, AUX);
     }
 }
 template <bool Q8>
@@ -735,18 +735,18 @@ __device__ __forceinline__ bool phase_dout(const Args& a, Rs rs, LayerP w, int L
 }
 
 // ---- T_GLU: product = silu(gate . n) * (up . n), n = post RMSNorm of `after`
-template <bool Q8, int R>
+template <bool Q8, int R, int AUX = kNT>
 __device__ __forceinline__ void glu_load(LayerP w, int u, f4* wb) {
     const int row = u * GLU_RPW + R;
     if (row < I) {
-        load_row_h<Q8, 8 * R>(wb, rsrc(w->gate), row, I);
-        load_row_h<Q8, 8 * R + 4>(wb, rsrc(w->up), row, I);
+        load_row_h<Q8, 8 * R, AUX>(wb, rsrc(w->gate), row, I);
+        load_row_h<Q8, 8 * R + 4, AUX>(wb, rsrc(w->up), row, I);
     }
 }
-template <bool Q8>
+template <bool Q8, int AUX = kNT>
 __device__ __forceinline__ void prefetch_glu(LayerP w, int u, f4* wb, int part) {
     if (part == 0)
-        glu_load<Q8, 0>(w, u, wb);
+        glu_load<Q8, 0, AUX>(w, u, wb);
     else
         glu_load<Q8, 1>(w, u, wb);
 }
@@ -787,21 +787,21 @@ __device__ __forceinline__ bool phase_down(const Args& a, Rs rs, LayerP w, int p
 }
 
 // ---- T_AQKV: q ([Q | gate] per head), k, v rows of an attention layer
-template <bool Q8, int R>
+template <bool Q8, int R, int AUX = kNT>
 __device__ __forceinline__ void aqkv_load(LayerP w, int u, f4* wb) {
     const int row = u * AQKV_RPW + R;
     if (row < QROWS)
-        load_row_h<Q8, 4 * R>(wb, rsrc(w->q), row, QROWS);
+        load_row_h<Q8, 4 * R, AUX>(wb, rsrc(w->q), row, QROWS);
     else if (row < QROWS + KVR)
-        load_row_h<Q8, 4 * R>(wb, rsrc(w->k), row - QROWS, KVR);
+        load_row_h<Q8, 4 * R, AUX>(wb, rsrc(w->k), row - QROWS, KVR);
     else if (row < AQKV_ROWS)
-        load_row_h<Q8, 4 * R>(wb, rsrc(w->v), row - QROWS - KVR, KVR);
+        load_row_h<Q8, 4 * R, AUX>(wb, rsrc(w->v), row - QROWS - KVR, KVR);
 }
-template <bool Q8>
+template <bool Q8, int AUX = kNT>
 __device__ __forceinline__ void prefetch_aqkv(LayerP w, int u, f4* wb, int part) {
     if (part == 0) {
-        aqkv_load<Q8, 0>(w, u, wb);
-        aqkv_load<Q8, 1>(w, u, wb);
+        aqkv_load<Q8, 0, AUX>(w, u, wb);
+        aqkv_load<Q8, 1, AUX>(w, u, wb);
     } else {
         aqkv_load<Q8, 2>(w, u, wb);
     }
@@ -1124,11 +1124,10 @@ __device__ __forceinline__ bool phase_o(const Args& a, Rs rs, int L, int p, int 
 // at a time with the next 4 in flight; per-wave (max, first index,
 // non-finite count).
 constexpr int LM_G = 4;
-// The first LM_KEEP rows of each wave's lm_head slice are read with
-// allocating loads, every other weight with non-temporal ones: that part of
-// the head (fp32: 201 MB of the 256 MB memory-side cache) stays there from
-// one step to the next (measured: 24 rows beat 16; 40 thrash; int8 likewise).
-constexpr int LM_KEEP = 24;
+// The first LM_KEEP rows of each wave's lm_head slice can be read with
+// allocating loads like the kept phase weights below (24 rows: 201 MB in
+// fp32); the cache is worth more to the phases' first weights.
+constexpr int LM_KEEP = 0;
 __device__ __forceinline__ int lm_rows_per_wave(int vocab) { return (vocab + NW - 1) / NW; }
 template <bool Q8, int AUX>
 __device__ __forceinline__ void lm_load_as(Rs lm, int row0, int row_end, int vocab, f4* buf) {
@@ -1292,6 +1291,21 @@ __device__ __forceinline__ void out_barrier() {
 }
 // Part 0 of the first phase of layer L, or the LM head's first rows after the
 // last layer.
+// The weights that a phase's first polls queue behind (part 0 of DIN / AQKV /
+// GLU / DOWN) are read with allocating loads in the layers of these masks,
+// all other weights non-temporally: that much stays in the 256 MB memory-side
+// cache from one step to the next, so those polls wait less. Measured best:
+// AQKV in every attention layer and DIN in layers 0-11, 198 MB in fp32
+// (ahead of the same bytes of lm_head rows, of GLU or DOWN, or of DIN in all
+// layers; past ~250 MB the cache thrashes). The K/V rows are read with
+// allocating loads too (24.6 KB per position in fp32): from position
+// KEEP_MAX_POS on the cache is left to them (ctx 8192: 744 us per step
+// instead of 763 with both).
+constexpr unsigned long long kKeepDin = 0xfffull, kKeepAqkv = ~0ull, kKeepGlu = 0, kKeepDown = 0;
+constexpr int KEEP_MAX_POS = 1536;
+__device__ __forceinline__ bool kept(const Args& a, unsigned long long mask, int L) {
+    return a.pos < KEEP_MAX_POS && ((mask >> L) & 1ull);
+}
 template <bool Q8>
 __device__ __forceinline__ void prefetch_layer(const Args& a, int L, int u, f4* wb) {
     if (L >= a.nlayers) {
@@ -1299,10 +1313,17 @@ __device__ __forceinline__ void prefetch_layer(const Args& a, int L, int u, f4* 
         return;
     }
     const LayerP w = layer(a, L);
-    if (w->attention)
-        prefetch_aqkv<Q8>(w, u, wb, 0);
-    else
-        prefetch_din<Q8>(w, u, wb, 0);
+    if (w->attention) {
+        if (kept(a, kKeepAqkv, L))
+            prefetch_aqkv<Q8, 0>(w, u, wb, 0);
+        else
+            prefetch_aqkv<Q8>(w, u, wb, 0);
+    } else {
+        if (kept(a, kKeepDin, L))
+            prefetch_din<Q8, 0>(w, u, wb, 0);
+        else
+            prefetch_din<Q8>(w, u, wb, 0);
+    }
 }
 
 // Phase p (the tag index) runs, per DeltaNet layer, DIN MIX DOUT GLU DOWN and,
@@ -1357,11 +1378,17 @@ __global__ __launch_bounds__(THREADS, 1) void decode_kernel(Args a) {
             if (!phase_dout<Q8>(a, rs, w, L, p, opaque_uniform(unit), wb, l)) return;
         }
         out_barrier();
-        prefetch_glu<Q8>(w, opaque_uniform(unit), wb, 0);
+        if (kept(a, kKeepGlu, L))
+            prefetch_glu<Q8, 0>(w, opaque_uniform(unit), wb, 0);
+        else
+            prefetch_glu<Q8>(w, opaque_uniform(unit), wb, 0);
         ++p;
         if (!phase_glu<Q8>(a, rs, w, p, opaque_uniform(unit), wb, l)) return;
         out_barrier();
-        prefetch_row<Q8, I, 0>(w->down, opaque_uniform(unit), H, wb);
+        if (kept(a, kKeepDown, L))
+            prefetch_row<Q8, I, 0, 0>(w->down, opaque_uniform(unit), H, wb);
+        else
+            prefetch_row<Q8, I, 0>(w->down, opaque_uniform(unit), H, wb);
         ++p;
         if (!phase_down<Q8>(a, rs, w, p, opaque_uniform(unit), wb, l)) return;
         out_barrier();
