@@ -999,13 +999,19 @@ __device__ __forceinline__ bool phase_attn(const Args& a, Rs rs, LayerP w, int p
     for (int e = 0; e < 4; ++e) q[e] = lds4(&l.act[par][h * HD + sub * 4 + 64 * e]);
     float m = -INFINITY, lsum = 0.f;
     f4 acc[4] = {f4(0.f), f4(0.f), f4(0.f), f4(0.f)};
+    // chunks alternate between wb and nb: the next chunk's loads are in
+    // flight while this one is scored
+    f4 nb[KVE];
 #pragma unroll 1
-    for (int first = begin; first < end; first += SPAN) {
-        if (first != begin) {
-            load_kv_chunk(w, kvh, first, pos, wb);
-            if (has_new) patch_new(wb, kn, vn, first, pos);
-        }
+    for (int first = begin; first < end; first += 2 * SPAN) {
+        const int c1 = first + SPAN, c2 = first + 2 * SPAN;
+        if (c1 < end) load_kv_chunk(w, kvh, c1, pos, nb);
         attn_chunk(wb, q, first, end, m, lsum, acc);
+        if (c1 >= end) break;
+        if (has_new) patch_new(nb, kn, vn, c1, pos);
+        if (c2 < end) load_kv_chunk(w, kvh, c2, pos, wb);
+        attn_chunk(nb, q, c1, end, m, lsum, acc);
+        if (c2 < end && has_new) patch_new(wb, kn, vn, c2, pos);
     }
     // merge the 4 position slots
 #pragma unroll
