@@ -611,6 +611,9 @@ __device__ __forceinline__ bool phase_mix(const Args& a, Rs rs, LayerP w, int L,
         z_row<Q8, 1>(rs, wb, xv, u, t);
         return true;
     }
+    // the delta rule is the phase's critical path: its wave goes first on its
+    // SIMD (whose other wave streams z rows) until its state is written back
+    __builtin_amdgcn_s_setprio(3);
     const unsigned lane = lane_id();
     const int wave = int(threadIdx.x >> 6);
     const int h = u >> 3, cg = u & 7, pr = int(lane >> 4), j = cg * 16 + int(lane & 15);
@@ -678,6 +681,7 @@ __device__ __forceinline__ bool phase_mix(const Args& a, Rs rs, LayerP w, int L,
         stp(S, so + 2u * DV * 4u, wb[k].z);
         stp(S, so + 3u * DV * 4u, wb[k].w);
     }
+    __builtin_amdgcn_s_setprio(0);
     return true;
 }
 
