@@ -776,12 +776,26 @@ __device__ __forceinline__ bool phase_glu(const Args& a, Rs rs, LayerP w, int p,
     return true;
 }
 
+// One word of each 64-byte line a layer record can span (8-byte aligned
+// fields at offsets 0, 56, 120, 176 of 184 bytes), read through the scalar
+// cache and waited for: the next layer's first prefetch then finds its
+// pointers there instead of waiting on a miss.
+__device__ __forceinline__ void touch_record(LayerP w) {
+    const int x0 = w->attention;
+    const float* x1 = w->k;
+    const float* x2 = w->a;
+    const float* x3 = w->recurrent;
+    asm volatile("" ::"s"(x0), "s"(x1), "s"(x2), "s"(x3));
+}
 // ---- T_DOWN: x = after + down . product
 template <bool Q8>
-__device__ __forceinline__ bool phase_down(const Args& a, Rs rs, LayerP w, int p, int u, f4* wb, Lds& l) {
+__device__ __forceinline__ bool phase_down(const Args& a, Rs rs, LayerP w, LayerP next, int p, int u, f4* wb,
+                                           Lds& l) {
     const int par = p & 1;
-    stage_tagged<I>(a, rs, SOFF(product), tag(a, p - 1), l.act[par], l, p,
-                    [&] { prefetch_row<Q8, I, 1>(w->down, u, H, wb); });
+    stage_tagged<I>(a, rs, SOFF(product), tag(a, p - 1), l.act[par], l, p, [&] {
+        prefetch_row<Q8, I, 1>(w->down, u, H, wb);
+        if (next) touch_record(next);
+    });
     if (!bsync(l, p)) return false;
     if (u >= H) return true;
     const float acc = dot_row_lds<Q8, I / 256>(wb, l.act[par]);
@@ -1400,7 +1414,8 @@ __global__ __launch_bounds__(THREADS, 1) void decode_kernel(Args a) {
         else
             prefetch_row<Q8, I, 0>(w->down, opaque_uniform(unit), H, wb);
         ++p;
-        if (!phase_down<Q8>(a, rs, w, p, opaque_uniform(unit), wb, l)) return;
+        if (!phase_down<Q8>(a, rs, w, L + 1 < a.nlayers ? layer(a, L + 1) : nullptr, p, opaque_uniform(unit), wb, l))
+            return;
         out_barrier();
         prefetch_layer<Q8>(a, L + 1, opaque_uniform(unit), wb);
         ++p;
