@@ -227,6 +227,7 @@ struct Lds {
     alignas(16) float wave[WAVES][2 * HD];  // wave-private scratch
     int fail;  // the earliest phase in which a lane of the block timed out (kNoFail: none)
     int token;  // this launch's token
+    int lmnext;  // the next lm_head row group of the block's range to hand out
 };
 constexpr int kNoFail = 0x7fffffff;
 
@@ -1148,33 +1149,20 @@ __device__ __forceinline__ bool phase_o(const Args& a, Rs rs, int L, int p, int 
 // at a time with the next 4 in flight; per-wave (max, first index,
 // non-finite count).
 constexpr int LM_G = 4;
-// The first LM_KEEP rows of each wave's lm_head slice can be read with
-// allocating loads like the kept phase weights below (24 rows: 201 MB in
-// fp32); the cache is worth more to the phases' first weights.
-constexpr int LM_KEEP = 0;
-__device__ __forceinline__ int lm_rows_per_wave(int vocab) { return (vocab + NW - 1) / NW; }
-template <bool Q8, int AUX>
-__device__ __forceinline__ void lm_load_as(Rs lm, int row0, int row_end, int vocab, f4* buf) {
+template <bool Q8>
+__device__ __forceinline__ void lm_load(Rs lm, int row0, int row_end, int vocab, f4* buf) {
 #pragma unroll
     for (int r = 0; r < LM_G; ++r)
         if (row0 + r < row_end) {
             if constexpr (Q8) {
-                buf[r * 4] = buffer_load_f4(lm, 16u * lane_id(), unsigned(vocab) * 4u + unsigned(row0 + r) * unsigned(H), AUX);
+                buf[r * 4] = ldw(lm, 16u * lane_id(), unsigned(vocab) * 4u + unsigned(row0 + r) * unsigned(H));
                 buf[r * 4 + 1] = f4{ldp(lm, unsigned(row0 + r) * 4u), 0.f, 0.f, 0.f};
             } else {
                 const unsigned lo = 16u * lane_id(), ro = unsigned(row0 + r) * unsigned(H * 4);
 #pragma unroll
-                for (int v = 0; v < 4; ++v) buf[r * 4 + v] = buffer_load_f4(lm, lo + 1024u * v, ro, AUX);
+                for (int v = 0; v < 4; ++v) buf[r * 4 + v] = ldw(lm, lo + 1024u * v, ro);
             }
         }
-}
-// rows row0 .. row0 + LM_G - 1 (below row_end) of a slice starting at first
-template <bool Q8>
-__device__ __forceinline__ void lm_load(Rs lm, int first, int row0, int row_end, int vocab, f4* buf) {
-    if (row0 - first < LM_KEEP)
-        lm_load_as<Q8, 0>(lm, row0, row_end, vocab, buf);
-    else
-        lm_load_as<Q8, kNT>(lm, row0, row_end, vocab, buf);
 }
 template <bool Q8>
 __device__ __forceinline__ void lm_rows(Rs lg, const f4* buf, const f4 (&xv)[4], int row0, int row_end, float& best,
@@ -1201,10 +1189,26 @@ __device__ __forceinline__ void lm_rows(Rs lg, const f4* buf, const f4 (&xv)[4],
         }
     }
 }
+// The block's waves share the block's range of rows in groups of LM_G: each
+// wave's first group is fixed (wave w: group w, prefetched), the rest are
+// handed out in order by an LDS counter, so the waves of a block finish
+// together (the second wave on each SIMD streams more slowly than the first).
+// Every row is computed the same way whichever wave takes it.
+__device__ __forceinline__ void lm_block_range(int u, int vocab, int& first, int& last) {
+    const int rb = (vocab + BLOCKS - 1) / BLOCKS;
+    first = min(vocab, (u % BLOCKS) * rb);
+    last = min(vocab, first + rb);
+}
 template <bool Q8>
 __device__ __forceinline__ void prefetch_lm(const Args& a, int u, f4* wb) {
-    const int rpw = lm_rows_per_wave(a.vocab), row0 = u * rpw, row_end = min(a.vocab, row0 + rpw);
-    lm_load<Q8>(rsrc(a.lm_head), row0, row0, row_end, a.vocab, wb);
+    int first, last;
+    lm_block_range(u, a.vocab, first, last);
+    lm_load<Q8>(rsrc(a.lm_head), first + LM_G * (u / BLOCKS), last, a.vocab, wb);
+}
+__device__ __forceinline__ int lm_grab(Lds& l, int first) {
+    int g = 0;
+    if (lane_id() == 0) g = __hip_atomic_fetch_add(&l.lmnext, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    return first + LM_G * __builtin_amdgcn_readfirstlane(g);
 }
 template <bool Q8>
 __device__ __forceinline__ bool phase_lm(const Args& a, Rs rs, int p, int u, f4* wb, Lds& l) {
@@ -1214,17 +1218,26 @@ __device__ __forceinline__ bool phase_lm(const Args& a, Rs rs, int p, int u, f4*
     if (!bsync(l, p)) return false;
     f4 xv[4];
     normed_chunks<Q8>(l, par, a.eps, xv);
-    const int rpw = lm_rows_per_wave(a.vocab), row0 = u * rpw, row_end = min(a.vocab, row0 + rpw);
+    int first, last;
+    lm_block_range(u, a.vocab, first, last);
     const Rs lm = rsrc(a.lm_head), lg = rsrc(a.logits);
     float best = -INFINITY;
     unsigned at = 0xffffffffu, bad = 0;
     f4 nb[4 * LM_G];
-    for (int r = row0; r < row_end; r += 2 * LM_G) {
-        lm_load<Q8>(lm, row0, r + LM_G, row_end, a.vocab, nb);
-        lm_rows<Q8>(lg, wb, xv, r, row_end, best, at, bad);
-        if (r + LM_G >= row_end) break;
-        lm_load<Q8>(lm, row0, r + 2 * LM_G, row_end, a.vocab, wb);
-        lm_rows<Q8>(lg, nb, xv, r + LM_G, row_end, best, at, bad);
+    // groups alternate between wb and nb; the counter only grows, so once a
+    // grabbed group lies past the range every later one does too
+    int c0 = first + LM_G * (u / BLOCKS), c1 = lm_grab(l, first);
+    lm_load<Q8>(lm, c1, last, a.vocab, nb);
+    for (;;) {
+        if (c0 >= last) break;
+        lm_rows<Q8>(lg, wb, xv, c0, last, best, at, bad);
+        if (c1 >= last) break;
+        c0 = lm_grab(l, first);
+        lm_load<Q8>(lm, c0, last, a.vocab, wb);
+        lm_rows<Q8>(lg, nb, xv, c1, last, best, at, bad);
+        if (c0 >= last) break;
+        c1 = lm_grab(l, first);
+        lm_load<Q8>(lm, c1, last, a.vocab, nb);
     }
     if (lane_id() == 0) {
         const unsigned o = SOFF(lmpart) + unsigned(u) * 32u, t = tag(a, p);
@@ -1363,6 +1376,7 @@ __global__ __launch_bounds__(THREADS, 1) void decode_kernel(Args a) {
     const int unit = wave * BLOCKS + int(blockIdx.x);  // rows spread wave-major over blocks
     if (threadIdx.x == 0) {
         l.fail = kNoFail;
+        l.lmnext = WAVES;  // groups 0 .. WAVES - 1 are the waves' first, prefetched ones
         int tok = a.token;
         if (a.chain) {  // the previous launch's argmax (kernel boundary: its stores are visible)
             const float f = ldp(rsrc(a.picks), 0);
