@@ -211,6 +211,22 @@ def main():
            f"prefill_{args.prompt}_tok_s": round(args.prompt / prefill_s, 1),
            "roofline": roofline}
 
+    # attainable read bandwidth: the stream-read program (4 GiB, the decode
+    # kernel's load pattern) in a child process, median of 10 passes
+    reader = ROOT / "qwen-rust-inference_amd" / "bin" / "stream_read"
+    if reader.exists():
+        import subprocess
+        r = subprocess.run([str(reader), "4096", "10"], capture_output=True, text=True, timeout=120)
+        if r.returncode == 0 and r.stdout.strip():
+            sr = json.loads(r.stdout.strip().splitlines()[-1])
+            out["hbm_stream_read_gbs"] = sr["gbs"]
+            out["hbm_weight_read_frac_of_stream_read"] = round(hbm / sr["gbs"], 4)
+            roofline["attainable"] = sr["gbs"]
+            log(f"stream read: {sr['gbs']:.0f} GB/s attainable ({sr['gbs'] / HBM_PEAK_GBS:.1%} of the nominal peak); "
+                f"decode weight-read is {hbm / sr['gbs']:.1%} of it")
+        else:
+            log(f"stream read failed: {r.stderr.strip()[-200:]}")
+
     if args.long:
         # Decode at ctx 8192 (config 4): the context's DeltaNet states and
         # K/V rows are seeded synthetic state written into the run (a decode
