@@ -1339,6 +1339,9 @@ __device__ __forceinline__ void out_barrier() {
 // KEEP_MAX_POS on the cache is left to them (ctx 8192: 744 us per step
 // instead of 763 with both).
 constexpr unsigned long long kKeepDin = 0xfffull, kKeepAqkv = ~0ull, kKeepGlu = 0, kKeepDown = 0;
+// int8 weights are a quarter of the bytes: part 0 of every heavy phase in
+// every layer fits (about 210 MB)
+constexpr unsigned long long kKeepAllQ8 = ~0ull;
 constexpr int KEEP_MAX_POS = 1536;
 __device__ __forceinline__ bool kept(const Args& a, unsigned long long mask, int L) {
     return a.pos < KEEP_MAX_POS && ((mask >> L) & 1ull);
@@ -1351,12 +1354,12 @@ __device__ __forceinline__ void prefetch_layer(const Args& a, int L, int u, f4* 
     }
     const LayerP w = layer(a, L);
     if (w->attention) {
-        if (kept(a, kKeepAqkv, L))
+        if (kept(a, Q8 ? kKeepAllQ8 : kKeepAqkv, L))
             prefetch_aqkv<Q8, 0>(w, u, wb, 0);
         else
             prefetch_aqkv<Q8>(w, u, wb, 0);
     } else {
-        if (kept(a, kKeepDin, L))
+        if (kept(a, Q8 ? kKeepAllQ8 : kKeepDin, L))
             prefetch_din<Q8, 0>(w, u, wb, 0);
         else
             prefetch_din<Q8>(w, u, wb, 0);
@@ -1416,14 +1419,14 @@ __global__ __launch_bounds__(THREADS, 1) void decode_kernel(Args a) {
             if (!phase_dout<Q8>(a, rs, w, L, p, opaque_uniform(unit), wb, l)) return;
         }
         out_barrier();
-        if (kept(a, kKeepGlu, L))
+        if (kept(a, Q8 ? kKeepAllQ8 : kKeepGlu, L))
             prefetch_glu<Q8, 0>(w, opaque_uniform(unit), wb, 0);
         else
             prefetch_glu<Q8>(w, opaque_uniform(unit), wb, 0);
         ++p;
         if (!phase_glu<Q8>(a, rs, w, p, opaque_uniform(unit), wb, l)) return;
         out_barrier();
-        if (kept(a, kKeepDown, L))
+        if (kept(a, Q8 ? kKeepAllQ8 : kKeepDown, L))
             prefetch_row<Q8, I, 0, 0>(w->down, opaque_uniform(unit), H, wb);
         else
             prefetch_row<Q8, I, 0>(w->down, opaque_uniform(unit), H, wb);
