@@ -55,6 +55,7 @@ def lib():
         L.qo_delta_rule.argtypes = [_F, _F, _F, ctypes.c_int64, ctypes.c_int64, ctypes.c_float, ctypes.c_float, _F,
                                     _F]
         L.qo_rotate.argtypes = [_F, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_float]
+        L.qo_attend.argtypes = [_F, _F, _F, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, _F]
         L.qo_set_threads.argtypes = [ctypes.c_int]
         _lib = L
     return _lib
@@ -198,3 +199,15 @@ def delta_rule(q, k, v, g, beta, state):
 def rotate(x, position, dim, theta):
     check(lib().qo_rotate(fp(x), x.size, position, dim, theta))
     return x
+
+
+def attend(query, keys, values, heads, kv_heads, d):
+    """attend (reference src/attention.rs:63-130): query [heads * d], keys and
+    values [positions, kv_heads * d]; returns the context [heads * d]."""
+    q = np.ascontiguousarray(query, dtype=np.float32).reshape(-1)
+    k = np.ascontiguousarray(keys, dtype=np.float32).reshape(-1)
+    v = np.ascontiguousarray(values, dtype=np.float32).reshape(-1)
+    positions = k.size // (kv_heads * d)
+    out = np.empty(heads * d, dtype=np.float32)
+    check(lib().qo_attend(fp(q), fp(k), fp(v), positions, heads, kv_heads, d, fp(out)))
+    return out

@@ -19,7 +19,15 @@
 //   * projections: integer-exact KATs and fp64 brute force;
 //   * Vector backend vs Reference backend on every record (both reference
 //     orders are restated; they differ only in summation order);
-//   * int8 quantiser: the reference's invariants (|w - s q| <= s/2, zero row).
+//   * int8 quantiser: the reference's invariants (|w - s q| <= s/2, zero row);
+//   * attend: the reference's hand examples (tests/components.rs:117-150: the
+//     1:3 read of 5 and the 4Q/2KV GQA grouping [3, 3, 12, 12]) and a float64
+//     dense softmax at 8Q/2KV;
+//   * rotate: the float64 closed form angle = pos * theta^(-2i/dim) at dims 8-64
+//     and positions up to 8190;
+//   * the whole forward on a config with 2 KV heads, rotary 16 of 32 and 2 key
+//     heads for 4 value heads, bit for bit against the engine's op sequence on
+//     the reference's own CPU test bridge (tests/test_engine_cpu.py).
 #include "../include/qwen_model.h"
 
 #include <atomic>
@@ -360,7 +368,42 @@ struct Tracer {
     }
 };
 
-// src/attention.rs:72-130 (attend_traced) and 189-207 (finish).
+// src/attention.rs:72-130 (attend_traced): per query head h the KV head
+// h / (heads / kv_heads) (contiguous groups), scores q.k / sqrt(d) over every
+// cached position, softmax, probability-weighted sum of the values.
+std::vector<float> attend(const float* query, const std::vector<std::vector<float>>& keys,
+                          const std::vector<std::vector<float>>& values, size_t heads, size_t kvh, size_t d,
+                          std::vector<float>* all_scores, std::vector<float>* all_probs) {
+    require(heads > 0 && kvh > 0 && d > 0 && heads % kvh == 0, "invalid GQA");
+    require(!keys.empty() && keys.size() == values.size(), "attention shape mismatch");
+    finite(query, heads * d);
+    for (size_t p = 0; p < keys.size(); ++p) {
+        require(keys[p].size() == kvh * d && values[p].size() == kvh * d, "KV shape mismatch");
+        finite(keys[p]);
+        finite(values[p]);
+    }
+    std::vector<float> out(heads * d, 0.f);
+    for (size_t h = 0; h < heads; ++h) {
+        size_t kv = h / (heads / kvh);
+        const float* q = query + h * d;
+        std::vector<float> scores(keys.size());
+        for (size_t p = 0; p < keys.size(); ++p) {
+            const float* kk = keys[p].data() + kv * d;
+            float sum = kSumStart;
+            for (size_t i = 0; i < d; ++i) sum += q[i] * kk[i];
+            scores[p] = sum / std::sqrt(float(d));
+        }
+        auto probs = softmax(scores);
+        if (all_scores) all_scores->insert(all_scores->end(), scores.begin(), scores.end());
+        if (all_probs) all_probs->insert(all_probs->end(), probs.begin(), probs.end());
+        for (size_t p = 0; p < values.size(); ++p)
+            for (size_t i = 0; i < d; ++i) out[h * d + i] += probs[p] * values[p][kv * d + i];
+    }
+    finite(out);
+    return out;
+}
+
+// src/attention.rs:132-226 (project, step) and 189-207 (finish).
 std::vector<float> attention_step(const qo_model& m, const qo_model::Layer& w, const std::vector<float>& x,
                                   qo_state::Layer& s, size_t position, int backend, int layer, const Tracer& tr) {
     const QwConfig& c = m.c;
@@ -391,26 +434,8 @@ std::vector<float> attention_step(const qo_model& m, const qo_model::Layer& w, c
     // step: the cache keeps the rotated key and the raw value (src/attention.rs:208-226)
     s.keys.push_back(key);
     s.values.push_back(value);
-    // attend_traced
-    require(heads % kvh == 0, "invalid GQA");
-    std::vector<float> out(heads * d, 0.f), all_scores, all_probs;
-    for (size_t h = 0; h < heads; ++h) {
-        size_t kv = h / (heads / kvh);
-        const float* q = query.data() + h * d;
-        std::vector<float> scores(s.keys.size());
-        for (size_t p = 0; p < s.keys.size(); ++p) {
-            const float* kk = s.keys[p].data() + kv * d;
-            float sum = kSumStart;
-            for (size_t i = 0; i < d; ++i) sum += q[i] * kk[i];
-            scores[p] = sum / std::sqrt(float(d));
-        }
-        auto probs = softmax(scores);
-        all_scores.insert(all_scores.end(), scores.begin(), scores.end());
-        all_probs.insert(all_probs.end(), probs.begin(), probs.end());
-        for (size_t p = 0; p < s.values.size(); ++p)
-            for (size_t i = 0; i < d; ++i) out[h * d + i] += probs[p] * s.values[p][kv * d + i];
-    }
-    finite(out);
+    std::vector<float> all_scores, all_probs;
+    std::vector<float> out = attend(query.data(), s.keys, s.values, heads, kvh, d, &all_scores, &all_probs);
     std::vector<float> gated = out;
     for (size_t i = 0; i < gated.size(); ++i) gated[i] *= sigmoid(gate[i]);
     std::vector<float> output = project(w.o, gated, backend);
@@ -809,6 +834,21 @@ int qo_delta_rule(const float* q, const float* k, const float* v, int64_t kd, in
     return guarded([&] {
         auto y = delta_rule(q, k, v, size_t(kd), size_t(vd), g, beta, state);
         std::memcpy(out, y.data(), y.size() * 4);
+    });
+}
+// attend (src/attention.rs:63-71): query [heads * d]; keys / values [positions][kv_heads * d].
+int qo_attend(const float* query, const float* keys, const float* values, int64_t positions, int64_t heads,
+              int64_t kv_heads, int64_t d, float* out) {
+    return guarded([&] {
+        require(positions > 0 && kv_heads > 0 && d > 0, "invalid attention shape");
+        size_t row = size_t(kv_heads * d);
+        std::vector<std::vector<float>> k, v;
+        for (int64_t p = 0; p < positions; ++p) {
+            k.emplace_back(keys + size_t(p) * row, keys + size_t(p + 1) * row);
+            v.emplace_back(values + size_t(p) * row, values + size_t(p + 1) * row);
+        }
+        auto o = attend(query, k, v, size_t(heads), size_t(kv_heads), size_t(d), nullptr, nullptr);
+        std::memcpy(out, o.data(), o.size() * sizeof(float));
     });
 }
 int qo_rotate(float* x, int64_t len, int64_t position, int64_t dim, float theta) {

@@ -1518,6 +1518,9 @@ hipError_t scratch_acquire(int dev, hipStream_t s, qr::dec::Scratch** out, unsig
     *epoch = 0;
     e = hipMemsetAsync(*out, 0, sizeof(qr::dec::Scratch), s);  // tag 0: never expected
     if (e == hipSuccess) e = hipStreamSynchronize(s);
+    // A buffer whose clearing failed may hold any tag: it never enters a plan
+    // or the pool (and, being uncached, is not handed back to HIP either).
+    if (e != hipSuccess) *out = nullptr;
     return e;
 }
 void scratch_release(int dev, qr::dec::Scratch* p, unsigned epoch) {

@@ -505,6 +505,27 @@ struct QeRun {
         std::vector<QrDecodeLayer> layers;
         const DeviceBlock* attn = nullptr;
         const DeviceBlock* delta = nullptr;
+        // The plan carries one eps for every norm (block, q/k, gated) and one
+        // attention / DeltaNet geometry: decline it unless every block agrees.
+        const float eps = c.rms_norm_eps;
+        for (const DeviceBlock& b : model->blocks) {
+            if (b.eps != eps) return;
+            if (b.attention) {
+                if (b.ac.eps != eps) return;
+                if (attn && (b.ac.heads != attn->ac.heads || b.ac.kv_heads != attn->ac.kv_heads ||
+                             b.ac.head_dim != attn->ac.head_dim || b.ac.rotary_dim != attn->ac.rotary_dim ||
+                             b.ac.theta != attn->ac.theta))
+                    return;
+                attn = &b;
+            } else {
+                if (b.dc.eps != eps) return;
+                if (delta && (b.dc.key_heads != delta->dc.key_heads || b.dc.value_heads != delta->dc.value_heads ||
+                              b.dc.key_dim != delta->dc.key_dim || b.dc.value_dim != delta->dc.value_dim ||
+                              b.dc.kernel != delta->dc.kernel))
+                    return;
+                delta = &b;
+            }
+        }
         for (size_t l = 0; l < model->blocks.size(); ++l) {
             const DeviceBlock& b = model->blocks[l];
             MixerRun& m = mixers[l];
@@ -525,7 +546,6 @@ struct QeRun {
                 d.qk_norm = b.qkn.p;
                 d.keys = m.keys.p;
                 d.values = m.values.p;
-                attn = &b;
             } else {
                 if (!ok(b.qkv) || !ok(b.z) || !ok(b.a) || !ok(b.b) || !ok(b.out)) return;
                 d.qkv = b.qkv.buffer.p;
@@ -538,7 +558,6 @@ struct QeRun {
                 d.out = b.out.buffer.p;
                 d.conv_state = m.conv_state.p;
                 d.recurrent = m.recurrent.p;
-                delta = &b;
             }
             layers.push_back(d);
         }

@@ -8,7 +8,7 @@ from pathlib import Path
 
 import numpy as np
 
-from .engine import BRIDGE, EngineError
+from .engine import BRIDGE, EngineError, require_current
 
 _F = ctypes.POINTER(ctypes.c_float)
 
@@ -78,6 +78,8 @@ class Bridge:
     def __init__(self, path: str | Path = BRIDGE, kind: int = 1):
         if not Path(path).exists():
             raise EngineError(f"bridge library missing: {path}")
+        if Path(path).resolve() == BRIDGE.resolve():
+            require_current(BRIDGE)
         self.L = L = ctypes.CDLL(str(path))
         L.qr_error.restype = ctypes.c_char_p
         L.qr_error.argtypes = [ctypes.c_void_p]

@@ -49,11 +49,43 @@ class EngineError(RuntimeError):
     pass
 
 
+STAMP = LIB_DIR / "sources.sha256"
+
+
+def source_digest() -> str:
+    """SHA-256 over every source the two libraries are built from (kernels,
+    bridge, engine, headers, Makefile), in a fixed order."""
+    import hashlib
+    h = hashlib.sha256()
+    files = sorted((PKG / "csrc").glob("*")) + sorted((PKG / "engine").glob("*")) + \
+        sorted((PKG.parent / "include").glob("*.h")) + [PKG / "Makefile"]
+    for f in files:
+        if f.is_file():
+            h.update(f.name.encode() + b"\0" + f.read_bytes() + b"\0")
+    return h.hexdigest()
+
+
+def write_stamp():
+    STAMP.write_text(source_digest() + "\n")
+
+
+def is_current() -> bool:
+    """True when both libraries exist and were built from the sources as they are."""
+    return BRIDGE.exists() and ENGINE.exists() and STAMP.exists() and \
+        STAMP.read_text().strip() == source_digest()
+
+
+def require_current(path: Path):
+    if not path.exists():
+        raise EngineError(f"library missing: {path} (run __graft_entry__.build())")
+    if not is_current():
+        raise EngineError(f"{path.name} was not built from the current sources (run __graft_entry__.build())")
+
+
 def lib():
     global _lib
     if _lib is None:
-        if not ENGINE.exists():
-            raise EngineError(f"engine library missing: {ENGINE} (run __graft_entry__.build())")
+        require_current(ENGINE)
         L = ctypes.CDLL(str(ENGINE))
         L.qe_last_error.restype = ctypes.c_char_p
         L.qe_model_load.restype = ctypes.c_void_p

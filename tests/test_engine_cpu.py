@@ -85,6 +85,45 @@ def test_tiny_greedy_prefill_chunks_and_decode(tiny, bridge):
         del o_last
 
 
+def config_gqa():
+    """A small hybrid whose attention has 2 KV heads for 8 query heads and a
+    16-wide rotary part of a 32-wide head (theta 1e6), and whose DeltaNet
+    has 2 key heads feeding 4 value heads: the head-to-group mappings and the
+    RoPE frequencies for i > 0 that the fixture and the tiny model (1 KV head,
+    rotary 2 or 8) leave unexercised."""
+    return M.make_config(hidden=64, intermediate=128, vocab=256,
+                         layer_types=["linear_attention", "full_attention", "linear_attention", "full_attention"],
+                         heads=8, kv_heads=2, head_dim=32, rotary_dim=16, key_heads=2, value_heads=4, key_dim=16,
+                         value_dim=8, conv_kernel=4, max_positions=256, eps=1e-6, theta=1e6)
+
+
+@pytest.mark.parametrize("bridge", BRIDGES)
+def test_gqa_config_bitwise(bridge):
+    """The engine's op sequence on the CPU bridges (ours, and the reference's
+    own) equals the oracle's Backend::Reference forward bit for bit on the
+    GQA config: logits of every prompt position, the greedy continuation and
+    every state part."""
+    c = config_gqa()
+    w = M.synthetic_weights(c, seed=3, std=0.1)
+    ids = [int(v) for v in np.random.default_rng(9).integers(0, c.vocab_size, 40)]
+    s = O.Oracle(w).new_state()
+    run = E.Model(w, bridge=bridge, kind=E.KIND_CPU_TEST).new_run(64)
+    for t in ids:
+        assert np.array_equal(run.step(t), s.step(t, O.REFERENCE))
+    want = []
+    logits = None
+    for i in range(8):
+        logits = s.step(want[-1] if want else ids[-1], O.REFERENCE)
+        want.append(O.select_greedy(logits))
+    run2 = E.Model(w, bridge=bridge, kind=E.KIND_CPU_TEST).new_run(64, chunk=16)
+    run2.prefill(ids)
+    got, _ = run2.decode_greedy(ids[-1], 9)
+    assert got[1:] == want
+    for layer in range(c.num_layers):
+        for which in range(4):
+            assert np.array_equal(run2.state(layer, which), s.part(layer, which)), (layer, which)
+
+
 @pytest.mark.parametrize("bridge", BRIDGES)
 def test_verify_rollback_and_accept(tiny, bridge):
     """verify_rollback + accept(k) leaves exactly the state of k sequential

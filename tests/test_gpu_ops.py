@@ -5,6 +5,7 @@ embedding ops bit-exact."""
 import numpy as np
 import pytest
 
+from bridges import both, rnd
 from conftest import ROOT
 from parity import FP32_RTOL, dot_bound, parity
 from qwen_mi355x.bridge import Bridge, pack_bf16, pack_int8
@@ -28,23 +29,6 @@ def cpu():
     b = Bridge(OPS, kind=0)
     yield b
     b.close()
-
-
-def both(gpu, cpu, op, count, inputs, outputs, n=(), f=(), slots=None):
-    """Run `op` on both bridges. inputs: {slot: array}; outputs: {slot: size}
-    (an output slot may also be an input). Returns ({slot: gpu}, {slot: cpu})."""
-    res = []
-    for br in (gpu, cpu):
-        bufs = {}
-        for s, arr in inputs.items():
-            bufs[s] = br.upload(np.ascontiguousarray(arr))
-        for s, size in outputs.items():
-            if s not in bufs:
-                bufs[s] = br.alloc(size)
-        p = [bufs.get(i, 0) for i in range(8)]
-        br.run(op, count, p, n, f)
-        res.append({s: bufs[s].read(size) for s, size in outputs.items()})
-    return res
 
 
 SHAPES_08B = [(6144, 1024), (2048, 1024), (16, 1024), (4096, 1024), (512, 1024), (1024, 2048), (3584, 1024),
@@ -250,10 +234,6 @@ def test_argmax_known_answers(gpu):
             out = gpu.alloc(2 * rows)
             gpu.run("ARGMAX", rows, [out, buf], [n])
             assert np.array_equal(out.read(), want), (n, rows)
-
-
-def rnd(rng, n, scale=1.0):
-    return (rng.standard_normal(n) * scale).astype(np.float32)
 
 
 @pytest.mark.parametrize("d,groups", [(1024, 1), (1024, 3), (128, 16), (128, 48), (8, 5), (256, 8)])

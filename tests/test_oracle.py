@@ -208,12 +208,56 @@ def test_projection_brute_force_and_orders():
 
 
 def test_attention_hand_examples():
-    """attend (reference tests/components.rs:117-150) through a one-layer
-    attention model is covered by the fixture; the closed form of the
-    rotate-half RoPE at position 0 is the identity."""
+    """attend (reference tests/components.rs:117-150): one head reading
+    exp(0):exp(ln 3) = 1:3 of the values 2 and 6 gives 5; with 4 query heads
+    over 2 KV heads, heads 0-1 read KV head 0 and heads 2-3 KV head 1
+    (contiguous groups; a modulo mapping gives [3, 12, 3, 12])."""
+    one = O.attend(np.array([1], np.float32), np.array([[0], [math.log(3)]], np.float32),
+                   np.array([[2], [6]], np.float32), 1, 1, 1)
+    close(one, [5], 1e-6, 1e-6)
+    gqa = O.attend(np.ones(4, np.float32), np.zeros((2, 2), np.float32), np.array([[2, 10], [4, 14]], np.float32),
+                   4, 2, 1)
+    close(gqa, [3, 3, 12, 12], 1e-6, 1e-6)
+    # 8 query heads over 2 KV heads at head_dim 4 against a float64 dense
+    # softmax, every head with its own query: the group of head h is h // 4
+    rng = np.random.default_rng(17)
+    q = rng.standard_normal(8 * 4).astype(np.float32)
+    k = rng.standard_normal((6, 2 * 4)).astype(np.float32)
+    v = rng.standard_normal((6, 2 * 4)).astype(np.float32)
+    got = O.attend(q, k, v, 8, 2, 4)
+    for h in range(8):
+        g = h // 4
+        s = k[:, g * 4:(g + 1) * 4].astype(np.float64) @ q[h * 4:(h + 1) * 4].astype(np.float64) / 2.0
+        p = np.exp(s - s.max())
+        p /= p.sum()
+        close(got[h * 4:(h + 1) * 4], p @ v[:, g * 4:(g + 1) * 4].astype(np.float64), 1e-5, 1e-5)
+    # the rotate-half RoPE at position 0 is the identity
     x = np.arange(8, dtype=np.float32)
-    y = O.rotate(x.copy(), 0, 8, 1e7)
-    assert np.array_equal(x, y)
+    assert np.array_equal(O.rotate(x.copy(), 0, 8, 1e7), x)
+
+
+@pytest.mark.parametrize("position,dim,length,theta", [(1, 64, 256, 1e7), (453, 64, 256, 1e7), (8190, 64, 256, 1e7),
+                                                       (7, 8, 16, 1e4), (3, 16, 20, 1e6)])
+def test_rope_closed_form(position, dim, length, theta):
+    """rotate (reference src/attention.rs:41-57) against the RoFormer /
+    upstream definition in float64: inv_freq_i = theta^(-2i/dim) for
+    i < dim/2, angle = position * inv_freq_i, and the rotate-half pairing of
+    x[i] with x[i + dim/2]; dims past `dim` pass through. A frequency
+    exponent of i/dim, an adjacent-pair rotation or a wrong sign fails."""
+    rng = np.random.default_rng(position + dim)
+    x = rng.standard_normal(length).astype(np.float32)
+    got = O.rotate(x.copy(), position, dim, theta)
+    half = dim // 2
+    i = np.arange(half, dtype=np.float64)
+    angle = position * theta ** (-2.0 * i / dim)
+    a, b = x[:half].astype(np.float64), x[half:dim].astype(np.float64)
+    want = x.astype(np.float64).copy()
+    want[:half] = a * np.cos(angle) - b * np.sin(angle)
+    want[half:dim] = b * np.cos(angle) + a * np.sin(angle)
+    # float32 angles: |error| <= a few ulp of the angle (position up to 8190)
+    tol = 4 * np.spacing(np.float32(max(position, 1))) * (np.abs(a) + np.abs(b)).max() + 1e-6
+    assert np.max(np.abs(got - want)) <= tol, np.max(np.abs(got - want))
+    assert np.array_equal(got[dim:], x[dim:])
 
 
 def test_int8_quantizer_invariants():
