@@ -181,6 +181,11 @@ typedef struct QrDecodeDesc {
      * rows fp32 scales, then the int8 values row-major, four to a word). */
     int32_t weights;
     int32_t embedding_bf16;  /* embedding is packed BF16 (element 2i in the low half of word i) */
+    /* Rows of `logits` ([rows, vocab]) and `picks` ([rows, 2]) a launch may
+     * write (1..8), and the snapshot copies that follow each DeltaNet layer's
+     * conv_state and recurrent state (0..7; copy s of a [n] state at
+     * state + s * n, the layout of the ops' snapshot mode). */
+    int32_t rows, snapshots;
 } QrDecodeDesc;
 enum { QR_DECODE_F32 = 0, QR_DECODE_INT8 = 2 };
 typedef struct QrDecodePlan QrDecodePlan;
@@ -196,6 +201,14 @@ int qr_decode_step(Context* c, QrDecodePlan* p, int token, int position);
  * back before the next step (src/device.rs:1568-1584); the tokens are the
  * same. */
 int qr_decode_steps(Context* c, QrDecodePlan* p, int first_token, int position, int n, int32_t* ids, float* bad);
+/* One launch of the step for a verify row: token at position, its logits in
+ * logits row `row` and [argmax, non-finite count] in picks row `row`, and when
+ * snap > 0 the DeltaNet states after this token also written to snapshot copy
+ * `snap`. Every row is the same kernel as qr_decode_step, so a verify row is
+ * bit for bit the decode step of its position (the reference's contract for
+ * verify rows, native/rocm/bridge.cpp:197-215, src/device.rs:1514-1531). No
+ * counterpart in the reference's ABI. */
+int qr_decode_step_row(Context* c, QrDecodePlan* p, int token, int position, int row, int snap);
 void qr_decode_plan_free(Context* c, QrDecodePlan* p);
 
 /* Embedding rows of a prefill chunk in one call: dst[r, 0..width) = row

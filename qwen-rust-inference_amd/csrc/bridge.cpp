@@ -569,6 +569,12 @@ int qr_decode_step(Context* c, QrDecodePlan* p, int token, int position) {
     if (token < 0) return fail(c, "decode step token", -1);
     return launched(c, "decode step", qr::decode_step(p, token, position, -1, c->stream));
 }
+int qr_decode_step_row(Context* c, QrDecodePlan* p, int token, int position, int row, int snap) {
+    if (!p) return fail(c, "decode step without a plan", -1);
+    auto sc = scope(c, [&] { return std::string("decode_step"); });
+    if (token < 0 || row < 0 || snap < 0) return fail(c, "decode step token / row / snapshot", -1);
+    return launched(c, "decode step", qr::decode_step(p, token, position, -1, c->stream, row, snap));
+}
 int qr_decode_steps(Context* c, QrDecodePlan* p, int first_token, int position, int n, int32_t* ids, float* bad) {
     if (!p || !ids || !bad || n < 1 || first_token < 0 || position < 0) return fail(c, "decode steps shape", -1);
     int e = qr::decode_history_clear(p, n, c->stream);

@@ -115,7 +115,8 @@ int decode_plan_create(const QrDecodeDesc& d, QrDecodePlan** out, hipStream_t s,
 void decode_plan_free(QrDecodePlan* p);
 // token -1: the previous launch's argmax (read on the device). slot >= 0: the
 // step's [argmax, non-finite count] also goes to history slot `slot`.
-int decode_step(QrDecodePlan* p, int token, int position, int slot, hipStream_t s);
+// slot >= 0: the chained-steps history slot; row: logits / picks row; snap: snapshot copy (0: none).
+int decode_step(QrDecodePlan* p, int token, int position, int slot, hipStream_t s, int row = 0, int snap = 0);
 int decode_history_clear(QrDecodePlan* p, int n, hipStream_t s);
 int decode_history_read(QrDecodePlan* p, int n, float* out, hipStream_t s);
 

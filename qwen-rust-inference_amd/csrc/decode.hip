@@ -104,6 +104,7 @@ struct Args {
     int emb_bf16;  // the embedding table is packed BF16 (two per word, element 2i low)
     int chain;     // 1: the token is the previous launch's argmax (picks[0]), not `token`
     float* hist;   // when set: this launch's [argmax, non-finite count] also lands here
+    int snap;      // > 0: the updated DeltaNet conv and recurrent states are also written to this snapshot copy
     unsigned epoch;
     float eps;
     float rope_cs[ROT / 2], rope_sn[ROT / 2];  // cos / sin of pos / theta^(2i / rot)
@@ -557,6 +558,12 @@ __device__ __forceinline__ bool phase_din(const Args& a, Rs rs, LayerP w, int L,
         stp(hs, ho, h1);
         stp(hs, ho + 4, h2);
         stp(hs, ho + 8, mine);
+        if (a.snap > 0) {  // copy `snap` of the history (the layout of the op path's snapshots)
+            const unsigned so = ho + unsigned(a.snap) * unsigned(CH * (CONVK - 1) * 4);
+            stp(hs, so, h1);
+            stp(hs, so + 4, h2);
+            stp(hs, so + 8, mine);
+        }
     } else if (lane < DIN_RPW && row < DIN_ROWS) {
         stt(rs, SOFF(ab) + 8u * unsigned(row - CH), mine, t);
     }
@@ -681,6 +688,17 @@ __device__ __forceinline__ bool phase_mix(const Args& a, Rs rs, LayerP w, int L,
         stp(S, so + DV * 4u, wb[k].y);
         stp(S, so + 2u * DV * 4u, wb[k].z);
         stp(S, so + 3u * DV * 4u, wb[k].w);
+    }
+    if (a.snap > 0) {  // the same state into snapshot copy `snap` (one [VH][DK][DV] state per copy)
+        const unsigned sb = base + unsigned(a.snap) * unsigned(VH * DK * DV * 4);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const unsigned so = sb + unsigned(4 * k) * DV * 4u;
+            stp(S, so, wb[k].x);
+            stp(S, so + DV * 4u, wb[k].y);
+            stp(S, so + 2u * DV * 4u, wb[k].z);
+            stp(S, so + 3u * DV * 4u, wb[k].w);
+        }
     }
     __builtin_amdgcn_s_setprio(0);
     return true;
@@ -1453,6 +1471,10 @@ struct QrDecodePlan {
     int device = 0;
     std::vector<float> host_denom;  // theta^(2i / rot) by the host libm
     int capacity = 0;
+    int snapshots = 0;          // snapshot copies behind each DeltaNet state (desc.snapshots)
+    int rows = 1;               // logits / picks rows (desc.rows)
+    float* logits = nullptr;    // row 0 of the logits rows ([rows, vocab])
+    float* picks = nullptr;     // row 0 of the [argmax, non-finite count] rows
     bool q8 = false;  // int8 matrices and LM head: decode_kernel<true>
     float* hist = nullptr;  // [capacity][argmax, non-finite count] of chained steps
 };
@@ -1467,6 +1489,8 @@ const char* decode_unsupported(const QrDecodeDesc& d) {
         return "one-launch decode is built for the Qwen3.5-0.8B geometry only";
     if (d.layers < 1 || d.layers > 64) return "one-launch decode: 1..64 layers";
     if (d.vocab < 1 || d.capacity < 1) return "one-launch decode: empty vocabulary or capacity";
+    if (d.rows < 1 || d.rows > 8 || d.snapshots < 0 || d.snapshots > 7)
+        return "one-launch decode: 1..8 logits rows and 0..7 snapshots";
     // every buffer offset is 32-bit: the largest matrix and cache must stay under 4 GiB
     if (double(d.vocab) * H * 4.0 >= 4294967296.0 || double(d.capacity) * NKV * HD * 4.0 >= 4294967296.0)
         return "one-launch decode: vocabulary or capacity beyond 32-bit offsets";
@@ -1548,6 +1572,10 @@ int decode_plan_create(const QrDecodeDesc& d, QrDecodePlan** out, hipStream_t s,
     auto* p = new QrDecodePlan;
     std::memset(&p->args, 0, sizeof(p->args));
     p->capacity = d.capacity;
+    p->snapshots = d.snapshots;
+    p->rows = d.rows;
+    p->logits = d.logits;
+    p->picks = d.picks;
     p->q8 = q8;
     p->device = dev;
     unsigned epoch = 0;
@@ -1595,11 +1623,15 @@ void decode_plan_free(QrDecodePlan* p) {
     delete p;
 }
 
-int decode_step(QrDecodePlan* p, int token, int position, int slot, hipStream_t s) {
+int decode_step(QrDecodePlan* p, int token, int position, int slot, hipStream_t s, int row, int snap) {
     using namespace dec;
     Args& a = p->args;
-    if (token < -1 || token >= a.vocab || position < 0 || position >= p->capacity || slot >= p->capacity)
+    if (token < -1 || token >= a.vocab || position < 0 || position >= p->capacity || slot >= p->capacity ||
+        row < 0 || row >= p->rows || snap < 0 || snap > p->snapshots || (row > 0 && token < 0))
         return int(hipErrorInvalidValue);
+    a.logits = p->logits + size_t(row) * size_t(a.vocab);
+    a.picks = p->picks + 2 * row;
+    a.snap = snap;
     a.chain = token < 0 ? 1 : 0;
     a.token = token < 0 ? 0 : token;
     a.hist = slot < 0 ? nullptr : p->hist + 2 * slot;

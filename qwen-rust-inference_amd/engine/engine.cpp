@@ -89,6 +89,7 @@ struct Api {
     int (*delta_mixer)(Context*, const QrDelta*) = nullptr;
     int (*decode_plan)(Context*, const QrDecodeDesc*, QrDecodePlan**) = nullptr;
     int (*decode_step)(Context*, QrDecodePlan*, int, int) = nullptr;
+    int (*decode_step_row)(Context*, QrDecodePlan*, int, int, int, int) = nullptr;
     int (*decode_steps)(Context*, QrDecodePlan*, int, int, int, int32_t*, float*) = nullptr;
     void (*decode_free)(Context*, QrDecodePlan*) = nullptr;
     int (*embed_rows)(Context*, float*, const float*, int, int, int, const int32_t*, int) = nullptr;
@@ -161,6 +162,7 @@ struct Api {
             decode_step = symbol<decltype(decode_step)>("qr_decode_step", false);
             decode_free = symbol<decltype(decode_free)>("qr_decode_plan_free", false);
             decode_steps = symbol<decltype(decode_steps)>("qr_decode_steps", false);
+            decode_step_row = symbol<decltype(decode_step_row)>("qr_decode_step_row", false);
             if (!decode_plan || !decode_step || !decode_free) decode_plan = nullptr;
         }
         if (!(disable & QE_NO_EMBED_ROWS)) embed_rows = symbol<decltype(embed_rows)>("qr_embed_rows", false);
@@ -586,6 +588,8 @@ struct QeRun {
         desc.layer = layers.data();
         desc.weights = q8 ? QR_DECODE_INT8 : QR_DECODE_F32;
         desc.embedding_bf16 = model->embedding.bf16 ? 1 : 0;
+        desc.rows = int32(std::min(kVerifyRows, chunk));
+        desc.snapshots = int32(snapshots);
         QrDecodePlan* p = nullptr;
         if (a->decode_plan(a->ctx, &desc, &p) == 0) plan = p;
     }
@@ -605,6 +609,30 @@ struct QeRun {
             out = logits.read(size_t(model->config.vocab_size));
         }
         position += 1;
+        return out;
+    }
+    // The rows of a verify pass through the plan, one launch per row (the
+    // decode step of each row's position, so every row equals the sequential
+    // decode step bit for bit, as the reference requires of verify rows,
+    // src/device.rs:1514-1531): row r's logits / picks in row r of the run's
+    // buffers, the DeltaNet states after row r in snapshot copy r + 1 for
+    // r < snapshot_rows (what accept restores). The launches are queued back
+    // to back; the host reads once at the end.
+    std::vector<float> forward_planned_rows(const uint32_t* ids, size_t t) {
+        const Api* a = api();
+        for (size_t r = 0; r < t; ++r)
+            a->check(a->decode_step_row(a->ctx, plan, int(ids[r]), int(position + r), int(r),
+                                        r < snapshot_rows ? int(r + 1) : 0));
+        std::vector<float> out;
+        std::vector<float> pk(2 * t);
+        a->check(a->read(a->ctx, pk.data(), picks.p, pk.size()));
+        for (size_t r = 0; r < t; ++r) require(pk[2 * r + 1] < 1e30f, "one-launch decode step timed out at a stage barrier");
+        if (greedy_rows) {
+            picked = read_picks(0, t);
+        } else {
+            out = logits.read(size_t(model->config.vocab_size) * t);
+        }
+        position += t;
         return out;
     }
 
@@ -838,6 +866,12 @@ struct QeRun {
         if (plan && t == 1 && !rec && logit_rows == 1 && snapshot_rows == 0 && pick_slot == 0) {
             auto out = forward_planned(ids[0]);
             logits_unread = greedy_rows;
+            return out;
+        }
+        if (plan && a->decode_step_row && t > 1 && !rec && logit_rows == t && pick_slot == 0 &&
+            t <= std::min(kVerifyRows, chunk)) {
+            auto out = forward_planned_rows(ids, t);
+            logits_unread = false;
             return out;
         }
         size_t h = size_t(model->config.hidden_size);
