@@ -11,15 +11,21 @@ stream synchronisation on both sides. value = decode tokens/s at ctx 454.
 Also reported: weight-read HBM GB/s of the decode step; the prefill rate of
 the prompt; the 2644- and 10,240-token prefills (config 3: median of timed
 runs, tok/s and FLOP rate against the fp32 MFMA peak; --no-prefill skips);
-decode at ctx 8192 (config 4; --no-long skips); int8 decode at ctx 454 and
-a 4-row verify with snapshots (config 5; --no-int8 skips). roofline: the one-launch decode kernel
+decode at ctx 8192 after a real 8192-token prefill (config 4; --no-long
+skips); int8 decode at ctx 454 and a 4-row verify with snapshots (config 5;
+--no-int8 skips); the drop-in rates (an unmodified reference engine: the op
+sequence of bridge calls, no one-launch step or fp32 fusions, prefill in
+128-token chunks; --no-dropin skips). roofline: the one-launch decode kernel
 (decode_kernel: every layer, lm_head and argmax of a step), timed with a
 hipEvent pair around each launch on the bridge's stream in a profiled pass of
 the same decode; achieved = the step's algorithmic HBM bytes (every matrix
 once, DeltaNet recurrent and conv states read and written, K/V rows of the
 context read and the new row written, logits written) / launch duration.
 cpu_baseline: the CPU oracle (restatement of the reference's Backend::Vector
-path) on a bounded sample on this host.
+path) on this host, decode steps at ctx 454 from the GPU run's state after
+the prompt: one warmup step and --cpu-steps timed steps, at the reference's
+default thread count min(cores, 8) (the value) and at every core of this
+job's CPU share (at most 16 on a one-GPU box).
 """
 import argparse
 import json
@@ -37,6 +43,45 @@ HBM_PEAK_GBS = 8000.0
 # HBM bytes per decode_kernel launch at ctx ~590 from the rocprofv3 FETCH_SIZE / WRITE_SIZE passes
 # (calibrated on a 512 MiB copy; profiles/decode_kernel_config2.md).
 DECODE_TRAFFIC_BYTES = 3_158_000_000
+PREFILL_CHUNK = 128  # the reference engine's prefill chunk (src/device.rs)
+
+
+def mall_resident_bytes(c) -> int:
+    """Weight bytes the one-launch decode reads with allocating loads below
+    position 1536 (csrc/decode.hip kKeepAqkv / kKeepDin, fp32): part 0 (rows
+    3u and 3u + 1) of q|k|v in every attention layer and part 0 (rows 4u and
+    4u + 1) of qkv|a|b in the DeltaNet layers among layers 0-11, over the
+    2048 wave units u. They stay in the 256 MB memory-side cache between
+    steps, so that part of the weight-read rate is not HBM traffic."""
+    units = 2048
+    aqkv_rows = 2 * c.num_heads * c.head_dim + 2 * c.num_kv_heads * c.head_dim
+    din_rows = c.channels + 2 * c.value_heads
+    aqkv = sum(1 for u in range(units) for r in (0, 1) if 3 * u + r < aqkv_rows)
+    din = sum(1 for u in range(units) for r in (0, 1) if 4 * u + r < din_rows)
+    row = 4 * c.hidden_size
+    attn = [layer for layer in range(c.num_layers) if c.attention[layer]]
+    delta_kept = [layer for layer in range(min(12, c.num_layers)) if not c.attention[layer]]
+    return row * (aqkv * len(attn) + din * len(delta_kept))
+
+
+def host_cpu():
+    """nproc, the CPU model and the cgroup CPU quota (the reference records the
+    same, src/benchmark.rs:156-174)."""
+    model = ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    try:
+        quota = open("/sys/fs/cgroup/cpu.max").read().strip()
+    except OSError:
+        quota = "n/a"
+    return {"nproc": os.cpu_count(), "affinity": len(os.sched_getaffinity(0)), "model": model, "cgroup_cpu_max": quota}
+
+
 MFMA_F32_PEAK_TFLOPS = 157.3
 METRIC = "decode tok/s @ctx 454 & 8192 + HBM GB/s; prefill tok/s @2644"
 
@@ -99,7 +144,10 @@ def main():
     ap.add_argument("--no-long", dest="long", action="store_false", help="skip decode at ctx 8192 (config 4)")
     ap.add_argument("--no-int8", dest="int8", action="store_false",
                     help="skip the int8 decode and 4-row verify at ctx 454 (config 5)")
-    ap.add_argument("--cpu-steps", type=int, default=6, help="oracle steps of the CPU baseline sample (0: skip)")
+    ap.add_argument("--no-dropin", dest="dropin", action="store_false",
+                    help="skip the drop-in (unmodified reference engine call sequence) rates")
+    ap.add_argument("--cpu-steps", type=int, default=3,
+                    help="timed oracle decode steps per thread count of the CPU baseline (0: skip)")
     ap.add_argument("--profile-steps", type=int, default=16)
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="also run one device copy of MIB MiB (a plain copy kernel of known size, the scale "
@@ -184,6 +232,9 @@ def main():
                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": DECODE_TRAFFIC_BYTES,
                     "kernel": "decode_kernel (one-launch decode step: 24 layers, lm_head, argmax)",
                     "bytes_per_launch": bytes_total // calls, "launch_us": round(step_ms / calls * 1e3, 2),
+                    "mall_resident_bytes": mall_resident_bytes(c),
+                    "note": "achieved counts every weight byte once per step; mall_resident_bytes of them are kept "
+                            "in the 256 MB memory-side cache between steps and do not reach HBM",
                     "launches": calls, "context": [pos0 + 1, pos0 + calls],
                     "bridge_gpu_us_per_step": round(total_ms / args.profile_steps * 1e3, 1)}
     else:  # op sequence (the bridge declined the plan): the fp32 GEMVs
@@ -228,33 +279,25 @@ def main():
             log(f"stream read failed: {r.stderr.strip()[-200:]}")
 
     if args.long:
-        # Decode at ctx 8192 (config 4): the context's DeltaNet states and
-        # K/V rows are seeded synthetic state written into the run (a decode
-        # step's cost does not depend on their values), then 64 greedy steps.
+        # Decode at ctx 8192 (config 4): a real prefill of 8192 uniform random
+        # ids (seed 5, one chunk), then 2 untimed and 64 timed greedy steps.
         n = 8192
-        r3 = model.new_run(n + 80, chunk=64)
-        r3.set_position(n - 1)
-        rng = np.random.default_rng(5)
-        for layer in range(c.num_layers):
-            for which in range(4):
-                size = r3.state(layer, which).size
-                if size:
-                    scale = 0.05 if which == 1 else 1.0
-                    r3.write_state(layer, which, (rng.standard_normal(size) * scale).astype(np.float32))
-        tok = int(rng.integers(0, c.vocab_size))
+        ids4 = [int(v) for v in np.random.default_rng(5).integers(0, c.vocab_size, n)]
+        r3 = model.new_run(n + 80, chunk=n)
+        tok = int(np.argmax(r3.prefill(ids4)))
         for _ in range(2):
             tok = r3.step_greedy(tok)
         model.sync()
         t = time.perf_counter()
         r3.decode_greedy(tok, 65)
         dt = time.perf_counter() - t
-        long_bytes = sum(step_bytes(c, weight_bytes, p + 1) for p in range(n + 1, n + 65)) / 64
+        long_bytes = sum(step_bytes(c, weight_bytes, p + 1) for p in range(n + 2, n + 66)) / 64
         out["decode_8192_tok_s"] = round(64 / dt, 2)
         out["decode_8192_hbm_frac"] = round(long_bytes * 64 / dt / 1e9 / HBM_PEAK_GBS, 4)
         # the target's measure: weight bytes only (the K/V read is outside it)
         out["decode_8192_weight_read_frac"] = round(weight_bytes * 64 / dt / 1e9 / HBM_PEAK_GBS, 4)
         log(f"decode @8192: {dt / 64 * 1e3:.3f} ms/token, {long_bytes * 64 / dt / 1e9:.0f} GB/s algorithmic")
-        del r3
+        r3.close()
 
     if args.int8:
         # Config 5: int8 per-row weights (quantised on the host by the engine, as the
@@ -292,7 +335,43 @@ def main():
         dt = (time.perf_counter() - t) / reps
         out["int8_verify4_ms"] = round(dt * 1e3, 3)
         log(f"int8 4-row verify with snapshots + accept(1): {dt * 1e3:.3f} ms")
-        del r8, m8
+        r8.close()
+        m8.close()
+
+    if args.dropin:
+        # What an unmodified reference engine would get from this bridge: its
+        # fp32 call sequence (one qr_gemv per matrix plus separate norm ops, no
+        # one-launch step, a per-token embedding copy) and 128-token prefill
+        # chunks (src/device.rs PREFILL_CHUNK).
+        md = E.Model(w, disable=E.NO_DECODE_STEP | E.NO_F32_FUSIONS | E.NO_EMBED_ROWS)
+        rd = md.new_run(args.prompt + 64, chunk=PREFILL_CHUNK)
+        tok = int(np.argmax(rd.prefill(prompt)))
+        for _ in range(3):
+            tok = rd.step_greedy(tok)
+        md.sync()
+        t = time.perf_counter()
+        for _ in range(32):
+            tok = rd.step_greedy(tok)
+        md.sync()
+        dt = (time.perf_counter() - t) / 32
+        out["decode_454_dropin_tok_s"] = round(1.0 / dt, 2)
+        log(f"drop-in decode @454 (op sequence): {dt * 1e3:.3f} ms/token")
+        rd.close()
+        n = 2644
+        ids2 = [int(v) for v in np.random.default_rng(2).integers(0, c.vocab_size, n)]
+        times = []
+        for rep in range(3):
+            r2 = md.new_run(n, chunk=PREFILL_CHUNK)
+            md.sync()
+            t = time.perf_counter()
+            r2.prefill(ids2)
+            if rep:
+                times.append(time.perf_counter() - t)
+            r2.close()
+        dt = float(np.median(times))
+        out["prefill_2644_chunk128_tok_s"] = round(n / dt, 1)
+        log(f"drop-in prefill 2644 in 128-token chunks: {dt * 1e3:.1f} ms")
+        md.close()
 
     # prefill last: measured right after the 10,240-token prefill, the ctx-8192
     # decode took 0.761 ms per token, measured before the prefills 0.743 ms
@@ -312,7 +391,7 @@ def main():
                 dt = time.perf_counter() - t
                 if rep:
                     times.append(dt)
-                del r2
+                r2.close()
             dt = float(np.median(times))
             tflops = prefill_flops(c, n, weight_bytes // 4) / dt / 1e12
             out[f"prefill_{n}_tok_s"] = round(n / dt, 1)
@@ -333,22 +412,41 @@ def main():
         br.close()
 
     if args.cpu_steps > 0:
+        # The oracle (C++ restatement of the reference's Backend::Vector CPU
+        # decode) from the GPU run's state after the 454-token prompt, on the
+        # same greedy tokens: decode steps at ctx 454.
         import oracle as O
-        threads = min(16, os.cpu_count() or 1)
-        O.set_threads(threads)
-        s = O.Oracle(w).new_state()
-        times = []
-        for tok in prompt[:args.cpu_steps]:
+        cpu = host_cpu()
+        share = min(cpu["affinity"], 16)
+        rc = model.new_run(args.prompt + 8, chunk=args.prompt)
+        rc.prefill(prompt)
+        parts = {(layer, which): rc.state(layer, which) for layer in range(c.num_layers) for which in range(4)}
+        rc.close()
+        oracle = O.Oracle(w)
+        rates = {}
+        for threads in sorted({min(share, 8), share}):
+            O.set_threads(threads)
+            s = oracle.new_state()
+            s.load(args.prompt, lambda layer, which: parts[(layer, which)])
+            s.step(ids[0], O.VECTOR)  # warmup
             t = time.perf_counter()
-            s.step(tok, O.VECTOR)
-            times.append(time.perf_counter() - t)
-        per = sum(times[1:]) / max(1, len(times) - 1)
-        out["cpu_baseline"] = {"value": round(1.0 / per, 3), "unit": "tok/s", "cores": threads, "kind": "port",
-                               "sample": f"{args.cpu_steps} token-by-token steps (positions 0-{args.cpu_steps - 1}) of "
-                                         "the config-2 prompt through the CPU oracle's Backend::Vector path (C++ "
-                                         "restatement of the reference's Rust CPU decode), first step untimed; "
-                                         f"{threads} threads"}
-        log(f"cpu baseline: {per * 1e3:.1f} ms/token on {threads} threads")
+            for tok in ids[1:1 + args.cpu_steps]:
+                s.step(tok, O.VECTOR)
+            rates[threads] = args.cpu_steps / (time.perf_counter() - t)
+            log(f"cpu baseline: {1e3 / rates[threads]:.1f} ms/token on {threads} threads")
+            del s
+        default = min(share, 8)
+        out["cpu_baseline"] = {"value": round(rates[default], 3), "unit": "tok/s", "cores": default, "kind": "port",
+                               "sample": f"{args.cpu_steps} decode steps at ctx {args.prompt + 2}.."
+                                         f"{args.prompt + 1 + args.cpu_steps} (after one warmup step) of the config-2 "
+                                         "greedy tokens, from the GPU run's state after the prompt, through the CPU "
+                                         "oracle's Backend::Vector path (C++ restatement of the reference's Rust CPU "
+                                         f"decode); {default} threads = the reference default min(cores, 8)",
+                               "all_cores": {"value": round(rates[share], 3), "cores": share},
+                               "host": cpu}
+
+    run.close()
+    model.close()
     print(json.dumps(out), flush=True)
 
 

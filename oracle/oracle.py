@@ -57,6 +57,7 @@ def lib():
         L.qo_rotate.argtypes = [_F, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_float]
         L.qo_attend.argtypes = [_F, _F, _F, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, _F]
         L.qo_set_threads.argtypes = [ctypes.c_int]
+        L.qo_state_load.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p]
         _lib = L
     return _lib
 
@@ -134,6 +135,19 @@ class State:
             fn = _TRACE()
         check(lib().qo_step(self.oracle.ptr, self.ptr, int(token), backend, fp(logits), None, fn, None))
         return (logits, records) if trace else logits
+
+    def load(self, position: int, read):
+        """Replace the whole state with `position` tokens' worth; read(layer,
+        which) returns each part as part() lays it out."""
+        c = self.oracle.config
+        keep = []
+        table = (ctypes.c_void_p * (4 * c.num_layers))()
+        for layer in range(c.num_layers):
+            for which in range(4):
+                v = np.ascontiguousarray(read(layer, which), dtype=np.float32)
+                keep.append(v)
+                table[4 * layer + which] = v.ctypes.data if v.size else None
+        check(lib().qo_state_load(self.oracle.ptr, self.ptr, int(position), table))
 
     def part(self, layer: int, which: int) -> np.ndarray:
         """which: 0 conv history, 1 recurrent state, 2 keys, 3 values."""

@@ -756,6 +756,33 @@ int qo_state_read(const qo_model* m, const qo_state* s, int layer, int which, fl
     }
     return 0;
 }
+// Replaces the whole state with `position` tokens' worth (the reference's
+// load_state for a CPU ModelState, src/device.rs:2380-2537): parts[layer * 4 +
+// which] as qo_state_read lays them out (keys / values: position rows).
+int qo_state_load(const qo_model* m, qo_state* s, int64_t position, const float* const* parts) {
+    return guarded([&] {
+        require(position >= 0, "state position");
+        size_t w = size_t(m->c.num_kv_heads * m->c.head_dim);
+        for (size_t l = 0; l < s->layers.size(); ++l) {
+            auto& L = s->layers[l];
+            const float* const* p = parts + 4 * l;
+            if (m->layers[l].attention) {
+                require(position == 0 || (p[2] && p[3]), "state part missing");
+                L.keys.assign(size_t(position), std::vector<float>(w));
+                L.values.assign(size_t(position), std::vector<float>(w));
+                for (size_t r = 0; r < size_t(position); ++r) {
+                    std::memcpy(L.keys[r].data(), p[2] + r * w, w * 4);
+                    std::memcpy(L.values[r].data(), p[3] + r * w, w * 4);
+                }
+            } else {
+                require(p[0] && p[1], "state part missing");
+                std::memcpy(L.conv.data(), p[0], L.conv.size() * 4);
+                std::memcpy(L.recurrent.data(), p[1], L.recurrent.size() * 4);
+            }
+        }
+        s->position = size_t(position);
+    });
+}
 
 // One token through the model (Model::step, src/model.rs:335-382). backend:
 // 0 = Backend::Reference, 2 = Backend::Vector. logits_out: vocab floats (or

@@ -295,3 +295,19 @@ def test_greedy_selection_rules():
     assert O.select_greedy(np.array([-1], np.float32)) == 0
     with pytest.raises(RuntimeError):
         O.select_greedy(np.array([1, np.nan], np.float32))
+
+
+def test_state_load_round_trip(fixture_model):
+    """A state loaded part by part (the CPU side of the reference's
+    load_state / inspect_state interchange, src/device.rs:2380-2537)
+    continues exactly like the state it was read from."""
+    s = fixture_model.new_state()
+    for tok in [1, 4, 2, 8, 3, 5, 7]:
+        s.step(tok, O.REFERENCE)
+    t = fixture_model.new_state()
+    t.load(s.position, s.part)
+    assert t.position == s.position
+    for tok in [6, 2]:
+        assert np.array_equal(t.step(tok, O.REFERENCE), s.step(tok, O.REFERENCE))
+    with pytest.raises(RuntimeError):
+        t.load(3, lambda layer, which: np.zeros(0, np.float32))
