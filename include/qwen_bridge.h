@@ -211,6 +211,16 @@ int qr_decode_steps(Context* c, QrDecodePlan* p, int first_token, int position, 
 int qr_decode_step_row(Context* c, QrDecodePlan* p, int token, int position, int row, int snap);
 void qr_decode_plan_free(Context* c, QrDecodePlan* p);
 
+/* Op 16 (Argmax) without any allocation: the same slot meanings and result
+ * as qr_run(c, QR_ARGMAX, rows, a) (p[0]: [rows, 2] out, p[1]: [rows, n[0]]
+ * logits), but the per-slice partials live in a fixed per-device array of the
+ * library (12 KiB, held until the process ends), so no call allocates device
+ * memory. At most 8 rows of at most 1,048,576 entries (larger inputs are
+ * refused with an error). Calls that overlap on one device share the array
+ * and race. No counterpart in the reference; for callers that cannot
+ * allocate (code under HIP graph capture, tight serving loops). */
+int qr_argmax_fixed(Context* c, int rows, const Params* a);
+
 /* Embedding rows of a prefill chunk in one call: dst[r, 0..width) = row
  * ids[r] of `table` for r < n (ids on the host, each checked against
  * table_rows; bf16 != 0: `table` is packed BF16 and the rows are widened).

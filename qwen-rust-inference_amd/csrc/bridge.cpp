@@ -270,6 +270,7 @@ int qr_create(Context** out) {
     }
     h = hipMalloc(reinterpret_cast<void**>(&c->ticket), 256);
     if (h == hipSuccess) h = hipMemset(c->ticket, 0, 256);
+    if (h == hipSuccess) h = hipError_t(qr::argmax_fixed_init());  // qr_argmax_fixed's array on this device
     if (h != hipSuccess) {
         (void)hipStreamDestroy(c->stream);
         delete c;
@@ -550,6 +551,16 @@ int qr_delta_mixer(Context* c, const QrDelta* d) {
     if (int s = qr_run(c, QR_DELTA_QK, vh * t, &qk)) return s;
     if (int s = qr_run(c, QR_DELTA_RULE_GATED, vd, &rule)) return s;
     return qr_run(c, QR_RMS_NORM_GATE, vh * t, &gate);
+}
+
+// Argmax with fixed partials (no counterpart in the reference's ABI).
+int qr_argmax_fixed(Context* c, int rows, const Params* ap) {
+    if (!ap) return fail(c, "argmax arguments", -1);
+    const Params& a = *ap;
+    if (rows < 1 || rows > qr::kArgmaxFixedRows || a.n[0] < 1 || a.n[0] > qr::kArgmaxFixedLength)
+        return fail(c, "qr_argmax_fixed: rows must be 1..8 and the row length 1..1048576", -1);
+    // (not bracketed by the profiler: its events are created on demand)
+    return launched(c, "argmax_fixed", qr::run_argmax_fixed(c->stream, rows, a));
 }
 
 // One-launch decode (no counterpart in the reference's ABI).

@@ -101,6 +101,13 @@ int run_embed(hipStream_t s, int op, int count, const Params& a);
 // dst[r] = table row ids[r] (fp32, or packed BF16 widened), r < n; ids on the host.
 int run_embed_rows(hipStream_t s, float* dst, const void* table, int width, bool bf16, const int32_t* ids, int n);
 int run_argmax(hipStream_t s, int rows, const Params& a, float* parts, size_t parts_len);
+// The same argmax with its partials in a fixed per-device array: at most
+// kArgmaxFixedRows rows of kArgmaxFixedLength entries; allocates nothing.
+// argmax_fixed_init resolves the array's device address for the current
+// device (once per device).
+constexpr int kArgmaxFixedRows = 8, kArgmaxFixedLength = 1 << 20;
+int argmax_fixed_init();
+int run_argmax_fixed(hipStream_t s, int rows, const Params& a);
 size_t argmax_parts_needed(int rows, int n);
 
 // attention.hip --------------------------------------------------------------

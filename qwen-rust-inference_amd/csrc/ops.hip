@@ -6,6 +6,8 @@
 // (native/rocm/reference.h:117-232, slot meanings there); the decomposition is
 // this file's own: a wave or block per group for reductions, P lanes per
 // DeltaNet value column with the column's state in VGPRs.
+#include <mutex>
+
 #include "common.h"
 
 namespace qr {
@@ -561,6 +563,49 @@ int run_argmax(hipStream_t s, int rows, const Params& a, float* parts, size_t pa
     if (int e = int(hipGetLastError())) return e;
     hipLaunchKernelGGL(argmax_merge_kernel, dim3(unsigned(rows)), dim3(256), 0, s, a, parts, slices);
     return int(hipGetLastError());
+}
+
+// ---- the argmax with its slice partials in a fixed device array (no
+// allocation on any call; for callers that cannot allocate). Every device the
+// library runs on holds one copy of `scratch` until the process ends; every
+// call on a device shares it, so calls that overlap on one device race (the
+// slices kernel writes every partial the merge reads, so nothing needs
+// clearing between calls). In host code `scratch` names a host-side stand-in:
+// kernels get the device address that hipGetSymbolAddress returns, kept per
+// device.
+namespace {
+static __device__ __align__(256) float scratch[kArgmaxFixedRows * (kArgmaxFixedLength / kArgmaxSlice) * 3];
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+float* g_scratch_ptr[kMaxDevices] = {};
+}  // namespace
+
+int argmax_fixed_init() {
+    int dev = 0;
+    if (hipError_t e = hipGetDevice(&dev)) return int(e);
+    if (dev < 0 || dev >= kMaxDevices) return int(hipErrorInvalidDevice);
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if (!g_scratch_ptr[dev]) {
+        void* ptr = nullptr;
+        if (hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch))) return int(e);
+        g_scratch_ptr[dev] = static_cast<float*>(ptr);
+    }
+    return 0;
+}
+
+int run_argmax_fixed(hipStream_t s, int rows, const Params& a) {
+    const int n = a.n[0];
+    if (rows < 1 || rows > kArgmaxFixedRows || n < 1 || n > kArgmaxFixedLength) return int(hipErrorInvalidValue);
+    if (int e = argmax_fixed_init()) return e;
+    int dev = 0;
+    if (hipError_t e = hipGetDevice(&dev)) return int(e);
+    float* parts = nullptr;
+    {
+        std::lock_guard<std::mutex> lock(g_scratch_mutex);
+        parts = g_scratch_ptr[dev];
+    }
+    constexpr size_t floats = sizeof(scratch) / sizeof(float);
+    return run_argmax(s, rows, a, parts, floats);
 }
 
 }  // namespace qr

@@ -37,7 +37,7 @@ BRIDGE_SYMBOLS = [
     "qr_gemm_bf16_glu", "qr_gemm_i8_glu", "qr_gemm_bf16_add_norm", "qr_gemm_i8_add_norm", "qr_delta_mixer",
     "qr_gemm_f32_group", "qr_gemm_f32_glu", "qr_gemm_f32_add_norm", "qr_profile", "qr_profile_read",
     "qr_decode_plan", "qr_decode_step", "qr_decode_steps", "qr_decode_step_row", "qr_decode_plan_free",
-    "qr_embed_rows",
+    "qr_embed_rows", "qr_argmax_fixed",
 ]
 
 _F = ctypes.POINTER(ctypes.c_float)
