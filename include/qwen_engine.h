@@ -121,6 +121,44 @@ int64_t qe_checkpoint_position(const QeCheckpoint* c);
  * src/device/cli.rs:797-812). ids: n_new outputs. */
 int qe_decode_greedy(QeRun* r, uint32_t first, int64_t n_new, uint32_t* ids, double* seconds);
 
+/* Greedy speculative decoding (generate, src/device/speculative.rs:53-160):
+ * prefill `prompt`, then repeatedly draft up to `depth` tokens after the last
+ * emitted one, check [last, drafts] in one verify_rollback_greedy pass,
+ * emit the leading drafts that equal the model's own picks plus the pick after
+ * them, and accept that many rows. Every emitted token is the main model's
+ * argmax of a verify row, and verify rows equal decode steps bit for bit, so
+ * the output equals plain greedy decoding. Stops after an `eos` token or
+ * `max_new` tokens. The run must be fresh (position 0) with at least `depth`
+ * snapshots (qe_run_new(..., snapshots >= depth)).
+ *
+ * A draft source (the reference's `Draft` trait, speculative.rs:162-183,
+ * without its hidden-state rows, which feed the MTP head): `absorb` receives
+ * the true next tokens (prompt[1..] and the first pick after the prefill, then
+ * each pass's emitted tokens); `draft` writes up to k tokens and returns how
+ * many (or < 0 on error). */
+typedef struct QeDraft {
+    void* user;
+    int (*absorb)(void* user, const uint32_t* next, int64_t n);
+    int64_t (*draft)(void* user, int64_t k, uint32_t* out);
+} QeDraft;
+/* SpeculativeStats (speculative.rs:30-46): verify passes, drafts offered /
+ * accepted at depth j (j < 8), seconds in prefill, drafting and verify. */
+typedef struct QeSpecStats {
+    int64_t passes;
+    int64_t offered[8];
+    int64_t accepted[8];
+    double prefill_s, draft_s, verify_s;
+} QeSpecStats;
+int qe_speculative_generate(QeRun* r, const QeDraft* draft, const uint32_t* prompt, int64_t n_prompt,
+                            int64_t max_new, int64_t depth, const uint32_t* eos, int64_t n_eos, uint32_t* out,
+                            int64_t* n_out, QeSpecStats* stats);
+/* A prompt-lookup draft: the longest suffix of the token history (prompt and
+ * emitted tokens, up to `max_ngram` tokens) that occurred earlier proposes the
+ * tokens that followed its most recent earlier occurrence. No model, so it
+ * suits the random-weight configurations; free with qe_draft_ngram_free. */
+QeDraft* qe_draft_ngram_new(int64_t max_ngram);
+void qe_draft_ngram_free(QeDraft* d);
+
 /* Row-wise symmetric int8 quantiser (src/device.rs:220-239) as the engine
  * uploads it. */
 void qe_quantize_int8_rows(const float* w, int64_t rows, int64_t cols, float* scales, int8_t* q);

@@ -4,6 +4,7 @@
 // reference's own Rust engine binds the same bridge unchanged.
 #include <dlfcn.h>
 
+#include <algorithm>
 #include <atomic>
 #include <chrono>
 #include <cmath>
@@ -1402,6 +1403,129 @@ int qe_restore(QeRun* r, const QeCheckpoint* c) {
 }
 void qe_checkpoint_free(QeCheckpoint* c) { delete c; }
 int64_t qe_checkpoint_position(const QeCheckpoint* c) { return int64_t(c->position); }
+
+// generate (src/device/speculative.rs:53-160), greedy, without the MTP
+// head's hidden rows.
+int qe_speculative_generate(QeRun* r, const QeDraft* draft, const uint32_t* prompt, int64_t n_prompt,
+                            int64_t max_new, int64_t depth, const uint32_t* eos, int64_t n_eos, uint32_t* out,
+                            int64_t* n_out, QeSpecStats* stats) {
+    return guarded([&] {
+        require(draft && draft->absorb && draft->draft && out && n_out, "speculative: missing draft or output");
+        require(n_prompt > 0 && depth >= 1 && depth <= 7 && size_t(depth) <= r->snapshots && r->position == 0,
+                "speculative: empty prompt, depth beyond the run's snapshots, or used run");
+        using clock = std::chrono::steady_clock;
+        auto secs = [](clock::time_point t) { return std::chrono::duration<double>(clock::now() - t).count(); };
+        QeSpecStats st{};
+        auto is_eos = [&](uint32_t id) { return std::find(eos, eos + std::max<int64_t>(n_eos, 0), id) != eos + std::max<int64_t>(n_eos, 0); };
+        int64_t n = 0;
+        *n_out = 0;
+        if (max_new > 0) {
+            auto t = clock::now();
+            auto logits = r->prefill(prompt, size_t(n_prompt));
+            require(logits.has_value(), "speculative: prefill returned no logits");
+            st.prefill_s = secs(t);
+            uint32_t cur = QeRun::select_greedy(*logits);
+            out[n++] = cur;
+            // the draft absorbs the true next token of every prompt position
+            std::vector<uint32_t> next(prompt + 1, prompt + n_prompt);
+            next.push_back(cur);
+            t = clock::now();
+            require(draft->absorb(draft->user, next.data(), int64_t(next.size())) == 0, "speculative: draft absorb failed");
+            st.draft_s += secs(t);
+            while (!is_eos(cur) && n < max_new) {
+                // a pass emits up to k + 1 tokens and needs k + 1 positions
+                const int64_t room = std::min<int64_t>(max_new - n, int64_t(r->capacity - r->position));
+                require(room > 0, "speculative: run capacity exhausted");
+                const int64_t k = std::min<int64_t>(depth, room - 1);
+                std::vector<uint32_t> rows(size_t(k) + 1);
+                rows[0] = cur;
+                t = clock::now();
+                const int64_t got = k > 0 ? draft->draft(draft->user, k, rows.data() + 1) : 0;
+                st.draft_s += secs(t);
+                require(got >= 0 && got <= k, "speculative: draft failed");
+                for (int64_t j = 1; j <= got; ++j)
+                    require(rows[size_t(j)] < uint32_t(r->model->config.vocab_size), "speculative: draft token out of range");
+                rows.resize(size_t(got) + 1);
+                t = clock::now();
+                const auto picks = r->verify_rollback_greedy(rows.data(), rows.size());
+                std::vector<uint32_t> emitted;
+                for (int64_t j = 0; j < got; ++j) st.offered[j] += 1;
+                for (size_t j = 0; j < picks.size(); ++j) {
+                    emitted.push_back(picks[j]);
+                    if (j == size_t(got) || picks[j] != rows[j + 1]) break;
+                    st.accepted[j] += 1;
+                    if (is_eos(picks[j])) break;
+                }
+                r->accept(emitted.size());
+                st.verify_s += secs(t);
+                st.passes += 1;
+                t = clock::now();
+                require(draft->absorb(draft->user, emitted.data(), int64_t(emitted.size())) == 0,
+                        "speculative: draft absorb failed");
+                st.draft_s += secs(t);
+                for (uint32_t id : emitted) {
+                    out[n++] = id;
+                    cur = id;
+                    if (is_eos(id) || n >= max_new) break;
+                }
+            }
+        }
+        *n_out = n;
+        if (stats) *stats = st;
+    });
+}
+
+namespace {
+// Prompt-lookup drafting over the token history.
+struct NgramDraft {
+    QeDraft api{};
+    size_t max_ngram = 3;
+    std::vector<uint32_t> history;
+};
+int ngram_absorb(void* user, const uint32_t* next, int64_t n) {
+    auto* d = static_cast<NgramDraft*>(user);
+    if (n < 0 || (n > 0 && !next)) return -1;
+    // the history is the prompt's first token (never "next") plus every true next token
+    d->history.insert(d->history.end(), next, next + n);
+    return 0;
+}
+int64_t ngram_draft(void* user, int64_t k, uint32_t* out) {
+    auto* d = static_cast<NgramDraft*>(user);
+    const auto& h = d->history;
+    for (size_t len = std::min(d->max_ngram, h.size() > 0 ? h.size() - 1 : 0); len >= 1; --len) {
+        const uint32_t* tail = h.data() + h.size() - len;
+        // the most recent earlier occurrence with k tokens after it, else the
+        // one with the longest continuation
+        size_t best_from = 0;
+        int64_t best = 0;
+        for (size_t start = h.size() - len; start-- > 0 && best < k;) {
+            if (std::equal(tail, tail + len, h.data() + start)) {
+                const size_t from = start + len;
+                const int64_t m = std::min<int64_t>(k, int64_t(h.size() - from));
+                if (m > best) {
+                    best = m;
+                    best_from = from;
+                }
+            }
+        }
+        if (best > 0) {
+            std::copy(h.begin() + long(best_from), h.begin() + long(best_from) + best, out);
+            return best;
+        }
+    }
+    return 0;
+}
+}  // namespace
+
+QeDraft* qe_draft_ngram_new(int64_t max_ngram) {
+    auto* d = new NgramDraft;
+    d->max_ngram = size_t(std::max<int64_t>(1, max_ngram));
+    d->api = QeDraft{d, ngram_absorb, ngram_draft};
+    return &d->api;
+}
+void qe_draft_ngram_free(QeDraft* d) {
+    if (d) delete static_cast<NgramDraft*>(d->user);
+}
 
 int qe_decode_greedy(QeRun* r, uint32_t first, int64_t n_new, uint32_t* ids, double* seconds) {
     return guarded([&] {

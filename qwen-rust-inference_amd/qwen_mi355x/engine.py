@@ -43,6 +43,22 @@ BRIDGE_SYMBOLS = [
 _F = ctypes.POINTER(ctypes.c_float)
 _U32 = ctypes.POINTER(ctypes.c_uint32)
 RECORD_FN = ctypes.CFUNCTYPE(None, ctypes.c_void_p, ctypes.c_int, ctypes.c_char_p, _F, ctypes.c_int64)
+ABSORB_FN = ctypes.CFUNCTYPE(ctypes.c_int, ctypes.c_void_p, _U32, ctypes.c_int64)
+DRAFT_FN = ctypes.CFUNCTYPE(ctypes.c_int64, ctypes.c_void_p, ctypes.c_int64, _U32)
+
+
+class QeDraft(ctypes.Structure):
+    _fields_ = [("user", ctypes.c_void_p), ("absorb", ABSORB_FN), ("draft", DRAFT_FN)]
+
+
+class SpecStats(ctypes.Structure):
+    """SpeculativeStats (reference src/device/speculative.rs:30-46)."""
+    _fields_ = [("passes", ctypes.c_int64), ("offered", ctypes.c_int64 * 8), ("accepted", ctypes.c_int64 * 8),
+                ("prefill_s", ctypes.c_double), ("draft_s", ctypes.c_double), ("verify_s", ctypes.c_double)]
+
+    def as_dict(self, depth: int) -> dict:
+        return {"passes": self.passes, "offered": list(self.offered[:depth]), "accepted": list(self.accepted[:depth]),
+                "prefill_s": self.prefill_s, "draft_s": self.draft_s, "verify_s": self.verify_s}
 _lib = None
 
 
@@ -134,6 +150,12 @@ def lib():
         L.qe_decode_greedy.argtypes = [ctypes.c_void_p, ctypes.c_uint32, ctypes.c_int64, _U32,
                                        ctypes.POINTER(ctypes.c_double)]
         L.qe_quantize_int8_rows.argtypes = [_F, ctypes.c_int64, ctypes.c_int64, _F, ctypes.c_void_p]
+        L.qe_speculative_generate.argtypes = [ctypes.c_void_p, ctypes.POINTER(QeDraft), _U32, ctypes.c_int64,
+                                              ctypes.c_int64, ctypes.c_int64, _U32, ctypes.c_int64, _U32,
+                                              ctypes.POINTER(ctypes.c_int64), ctypes.POINTER(SpecStats)]
+        L.qe_draft_ngram_new.restype = ctypes.POINTER(QeDraft)
+        L.qe_draft_ngram_new.argtypes = [ctypes.c_int64]
+        L.qe_draft_ngram_free.argtypes = [ctypes.POINTER(QeDraft)]
         L.qw_synth_normal.argtypes = [_F, ctypes.c_uint64, ctypes.c_uint64, ctypes.c_uint64, ctypes.c_float,
                                       ctypes.c_int]
         _lib = L
@@ -354,6 +376,47 @@ class Run:
 
     def restore(self, c: Checkpoint):
         _check(lib().qe_restore(self.ptr, c.ptr))
+
+    def speculative_generate(self, prompt, max_new: int, depth: int, draft="ngram", eos=()):
+        """generate (reference src/device/speculative.rs:53-160) on this fresh
+        run (snapshots >= depth). draft: "ngram" (the engine's prompt-lookup
+        draft) or an object with absorb(tokens) and draft(k) -> list of ids.
+        Returns (tokens, stats dict)."""
+        prompt = np.ascontiguousarray(prompt, dtype=np.uint32)
+        eos_a = np.ascontiguousarray(list(eos) or [0], dtype=np.uint32)
+        out = np.empty(max(max_new, 1), dtype=np.uint32)
+        n = ctypes.c_int64()
+        st = SpecStats()
+        owned = None
+        if draft == "ngram":
+            owned = lib().qe_draft_ngram_new(3)
+            dp = owned
+        else:
+            def absorb(_u, toks, k):
+                try:
+                    draft.absorb([int(toks[i]) for i in range(k)])
+                    return 0
+                except Exception:  # noqa: BLE001 - reported to the engine as a failed draft
+                    return -1
+
+            def make(_u, k, outp):
+                try:
+                    ids = list(draft.draft(int(k)))[:k]
+                    for i, v in enumerate(ids):
+                        outp[i] = int(v)
+                    return len(ids)
+                except Exception:  # noqa: BLE001
+                    return -1
+            keep = (ABSORB_FN(absorb), DRAFT_FN(make))
+            d = QeDraft(None, keep[0], keep[1])
+            dp = ctypes.pointer(d)
+        try:
+            _check(lib().qe_speculative_generate(self.ptr, dp, _up(prompt), prompt.size, max_new, depth, _up(eos_a),
+                                                 len(eos), _up(out), ctypes.byref(n), ctypes.byref(st)))
+        finally:
+            if owned is not None:
+                lib().qe_draft_ngram_free(owned)
+        return [int(v) for v in out[:n.value]], st.as_dict(depth)
 
     def decode_greedy(self, first: int, n_new: int):
         """n_new greedy tokens starting with `first` (n_new - 1 forwards);

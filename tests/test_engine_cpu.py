@@ -227,3 +227,50 @@ def test_int8_against_dequantised_oracle(tiny):
     parity(run.prefill(ids), want, rtol=INT8_RTOL, where="int8 logits")
     for t in (3, 77, 500):
         parity(run.step(t), st.step(t, O.REFERENCE), rtol=INT8_RTOL, where="int8 decode")
+
+
+class Replay:
+    """A draft source that proposes a known continuation (`want`: the plain
+    greedy tokens after the prompt), with the tokens at `wrong` indices of
+    `want` replaced, so that their verify rows reject them."""
+
+    def __init__(self, prompt_len, want, wrong=(), vocab=512):
+        self.prompt_len, self.want, self.wrong, self.vocab = prompt_len, want, set(wrong), vocab
+        self.absorbed = 0
+
+    def absorb(self, tokens):
+        self.absorbed += len(tokens)
+
+    def draft(self, k):
+        known = self.absorbed - (self.prompt_len - 1)
+        out = []
+        for i in range(known, min(known + k, len(self.want))):
+            out.append((self.want[i] + 1) % self.vocab if i in self.wrong else self.want[i])
+        return out
+
+
+@pytest.mark.parametrize("bridge", BRIDGES)
+@pytest.mark.parametrize("depth", [1, 2, 3])
+def test_speculative_equals_greedy(tiny, bridge, depth):
+    """generate (reference src/device/speculative.rs:53-160): the output equals
+    plain greedy decoding whatever the drafts (all right, some wrong, the
+    prompt-lookup draft); a fully right draft has every offered token
+    accepted; an eos token stops it (emitted, then nothing more)."""
+    c, w = tiny
+    ids = tiny_prompt()
+    m = E.Model(w, bridge=bridge, kind=E.KIND_CPU_TEST)
+    plain = m.new_run(64)
+    want, _ = plain.decode_greedy(O.select_greedy(plain.prefill(ids)), 24)
+    for draft in (Replay(len(ids), want), Replay(len(ids), want, wrong=range(1, 24, 3)), "ngram"):
+        run = m.new_run(64, chunk=16, snapshots=depth)
+        got, st = run.speculative_generate(ids, 24, depth, draft=draft)
+        assert got == want
+        assert run.position == len(ids) + 23
+        if isinstance(draft, Replay) and not draft.wrong:
+            assert st["accepted"] == st["offered"] and st["passes"] <= -(-23 // (depth + 1)) + 1
+    stop = want[5]
+    run = m.new_run(64, chunk=16, snapshots=depth)
+    got, _ = run.speculative_generate(ids, 24, depth, draft=Replay(len(ids), want), eos=[stop])
+    assert got == want[:want.index(stop) + 1]
+    with pytest.raises(E.EngineError):
+        m.new_run(64, chunk=16, snapshots=depth - 1).speculative_generate(ids, 24, depth)

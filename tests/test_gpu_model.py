@@ -416,6 +416,28 @@ def test_qwen08b_verify_rows_equal_decode_steps(qwen08b, qwen08b_models, fmt):
         m.close()
 
 
+@pytest.mark.parametrize("depth", [1, 2, 3])
+def test_qwen08b_speculative_equals_greedy(qwen08b, qwen08b_models, depth):
+    """generate (reference src/device/speculative.rs:53-160) on the 0.8B model
+    with the one-launch decode: the output equals plain greedy decoding for
+    drafts that are all right, partly wrong, and the prompt-lookup draft."""
+    from test_engine_cpu import Replay
+    c, _ = qwen08b
+    fast, _ = qwen08b_models
+    prompt = [int(v) for v in np.random.default_rng(14).integers(0, c.vocab_size, 100)]
+    plain = fast.new_run(160, chunk=128)
+    want, _ = plain.decode_greedy(O.select_greedy(plain.prefill(prompt)), 40)
+    for draft in (Replay(len(prompt), want, vocab=c.vocab_size),
+                  Replay(len(prompt), want, wrong=range(2, 40, 5), vocab=c.vocab_size), "ngram"):
+        run = fast.new_run(160, chunk=128, snapshots=depth)
+        assert run.decode_plan
+        got, st = run.speculative_generate(prompt, 40, depth, draft=draft)
+        print(f"depth {depth}, draft {getattr(draft, 'wrong', draft)!s:.20}: {st}", flush=True)
+        assert got == want
+        if isinstance(draft, Replay) and not draft.wrong:
+            assert st["accepted"] == st["offered"]
+
+
 def test_qwen08b_chained_greedy_bounds(qwen08b_models):
     """Chained greedy decoding refuses to run past the run's capacity or from an
     out-of-range token (checked on the host, before any launch), and leaves the

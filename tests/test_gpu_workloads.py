@@ -176,14 +176,31 @@ def test_c3_prefill_2644_reference_chunks(weights, fast):
 
 def test_c3_prefill_10240_one_chunk_vs_chunks(weights, fast):
     """10,240 tokens (seed 2) in one chunk against 128-token chunks: last-row
-    logits and every state part, whole, within the fp32 bound."""
+    logits and every state part, whole. Both sides are GPU results, each
+    within the fp32 bound of the exact value (the one-chunk prefill is held
+    to it against the oracle at 2644 and 8192 tokens), so their difference is
+    held to twice the bound."""
     c, _ = weights
     ids = [int(v) for v in np.random.default_rng(2).integers(0, c.vocab_size, 10240)]
     a, b = fast.new_run(10240, chunk=10240), fast.new_run(10240, chunk=128)
     la, lb = a.prefill(ids), b.prefill(ids)
-    parity(la, lb, where="10240 logits")
+    worst = [parity(la, lb, rtol=2 * FP32_RTOL, where="10240 logits")]
     for layer, which in nonempty_parts(a, c):
-        parity(a.state(layer, which), b.state(layer, which), where=f"10240 state {layer}/{which}")
+        worst.append(parity(a.state(layer, which), b.state(layer, which), rtol=2 * FP32_RTOL,
+                            where=f"10240 state {layer}/{which}"))
+    print(f"10240 one chunk vs 128-token chunks: largest relative difference {max(worst):.3e}", flush=True)
+
+
+def test_c4_prefill_8192_one_chunk(weights, fast):
+    """The whole 8192-token prompt in one prefill chunk against the oracle:
+    last-row logits, pick and 1024 samples of every state part."""
+    c, _ = weights
+    rec = G.load("c4")
+    run = fast.new_run(8192, chunk=8192)
+    logits = run.prefill([int(v) for v in rec["prompt"]])
+    margin, bound = check_logits("c4", (8192,), logits, rec, "p8192_", FP32_RTOL, "c4 one chunk")
+    check_pick(int(np.argmax(logits)), int(rec["p8192_pick"]), margin, bound, "c4 one chunk")
+    check_state("c4", 8192, run, c, rec, "p8192_state", FP32_RTOL, "c4 one chunk")
 
 
 def test_c4_prefill_8192_checkpoints_and_greedy(weights, fast):
