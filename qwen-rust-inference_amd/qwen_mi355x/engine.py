@@ -365,6 +365,42 @@ class Run:
     def set_position(self, position: int):
         _check(lib().qe_state_set_position(self.ptr, position))
 
+    def inspect_state(self) -> dict:
+        """inspect_state (reference src/device.rs:2380-2424): every state part
+        at the current position, {(layer, which): values}."""
+        n = lib().qe_state_size(self.ptr, 0, 0)
+        if n < 0:
+            raise EngineError(lib().qe_last_error().decode())
+        out = {}
+        layer = 0
+        while lib().qe_state_size(self.ptr, layer, 0) >= 0:
+            for which in range(4):
+                out[(layer, which)] = self.state(layer, which)
+            layer += 1
+        return out
+
+    def load_state(self, position: int, read):
+        """load_state (reference src/device.rs:2493-2516): a complete host
+        state of `position` tokens (read(layer, which) returns each part as
+        state() lays it out: keys / values `position` rows) into this run."""
+        self.set_position(position)
+        layer = 0
+        while lib().qe_state_size(self.ptr, layer, 0) >= 0:
+            for which in range(4):
+                want = self.state_size(layer, which)
+                v = np.ascontiguousarray(read(layer, which), dtype=np.float32).reshape(-1)
+                if v.size != want:
+                    raise EngineError(f"state part {layer}/{which}: {v.size} values, the run holds {want}")
+                if want:
+                    self.write_state(layer, which, v)
+            layer += 1
+
+    def state_size(self, layer: int, which: int) -> int:
+        n = lib().qe_state_size(self.ptr, layer, which)
+        if n < 0:
+            raise EngineError(lib().qe_last_error().decode())
+        return int(n)
+
     def checkpoint(self) -> Checkpoint:
         p = lib().qe_checkpoint(self.ptr)
         if not p:

@@ -438,6 +438,76 @@ def test_qwen08b_speculative_equals_greedy(qwen08b, qwen08b_models, depth):
             assert st["accepted"] == st["offered"]
 
 
+def test_qwen08b_state_interchange_with_oracle(qwen08b, qwen08b_models):
+    """CPU <-> GPU state interchange (the reference's inspect_state /
+    load_state, src/device.rs:2380-2516): the oracle's state after a prompt,
+    loaded into a one-launch run, continues with the oracle's greedy tokens
+    and logits; a GPU run's state loaded into the oracle continues with the
+    GPU's logits."""
+    c, w = qwen08b
+    fast, _ = qwen08b_models
+    o = O.Oracle(w)
+    prompt = [int(v) for v in np.random.default_rng(15).integers(0, c.vocab_size, 20)]
+    want, want_logits, s = oracle_greedy(o, prompt, 5)
+    cpu_state = o.new_state()
+    for t in prompt:
+        cpu_state.step(t, O.VECTOR)
+    run = fast.new_run(64, chunk=32)
+    assert run.decode_plan
+    run.load_state(len(prompt), cpu_state.part)
+    assert run.position == len(prompt)
+    for i in range(4):
+        parity(run.step(want[i]), want_logits[i + 1], where=f"after load_state, step {i}")
+    for layer, which in [(0, 0), (0, 1), (3, 2), (3, 3), (23, 2)]:
+        parity(run.state(layer, which), s.part(layer, which), where=f"state {layer}/{which}")
+    g = fast.new_run(64, chunk=32)
+    g.load_state(len(prompt), cpu_state.part)
+    got, _ = g.decode_greedy(want[0], 5)
+    assert got == want
+    # GPU -> CPU
+    gpu = fast.new_run(64, chunk=32)
+    gpu.prefill(prompt + want[:4])
+    back = o.new_state()
+    back.load(gpu.position, lambda layer, which: gpu.state(layer, which))
+    for t in [11, 22222]:
+        parity(gpu.step(t), back.step(t, O.VECTOR), where="after loading the GPU state into the oracle")
+
+
+def test_qwen08b_checkpoint_restore_across_verify(qwen08b, qwen08b_models):
+    """checkpoint / restore (reference src/device.rs:2425-2490) around a
+    verify_rollback + accept on the one-launch path: restoring the earlier
+    checkpoint brings back its DeltaNet states bit for bit and the same
+    continuation; a checkpoint after accept restores the accepted state."""
+    c, _ = qwen08b
+    fast, _ = qwen08b_models
+    prompt = [int(v) for v in np.random.default_rng(16).integers(0, c.vocab_size, 40)]
+    run = fast.new_run(96, chunk=64, snapshots=3)
+    run.prefill(prompt)
+    before = run.inspect_state()
+    cp = run.checkpoint()
+    run.verify_rollback([7, 8, 9, 10])
+    run.accept(2)
+    after = run.inspect_state()
+    cp2 = run.checkpoint()
+    a = run.step(123)
+    run.restore(cp)
+    assert run.position == 40
+    now = run.inspect_state()
+    for key, v in before.items():
+        assert np.array_equal(now[key], v), key
+    ref = fast.new_run(96, chunk=64)
+    ref.prefill(prompt)
+    assert np.array_equal(run.step(7), ref.step(7))
+    # the accepted rows again (the same K/V rows at 40, 41), then back to cp2
+    run.step(8)
+    run.restore(cp2)
+    assert run.position == 42
+    now = run.inspect_state()
+    for key, v in after.items():
+        assert np.array_equal(now[key], v), key
+    assert np.array_equal(run.step(123), a)
+
+
 def test_qwen08b_chained_greedy_bounds(qwen08b_models):
     """Chained greedy decoding refuses to run past the run's capacity or from an
     out-of-range token (checked on the host, before any launch), and leaves the
