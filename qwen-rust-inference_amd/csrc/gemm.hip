@@ -1,11 +1,11 @@
 // Prefill projections Y[batch, rows] = X[batch, cols] . A^T (batch >= 5) on
 // gfx950, fp32 / BF16 / int8-per-row weights, fp32 accumulation.
 //
-// fp32 weights (the prefill of every config): FP32 MFMA
-// (v_mfma_f32_32x32x2_f32). A 128 (tokens) x 128 (rows) output tile per
-// 256-thread block, 2 x 2 waves of 64 x 64 (2 x 2 MFMA tiles each); K in
-// steps of 16 through LDS, k-major ([k][m], [k][n]) so each MFMA operand is
-// one conflict-free ds_read_b32 per lane; the next K step's global loads are
+// fp32 weights (the prefill of every config): BF16 MFMA
+// (v_mfma_f32_32x32x16_bf16) on operands split into three BF16 parts each,
+// which keeps fp32 accuracy (gemm_bf3_kernel below). A 128 (tokens) x 128
+// (rows) output tile per 256-thread block, 2 x 2 waves of 64 x 64 (2 x 2 MFMA
+// tiles each); K in steps of 32 through LDS; the next K step's global loads are
 // in flight (registers) while the current one is multiplied.
 // fp32 weights with at most 16 rows: gemm_skinny_kernel (lanes over columns).
 // Fewer 128 x 128 tiles than CUs: K split into chunks (partials + an ordered
@@ -22,38 +22,66 @@ namespace {
 typedef float f16v __attribute__((ext_vector_type(16)));
 typedef float f4v __attribute__((ext_vector_type(4)));
 
-// LDS rows of 132 floats: the two lane halves of an MFMA operand read take
-// rows k and k + 8 (8 * 132 = 32 banks apart), and the four k-quads a wave
-// stores land 16 banks apart, so neither side has bank conflicts.
-constexpr int MM = 128, MN = 128, MK = 16, MPAD = 4;
+constexpr int MM = 128, MN = 128;
 
-// One 16-deep K step of two 64-row blocks into registers: thread t loads row
-// t / 4 of each (v[0] from `top`, v[1] from `bottom`), 4 consecutive k at
-// (t % 4) * 4; zero outside the matrix or past k_end.
-__device__ __forceinline__ void mfma_load(const float* top, int top_r0, const float* bottom, int bottom_r0, int rows,
-                                          int cols, int k0, int k_end, f4v (&v)[2]) {
-    const int t = threadIdx.x, kq = (t & 3) * 4, k = k0 + kq;
+// ---- fp32 products on BF16 MFMA. Every fp32 operand is split into three
+// BF16 parts, x = x0 + x1 + x2 (x0 = bf16(x), x1 = bf16(x - x0), x2 =
+// bf16(x - x0 - x1); each residual is exact in fp32), and the six part
+// products x_p y_q with p + q <= 2 are summed in fp32. The dropped products
+// are below 2^-24 |x y| and every BF16 x BF16 product is exact, so a dot
+// product keeps fp32 accuracy, while v_mfma_f32_32x32x16_bf16 does 16x the
+// MACs per cycle of the fp32 MFMA (six of them per K step: 2.7x the rate).
+// Per 32-deep K step each thread loads 4 float4 of X and of W, splits them and
+// stores the three BF16 planes in LDS ([plane][row][k], rows of 40 BF16 = 80
+// bytes, so the 16-byte operand reads of 8 consecutive lanes hit distinct
+// banks). MFMA operands: lane l holds A[l % 32][8 (l / 32) + e] and
+// B[8 (l / 32) + e][l % 32], e = 0..7; accumulator register r of lane l is
+// D[8 (r / 4) + 4 (l / 32) + r % 4][l % 32].
+constexpr int B3K = 32, B3ROW = 40;
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+
+// One 32-deep K step of 128 rows (0-63 of `top` from top_r0, 64-127 of
+// `bottom` from bottom_r0) into registers: float4 q of thread t is row
+// (t + 256 q) / 8, k = 4 ((t + 256 q) % 8); zero outside the matrix or past k_end.
+__device__ __forceinline__ void b3_load(const float* top, int top_r0, const float* bottom, int bottom_r0, int rows,
+                                        int cols, int k0, int k_end, f4v (&v)[4]) {
+    const int t = threadIdx.x;
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const float* m = i ? bottom : top;
-        const int r = (i ? bottom_r0 : top_r0) + (t >> 2);
+    for (int q = 0; q < 4; ++q) {
+        const int f = t + 256 * q, rr = f >> 3, k = k0 + (f & 7) * 4;
+        const float* m = rr < 64 ? top : bottom;
+        const int r = (rr < 64 ? top_r0 : bottom_r0) + (rr & 63);
         if (r < rows && k + 3 < k_end) {
-            v[i] = *reinterpret_cast<const f4v*>(m + size_t(r) * cols + k);
+            v[q] = *reinterpret_cast<const f4v*>(m + size_t(r) * cols + k);
         } else {
             f4v z = {0.f, 0.f, 0.f, 0.f};
             for (int e = 0; e < 4; ++e)
                 if (r < rows && k + e < k_end) z[e] = m[size_t(r) * cols + k + e];
-            v[i] = z;
+            v[q] = z;
         }
     }
 }
-__device__ __forceinline__ void mfma_store(float (*lds)[MM + MPAD], const f4v (&v)[2]) {
-    const int t = threadIdx.x, kq = (t & 3) * 4;
+// The three BF16 planes of the loaded values into LDS.
+__device__ __forceinline__ void b3_store(__bf16 (*lds)[128][B3ROW], const f4v (&v)[4]) {
+    const int t = threadIdx.x;
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const int r = (t >> 2) + 64 * i;
+    for (int q = 0; q < 4; ++q) {
+        const int f = t + 256 * q, rr = f >> 3, kq = (f & 7) * 4;
+        bf16x4 p0, p1, p2;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) lds[kq + e][r] = v[i][e];
+        for (int e = 0; e < 4; ++e) {
+            const float x = v[q][e];
+            const __bf16 h0 = __bf16(x);
+            const float r1 = x - float(h0);
+            const __bf16 h1 = __bf16(r1);
+            p0[e] = h0;
+            p1[e] = h1;
+            p2[e] = __bf16(r1 - float(h1));
+        }
+        *reinterpret_cast<bf16x4*>(&lds[0][rr][kq]) = p0;
+        *reinterpret_cast<bf16x4*>(&lds[1][rr][kq]) = p1;
+        *reinterpret_cast<bf16x4*>(&lds[2][rr][kq]) = p2;
     }
 }
 
@@ -65,10 +93,10 @@ __device__ __forceinline__ void mfma_store(float (*lds)[MM + MPAD], const f4v (&
 // the same lane. blockIdx.z: the K split [z * kchunk, +kchunk); with more than
 // one split the block writes its partial sums to y + z * batch * rows.
 template <bool GLU>
-__global__ __launch_bounds__(256) void gemm_mfma_kernel(float* y, const float* a, const float* a2, const float* x,
-                                                        int rows, int cols, int batch, int kchunk) {
-    __shared__ float xs[2][MK][MM + MPAD];
-    __shared__ float ws[2][MK][MN + MPAD];
+__global__ __launch_bounds__(256) void gemm_bf3_kernel(float* y, const float* a, const float* a2, const float* x,
+                                                       int rows, int cols, int batch, int kchunk) {
+    __shared__ __bf16 xs[3][128][B3ROW];
+    __shared__ __bf16 ws[3][128][B3ROW];
     constexpr int NT = GLU ? 64 : MN;  // output rows per block
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int wm = (wave >> 1) * 64, wn = (wave & 1) * (GLU ? 32 : 64);
@@ -84,40 +112,48 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(float* y, const float* a
         for (int j = 0; j < 2; ++j)
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
-    f4v xv[2], wv[2];
-    mfma_load(x, m0, x, m0 + 64, batch, cols, kbeg, kend, xv);
-    mfma_load(a, n0, wbot, wbot_r0, rows, cols, kbeg, kend, wv);
-    mfma_store(xs[0], xv);
-    mfma_store(ws[0], wv);
+    f4v xv[4], wv[4];
+    b3_load(x, m0, x, m0 + 64, batch, cols, kbeg, kend, xv);
+    b3_load(a, n0, wbot, wbot_r0, rows, cols, kbeg, kend, wv);
+    b3_store(xs, xv);
+    b3_store(ws, wv);
     __syncthreads();
-    int buf = 0;
-    for (int k0 = kbeg; k0 < kend; k0 += MK) {
-        const bool more = k0 + MK < kend;
+    const int ar = lane & 31, ak = 8 * (lane >> 5);
+    for (int k0 = kbeg; k0 < kend; k0 += B3K) {
+        const bool more = k0 + B3K < kend;
         if (more) {  // next K step in flight while this one is multiplied
-            mfma_load(x, m0, x, m0 + 64, batch, cols, k0 + MK, kend, xv);
-            mfma_load(a, n0, wbot, wbot_r0, rows, cols, k0 + MK, kend, wv);
+            b3_load(x, m0, x, m0 + 64, batch, cols, k0 + B3K, kend, xv);
+            b3_load(a, n0, wbot, wbot_r0, rows, cols, k0 + B3K, kend, wv);
         }
 #pragma unroll
-        for (int kk = 0; kk < MK / 2; ++kk) {
-            const int k = kk + (MK / 2) * (lane >> 5);  // A[i = lane % 32][k], B[k][j = lane % 32]
-            float av[2], bv[2];
+        for (int ks = 0; ks < B3K / 16; ++ks) {
+            bf16x8 av[2][3], bv[2][3];
 #pragma unroll
-            for (int i = 0; i < 2; ++i) av[i] = xs[buf][k][wm + 32 * i + (lane & 31)];
+            for (int p = 0; p < 3; ++p) {
 #pragma unroll
-            for (int j = 0; j < 2; ++j) bv[j] = ws[buf][k][(GLU ? 64 * j + wn : wn + 32 * j) + (lane & 31)];
+                for (int i = 0; i < 2; ++i) av[i][p] = *reinterpret_cast<const bf16x8*>(&xs[p][wm + 32 * i + ar][16 * ks + ak]);
 #pragma unroll
-            for (int i = 0; i < 2; ++i)
+                for (int j = 0; j < 2; ++j)
+                    bv[j][p] = *reinterpret_cast<const bf16x8*>(&ws[p][(GLU ? 64 * j + wn : wn + 32 * j) + ar][16 * ks + ak]);
+            }
+            // the six part products, smallest first; the four tiles interleaved
 #pragma unroll
-                for (int j = 0; j < 2; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i], bv[j], acc[i][j], 0, 0, 0);
-        }
-        if (more) {
-            mfma_store(xs[buf ^ 1], xv);
-            mfma_store(ws[buf ^ 1], wv);
+            for (int pq = 0; pq < 6; ++pq) {
+                constexpr int P[6] = {2, 1, 0, 1, 0, 0}, Q[6] = {0, 1, 2, 0, 1, 0};
+#pragma unroll
+                for (int i = 0; i < 2; ++i)
+#pragma unroll
+                    for (int j = 0; j < 2; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av[i][P[pq]], bv[j][Q[pq]], acc[i][j], 0, 0, 0);
+            }
         }
         __syncthreads();
-        buf ^= 1;
+        if (more) {
+            b3_store(xs, xv);
+            b3_store(ws, wv);
+            __syncthreads();
+        }
     }
-    // D[i][j]: lane l, register r holds row 8 (r / 4) + 4 (l / 32) + r % 4, column l % 32
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
@@ -143,14 +179,14 @@ __global__ __launch_bounds__(256) void split_sum_kernel(float* y, const float* p
 }
 
 // K splits of an fp32 MFMA GEMM: fewer 128 x 128 tiles than CUs leave CUs
-// idle, so K is cut into up to 4 chunks (multiples of the 16-deep step) until
+// idle, so K is cut into up to 4 chunks (multiples of the 32-deep step) until
 // there are about two blocks per CU.
 int mfma_splits(int rows, int cols, int batch, int& kchunk) {
     const long tiles = long(ceil_div(rows, MN)) * long(ceil_div(batch, MM));
     int splits = 1;
     if (rows % 4 == 0)
-        while (splits < 4 && tiles * splits < 2 * 256 && cols / (splits + 1) >= 4 * MK) ++splits;
-    kchunk = int(ceil_div(ceil_div(cols, splits), MK)) * MK;
+        while (splits < 4 && tiles * splits < 2 * 256 && cols / (splits + 1) >= 2 * B3K) ++splits;
+    kchunk = int(ceil_div(ceil_div(cols, splits), B3K)) * B3K;
     return int(ceil_div(cols, kchunk));
 }
 
@@ -283,12 +319,12 @@ int gemm(hipStream_t s, WeightType t, float* y, const void* a, const float* x, i
             const int splits = mfma_splits(rows, cols, batch, kchunk);
             const dim3 g(ceil_div(rows, MN), ceil_div(batch, MM), unsigned(splits));
             if (splits == 1) {
-                hipLaunchKernelGGL(gemm_mfma_kernel<false>, g, dim3(256), 0, s, y, af, af, x, rows, cols, batch, kchunk);
+                hipLaunchKernelGGL(gemm_bf3_kernel<false>, g, dim3(256), 0, s, y, af, af, x, rows, cols, batch, kchunk);
                 break;
             }
             const size_t n = size_t(rows) * size_t(batch);
             if (!work || work_len < size_t(splits) * n) return int(hipErrorInvalidValue);
-            hipLaunchKernelGGL(gemm_mfma_kernel<false>, g, dim3(256), 0, s, work, af, af, x, rows, cols, batch, kchunk);
+            hipLaunchKernelGGL(gemm_bf3_kernel<false>, g, dim3(256), 0, s, work, af, af, x, rows, cols, batch, kchunk);
             if (hipError_t e = hipGetLastError()) return int(e);
             hipLaunchKernelGGL(split_sum_kernel, dim3(ceil_div(long(n / 4), 256)), dim3(256), 0, s, y,
                                static_cast<const float*>(work), splits, n / 4);
@@ -314,7 +350,7 @@ bool gemm_glu_fused(WeightType t, const void* gate, const void* up, const float*
 int gemm_glu(hipStream_t s, float* product, const float* gate, const float* up, const float* x, int rows, int cols,
              int batch) {
     const dim3 g(ceil_div(rows, 64), ceil_div(batch, MM), 1);
-    hipLaunchKernelGGL(gemm_mfma_kernel<true>, g, dim3(256), 0, s, product, gate, up, x, rows, cols, batch, cols);
+    hipLaunchKernelGGL(gemm_bf3_kernel<true>, g, dim3(256), 0, s, product, gate, up, x, rows, cols, batch, cols);
     return int(hipGetLastError());
 }
 
