@@ -159,6 +159,31 @@ int qe_speculative_generate(QeRun* r, const QeDraft* draft, const uint32_t* prom
 QeDraft* qe_draft_ngram_new(int64_t max_ngram);
 void qe_draft_ngram_free(QeDraft* d);
 
+/* One weight edit (the reference's Edit, src/edit.rs:9-17) on the FFN
+ * product of `layer` before its down projection: direction NULL scales
+ * product[j] by (1 - coefficient) for every listed column j (unit
+ * disabling); a direction d (hidden floats) removes the d component of the
+ * down columns w_j, adding -coefficient * d (d . w_j) / (d . d) * product[j]
+ * to the FFN output. tensor_name must be
+ * "model.language_model.layers.<layer>.mlp.down_proj.weight". */
+typedef struct QeEdit {
+    int32_t layer;
+    const char* tensor_name;
+    const int64_t* columns;
+    int64_t n_columns;
+    const float* direction;
+    float coefficient;
+} QeEdit;
+/* set_edit (src/device.rs:1401-1438): apply `edits` to every following
+ * forward of the run (n == 0 removes them; reset keeps them), validated as
+ * EditManifest::validate (src/edit.rs:19-58) without the model revision.
+ * `tensors` is the host tensor table the model was loaded from (slot order of
+ * include/qwen_model.h): the engine copies the down matrices of the edited
+ * layers, the fp32 columns the corrections use. Runs with an edit take the
+ * op sequence (the product is read back, edited on the host and written
+ * back; the capture records gain "ffn_intervened_product"). */
+int qe_run_set_edit(QeRun* r, const QeEdit* edits, int64_t n, const float* const* tensors);
+
 /* Row-wise symmetric int8 quantiser (src/device.rs:220-239) as the engine
  * uploads it. */
 void qe_quantize_int8_rows(const float* w, int64_t rows, int64_t cols, float* scales, int8_t* q);

@@ -58,6 +58,8 @@ def lib():
         L.qo_attend.argtypes = [_F, _F, _F, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, _F]
         L.qo_set_threads.argtypes = [ctypes.c_int]
         L.qo_state_load.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p]
+        L.qo_model_set_edit.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_void_p,
+                                        ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]
         _lib = L
     return _lib
 
@@ -100,6 +102,22 @@ class Oracle:
         """Project the vocabulary with `w` [vocab, hidden] instead of the embedding."""
         self._lm_head = np.ascontiguousarray(w, dtype=np.float32)
         lib().qo_model_set_lm_head(self.ptr, fp(self._lm_head))
+
+    def set_edit(self, edits):
+        """The edit manifest every following step applies (the reference's
+        EditManifest, src/edit.rs): a list of dicts with layer, columns,
+        direction (hidden floats or None) and coefficient; [] removes it."""
+        n = len(edits)
+        layers = np.array([e["layer"] for e in edits] or [0], np.int32)
+        offsets = np.cumsum([0] + [len(e["columns"]) for e in edits]).astype(np.int64)
+        columns = np.array([j for e in edits for j in e["columns"]] or [0], np.int64)
+        dirs = [None if e.get("direction") is None else np.ascontiguousarray(e["direction"], dtype=np.float32)
+                for e in edits]
+        self._edit_dirs = dirs
+        table = (ctypes.c_void_p * max(n, 1))(*[d.ctypes.data if d is not None else None for d in dirs])
+        coef = np.array([e["coefficient"] for e in edits] or [0], np.float32)
+        check(lib().qo_model_set_edit(self.ptr, n, layers.ctypes.data, offsets.ctypes.data, columns.ctypes.data,
+                                      table, coef.ctypes.data))
 
     def new_state(self) -> "State":
         return State(self, lib().qo_state_create(self.ptr))

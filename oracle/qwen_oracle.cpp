@@ -346,6 +346,13 @@ struct qo_model {
         const float *conv, *dt, *a_log, *dnorm;
     };
     std::vector<Layer> layers;
+    struct Edit {
+        size_t layer;
+        std::vector<size_t> columns;
+        std::vector<float> direction;  // empty: disable the units
+        float coefficient;
+    };
+    std::vector<Edit> edits;  // the EditManifest applied by every step (src/edit.rs)
     size_t channels() const { return size_t(2 * c.key_heads * c.key_dim + c.value_heads * c.value_dim); }
 };
 
@@ -563,6 +570,31 @@ std::vector<float> delta_step(const qo_model& m, const qo_model::Layer& w, const
     return output;
 }
 
+// EditManifest::apply (src/edit.rs:59-110): direction-less edits scale their
+// product units by (1 - coefficient); then each direction edit adds
+// -coefficient * d * (d . w_j) / (d . d) * product[j] for its columns j
+// (w_j = column j of down), every sum a left fold.
+std::vector<float> apply_edits(const qo_model& m, size_t layer, std::vector<float>& product, const Matrix& down) {
+    require(product.size() == down.cols, "edit product shape mismatch");
+    std::vector<float> correction(down.rows, 0.f);
+    for (const auto& e : m.edits)
+        if (e.layer == layer && e.direction.empty())
+            for (size_t j : e.columns) product[j] *= 1.f - e.coefficient;
+    for (const auto& e : m.edits) {
+        if (e.layer != layer || e.direction.empty()) continue;
+        float denominator = kSumStart;
+        for (float v : e.direction) denominator += v * v;
+        for (size_t j : e.columns) {
+            float dot = kSumStart;
+            for (size_t r = 0; r < down.rows; ++r) dot += e.direction[r] * down.d[r * down.cols + j];
+            const float projection = dot / denominator;
+            for (size_t r = 0; r < down.rows; ++r) correction[r] -= e.coefficient * e.direction[r] * projection * product[j];
+        }
+    }
+    finite(correction);
+    return correction;
+}
+
 // src/model.rs:53-99 (step_hidden) with src/block.rs:55-101 and src/ffn.rs:41-75.
 void model_step(const qo_model& m, qo_state& st, uint32_t id, int backend, float* logits_out, float* norm_out,
                 const Tracer& tr) {
@@ -584,13 +616,15 @@ void model_step(const qo_model& m, qo_state& st, uint32_t id, int backend, float
                                        : delta_step(m, w, input_norm, st.layers[l], backend, L, tr);
         auto after_mixer = add(x, mixed);
         auto post_norm = rms_norm(after_mixer.data(), H, w.post_norm, c.rms_norm_eps, true);
-        // FFN (src/ffn.rs:41-75); no edit manifest: the correction is zeros.
+        // FFN (src/ffn.rs:41-75) with the edit manifest (src/edit.rs:59-110)
         auto gate = project(w.gate, post_norm, backend);
         auto up = project(w.up, post_norm, backend);
         auto activated = silu(gate);
         auto product = multiply(activated, up);
-        auto down = project(w.down, product, backend);
-        auto ffn = add(down, std::vector<float>(H, 0.f));
+        auto intervened = product;
+        auto correction = apply_edits(m, l, intervened, w.down);
+        auto down = project(w.down, intervened, backend);
+        auto ffn = add(down, correction);
         auto output = add(after_mixer, ffn);
         tr(L, "mixer", mixed);
         tr(L, "after_mixer", after_mixer);
@@ -599,7 +633,7 @@ void model_step(const qo_model& m, qo_state& st, uint32_t id, int backend, float
         tr(L, "ffn.up", up);
         tr(L, "ffn.silu", activated);
         tr(L, "ffn.product", product);
-        tr(L, "ffn.intervened_product", product);
+        tr(L, "ffn.intervened_product", intervened);
         tr(L, "ffn.output", ffn);
         tr(L, "layer", output);
         x = std::move(output);
@@ -861,6 +895,30 @@ int qo_delta_rule(const float* q, const float* k, const float* v, int64_t kd, in
     return guarded([&] {
         auto y = delta_rule(q, k, v, size_t(kd), size_t(vd), g, beta, state);
         std::memcpy(out, y.data(), y.size() * 4);
+    });
+}
+// The edit manifest every following step applies (Model::step's edit,
+// src/model.rs:53-99): n edits; edit k has layer layers[k], columns
+// columns[offsets[k] .. offsets[k + 1]), direction directions[k] (hidden
+// floats, or NULL) and coefficients[k]. n = 0 removes it.
+int qo_model_set_edit(qo_model* m, int64_t n, const int32_t* layers, const int64_t* offsets, const int64_t* columns,
+                      const float* const* directions, const float* coefficients) {
+    return guarded([&] {
+        std::vector<qo_model::Edit> out;
+        for (int64_t k = 0; k < n; ++k) {
+            require(layers[k] >= 0 && size_t(layers[k]) < m->layers.size(), "edit target mismatch");
+            qo_model::Edit e;
+            e.layer = size_t(layers[k]);
+            for (int64_t j = offsets[k]; j < offsets[k + 1]; ++j) {
+                require(columns[j] >= 0 && columns[j] < m->c.intermediate_size, "invalid edit target");
+                e.columns.push_back(size_t(columns[j]));
+            }
+            if (directions && directions[k])
+                e.direction.assign(directions[k], directions[k] + m->c.hidden_size);
+            e.coefficient = coefficients[k];
+            out.push_back(std::move(e));
+        }
+        m->edits = std::move(out);
     });
 }
 // attend (src/attention.rs:63-71): query [heads * d]; keys / values [positions][kv_heads * d].

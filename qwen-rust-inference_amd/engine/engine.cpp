@@ -487,6 +487,18 @@ struct QeRun {
     // The bridge's one-launch decode step over this run's buffers (fp32
     // matrices only), used by forward for uncaptured one-token steps.
     QrDecodePlan* plan = nullptr;
+    // The weight-edit overlay (set_edit, src/device.rs:1401-1438): the
+    // validated edits and host fp32 copies of the down matrices of the edited
+    // layers ([hidden, intermediate] row-major); applied by forward_body.
+    struct EditEntry {
+        size_t layer;
+        std::vector<size_t> columns;
+        std::vector<float> direction;  // empty: disable the units
+        float coefficient;
+    };
+    std::vector<EditEntry> edits;
+    std::vector<std::vector<float>> edit_down;  // per layer; empty when not edited
+    bool edited(size_t layer) const { return layer < edit_down.size() && !edit_down[layer].empty(); }
 
     const Api* api() const { return model->api.get(); }
     ~QeRun() { drop_plan(); }
@@ -594,6 +606,33 @@ struct QeRun {
         QrDecodePlan* p = nullptr;
         if (a->decode_plan(a->ctx, &desc, &p) == 0) plan = p;
     }
+    // EditManifest::apply (src/edit.rs:59-110) on one row of the FFN product:
+    // units of the direction-less edits scaled by (1 - coefficient), then the
+    // correction -coefficient * d (d . w_j) / (d . d) * product[j] summed over
+    // the direction edits' columns j (w_j: column j of down).
+    std::vector<float> apply_edit(size_t layer, float* product) const {
+        const size_t h = size_t(model->config.hidden_size), i_size = size_t(model->config.intermediate_size);
+        const std::vector<float>& down = edit_down[layer];
+        for (const EditEntry& e : edits)
+            if (e.layer == layer && e.direction.empty())
+                for (size_t j : e.columns) product[j] *= 1.f - e.coefficient;
+        std::vector<float> correction(h, 0.f);
+        for (const EditEntry& e : edits) {
+            if (e.layer != layer || e.direction.empty()) continue;
+            const std::vector<float>& d = e.direction;
+            float denominator = -0.f;
+            for (float v : d) denominator += v * v;
+            for (size_t j : e.columns) {
+                float dot = -0.f;
+                for (size_t r = 0; r < h; ++r) dot += d[r] * down[r * i_size + j];
+                const float projection = dot / denominator;
+                for (size_t r = 0; r < h; ++r) correction[r] -= e.coefficient * d[r] * projection * product[j];
+            }
+        }
+        for (float v : correction) require(std::isfinite(v), "NaN/Inf detected");
+        return correction;
+    }
+
     // One uncaptured token through the plan (the work of forward_body for
     // t == 1, logit_rows == 1): logits and [argmax, non-finite count] land in
     // the run's logits / picks buffers.
@@ -864,12 +903,12 @@ struct QeRun {
         require(t > 0 && t <= chunk && (!rec || t == 1) && (logit_rows <= 1 || logit_rows == t),
                 "device forward chunk/capture");
         const Api* a = api();
-        if (plan && t == 1 && !rec && logit_rows == 1 && snapshot_rows == 0 && pick_slot == 0) {
+        if (plan && edits.empty() && t == 1 && !rec && logit_rows == 1 && snapshot_rows == 0 && pick_slot == 0) {
             auto out = forward_planned(ids[0]);
             logits_unread = greedy_rows;
             return out;
         }
-        if (plan && a->decode_step_row && t > 1 && !rec && logit_rows == t && pick_slot == 0 &&
+        if (plan && edits.empty() && a->decode_step_row && t > 1 && !rec && logit_rows == t && pick_slot == 0 &&
             t <= std::min(kVerifyRows, chunk)) {
             auto out = forward_planned_rows(ids, t);
             logits_unread = false;
@@ -1010,16 +1049,34 @@ struct QeRun {
                 a->op(SiluProduct, i_size * t, {product.p, gate.p, up.p}, {}, {});
             }
             record(layer, "ffn_product", product, i_size);
+            // Edit overlay (src/device.rs:2198-2250): the product read back,
+            // EditManifest::apply row by row, written back; after the down
+            // projection the direction-removal correction is added.
+            std::vector<float> correction;
+            if (edited(layer)) {
+                auto rows = product.read(t * i_size);
+                for (size_t r = 0; r < t; ++r) {
+                    auto c = apply_edit(layer, rows.data() + r * i_size);
+                    correction.insert(correction.end(), c.begin(), c.end());
+                }
+                product.write(rows.data(), rows.size());
+                record(layer, "ffn_intervened_product", product, i_size);
+            }
             const bool last = layer + 1 == model->blocks.size();
             const DeviceBlock* next = (!last && fused_add_norm) ? &model->blocks[layer + 1] : nullptr;
             const Buffer& weight = last ? model->norm : model->blocks[layer + 1].input;
             const float eps = last ? cfg.rms_norm_eps : model->blocks[layer + 1].eps;
             bool down_normed;
-            if (next || last)
+            if ((next || last) && correction.empty())
                 down_normed = project_norm(b.down, product, ffn, x, residual, ffn, weight, eps);
             else {
                 b.down.project(product, ffn, t);
                 down_normed = false;
+            }
+            if (!correction.empty()) {
+                // `mixed` is free after the residual add above: the correction's staging
+                mixed.write(correction.data(), correction.size());
+                a->op(Add, h * t, {ffn.p, ffn.p, mixed.p}, {}, {});
             }
             record(layer, "ffn", ffn, h);
             normed = next != nullptr;
@@ -1527,13 +1584,65 @@ void qe_draft_ngram_free(QeDraft* d) {
     if (d) delete static_cast<NgramDraft*>(d->user);
 }
 
+// set_edit (src/device.rs:1401-1438) with EditManifest::validate
+// (src/edit.rs:19-58), without the model revision (the engine loads tensors,
+// not a checkpoint with a revision).
+int qe_run_set_edit(QeRun* r, const QeEdit* edits, int64_t n, const float* const* tensors) {
+    return guarded([&] {
+        const QwConfig& c = r->model->config;
+        if (n <= 0 || !edits) {
+            r->edits.clear();
+            r->edit_down.clear();
+            return;
+        }
+        const size_t h = size_t(c.hidden_size), i_size = size_t(c.intermediate_size);
+        std::vector<QeRun::EditEntry> out;
+        std::vector<std::vector<float>> down(size_t(c.num_layers));
+        for (int64_t k = 0; k < n; ++k) {
+            const QeEdit& e = edits[k];
+            require(e.layer >= 0 && e.layer < c.num_layers && e.tensor_name &&
+                        std::string(e.tensor_name) ==
+                            "model.language_model.layers." + std::to_string(e.layer) + ".mlp.down_proj.weight",
+                    "edit target mismatch");
+            require(e.n_columns > 0 && e.columns && std::isfinite(e.coefficient), "invalid edit columns/coefficient");
+            std::vector<size_t> cols;
+            for (int64_t j = 0; j < e.n_columns; ++j) {
+                require(e.columns[j] >= 0 && size_t(e.columns[j]) < i_size, "invalid edit columns/coefficient");
+                cols.push_back(size_t(e.columns[j]));
+            }
+            std::vector<size_t> unique = cols;
+            std::sort(unique.begin(), unique.end());
+            require(std::adjacent_find(unique.begin(), unique.end()) == unique.end(), "duplicate edit column");
+            std::vector<float> dir;
+            if (e.direction) {
+                dir.assign(e.direction, e.direction + h);
+                float norm = -0.f;
+                for (float v : dir) {
+                    require(std::isfinite(v), "NaN/Inf detected");
+                    norm += v * v;
+                }
+                require(std::isfinite(norm) && norm > 0.f, "invalid direction norm");
+            }
+            out.push_back(QeRun::EditEntry{size_t(e.layer), cols, dir, e.coefficient});
+            if (down[size_t(e.layer)].empty()) {
+                const float* w = tensors ? tensors[QW_SLOTS_BASE + e.layer * QW_SLOTS_LAYER + QW_DOWN] : nullptr;
+                require(w != nullptr, "edit needs the down matrix of every edited layer");
+                down[size_t(e.layer)].assign(w, w + h * i_size);
+            }
+        }
+        r->edits = std::move(out);
+        r->edit_down = std::move(down);
+    });
+}
+
 int qe_decode_greedy(QeRun* r, uint32_t first, int64_t n_new, uint32_t* ids, double* seconds) {
     return guarded([&] {
         double total = 0;
         uint32_t token = first;
         // the planned steps of step_greedy (forward's one-launch conditions),
         // queued back to back with one read-back
-        if (n_new > 1 && r->plan && r->api()->decode_steps && r->snapshot_rows == 0 && r->pick_slot == 0) {
+        if (n_new > 1 && r->plan && r->edits.empty() && r->api()->decode_steps && r->snapshot_rows == 0 &&
+            r->pick_slot == 0) {
             const Api* a = r->api();
             require(!r->failed, "device run failed; reset required");
             require(first < uint32_t(r->model->config.vocab_size) && r->position + size_t(n_new - 1) <= r->capacity,

@@ -51,6 +51,12 @@ class QeDraft(ctypes.Structure):
     _fields_ = [("user", ctypes.c_void_p), ("absorb", ABSORB_FN), ("draft", DRAFT_FN)]
 
 
+class QeEdit(ctypes.Structure):
+    _fields_ = [("layer", ctypes.c_int32), ("tensor_name", ctypes.c_char_p), ("columns", ctypes.POINTER(ctypes.c_int64)),
+                ("n_columns", ctypes.c_int64), ("direction", ctypes.POINTER(ctypes.c_float)),
+                ("coefficient", ctypes.c_float)]
+
+
 class SpecStats(ctypes.Structure):
     """SpeculativeStats (reference src/device/speculative.rs:30-46)."""
     _fields_ = [("passes", ctypes.c_int64), ("offered", ctypes.c_int64 * 8), ("accepted", ctypes.c_int64 * 8),
@@ -153,6 +159,7 @@ def lib():
         L.qe_speculative_generate.argtypes = [ctypes.c_void_p, ctypes.POINTER(QeDraft), _U32, ctypes.c_int64,
                                               ctypes.c_int64, ctypes.c_int64, _U32, ctypes.c_int64, _U32,
                                               ctypes.POINTER(ctypes.c_int64), ctypes.POINTER(SpecStats)]
+        L.qe_run_set_edit.argtypes = [ctypes.c_void_p, ctypes.POINTER(QeEdit), ctypes.c_int64, ctypes.c_void_p]
         L.qe_draft_ngram_new.restype = ctypes.POINTER(QeDraft)
         L.qe_draft_ngram_new.argtypes = [ctypes.c_int64]
         L.qe_draft_ngram_free.argtypes = [ctypes.POINTER(QeDraft)]
@@ -412,6 +419,24 @@ class Run:
 
     def restore(self, c: Checkpoint):
         _check(lib().qe_restore(self.ptr, c.ptr))
+
+    def set_edit(self, edits, weights=None):
+        """set_edit (reference src/device.rs:1401-1438): a list of dicts with
+        layer, columns, direction (hidden floats or None), coefficient and
+        optionally tensor_name; [] removes the edit. `weights`: the tensor set
+        the model was loaded from (default: the model's own)."""
+        weights = weights or self.model.weights
+        arr = (QeEdit * max(len(edits), 1))()
+        keep = []
+        for i, e in enumerate(edits):
+            cols = np.ascontiguousarray(e["columns"], dtype=np.int64)
+            name = e.get("tensor_name", f"model.language_model.layers.{e['layer']}.mlp.down_proj.weight").encode()
+            d = None if e.get("direction") is None else np.ascontiguousarray(e["direction"], dtype=np.float32)
+            keep += [cols, name, d]
+            arr[i] = QeEdit(e["layer"], name, cols.ctypes.data_as(ctypes.POINTER(ctypes.c_int64)), cols.size,
+                            None if d is None else d.ctypes.data_as(ctypes.POINTER(ctypes.c_float)), e["coefficient"])
+        _check(lib().qe_run_set_edit(self.ptr, arr, len(edits), ctypes.cast(weights.table, ctypes.c_void_p)))
+        self._edit_keep = keep
 
     def speculative_generate(self, prompt, max_new: int, depth: int, draft="ngram", eos=()):
         """generate (reference src/device/speculative.rs:53-160) on this fresh

@@ -274,3 +274,62 @@ def test_speculative_equals_greedy(tiny, bridge, depth):
     assert got == want[:want.index(stop) + 1]
     with pytest.raises(E.EngineError):
         m.new_run(64, chunk=16, snapshots=depth - 1).speculative_generate(ids, 24, depth)
+
+
+def fixture_edits(hidden):
+    """The reference's device edit test manifest (src/device/tests.rs:212-243):
+    unit 3 of layer 1 disabled, and the direction d = e_0 - 0.5 e_{hidden-1}
+    removed from columns 0 and 5 of layer 2's down matrix with coefficient 0.7."""
+    d = np.zeros(hidden, np.float32)
+    d[0], d[hidden - 1] = 1.0, -0.5
+    return [dict(layer=1, columns=[3], direction=None, coefficient=1.0),
+            dict(layer=2, columns=[0, 5], direction=d, coefficient=0.7)]
+
+
+@pytest.mark.parametrize("bridge", BRIDGES)
+@pytest.mark.parametrize("fmt", [E.F32, E.BF16_EXACT])
+def test_edit_overlay_matches_oracle(fixture, bridge, fmt):
+    """cpu_bridge_edit_overlay_matches_cpu (reference src/device/tests.rs:208-300):
+    the engine's edit overlay equals the CPU model's edited run bit for bit
+    (captured intervened product, FFN output, logits) in decode, in chunked
+    prefill, after reset, and removing it restores the plain run; invalid
+    manifests are refused."""
+    c, w = M.fixture_config_and_weights(fixture)
+    ids = fixture["ids"]
+    edits = fixture_edits(c.hidden_size)
+    plain_o, edited_o = O.Oracle(w), O.Oracle(w)
+    edited_o.set_edit(edits)
+    ps, es = plain_o.new_state(), edited_o.new_state()
+    plain, edited = [], []
+    for tok in ids:
+        plain.append(ps.step(tok, O.REFERENCE))
+        edited.append(es.step(tok, O.REFERENCE, trace=True))
+    assert np.max(np.abs(plain[-1] - edited[-1][0])) > 1e-3, "the edit must matter"
+    m = E.Model(w, bridge=bridge, kind=E.KIND_CPU_TEST, fmt=fmt)
+    run = m.new_run(len(ids))
+    run.set_edit(edits)
+    for p, tok in enumerate(ids):
+        logits, rec = run.step(tok, capture=True)
+        want, orec = edited[p]
+        omap = {(l, n): v for (l, n, v) in orec}
+        got = {(l, n): v for (l, n, v) in rec}
+        for layer in (1, 2):
+            assert np.array_equal(got[(layer, "ffn_intervened_product")], omap[(layer, "ffn.intervened_product")])
+            assert np.array_equal(got[(layer, "ffn")], omap[(layer, "ffn.output")])
+        assert (0, "ffn_intervened_product") not in got
+        assert np.array_equal(logits, want)
+    run = m.new_run(len(ids), chunk=3)
+    run.set_edit(edits)
+    assert np.array_equal(run.prefill(ids), edited[-1][0])
+    run.reset()
+    assert np.array_equal(run.prefill(ids), edited[-1][0])
+    run.reset()
+    run.set_edit([])
+    assert np.array_equal(run.prefill(ids), plain[-1])
+    bad = [dict(edits[0], tensor_name="model.language_model.layers.0.mlp.down_proj.weight")]
+    with pytest.raises(E.EngineError, match="target"):
+        run.set_edit(bad)
+    with pytest.raises(E.EngineError, match="duplicate"):
+        run.set_edit([dict(edits[0], columns=[3, 3])])
+    with pytest.raises(E.EngineError, match="direction"):
+        run.set_edit([dict(edits[1], direction=np.zeros(c.hidden_size, np.float32))])

@@ -508,6 +508,71 @@ def test_qwen08b_checkpoint_restore_across_verify(qwen08b, qwen08b_models):
     assert np.array_equal(run.step(123), a)
 
 
+def test_edit_overlay_against_oracle(fixture):
+    """The edit overlay (reference src/device.rs:2198-2250) on the HIP bridge:
+    the fixture model with the reference test's manifest against the oracle's
+    edited run (intervened product, FFN output, logits), in decode and chunked
+    prefill; removing it restores the plain run."""
+    from test_engine_cpu import fixture_edits
+    c, w = M.fixture_config_and_weights(fixture)
+    ids = fixture["ids"]
+    edits = fixture_edits(c.hidden_size)
+    o = O.Oracle(w)
+    o.set_edit(edits)
+    s = o.new_state()
+    m = E.Model(w)
+    run = m.new_run(len(ids))
+    run.set_edit(edits)
+    want = None
+    for tok in ids:
+        logits, rec = run.step(tok, capture=True)
+        want, orec = s.step(tok, O.REFERENCE, trace=True)
+        omap = {(l, n): v for (l, n, v) in orec}
+        got = {(l, n): v for (l, n, v) in rec}
+        for layer in (1, 2):
+            parity(got[(layer, "ffn_intervened_product")], omap[(layer, "ffn.intervened_product")], where="product")
+            parity(got[(layer, "ffn")], omap[(layer, "ffn.output")], where="ffn")
+        parity(logits, want, where="edited logits")
+    run = m.new_run(len(ids), chunk=3)
+    run.set_edit(edits)
+    parity(run.prefill(ids), want, where="edited prefill")
+    run.reset()
+    run.set_edit([])
+    plain = O.Oracle(w).new_state()
+    for tok in ids:
+        last = plain.step(tok, O.REFERENCE)
+    parity(run.prefill(ids), last, where="edit removed")
+
+
+def test_qwen08b_edit_takes_the_op_sequence(qwen08b, qwen08b_models):
+    """With an edit the 0.8B run leaves the one-launch decode (the overlay
+    needs the product on the host) and matches the oracle's edited run."""
+    c, w = qwen08b
+    fast, _ = qwen08b_models
+    d = np.zeros(c.hidden_size, np.float32)
+    d[:8] = 1.0
+    edits = [dict(layer=4, columns=[7, 1000], direction=None, coefficient=1.0),
+             dict(layer=21, columns=[3, 3000], direction=d, coefficient=0.5)]
+    o = O.Oracle(w)
+    o.set_edit(edits)
+    s = o.new_state()
+    run = fast.new_run(16, chunk=8)
+    run.set_edit(edits)
+    for i, t in enumerate([5, 77, 12345, 200000]):
+        parity(run.step(t), s.step(t, O.VECTOR), where=f"0.8B edited step {i}")
+    # greedy decoding with the edit stays on the op sequence too
+    want = [O.select_greedy(s.step(9, O.VECTOR))]
+    for _ in range(2):
+        want.append(O.select_greedy(s.step(want[-1], O.VECTOR)))
+    got, _ = run.decode_greedy(9, 4)
+    assert got[1:] == want
+    run.set_edit([])
+    s2 = O.Oracle(w).new_state()
+    r2 = fast.new_run(16, chunk=8)
+    for t in [5, 77]:
+        parity(r2.step(t), s2.step(t, O.VECTOR), where="0.8B after removal")
+
+
 def test_qwen08b_chained_greedy_bounds(qwen08b_models):
     """Chained greedy decoding refuses to run past the run's capacity or from an
     out-of-range token (checked on the host, before any launch), and leaves the

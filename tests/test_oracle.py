@@ -311,3 +311,33 @@ def test_state_load_round_trip(fixture_model):
         assert np.array_equal(t.step(tok, O.REFERENCE), s.step(tok, O.REFERENCE))
     with pytest.raises(RuntimeError):
         t.load(3, lambda layer, which: np.zeros(0, np.float32))
+
+
+def test_edit_overlay_closed_form(fixture):
+    """EditManifest::apply (reference src/edit.rs:59-110) against what it
+    stands for: disabling unit j with coefficient 1 is the model whose down
+    column j is zero; removing direction d from columns J with coefficient a
+    is the model whose down columns w_j (j in J) are w_j - a d (d.w_j)/(d.d)
+    (reference comment src/edit.rs:88-91). The edited oracle matches both
+    weight-edited oracles, on every prompt position."""
+    c, w = M.fixture_config_and_weights(fixture)
+    H, I = c.hidden_size, c.intermediate_size
+    d = np.zeros(H, np.float32)
+    d[0], d[H - 1] = 1.0, -0.5
+    edits = [dict(layer=1, columns=[3], direction=None, coefficient=1.0),
+             dict(layer=2, columns=[0, 5], direction=d, coefficient=0.7)]
+    o = O.Oracle(w)
+    o.set_edit(edits)
+    t = dict(w.tensors)
+    down1 = t[M.QW_SLOTS_BASE + 1 * M.QW_SLOTS_LAYER + M.DOWN].reshape(H, I).copy()
+    down1[:, 3] = 0
+    down2 = t[M.QW_SLOTS_BASE + 2 * M.QW_SLOTS_LAYER + M.DOWN].reshape(H, I).astype(np.float64)
+    dd = d.astype(np.float64)
+    for j in (0, 5):
+        down2[:, j] -= 0.7 * dd * (dd @ down2[:, j]) / (dd @ dd)
+    t[M.QW_SLOTS_BASE + 1 * M.QW_SLOTS_LAYER + M.DOWN] = np.ascontiguousarray(down1.reshape(-1))
+    t[M.QW_SLOTS_BASE + 2 * M.QW_SLOTS_LAYER + M.DOWN] = np.ascontiguousarray(down2.astype(np.float32).reshape(-1))
+    ref = O.Oracle(M.Weights(c, t))
+    a, b = o.new_state(), ref.new_state()
+    for tok in fixture["ids"]:
+        close(a.step(tok, O.REFERENCE), b.step(tok, O.REFERENCE), 1e-6, 1e-5)
