@@ -184,6 +184,31 @@ typedef struct QeEdit {
  * back; the capture records gain "ffn_intervened_product"). */
 int qe_run_set_edit(QeRun* r, const QeEdit* edits, int64_t n, const float* const* tensors);
 
+/* Checkpoint reader (the reference's read_checkpoint_kept and decode_tensor,
+ * src/weights.rs:168-186, 364-466): one streaming pass over a safetensors
+ * file, every byte through SHA-256; header checks (contiguous offsets, sizes =
+ * shape x dtype size, data ending at the end of the file); F32 decoded, BF16
+ * kept as bits, NaN/Inf refused; tensors named in `ignored` hashed and skipped
+ * (any dtype). NULL (message in qe_safetensors_error) on any failure, or when
+ * expected_sha256 (64 lowercase hex digits) is given and the file does not
+ * hash to it. */
+typedef struct QeSafetensors QeSafetensors;
+enum { QE_ST_F32 = 0, QE_ST_BF16 = 1 };
+QeSafetensors* qe_safetensors_read(const char* path, const char* expected_sha256, const char* const* ignored,
+                                   int64_t n_ignored);
+const char* qe_safetensors_error(void);
+void qe_safetensors_free(QeSafetensors* s);
+/* The file's SHA-256 (hex). */
+const char* qe_safetensors_sha256(const QeSafetensors* s);
+/* Tensors in data order: name, dtype (QE_ST_*, -1 for another dtype of an
+ * ignored tensor), kept flag, rank and shape (up to 8 dims). */
+int64_t qe_safetensors_count(const QeSafetensors* s);
+int qe_safetensors_info(const QeSafetensors* s, int64_t i, const char** name, int* dtype, int* kept, int* ndim,
+                        int64_t* shape);
+/* A kept tensor as n fp32 values (BF16 widened exactly), or a BF16 tensor's bits. */
+int qe_safetensors_f32(const QeSafetensors* s, const char* name, float* out, int64_t n);
+int qe_safetensors_bf16(const QeSafetensors* s, const char* name, uint16_t* out, int64_t n);
+
 /* Row-wise symmetric int8 quantiser (src/device.rs:220-239) as the engine
  * uploads it. */
 void qe_quantize_int8_rows(const float* w, int64_t rows, int64_t cols, float* scales, int8_t* q);
