@@ -40,9 +40,9 @@ for p in (str(ROOT / "qwen-rust-inference_amd"), str(ROOT / "oracle")):
         sys.path.insert(0, p)
 
 HBM_PEAK_GBS = 8000.0
-# HBM bytes per decode_kernel launch at ctx ~590 from the rocprofv3 FETCH_SIZE / WRITE_SIZE passes
-# (calibrated on a 512 MiB copy; profiles/decode_kernel_config2.md).
-DECODE_TRAFFIC_BYTES = 3_158_000_000
+# HBM bytes per decode_kernel launch at ctx ~490 from the rocprofv3 FETCH_SIZE / WRITE_SIZE passes
+# (FETCH_SIZE x 2.0, WRITE_SIZE x 1.0, calibrated on a 512 MiB copy; profiles/decode_kernel_config2.md).
+DECODE_TRAFFIC_BYTES = 3_159_121_254
 PREFILL_CHUNK = 128  # the reference engine's prefill chunk (src/device.rs)
 
 
@@ -186,9 +186,10 @@ def main():
             t = time.perf_counter()
             r2.prefill(ids2)
             times.append(time.perf_counter() - t)
-            del r2
+            r2.close()
         print(json.dumps({"mode": "only-prefill", "tokens": n, "prefill_ms": [round(x * 1e3, 2) for x in times]}),
               flush=True)
+        model.close()
         return
     prompt = [int(v) for v in np.random.default_rng(4).integers(0, c.vocab_size, args.prompt)]
 
