@@ -196,8 +196,7 @@ int glu(Context* c, qr::WeightType t, float* product, float* gate_y, float* up_y
     }
     if (qr::gemm_glu_fused(t, gate, up, x, rows, cols, batch)) {  // gate_y / up_y untouched, as the reference's fused GLU
         auto s = scope(c, [&] { return std::string("gemm_") + wname(t) + "_glu 2x" + shape(rows, cols, batch); });
-        return launched(c, "gemm_glu", qr::gemm_glu(c->stream, product, static_cast<const float*>(gate),
-                                                    static_cast<const float*>(up), x, rows, cols, batch));
+        return launched(c, "gemm_glu", qr::gemm_glu(c->stream, t, product, gate, up, x, rows, cols, batch));
     }
     if (int s = project(c, t, gate_y, gate, x, rows, cols, batch)) return s;
     if (int s = project(c, t, up_y, up, x, rows, cols, batch)) return s;

@@ -84,10 +84,10 @@ int gemm(hipStream_t s, WeightType t, float* y, const void* a, const float* x, i
          float* work, size_t work_len);
 size_t gemm_scratch(WeightType t, int rows, int cols, int batch);
 bool gemm_preferred(WeightType t, int rows, int cols, int batch);
-// product[batch, rows] = silu(X G^T) * (X U^T) in one kernel (prefill, fp32 weights).
+// product[batch, rows] = silu(X G^T) * (X U^T) in one kernel (prefill, any weight format).
 bool gemm_glu_fused(WeightType t, const void* gate, const void* up, const float* x, int rows, int cols, int batch);
-int gemm_glu(hipStream_t s, float* product, const float* gate, const float* up, const float* x, int rows, int cols,
-             int batch);
+int gemm_glu(hipStream_t s, WeightType t, float* product, const void* gate, const void* up, const float* x, int rows,
+             int cols, int batch);
 
 // ops.hip --------------------------------------------------------------------
 int run_elementwise(hipStream_t s, int op, int count, const Params& a);

@@ -42,27 +42,52 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 
 // One 32-deep K step of 128 rows (0-63 of `top` from top_r0, 64-127 of
-// `bottom` from bottom_r0) into registers: float4 q of thread t is row
-// (t + 256 q) / 8, k = 4 ((t + 256 q) % 8); zero outside the matrix or past k_end.
-__device__ __forceinline__ void b3_load(const float* top, int top_r0, const float* bottom, int bottom_r0, int rows,
+// `bottom` from bottom_r0) into registers: quad q of thread t is row
+// (t + 256 q) / 8, k = 4 ((t + 256 q) % 8), as fp32 (BF16 widened and int8
+// converted exactly); zero outside the matrix or past k_end. T is the
+// weight format of the matrix (X is always fp32); an int8 matrix's values
+// follow its `rows` fp32 scales.
+template <WeightType T>
+__device__ __forceinline__ float b3_elem(const void* m, int rows, int cols, int r, int k) {
+    const size_t e = size_t(r) * cols + k;
+    if constexpr (T == WeightType::F32) return static_cast<const float*>(m)[e];
+    if constexpr (T == WeightType::BF16) return __uint_as_float(uint32_t(static_cast<const uint16_t*>(m)[e]) << 16);
+    return float(reinterpret_cast<const int8_t*>(static_cast<const float*>(m) + rows)[e]);
+}
+template <WeightType T>
+__device__ __forceinline__ void b3_load(const void* top, int top_r0, const void* bottom, int bottom_r0, int rows,
                                         int cols, int k0, int k_end, f4v (&v)[4]) {
     const int t = threadIdx.x;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
         const int f = t + 256 * q, rr = f >> 3, k = k0 + (f & 7) * 4;
-        const float* m = rr < 64 ? top : bottom;
+        const void* m = rr < 64 ? top : bottom;
         const int r = (rr < 64 ? top_r0 : bottom_r0) + (rr & 63);
         if (r < rows && k + 3 < k_end) {
-            v[q] = *reinterpret_cast<const f4v*>(m + size_t(r) * cols + k);
+            const size_t e = size_t(r) * cols + k;
+            if constexpr (T == WeightType::F32) {
+                v[q] = *reinterpret_cast<const f4v*>(static_cast<const float*>(m) + e);
+            } else if constexpr (T == WeightType::BF16) {
+                const uint2 w = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(m) + e);
+                v[q] = f4v{__uint_as_float(w.x << 16), __uint_as_float(w.x & 0xffff0000u), __uint_as_float(w.y << 16),
+                           __uint_as_float(w.y & 0xffff0000u)};
+            } else {
+                const unsigned w = *reinterpret_cast<const unsigned*>(
+                    reinterpret_cast<const int8_t*>(static_cast<const float*>(m) + rows) + e);
+                v[q] = f4v{float(int(w << 24) >> 24), float(int(w << 16) >> 24), float(int(w << 8) >> 24),
+                           float(int(w) >> 24)};
+            }
         } else {
             f4v z = {0.f, 0.f, 0.f, 0.f};
             for (int e = 0; e < 4; ++e)
-                if (r < rows && k + e < k_end) z[e] = m[size_t(r) * cols + k + e];
+                if (r < rows && k + e < k_end) z[e] = b3_elem<T>(m, rows, cols, r, k + e);
             v[q] = z;
         }
     }
 }
-// The three BF16 planes of the loaded values into LDS.
+// The BF16 planes of the loaded values into LDS: three (x0, x1, x2) or, for
+// values exact in BF16 (BF16 and int8 weights), the one.
+template <int PLANES>
 __device__ __forceinline__ void b3_store(__bf16 (*lds)[128][B3ROW], const f4v (&v)[4]) {
     const int t = threadIdx.x;
 #pragma unroll
@@ -73,15 +98,19 @@ __device__ __forceinline__ void b3_store(__bf16 (*lds)[128][B3ROW], const f4v (&
         for (int e = 0; e < 4; ++e) {
             const float x = v[q][e];
             const __bf16 h0 = __bf16(x);
-            const float r1 = x - float(h0);
-            const __bf16 h1 = __bf16(r1);
             p0[e] = h0;
-            p1[e] = h1;
-            p2[e] = __bf16(r1 - float(h1));
+            if constexpr (PLANES == 3) {
+                const float r1 = x - float(h0);
+                const __bf16 h1 = __bf16(r1);
+                p1[e] = h1;
+                p2[e] = __bf16(r1 - float(h1));
+            }
         }
         *reinterpret_cast<bf16x4*>(&lds[0][rr][kq]) = p0;
-        *reinterpret_cast<bf16x4*>(&lds[1][rr][kq]) = p1;
-        *reinterpret_cast<bf16x4*>(&lds[2][rr][kq]) = p2;
+        if constexpr (PLANES == 3) {
+            *reinterpret_cast<bf16x4*>(&lds[1][rr][kq]) = p1;
+            *reinterpret_cast<bf16x4*>(&lds[2][rr][kq]) = p2;
+        }
     }
 }
 
@@ -92,18 +121,22 @@ __device__ __forceinline__ void b3_store(__bf16 (*lds)[128][B3ROW], const f4v (&
 // up (j = 1), so a gate value and its up partner sit in the same register of
 // the same lane. blockIdx.z: the K split [z * kchunk, +kchunk); with more than
 // one split the block writes its partial sums to y + z * batch * rows.
-template <bool GLU>
-__global__ __launch_bounds__(256) void gemm_bf3_kernel(float* y, const float* a, const float* a2, const float* x,
+// T: fp32 weights take all six part products; BF16 and int8 weights are exact
+// in BF16 (one plane), so x0 w, x1 w and x2 w; int8 sums are scaled after the
+// sum (scale * sum(q x), the reference's qr_gemm_i8).
+template <WeightType T, bool GLU>
+__global__ __launch_bounds__(256) void gemm_bf3_kernel(float* y, const void* a, const void* a2, const float* x,
                                                        int rows, int cols, int batch, int kchunk) {
+    constexpr int WP = T == WeightType::F32 ? 3 : 1;
     __shared__ __bf16 xs[3][128][B3ROW];
-    __shared__ __bf16 ws[3][128][B3ROW];
+    __shared__ __bf16 ws[WP][128][B3ROW];
     constexpr int NT = GLU ? 64 : MN;  // output rows per block
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int wm = (wave >> 1) * 64, wn = (wave & 1) * (GLU ? 32 : 64);
     const int m0 = blockIdx.y * MM, n0 = blockIdx.x * NT;
     const int kbeg = int(blockIdx.z) * kchunk, kend = min(cols, kbeg + kchunk);
     float* out = y + size_t(blockIdx.z) * size_t(batch) * size_t(rows);
-    const float* wbot = GLU ? a2 : a;
+    const void* wbot = GLU ? a2 : a;
     const int wbot_r0 = GLU ? n0 : n0 + 64;
     f16v acc[2][2];
 #pragma unroll
@@ -113,44 +146,48 @@ __global__ __launch_bounds__(256) void gemm_bf3_kernel(float* y, const float* a,
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
     f4v xv[4], wv[4];
-    b3_load(x, m0, x, m0 + 64, batch, cols, kbeg, kend, xv);
-    b3_load(a, n0, wbot, wbot_r0, rows, cols, kbeg, kend, wv);
-    b3_store(xs, xv);
-    b3_store(ws, wv);
+    b3_load<WeightType::F32>(x, m0, x, m0 + 64, batch, cols, kbeg, kend, xv);
+    b3_load<T>(a, n0, wbot, wbot_r0, rows, cols, kbeg, kend, wv);
+    b3_store<3>(xs, xv);
+    b3_store<WP>(ws, wv);
     __syncthreads();
     const int ar = lane & 31, ak = 8 * (lane >> 5);
     for (int k0 = kbeg; k0 < kend; k0 += B3K) {
         const bool more = k0 + B3K < kend;
         if (more) {  // next K step in flight while this one is multiplied
-            b3_load(x, m0, x, m0 + 64, batch, cols, k0 + B3K, kend, xv);
-            b3_load(a, n0, wbot, wbot_r0, rows, cols, k0 + B3K, kend, wv);
+            b3_load<WeightType::F32>(x, m0, x, m0 + 64, batch, cols, k0 + B3K, kend, xv);
+            b3_load<T>(a, n0, wbot, wbot_r0, rows, cols, k0 + B3K, kend, wv);
         }
 #pragma unroll
         for (int ks = 0; ks < B3K / 16; ++ks) {
-            bf16x8 av[2][3], bv[2][3];
+            bf16x8 av[2][3], bv[2][WP];
 #pragma unroll
-            for (int p = 0; p < 3; ++p) {
+            for (int p = 0; p < 3; ++p)
 #pragma unroll
                 for (int i = 0; i < 2; ++i) av[i][p] = *reinterpret_cast<const bf16x8*>(&xs[p][wm + 32 * i + ar][16 * ks + ak]);
 #pragma unroll
+            for (int p = 0; p < WP; ++p)
+#pragma unroll
                 for (int j = 0; j < 2; ++j)
                     bv[j][p] = *reinterpret_cast<const bf16x8*>(&ws[p][(GLU ? 64 * j + wn : wn + 32 * j) + ar][16 * ks + ak]);
-            }
-            // the six part products, smallest first; the four tiles interleaved
+            // the part products, smallest first; the four tiles interleaved
+            constexpr int NPQ = WP == 3 ? 6 : 3;
 #pragma unroll
-            for (int pq = 0; pq < 6; ++pq) {
+            for (int pq = 0; pq < NPQ; ++pq) {
                 constexpr int P[6] = {2, 1, 0, 1, 0, 0}, Q[6] = {0, 1, 2, 0, 1, 0};
+                constexpr int P1[3] = {2, 1, 0};
+                const int pa = WP == 3 ? P[pq] : P1[pq], pb = WP == 3 ? Q[pq] : 0;
 #pragma unroll
                 for (int i = 0; i < 2; ++i)
 #pragma unroll
                     for (int j = 0; j < 2; ++j)
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av[i][P[pq]], bv[j][Q[pq]], acc[i][j], 0, 0, 0);
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av[i][pa], bv[j][pb], acc[i][j], 0, 0, 0);
             }
         }
         __syncthreads();
         if (more) {
-            b3_store(xs, xv);
-            b3_store(ws, wv);
+            b3_store<3>(xs, xv);
+            b3_store<WP>(ws, wv);
             __syncthreads();
         }
     }
@@ -160,10 +197,22 @@ __global__ __launch_bounds__(256) void gemm_bf3_kernel(float* y, const float* a,
         for (int j = 0; j < (GLU ? 1 : 2); ++j) {
             const int n = n0 + wn + 32 * j + (lane & 31);
             if (n >= rows) continue;
+            float sg = 1.f, su = 1.f;  // int8 row scales (gate / up, or the row's)
+            if constexpr (T == WeightType::I8) {
+                sg = static_cast<const float*>(a)[n];
+                su = GLU ? static_cast<const float*>(a2)[n] : sg;
+            }
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int m = m0 + wm + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                if (m < batch) out[size_t(m) * rows + n] = GLU ? siluf_(acc[i][0][r]) * acc[i][1][r] : acc[i][j][r];
+                if (m >= batch) continue;
+                if constexpr (GLU) {
+                    const float g = T == WeightType::I8 ? sg * acc[i][0][r] : acc[i][0][r];
+                    const float u = T == WeightType::I8 ? su * acc[i][1][r] : acc[i][1][r];
+                    out[size_t(m) * rows + n] = siluf_(g) * u;
+                } else {
+                    out[size_t(m) * rows + n] = T == WeightType::I8 ? sg * acc[i][j][r] : acc[i][j][r];
+                }
             }
         }
 }
@@ -291,45 +340,58 @@ __global__ __launch_bounds__(256) void gemm_skinny_kernel(float* y, const float*
 
 bool gemm_preferred(WeightType, int, int, int batch) { return batch > 4; }
 
-static bool mfma_ok(const void* a, const float* x, int cols) {
-    return cols % 4 == 0 && (reinterpret_cast<uintptr_t>(a) | reinterpret_cast<uintptr_t>(x)) % 16 == 0;
+// The split-BF16 kernel loads 4 consecutive k of a row at once (16 bytes of
+// X or fp32 weights, 8 of BF16, 4 of int8).
+static bool mfma_ok(WeightType t, const void* a, const float* x, int cols) {
+    return cols % 4 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0 &&
+           reinterpret_cast<uintptr_t>(a) % (t == WeightType::F32 ? 16 : t == WeightType::BF16 ? 8 : 4) == 0;
 }
 
 size_t gemm_scratch(WeightType t, int rows, int cols, int batch) {
-    if (t != WeightType::F32 || rows <= SK_ROWS) return 0;
+    if (t == WeightType::F32 && rows <= SK_ROWS) return 0;
     int kchunk;
     const int splits = mfma_splits(rows, cols, batch, kchunk);
     return splits > 1 ? size_t(splits) * size_t(rows) * size_t(batch) : 0;
 }
 
+// The split-BF16 MFMA kernel over every weight format (with the K split), or
+// -1 when the shape does not fit it.
+template <WeightType T>
+int gemm_bf3(hipStream_t s, float* y, const void* a, const float* x, int rows, int cols, int batch, float* work,
+             size_t work_len) {
+    int kchunk;
+    const int splits = mfma_splits(rows, cols, batch, kchunk);
+    const dim3 g(ceil_div(rows, MN), ceil_div(batch, MM), unsigned(splits));
+    if (splits == 1) {
+        hipLaunchKernelGGL((gemm_bf3_kernel<T, false>), g, dim3(256), 0, s, y, a, a, x, rows, cols, batch, kchunk);
+        return int(hipGetLastError());
+    }
+    const size_t n = size_t(rows) * size_t(batch);
+    if (!work || work_len < size_t(splits) * n) return int(hipErrorInvalidValue);
+    hipLaunchKernelGGL((gemm_bf3_kernel<T, false>), g, dim3(256), 0, s, work, a, a, x, rows, cols, batch, kchunk);
+    if (hipError_t e = hipGetLastError()) return int(e);
+    hipLaunchKernelGGL(split_sum_kernel, dim3(ceil_div(long(n / 4), 256)), dim3(256), 0, s, y,
+                       static_cast<const float*>(work), splits, n / 4);
+    return int(hipGetLastError());
+}
+
 int gemm(hipStream_t s, WeightType t, float* y, const void* a, const float* x, int rows, int cols, int batch,
          float* work, size_t work_len) {
     dim3 grid(ceil_div(rows, BN), ceil_div(batch, BM));
+    if (mfma_ok(t, a, x, cols)) {
+        if (t == WeightType::F32 && rows <= SK_ROWS) {
+            hipLaunchKernelGGL(gemm_skinny_kernel, dim3(ceil_div(batch, 4 * SK_TOK)), dim3(256), 0, s, y,
+                               static_cast<const float*>(a), x, rows, cols, batch);
+            return int(hipGetLastError());
+        }
+        switch (t) {
+        case WeightType::F32: return gemm_bf3<WeightType::F32>(s, y, a, x, rows, cols, batch, work, work_len);
+        case WeightType::BF16: return gemm_bf3<WeightType::BF16>(s, y, a, x, rows, cols, batch, work, work_len);
+        case WeightType::I8: return gemm_bf3<WeightType::I8>(s, y, a, x, rows, cols, batch, work, work_len);
+        }
+    }
     switch (t) {
     case WeightType::F32:
-        // 16-byte aligned rows for the vector loads
-        if (mfma_ok(a, x, cols)) {
-            const float* af = static_cast<const float*>(a);
-            if (rows <= SK_ROWS) {
-                hipLaunchKernelGGL(gemm_skinny_kernel, dim3(ceil_div(batch, 4 * SK_TOK)), dim3(256), 0, s, y, af, x,
-                                   rows, cols, batch);
-                break;
-            }
-            int kchunk;
-            const int splits = mfma_splits(rows, cols, batch, kchunk);
-            const dim3 g(ceil_div(rows, MN), ceil_div(batch, MM), unsigned(splits));
-            if (splits == 1) {
-                hipLaunchKernelGGL(gemm_bf3_kernel<false>, g, dim3(256), 0, s, y, af, af, x, rows, cols, batch, kchunk);
-                break;
-            }
-            const size_t n = size_t(rows) * size_t(batch);
-            if (!work || work_len < size_t(splits) * n) return int(hipErrorInvalidValue);
-            hipLaunchKernelGGL(gemm_bf3_kernel<false>, g, dim3(256), 0, s, work, af, af, x, rows, cols, batch, kchunk);
-            if (hipError_t e = hipGetLastError()) return int(e);
-            hipLaunchKernelGGL(split_sum_kernel, dim3(ceil_div(long(n / 4), 256)), dim3(256), 0, s, y,
-                               static_cast<const float*>(work), splits, n / 4);
-            break;
-        }
         hipLaunchKernelGGL(gemm_tiled_kernel<WeightType::F32>, grid, dim3(256), 0, s, y, a, x, rows, cols, batch);
         break;
     case WeightType::BF16:
@@ -343,14 +405,26 @@ int gemm(hipStream_t s, WeightType t, float* y, const void* a, const float* x, i
 }
 
 bool gemm_glu_fused(WeightType t, const void* gate, const void* up, const float* x, int rows, int cols, int batch) {
-    return t == WeightType::F32 && gemm_preferred(t, rows, cols, batch) && mfma_ok(gate, x, cols) &&
-           mfma_ok(up, x, cols);
+    return gemm_preferred(t, rows, cols, batch) && mfma_ok(t, gate, x, cols) && mfma_ok(t, up, x, cols);
 }
 
-int gemm_glu(hipStream_t s, float* product, const float* gate, const float* up, const float* x, int rows, int cols,
-             int batch) {
+int gemm_glu(hipStream_t s, WeightType t, float* product, const void* gate, const void* up, const float* x, int rows,
+             int cols, int batch) {
     const dim3 g(ceil_div(rows, 64), ceil_div(batch, MM), 1);
-    hipLaunchKernelGGL(gemm_bf3_kernel<true>, g, dim3(256), 0, s, product, gate, up, x, rows, cols, batch, cols);
+    switch (t) {
+    case WeightType::F32:
+        hipLaunchKernelGGL((gemm_bf3_kernel<WeightType::F32, true>), g, dim3(256), 0, s, product, gate, up, x, rows,
+                           cols, batch, cols);
+        break;
+    case WeightType::BF16:
+        hipLaunchKernelGGL((gemm_bf3_kernel<WeightType::BF16, true>), g, dim3(256), 0, s, product, gate, up, x, rows,
+                           cols, batch, cols);
+        break;
+    case WeightType::I8:
+        hipLaunchKernelGGL((gemm_bf3_kernel<WeightType::I8, true>), g, dim3(256), 0, s, product, gate, up, x, rows,
+                           cols, batch, cols);
+        break;
+    }
     return int(hipGetLastError());
 }
 
