@@ -11,9 +11,11 @@
 // Fewer 128 x 128 tiles than CUs: K split into chunks (partials + an ordered
 // sum). The prefill GLU: gate and up in one MFMA kernel with silu(g) * u in
 // the epilogue.
-// BF16 / int8 weights: the LDS-tiled FMA kernel below (64 x 64 tile, 4 x 4
-// outputs per thread). int8 rows are scaled after the sum (scale * sum(q x),
-// as the reference's qr_gemm_i8, native/rocm/bridge.cpp:620-653).
+// BF16 / int8 weights (exact in BF16): the same kernel with one weight plane
+// and three part products; int8 rows are scaled after the sum (scale *
+// sum(q x), as the reference's qr_gemm_i8, native/rocm/bridge.cpp:620-653).
+// Shapes the MFMA kernel does not take (cols % 4 != 0, unaligned operands):
+// the LDS-tiled FMA kernel (64 x 64 tile, 4 x 4 outputs per thread).
 #include "common.h"
 
 namespace qr {
@@ -42,65 +44,67 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 
 // One 32-deep K step of 128 rows (0-63 of `top` from top_r0, 64-127 of
-// `bottom` from bottom_r0) into registers: quad q of thread t is row
-// (t + 256 q) / 8, k = 4 ((t + 256 q) % 8), as fp32 (BF16 widened and int8
-// converted exactly); zero outside the matrix or past k_end. T is the
-// weight format of the matrix (X is always fp32); an int8 matrix's values
-// follow its `rows` fp32 scales.
-template <WeightType T>
-__device__ __forceinline__ float b3_elem(const void* m, int rows, int cols, int r, int k) {
-    const size_t e = size_t(r) * cols + k;
-    if constexpr (T == WeightType::F32) return static_cast<const float*>(m)[e];
-    if constexpr (T == WeightType::BF16) return __uint_as_float(uint32_t(static_cast<const uint16_t*>(m)[e]) << 16);
-    return float(reinterpret_cast<const int8_t*>(static_cast<const float*>(m) + rows)[e]);
-}
+// `bottom` from bottom_r0) into registers, as the raw words of the format:
+// quad q of thread t is row (t + 256 q) / 8, k = 4 ((t + 256 q) % 8) (16 bytes
+// of fp32, 8 of BF16 in .x/.y, 4 of int8 in .x; an int8 matrix's values follow
+// its `rows` fp32 scales). k and k_end are multiples of 4 (cols % 4 == 0 and
+// K chunks of whole 32-deep steps), so a quad is wholly inside or wholly
+// outside [0, k_end). A quad outside the matrix is loaded from row 0, k 0 and
+// its bit in `ok` cleared; b3_store writes it as zeros. Every quad is one
+// unconditional load into its own registers and nothing reads them before
+// b3_store, so the next step's loads stay in flight during the MFMAs.
 template <WeightType T>
 __device__ __forceinline__ void b3_load(const void* top, int top_r0, const void* bottom, int bottom_r0, int rows,
-                                        int cols, int k0, int k_end, f4v (&v)[4]) {
+                                        int cols, int k0, int k_end, uint4 (&v)[4], unsigned& ok) {
     const int t = threadIdx.x;
+    ok = 0;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
         const int f = t + 256 * q, rr = f >> 3, k = k0 + (f & 7) * 4;
         const void* m = rr < 64 ? top : bottom;
         const int r = (rr < 64 ? top_r0 : bottom_r0) + (rr & 63);
-        if (r < rows && k + 3 < k_end) {
-            const size_t e = size_t(r) * cols + k;
-            if constexpr (T == WeightType::F32) {
-                v[q] = *reinterpret_cast<const f4v*>(static_cast<const float*>(m) + e);
-            } else if constexpr (T == WeightType::BF16) {
-                const uint2 w = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(m) + e);
-                v[q] = f4v{__uint_as_float(w.x << 16), __uint_as_float(w.x & 0xffff0000u), __uint_as_float(w.y << 16),
-                           __uint_as_float(w.y & 0xffff0000u)};
-            } else {
-                const unsigned w = *reinterpret_cast<const unsigned*>(
-                    reinterpret_cast<const int8_t*>(static_cast<const float*>(m) + rows) + e);
-                v[q] = f4v{float(int(w << 24) >> 24), float(int(w << 16) >> 24), float(int(w << 8) >> 24),
-                           float(int(w) >> 24)};
-            }
+        const bool in = r < rows && k < k_end;
+        ok |= unsigned(in) << q;
+        const size_t e = in ? size_t(r) * cols + k : 0;
+        if constexpr (T == WeightType::F32) {
+            v[q] = *reinterpret_cast<const uint4*>(static_cast<const float*>(m) + e);
+        } else if constexpr (T == WeightType::BF16) {
+            const uint2 w = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(m) + e);
+            v[q].x = w.x;
+            v[q].y = w.y;
         } else {
-            f4v z = {0.f, 0.f, 0.f, 0.f};
-            for (int e = 0; e < 4; ++e)
-                if (r < rows && k + e < k_end) z[e] = b3_elem<T>(m, rows, cols, r, k + e);
-            v[q] = z;
+            v[q].x = *reinterpret_cast<const unsigned*>(reinterpret_cast<const int8_t*>(static_cast<const float*>(m) + rows) + e);
         }
     }
 }
-// The BF16 planes of the loaded values into LDS: three (x0, x1, x2) or, for
-// values exact in BF16 (BF16 and int8 weights), the one.
-template <int PLANES>
-__device__ __forceinline__ void b3_store(__bf16 (*lds)[128][B3ROW], const f4v (&v)[4]) {
+// The loaded quads as fp32 (BF16 widened and int8 converted exactly; zeros
+// where `ok` is clear), split into BF16 planes in LDS: three (x0, x1, x2) for
+// fp32 or, for values exact in BF16 (BF16 and int8 weights), the one.
+template <WeightType T>
+__device__ __forceinline__ void b3_store(__bf16 (*lds)[128][B3ROW], const uint4 (&v)[4], unsigned ok) {
+    constexpr int PLANES = T == WeightType::F32 ? 3 : 1;
     const int t = threadIdx.x;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
         const int f = t + 256 * q, rr = f >> 3, kq = (f & 7) * 4;
+        f4v x;
+        if constexpr (T == WeightType::F32) {
+            x = f4v{__uint_as_float(v[q].x), __uint_as_float(v[q].y), __uint_as_float(v[q].z), __uint_as_float(v[q].w)};
+        } else if constexpr (T == WeightType::BF16) {
+            x = f4v{__uint_as_float(v[q].x << 16), __uint_as_float(v[q].x & 0xffff0000u), __uint_as_float(v[q].y << 16),
+                    __uint_as_float(v[q].y & 0xffff0000u)};
+        } else {
+            const unsigned w = v[q].x;
+            x = f4v{float(int(w << 24) >> 24), float(int(w << 16) >> 24), float(int(w << 8) >> 24), float(int(w) >> 24)};
+        }
+        if (!((ok >> q) & 1u)) x = f4v{0.f, 0.f, 0.f, 0.f};
         bf16x4 p0, p1, p2;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-            const float x = v[q][e];
-            const __bf16 h0 = __bf16(x);
+            const __bf16 h0 = __bf16(x[e]);
             p0[e] = h0;
             if constexpr (PLANES == 3) {
-                const float r1 = x - float(h0);
+                const float r1 = x[e] - float(h0);
                 const __bf16 h1 = __bf16(r1);
                 p1[e] = h1;
                 p2[e] = __bf16(r1 - float(h1));
@@ -145,18 +149,19 @@ __global__ __launch_bounds__(256) void gemm_bf3_kernel(float* y, const void* a, 
         for (int j = 0; j < 2; ++j)
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
-    f4v xv[4], wv[4];
-    b3_load<WeightType::F32>(x, m0, x, m0 + 64, batch, cols, kbeg, kend, xv);
-    b3_load<T>(a, n0, wbot, wbot_r0, rows, cols, kbeg, kend, wv);
-    b3_store<3>(xs, xv);
-    b3_store<WP>(ws, wv);
+    uint4 xv[4], wv[4];
+    unsigned xok, wok;
+    b3_load<WeightType::F32>(x, m0, x, m0 + 64, batch, cols, kbeg, kend, xv, xok);
+    b3_load<T>(a, n0, wbot, wbot_r0, rows, cols, kbeg, kend, wv, wok);
+    b3_store<WeightType::F32>(xs, xv, xok);
+    b3_store<T>(ws, wv, wok);
     __syncthreads();
     const int ar = lane & 31, ak = 8 * (lane >> 5);
     for (int k0 = kbeg; k0 < kend; k0 += B3K) {
         const bool more = k0 + B3K < kend;
         if (more) {  // next K step in flight while this one is multiplied
-            b3_load<WeightType::F32>(x, m0, x, m0 + 64, batch, cols, k0 + B3K, kend, xv);
-            b3_load<T>(a, n0, wbot, wbot_r0, rows, cols, k0 + B3K, kend, wv);
+            b3_load<WeightType::F32>(x, m0, x, m0 + 64, batch, cols, k0 + B3K, kend, xv, xok);
+            b3_load<T>(a, n0, wbot, wbot_r0, rows, cols, k0 + B3K, kend, wv, wok);
         }
 #pragma unroll
         for (int ks = 0; ks < B3K / 16; ++ks) {
@@ -186,8 +191,8 @@ __global__ __launch_bounds__(256) void gemm_bf3_kernel(float* y, const void* a, 
         }
         __syncthreads();
         if (more) {
-            b3_store<3>(xs, xv);
-            b3_store<WP>(ws, wv);
+            b3_store<WeightType::F32>(xs, xv, xok);
+            b3_store<T>(ws, wv, wok);
             __syncthreads();
         }
     }
