@@ -214,10 +214,17 @@ __device__ __forceinline__ f4v mfma16(float x, float y, f4v acc) {
 // read), then O += L D over the tokens up to its rows and S rows of tiles w
 // and w + 4 (phase 2: one D read feeds all three products). The next chunk's
 // phase-1 operands are loaded while phase 2 runs.
+// Blocks are dealt to the 8 XCDs round-robin by index; the index is remapped
+// so that the 8 slices of a head run on one XCD: every slice reads the whole
+// chunk record, and this way 7 of the 8 reads hit that XCD's L2 instead of
+// the memory-side cache or HBM.
+constexpr int kXcds = 8;
 __global__ __launch_bounds__(256) void rule_chunk_scan_kernel(Params a, int c0, int chunks, const float* scratch) {
     __shared__ float sl[kD][kSlice];
     __shared__ float dl[kC][kSlice];
-    const int h = int(blockIdx.x) / kSlices, js = int(blockIdx.x) % kSlices;
+    const int nb = int(gridDim.x), b = int(blockIdx.x);
+    const int i = nb % kXcds == 0 ? (b % kXcds) * (nb / kXcds) + b / kXcds : b;
+    const int h = i / kSlices, js = i % kSlices;
     const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, lc = l & 15, q = l >> 4;
     const int vh = a.n[3], tokens = a.n[4] > 0 ? a.n[4] : 1;
     float* state = a.p[4] + size_t(h) * kD * kD + js * kSlice;

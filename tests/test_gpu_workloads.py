@@ -78,7 +78,18 @@ def check_pick(got, want, margin, bound, where):
     return False
 
 
-def check_state(name, point, run, c, rec, key, rtol, where):
+# The DeltaNet recurrent state (part 1) after thousands of tokens: the rule's
+# residual d = beta (v - S^T k) cancels, which amplifies fp32 ordering noise
+# there. Measured on the 8192-token prompt of C4: two correct fp32 GPU
+# evaluations (one prefill chunk against 128-token chunks) differ by up to
+# 1.15e-4 in the recurrent state of layers 17-21, while every conv, key and
+# value part agrees to 4.1e-5 and the logits to 3.4e-5; each of the two is
+# within 1.2e-4 of the oracle there. Past 4096 tokens the recurrent state is
+# held to twice the fp32 bound, every other part and the logits to the bound.
+LONG_RECURRENT_RTOL = 2 * FP32_RTOL
+
+
+def check_state(name, point, run, c, rec, key, rtol, where, recurrent_rtol=None):
     parts = nonempty_parts(run, c)
     flat = rec[key]
     k = flat.size // len(parts)
@@ -86,7 +97,8 @@ def check_state(name, point, run, c, rec, key, rtol, where):
     for n, (layer, which) in enumerate(parts):
         v = run.state(layer, which)
         got = v[G.sample(name, (point, layer, which, k), v.size, k)]
-        parity(got, flat[n * k:(n + 1) * k], rtol=rtol, where=f"{where} state {layer}/{which}")
+        r = recurrent_rtol if (recurrent_rtol is not None and which == 1) else rtol
+        parity(got, flat[n * k:(n + 1) * k], rtol=r, where=f"{where} state {layer}/{which}")
 
 
 def walk_checkpoints(name, run, c, rec, rtol=FP32_RTOL):
@@ -102,7 +114,8 @@ def walk_checkpoints(name, run, c, rec, rtol=FP32_RTOL):
         assert run.position == p
         margin, bound = check_logits(name, (p,), logits, rec, f"p{p}_", rtol, f"{name} checkpoint {p}")
         check_pick(int(np.argmax(logits)), int(rec[f"p{p}_pick"]), margin, bound, f"{name} checkpoint {p}")
-        check_state(name, p, run, c, rec, f"p{p}_state", rtol, f"{name} checkpoint {p}")
+        check_state(name, p, run, c, rec, f"p{p}_state", rtol, f"{name} checkpoint {p}",
+                    recurrent_rtol=LONG_RECURRENT_RTOL if p > 4096 and rtol == FP32_RTOL else None)
         margins.append(margin)
         print(f"{name}: checkpoint {p} ok (top-2 margin {margin:.3e})", flush=True)
     return logits
@@ -200,7 +213,7 @@ def test_c4_prefill_8192_one_chunk(weights, fast):
     logits = run.prefill([int(v) for v in rec["prompt"]])
     margin, bound = check_logits("c4", (8192,), logits, rec, "p8192_", FP32_RTOL, "c4 one chunk")
     check_pick(int(np.argmax(logits)), int(rec["p8192_pick"]), margin, bound, "c4 one chunk")
-    check_state("c4", 8192, run, c, rec, "p8192_state", FP32_RTOL, "c4 one chunk")
+    check_state("c4", 8192, run, c, rec, "p8192_state", FP32_RTOL, "c4 one chunk", recurrent_rtol=LONG_RECURRENT_RTOL)
 
 
 def test_c4_prefill_8192_checkpoints_and_greedy(weights, fast):
@@ -212,7 +225,8 @@ def test_c4_prefill_8192_checkpoints_and_greedy(weights, fast):
     assert run.decode_plan
     walk_checkpoints("c4", run, c, rec)
     greedy_against_fixture("c4", run, rec)
-    check_state("c4", 3_000_000, run, c, rec, "greedy_state", FP32_RTOL, "c4 after greedy")
+    check_state("c4", 3_000_000, run, c, rec, "greedy_state", FP32_RTOL, "c4 after greedy",
+                recurrent_rtol=LONG_RECURRENT_RTOL)
 
 
 def test_c4_one_launch_vs_op_sequence_at_8192(weights, fast):
@@ -223,6 +237,7 @@ def test_c4_one_launch_vs_op_sequence_at_8192(weights, fast):
     rec = G.load("c4")
     ids = [int(v) for v in rec["prompt"]]
     ops = E.Model(w, disable=E.NO_DECODE_STEP)
+    ops.set_run_budget(64 << 30)
     a, b = fast.new_run(8192 + 72, chunk=8192), ops.new_run(8192 + 72, chunk=8192)
     assert a.decode_plan and not b.decode_plan
     a.prefill(ids)
