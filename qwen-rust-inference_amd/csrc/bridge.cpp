@@ -172,8 +172,25 @@ int group(Context* c, qr::WeightType t, int n, const QrProjection* items, const 
     for (int i = 0; i < n; ++i)
         if (items[i].rows < 1) return fail(c, "GEMM group shape", -1);
     if (qr::gemm_preferred(t, items[0].rows, cols, batch)) {
-        for (int i = 0; i < n; ++i)
+        for (int i = 0; i < n; ++i) {
+            // two consecutive few-row fp32 matrices (the DeltaNet a / b) in one launch
+            if (i + 1 < n && qr::gemm_ab_ok(t, items[i].a, x, items[i].rows, cols, batch) &&
+                qr::gemm_ab_ok(t, items[i + 1].a, x, items[i + 1].rows, cols, batch)) {
+                auto sc = scope(c, [&] {
+                    return std::string("gemm_f32_ab ") + shape(items[i].rows, cols, batch) + "+" +
+                           shape(items[i + 1].rows, cols, batch);
+                });
+                if (int st = launched(c, "gemm_ab",
+                                      qr::gemm_ab(c->stream, items[i].y, static_cast<const float*>(items[i].a),
+                                                  items[i].rows, items[i + 1].y,
+                                                  static_cast<const float*>(items[i + 1].a), items[i + 1].rows, x,
+                                                  cols, batch)))
+                    return st;
+                ++i;
+                continue;
+            }
             if (int s = project(c, t, items[i].y, items[i].a, x, items[i].rows, cols, batch)) return s;
+        }
         return 0;
     }
     qr::GemvItem its[64];

@@ -84,6 +84,12 @@ int gemm(hipStream_t s, WeightType t, float* y, const void* a, const float* x, i
          float* work, size_t work_len);
 size_t gemm_scratch(WeightType t, int rows, int cols, int batch);
 bool gemm_preferred(WeightType t, int rows, int cols, int batch);
+// Y1 = X A1^T and (rows2 > 0) Y2 = X A2^T in one launch for fp32 matrices of
+// at most 16 rows and 1024 columns (the DeltaNet a / b projections of
+// prefill), when gemm_ab_ok holds for each.
+bool gemm_ab_ok(WeightType t, const void* a, const float* x, int rows, int cols, int batch);
+int gemm_ab(hipStream_t s, float* y1, const float* a1, int rows1, float* y2, const float* a2, int rows2,
+            const float* x, int cols, int batch);
 // product[batch, rows] = silu(X G^T) * (X U^T) in one kernel (prefill, any weight format).
 bool gemm_glu_fused(WeightType t, const void* gate, const void* up, const float* x, int rows, int cols, int batch);
 int gemm_glu(hipStream_t s, WeightType t, float* product, const void* gate, const void* up, const float* x, int rows,

@@ -7,7 +7,9 @@
 // (rows) output tile per 256-thread block, 2 x 2 waves of 64 x 64 (2 x 2 MFMA
 // tiles each); K in steps of 32 through LDS; the next K step's global loads are
 // in flight (registers) while the current one is multiplied.
-// fp32 weights with at most 16 rows: gemm_skinny_kernel (lanes over columns).
+// fp32 weights with at most 16 rows (the DeltaNet a / b projections):
+// gemm_ab_kernel, two such matrices per launch (x read once), up to 1024
+// columns; wider rows: gemm_skinny_kernel (lanes over columns).
 // Fewer 128 x 128 tiles than CUs: K split into chunks (partials + an ordered
 // sum). The prefill GLU: gate and up in one MFMA kernel with silu(g) * u in
 // the epilogue.
@@ -341,6 +343,68 @@ __global__ __launch_bounds__(256) void gemm_skinny_kernel(float* y, const float*
     if (m0 + t < batch && r < rows) y[size_t(m0 + t) * rows + r] = sum;
 }
 
+// Up to two fp32 matrices of 32 rows together (the DeltaNet a / b
+// projections, 16 rows each) over at most 1024 columns of the same x, in one
+// launch that reads x once. Lane l of wave w holds row l % 32 (rows of matrix
+// 1, then matrix 2) over columns [64 s, 64 s + 64), s = 2 w + l / 32, in
+// registers for the whole launch; the block stages 8 token rows of x in LDS,
+// every lane forms its 64-term dot for each token, and the 16 partials of a
+// (token, row) are summed in slot order. Blocks stride over the 8-token groups.
+constexpr int AB_ROWS = 32, AB_COLS = 1024, AB_TOK = 8, AB_SLOTS = AB_COLS / 64;
+struct AbMats {
+    float* y[2];
+    const float* a[2];
+    int rows[2];
+};
+__global__ __launch_bounds__(512) void gemm_ab_kernel(AbMats m, const float* x, int cols, int batch) {
+    __shared__ f4v xs[AB_TOK][AB_COLS / 4];
+    __shared__ float part[AB_TOK][AB_SLOTS][AB_ROWS + 1];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int r = lane & 31, slot = 2 * wave + (lane >> 5);
+    const int rows = m.rows[0] + m.rows[1];
+    const int mi = r < m.rows[0] ? 0 : 1, rr = mi ? r - m.rows[0] : r;
+    f4v wv[16];
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+        const int k = 64 * slot + 4 * e;
+        wv[e] = r < rows && k < cols ? *reinterpret_cast<const f4v*>(m.a[mi] + size_t(rr) * cols + k)
+                                     : f4v{0.f, 0.f, 0.f, 0.f};
+    }
+    for (int g = int(blockIdx.x); g * AB_TOK < batch; g += int(gridDim.x)) {
+        const int t0 = g * AB_TOK;
+        for (int i = int(threadIdx.x); i < AB_TOK * AB_COLS / 4; i += 512) {
+            const int t = i / (AB_COLS / 4), k = 4 * (i % (AB_COLS / 4));
+            xs[t][k / 4] = t0 + t < batch && k < cols ? *reinterpret_cast<const f4v*>(x + size_t(t0 + t) * cols + k)
+                                                      : f4v{0.f, 0.f, 0.f, 0.f};
+        }
+        __syncthreads();
+#pragma unroll
+        for (int t = 0; t < AB_TOK; ++t) {
+            float acc = 0.f;
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const f4v xv = xs[t][16 * slot + e];
+                acc = fmaf(wv[e].x, xv.x, acc);
+                acc = fmaf(wv[e].y, xv.y, acc);
+                acc = fmaf(wv[e].z, xv.z, acc);
+                acc = fmaf(wv[e].w, xv.w, acc);
+            }
+            part[t][slot][r] = acc;
+        }
+        __syncthreads();
+        if (int(threadIdx.x) < AB_TOK * AB_ROWS) {
+            const int t = int(threadIdx.x) / AB_ROWS, o = int(threadIdx.x) % AB_ROWS;
+            if (o < rows && t0 + t < batch) {
+                float sum = 0.f;
+                for (int j = 0; j < AB_SLOTS; ++j) sum += part[t][j][o];
+                const int oi = o < m.rows[0] ? 0 : 1, orow = oi ? o - m.rows[0] : o;
+                m.y[oi][size_t(t0 + t) * m.rows[oi] + orow] = sum;
+            }
+        }
+        __syncthreads();
+    }
+}
+
 }  // namespace
 
 bool gemm_preferred(WeightType, int, int, int batch) { return batch > 4; }
@@ -357,6 +421,21 @@ size_t gemm_scratch(WeightType t, int rows, int cols, int batch) {
     int kchunk;
     const int splits = mfma_splits(rows, cols, batch, kchunk);
     return splits > 1 ? size_t(splits) * size_t(rows) * size_t(batch) : 0;
+}
+
+bool gemm_ab_ok(WeightType t, const void* a, const float* x, int rows, int cols, int batch) {
+    return t == WeightType::F32 && gemm_preferred(t, rows, cols, batch) && rows >= 1 && rows <= AB_ROWS / 2 &&
+           cols <= AB_COLS && mfma_ok(t, a, x, cols);
+}
+int gemm_ab(hipStream_t s, float* y1, const float* a1, int rows1, float* y2, const float* a2, int rows2,
+            const float* x, int cols, int batch) {
+    if (rows1 < 1 || rows2 < 0 || rows1 + rows2 > AB_ROWS || (rows2 > 0 && (!y2 || !a2)) || cols % 4 != 0 ||
+        cols > AB_COLS || batch < 1)
+        return int(hipErrorInvalidValue);
+    const AbMats m{{y1, rows2 > 0 ? y2 : y1}, {a1, rows2 > 0 ? a2 : a1}, {rows1, rows2}};
+    const int groups = int(ceil_div(batch, AB_TOK));
+    hipLaunchKernelGGL(gemm_ab_kernel, dim3(unsigned(groups < 256 ? groups : 256)), dim3(512), 0, s, m, x, cols, batch);
+    return int(hipGetLastError());
 }
 
 // The split-BF16 MFMA kernel over every weight format (with the K split), or
@@ -385,6 +464,7 @@ int gemm(hipStream_t s, WeightType t, float* y, const void* a, const float* x, i
     dim3 grid(ceil_div(rows, BN), ceil_div(batch, BM));
     if (mfma_ok(t, a, x, cols)) {
         if (t == WeightType::F32 && rows <= SK_ROWS) {
+            if (cols <= AB_COLS) return gemm_ab(s, y, static_cast<const float*>(a), rows, nullptr, nullptr, 0, x, cols, batch);
             hipLaunchKernelGGL(gemm_skinny_kernel, dim3(ceil_div(batch, 4 * SK_TOK)), dim3(256), 0, s, y,
                                static_cast<const float*>(a), x, rows, cols, batch);
             return int(hipGetLastError());
