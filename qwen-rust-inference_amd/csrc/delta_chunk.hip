@@ -212,91 +212,131 @@ __device__ __forceinline__ f4v mfma16(float x, float y, f4v acc) {
 // One block per (head, 16-column slice of S), 4 waves. Wave w: rows 16w..16w+15
 // of D and of O (phase 1: D = U - W S0 and O = e^G Q S0, sharing every S0
 // read), then O += L D over the tokens up to its rows and S rows of tiles w
-// and w + 4 (phase 2: one D read feeds all three products). The next chunk's
-// phase-1 operands are loaded while phase 2 runs.
+// and w + 4 (phase 2: one D read feeds all three products).
+// S and D live in LDS in B-operand order: entry [l][s] is row 4 s + l / 16,
+// column l % 16, the value lane l feeds the MFMA step s (k = 4 s + l / 16)
+// of a product over them, so each lane takes all of its operands in a few
+// 16-byte reads and one wait (rows padded to 36 / 20 floats: the 16-byte
+// reads of 8 consecutive lanes hit distinct banks).
+// Operand loads run a phase ahead: chunk c + 1's -W, e^G Q and U are issued
+// once phase 1 of chunk c has consumed chunk c's, its L and K^T once phase 2
+// has; the barriers wait for LDS only, so those loads stay in flight across
+// them (__syncthreads() would also wait for every outstanding load).
 // Blocks are dealt to the 8 XCDs round-robin by index; the index is remapped
 // so that the 8 slices of a head run on one XCD: every slice reads the whole
 // chunk record, and this way 7 of the 8 reads hit that XCD's L2 instead of
 // the memory-side cache or HBM.
 constexpr int kXcds = 8;
-__global__ __launch_bounds__(256) void rule_chunk_scan_kernel(Params a, int c0, int chunks, const float* scratch) {
-    __shared__ float sl[kD][kSlice];
-    __shared__ float dl[kC][kSlice];
+constexpr int kSRow = 36, kDRow = 20;
+typedef __amdgpu_buffer_rsrc_t Rs;
+__device__ void buffer_store_f32(float v, Rs r, unsigned voff, unsigned soff, int aux) __asm("llvm.amdgcn.raw.ptr.buffer.store.f32");
+// Block barrier for LDS traffic only: the block's LDS writes done
+// (lgkmcnt(0)), then s_barrier; outstanding global loads and stores are not
+// waited for.
+__device__ __forceinline__ void lds_barrier() {
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0); vmcnt and expcnt not waited
+    __builtin_amdgcn_s_barrier();
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+__device__ __forceinline__ const float* scan_rec(const float* __restrict__ scratch, int c, int vh, int h) {
+    return scratch + (size_t(c) * vh + h) * kRec;
+}
+// Phase-1 operands of a chunk: -W and e^G Q rows of tile w, U of the slice.
+__device__ __forceinline__ void scan_load1(const float* rec, int w, int js, int l, f4v (&wv)[8], f4v (&qv)[8], f4v& uv) {
+    const f4v* W = reinterpret_cast<const f4v*>(rec + kW) + w * 512 + l;
+    const f4v* Q = reinterpret_cast<const f4v*>(rec + kQ) + w * 512 + l;
+#pragma unroll
+    for (int m = 0; m < 8; ++m) {
+        wv[m] = W[m * 64];
+        qv[m] = Q[m * 64];
+    }
+    uv = reinterpret_cast<const f4v*>(rec + kU)[(w * kSlices + js) * 64 + l];
+}
+// Phase-2 operands: L rows of tile w, K^T rows of tiles w and w + 4.
+__device__ __forceinline__ void scan_load2(const float* rec, int w, int l, f4v (&lv)[4], f4v (&k0)[4], f4v (&k1)[4]) {
+    const f4v* Lp = reinterpret_cast<const f4v*>(rec + kL) + w * 256 + l;
+    const f4v* Kp = reinterpret_cast<const f4v*>(rec + kK) + l;
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+        lv[m] = Lp[m * 64];
+        k0[m] = Kp[w * 256 + m * 64];
+        k1[m] = Kp[(w + 4) * 256 + m * 64];
+    }
+}
+__global__ __launch_bounds__(256) void rule_chunk_scan_kernel(Params a, int c0, int chunks,
+                                                              const float* __restrict__ scratch) {
+    __shared__ __attribute__((aligned(16))) float sl[64][kSRow];
+    __shared__ __attribute__((aligned(16))) float dl[64][kDRow];
     const int nb = int(gridDim.x), b = int(blockIdx.x);
     const int i = nb % kXcds == 0 ? (b % kXcds) * (nb / kXcds) + b / kXcds : b;
     const int h = i / kSlices, js = i % kSlices;
     const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, lc = l & 15, q = l >> 4;
     const int vh = a.n[3], tokens = a.n[4] > 0 ? a.n[4] : 1;
     float* state = a.p[4] + size_t(h) * kD * kD + js * kSlice;
-    for (int e = tid; e < kD * kSlice; e += 256) sl[e / kSlice][e % kSlice] = state[size_t(e / kSlice) * kD + e % kSlice];
-    auto load1 = [&](int c, f4v (&wv)[8], f4v (&qv)[8], f4v& uv) {
-        const float* rec = scratch + (size_t(c) * vh + h) * kRec;
-        const f4v* W = reinterpret_cast<const f4v*>(rec + kW) + w * 512 + l;
-        const f4v* Q = reinterpret_cast<const f4v*>(rec + kQ) + w * 512 + l;
-#pragma unroll
-        for (int m = 0; m < 8; ++m) {
-            wv[m] = W[m * 64];
-            qv[m] = Q[m * 64];
-        }
-        uv = reinterpret_cast<const f4v*>(rec + kU)[(w * kSlices + js) * 64 + l];
-    };
-    f4v wv[8], qv[8], uv;
-    load1(0, wv, qv, uv);
+    // the output as a buffer of exactly tokens x vh x kD floats (its size is
+    // checked below 2^31 bytes on the host): stores past it are dropped, so
+    // the ragged last chunk needs no per-lane branch around its stores
+    const Rs out_rs = __builtin_amdgcn_make_buffer_rsrc(a.p[0], 0, tokens * vh * kD * 4, 0x00020000);
+    for (int e = tid; e < kD * kSlice; e += 256) {  // S row k, column j -> [16 (k % 4) + j][k / 4]
+        const int k = e / kSlice, j = e % kSlice;
+        sl[16 * (k & 3) + j][k >> 2] = state[size_t(k) * kD + j];
+    }
+    f4v wv[8], qv[8], uv, lv[4], k0[4], k1[4];
+    scan_load1(scan_rec(scratch, 0, vh, h), w, js, l, wv, qv, uv);
+    scan_load2(scan_rec(scratch, 0, vh, h), w, l, lv, k0, k1);
     __syncthreads();
     for (int c = 0; c < chunks; ++c) {
-        const float* rec = scratch + (size_t(c) * vh + h) * kRec;
         const int t0 = (c0 + c) * kC;
-        f4v lv[4], k0[4], k1[4];  // phase-2 operands: L rows of tile w, K^T rows of tiles w and w + 4
-        {
-            const f4v* Lp = reinterpret_cast<const f4v*>(rec + kL) + w * 256 + l;
-            const f4v* Kp = reinterpret_cast<const f4v*>(rec + kK) + l;
+        const int cn = c + 1 < chunks ? c + 1 : c;  // the last chunk reloads itself
+        const float decay = scan_rec(scratch, c, vh, h)[kG];
+        f4v sb[8];  // S in B-operand order: step s = 4 m + e is sb[m][e]
 #pragma unroll
-            for (int m = 0; m < 4; ++m) {
-                lv[m] = Lp[m * 64];
-                k0[m] = Kp[w * 256 + m * 64];
-                k1[m] = Kp[(w + 4) * 256 + m * 64];
-            }
-        }
-        const float decay = rec[kG];
+        for (int m = 0; m < 8; ++m) sb[m] = *reinterpret_cast<const f4v*>(&sl[l][4 * m]);
         f4v dacc = uv, oacc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int m = 0; m < 8; ++m)
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                const float b = sl[16 * m + 4 * e + q][lc];  // k = 4 (4m + e) + q
-                dacc = mfma16(wv[m][e], b, dacc);
-                oacc = mfma16(qv[m][e], b, oacc);
+                dacc = mfma16(wv[m][e], sb[m][e], dacc);
+                oacc = mfma16(qv[m][e], sb[m][e], oacc);
             }
+        scan_load1(scan_rec(scratch, cn, vh, h), w, js, l, wv, qv, uv);
 #pragma unroll
-        for (int r = 0; r < 4; ++r) dl[16 * w + 4 * q + r][lc] = dacc[r];
-        __syncthreads();
-        if (c + 1 < chunks) load1(c + 1, wv, qv, uv);
+        for (int r = 0; r < 4; ++r) dl[16 * r + lc][4 * w + q] = dacc[r];  // D row 16 w + 4 q + r
+        lds_barrier();
         f4v s0, s1;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            s0[r] = decay * sl[16 * w + 4 * q + r][lc];
-            s1[r] = decay * sl[16 * (w + 4) + 4 * q + r][lc];
+        for (int r = 0; r < 4; ++r) {  // S rows 16 w + 4 q + r and 16 (w + 4) + 4 q + r
+            s0[r] = decay * sl[16 * r + lc][4 * w + q];
+            s1[r] = decay * sl[16 * r + lc][4 * w + 16 + q];
         }
+        f4v db[4];
+#pragma unroll
+        for (int m = 0; m < 4; ++m) db[m] = *reinterpret_cast<const f4v*>(&dl[l][4 * m]);
 #pragma unroll
         for (int m = 0; m < 4; ++m)
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                const float b = dl[16 * m + 4 * e + q][lc];
-                if (m <= w) oacc = mfma16(lv[m][e], b, oacc);  // L is zero past the tile's last token
-                s0 = mfma16(k0[m][e], b, s0);
-                s1 = mfma16(k1[m][e], b, s1);
+                if (m <= w) oacc = mfma16(lv[m][e], db[m][e], oacc);  // L is zero past the tile's last token
+                s0 = mfma16(k0[m][e], db[m][e], s0);
+                s1 = mfma16(k1[m][e], db[m][e], s1);
             }
-        float* out = a.p[0] + size_t(h) * kD + js * kSlice + lc;
+        scan_load2(scan_rec(scratch, cn, vh, h), w, l, lv, k0, k1);
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            const int t = t0 + 16 * w + 4 * q + r;
-            if (t < tokens) out[size_t(t) * vh * kD] = oacc[r];
-            sl[16 * w + 4 * q + r][lc] = s0[r];
-            sl[16 * (w + 4) + 4 * q + r][lc] = s1[r];
+            const int t = t0 + 16 * w + 4 * q + r;  // rows t >= tokens fall outside out_rs: dropped
+            buffer_store_f32(oacc[r], out_rs, unsigned(((t * vh + h) * kD + js * kSlice + lc) * 4), 0, 0);
+            sl[16 * r + lc][4 * w + q] = s0[r];
+            sl[16 * r + lc][4 * w + 16 + q] = s1[r];
         }
-        __syncthreads();
+        lds_barrier();
     }
-    for (int e = tid; e < kD * kSlice; e += 256) state[size_t(e / kSlice) * kD + e % kSlice] = sl[e / kSlice][e % kSlice];
+    __syncthreads();
+    for (int e = tid; e < kD * kSlice; e += 256) {
+        const int k = e / kSlice, j = e % kSlice;
+        state[size_t(k) * kD + j] = sl[16 * (k & 3) + j][k >> 2];
+    }
 }
 
 }  // namespace
@@ -306,7 +346,8 @@ bool delta_rule_chunked_ok(const Params& a, int count) {
     const uintptr_t vec = reinterpret_cast<uintptr_t>(a.p[1]) | reinterpret_cast<uintptr_t>(a.p[2]) |
                           reinterpret_cast<uintptr_t>(a.p[3]);  // float4 loads of q, k, v rows
     return a.n[0] == kD && a.n[1] == kD && a.n[3] >= 1 && count == a.n[3] * kD && a.n[6] <= 0 &&
-           tokens >= kChunkMinTokens && vec % 16 == 0 && a.n[5] % 4 == 0 && a.n[2] >= 0;
+           tokens >= kChunkMinTokens && vec % 16 == 0 && a.n[5] % 4 == 0 && a.n[2] >= 0 &&
+           int64_t(tokens) * a.n[3] * kD * 4 < (int64_t(1) << 31);  // the scan's output buffer resource
 }
 
 size_t delta_rule_chunked_scratch(const Params& a) {
