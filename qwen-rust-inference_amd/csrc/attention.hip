@@ -357,11 +357,245 @@ __global__ __launch_bounds__(64 * G) void attention_prefill_kernel(ReadArgs a) {
     }
 }
 
+// ---- D = 256, G = 4 (the attention layers of the Qwen3.5-0.8B shape): the
+// block / share decomposition, masking and online softmax of
+// attention_prefill_kernel, with both products on BF16 MFMA
+// (v_mfma_f32_32x32x16_bf16) over operands split into three BF16 parts each
+// (x = x0 + x1 + x2, the six part products with p + q <= 2 summed smallest
+// first: fp32 accuracy, as the prefill GEMM) at 2.7x the rate of the fp32
+// MFMA.
+// 8 waves: wave w is query head w % 4 of the group over dims 128 (w / 4) ..
+// + 127 (its half). S^T = K Q^T over the half: A = the tile's K rows (three
+// planes in LDS), B = Q^T (three planes in registers, split once); the two
+// halves' partial scores are exchanged through LDS and added (the same sum
+// on both waves), so both run the same softmax. O^T += V^T P^T over the
+// half's dims: A = V^T (three planes in LDS, transposed), B = P^T taken
+// straight from the score accumulator: lane l holds keys 8 (r / 4) +
+// 4 (l / 32) + r % 4 of its query in register r, so MFMA k index 8 (l / 32)
+// + e of step s is key 16 s + 8 (e / 4) + 4 (l / 32) + e % 4 when the B
+// operand of step s is registers 8 s .. 8 s + 7; V^T keeps its key positions
+// in that order (bits 2 and 3 of the key swapped), so no value crosses
+// lanes.
+// One K/V tile in LDS (K 3 x 32 x 264 and V^T 3 x 256 x 40 BF16, 110 KB; rows
+// padded so the 16-byte operand reads of 8 consecutive lanes hit distinct
+// banks) plus the 32 KB score exchange: the next tile's K values are loaded
+// into registers during the current tile's products (its V values when it is
+// staged: both would not fit the 256 registers of a wave at two waves per
+// SIMD) and split into LDS between two barriers.
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+constexpr int B3_KROW = 256 + 8, B3_VROW = 40;
+
+struct Split3 {
+    __bf16 h[3];
+};
+__device__ __forceinline__ Split3 split3(float x) {
+    Split3 o;
+    o.h[0] = __bf16(x);
+    const float r1 = x - float(o.h[0]);
+    o.h[1] = __bf16(r1);
+    o.h[2] = __bf16(r1 - float(o.h[1]));
+    return o;
+}
+// the V^T position of tile key k: bits 2 and 3 swapped
+__device__ __forceinline__ int vpos(int k) { return (k & ~12) | ((k & 4) << 1) | ((k & 8) >> 1); }
+
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void attention_prefill_bf3_kernel(
+    ReadArgs a) {
+    constexpr int D = 256, G = 4, HALF = D / 2, DT = HALF / 32;
+    __shared__ __attribute__((aligned(16))) __bf16 ks[3][32][B3_KROW];
+    __shared__ __attribute__((aligned(16))) __bf16 vt[3][D][B3_VROW];
+    __shared__ float xch[8][16][64];
+    const int qtiles = (a.rows + 31) / 32;
+    const int q0 = (qtiles - 1 - int(blockIdx.x)) * 32, kvh = blockIdx.y;  // longest rows first
+    const int tid = int(threadIdx.x), lane = tid & 63, w = tid >> 6, lc = lane & 31, hl = lane >> 5;
+    const int g = w & 3, dh = w >> 2, d0 = dh * HALF;
+    const int head = kvh * G + g, qrow = q0 + lc;
+    const int len = a.length0 + qrow;  // positions [0, len) visible to this lane's query
+    const int len_max = a.length0 + min(a.rows, q0 + 32) - 1;
+    const int all_tiles = (len_max + 31) / 32, share = (all_tiles + a.splits - 1) / a.splits;
+    const int t_begin = int(blockIdx.z) * share, t_end = min(all_tiles, t_begin + share);
+    if (t_begin >= t_end) {  // an empty share (early query tiles): a neutral partial
+        if (qrow < a.rows && dh == 0) {
+            float* part = a.parts + ((size_t(qrow) * a.heads + head) * a.splits + blockIdx.z) * (D + 2);
+            for (int i = hl; i < D + 2; i += 2) part[i] = i == 0 ? -INFINITY : 0.f;
+        }
+        return;
+    }
+    const float scale = 1.f / sqrtf(float(D));
+    const size_t rowstride = size_t(a.kv) * D;
+    bf16x8 qb[3][8];  // Q^T planes: step s, element e = dim d0 + 16 s + 8 hl + e of this lane's query
+    {
+        const float* qp = a.query + (size_t(qrow) * a.heads + head) * D + d0 + 8 * hl;
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+            const f4v z = {0.f, 0.f, 0.f, 0.f};
+            const f4v v0 = qrow < a.rows ? *reinterpret_cast<const f4v*>(qp + 16 * s) : z;
+            const f4v v1 = qrow < a.rows ? *reinterpret_cast<const f4v*>(qp + 16 * s + 4) : z;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const Split3 x = split3(e < 4 ? v0[e] : v1[e - 4]);
+#pragma unroll
+                for (int p = 0; p < 3; ++p) qb[p][s][e] = x.h[p];
+            }
+        }
+    }
+    // this thread's share of a tile: K quads f = tid + 512 i (key f / 64, dims
+    // 4 (f % 64)); one V block of 4 keys x 4 dims b = tid (keys 4 (b / 64) + r,
+    // dims 4 (b % 64)); every row read as 64 consecutive 16-byte loads
+    f4v kp[4];
+    auto fetch = [&](int t) {
+        const f4v z = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int f = tid + 512 * i, pos = t * 32 + (f >> 6), c = (f & 63) * 4;
+            kp[i] = pos < len_max ? *reinterpret_cast<const f4v*>(a.keys + size_t(pos) * rowstride + size_t(kvh) * D + c)
+                                  : z;
+        }
+    };
+    auto stage = [&](int t) {
+        f4v vp[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const f4v z = {0.f, 0.f, 0.f, 0.f};
+            const int pos = t * 32 + 4 * (tid >> 6) + r, c = (tid & 63) * 4;
+            vp[r] = pos < len_max ? *reinterpret_cast<const f4v*>(a.values + size_t(pos) * rowstride + size_t(kvh) * D + c)
+                                  : z;
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int f = tid + 512 * i, key = f >> 6, c = (f & 63) * 4;
+            bf16x4 h[3];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const Split3 x = split3(kp[i][e]);
+#pragma unroll
+                for (int p = 0; p < 3; ++p) h[p][e] = x.h[p];
+            }
+#pragma unroll
+            for (int p = 0; p < 3; ++p) *reinterpret_cast<bf16x4*>(&ks[p][key][c]) = h[p];
+        }
+        const int p0 = vpos(4 * (tid >> 6)), c = (tid & 63) * 4;
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+            bf16x4 h[3];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const Split3 x = split3(vp[r][d]);
+#pragma unroll
+                for (int p = 0; p < 3; ++p) h[p][r] = x.h[p];
+            }
+#pragma unroll
+            for (int p = 0; p < 3; ++p) *reinterpret_cast<bf16x4*>(&vt[p][c + d][p0]) = h[p];
+        }
+    };
+    constexpr int P[6] = {2, 1, 0, 1, 0, 0}, Q[6] = {0, 1, 2, 0, 1, 0};  // part products, smallest first
+    fetch(t_begin);
+    stage(t_begin);
+    __syncthreads();
+    f16v o[DT];
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[dt][r] = 0.f;
+    float m = -INFINITY, l = 0.f;
+    for (int t = t_begin; t < t_end; ++t) {
+        if (t + 1 < t_end) fetch(t + 1);
+        f16v sc;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) sc[r] = 0.f;
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+            bf16x8 ka[3];
+#pragma unroll
+            for (int p = 0; p < 3; ++p) ka[p] = *reinterpret_cast<const bf16x8*>(&ks[p][lc][d0 + 16 * s + 8 * hl]);
+#pragma unroll
+            for (int pq = 0; pq < 6; ++pq) sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka[P[pq]], qb[Q[pq]][s], sc, 0, 0, 0);
+        }
+#pragma unroll
+        for (int r = 0; r < 16; ++r) xch[w][r][lane] = sc[r];
+        __syncthreads();
+        float mx = -INFINITY;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const float full = sc[r] + xch[w ^ 4][r][lane];  // the two halves' dims (addition commutes: same on both)
+            const float v = t * 32 + acc_row(r, hl) < len ? full * scale : -INFINITY;
+            sc[r] = v;
+            mx = fmaxf(mx, v);
+        }
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        // -inf while a row has seen no visible position (a KV share past its length)
+        const float mn = fmaxf(m, mx), mref = mn == -INFINITY ? 0.f : mn;
+        const float corr = expf(m - mref);
+        m = mn;
+        float ps = 0.f;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            sc[r] = expf(sc[r] - mref);
+            ps += sc[r];
+        }
+        l = l * corr + ps;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) o[dt] *= corr;
+        // key steps outermost, so one step's P^T planes are live at a time
+        // (each accumulator still takes step 0's products, then step 1's)
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+            bf16x8 pb[3];  // P^T planes of step s: element e = register 8 s + e
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const Split3 x = split3(sc[8 * s + e]);
+#pragma unroll
+                for (int p = 0; p < 3; ++p) pb[p][e] = x.h[p];
+            }
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) {
+                bf16x8 va[3];
+#pragma unroll
+                for (int p = 0; p < 3; ++p)
+                    va[p] = *reinterpret_cast<const bf16x8*>(&vt[p][d0 + 32 * dt + lc][16 * s + 8 * hl]);
+#pragma unroll
+                for (int pq = 0; pq < 6; ++pq)
+                    o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va[P[pq]], pb[Q[pq]], o[dt], 0, 0, 0);
+            }
+        }
+        __syncthreads();
+        if (t + 1 < t_end) {
+            stage(t + 1);
+            __syncthreads();
+        }
+    }
+    const float den = l + __shfl_xor(l, 32, 64);
+    if (qrow < a.rows && a.splits == 1) {
+        const size_t base = (size_t(qrow) * a.heads + head) * D + d0;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const size_t idx = base + dt * 32 + acc_row(r, hl);
+                a.out[idx] = (o[dt][r] / den) * sigmoidf_(a.gate[idx]);
+            }
+    } else if (qrow < a.rows) {
+        float* part = a.parts + ((size_t(qrow) * a.heads + head) * a.splits + blockIdx.z) * (D + 2);
+        if (hl == 0 && dh == 0) {
+            part[0] = m;
+            part[1] = den;
+        }
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) part[2 + d0 + dt * 32 + acc_row(r, hl)] = o[dt][r];
+    }
+}
+
 template <int D, int G>
 int launch_prefill_g(hipStream_t s, const ReadArgs& a) {
     if constexpr (prefill_shape_ok(D, G)) {
-        hipLaunchKernelGGL((attention_prefill_kernel<D, G>),
-                           dim3(ceil_div(a.rows, 32), unsigned(a.kv), unsigned(a.splits)), dim3(64 * G), 0, s, a);
+        const dim3 grid(ceil_div(a.rows, 32), unsigned(a.kv), unsigned(a.splits));
+        if constexpr (D == 256 && G == 4)
+            hipLaunchKernelGGL(attention_prefill_bf3_kernel, grid, dim3(512), 0, s, a);
+        else
+            hipLaunchKernelGGL((attention_prefill_kernel<D, G>), grid, dim3(64 * G), 0, s, a);
         if (a.splits == 1) return int(hipGetLastError());
         if (hipError_t e = hipGetLastError()) return int(e);
         const long total = long(a.rows) * a.heads * a.d;
