@@ -28,6 +28,17 @@ struct Error {
 void require(bool ok, const std::string& what) {
     if (!ok) throw Error{what};
 }
+// the message is built only on failure (checks over every element of a
+// vector run this once per element)
+void require(bool ok, const char* what) {
+    if (!ok) throw Error{what};
+}
+// Every value finite (the reference's NaN/Inf check on device reads and
+// uploads): one pass that stops at the first non-finite value.
+void require_finite(const float* v, size_t n) {
+    for (size_t i = 0; i < n; ++i)
+        if (!std::isfinite(v[i])) throw Error{"NaN/Inf detected"};
+}
 template <class F>
 int guarded(F&& f) {
     try {
@@ -247,13 +258,13 @@ struct Buffer {
         require(n > 0 && n <= len, "device read bounds");
         std::vector<float> host(n);
         api->check(api->read(api->ctx, host.data(), p, n));
-        for (float v : host) require(std::isfinite(v), "NaN/Inf detected");
+        require_finite(host.data(), host.size());
         return host;
     }
 };
 
 Buffer upload(const Api* api, const float* v, size_t n) {
-    for (size_t i = 0; i < n; ++i) require(std::isfinite(v[i]), "NaN/Inf detected");
+    require_finite(v, n);
     Buffer b(api, n);
     b.write(v, n);
     return b;
@@ -629,7 +640,7 @@ struct QeRun {
                 for (size_t r = 0; r < h; ++r) correction[r] -= e.coefficient * d[r] * projection * product[j];
             }
         }
-        for (float v : correction) require(std::isfinite(v), "NaN/Inf detected");
+        require_finite(correction.data(), correction.size());
         return correction;
     }
 
@@ -833,7 +844,7 @@ struct QeRun {
     }
     // select (src/generate.rs:30-41)
     static uint32_t select_greedy(const std::vector<float>& logits) {
-        for (float v : logits) require(std::isfinite(v), "NaN/Inf detected");
+        require_finite(logits.data(), logits.size());
         size_t best = 0;
         for (size_t i = 1; i < logits.size(); ++i)
             if (logits[i] > logits[best]) best = i;
@@ -1400,7 +1411,7 @@ int qe_state_write(QeRun* r, int layer, int which, const float* values, int64_t 
         require(n >= 0, "negative length");
         if (n == 0) return;
         const Buffer& b = r->state_buffer(layer, which);
-        for (int64_t i = 0; i < n; ++i) require(std::isfinite(values[i]), "NaN/Inf detected");
+        require_finite(values, size_t(n));
         b.write(values, size_t(n));
     });
 }
