@@ -441,8 +441,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         }
     }
     // this thread's share of a tile: K quads f = tid + 512 i (key f / 64, dims
-    // 4 (f % 64)); one V block of 4 keys x 4 dims b = tid (keys 4 (b / 64) + r,
-    // dims 4 (b % 64)); every row read as 64 consecutive 16-byte loads
+    // 4 (f % 64): every row read as 64 consecutive 16-byte loads) and one V
+    // block of 4 keys x 4 dims (below)
     f4v kp[4];
     auto fetch = [&](int t) {
         const f4v z = {0.f, 0.f, 0.f, 0.f};
@@ -454,11 +454,16 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         }
     };
     auto stage = [&](int t) {
+        // V: key quad tid % 8, dim quad tid / 8, so the 8 lanes of a dim quad
+        // write one V^T row's 32 positions (64 contiguous bytes) and each
+        // 16-lane group of a write covers two rows on disjoint banks; the
+        // global reads are 128 contiguous bytes per row
+        const int kq = tid & 7, cq = tid >> 3;
         f4v vp[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const f4v z = {0.f, 0.f, 0.f, 0.f};
-            const int pos = t * 32 + 4 * (tid >> 6) + r, c = (tid & 63) * 4;
+            const int pos = t * 32 + 4 * kq + r, c = 4 * cq;
             vp[r] = pos < len_max ? *reinterpret_cast<const f4v*>(a.values + size_t(pos) * rowstride + size_t(kvh) * D + c)
                                   : z;
         }
@@ -475,7 +480,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
             for (int p = 0; p < 3; ++p) *reinterpret_cast<bf16x4*>(&ks[p][key][c]) = h[p];
         }
-        const int p0 = vpos(4 * (tid >> 6)), c = (tid & 63) * 4;
+        const int p0 = vpos(4 * kq), c = 4 * cq;
 #pragma unroll
         for (int d = 0; d < 4; ++d) {
             bf16x4 h[3];
