@@ -38,7 +38,8 @@ enum QeDisable {
     QE_NO_ARGMAX = 16,       /* qr_argmax (ops 16-17) */
     QE_NO_SNAPSHOTS = 32,    /* qr_snapshots */
     QE_NO_DECODE_STEP = 64,  /* qr_decode_plan / qr_decode_step */
-    QE_NO_EMBED_ROWS = 128   /* qr_embed_rows */
+    QE_NO_EMBED_ROWS = 128,  /* qr_embed_rows */
+    QE_NO_BLAS_GEMM = 256    /* qr_gemm_f32_prepare (prefill projections on hipBLASLt) */
 };
 
 /* Record callback of a captured step: (layer, name, values, n). Names follow

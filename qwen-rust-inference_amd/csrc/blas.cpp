@@ -1,0 +1,185 @@
+// Prefill projections of prepared fp32 matrices as ONE BF16 GEMM on
+// hipBLASLt. The three-way BF16 split of both operands (x = x0 + x1 + x2,
+// each residual exact in fp32) turns the fp32 product X W^T into the sum of
+// the six part products x_p w_q with p + q <= 2; laid out along K (split6 in
+// gemm.hip: X rows [x2 x1 x0 x1 x0 x0], W rows [w0 w1 w2 w0 w1 w0]) that sum
+// is a plain BF16 GEMM with K' = 6 K, fp32 accumulation and fp32 output. Every
+// BF16 x BF16 product is exact in fp32 and the dropped products are below
+// 2^-24 |x w|, so the result keeps fp32 accuracy (as gemm_bf3_kernel, which
+// runs the same products in its own tiles).
+//
+// hipBLASLt column-major view: C (rows x batch, ldc = rows) = op(A) op(B) with
+// A = W6 stored [rows][6 cols] (op T, lda = 6 cols) and B = X6 stored
+// [batch][6 cols] (op N, ldb = 6 cols); C is Y[batch][rows] row-major.
+#include <hipblaslt/hipblaslt.h>
+
+#include <map>
+#include <mutex>
+#include <new>
+#include <tuple>
+
+#include "common.h"
+
+namespace qr {
+namespace {
+
+constexpr size_t kWorkspace = size_t(64) << 20;
+// hipBLASLt's first candidates for a shape; the fastest of the first kTimed is
+// chosen by timing when the batch has at least kTimedBatch tokens (on the
+// prefill shapes of the 0.8B model the fastest was always among the first 8,
+// up to 1.4x faster than the first), else the first is taken. The timing
+// costs a few ms per new shape.
+constexpr int kCandidates = 8, kTimed = 8, kTimedBatch = 256;
+using Shape = std::tuple<int, int, int>;  // rows, cols, batch
+// The candidate chosen for a shape (its index in hipBLASLt's heuristic list),
+// shared by every context of the process so that a shape always runs the same
+// algorithm, hence the same summation order.
+std::mutex g_choice_mu;
+std::map<Shape, int> g_choice;
+
+}  // namespace
+
+struct Blas {
+    hipblasLtHandle_t handle = nullptr;
+    void* ws = nullptr;
+    struct Plan {
+        hipblasLtMatmulDesc_t op = nullptr;
+        hipblasLtMatrixLayout_t la = nullptr, lb = nullptr, lc = nullptr;
+        hipblasLtMatmulAlgo_t algo{};
+    };
+    std::map<Shape, Plan> plans;
+};
+
+namespace {
+
+void destroy_plan(Blas::Plan& p) {
+    if (p.la) (void)hipblasLtMatrixLayoutDestroy(p.la);
+    if (p.lb) (void)hipblasLtMatrixLayoutDestroy(p.lb);
+    if (p.lc) (void)hipblasLtMatrixLayoutDestroy(p.lc);
+    if (p.op) (void)hipblasLtMatmulDescDestroy(p.op);
+    p = Blas::Plan{};
+}
+
+// The plan of a shape: descriptors, then the algorithm: the process's earlier
+// choice for this shape, or the fastest of hipBLASLt's candidates timed here
+// on the call's own operands (each run overwrites y; the call's real run
+// follows).
+int make_plan(Blas* b, hipStream_t s, float* y, const __bf16* w6, const __bf16* x6, const Shape& key,
+              Blas::Plan& p) {
+    const int rows = std::get<0>(key), cols = std::get<1>(key), batch = std::get<2>(key);
+    const int64_t m = rows, n = batch, k = 6 * int64_t(cols);
+    const hipblasOperation_t ta = HIPBLAS_OP_T, tb = HIPBLAS_OP_N;
+    bool ok = hipblasLtMatmulDescCreate(&p.op, HIPBLAS_COMPUTE_32F, HIP_R_32F) == HIPBLAS_STATUS_SUCCESS &&
+              hipblasLtMatmulDescSetAttribute(p.op, HIPBLASLT_MATMUL_DESC_TRANSA, &ta, sizeof(ta)) ==
+                  HIPBLAS_STATUS_SUCCESS &&
+              hipblasLtMatmulDescSetAttribute(p.op, HIPBLASLT_MATMUL_DESC_TRANSB, &tb, sizeof(tb)) ==
+                  HIPBLAS_STATUS_SUCCESS &&
+              hipblasLtMatrixLayoutCreate(&p.la, HIP_R_16BF, k, m, k) == HIPBLAS_STATUS_SUCCESS &&
+              hipblasLtMatrixLayoutCreate(&p.lb, HIP_R_16BF, k, n, k) == HIPBLAS_STATUS_SUCCESS &&
+              hipblasLtMatrixLayoutCreate(&p.lc, HIP_R_32F, m, n, m) == HIPBLAS_STATUS_SUCCESS;
+    hipblasLtMatmulPreference_t pref = nullptr;
+    ok = ok && hipblasLtMatmulPreferenceCreate(&pref) == HIPBLAS_STATUS_SUCCESS;
+    size_t ws = kWorkspace;
+    ok = ok && hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &ws,
+                                                     sizeof(ws)) == HIPBLAS_STATUS_SUCCESS;
+    hipblasLtMatmulHeuristicResult_t res[kCandidates];
+    int got = 0;
+    ok = ok && hipblasLtMatmulAlgoGetHeuristic(b->handle, p.op, p.la, p.lb, p.lc, p.lc, pref, kCandidates, res,
+                                               &got) == HIPBLAS_STATUS_SUCCESS &&
+         got > 0;
+    if (pref) (void)hipblasLtMatmulPreferenceDestroy(pref);
+    if (!ok) {
+        destroy_plan(p);
+        return int(hipErrorNotSupported);
+    }
+    int choice = -1;
+    {
+        std::lock_guard<std::mutex> lock(g_choice_mu);
+        auto it = g_choice.find(key);
+        if (it != g_choice.end() && it->second < got) choice = it->second;
+    }
+    if (choice < 0 && batch < kTimedBatch) choice = 0;
+    if (choice < 0) {
+        const float alpha = 1.f, beta = 0.f;
+        hipEvent_t e0 = nullptr, e1 = nullptr;
+        if (hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess) {
+            if (e0) (void)hipEventDestroy(e0);
+            destroy_plan(p);
+            return int(hipErrorOutOfMemory);
+        }
+        float best = 0.f;
+        for (int i = 0; i < got && i < kTimed; ++i) {
+            auto run = [&] {
+                return hipblasLtMatmul(b->handle, p.op, &alpha, w6, p.la, x6, p.lb, &beta, y, p.lc, y, p.lc,
+                                       &res[i].algo, b->ws, kWorkspace, s) == HIPBLAS_STATUS_SUCCESS;
+            };
+            if (!run()) continue;  // warm-up; a candidate that fails is skipped
+            bool timed = hipEventRecord(e0, s) == hipSuccess;
+            for (int r = 0; r < 2 && timed; ++r) timed = run();
+            timed = timed && hipEventRecord(e1, s) == hipSuccess && hipEventSynchronize(e1) == hipSuccess;
+            float ms = 0.f;
+            if (timed && hipEventElapsedTime(&ms, e0, e1) == hipSuccess && (choice < 0 || ms < best)) {
+                choice = i;
+                best = ms;
+            }
+        }
+        (void)hipEventDestroy(e0);
+        (void)hipEventDestroy(e1);
+        if (choice < 0) {
+            destroy_plan(p);
+            return int(hipErrorNotSupported);
+        }
+        std::lock_guard<std::mutex> lock(g_choice_mu);
+        choice = g_choice.emplace(key, choice).first->second;  // another context may have chosen meanwhile
+        if (choice >= got) choice = 0;
+    }
+    p.algo = res[choice].algo;
+    return 0;
+}
+
+}  // namespace
+
+int blas_create(Blas** out) {
+    *out = nullptr;
+    Blas* b = new (std::nothrow) Blas;
+    if (!b) return int(hipErrorOutOfMemory);
+    if (hipblasLtCreate(&b->handle) != HIPBLAS_STATUS_SUCCESS) {
+        delete b;
+        return int(hipErrorNotInitialized);
+    }
+    const hipError_t e = hipMalloc(&b->ws, kWorkspace);
+    if (e != hipSuccess) {
+        (void)hipblasLtDestroy(b->handle);
+        delete b;
+        return int(e);
+    }
+    *out = b;
+    return 0;
+}
+
+void blas_destroy(Blas* b) {
+    if (!b) return;
+    for (auto& kv : b->plans) destroy_plan(kv.second);
+    if (b->ws) (void)hipFree(b->ws);
+    if (b->handle) (void)hipblasLtDestroy(b->handle);
+    delete b;
+}
+
+int blas_gemm6(Blas* b, hipStream_t s, float* y, const __bf16* w6, const __bf16* x6, int rows, int cols, int batch) {
+    if (!b || rows < 1 || cols < 1 || batch < 1) return int(hipErrorInvalidValue);
+    const Shape key{rows, cols, batch};
+    auto it = b->plans.find(key);
+    if (it == b->plans.end()) {
+        Blas::Plan p;
+        if (int st = make_plan(b, s, y, w6, x6, key, p)) return st;
+        it = b->plans.emplace(key, p).first;
+    }
+    const Blas::Plan& p = it->second;
+    const float alpha = 1.f, beta = 0.f;
+    return hipblasLtMatmul(b->handle, p.op, &alpha, w6, p.la, x6, p.lb, &beta, y, p.lc, y, p.lc, &p.algo, b->ws,
+                           kWorkspace, s) == HIPBLAS_STATUS_SUCCESS
+               ? 0
+               : int(hipErrorLaunchFailure);
+}
+
+}  // namespace qr

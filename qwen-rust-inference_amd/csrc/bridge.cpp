@@ -27,6 +27,17 @@ struct Context {
     size_t rule_chunks_len = 0;
     float* gemm_work = nullptr;  // K-split partial sums of prefill GEMMs
     size_t gemm_work_len = 0;
+    // Prepared fp32 matrices (qr_gemm_f32_prepare): the K'-concatenated BF16
+    // planes of each, by the matrix's device address, for the hipBLASLt path
+    // of prefill projections; dropped when the matrix is freed or written.
+    struct Prepared {
+        int rows, cols;
+        __bf16* w6;
+    };
+    std::map<const float*, Prepared> prepared;
+    qr::Blas* blas = nullptr;
+    __bf16* x6 = nullptr;  // the split planes of a projection's input
+    size_t x6_len = 0;     // in BF16 elements
     // RoPE denominators theta^(2i / rot) per (theta bits, rot), device copies.
     std::map<std::pair<uint32_t, int>, float*> rope;
     // Profiler (qr_profile / QWEN_ROCM_PROFILE=1): a hipEvent pair on the
@@ -128,6 +139,55 @@ int ensure(Context* c, float** buf, size_t* len, size_t need, const char* what) 
 
 const void* i8_packed(const float* packed) { return packed; }
 
+// ---- prepared fp32 matrices on hipBLASLt (csrc/blas.cpp)
+// Projections of at least this many tokens take the hipBLASLt path when their
+// matrix is prepared (fewer tokens: the split-BF16 kernel, whose tiles the
+// small batches fill as well).
+constexpr int kBlasMinBatch = 64;
+
+const Context::Prepared* prepared_for(Context* c, const void* a, int rows, int cols, int batch) {
+    if (batch < kBlasMinBatch || rows <= 16) return nullptr;
+    auto it = c->prepared.find(static_cast<const float*>(a));
+    if (it == c->prepared.end() || it->second.rows != rows || it->second.cols != cols) return nullptr;
+    return &it->second;
+}
+// x's split planes into c->x6 (grown as needed).
+int split_input(Context* c, const float* x, int cols, int batch) {
+    const size_t need = size_t(batch) * 6 * size_t(cols);
+    if (need > c->x6_len) {
+        if (c->x6) {
+            (void)hipStreamSynchronize(c->stream);
+            (void)hipFree(c->x6);
+            c->x6 = nullptr;
+            c->x6_len = 0;
+        }
+        auto st = hipMalloc(reinterpret_cast<void**>(&c->x6), need * sizeof(__bf16));
+        if (st != hipSuccess) return fail(c, "hipMalloc split input", int(st));
+        c->x6_len = need;
+    }
+    auto s = scope(c, [&] { return std::string("split6 ") + shape(batch, cols, 1); });
+    return launched(c, "split6", qr::split6(c->stream, c->x6, x, batch, cols, false));
+}
+int blas_project(Context* c, float* y, const Context::Prepared& p, int batch) {
+    auto s = scope(c, [&] { return std::string("gemm_f32_blas ") + shape(p.rows, p.cols, batch); });
+    return launched(c, "hipBLASLt GEMM", qr::blas_gemm6(c->blas, c->stream, y, p.w6, c->x6, p.rows, p.cols, batch));
+}
+void drop_prepared(Context* c, std::map<const float*, Context::Prepared>::iterator it) {
+    (void)hipStreamSynchronize(c->stream);  // queued GEMMs may still read the planes
+    (void)hipFree(it->second.w6);
+    c->prepared.erase(it);
+}
+// Drops the planes of every prepared matrix that [p, p + n) overlaps.
+void invalidate_prepared(Context* c, const float* p, size_t n) {
+    for (auto it = c->prepared.begin(); it != c->prepared.end();) {
+        const float* a = it->first;
+        const size_t len = size_t(it->second.rows) * size_t(it->second.cols);
+        auto next = std::next(it);
+        if (p < a + len && a < p + n) drop_prepared(c, it);
+        it = next;
+    }
+}
+
 // The RoPE denominators of (theta, rot): powf(theta, float(2i) / float(rot)),
 // the expression of the reference's rotate (src/attention.rs:49-50 and
 // reference.h:41-47), evaluated by the host libm once per pair.
@@ -155,6 +215,12 @@ int rope_table(Context* c, float theta, int rot, const float** out) {
 
 int project(Context* c, qr::WeightType t, float* y, const void* a, const float* x, int rows, int cols, int batch) {
     if (rows < 1 || cols < 1 || batch < 1) return fail(c, "projection shape", -1);
+    if (t == qr::WeightType::F32) {
+        if (const Context::Prepared* p = prepared_for(c, a, rows, cols, batch)) {
+            if (int st = split_input(c, x, cols, batch)) return st;
+            return blas_project(c, y, *p, batch);
+        }
+    }
     if (!qr::gemm_preferred(t, rows, cols, batch)) {
         auto s = scope(c, [&] { return std::string("gemv_") + wname(t) + " " + shape(rows, cols, batch); });
         qr::GemvItem it{y, a, rows};
@@ -172,7 +238,18 @@ int group(Context* c, qr::WeightType t, int n, const QrProjection* items, const 
     for (int i = 0; i < n; ++i)
         if (items[i].rows < 1) return fail(c, "GEMM group shape", -1);
     if (qr::gemm_preferred(t, items[0].rows, cols, batch)) {
+        bool split = false;  // x's planes, made at the group's first prepared matrix
         for (int i = 0; i < n; ++i) {
+            if (t == qr::WeightType::F32) {
+                if (const Context::Prepared* p = prepared_for(c, items[i].a, items[i].rows, cols, batch)) {
+                    if (!split) {
+                        if (int st = split_input(c, x, cols, batch)) return st;
+                        split = true;
+                    }
+                    if (int st = blas_project(c, items[i].y, *p, batch)) return st;
+                    continue;
+                }
+            }
             // two consecutive few-row fp32 matrices (the DeltaNet a / b) in one launch
             if (i + 1 < n && qr::gemm_ab_ok(t, items[i].a, x, items[i].rows, cols, batch) &&
                 qr::gemm_ab_ok(t, items[i + 1].a, x, items[i + 1].rows, cols, batch)) {
@@ -210,6 +287,21 @@ int glu(Context* c, qr::WeightType t, float* product, float* gate_y, float* up_y
     if (!qr::gemm_preferred(t, rows, cols, batch)) {
         auto s = scope(c, [&] { return std::string("gemv_") + wname(t) + "_glu 2x" + shape(rows, cols, batch); });
         return launched(c, "gemv_glu", qr::gemv_glu(c->stream, t, product, gate, up, x, rows, cols, batch));
+    }
+    if (t == qr::WeightType::F32) {
+        const Context::Prepared* pg = prepared_for(c, gate, rows, cols, batch);
+        const Context::Prepared* pu = prepared_for(c, up, rows, cols, batch);
+        if (pg && pu) {  // gate and up on hipBLASLt into gate_y / up_y, then silu(gate_y) * up_y
+            if (int st = split_input(c, x, cols, batch)) return st;
+            if (int st = blas_project(c, gate_y, *pg, batch)) return st;
+            if (int st = blas_project(c, up_y, *pu, batch)) return st;
+            Params p{};
+            p.p[0] = product;
+            p.p[1] = gate_y;
+            p.p[2] = up_y;
+            auto s = scope(c, [&] { return std::string("silu_product ") + shape(rows, batch, 1); });
+            return launched(c, "silu_product", qr::run_elementwise(c->stream, QR_SILU_PRODUCT, rows * batch, p));
+        }
     }
     if (qr::gemm_glu_fused(t, gate, up, x, rows, cols, batch)) {  // gate_y / up_y untouched, as the reference's fused GLU
         auto s = scope(c, [&] { return std::string("gemm_") + wname(t) + "_glu 2x" + shape(rows, cols, batch); });
@@ -374,6 +466,9 @@ void qr_destroy(Context* c) {
     if (c->attn_parts) (void)hipFree(c->attn_parts);
     if (c->rule_chunks) (void)hipFree(c->rule_chunks);
     if (c->gemm_work) (void)hipFree(c->gemm_work);
+    for (auto& kv : c->prepared) (void)hipFree(kv.second.w6);
+    if (c->x6) (void)hipFree(c->x6);
+    qr::blas_destroy(c->blas);
     (void)hipStreamDestroy(c->stream);
     delete c;
 }
@@ -392,11 +487,12 @@ int qr_alloc(Context* c, float** p, size_t n) {
 }
 
 void qr_free(Context* c, float* p) {
-    (void)c;
+    if (!c->prepared.empty()) invalidate_prepared(c, p, 1);
     (void)hipFree(p);
 }
 
 int qr_write(Context* c, float* p, const float* host, size_t n) {
+    if (!c->prepared.empty()) invalidate_prepared(c, p, n);
     auto s = hipMemcpyAsync(p, host, n * sizeof(float), hipMemcpyHostToDevice, c->stream);
     if (s != hipSuccess) return fail(c, "H2D", int(s));
     return qr_sync(c);  // the host slice may be gone after return
@@ -409,6 +505,7 @@ int qr_read(Context* c, float* host, const float* p, size_t n) {
 }
 
 int qr_copy(Context* c, float* dest, const float* src, size_t n) {
+    if (!c->prepared.empty()) invalidate_prepared(c, dest, n);
     auto sc = scope(c, [&] { return std::string("copy"); });
     auto s = hipMemcpyAsync(dest, src, n * sizeof(float), hipMemcpyDeviceToDevice, c->stream);
     return s == hipSuccess ? 0 : fail(c, "D2D", int(s));
@@ -494,6 +591,31 @@ int qr_gemm_i8_group(Context* c, int n, const QrProjection* items, const float* 
 int qr_gemm_f32_glu(Context* c, float* product, float* gate_y, float* up_y, const float* gate, const float* up,
                     const float* x, int rows, int cols, int batch) {
     return glu(c, qr::WeightType::F32, product, gate_y, up_y, gate, up, x, rows, cols, batch);
+}
+int qr_gemm_f32_prepare(Context* c, const float* a, int rows, int cols) {
+    if (!a || rows < 1 || cols < 4 || cols % 4 != 0 || reinterpret_cast<uintptr_t>(a) % 16 != 0)
+        return fail(c, "GEMM prepare shape", -1);
+    auto it = c->prepared.find(a);
+    if (it != c->prepared.end()) {
+        if (it->second.rows == rows && it->second.cols == cols) return 0;
+        drop_prepared(c, it);
+    }
+    if (!c->blas)
+        if (int st = qr::blas_create(&c->blas)) return fail(c, "hipBLASLt context", st);
+    __bf16* w6 = nullptr;
+    auto st = hipMalloc(reinterpret_cast<void**>(&w6), size_t(rows) * 6 * size_t(cols) * sizeof(__bf16));
+    if (st != hipSuccess) return fail(c, "hipMalloc GEMM planes", int(st));
+    if (int e = qr::split6(c->stream, w6, a, rows, cols, true)) {
+        (void)hipFree(w6);
+        return fail(c, "split6", e);
+    }
+    c->prepared[a] = Context::Prepared{rows, cols, w6};
+    return 0;
+}
+int qr_gemm_f32_release(Context* c, const float* a) {
+    auto it = c->prepared.find(a);
+    if (it != c->prepared.end()) drop_prepared(c, it);
+    return 0;
 }
 int qr_gemm_bf16_glu(Context* c, float* product, float* gate_y, float* up_y, const float* gate, const float* up,
                      const float* x, int rows, int cols, int batch) {

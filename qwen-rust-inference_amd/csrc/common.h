@@ -84,6 +84,18 @@ int gemm(hipStream_t s, WeightType t, float* y, const void* a, const float* x, i
          float* work, size_t work_len);
 size_t gemm_scratch(WeightType t, int rows, int cols, int batch);
 bool gemm_preferred(WeightType t, int rows, int cols, int batch);
+// [rows, cols] fp32 -> [rows, 6 cols] BF16: the three-way split planes of
+// every row laid out for one BF16 GEMM with K' = 6 K (weight: the W order
+// [w0 w1 w2 w0 w1 w0], else the X order [x2 x1 x0 x1 x0 x0]); cols % 4 == 0.
+int split6(hipStream_t s, __bf16* out, const float* in, int rows, int cols, bool weight);
+// Y[batch, rows] = X6 W6^T on hipBLASLt (BF16 inputs, fp32 accumulation and
+// output) for K'-concatenated planes of split6: the fp32 product X W^T to
+// fp32 accuracy. One Blas per bridge context; the algorithm of each shape is
+// chosen once per process by timing hipBLASLt's candidates.
+struct Blas;
+int blas_create(Blas** out);
+void blas_destroy(Blas* b);
+int blas_gemm6(Blas* b, hipStream_t s, float* y, const __bf16* w6, const __bf16* x6, int rows, int cols, int batch);
 // Y1 = X A1^T and (rows2 > 0) Y2 = X A2^T in one launch for fp32 matrices of
 // at most 16 rows and 1024 columns (the DeltaNet a / b projections of
 // prefill), when gemm_ab_ok holds for each.

@@ -405,6 +405,50 @@ __global__ __launch_bounds__(512) void gemm_ab_kernel(AbMats m, const float* x, 
     }
 }
 
+// The K'-concatenated BF16 planes of an fp32 matrix for one BF16 GEMM with
+// K' = 6 K whose products are the six part products of the three-way split:
+// row r of a matrix becomes [x2 | x1 | x0 | x1 | x0 | x0] (the activations X)
+// or [w0 | w1 | w2 | w0 | w1 | w0] (the weights W), so block b of K' pairs
+// x_{P[b]} with w_{Q[b]} for (P, Q) = (2,0) (1,1) (0,2) (1,0) (0,1) (0,0);
+// every BF16 x BF16 product is exact in fp32. Block: one row; thread: 8
+// consecutive values per step with 16-byte stores per plane when cols % 8 ==
+// 0 (every plane then starts 16-byte aligned), else 4 values with 8-byte
+// stores (cols % 4 == 0); each plane's stores coalesced.
+__device__ __forceinline__ void split3_4(f4v v, bf16x4 (&h)[3]) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        h[0][e] = __bf16(v[e]);
+        const float r1 = v[e] - float(h[0][e]);
+        h[1][e] = __bf16(r1);
+        h[2][e] = __bf16(r1 - float(h[1][e]));
+    }
+}
+__global__ __launch_bounds__(256) void split6_kernel(__bf16* out, const float* in, int cols, int weight) {
+    constexpr int XP[6] = {2, 1, 0, 1, 0, 0}, WQ[6] = {0, 1, 2, 0, 1, 0};
+    const float* src = in + size_t(blockIdx.x) * cols;
+    __bf16* row = out + size_t(blockIdx.x) * 6 * cols;
+    if (cols % 8 == 0) {
+        for (int k = 8 * int(threadIdx.x); k < cols; k += 8 * 256) {
+            bf16x4 lo[3], hi[3];
+            split3_4(*reinterpret_cast<const f4v*>(src + k), lo);
+            split3_4(*reinterpret_cast<const f4v*>(src + k + 4), hi);
+#pragma unroll
+            for (int b = 0; b < 6; ++b) {
+                const int p = weight ? WQ[b] : XP[b];
+                *reinterpret_cast<bf16x8*>(row + size_t(b) * cols + k) =
+                    __builtin_shufflevector(lo[p], hi[p], 0, 1, 2, 3, 4, 5, 6, 7);
+            }
+        }
+    } else {
+        for (int k = 4 * int(threadIdx.x); k < cols; k += 4 * 256) {
+            bf16x4 h[3];
+            split3_4(*reinterpret_cast<const f4v*>(src + k), h);
+#pragma unroll
+            for (int b = 0; b < 6; ++b) *reinterpret_cast<bf16x4*>(row + size_t(b) * cols + k) = h[weight ? WQ[b] : XP[b]];
+        }
+    }
+}
+
 }  // namespace
 
 bool gemm_preferred(WeightType, int, int, int batch) { return batch > 4; }
@@ -421,6 +465,14 @@ size_t gemm_scratch(WeightType t, int rows, int cols, int batch) {
     int kchunk;
     const int splits = mfma_splits(rows, cols, batch, kchunk);
     return splits > 1 ? size_t(splits) * size_t(rows) * size_t(batch) : 0;
+}
+
+int split6(hipStream_t s, __bf16* out, const float* in, int rows, int cols, bool weight) {
+    if (rows < 1 || cols < 4 || cols % 4 != 0 || reinterpret_cast<uintptr_t>(in) % 16 != 0 ||
+        reinterpret_cast<uintptr_t>(out) % 16 != 0)
+        return int(hipErrorInvalidValue);
+    hipLaunchKernelGGL(split6_kernel, dim3(unsigned(rows)), dim3(256), 0, s, out, in, cols, weight ? 1 : 0);
+    return int(hipGetLastError());
 }
 
 bool gemm_ab_ok(WeightType t, const void* a, const float* x, int rows, int cols, int batch) {

@@ -156,6 +156,13 @@ class Bridge:
         self._check(fn(self.ctx, ctypes.c_void_p(y.ptr), ctypes.c_void_p(a.ptr), ctypes.c_void_p(x.ptr), rows, cols,
                        batch))
 
+    def prepare(self, a: Buffer, rows: int, cols: int):
+        """qr_gemm_f32_prepare: keep a's split planes for the hipBLASLt prefill path."""
+        self._check(self.L.qr_gemm_f32_prepare(self.ctx, ctypes.c_void_p(a.ptr), rows, cols))
+
+    def release(self, a: Buffer):
+        self._check(self.L.qr_gemm_f32_release(self.ctx, ctypes.c_void_p(a.ptr)))
+
     def gemv(self, y: Buffer, a: Buffer, x: Buffer, rows: int, cols: int, kind: str = "f32"):
         fn = {"f32": self.L.qr_gemv, "bf16": self.L.qr_gemv_bf16}[kind]
         self._check(fn(self.ctx, ctypes.c_void_p(y.ptr), ctypes.c_void_p(a.ptr), ctypes.c_void_p(x.ptr), rows, cols))

@@ -28,6 +28,7 @@ F32, BF16_EXACT, INT8 = 0, 1, 2
 NO_F32_FUSIONS, NO_FUSIONS, NO_DELTA_MIXER, NO_FUSED_OPS, NO_ARGMAX, NO_SNAPSHOTS = 1, 2, 4, 8, 16, 32
 NO_DECODE_STEP = 64
 NO_EMBED_ROWS = 128
+NO_BLAS_GEMM = 256
 
 # Every entry point of include/qwen_bridge.h.
 BRIDGE_SYMBOLS = [
@@ -37,7 +38,7 @@ BRIDGE_SYMBOLS = [
     "qr_gemm_bf16_glu", "qr_gemm_i8_glu", "qr_gemm_bf16_add_norm", "qr_gemm_i8_add_norm", "qr_delta_mixer",
     "qr_gemm_f32_group", "qr_gemm_f32_glu", "qr_gemm_f32_add_norm", "qr_profile", "qr_profile_read",
     "qr_decode_plan", "qr_decode_step", "qr_decode_steps", "qr_decode_step_row", "qr_decode_plan_free",
-    "qr_embed_rows", "qr_argmax_fixed",
+    "qr_embed_rows", "qr_argmax_fixed", "qr_gemm_f32_prepare", "qr_gemm_f32_release",
 ]
 
 _F = ctypes.POINTER(ctypes.c_float)

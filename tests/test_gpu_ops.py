@@ -155,6 +155,81 @@ def test_group_glu_equal_separate_calls(gpu, kind, batch):
     parity(prod.read(), want, where="glu")
 
 
+@pytest.mark.parametrize("rows,cols,batch", [(6144, 1024, 2644), (1024, 2048, 130), (1024, 3584, 64), (512, 1024, 454),
+                                            (4096, 1024, 10240), (40, 12, 65), (2048, 1024, 63)])
+def test_gemm_f32_prepared(gpu, rows, cols, batch):
+    """qr_gemm_f32_prepare: the projection of a prepared matrix (one BF16 GEMM
+    with K' = 6 cols on hipBLASLt from 64 tokens, the split-BF16 kernel below)
+    against fp64 with the fp32 dot-product bound on sampled rows, twice
+    bitwise-equal (the algorithm of a shape is fixed), and within the bound of
+    the unprepared kernel's result."""
+    print(f"gemm f32 prepared {rows}x{cols} batch {batch}", flush=True)
+    rng = np.random.default_rng(rows + 3 * cols + batch)
+    w = (rng.standard_normal(rows * cols) * 0.02).astype(np.float32)
+    x = rng.standard_normal(batch * cols).astype(np.float32)
+    a, xb = gpu.upload(w), gpu.upload(x)
+    plain, y1, y2 = gpu.alloc(batch * rows), gpu.alloc(batch * rows), gpu.alloc(batch * rows)
+    gpu.gemm(plain, a, xb, rows, cols, batch)
+    gpu.prepare(a, rows, cols)
+    gpu.gemm(y1, a, xb, rows, cols, batch)
+    gpu.gemm(y2, a, xb, rows, cols, batch)
+    got = y1.read().reshape(batch, rows)
+    assert np.array_equal(got, y2.read().reshape(batch, rows))
+    idx = np.unique(np.random.default_rng(0).integers(0, batch, 64))
+    X, W = x.reshape(batch, cols)[idx].astype(np.float64), w.reshape(rows, cols).astype(np.float64)
+    want = X @ W.T
+    bound = np.abs(X) @ np.abs(W.T) * 2e-5 + 1e-30
+    assert np.all(np.abs(got[idx] - want) <= bound), np.max(np.abs(got[idx] - want) / bound)
+    other = plain.read().reshape(batch, rows)[idx]
+    assert np.all(np.abs(got[idx] - other) <= 2 * bound)
+
+
+def test_prepared_group_glu_and_invalidation(gpu):
+    """Prepared matrices in a group (x split once) and a GLU (gate_y / up_y
+    written, then silu(gate) * up) equal the separate prepared projections
+    bitwise; a qr_write into a prepared matrix drops its planes, so the next
+    projection follows the new values; release and free are accepted."""
+    rng = np.random.default_rng(5)
+    cols, batch = 1024, 300
+    shapes = [6144, 2048, 16, 16]
+    ws = [(rng.standard_normal(r * cols) * 0.02).astype(np.float32) for r in shapes]
+    mats = [gpu.upload(w) for w in ws]
+    for m, r in zip(mats, shapes):
+        if r > 16:
+            gpu.prepare(m, r, cols)
+    x = gpu.upload(rng.standard_normal(batch * cols).astype(np.float32))
+    ys = [gpu.alloc(batch * r) for r in shapes]
+    gpu.group(list(zip(ys, mats, shapes)), x, cols, batch)
+    for y, m, r in zip(ys, mats, shapes):
+        one = gpu.alloc(batch * r)
+        gpu.gemm(one, m, x, r, cols, batch)
+        assert np.array_equal(y.read(), one.read()), r
+    rows = 3584
+    gw, uw = [(rng.standard_normal(rows * cols) * 0.02).astype(np.float32) for _ in range(2)]
+    g, u = gpu.upload(gw), gpu.upload(uw)
+    gpu.prepare(g, rows, cols)
+    gpu.prepare(u, rows, cols)
+    prod, gy, uy = gpu.alloc(batch * rows), gpu.alloc(batch * rows), gpu.alloc(batch * rows)
+    gpu.glu(prod, gy, uy, g, u, x, rows, cols, batch)
+    g1, u1 = gpu.alloc(batch * rows), gpu.alloc(batch * rows)
+    gpu.gemm(g1, g, x, rows, cols, batch)
+    gpu.gemm(u1, u, x, rows, cols, batch)
+    assert np.array_equal(gy.read(), g1.read()) and np.array_equal(uy.read(), u1.read())
+    gv, uv = g1.read().astype(np.float64), u1.read().astype(np.float64)
+    parity(prod.read(), gv / (1 + np.exp(-gv)) * uv, where="prepared glu")
+    # rewrite the first matrix: its planes are dropped, the projection follows the new weights
+    new = (rng.standard_normal(shapes[0] * cols) * 0.02).astype(np.float32)
+    mats[0].write(new)
+    y = gpu.alloc(batch * shapes[0])
+    gpu.gemm(y, mats[0], x, shapes[0], cols, batch)
+    X = x.read().reshape(batch, cols)[:16].astype(np.float64)
+    W = new.reshape(shapes[0], cols).astype(np.float64)
+    bound = np.abs(X) @ np.abs(W.T) * 2e-5 + 1e-30
+    assert np.all(np.abs(y.read().reshape(batch, shapes[0])[:16] - X @ W.T) <= bound)
+    gpu.release(mats[1])
+    gpu.release(mats[1])  # releasing twice (or an unprepared matrix) is accepted
+
+
 @pytest.mark.parametrize("kind", ["f32", "bf16", "i8"])
 @pytest.mark.parametrize("rows,cols", [(1024, 2048), (1024, 3584), (64, 256), (8, 16)])
 def test_add_norm_tail(gpu, cpu, kind, rows, cols):
