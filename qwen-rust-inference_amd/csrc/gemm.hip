@@ -423,12 +423,13 @@ __device__ __forceinline__ void split3_4(f4v v, bf16x4 (&h)[3]) {
         h[2][e] = __bf16(r1 - float(h[1][e]));
     }
 }
-__global__ __launch_bounds__(256) void split6_kernel(__bf16* out, const float* in, int cols, int weight) {
+constexpr int SPLIT6_THREADS = 128;  // a 1024-column row: one pass of 8 values per thread
+__global__ __launch_bounds__(SPLIT6_THREADS) void split6_kernel(__bf16* out, const float* in, int cols, int weight) {
     constexpr int XP[6] = {2, 1, 0, 1, 0, 0}, WQ[6] = {0, 1, 2, 0, 1, 0};
     const float* src = in + size_t(blockIdx.x) * cols;
     __bf16* row = out + size_t(blockIdx.x) * 6 * cols;
     if (cols % 8 == 0) {
-        for (int k = 8 * int(threadIdx.x); k < cols; k += 8 * 256) {
+        for (int k = 8 * int(threadIdx.x); k < cols; k += 8 * SPLIT6_THREADS) {
             bf16x4 lo[3], hi[3];
             split3_4(*reinterpret_cast<const f4v*>(src + k), lo);
             split3_4(*reinterpret_cast<const f4v*>(src + k + 4), hi);
@@ -440,7 +441,7 @@ __global__ __launch_bounds__(256) void split6_kernel(__bf16* out, const float* i
             }
         }
     } else {
-        for (int k = 4 * int(threadIdx.x); k < cols; k += 4 * 256) {
+        for (int k = 4 * int(threadIdx.x); k < cols; k += 4 * SPLIT6_THREADS) {
             bf16x4 h[3];
             split3_4(*reinterpret_cast<const f4v*>(src + k), h);
 #pragma unroll
@@ -471,7 +472,7 @@ int split6(hipStream_t s, __bf16* out, const float* in, int rows, int cols, bool
     if (rows < 1 || cols < 4 || cols % 4 != 0 || reinterpret_cast<uintptr_t>(in) % 16 != 0 ||
         reinterpret_cast<uintptr_t>(out) % 16 != 0)
         return int(hipErrorInvalidValue);
-    hipLaunchKernelGGL(split6_kernel, dim3(unsigned(rows)), dim3(256), 0, s, out, in, cols, weight ? 1 : 0);
+    hipLaunchKernelGGL(split6_kernel, dim3(unsigned(rows)), dim3(SPLIT6_THREADS), 0, s, out, in, cols, weight ? 1 : 0);
     return int(hipGetLastError());
 }
 
