@@ -25,7 +25,9 @@ struct ReadArgs {
     const float* values;
     const float* gate;
     float* parts;  // [rows][heads][splits][d + 2] when splits > 1
-    int d, heads, kv, length0, rows, span, splits;
+    char* kpl;     // attention_prefill_bf3_kernel: K planes, [kv][tiles] blocks of B3_KBLK bytes
+    char* vpl;     // ... and V^T planes, [kv][tiles] blocks of B3_VBLK bytes
+    int d, heads, kv, length0, rows, span, splits, tiles;
 };
 
 template <int D, int G>
@@ -376,15 +378,26 @@ __global__ __launch_bounds__(64 * G) void attention_prefill_kernel(ReadArgs a) {
 // operand of step s is registers 8 s .. 8 s + 7; V^T keeps its key positions
 // in that order (bits 2 and 3 of the key swapped), so no value crosses
 // lanes.
-// One K/V tile in LDS (K 3 x 32 x 264 and V^T 3 x 256 x 40 BF16, 110 KB; rows
-// padded so the 16-byte operand reads of 8 consecutive lanes hit distinct
-// banks) plus the 32 KB score exchange: the next tile's K values are loaded
-// into registers during the current tile's products (its V values when it is
-// staged: both would not fit the 256 registers of a wave at two waves per
-// SIMD) and split into LDS between two barriers.
+// The three BF16 planes of K and of V^T are made once per call, before the
+// attention kernel, by kv_planes_kernel (every block re-splitting its KV
+// head's rows would repeat the split n / 32 times), in exactly the LDS layout
+// of one tile: K 3 x 32 x 264 (rows padded so the 16-byte operand reads of 8
+// consecutive lanes hit distinct banks) and V^T 3 x 256 x 40 with its key
+// positions in the score accumulator's order (below), each tile block padded
+// to whole 8 KiB rounds of 16-byte LDS DMA (56 and 64 KiB). The attention
+// kernel stages a tile by LDS DMA (global_load_lds_dwordx4: 64 lanes x 16 B
+// straight into LDS, no registers): each of the 8 waves issues 7 K and 8 V
+// instructions. K of tile t + 1 is loaded while tile t's softmax and PV
+// product run (K is not read after the score product), and V of tile t + 1
+// while tile t + 1's score product runs (V is not read before the PV
+// product), so one K buffer and one V buffer suffice (56 + 64 + 32 KiB score
+// exchange = 152 KiB) and the barriers wait for LDS only, never for loads in
+// flight.
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 constexpr int B3_KROW = 256 + 8, B3_VROW = 40;
+constexpr int B3_KBLK = 56 * 1024, B3_VBLK = 64 * 1024;  // bytes per tile (3 x 32 x 264 and 3 x 256 x 40 BF16, padded)
+constexpr int B3_KDMA = B3_KBLK / 8192, B3_VDMA = B3_VBLK / 8192;  // DMA instructions per wave per tile
 
 struct Split3 {
     __bf16 h[3];
@@ -400,15 +413,117 @@ __device__ __forceinline__ Split3 split3(float x) {
 // the V^T position of tile key k: bits 2 and 3 swapped
 __device__ __forceinline__ int vpos(int k) { return (k & ~12) | ((k & 4) << 1) | ((k & 8) >> 1); }
 
+// One block per (tile of 32 positions, KV head): K and V rows of positions
+// [32 t, 32 t + 32) split into their planes; positions at or past `len` (no
+// query sees them) and the padding are zero.
+__global__ __launch_bounds__(256) void kv_planes_kernel(ReadArgs a, int len) {
+    constexpr int D = 256;
+    const int t = int(blockIdx.x), kvh = int(blockIdx.y), tid = int(threadIdx.x);
+    const size_t rowstride = size_t(a.kv) * D, blk = size_t(kvh) * a.tiles + t;
+    __bf16* kb = reinterpret_cast<__bf16*>(a.kpl + blk * B3_KBLK);
+    __bf16* vb = reinterpret_cast<__bf16*>(a.vpl + blk * B3_VBLK);
+    const f4v z = {0.f, 0.f, 0.f, 0.f};
+    f4v kv[8], vv[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {  // K: key f / 64, dims 4 (f % 64)
+        const int f = tid + 256 * i, pos = 32 * t + (f >> 6), c = (f & 63) * 4;
+        kv[i] = pos < len ? *reinterpret_cast<const f4v*>(a.keys + size_t(pos) * rowstride + size_t(kvh) * D + c) : z;
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {  // V: key quad b % 8, dim quad b / 8
+        const int b = tid + 256 * i, kq = b & 7, cq = b >> 3;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int pos = 32 * t + 4 * kq + r;
+            vv[4 * i + r] = pos < len ? *reinterpret_cast<const f4v*>(a.values + size_t(pos) * rowstride +
+                                                                      size_t(kvh) * D + 4 * cq)
+                                      : z;
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int f = tid + 256 * i, key = f >> 6, c = (f & 63) * 4;
+        bf16x4 h[3];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const Split3 x = split3(kv[i][e]);
+#pragma unroll
+            for (int p = 0; p < 3; ++p) h[p][e] = x.h[p];
+        }
+#pragma unroll
+        for (int p = 0; p < 3; ++p) *reinterpret_cast<bf16x4*>(kb + (p * 32 + key) * B3_KROW + c) = h[p];
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int b = tid + 256 * i, kq = b & 7, cq = b >> 3, p0 = vpos(4 * kq);
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+            bf16x4 h[3];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const Split3 x = split3(vv[4 * i + r][d]);
+#pragma unroll
+                for (int p = 0; p < 3; ++p) h[p][r] = x.h[p];
+            }
+#pragma unroll
+            for (int p = 0; p < 3; ++p) *reinterpret_cast<bf16x4*>(vb + (p * D + 4 * cq + d) * B3_VROW + p0) = h[p];
+        }
+    }
+    // padding: K row ends (96 x 16 B) and tail, V^T row ends (768 x 16 B) and tail
+    const bf16x8 zb = {};
+    if (tid < 96) *reinterpret_cast<bf16x8*>(kb + tid * B3_KROW + 256) = zb;
+    for (int e = 3 * 32 * B3_KROW + 8 * tid; e < B3_KBLK / 2; e += 8 * 256) *reinterpret_cast<bf16x8*>(kb + e) = zb;
+    for (int r = tid; r < 3 * D; r += 256) *reinterpret_cast<bf16x8*>(vb + r * B3_VROW + 32) = zb;
+    for (int e = 3 * D * B3_VROW + 8 * tid; e < B3_VBLK / 2; e += 8 * 256) *reinterpret_cast<bf16x8*>(vb + e) = zb;
+}
+
+// LDS barrier that leaves the DMA loads in flight: LDS operations done
+// (lgkmcnt(0)), then s_barrier.
+__device__ __forceinline__ void b3_lds_barrier() {
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0xc07f);
+    __builtin_amdgcn_s_barrier();
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+// Waits until at most N vector memory operations of this wave are in flight
+// (lgkmcnt and expcnt not waited).
+template <int N>
+__device__ __forceinline__ void b3_vm_wait() {
+    static_assert(N >= 0 && N < 64, "vmcnt");
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+// This wave's N DMA instructions of one tile block: 1 KiB each, instruction i
+// of wave w copies bytes 1 KiB (8 i + w) .. + 1023 (M0 = the LDS byte address,
+// lane l's 16 bytes land at M0 + 16 l). Written as inline assembly so that
+// the compiler, which cannot tell which LDS array an LDS DMA writes, does not
+// wait for every one in flight before each LDS read: the kernel orders them
+// itself (b3_vm_wait before the barrier that publishes a tile).
+template <int N>
+__device__ __forceinline__ void b3_dma(const char* src, const void* dst, int w, int lane) {
+    const unsigned lds = unsigned(reinterpret_cast<size_t>((__attribute__((address_space(3))) const char*)dst));
+    const unsigned voff = unsigned(lane) * 16u;
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+        const int c = 8 * i + w;
+        const char* base = src + c * 1024;
+        asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, %2" ::"v"(voff), "s"(lds + unsigned(c) * 1024u),
+                     "s"(base)
+                     : "memory", "m0");
+    }
+}
+
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void attention_prefill_bf3_kernel(
     ReadArgs a) {
     constexpr int D = 256, G = 4, HALF = D / 2, DT = HALF / 32;
-    __shared__ __attribute__((aligned(16))) __bf16 ks[3][32][B3_KROW];
-    __shared__ __attribute__((aligned(16))) __bf16 vt[3][D][B3_VROW];
+    __shared__ __attribute__((aligned(16))) __bf16 ks[B3_KBLK / 2];  // [3][32][B3_KROW] + DMA padding
+    __shared__ __attribute__((aligned(16))) __bf16 vt[B3_VBLK / 2];  // [3][D][B3_VROW] + DMA padding
     __shared__ float xch[8][16][64];
     const int qtiles = (a.rows + 31) / 32;
     const int q0 = (qtiles - 1 - int(blockIdx.x)) * 32, kvh = blockIdx.y;  // longest rows first
-    const int tid = int(threadIdx.x), lane = tid & 63, w = tid >> 6, lc = lane & 31, hl = lane >> 5;
+    const int tid = int(threadIdx.x), lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6), lc = lane & 31,
+              hl = lane >> 5;
     const int g = w & 3, dh = w >> 2, d0 = dh * HALF;
     const int head = kvh * G + g, qrow = q0 + lc;
     const int len = a.length0 + qrow;  // positions [0, len) visible to this lane's query
@@ -423,7 +538,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         return;
     }
     const float scale = 1.f / sqrtf(float(D));
-    const size_t rowstride = size_t(a.kv) * D;
+    const char* kblk = a.kpl + size_t(kvh) * a.tiles * B3_KBLK;
+    const char* vblk = a.vpl + size_t(kvh) * a.tiles * B3_VBLK;
     bf16x8 qb[3][8];  // Q^T planes: step s, element e = dim d0 + 16 s + 8 hl + e of this lane's query
     {
         const float* qp = a.query + (size_t(qrow) * a.heads + head) * D + d0 + 8 * hl;
@@ -440,64 +556,11 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
             }
         }
     }
-    // this thread's share of a tile: K quads f = tid + 512 i (key f / 64, dims
-    // 4 (f % 64): every row read as 64 consecutive 16-byte loads) and one V
-    // block of 4 keys x 4 dims (below)
-    f4v kp[4];
-    auto fetch = [&](int t) {
-        const f4v z = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int f = tid + 512 * i, pos = t * 32 + (f >> 6), c = (f & 63) * 4;
-            kp[i] = pos < len_max ? *reinterpret_cast<const f4v*>(a.keys + size_t(pos) * rowstride + size_t(kvh) * D + c)
-                                  : z;
-        }
-    };
-    auto stage = [&](int t) {
-        // V: key quad tid % 8, dim quad tid / 8, so the 8 lanes of a dim quad
-        // write one V^T row's 32 positions (64 contiguous bytes) and each
-        // 16-lane group of a write covers two rows on disjoint banks; the
-        // global reads are 128 contiguous bytes per row
-        const int kq = tid & 7, cq = tid >> 3;
-        f4v vp[4];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const f4v z = {0.f, 0.f, 0.f, 0.f};
-            const int pos = t * 32 + 4 * kq + r, c = 4 * cq;
-            vp[r] = pos < len_max ? *reinterpret_cast<const f4v*>(a.values + size_t(pos) * rowstride + size_t(kvh) * D + c)
-                                  : z;
-        }
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int f = tid + 512 * i, key = f >> 6, c = (f & 63) * 4;
-            bf16x4 h[3];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const Split3 x = split3(kp[i][e]);
-#pragma unroll
-                for (int p = 0; p < 3; ++p) h[p][e] = x.h[p];
-            }
-#pragma unroll
-            for (int p = 0; p < 3; ++p) *reinterpret_cast<bf16x4*>(&ks[p][key][c]) = h[p];
-        }
-        const int p0 = vpos(4 * kq), c = 4 * cq;
-#pragma unroll
-        for (int d = 0; d < 4; ++d) {
-            bf16x4 h[3];
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const Split3 x = split3(vp[r][d]);
-#pragma unroll
-                for (int p = 0; p < 3; ++p) h[p][r] = x.h[p];
-            }
-#pragma unroll
-            for (int p = 0; p < 3; ++p) *reinterpret_cast<bf16x4*>(&vt[p][c + d][p0]) = h[p];
-        }
-    };
     constexpr int P[6] = {2, 1, 0, 1, 0, 0}, Q[6] = {0, 1, 2, 0, 1, 0};  // part products, smallest first
-    fetch(t_begin);
-    stage(t_begin);
-    __syncthreads();
+    b3_dma<B3_KDMA>(kblk + size_t(t_begin) * B3_KBLK, ks, w, lane);
+    b3_dma<B3_VDMA>(vblk + size_t(t_begin) * B3_VBLK, vt, w, lane);
+    b3_vm_wait<B3_VDMA>();  // this wave's K instructions done
+    b3_lds_barrier();
     f16v o[DT];
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt)
@@ -505,7 +568,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         for (int r = 0; r < 16; ++r) o[dt][r] = 0.f;
     float m = -INFINITY, l = 0.f;
     for (int t = t_begin; t < t_end; ++t) {
-        if (t + 1 < t_end) fetch(t + 1);
+        const bool more = t + 1 < t_end;
         f16v sc;
 #pragma unroll
         for (int r = 0; r < 16; ++r) sc[r] = 0.f;
@@ -513,13 +576,15 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         for (int s = 0; s < 8; ++s) {
             bf16x8 ka[3];
 #pragma unroll
-            for (int p = 0; p < 3; ++p) ka[p] = *reinterpret_cast<const bf16x8*>(&ks[p][lc][d0 + 16 * s + 8 * hl]);
+            for (int p = 0; p < 3; ++p)
+                ka[p] = *reinterpret_cast<const bf16x8*>(&ks[(p * 32 + lc) * B3_KROW + d0 + 16 * s + 8 * hl]);
 #pragma unroll
             for (int pq = 0; pq < 6; ++pq) sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka[P[pq]], qb[Q[pq]][s], sc, 0, 0, 0);
         }
 #pragma unroll
         for (int r = 0; r < 16; ++r) xch[w][r][lane] = sc[r];
-        __syncthreads();
+        b3_lds_barrier();  // scores exchanged; every wave is past its K reads
+        if (more) b3_dma<B3_KDMA>(kblk + size_t(t + 1) * B3_KBLK, ks, w, lane);
         float mx = -INFINITY;
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
@@ -540,8 +605,16 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
             ps += sc[r];
         }
         l = l * corr + ps;
+        if (__any(corr != 1.f)) {  // a running maximum moved (scaling by 1 is exact: skipped)
 #pragma unroll
-        for (int dt = 0; dt < DT; ++dt) o[dt] *= corr;
+            for (int dt = 0; dt < DT; ++dt) o[dt] *= corr;
+        }
+        // V of this tile landed (the next tile's K may still be in flight)
+        if (more)
+            b3_vm_wait<B3_KDMA>();
+        else
+            b3_vm_wait<0>();
+        b3_lds_barrier();
         // key steps outermost, so one step's P^T planes are live at a time
         // (each accumulator still takes step 0's products, then step 1's)
 #pragma unroll
@@ -558,16 +631,17 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                 bf16x8 va[3];
 #pragma unroll
                 for (int p = 0; p < 3; ++p)
-                    va[p] = *reinterpret_cast<const bf16x8*>(&vt[p][d0 + 32 * dt + lc][16 * s + 8 * hl]);
+                    va[p] = *reinterpret_cast<const bf16x8*>(
+                        &vt[(p * D + d0 + 32 * dt + lc) * B3_VROW + 16 * s + 8 * hl]);
 #pragma unroll
                 for (int pq = 0; pq < 6; ++pq)
                     o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va[P[pq]], pb[Q[pq]], o[dt], 0, 0, 0);
             }
         }
-        __syncthreads();
-        if (t + 1 < t_end) {
-            stage(t + 1);
-            __syncthreads();
+        if (more) {
+            b3_vm_wait<0>();   // the next tile's K landed
+            b3_lds_barrier();  // ... for every wave, and every wave is past its V reads
+            b3_dma<B3_VDMA>(vblk + size_t(t + 1) * B3_VBLK, vt, w, lane);
         }
     }
     const float den = l + __shfl_xor(l, 32, 64);
@@ -597,9 +671,11 @@ template <int D, int G>
 int launch_prefill_g(hipStream_t s, const ReadArgs& a) {
     if constexpr (prefill_shape_ok(D, G)) {
         const dim3 grid(ceil_div(a.rows, 32), unsigned(a.kv), unsigned(a.splits));
-        if constexpr (D == 256 && G == 4)
+        if constexpr (D == 256 && G == 4) {
+            hipLaunchKernelGGL(kv_planes_kernel, dim3(unsigned(a.tiles), unsigned(a.kv)), dim3(256), 0, s, a,
+                               a.length0 + a.rows - 1);
             hipLaunchKernelGGL(attention_prefill_bf3_kernel, grid, dim3(512), 0, s, a);
-        else
+        } else
             hipLaunchKernelGGL((attention_prefill_kernel<D, G>), grid, dim3(64 * G), 0, s, a);
         if (a.splits == 1) return int(hipGetLastError());
         if (hipError_t e = hipGetLastError()) return int(e);
@@ -657,6 +733,14 @@ int prefill_splits(int rows, int kv) {
     return int(s < 1 ? 1 : s > 8 ? 8 : s);
 }
 
+// Scratch of a prefill call, in floats: the split partials, then (head dim
+// 256, 4 query heads per KV head) the K and V^T planes at a 256-byte boundary.
+size_t prefill_parts_floats(int tokens, int heads, int kv, int d) {
+    const int splits = prefill_splits(tokens, kv);
+    return splits > 1 ? (size_t(tokens) * heads * splits * (d + 2) + 63) / 64 * 64 : 0;
+}
+int prefill_tiles(int length0, int tokens) { return ceil_div(length0 + tokens - 1, 32); }
+
 }  // namespace
 
 size_t attention_scratch_needed(const Params& a) {
@@ -664,8 +748,10 @@ size_t attention_scratch_needed(const Params& a) {
     const int group = a.n[2] > 0 ? a.n[1] / a.n[2] : 0;
     if (tokens > 1) {
         if (!prefill_path(a.n[0], group, tokens)) return 0;
-        const int splits = prefill_splits(tokens, a.n[2]);
-        return splits > 1 ? size_t(tokens) * a.n[1] * splits * (a.n[0] + 2) : 0;
+        size_t need = prefill_parts_floats(tokens, a.n[1], a.n[2], a.n[0]);
+        if (a.n[0] == 256 && group == 4)
+            need += size_t(a.n[2]) * prefill_tiles(a.n[3], tokens) * (B3_KBLK + B3_VBLK) / sizeof(float);
+        return need;
     }
     int span;
     const int splits = decode_splits(a.n[3], a.n[2], span);
@@ -698,9 +784,15 @@ int run_attention_read(hipStream_t s, int heads_count, const Params& p, float* s
     }
     if (prefill_path(a.d, group, a.rows)) {
         a.splits = prefill_splits(a.rows, a.kv);
-        if (a.splits > 1) {
-            if (size_t(a.rows) * a.heads * a.splits * (a.d + 2) > scratch_len) return int(hipErrorInvalidValue);
-            a.parts = scratch;
+        const size_t parts = prefill_parts_floats(a.rows, a.heads, a.kv, a.d);
+        if (parts > scratch_len) return int(hipErrorInvalidValue);
+        if (a.splits > 1) a.parts = scratch;
+        if (a.d == 256 && group == 4) {
+            a.tiles = prefill_tiles(a.length0, a.rows);
+            const size_t planes = size_t(a.kv) * a.tiles * (B3_KBLK + B3_VBLK) / sizeof(float);
+            if (parts + planes > scratch_len) return int(hipErrorInvalidValue);
+            a.kpl = reinterpret_cast<char*>(scratch + parts);
+            a.vpl = a.kpl + size_t(a.kv) * a.tiles * B3_KBLK;
         }
         switch (a.d) {
         case 64: return launch_prefill<64>(s, a, group);
