@@ -42,6 +42,23 @@ __global__ __launch_bounds__(256) void elementwise_kernel(int op, int count, Par
     }
 }
 
+// Add and SiluProduct four elements per thread (count % 4 == 0, operands
+// 16-byte aligned): one 16-byte load per operand.
+__global__ __launch_bounds__(256) void elementwise4_kernel(int op, int count4, Params a) {
+    typedef float f4 __attribute__((ext_vector_type(4)));
+    for (long t = blockIdx.x * long(blockDim.x) + threadIdx.x; t < count4; t += long(gridDim.x) * blockDim.x) {
+        const f4 x = reinterpret_cast<const f4*>(a.p[1])[t], y = reinterpret_cast<const f4*>(a.p[2])[t];
+        f4 r;
+        if (op == QR_ADD) {
+            r = x + y;
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) r[e] = siluf_(x[e]) * y[e];
+        }
+        reinterpret_cast<f4*>(a.p[0])[t] = r;
+    }
+}
+
 // ---------------------------------------------------------------- RMSNorm family
 // RmsNorm (1), AddRmsNorm (12), RmsNormGate (13): reference.h:120-126,194-207.
 // One wave per group when d <= 256, else one block per group.
@@ -78,6 +95,53 @@ __global__ __launch_bounds__(256) void rms_family_kernel(int op, int groups, Par
             a.p[0][off + i] = siluf_(a.p[3][off + i]) * ((a.p[1][off + i] * r) * (a.p[2][i] + offset));
             break;
         }
+    }
+}
+
+// The same ops with one wave per group and the group in registers when
+// d = 64 PER: lane l holds elements V (l + 64 j) .. + V - 1 (V = min(PER, 4),
+// j < PER / V), so every load and store of a wave is one contiguous run and
+// each input is read once (the block form above reads a group twice and
+// waits on two block barriers).
+template <int PER>
+__global__ __launch_bounds__(256) void rms_rows_kernel(int op, int groups, Params a) {
+    constexpr int V = PER >= 4 ? 4 : PER, NV = PER / V;
+    typedef float fv __attribute__((ext_vector_type(V)));
+    const int g = int(blockIdx.x) * 4 + int(threadIdx.x >> 6);
+    if (g >= groups) return;  // whole waves only: no block barrier
+    const int lane = int(threadIdx.x & 63), d = 64 * PER;
+    const size_t off = size_t(g) * d;
+    const float eps = a.f[0], offset = a.f[1];
+    fv x[NV];
+    float ss = 0.f;
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        const size_t i = off + size_t(V) * (lane + 64 * j);
+        x[j] = *reinterpret_cast<const fv*>(a.p[1] + i);
+        if (op == QR_ADD_RMS_NORM) {
+            x[j] += *reinterpret_cast<const fv*>(a.p[2] + i);
+            *reinterpret_cast<fv*>(a.p[0] + i) = x[j];
+        }
+#pragma unroll
+        for (int e = 0; e < V; ++e) ss += x[j][e] * x[j][e];
+    }
+    ss = wave_sum(ss);
+    const float r = 1.f / sqrtf(ss / float(d) + eps);
+    const float* w = op == QR_ADD_RMS_NORM ? a.p[4] : a.p[2];
+    float* out = op == QR_ADD_RMS_NORM ? a.p[3] : a.p[0];
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        const int c = V * (lane + 64 * j);
+        const fv wv = *reinterpret_cast<const fv*>(w + c);
+        fv y;
+#pragma unroll
+        for (int e = 0; e < V; ++e) y[e] = (x[j][e] * r) * (wv[e] + offset);
+        if (op == QR_RMS_NORM_GATE) {
+            const fv z = *reinterpret_cast<const fv*>(a.p[3] + off + c);
+#pragma unroll
+            for (int e = 0; e < V; ++e) y[e] = siluf_(z[e]) * y[e];
+        }
+        *reinterpret_cast<fv*>(out + off + c) = y;
     }
 }
 
@@ -458,11 +522,39 @@ unsigned grid_for(long n) {
 }  // namespace
 
 int run_elementwise(hipStream_t s, int op, int count, const Params& a) {
+    if ((op == QR_ADD || op == QR_SILU_PRODUCT) && count % 4 == 0 &&
+        (reinterpret_cast<uintptr_t>(a.p[0]) | reinterpret_cast<uintptr_t>(a.p[1]) |
+         reinterpret_cast<uintptr_t>(a.p[2])) % 16 == 0) {
+        hipLaunchKernelGGL(elementwise4_kernel, dim3(grid_for(count / 4)), dim3(256), 0, s, op, count / 4, a);
+        return int(hipGetLastError());
+    }
     hipLaunchKernelGGL(elementwise_kernel, dim3(grid_for(count)), dim3(256), 0, s, op, count, a);
     return int(hipGetLastError());
 }
 
+// The register form when the group is 64 PER elements and every operand is
+// aligned to its vector width.
+template <int PER>
+bool launch_rms_rows(hipStream_t s, int op, int groups, const Params& a) {
+    constexpr uintptr_t align = (PER >= 4 ? 4 : PER) * sizeof(float);
+    const int slots[] = {0, 1, 2, 3, 4};
+    const int used = op == QR_ADD_RMS_NORM ? 5 : op == QR_RMS_NORM_GATE ? 4 : 3;
+    for (int k = 0; k < used; ++k)
+        if (reinterpret_cast<uintptr_t>(a.p[slots[k]]) % align != 0) return false;
+    hipLaunchKernelGGL(rms_rows_kernel<PER>, dim3(ceil_div(groups, 4)), dim3(256), 0, s, op, groups, a);
+    return true;
+}
+
 int run_rms_family(hipStream_t s, int op, int groups, const Params& a) {
+    bool done = false;
+    switch (a.n[0]) {
+    case 128: done = launch_rms_rows<2>(s, op, groups, a); break;
+    case 256: done = launch_rms_rows<4>(s, op, groups, a); break;
+    case 512: done = launch_rms_rows<8>(s, op, groups, a); break;
+    case 1024: done = launch_rms_rows<16>(s, op, groups, a); break;
+    case 2048: done = launch_rms_rows<32>(s, op, groups, a); break;
+    }
+    if (done) return int(hipGetLastError());
     if (a.n[0] <= 256)
         hipLaunchKernelGGL(rms_family_kernel<true>, dim3(ceil_div(groups, 4)), dim3(256), 0, s, op, groups, a);
     else

@@ -311,8 +311,11 @@ def test_argmax_known_answers(gpu):
             assert np.array_equal(out.read(), want), (n, rows)
 
 
-@pytest.mark.parametrize("d,groups", [(1024, 1), (1024, 3), (128, 16), (128, 48), (8, 5), (256, 8)])
+@pytest.mark.parametrize("d,groups", [(1024, 1), (1024, 3), (128, 16), (128, 48), (8, 5), (256, 8), (2048, 5), (512, 7),
+                                      (1024, 9), (64, 3)])
 def test_rms_family(gpu, cpu, d, groups):
+    """RmsNorm, AddRmsNorm, RmsNormGate: the register form (d = 64 PER for
+    PER 2..32, ragged last block of 4 groups) and the generic forms."""
     rng = np.random.default_rng(d + groups)
     x, w, u, z = rnd(rng, d * groups), rnd(rng, d, 0.1), rnd(rng, d * groups), rnd(rng, d * groups)
     g, c = both(gpu, cpu, "RMS_NORM", groups, {1: x, 2: w}, {0: d * groups}, [d], [1e-6, 1.0])
