@@ -13,8 +13,8 @@
 //   S_C = e^{G_63} S0 + (e^{G_63 - G} K)^T D.
 // Everything but S0 depends on the chunk's own inputs only:
 // rule_chunk_prep_kernel builds U, -W, e^G Q, (e^{G_63-G} K)^T and L for all
-// (chunk, head) pairs at once (the triangular solve is a forward substitution,
-// one column per thread); rule_chunk_scan_kernel then walks the chunks in
+// (chunk, head) pairs at once (8 waves; the triangular solve by 16-row blocks
+// on MFMA with the inverses of the diagonal blocks); rule_chunk_scan_kernel then walks the chunks in
 // order, one block per (head, 16-column slice of S) with the slice in LDS.
 // Tokens past the end of the last chunk are zero with g = 0 and beta = 0,
 // which leaves D, O and S unchanged. G is summed in double so that
@@ -47,11 +47,18 @@ typedef float f4v __attribute__((ext_vector_type(4)));
 // U in accumulator order: f4 (tile, js, l) holds rows 16 tile + 4 (l / 16) + e
 // of column 16 js + l % 16; f4 index (tile * kSlices + js) * 64 + l.
 
-__global__ __launch_bounds__(256) void rule_chunk_prep_kernel(Params a, int gated, int c0, float* scratch) {
+constexpr int kPrep = 512;              // threads of a prep block (8 waves)
+constexpr int kPrepLoads = kC * kD / 4 / kPrep;  // float4 of q (of k, of V) per thread
+
+__global__ __launch_bounds__(kPrep) void rule_chunk_prep_kernel(Params a, int gated, int c0, float* scratch) {
     // row stride 132 (4 mod 64 banks): the Gram products' MFMA operand reads
     // (16 rows x 4 interleaved k per step) hit 64 distinct banks
     __shared__ float ks[kC][kD + 4], qs[kC][kD + 4];
+    // am holds A transposed: am[s][t] = A_ts (s < t), so the solve's column
+    // sweeps read rows
     __shared__ float am[kC][kC + 4], lm[kC][kC + 4];
+    // inverses of the four 16 x 16 diagonal blocks of I + A: li[i][t][s] = ((I + A)_ii^-1)_ts
+    __shared__ float li[kC / 16][16][16];
     __shared__ double gd[kC];
     __shared__ float bs[kC], eg[kC], el[kC];
     const int tid = threadIdx.x, h = blockIdx.y, c = c0 + int(blockIdx.x);
@@ -59,19 +66,41 @@ __global__ __launch_bounds__(256) void rule_chunk_prep_kernel(Params a, int gate
     const int t0 = c * kC, n = min(kC, tokens - t0);
     float* rec = scratch + (size_t(blockIdx.x) * vh + h) * kRec;
     f4v* rec4 = reinterpret_cast<f4v*>(rec);
-    {  // q and k rows: every thread's 8 + 8 float4 loads in flight together
-        f4v kv[8], qv[8];
+    // Every global input of the block is requested up front: the gate inputs
+    // (wave 0), q and k rows, and the V rows, held in registers until the
+    // right-hand sides are formed, so no later phase waits on a load.
+    float ga = 0.f, gb = 0.f, gdt = 0.f, galog = 0.f;
+    if (tid < n) {
+        const int gi = (t0 + tid) * vh + h;
+        ga = a.p[5][gi];
+        gb = a.p[6][gi];
+        if (gated) {
+            gdt = a.p[7][h];
+            galog = a.p[7][vh + h];
+        }
+    }
+    f4v vv[kPrepLoads];
+    {  // q and k rows: every thread's float4 loads in flight together
+        f4v kv[kPrepLoads], qv[kPrepLoads];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const int e = tid + 256 * j, r = e >> 5, i = (e & 31) * 4;
+        for (int j = 0; j < kPrepLoads; ++j) {
+            const int e = tid + kPrep * j, r = e >> 5, i = (e & 31) * 4;
             const size_t off = size_t(t0 + r) * vh * kD + size_t(h) * kD + i;
             const f4v z = {0.f, 0.f, 0.f, 0.f};
             kv[j] = r < n ? *reinterpret_cast<const f4v*>(a.p[2] + off) : z;
             qv[j] = r < n ? *reinterpret_cast<const f4v*>(a.p[1] + off) : z;
         }
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const int e = tid + 256 * j, r = e >> 5, i = (e & 31) * 4;
+        for (int j = 0; j < kPrepLoads; ++j) {
+            const int e = tid + kPrep * j, t = e >> 5, i = (e & 31) * 4;
+            const f4v z = {0.f, 0.f, 0.f, 0.f};
+            vv[j] = t < n ? *reinterpret_cast<const f4v*>(a.p[3] + size_t(t0 + t) * stride + 2 * size_t(kh) * kD +
+                                                          size_t(h) * kD + i)
+                          : z;
+        }
+#pragma unroll
+        for (int j = 0; j < kPrepLoads; ++j) {
+            const int e = tid + kPrep * j, r = e >> 5, i = (e & 31) * 4;
             *reinterpret_cast<f4v*>(&ks[r][i]) = kv[j];
             *reinterpret_cast<f4v*>(&qs[r][i]) = qv[j];
         }
@@ -79,13 +108,12 @@ __global__ __launch_bounds__(256) void rule_chunk_prep_kernel(Params a, int gate
     if (tid < kC) {  // wave 0: gates and the inclusive prefix of g
         float g = 0.f, b = 0.f;
         if (tid < n) {
-            const int gi = (t0 + tid) * vh + h;
             if (gated) {
-                g = -expf(a.p[7][vh + h]) * softplusf_(a.p[5][gi] + a.p[7][h]);
-                b = sigmoidf_(a.p[6][gi]);
+                g = -expf(galog) * softplusf_(ga + gdt);
+                b = sigmoidf_(gb);
             } else {
-                g = a.p[5][gi];
-                b = a.p[6][gi];
+                g = ga;
+                b = gb;
             }
         }
         double G = g;
@@ -101,39 +129,53 @@ __global__ __launch_bounds__(256) void rule_chunk_prep_kernel(Params a, int gate
         el[tid] = expf(float(last - G));
     }
     __syncthreads();
-    {  // Gram products K K^T and Q K^T on MFMA, the 10 lower 16 x 16 tiles (sj <= ti);
-       // a tile's two products share the B operand (rows of K)
+    {  // Gram products K K^T and Q K^T on MFMA, the 10 lower 16 x 16 tiles (sj <= ti)
         const int w = tid >> 6, l = tid & 63, lc = l & 15, q = l >> 4;
-        for (int e = tid; e < 6 * 256; e += 256) {  // the upper tiles are zero
+        for (int e = tid; e < 6 * 256; e += kPrep) {  // the upper tiles are zero
             const int tile = e >> 8, ti = tile < 3 ? 0 : tile < 5 ? 1 : 2, sj = tile < 3 ? tile + 1 : tile < 5 ? tile - 1 : 3;
             const int t = 16 * ti + ((e >> 4) & 15), s2 = 16 * sj + (e & 15);
-            am[t][s2] = 0.f;
             lm[t][s2] = 0.f;
         }
-        // wave w: tiles w, w + 4, w + 8 of the list (ti, sj) = (0,0) (1,0) (1,1) (2,0) ... (3,3)
-        for (int j = w; j < 10; j += 4) {
+        // the 20 products (tile j of the list (ti, sj) = (0,0) (1,0) (1,1) (2,0) ... (3,3), K K^T
+        // or Q K^T) dealt to the 8 waves: product w + 8 k
+        for (int pr = w; pr < 20; pr += kPrep / 64) {
+            const int j = pr >> 1, qk = pr & 1;
             const int ti = j < 1 ? 0 : j < 3 ? 1 : j < 6 ? 2 : 3, sj = j - ti * (ti + 1) / 2;
-            f4v kk = {0.f, 0.f, 0.f, 0.f}, qk = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll 8
-            for (int st = 0; st < kD / 4; ++st) {
-                const int k = 4 * st + q;
-                const float b = ks[16 * sj + lc][k];
-                kk = __builtin_amdgcn_mfma_f32_16x16x4f32(ks[16 * ti + lc][k], b, kk, 0, 0, 0);
-                qk = __builtin_amdgcn_mfma_f32_16x16x4f32(qs[16 * ti + lc][k], b, qk, 0, 0, 0);
+            // MFMA step 4 m + e, lane (lc, q) takes k = 32 q + 4 m + e: a lane's operands of a
+            // tile are 8 contiguous float4 per matrix, read before the 32 MFMAs
+            float (*as)[kD + 4] = qk ? qs : ks;
+            // two independent accumulator chains (k below and above 64 within each lane group's
+            // 32), added at the end
+            f4v acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+            f4v xa[8], xb[8];
+#pragma unroll
+            for (int m = 0; m < 8; ++m) {
+                xa[m] = *reinterpret_cast<const f4v*>(&as[16 * ti + lc][32 * q + 4 * m]);
+                xb[m] = *reinterpret_cast<const f4v*>(&ks[16 * sj + lc][32 * q + 4 * m]);
             }
+#pragma unroll
+            for (int m = 0; m < 4; ++m)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    acc0 = __builtin_amdgcn_mfma_f32_16x16x4f32(xa[m][e], xb[m][e], acc0, 0, 0, 0);
+                    acc1 = __builtin_amdgcn_mfma_f32_16x16x4f32(xa[m + 4][e], xb[m + 4][e], acc1, 0, 0, 0);
+                }
+            const f4v acc = acc0 + acc1;
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int t = 16 * ti + 4 * q + r, s2 = 16 * sj + lc;
                 const float e = s2 <= t ? expf(float(gd[t] - gd[s2])) : 0.f;
-                am[t][s2] = s2 < t ? bs[t] * e * kk[r] : 0.f;
-                lm[t][s2] = e * qk[r];
+                if (qk)
+                    lm[t][s2] = e * acc[r];
+                else
+                    am[s2][t] = s2 < t ? bs[t] * e * acc[r] : 0.f;
             }
         }
     }
     __syncthreads();
     // e^G Q, (e^{G_63-G} K)^T and L into the record, one float4 of the
     // destination per thread step (contiguous stores)
-    for (int d = tid; d < kC * kD / 4; d += 256) {
+    for (int d = tid; d < kC * kD / 4; d += kPrep) {
         const int l = d & 63, lr = l & 15, q = l >> 4;
         {  // e^G Q: 4 tiles of 16 rows, K = 128 (8 float4 per lane)
             const int tile = d >> 9, m = (d >> 6) & 7, t = tile * 16 + lr, k = 16 * m + q;
@@ -149,49 +191,65 @@ __global__ __launch_bounds__(256) void rule_chunk_prep_kernel(Params a, int gate
             rec4[kL / 4 + d] = f4v{lm[t][k], lm[t][k + 4], lm[t][k + 8], lm[t][k + 12]};
         }
     }
+    if (tid >= kPrep - 64) {  // the last wave: lane (i, j) = column j of the inverse of diagonal block i,
+                              // by forward substitution (y_t = [t == j] - A_t0 y_0 - ..., in that order)
+        const int i = (tid & 63) >> 4, j = tid & 15, o = 16 * i;
+        float y[16];
+#pragma unroll
+        for (int t = 0; t < 16; ++t) y[t] = t == j ? 1.f : 0.f;
+#pragma unroll
+        for (int s2 = 0; s2 < 15; ++s2)
+#pragma unroll
+            for (int t = s2 + 1; t < 16; ++t) y[t] = fmaf(-am[o + s2][o + t], y[s2], y[t]);
+#pragma unroll
+        for (int t = 0; t < 16; ++t) li[i][t][j] = y[t];
+    }
     __syncthreads();
-    {  // right-hand sides: beta e^G K in ks, beta V in qs (the V loads all in flight together)
-        f4v vv[8];
+    {  // right-hand sides: beta e^G K in ks, beta V in qs
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const int e = tid + 256 * j, t = e >> 5, i = (e & 31) * 4;
-            const f4v z = {0.f, 0.f, 0.f, 0.f};
-            vv[j] = t < n ? *reinterpret_cast<const f4v*>(a.p[3] + size_t(t0 + t) * stride + 2 * size_t(kh) * kD +
-                                                          size_t(h) * kD + i)
-                          : z;
-        }
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const int e = tid + 256 * j, t = e >> 5, i = (e & 31) * 4;
+        for (int j = 0; j < kPrepLoads; ++j) {
+            const int e = tid + kPrep * j, t = e >> 5, i = (e & 31) * 4;
             f4v* kr = reinterpret_cast<f4v*>(&ks[t][i]);
             *kr = *kr * (bs[t] * eg[t]);
             *reinterpret_cast<f4v*>(&qs[t][i]) = vv[j] * bs[t];
         }
     }
     __syncthreads();
-    {  // forward substitution (I + A) X = B, one column per thread: W (threads 0..127), U (128..255),
-       // two partial sums per row; the solution replaces its right-hand side in LDS
-        const int col = tid & (kD - 1);
-        float* rhs = tid < kD ? &ks[0][col] : &qs[0][col];
+    {  // (I + A) X = B by blocks of 16 rows on MFMA, B = [beta e^G K | beta V] (256 columns, in
+       // ks | qs). Block row i: X_i = ((I + A)_ii)^-1 (B_i - A_{i,<i} X_{<i}): the first
+       // product over the solved rows (k = 4 step + lane / 16), the second over the 16 rows of
+       // the block with k = 4 (lane / 16) + step, so B_i - A X sits in the accumulator
+       // registers that operand needs (no data movement). Wave w owns the 16-column tiles
+       // 2 w and 2 w + 1 in every block row, so the solve needs no block barrier (a wave's
+       // LDS operations complete in order). The solution replaces B in LDS.
+        const int w = tid >> 6, l = tid & 63, lc = l & 15, q = l >> 4;
         constexpr int RS = kD + 4;  // row stride of ks / qs
-        float x[kC];
 #pragma unroll
-        for (int t = 0; t < kC; ++t) {
-            float r0 = rhs[t * RS], r1 = 0.f;
+        for (int i = 0; i < kC / 16; ++i) {
 #pragma unroll
-            for (int s = 0; s + 1 < t; s += 2) {
-                r0 = fmaf(-am[t][s], x[s], r0);
-                r1 = fmaf(-am[t][s + 1], x[s + 1], r1);
+            for (int ct = 0; ct < 2; ++ct) {
+                const int tile = 2 * w + ct;  // 16-column tile of the 256 combined columns
+                float* base = tile < kD / 16 ? &ks[0][16 * tile] : &qs[0][16 * tile - kD];
+                f4v acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int st = 0; st < 4 * i; ++st) {
+                    const int k = 4 * st + q;  // A[16 i + lc][k] = am[k][16 i + lc]
+                    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(am[k][16 * i + lc], base[k * RS + lc], acc, 0, 0, 0);
+                }
+                f4v b;  // B_i - A X: row 16 i + 4 q + r, column lc
+#pragma unroll
+                for (int r = 0; r < 4; ++r) b[r] = base[(16 * i + 4 * q + r) * RS + lc] - acc[r];
+                const f4v inv = *reinterpret_cast<const f4v*>(&li[i][lc][4 * q]);  // row lc, k = 4 q + st
+                f4v x = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int st = 0; st < 4; ++st) x = __builtin_amdgcn_mfma_f32_16x16x4f32(inv[st], b[st], x, 0, 0, 0);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) base[(16 * i + 4 * q + r) * RS + lc] = x[r];
             }
-            if (t & 1) r0 = fmaf(-am[t][t - 1], x[t - 1], r0);
-            x[t] = r0 + r1;
-            asm volatile("" ::: "memory");  // keep each row's LDS reads with its row
         }
-#pragma unroll
-        for (int t = 0; t < kC; ++t) rhs[t * RS] = x[t];
     }
     __syncthreads();
-    for (int d = tid; d < kC * kD / 4; d += 256) {
+    for (int d = tid; d < kC * kD / 4; d += kPrep) {
         const int l = d & 63, lr = l & 15, q = l >> 4;
         {  // -W, as e^G Q
             const int tile = d >> 9, m = (d >> 6) & 7, t = tile * 16 + lr, k = 16 * m + q;
@@ -362,7 +420,7 @@ int run_delta_rule_chunked(hipStream_t s, bool gated, const Params& a, float* sc
     const int chunks = int(ceil_div(tokens, kC));
     for (int c0 = 0; c0 < chunks; c0 += kGroupChunks) {
         const int group = chunks - c0 < kGroupChunks ? chunks - c0 : kGroupChunks;
-        hipLaunchKernelGGL(rule_chunk_prep_kernel, dim3(unsigned(group), unsigned(vh)), dim3(256), 0, s, a,
+        hipLaunchKernelGGL(rule_chunk_prep_kernel, dim3(unsigned(group), unsigned(vh)), dim3(kPrep), 0, s, a,
                            gated ? 1 : 0, c0, scratch);
         if (hipError_t e = hipGetLastError()) return int(e);
         hipLaunchKernelGGL(rule_chunk_scan_kernel, dim3(unsigned(vh * kSlices)), dim3(256), 0, s, a, c0, group,
