@@ -276,10 +276,11 @@ __device__ __forceinline__ f4v mfma16(float x, float y, f4v acc) {
 // of a product over them, so each lane takes all of its operands in a few
 // 16-byte reads and one wait (rows padded to 36 / 20 floats: the 16-byte
 // reads of 8 consecutive lanes hit distinct banks).
-// Operand loads run a phase ahead: chunk c + 1's -W, e^G Q and U are issued
-// once phase 1 of chunk c has consumed chunk c's, its L and K^T once phase 2
-// has; the barriers wait for LDS only, so those loads stay in flight across
-// them (__syncthreads() would also wait for every outstanding load).
+// Operand loads run a phase ahead: chunk c + 1's -W and e^G Q float4 m are
+// issued as soon as phase 1 of chunk c has consumed chunk c's (so the loads
+// go out while the MFMAs run), its L and K^T likewise in phase 2; the
+// barriers wait for LDS only, so those loads stay in flight across them
+// (__syncthreads() would also wait for every outstanding load).
 // Blocks are dealt to the 8 XCDs round-robin by index; the index is remapped
 // so that the 8 slices of a head run on one XCD: every slice reads the whole
 // chunk record, and this way 7 of the 8 reads hit that XCD's L2 instead of
@@ -352,14 +353,19 @@ __global__ __launch_bounds__(256) void rule_chunk_scan_kernel(Params a, int c0, 
 #pragma unroll
         for (int m = 0; m < 8; ++m) sb[m] = *reinterpret_cast<const f4v*>(&sl[l][4 * m]);
         f4v dacc = uv, oacc = {0.f, 0.f, 0.f, 0.f};
+        const float* recn = scan_rec(scratch, cn, vh, h);
 #pragma unroll
-        for (int m = 0; m < 8; ++m)
+        for (int m = 0; m < 8; ++m) {
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 dacc = mfma16(wv[m][e], sb[m][e], dacc);
                 oacc = mfma16(qv[m][e], sb[m][e], oacc);
             }
-        scan_load1(scan_rec(scratch, cn, vh, h), w, js, l, wv, qv, uv);
+            // float4 m is consumed: chunk cn's goes out while the MFMAs run
+            wv[m] = reinterpret_cast<const f4v*>(recn + kW)[w * 512 + m * 64 + l];
+            qv[m] = reinterpret_cast<const f4v*>(recn + kQ)[w * 512 + m * 64 + l];
+        }
+        uv = reinterpret_cast<const f4v*>(recn + kU)[(w * kSlices + js) * 64 + l];
 #pragma unroll
         for (int r = 0; r < 4; ++r) dl[16 * r + lc][4 * w + q] = dacc[r];  // D row 16 w + 4 q + r
         lds_barrier();
@@ -373,14 +379,18 @@ __global__ __launch_bounds__(256) void rule_chunk_scan_kernel(Params a, int c0, 
 #pragma unroll
         for (int m = 0; m < 4; ++m) db[m] = *reinterpret_cast<const f4v*>(&dl[l][4 * m]);
 #pragma unroll
-        for (int m = 0; m < 4; ++m)
+        for (int m = 0; m < 4; ++m) {
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 if (m <= w) oacc = mfma16(lv[m][e], db[m][e], oacc);  // L is zero past the tile's last token
                 s0 = mfma16(k0[m][e], db[m][e], s0);
                 s1 = mfma16(k1[m][e], db[m][e], s1);
             }
-        scan_load2(scan_rec(scratch, cn, vh, h), w, l, lv, k0, k1);
+            const f4v* Kp = reinterpret_cast<const f4v*>(recn + kK) + l;
+            lv[m] = reinterpret_cast<const f4v*>(recn + kL)[w * 256 + m * 64 + l];
+            k0[m] = Kp[w * 256 + m * 64];
+            k1[m] = Kp[(w + 4) * 256 + m * 64];
+        }
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const int t = t0 + 16 * w + 4 * q + r;  // rows t >= tokens fall outside out_rs: dropped
