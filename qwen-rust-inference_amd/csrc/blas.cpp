@@ -25,9 +25,10 @@ namespace {
 
 constexpr size_t kWorkspace = size_t(64) << 20;
 // hipBLASLt's first candidates for a shape; the fastest of the first kTimed is
-// chosen by timing when the batch has at least kTimedBatch tokens (on the
-// prefill shapes of the 0.8B model the fastest was always among the first 8,
-// up to 1.4x faster than the first), else the first is taken. The timing
+// chosen by timing (each candidate's fastest of three runs, so a transient
+// slowdown does not decide) when the batch has at least kTimedBatch tokens (on
+// the prefill shapes of the 0.8B model the fastest was always among the first
+// 8, up to 1.4x faster than the first), else the first is taken. The timing
 // costs a few ms per new shape.
 constexpr int kCandidates = 8, kTimed = 8, kTimedBatch = 256;
 using Shape = std::tuple<int, int, int>;  // rows, cols, batch
@@ -101,9 +102,13 @@ int make_plan(Blas* b, hipStream_t s, float* y, const __bf16* w6, const __bf16* 
     if (choice < 0 && batch < kTimedBatch) choice = 0;
     if (choice < 0) {
         const float alpha = 1.f, beta = 0.f;
-        hipEvent_t e0 = nullptr, e1 = nullptr;
-        if (hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess) {
-            if (e0) (void)hipEventDestroy(e0);
+        constexpr int kRuns = 3;  // each candidate: one warm-up run, then the fastest of kRuns timed runs
+        hipEvent_t ev[2 * kRuns] = {};
+        bool events = true;
+        for (auto& e : ev) events = events && hipEventCreate(&e) == hipSuccess;
+        if (!events) {
+            for (auto& e : ev)
+                if (e) (void)hipEventDestroy(e);
             destroy_plan(p);
             return int(hipErrorOutOfMemory);
         }
@@ -114,17 +119,23 @@ int make_plan(Blas* b, hipStream_t s, float* y, const __bf16* w6, const __bf16* 
                                        &res[i].algo, b->ws, kWorkspace, s) == HIPBLAS_STATUS_SUCCESS;
             };
             if (!run()) continue;  // warm-up; a candidate that fails is skipped
-            bool timed = hipEventRecord(e0, s) == hipSuccess;
-            for (int r = 0; r < 2 && timed; ++r) timed = run();
-            timed = timed && hipEventRecord(e1, s) == hipSuccess && hipEventSynchronize(e1) == hipSuccess;
+            bool timed = true;
+            for (int r = 0; r < kRuns && timed; ++r)
+                timed = hipEventRecord(ev[2 * r], s) == hipSuccess && run() &&
+                        hipEventRecord(ev[2 * r + 1], s) == hipSuccess;
+            timed = timed && hipEventSynchronize(ev[2 * kRuns - 1]) == hipSuccess;
             float ms = 0.f;
-            if (timed && hipEventElapsedTime(&ms, e0, e1) == hipSuccess && (choice < 0 || ms < best)) {
+            for (int r = 0; r < kRuns && timed; ++r) {
+                float one = 0.f;
+                timed = hipEventElapsedTime(&one, ev[2 * r], ev[2 * r + 1]) == hipSuccess;
+                if (r == 0 || one < ms) ms = one;
+            }
+            if (timed && (choice < 0 || ms < best)) {
                 choice = i;
                 best = ms;
             }
         }
-        (void)hipEventDestroy(e0);
-        (void)hipEventDestroy(e1);
+        for (auto& e : ev) (void)hipEventDestroy(e);
         if (choice < 0) {
             destroy_plan(p);
             return int(hipErrorNotSupported);
