@@ -38,6 +38,15 @@ struct Context {
     qr::Blas* blas = nullptr;
     __bf16* x6 = nullptr;  // the split planes of a projection's input
     size_t x6_len = 0;     // in BF16 elements
+    // A producer (a norm, or a GLU's product, over at least kBlasMinBatch rows
+    // of a width some prepared matrix takes) may leave its output's planes in
+    // x6 as it writes the output: they stand for x6_src (x6_rows x x6_cols)
+    // during the very next bridge call only (serial == x6_serial + 1), so
+    // nothing written in between can make them stale. Every entry point
+    // advances the serial.
+    const float* x6_src = nullptr;
+    int x6_rows = 0, x6_cols = 0;
+    unsigned long serial = 0, x6_serial = 0;
     // RoPE denominators theta^(2i / rot) per (theta bits, rot), device copies.
     std::map<std::pair<uint32_t, int>, float*> rope;
     // Profiler (qr_profile / QWEN_ROCM_PROFILE=1): a hipEvent pair on the
@@ -151,22 +160,46 @@ const Context::Prepared* prepared_for(Context* c, const void* a, int rows, int c
     if (it == c->prepared.end() || it->second.rows != rows || it->second.cols != cols) return nullptr;
     return &it->second;
 }
-// x's split planes into c->x6 (grown as needed).
-int split_input(Context* c, const float* x, int cols, int batch) {
+// c->x6 large enough for batch x 6 cols planes (queued work on the old buffer
+// drains first).
+int grow_x6(Context* c, int cols, int batch) {
     const size_t need = size_t(batch) * 6 * size_t(cols);
-    if (need > c->x6_len) {
-        if (c->x6) {
-            (void)hipStreamSynchronize(c->stream);
-            (void)hipFree(c->x6);
-            c->x6 = nullptr;
-            c->x6_len = 0;
-        }
-        auto st = hipMalloc(reinterpret_cast<void**>(&c->x6), need * sizeof(__bf16));
-        if (st != hipSuccess) return fail(c, "hipMalloc split input", int(st));
-        c->x6_len = need;
+    if (need <= c->x6_len) return 0;
+    c->x6_src = nullptr;
+    if (c->x6) {
+        (void)hipStreamSynchronize(c->stream);
+        (void)hipFree(c->x6);
+        c->x6 = nullptr;
+        c->x6_len = 0;
     }
+    auto st = hipMalloc(reinterpret_cast<void**>(&c->x6), need * sizeof(__bf16));
+    if (st != hipSuccess) return fail(c, "hipMalloc split input", int(st));
+    c->x6_len = need;
+    return 0;
+}
+// x's split planes into c->x6: already there when the previous bridge call
+// produced x with them, else split now.
+int split_input(Context* c, const float* x, int cols, int batch) {
+    if (c->x6_src == x && c->x6_rows == batch && c->x6_cols == cols && c->x6_serial + 1 == c->serial) return 0;
+    c->x6_src = nullptr;
+    if (int st = grow_x6(c, cols, batch)) return st;
     auto s = scope(c, [&] { return std::string("split6 ") + shape(batch, cols, 1); });
     return launched(c, "split6", qr::split6(c->stream, c->x6, x, batch, cols, false));
+}
+// Whether a producer of `rows` rows of width `cols` should also write the
+// planes: enough rows for the hipBLASLt path and a prepared matrix of that width.
+bool planes_wanted(Context* c, int cols, int rows) {
+    if (rows < kBlasMinBatch || !c->blas) return false;
+    for (auto& kv : c->prepared)
+        if (kv.second.cols == cols && kv.second.rows > 16) return true;
+    return false;
+}
+// Records that c->x6 now holds src's planes (for the next bridge call).
+void planes_made(Context* c, const float* src, int rows, int cols) {
+    c->x6_src = src;
+    c->x6_rows = rows;
+    c->x6_cols = cols;
+    c->x6_serial = c->serial;
 }
 int blas_project(Context* c, float* y, const Context::Prepared& p, int batch) {
     auto s = scope(c, [&] { return std::string("gemm_f32_blas ") + shape(p.rows, p.cols, batch); });
@@ -295,6 +328,16 @@ int glu(Context* c, qr::WeightType t, float* product, float* gate_y, float* up_y
             if (int st = split_input(c, x, cols, batch)) return st;
             if (int st = blas_project(c, gate_y, *pg, batch)) return st;
             if (int st = blas_project(c, up_y, *pu, batch)) return st;
+            if (planes_wanted(c, rows, batch)) {  // the product's planes for the next call (down)
+                if (int st = grow_x6(c, rows, batch)) return st;
+                auto s = scope(c, [&] { return std::string("silu_split6 ") + shape(rows, batch, 1); });
+                const int st = qr::silu_split6(c->stream, product, gate_y, up_y, c->x6, batch, rows);
+                if (st == 0) {
+                    planes_made(c, product, batch, rows);
+                    return launched(c, "silu_split6", 0);
+                }
+                if (st != int(hipErrorNotSupported)) return launched(c, "silu_split6", st);
+            }
             Params p{};
             p.p[0] = product;
             p.p[1] = gate_y;
@@ -402,6 +445,7 @@ int qr_create(Context** out) {
 }
 
 int qr_set_option(Context* c, const char* name, int value) {
+    ++c->serial;
     if (std::strcmp(name, "attention_f16") != 0 || (value != 0 && value != 1))
         return fail(c, "unknown bridge option", -1);
     if (value) return fail(c, "attention_f16 (16-bit prefill attention) is not offered: attention runs in fp32", -1);
@@ -409,6 +453,7 @@ int qr_set_option(Context* c, const char* name, int value) {
 }
 
 int qr_sync(Context* c) {
+    ++c->serial;
     auto s = hipStreamSynchronize(c->stream);
     if (s != hipSuccess) return fail(c, "hipStreamSynchronize", int(s));
     if (!c->timed.empty()) collect(c);
@@ -418,6 +463,7 @@ int qr_sync(Context* c) {
 // Profiler switch (no counterpart in the reference's ABI; its bridge had the
 // same event-pair profiler behind QWEN_ROCM_PROFILE, native/rocm/bridge.cpp:55-139).
 int qr_profile(Context* c, int on) {
+    ++c->serial;
     if (int s = qr_sync(c)) return s;
     c->profile = on != 0;
     if (on) c->totals.clear();
@@ -427,6 +473,7 @@ int qr_profile(Context* c, int on) {
 // Totals since qr_profile(c, 1) as text lines "calls<TAB>total_ms<TAB>label".
 // Returns the length the full text needs (the text is truncated to `len`).
 long qr_profile_read(Context* c, char* out, size_t len) {
+    ++c->serial;
     if (qr_sync(c)) return -1;
     std::string text;
     for (auto& [label, v] : c->totals) {
@@ -474,6 +521,7 @@ void qr_destroy(Context* c) {
 }
 
 int qr_alloc(Context* c, float** p, size_t n) {
+    ++c->serial;
     if (n == 0) return fail(c, "empty allocation", -1);
     auto s = hipMalloc(reinterpret_cast<void**>(p), n * sizeof(float));
     if (s != hipSuccess) return fail(c, "hipMalloc", int(s));
@@ -487,11 +535,13 @@ int qr_alloc(Context* c, float** p, size_t n) {
 }
 
 void qr_free(Context* c, float* p) {
+    ++c->serial;
     if (!c->prepared.empty()) invalidate_prepared(c, p, 1);
     (void)hipFree(p);
 }
 
 int qr_write(Context* c, float* p, const float* host, size_t n) {
+    ++c->serial;
     if (!c->prepared.empty()) invalidate_prepared(c, p, n);
     auto s = hipMemcpyAsync(p, host, n * sizeof(float), hipMemcpyHostToDevice, c->stream);
     if (s != hipSuccess) return fail(c, "H2D", int(s));
@@ -499,12 +549,14 @@ int qr_write(Context* c, float* p, const float* host, size_t n) {
 }
 
 int qr_read(Context* c, float* host, const float* p, size_t n) {
+    ++c->serial;
     auto s = hipMemcpyAsync(host, p, n * sizeof(float), hipMemcpyDeviceToHost, c->stream);
     if (s != hipSuccess) return fail(c, "D2H", int(s));
     return qr_sync(c);
 }
 
 int qr_copy(Context* c, float* dest, const float* src, size_t n) {
+    ++c->serial;
     if (!c->prepared.empty()) invalidate_prepared(c, dest, n);
     auto sc = scope(c, [&] { return std::string("copy"); });
     auto s = hipMemcpyAsync(dest, src, n * sizeof(float), hipMemcpyDeviceToDevice, c->stream);
@@ -512,6 +564,7 @@ int qr_copy(Context* c, float* dest, const float* src, size_t n) {
 }
 
 int qr_run(Context* c, int op, int count, const Params* ap) {
+    ++c->serial;
     if (op < QR_RMS_NORM || op > QR_EMBED_BF16_PICKED || count < 1 || !ap) return fail(c, "invalid kernel", -1);
     const Params& a = *ap;
     hipStream_t s = c->stream;
@@ -522,6 +575,15 @@ int qr_run(Context* c, int op, int count, const Params* ap) {
     case QR_ADD_RMS_NORM:
     case QR_RMS_NORM_GATE:
         if (a.n[0] < 1) return fail(c, "norm shape", -1);
+        if (op != QR_RMS_NORM_GATE && planes_wanted(c, a.n[0], count)) {  // the normed rows' planes too
+            if (int st = grow_x6(c, a.n[0], count)) return st;
+            const int st = qr::run_rms_family_planes(s, op, count, a, c->x6);
+            if (st == 0) {
+                planes_made(c, op == QR_ADD_RMS_NORM ? a.p[3] : a.p[0], count, a.n[0]);
+                return launched(c, "rms_norm", 0);
+            }
+            if (st != int(hipErrorNotSupported)) return launched(c, "rms_norm", st);
+        }
         return launched(c, "rms_norm", qr::run_rms_family(s, op, count, a));
     case QR_ADD:
     case QR_SILU_PRODUCT:
@@ -563,36 +625,46 @@ int qr_run(Context* c, int op, int count, const Params* ap) {
 }
 
 int qr_gemv(Context* c, float* y, const float* a, const float* x, int rows, int cols) {
+    ++c->serial;
     return project(c, qr::WeightType::F32, y, a, x, rows, cols, 1);
 }
 int qr_gemm(Context* c, float* y, const float* a, const float* x, int rows, int cols, int batch) {
+    ++c->serial;
     return project(c, qr::WeightType::F32, y, a, x, rows, cols, batch);
 }
 int qr_gemv_bf16(Context* c, float* y, const float* packed, const float* x, int rows, int cols) {
+    ++c->serial;
     return project(c, qr::WeightType::BF16, y, packed, x, rows, cols, 1);
 }
 int qr_gemm_bf16(Context* c, float* y, const float* packed, const float* x, int rows, int cols, int batch) {
+    ++c->serial;
     return project(c, qr::WeightType::BF16, y, packed, x, rows, cols, batch);
 }
 int qr_gemm_i8(Context* c, float* y, const float* packed, const float* x, int rows, int cols, int batch) {
+    ++c->serial;
     return project(c, qr::WeightType::I8, y, i8_packed(packed), x, rows, cols, batch);
 }
 
 int qr_gemm_f32_group(Context* c, int n, const QrProjection* items, const float* x, int cols, int batch) {
+    ++c->serial;
     return group(c, qr::WeightType::F32, n, items, x, cols, batch);
 }
 int qr_gemm_bf16_group(Context* c, int n, const QrProjection* items, const float* x, int cols, int batch) {
+    ++c->serial;
     return group(c, qr::WeightType::BF16, n, items, x, cols, batch);
 }
 int qr_gemm_i8_group(Context* c, int n, const QrProjection* items, const float* x, int cols, int batch) {
+    ++c->serial;
     return group(c, qr::WeightType::I8, n, items, x, cols, batch);
 }
 
 int qr_gemm_f32_glu(Context* c, float* product, float* gate_y, float* up_y, const float* gate, const float* up,
                     const float* x, int rows, int cols, int batch) {
+    ++c->serial;
     return glu(c, qr::WeightType::F32, product, gate_y, up_y, gate, up, x, rows, cols, batch);
 }
 int qr_gemm_f32_prepare(Context* c, const float* a, int rows, int cols) {
+    ++c->serial;
     if (!a || rows < 1 || cols < 4 || cols % 4 != 0 || reinterpret_cast<uintptr_t>(a) % 16 != 0)
         return fail(c, "GEMM prepare shape", -1);
     auto it = c->prepared.find(a);
@@ -613,33 +685,40 @@ int qr_gemm_f32_prepare(Context* c, const float* a, int rows, int cols) {
     return 0;
 }
 int qr_gemm_f32_release(Context* c, const float* a) {
+    ++c->serial;
     auto it = c->prepared.find(a);
     if (it != c->prepared.end()) drop_prepared(c, it);
     return 0;
 }
 int qr_gemm_bf16_glu(Context* c, float* product, float* gate_y, float* up_y, const float* gate, const float* up,
                      const float* x, int rows, int cols, int batch) {
+    ++c->serial;
     return glu(c, qr::WeightType::BF16, product, gate_y, up_y, gate, up, x, rows, cols, batch);
 }
 int qr_gemm_i8_glu(Context* c, float* product, float* gate_y, float* up_y, const float* gate, const float* up,
                    const float* x, int rows, int cols, int batch) {
+    ++c->serial;
     return glu(c, qr::WeightType::I8, product, gate_y, up_y, gate, up, x, rows, cols, batch);
 }
 
 int qr_gemm_f32_add_norm(Context* c, float* y, const float* a, const float* x, int rows, int cols,
                          const QrAddNormPost* post) {
+    ++c->serial;
     return add_norm(c, qr::WeightType::F32, y, a, x, rows, cols, post);
 }
 int qr_gemm_bf16_add_norm(Context* c, float* y, const float* packed, const float* x, int rows, int cols,
                           const QrAddNormPost* post) {
+    ++c->serial;
     return add_norm(c, qr::WeightType::BF16, y, packed, x, rows, cols, post);
 }
 int qr_gemm_i8_add_norm(Context* c, float* y, const float* packed, const float* x, int rows, int cols,
                         const QrAddNormPost* post) {
+    ++c->serial;
     return add_norm(c, qr::WeightType::I8, y, packed, x, rows, cols, post);
 }
 
 int qr_delta_mixer(Context* c, const QrDelta* d) {
+    ++c->serial;
     if (!d || d->tokens < 1 || d->value_heads < 1 || d->key_heads < 1 || d->value_heads % d->key_heads != 0)
         return fail(c, "delta mixer shape", -1);
     if (qr::delta_mixer_decode_ok(*d)) {
@@ -693,6 +772,7 @@ int qr_delta_mixer(Context* c, const QrDelta* d) {
 
 // Argmax with fixed partials (no counterpart in the reference's ABI).
 int qr_argmax_fixed(Context* c, int rows, const Params* ap) {
+    ++c->serial;
     if (!ap) return fail(c, "argmax arguments", -1);
     const Params& a = *ap;
     if (rows < 1 || rows > qr::kArgmaxFixedRows || a.n[0] < 1 || a.n[0] > qr::kArgmaxFixedLength)
@@ -703,6 +783,7 @@ int qr_argmax_fixed(Context* c, int rows, const Params* ap) {
 
 // One-launch decode (no counterpart in the reference's ABI).
 int qr_decode_plan(Context* c, const QrDecodeDesc* d, QrDecodePlan** out) {
+    ++c->serial;
     if (!d || !out) return fail(c, "decode plan arguments", -1);
     const char* why = nullptr;
     int s = qr::decode_plan_create(*d, out, c->stream, &why);
@@ -713,18 +794,21 @@ int qr_decode_plan(Context* c, const QrDecodeDesc* d, QrDecodePlan** out) {
     return 0;
 }
 int qr_decode_step(Context* c, QrDecodePlan* p, int token, int position) {
+    ++c->serial;
     if (!p) return fail(c, "decode step without a plan", -1);
     auto sc = scope(c, [&] { return std::string("decode_step"); });
     if (token < 0) return fail(c, "decode step token", -1);
     return launched(c, "decode step", qr::decode_step(p, token, position, -1, c->stream));
 }
 int qr_decode_step_row(Context* c, QrDecodePlan* p, int token, int position, int row, int snap) {
+    ++c->serial;
     if (!p) return fail(c, "decode step without a plan", -1);
     auto sc = scope(c, [&] { return std::string("decode_step"); });
     if (token < 0 || row < 0 || snap < 0) return fail(c, "decode step token / row / snapshot", -1);
     return launched(c, "decode step", qr::decode_step(p, token, position, -1, c->stream, row, snap));
 }
 int qr_decode_steps(Context* c, QrDecodePlan* p, int first_token, int position, int n, int32_t* ids, float* bad) {
+    ++c->serial;
     if (!p || !ids || !bad || n < 1 || first_token < 0 || position < 0) return fail(c, "decode steps shape", -1);
     int e = qr::decode_history_clear(p, n, c->stream);
     if (e) return launched(c, "decode steps", e);
@@ -747,12 +831,14 @@ int qr_decode_steps(Context* c, QrDecodePlan* p, int first_token, int position, 
     return 0;
 }
 void qr_decode_plan_free(Context* c, QrDecodePlan* p) {
+    ++c->serial;
     if (c) (void)hipStreamSynchronize(c->stream);
     qr::decode_plan_free(p);
 }
 
 int qr_embed_rows(Context* c, float* dst, const float* table, int table_rows, int width, int bf16,
                   const int32_t* ids, int n) {
+    ++c->serial;
     if (!dst || !table || !ids || width < 1 || n < 1) return fail(c, "embed_rows shape", -1);
     for (int r = 0; r < n; ++r)
         if (ids[r] < 0 || ids[r] >= table_rows) return fail(c, "embed_rows id out of range", -1);

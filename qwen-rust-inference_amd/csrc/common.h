@@ -88,6 +88,10 @@ bool gemm_preferred(WeightType t, int rows, int cols, int batch);
 // every row laid out for one BF16 GEMM with K' = 6 K (weight: the W order
 // [w0 w1 w2 w0 w1 w0], else the X order [x2 x1 x0 x1 x0 x0]); cols % 4 == 0.
 int split6(hipStream_t s, __bf16* out, const float* in, int rows, int cols, bool weight);
+// prod = silu(g) * u (rows x cols) and prod's split6 planes (activation order)
+// in one pass; hipErrorNotSupported (nothing launched) unless cols % 8 == 0 and
+// every pointer is 16-byte aligned.
+int silu_split6(hipStream_t s, float* prod, const float* g, const float* u, __bf16* out, int rows, int cols);
 // Y[batch, rows] = X6 W6^T on hipBLASLt (BF16 inputs, fp32 accumulation and
 // output) for K'-concatenated planes of split6: the fp32 product X W^T to
 // fp32 accuracy. One Blas per bridge context; the algorithm of each shape is
@@ -110,6 +114,10 @@ int gemm_glu(hipStream_t s, WeightType t, float* product, const void* gate, cons
 // ops.hip --------------------------------------------------------------------
 int run_elementwise(hipStream_t s, int op, int count, const Params& a);
 int run_rms_family(hipStream_t s, int op, int groups, const Params& a);
+// RmsNorm / AddRmsNorm whose normed rows are also written as split6 planes
+// (rows x 6 d BF16, activation order); hipErrorNotSupported (nothing launched)
+// when the op, width or alignment has no such form.
+int run_rms_family_planes(hipStream_t s, int op, int groups, const Params& a, __bf16* planes);
 int run_conv_silu(hipStream_t s, int count, const Params& a);
 int run_delta_qk(hipStream_t s, int count, const Params& a);
 int run_delta_rule(hipStream_t s, bool gated, int count, const Params& a);

@@ -103,10 +103,14 @@ __global__ __launch_bounds__(256) void rms_family_kernel(int op, int groups, Par
 // j < PER / V), so every load and store of a wave is one contiguous run and
 // each input is read once (the block form above reads a group twice and
 // waits on two block barriers).
+// planes (may be null): the output rows also as the K'-concatenated BF16
+// planes a prepared projection takes (row g: 6 segments of d, segment b the
+// split part {2, 1, 0, 1, 0, 0}[b] of x = x0 + x1 + x2; as split6 of gemm.hip).
 template <int PER>
-__global__ __launch_bounds__(256) void rms_rows_kernel(int op, int groups, Params a) {
+__global__ __launch_bounds__(256) void rms_rows_kernel(int op, int groups, Params a, __bf16* planes) {
     constexpr int V = PER >= 4 ? 4 : PER, NV = PER / V;
     typedef float fv __attribute__((ext_vector_type(V)));
+    typedef __bf16 hv __attribute__((ext_vector_type(V)));
     const int g = int(blockIdx.x) * 4 + int(threadIdx.x >> 6);
     if (g >= groups) return;  // whole waves only: no block barrier
     const int lane = int(threadIdx.x & 63), d = 64 * PER;
@@ -142,6 +146,20 @@ __global__ __launch_bounds__(256) void rms_rows_kernel(int op, int groups, Param
             for (int e = 0; e < V; ++e) y[e] = siluf_(z[e]) * y[e];
         }
         *reinterpret_cast<fv*>(out + off + c) = y;
+        if (planes) {
+            hv h[3];
+#pragma unroll
+            for (int e = 0; e < V; ++e) {
+                h[0][e] = __bf16(y[e]);
+                const float r1 = y[e] - float(h[0][e]);
+                h[1][e] = __bf16(r1);
+                h[2][e] = __bf16(r1 - float(h[1][e]));
+            }
+            constexpr int XP[6] = {2, 1, 0, 1, 0, 0};
+            __bf16* row = planes + size_t(g) * 6 * d + c;
+#pragma unroll
+            for (int b = 0; b < 6; ++b) *reinterpret_cast<hv*>(row + b * d) = h[XP[b]];
+        }
     }
 }
 
@@ -535,26 +553,35 @@ int run_elementwise(hipStream_t s, int op, int count, const Params& a) {
 // The register form when the group is 64 PER elements and every operand is
 // aligned to its vector width.
 template <int PER>
-bool launch_rms_rows(hipStream_t s, int op, int groups, const Params& a) {
+bool launch_rms_rows(hipStream_t s, int op, int groups, const Params& a, __bf16* planes) {
     constexpr uintptr_t align = (PER >= 4 ? 4 : PER) * sizeof(float);
     const int slots[] = {0, 1, 2, 3, 4};
     const int used = op == QR_ADD_RMS_NORM ? 5 : op == QR_RMS_NORM_GATE ? 4 : 3;
     for (int k = 0; k < used; ++k)
         if (reinterpret_cast<uintptr_t>(a.p[slots[k]]) % align != 0) return false;
-    hipLaunchKernelGGL(rms_rows_kernel<PER>, dim3(ceil_div(groups, 4)), dim3(256), 0, s, op, groups, a);
+    if (planes && reinterpret_cast<uintptr_t>(planes) % (align / 2) != 0) return false;
+    hipLaunchKernelGGL(rms_rows_kernel<PER>, dim3(ceil_div(groups, 4)), dim3(256), 0, s, op, groups, a, planes);
     return true;
+}
+bool launch_rms_rows_any(hipStream_t s, int op, int groups, const Params& a, __bf16* planes) {
+    switch (a.n[0]) {
+    case 128: return launch_rms_rows<2>(s, op, groups, a, planes);
+    case 256: return launch_rms_rows<4>(s, op, groups, a, planes);
+    case 512: return launch_rms_rows<8>(s, op, groups, a, planes);
+    case 1024: return launch_rms_rows<16>(s, op, groups, a, planes);
+    case 2048: return launch_rms_rows<32>(s, op, groups, a, planes);
+    }
+    return false;
+}
+
+int run_rms_family_planes(hipStream_t s, int op, int groups, const Params& a, __bf16* planes) {
+    if (op != QR_RMS_NORM && op != QR_ADD_RMS_NORM) return int(hipErrorNotSupported);
+    if (!launch_rms_rows_any(s, op, groups, a, planes)) return int(hipErrorNotSupported);
+    return int(hipGetLastError());
 }
 
 int run_rms_family(hipStream_t s, int op, int groups, const Params& a) {
-    bool done = false;
-    switch (a.n[0]) {
-    case 128: done = launch_rms_rows<2>(s, op, groups, a); break;
-    case 256: done = launch_rms_rows<4>(s, op, groups, a); break;
-    case 512: done = launch_rms_rows<8>(s, op, groups, a); break;
-    case 1024: done = launch_rms_rows<16>(s, op, groups, a); break;
-    case 2048: done = launch_rms_rows<32>(s, op, groups, a); break;
-    }
-    if (done) return int(hipGetLastError());
+    if (launch_rms_rows_any(s, op, groups, a, nullptr)) return int(hipGetLastError());
     if (a.n[0] <= 256)
         hipLaunchKernelGGL(rms_family_kernel<true>, dim3(ceil_div(groups, 4)), dim3(256), 0, s, op, groups, a);
     else

@@ -230,6 +230,64 @@ def test_prepared_group_glu_and_invalidation(gpu):
     gpu.release(mats[1])  # releasing twice (or an unprepared matrix) is accepted
 
 
+def test_planes_from_producers(gpu):
+    """A norm over >= 64 rows whose width a prepared matrix takes, and a
+    prepared GLU whose product width one does, leave their output's split
+    planes for the very next call: that projection equals the same projection
+    of a copy (split afresh) bitwise. Any call in between (here a sync or a
+    write into the output) makes the next projection split again, so it
+    follows what the buffer holds then."""
+    rng = np.random.default_rng(11)
+    h, inter, batch = 1024, 3584, 130
+    w_in = gpu.upload((rng.standard_normal(2048 * h) * 0.02).astype(np.float32))
+    gate = gpu.upload((rng.standard_normal(inter * h) * 0.02).astype(np.float32))
+    up = gpu.upload((rng.standard_normal(inter * h) * 0.02).astype(np.float32))
+    down = gpu.upload((rng.standard_normal(h * inter) * 0.02).astype(np.float32))
+    gpu.prepare(w_in, 2048, h)
+    gpu.prepare(gate, inter, h)
+    gpu.prepare(up, inter, h)
+    gpu.prepare(down, h, inter)
+    x = gpu.upload(rng.standard_normal(batch * h).astype(np.float32))
+    res = gpu.upload(rng.standard_normal(batch * h).astype(np.float32))
+    nw = gpu.upload((rng.standard_normal(h) * 0.1).astype(np.float32))
+
+    def proj_of_copy(src, a, rows, cols):
+        cp, out = gpu.alloc(batch * cols), gpu.alloc(batch * rows)
+        gpu.copy(cp, src, batch * cols)
+        gpu.gemm(out, a, cp, rows, cols, batch)
+        return out.read()
+
+    # RmsNorm -> projection
+    y = gpu.alloc(batch * h)
+    gpu.run("RMS_NORM", batch, [y, x, nw], [h], [1e-6, 1.0])
+    out = gpu.alloc(batch * 2048)
+    gpu.gemm(out, w_in, y, 2048, h, batch)
+    assert np.array_equal(out.read(), proj_of_copy(y, w_in, 2048, h))
+    # AddRmsNorm -> GLU -> down projection
+    s_, y2 = gpu.alloc(batch * h), gpu.alloc(batch * h)
+    gpu.run("ADD_RMS_NORM", batch, [s_, x, res, y2, nw], [h], [1e-6, 1.0])
+    prod, gy, uy = gpu.alloc(batch * inter), gpu.alloc(batch * inter), gpu.alloc(batch * inter)
+    gpu.glu(prod, gy, uy, gate, up, y2, inter, h, batch)
+    o1 = gpu.alloc(batch * h)
+    gpu.gemm(o1, down, prod, h, inter, batch)
+    o2 = gpu.alloc(batch * h)
+    gpu.sync()  # a call in between: the down projection splits the product again
+    gpu.gemm(o2, down, prod, h, inter, batch)
+    assert np.array_equal(o1.read(), o2.read())
+    assert np.array_equal(o1.read(), proj_of_copy(prod, down, h, inter))
+    gv, uv = gy.read().astype(np.float64), uy.read().astype(np.float64)
+    parity(prod.read(), gv / (1 + np.exp(-gv)) * uv, where="glu product with planes")
+    # a write between the norm and the projection: the projection follows the new values
+    gpu.run("RMS_NORM", batch, [y, x, nw], [h], [1e-6, 1.0])
+    new = rng.standard_normal(batch * h).astype(np.float32)
+    y.write(new)
+    gpu.gemm(out, w_in, y, 2048, h, batch)
+    X = new.reshape(batch, h)[:8].astype(np.float64)
+    W = w_in.read().reshape(2048, h).astype(np.float64)
+    bound = np.abs(X) @ np.abs(W.T) * 2e-5 + 1e-30
+    assert np.all(np.abs(out.read().reshape(batch, 2048)[:8] - X @ W.T) <= bound)
+
+
 @pytest.mark.parametrize("kind", ["f32", "bf16", "i8"])
 @pytest.mark.parametrize("rows,cols", [(1024, 2048), (1024, 3584), (64, 256), (8, 16)])
 def test_add_norm_tail(gpu, cpu, kind, rows, cols):
