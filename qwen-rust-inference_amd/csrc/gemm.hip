@@ -370,14 +370,29 @@ __global__ __launch_bounds__(512) void gemm_ab_kernel(AbMats m, const float* x, 
         wv[e] = r < rows && k < cols ? *reinterpret_cast<const f4v*>(m.a[mi] + size_t(rr) * cols + k)
                                      : f4v{0.f, 0.f, 0.f, 0.f};
     }
+    // the x rows of a round: this thread's float4 i = threadIdx.x + 512 j of
+    // the round's AB_TOK x AB_COLS block, loaded one round ahead
+    constexpr int XL = AB_TOK * AB_COLS / 4 / 512;
+    auto load_x = [&](int g, f4v (&v)[XL]) {
+#pragma unroll
+        for (int j = 0; j < XL; ++j) {
+            const int i = int(threadIdx.x) + 512 * j, t = i / (AB_COLS / 4), k = 4 * (i % (AB_COLS / 4));
+            v[j] = g * AB_TOK + t < batch && k < cols
+                       ? *reinterpret_cast<const f4v*>(x + size_t(g * AB_TOK + t) * cols + k)
+                       : f4v{0.f, 0.f, 0.f, 0.f};
+        }
+    };
+    f4v xn[XL];
+    load_x(int(blockIdx.x), xn);
     for (int g = int(blockIdx.x); g * AB_TOK < batch; g += int(gridDim.x)) {
         const int t0 = g * AB_TOK;
-        for (int i = int(threadIdx.x); i < AB_TOK * AB_COLS / 4; i += 512) {
-            const int t = i / (AB_COLS / 4), k = 4 * (i % (AB_COLS / 4));
-            xs[t][k / 4] = t0 + t < batch && k < cols ? *reinterpret_cast<const f4v*>(x + size_t(t0 + t) * cols + k)
-                                                      : f4v{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int j = 0; j < XL; ++j) {
+            const int i = int(threadIdx.x) + 512 * j;
+            xs[i / (AB_COLS / 4)][i % (AB_COLS / 4)] = xn[j];
         }
         __syncthreads();
+        load_x(g + int(gridDim.x), xn);  // the next round's rows stream in while this one is summed
 #pragma unroll
         for (int t = 0; t < AB_TOK; ++t) {
             float acc = 0.f;
@@ -392,6 +407,9 @@ __global__ __launch_bounds__(512) void gemm_ab_kernel(AbMats m, const float* x, 
             part[t][slot][r] = acc;
         }
         __syncthreads();
+        // no barrier after the sums: the next round writes xs only after every
+        // wave has passed the barrier above (all xs reads done) and part only
+        // after the next round's first barrier (all sums of this round done)
         if (int(threadIdx.x) < AB_TOK * AB_ROWS) {
             const int t = int(threadIdx.x) / AB_ROWS, o = int(threadIdx.x) % AB_ROWS;
             if (o < rows && t0 + t < batch) {
@@ -401,9 +419,9 @@ __global__ __launch_bounds__(512) void gemm_ab_kernel(AbMats m, const float* x, 
                 m.y[oi][size_t(t0 + t) * m.rows[oi] + orow] = sum;
             }
         }
-        __syncthreads();
     }
 }
+
 
 // The K'-concatenated BF16 planes of an fp32 matrix for one BF16 GEMM with
 // K' = 6 K whose products are the six part products of the three-way split:

@@ -259,6 +259,22 @@ __global__ __launch_bounds__(256) void conv_history_kernel(int count, Params a) 
 // ---------------------------------------------------------------- DeltaQk (5)
 // reference.h:134-143: per (token, value head) the L2-normalised query (then
 // / sqrt(d)) and key of its key head. One wave per item.
+// DeltaQk for d = 128 with each row in registers: lane l holds elements
+// 2 l, 2 l + 1 of q and of k (one 8-byte load each, the row read once).
+__global__ __launch_bounds__(256) void delta_qk_pairs_kernel(int count, Params a) {
+    typedef float f2 __attribute__((ext_vector_type(2)));
+    const int t = blockIdx.x * 4 + int(threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (t >= count) return;
+    constexpr int d = 128;
+    const int kh = a.n[0], vh = a.n[1], h = (t % vh) / (vh / kh), kd = kh * d;
+    const float* x = a.p[1] + size_t(t / vh) * a.n[3];
+    const f2 q = *reinterpret_cast<const f2*>(x + h * d + 2 * lane);
+    const f2 k = *reinterpret_cast<const f2*>(x + kd + h * d + 2 * lane);
+    const float sq = wave_sum(q.x * q.x + q.y * q.y), sk = wave_sum(k.x * k.x + k.y * k.y);
+    const float rq = 1.f / sqrtf(sq + 1e-6f), rk = 1.f / sqrtf(sk + 1e-6f), sd = sqrtf(float(d));
+    *reinterpret_cast<f2*>(a.p[0] + size_t(t) * d + 2 * lane) = f2{(q.x * rq) / sd, (q.y * rq) / sd};
+    *reinterpret_cast<f2*>(a.p[2] + size_t(t) * d + 2 * lane) = f2{k.x * rk, k.y * rk};
+}
 __global__ __launch_bounds__(256) void delta_qk_kernel(int count, Params a) {
     const int t = blockIdx.x * 4 + int(threadIdx.x >> 6), lane = threadIdx.x & 63;
     if (t >= count) return;
@@ -608,6 +624,12 @@ int run_conv_silu(hipStream_t s, int count, const Params& a) {
 }
 
 int run_delta_qk(hipStream_t s, int count, const Params& a) {
+    const uintptr_t al = reinterpret_cast<uintptr_t>(a.p[0]) | reinterpret_cast<uintptr_t>(a.p[1]) |
+                         reinterpret_cast<uintptr_t>(a.p[2]);
+    if (a.n[2] == 128 && al % 8 == 0 && a.n[3] % 2 == 0) {
+        hipLaunchKernelGGL(delta_qk_pairs_kernel, dim3(ceil_div(count, 4)), dim3(256), 0, s, count, a);
+        return int(hipGetLastError());
+    }
     hipLaunchKernelGGL(delta_qk_kernel, dim3(ceil_div(count, 4)), dim3(256), 0, s, count, a);
     return int(hipGetLastError());
 }

@@ -442,7 +442,8 @@ def test_conv_silu(gpu, cpu, k, tokens, snaps):
     parity(g[3], c[3], where="conv history")
 
 
-@pytest.mark.parametrize("kh,vh,d,tokens", [(16, 16, 128, 1), (16, 16, 128, 3), (2, 4, 3, 1), (4, 4, 16, 2)])
+@pytest.mark.parametrize("kh,vh,d,tokens", [(16, 16, 128, 1), (16, 16, 128, 3), (2, 4, 3, 1), (4, 4, 16, 2),
+                                             (8, 16, 128, 37)])
 def test_delta_qk(gpu, cpu, kh, vh, d, tokens):
     rng = np.random.default_rng(d + tokens)
     stride = 2 * kh * d + vh * d
