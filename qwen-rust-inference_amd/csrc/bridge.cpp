@@ -35,6 +35,16 @@ struct Context {
         __bf16* w6;
     };
     std::map<const float*, Prepared> prepared;
+    // A prepared GLU's gate and up planes side by side ([gate; up]: 2 rows x 6
+    // cols), made on the pair's first prefill GLU, so both projections run as one
+    // GEMM into glu_tmp ([batch][2 rows]); dropped with either matrix's planes.
+    struct GluPair {
+        int rows, cols;
+        __bf16* w6;
+    };
+    std::map<std::pair<const float*, const float*>, GluPair> glu_pairs;
+    float* glu_tmp = nullptr;
+    size_t glu_tmp_len = 0;
     qr::Blas* blas = nullptr;
     __bf16* x6 = nullptr;  // the split planes of a projection's input
     size_t x6_len = 0;     // in BF16 elements
@@ -207,6 +217,14 @@ int blas_project(Context* c, float* y, const Context::Prepared& p, int batch) {
 }
 void drop_prepared(Context* c, std::map<const float*, Context::Prepared>::iterator it) {
     (void)hipStreamSynchronize(c->stream);  // queued GEMMs may still read the planes
+    for (auto p = c->glu_pairs.begin(); p != c->glu_pairs.end();) {  // pairs holding a copy of them
+        auto next = std::next(p);
+        if (p->first.first == it->first || p->first.second == it->first) {
+            (void)hipFree(p->second.w6);
+            c->glu_pairs.erase(p);
+        }
+        p = next;
+    }
     (void)hipFree(it->second.w6);
     c->prepared.erase(it);
 }
@@ -324,20 +342,50 @@ int glu(Context* c, qr::WeightType t, float* product, float* gate_y, float* up_y
     if (t == qr::WeightType::F32) {
         const Context::Prepared* pg = prepared_for(c, gate, rows, cols, batch);
         const Context::Prepared* pu = prepared_for(c, up, rows, cols, batch);
+        if (pg && pu && rows % 8 == 0) {
+            // gate and up as ONE hipBLASLt GEMM over their planes side by side into glu_tmp
+            // (gate_y / up_y untouched, as the fused GLU), then silu(gate) * up from it
+            auto key = std::make_pair(gate, up);
+            auto it = c->glu_pairs.find(key);
+            if (it == c->glu_pairs.end()) {
+                const size_t half = size_t(rows) * 6 * size_t(cols);
+                Context::GluPair pair{rows, cols, nullptr};
+                auto st = hipMalloc(reinterpret_cast<void**>(&pair.w6), 2 * half * sizeof(__bf16));
+                if (st != hipSuccess) return fail(c, "hipMalloc GLU planes", int(st));
+                st = hipMemcpyAsync(pair.w6, pg->w6, half * sizeof(__bf16), hipMemcpyDeviceToDevice, c->stream);
+                if (st == hipSuccess)
+                    st = hipMemcpyAsync(pair.w6 + half, pu->w6, half * sizeof(__bf16), hipMemcpyDeviceToDevice,
+                                        c->stream);
+                if (st != hipSuccess) {
+                    (void)hipStreamSynchronize(c->stream);
+                    (void)hipFree(pair.w6);
+                    return fail(c, "GLU planes copy", int(st));
+                }
+                it = c->glu_pairs.emplace(key, pair).first;
+            }
+            if (int st = split_input(c, x, cols, batch)) return st;
+            if (int st = ensure(c, &c->glu_tmp, &c->glu_tmp_len, size_t(batch) * 2 * size_t(rows), "hipMalloc GLU"))
+                return st;
+            {
+                auto s = scope(c, [&] { return std::string("gemm_f32_blas_glu 2x") + shape(rows, cols, batch); });
+                if (int st = launched(c, "hipBLASLt GEMM", qr::blas_gemm6(c->blas, c->stream, c->glu_tmp,
+                                                                            it->second.w6, c->x6, 2 * rows, cols,
+                                                                            batch)))
+                    return st;
+            }
+            const bool planes = planes_wanted(c, rows, batch);  // the product's planes for the next call (down)
+            if (planes)
+                if (int st = grow_x6(c, rows, batch)) return st;
+            auto s = scope(c, [&] { return std::string("silu_split6 ") + shape(rows, batch, 1); });
+            const int st = qr::silu_split6(c->stream, product, c->glu_tmp, c->glu_tmp + rows, 2 * rows,
+                                           planes ? c->x6 : nullptr, batch, rows);
+            if (st == 0 && planes) planes_made(c, product, batch, rows);
+            return launched(c, "silu_split6", st);
+        }
         if (pg && pu) {  // gate and up on hipBLASLt into gate_y / up_y, then silu(gate_y) * up_y
             if (int st = split_input(c, x, cols, batch)) return st;
             if (int st = blas_project(c, gate_y, *pg, batch)) return st;
             if (int st = blas_project(c, up_y, *pu, batch)) return st;
-            if (planes_wanted(c, rows, batch)) {  // the product's planes for the next call (down)
-                if (int st = grow_x6(c, rows, batch)) return st;
-                auto s = scope(c, [&] { return std::string("silu_split6 ") + shape(rows, batch, 1); });
-                const int st = qr::silu_split6(c->stream, product, gate_y, up_y, c->x6, batch, rows);
-                if (st == 0) {
-                    planes_made(c, product, batch, rows);
-                    return launched(c, "silu_split6", 0);
-                }
-                if (st != int(hipErrorNotSupported)) return launched(c, "silu_split6", st);
-            }
             Params p{};
             p.p[0] = product;
             p.p[1] = gate_y;
@@ -514,6 +562,8 @@ void qr_destroy(Context* c) {
     if (c->rule_chunks) (void)hipFree(c->rule_chunks);
     if (c->gemm_work) (void)hipFree(c->gemm_work);
     for (auto& kv : c->prepared) (void)hipFree(kv.second.w6);
+    for (auto& kv : c->glu_pairs) (void)hipFree(kv.second.w6);
+    if (c->glu_tmp) (void)hipFree(c->glu_tmp);
     if (c->x6) (void)hipFree(c->x6);
     qr::blas_destroy(c->blas);
     (void)hipStreamDestroy(c->stream);

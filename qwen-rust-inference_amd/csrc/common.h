@@ -88,10 +88,11 @@ bool gemm_preferred(WeightType t, int rows, int cols, int batch);
 // every row laid out for one BF16 GEMM with K' = 6 K (weight: the W order
 // [w0 w1 w2 w0 w1 w0], else the X order [x2 x1 x0 x1 x0 x0]); cols % 4 == 0.
 int split6(hipStream_t s, __bf16* out, const float* in, int rows, int cols, bool weight);
-// prod = silu(g) * u (rows x cols) and prod's split6 planes (activation order)
-// in one pass; hipErrorNotSupported (nothing launched) unless cols % 8 == 0 and
-// every pointer is 16-byte aligned.
-int silu_split6(hipStream_t s, float* prod, const float* g, const float* u, __bf16* out, int rows, int cols);
+// prod = silu(g) * u (rows x cols; g and u rows ld apart) and, when out is not
+// null, prod's split6 planes (activation order), in one pass;
+// hipErrorNotSupported (nothing launched) unless cols % 8 == 0, ld % 4 == 0
+// and every pointer is 16-byte aligned.
+int silu_split6(hipStream_t s, float* prod, const float* g, const float* u, int ld, __bf16* out, int rows, int cols);
 // Y[batch, rows] = X6 W6^T on hipBLASLt (BF16 inputs, fp32 accumulation and
 // output) for K'-concatenated planes of split6: the fp32 product X W^T to
 // fp32 accuracy. One Blas per bridge context; the algorithm of each shape is

@@ -473,25 +473,26 @@ size_t gemm_scratch(WeightType t, int rows, int cols, int batch) {
     return splits > 1 ? size_t(splits) * size_t(rows) * size_t(batch) : 0;
 }
 
-// SiluProduct (reference.h SILU_PRODUCT) of a prefill GLU whose product feeds
-// a prepared projection: the fp32 product and its split6 planes (activation
-// order) in one pass, one thread per 8 consecutive elements of a row
-// (cols % 8 == 0), the grid over all rows.
-__global__ __launch_bounds__(256) void silu_split6_kernel(float* prod, const float* g, const float* u, __bf16* out,
-                                                          int cols, long chunks) {
+// SiluProduct (reference.h SILU_PRODUCT) of a prefill GLU from the rows of the
+// gate and up outputs (row stride ld), one thread per 8 consecutive elements
+// of a row (cols % 8 == 0), the grid over all rows; when `out` is set, the
+// product's split6 planes (activation order) too, for the projection after.
+__global__ __launch_bounds__(256) void silu_split6_kernel(float* prod, const float* g, const float* u, int ld,
+                                                          __bf16* out, int cols, long chunks) {
     constexpr int XP[6] = {2, 1, 0, 1, 0, 0};
     const int per_row = cols / 8;
     for (long c = blockIdx.x * long(blockDim.x) + threadIdx.x; c < chunks; c += long(gridDim.x) * blockDim.x) {
-        const size_t r = size_t(c / per_row), k = size_t(c % per_row) * 8, e0 = r * cols + k;
+        const size_t r = size_t(c / per_row), k = size_t(c % per_row) * 8, e0 = r * cols + k, i0 = r * ld + k;
         f4v v[2];
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
-            const f4v gv = *reinterpret_cast<const f4v*>(g + e0 + 4 * h);
-            const f4v uv = *reinterpret_cast<const f4v*>(u + e0 + 4 * h);
+            const f4v gv = *reinterpret_cast<const f4v*>(g + i0 + 4 * h);
+            const f4v uv = *reinterpret_cast<const f4v*>(u + i0 + 4 * h);
 #pragma unroll
             for (int e = 0; e < 4; ++e) v[h][e] = siluf_(gv[e]) * uv[e];
             *reinterpret_cast<f4v*>(prod + e0 + 4 * h) = v[h];
         }
+        if (!out) continue;
         bf16x4 lo[3], hi[3];
         split3_4(v[0], lo);
         split3_4(v[1], hi);
@@ -503,15 +504,15 @@ __global__ __launch_bounds__(256) void silu_split6_kernel(float* prod, const flo
     }
 }
 
-int silu_split6(hipStream_t s, float* prod, const float* g, const float* u, __bf16* out, int rows, int cols) {
-    if (rows < 1 || cols < 8 || cols % 8 != 0 ||
+int silu_split6(hipStream_t s, float* prod, const float* g, const float* u, int ld, __bf16* out, int rows, int cols) {
+    if (rows < 1 || cols < 8 || cols % 8 != 0 || ld % 4 != 0 || ld < cols ||
         (reinterpret_cast<uintptr_t>(prod) | reinterpret_cast<uintptr_t>(g) | reinterpret_cast<uintptr_t>(u) |
          reinterpret_cast<uintptr_t>(out)) % 16 != 0)
         return int(hipErrorNotSupported);
     const long chunks = long(rows) * (cols / 8);
     const long blocks = (chunks + 255) / 256;
     hipLaunchKernelGGL(silu_split6_kernel, dim3(unsigned(blocks < 65536 ? blocks : 65536)), dim3(256), 0, s, prod, g,
-                       u, out, cols, chunks);
+                       u, ld, out, cols, chunks);
     return int(hipGetLastError());
 }
 

@@ -185,10 +185,12 @@ def test_gemm_f32_prepared(gpu, rows, cols, batch):
 
 
 def test_prepared_group_glu_and_invalidation(gpu):
-    """Prepared matrices in a group (x split once) and a GLU (gate_y / up_y
-    written, then silu(gate) * up) equal the separate prepared projections
-    bitwise; a qr_write into a prepared matrix drops its planes, so the next
-    projection follows the new values; release and free are accepted."""
+    """Prepared matrices in a group (x split once) equal the separate prepared
+    projections bitwise; a prepared GLU (gate and up as one GEMM over their
+    planes side by side, then silu(gate) * up; gate_y / up_y untouched, as the
+    fused GLU) follows the separate projections to the fp32 bound; a qr_write
+    into a prepared matrix drops its planes (and the GLU pair's copy), so the
+    next projection follows the new values; release and free are accepted."""
     rng = np.random.default_rng(5)
     cols, batch = 1024, 300
     shapes = [6144, 2048, 16, 16]
@@ -214,9 +216,17 @@ def test_prepared_group_glu_and_invalidation(gpu):
     g1, u1 = gpu.alloc(batch * rows), gpu.alloc(batch * rows)
     gpu.gemm(g1, g, x, rows, cols, batch)
     gpu.gemm(u1, u, x, rows, cols, batch)
-    assert np.array_equal(gy.read(), g1.read()) and np.array_equal(uy.read(), u1.read())
+    assert not gy.read().any() and not uy.read().any()  # untouched
     gv, uv = g1.read().astype(np.float64), u1.read().astype(np.float64)
     parity(prod.read(), gv / (1 + np.exp(-gv)) * uv, where="prepared glu")
+    # a write into gate drops its planes and the pair's: the GLU follows the new gate
+    gw2 = (rng.standard_normal(rows * cols) * 0.02).astype(np.float32)
+    g.write(gw2)
+    gpu.prepare(g, rows, cols)
+    gpu.glu(prod, gy, uy, g, u, x, rows, cols, batch)
+    gpu.gemm(g1, g, x, rows, cols, batch)
+    gv = g1.read().astype(np.float64)
+    parity(prod.read(), gv / (1 + np.exp(-gv)) * uv, where="prepared glu after a write")
     # rewrite the first matrix: its planes are dropped, the projection follows the new weights
     new = (rng.standard_normal(shapes[0] * cols) * 0.02).astype(np.float32)
     mats[0].write(new)
@@ -275,7 +285,10 @@ def test_planes_from_producers(gpu):
     gpu.gemm(o2, down, prod, h, inter, batch)
     assert np.array_equal(o1.read(), o2.read())
     assert np.array_equal(o1.read(), proj_of_copy(prod, down, h, inter))
-    gv, uv = gy.read().astype(np.float64), uy.read().astype(np.float64)
+    g1, u1 = gpu.alloc(batch * inter), gpu.alloc(batch * inter)
+    gpu.gemm(g1, gate, y2, inter, h, batch)
+    gpu.gemm(u1, up, y2, inter, h, batch)
+    gv, uv = g1.read().astype(np.float64), u1.read().astype(np.float64)
     parity(prod.read(), gv / (1 + np.exp(-gv)) * uv, where="glu product with planes")
     # a write between the norm and the projection: the projection follows the new values
     gpu.run("RMS_NORM", batch, [y, x, nw], [h], [1e-6, 1.0])
