@@ -66,6 +66,11 @@ constexpr int SMAX = 256;           // attention splits per KV head
 constexpr int QPG = NH / NKV;       // query heads per KV head: the waves of one attention slot
 constexpr int MAXPH = 6 * 64 + 2;
 constexpr int DIN_RPW = 4, GLU_RPW = 2, AQKV_RPW = 3, Z_RPW = 2;
+// fp32 DeltaNet layers: units >= EARLY_U (waves 4..7 of every block) have no
+// DOUT row; they take GLU rows 0 .. GLU_EARLY_ROWS - 1 and load both of them
+// right after DOUT's barrier, while DOUT's rows are summed (the other GLU rows
+// go to units from 0 on, loaded at the usual time).
+constexpr int EARLY_U = 4 * BLOCKS, GLU_EARLY_ROWS = GLU_RPW * (NW - EARLY_U);
 constexpr int MIX_WAVES = VH * 8;  // 16 value columns per wave
 constexpr int COMB_WAVES = NH * (HD / 4);
 static_assert(DIN_RPW * NW >= DIN_ROWS && GLU_RPW * NW >= I && AQKV_RPW * NW >= AQKV_ROWS, "rows per wave");
@@ -730,8 +735,10 @@ __device__ __forceinline__ void prefetch_row(const float* m, int row, int rows, 
         for (int v = V0; v < V1; ++v) wb[v] = buffer_load_f4(r, lo + 1024u * v, ro, AUX);
     }
 }
+template <bool Q8, int R, int AUX>
+__device__ __forceinline__ void glu_load(LayerP w, int u, f4* wb);
 template <bool Q8>
-__device__ __forceinline__ bool phase_dout(const Args& a, Rs rs, LayerP w, int L, int p, int u, const f4* wb, Lds& l) {
+__device__ __forceinline__ bool phase_dout(const Args& a, Rs rs, LayerP w, int L, int p, int u, f4* wb, Lds& l) {
     const int par = p & 1;
     {
         const unsigned th = threadIdx.x;
@@ -750,7 +757,13 @@ __device__ __forceinline__ bool phase_dout(const Args& a, Rs rs, LayerP w, int L
         *reinterpret_cast<f4*>(&l.act[par][4 * th]) = sz * ((core * r) * nw);
     }
     if (!bsync(l, p)) return false;
-    if (u >= H) return true;
+    if (u >= H) {
+        if (!Q8 && u >= EARLY_U) {  // this unit's GLU rows, both parts, while DOUT's rows are summed
+            glu_load<Q8, 0, kNT>(w, u, wb);
+            glu_load<Q8, 1, kNT>(w, u, wb);
+        }
+        return true;
+    }
     const float acc = dot_row_lds<Q8, VD / 256>(wb, l.act[par]);
     const float res = input_at<Q8>(a, rs, L, p - 3, u, l, p);
     if (lane_id() == 0) stt(rs, SOFF(after) + 8u * unsigned(u), res + acc, tag(a, p));
@@ -758,9 +771,15 @@ __device__ __forceinline__ bool phase_dout(const Args& a, Rs rs, LayerP w, int L
 }
 
 // ---- T_GLU: product = silu(gate . n) * (up . n), n = post RMSNorm of `after`
+// The first of unit u's GLU_RPW rows (dn: a DeltaNet layer).
+template <bool Q8>
+__device__ __forceinline__ int glu_first(int u, bool dn) {
+    if (Q8 || !dn) return u * GLU_RPW;
+    return u >= EARLY_U ? (u - EARLY_U) * GLU_RPW : GLU_EARLY_ROWS + u * GLU_RPW;
+}
 template <bool Q8, int R, int AUX = kNT>
 __device__ __forceinline__ void glu_load(LayerP w, int u, f4* wb) {
-    const int row = u * GLU_RPW + R;
+    const int row = glu_first<Q8>(u, !w->attention) + R;
     if (row < I) {
         load_row_h<Q8, 8 * R, AUX>(wb, rsrc(w->gate), row, I);
         load_row_h<Q8, 8 * R + 4, AUX>(wb, rsrc(w->up), row, I);
@@ -768,14 +787,15 @@ __device__ __forceinline__ void glu_load(LayerP w, int u, f4* wb) {
 }
 template <bool Q8, int AUX = kNT>
 __device__ __forceinline__ void prefetch_glu(LayerP w, int u, f4* wb, int part) {
+    if (!Q8 && !w->attention && u >= EARLY_U) return;  // loaded in DOUT
     if (part == 0)
         glu_load<Q8, 0, AUX>(w, u, wb);
     else
         glu_load<Q8, 1>(w, u, wb);
 }
 template <bool Q8, int R>
-__device__ __forceinline__ void glu_row(Rs rs, const f4* wb, const f4 (&xv)[4], int u, unsigned t) {
-    const int row = u * GLU_RPW + R;
+__device__ __forceinline__ void glu_row(Rs rs, const f4* wb, const f4 (&xv)[4], int row0, unsigned t) {
+    const int row = row0 + R;
     if (row < I) {
         const float g = dot_row_h<Q8, 8 * R>(wb, xv), up = dot_row_h<Q8, 8 * R + 4>(wb, xv);
         if (lane_id() == 0) stt(rs, SOFF(product) + 8u * unsigned(row), silu(g) * up, t);
@@ -787,11 +807,12 @@ __device__ __forceinline__ bool phase_glu(const Args& a, Rs rs, LayerP w, int p,
     stage_norm(w->post_norm, par, l);
     stage_tagged<H>(a, rs, SOFF(after), tag(a, p - 1), l.act[par], l, p, [&] { prefetch_glu<Q8>(w, u, wb, 1); });
     if (!bsync(l, p)) return false;
-    if (u * GLU_RPW >= I) return true;
+    const int row0 = glu_first<Q8>(u, !w->attention);
+    if (row0 >= I) return true;
     f4 xv[4];
     normed_chunks<Q8>(l, par, a.eps, xv);
-    glu_row<Q8, 0>(rs, wb, xv, u, tag(a, p));
-    glu_row<Q8, 1>(rs, wb, xv, u, tag(a, p));
+    glu_row<Q8, 0>(rs, wb, xv, row0, tag(a, p));
+    glu_row<Q8, 1>(rs, wb, xv, row0, tag(a, p));
     return true;
 }
 
