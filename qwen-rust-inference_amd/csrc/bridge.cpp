@@ -57,6 +57,13 @@ struct Context {
     const float* x6_src = nullptr;
     int x6_rows = 0, x6_cols = 0;
     unsigned long serial = 0, x6_serial = 0;
+    // The width of the projection that took the last RmsNormGate output right
+    // after it (its rows span several groups), by group size: from then on such
+    // a norm writes its planes in rows of that width.
+    std::map<int, int> gate_width;
+    const float* gate_out = nullptr;
+    int gate_d = 0;
+    unsigned long gate_serial = 0;
     // RoPE denominators theta^(2i / rot) per (theta bits, rot), device copies.
     std::map<std::pair<uint32_t, int>, float*> rope;
     // Profiler (qr_profile / QWEN_ROCM_PROFILE=1): a hipEvent pair on the
@@ -190,6 +197,8 @@ int grow_x6(Context* c, int cols, int batch) {
 // x's split planes into c->x6: already there when the previous bridge call
 // produced x with them, else split now.
 int split_input(Context* c, const float* x, int cols, int batch) {
+    if (c->gate_out == x && c->gate_serial + 1 == c->serial && cols % c->gate_d == 0)
+        c->gate_width[c->gate_d] = cols;  // a gated norm's output projected: its row width
     if (c->x6_src == x && c->x6_rows == batch && c->x6_cols == cols && c->x6_serial + 1 == c->serial) return 0;
     c->x6_src = nullptr;
     if (int st = grow_x6(c, cols, batch)) return st;
@@ -625,14 +634,28 @@ int qr_run(Context* c, int op, int count, const Params* ap) {
     case QR_ADD_RMS_NORM:
     case QR_RMS_NORM_GATE:
         if (a.n[0] < 1) return fail(c, "norm shape", -1);
-        if (op != QR_RMS_NORM_GATE && planes_wanted(c, a.n[0], count)) {  // the normed rows' planes too
-            if (int st = grow_x6(c, a.n[0], count)) return st;
-            const int st = qr::run_rms_family_planes(s, op, count, a, c->x6);
-            if (st == 0) {
-                planes_made(c, op == QR_ADD_RMS_NORM ? a.p[3] : a.p[0], count, a.n[0]);
-                return launched(c, "rms_norm", 0);
+        {
+            // the output's planes too, in rows of the width its projection takes: d for the
+            // norms of a residual row, the learned width for a gated norm (groups of heads)
+            int width = a.n[0];
+            if (op == QR_RMS_NORM_GATE) {
+                auto it = c->gate_width.find(a.n[0]);
+                width = it == c->gate_width.end() ? 0 : it->second;
+                c->gate_out = a.p[0];
+                c->gate_d = a.n[0];
+                c->gate_serial = c->serial;
             }
-            if (st != int(hipErrorNotSupported)) return launched(c, "rms_norm", st);
+            const long total = long(count) * a.n[0];
+            if (width > 0 && total % width == 0 && planes_wanted(c, width, int(total / width))) {
+                const int rows = int(total / width);
+                if (int st = grow_x6(c, width, rows)) return st;
+                const int st = qr::run_rms_family_planes(s, op, count, a, c->x6, width);
+                if (st == 0) {
+                    planes_made(c, op == QR_ADD_RMS_NORM ? a.p[3] : a.p[0], rows, width);
+                    return launched(c, "rms_norm", 0);
+                }
+                if (st != int(hipErrorNotSupported)) return launched(c, "rms_norm", st);
+            }
         }
         return launched(c, "rms_norm", qr::run_rms_family(s, op, count, a));
     case QR_ADD:

@@ -115,10 +115,12 @@ int gemm_glu(hipStream_t s, WeightType t, float* product, const void* gate, cons
 // ops.hip --------------------------------------------------------------------
 int run_elementwise(hipStream_t s, int op, int count, const Params& a);
 int run_rms_family(hipStream_t s, int op, int groups, const Params& a);
-// RmsNorm / AddRmsNorm whose normed rows are also written as split6 planes
-// (rows x 6 d BF16, activation order); hipErrorNotSupported (nothing launched)
-// when the op, width or alignment has no such form.
-int run_rms_family_planes(hipStream_t s, int op, int groups, const Params& a, __bf16* planes);
+// RmsNorm / AddRmsNorm / RmsNormGate whose output is also written as split6
+// planes (activation order) of rows of `width` values (a multiple of the
+// group size that divides the output: groups * d / width rows of 6 width
+// BF16); hipErrorNotSupported (nothing launched) when the op, width or
+// alignment has no such form.
+int run_rms_family_planes(hipStream_t s, int op, int groups, const Params& a, __bf16* planes, int width);
 int run_conv_silu(hipStream_t s, int count, const Params& a);
 int run_delta_qk(hipStream_t s, int count, const Params& a);
 int run_delta_rule(hipStream_t s, bool gated, int count, const Params& a);

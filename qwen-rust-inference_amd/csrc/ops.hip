@@ -103,11 +103,13 @@ __global__ __launch_bounds__(256) void rms_family_kernel(int op, int groups, Par
 // j < PER / V), so every load and store of a wave is one contiguous run and
 // each input is read once (the block form above reads a group twice and
 // waits on two block barriers).
-// planes (may be null): the output rows also as the K'-concatenated BF16
-// planes a prepared projection takes (row g: 6 segments of d, segment b the
-// split part {2, 1, 0, 1, 0, 0}[b] of x = x0 + x1 + x2; as split6 of gemm.hip).
+// planes (may be null): the output also as the K'-concatenated BF16 planes a
+// prepared projection takes, the output read as rows of `width` values (a
+// multiple of d: consecutive groups form a row): row r holds 6 segments of
+// width, segment b the split part {2, 1, 0, 1, 0, 0}[b] of x = x0 + x1 + x2
+// (as split6 of gemm.hip).
 template <int PER>
-__global__ __launch_bounds__(256) void rms_rows_kernel(int op, int groups, Params a, __bf16* planes) {
+__global__ __launch_bounds__(256) void rms_rows_kernel(int op, int groups, Params a, __bf16* planes, int width) {
     constexpr int V = PER >= 4 ? 4 : PER, NV = PER / V;
     typedef float fv __attribute__((ext_vector_type(V)));
     typedef __bf16 hv __attribute__((ext_vector_type(V)));
@@ -156,9 +158,10 @@ __global__ __launch_bounds__(256) void rms_rows_kernel(int op, int groups, Param
                 h[2][e] = __bf16(r1 - float(h[1][e]));
             }
             constexpr int XP[6] = {2, 1, 0, 1, 0, 0};
-            __bf16* row = planes + size_t(g) * 6 * d + c;
+            const unsigned pe = unsigned(off) + unsigned(c), pr = pe / unsigned(width);  // element, plane row
+            __bf16* row = planes + size_t(pr) * 6 * width + (pe - pr * unsigned(width));
 #pragma unroll
-            for (int b = 0; b < 6; ++b) *reinterpret_cast<hv*>(row + b * d) = h[XP[b]];
+            for (int b = 0; b < 6; ++b) *reinterpret_cast<hv*>(row + size_t(b) * width) = h[XP[b]];
         }
     }
 }
@@ -569,35 +572,38 @@ int run_elementwise(hipStream_t s, int op, int count, const Params& a) {
 // The register form when the group is 64 PER elements and every operand is
 // aligned to its vector width.
 template <int PER>
-bool launch_rms_rows(hipStream_t s, int op, int groups, const Params& a, __bf16* planes) {
+bool launch_rms_rows(hipStream_t s, int op, int groups, const Params& a, __bf16* planes, int width) {
     constexpr uintptr_t align = (PER >= 4 ? 4 : PER) * sizeof(float);
     const int slots[] = {0, 1, 2, 3, 4};
     const int used = op == QR_ADD_RMS_NORM ? 5 : op == QR_RMS_NORM_GATE ? 4 : 3;
     for (int k = 0; k < used; ++k)
         if (reinterpret_cast<uintptr_t>(a.p[slots[k]]) % align != 0) return false;
     if (planes && reinterpret_cast<uintptr_t>(planes) % (align / 2) != 0) return false;
-    hipLaunchKernelGGL(rms_rows_kernel<PER>, dim3(ceil_div(groups, 4)), dim3(256), 0, s, op, groups, a, planes);
+    hipLaunchKernelGGL(rms_rows_kernel<PER>, dim3(ceil_div(groups, 4)), dim3(256), 0, s, op, groups, a, planes,
+                       width);
     return true;
 }
-bool launch_rms_rows_any(hipStream_t s, int op, int groups, const Params& a, __bf16* planes) {
+bool launch_rms_rows_any(hipStream_t s, int op, int groups, const Params& a, __bf16* planes, int width) {
     switch (a.n[0]) {
-    case 128: return launch_rms_rows<2>(s, op, groups, a, planes);
-    case 256: return launch_rms_rows<4>(s, op, groups, a, planes);
-    case 512: return launch_rms_rows<8>(s, op, groups, a, planes);
-    case 1024: return launch_rms_rows<16>(s, op, groups, a, planes);
-    case 2048: return launch_rms_rows<32>(s, op, groups, a, planes);
+    case 128: return launch_rms_rows<2>(s, op, groups, a, planes, width);
+    case 256: return launch_rms_rows<4>(s, op, groups, a, planes, width);
+    case 512: return launch_rms_rows<8>(s, op, groups, a, planes, width);
+    case 1024: return launch_rms_rows<16>(s, op, groups, a, planes, width);
+    case 2048: return launch_rms_rows<32>(s, op, groups, a, planes, width);
     }
     return false;
 }
 
-int run_rms_family_planes(hipStream_t s, int op, int groups, const Params& a, __bf16* planes) {
-    if (op != QR_RMS_NORM && op != QR_ADD_RMS_NORM) return int(hipErrorNotSupported);
-    if (!launch_rms_rows_any(s, op, groups, a, planes)) return int(hipErrorNotSupported);
+int run_rms_family_planes(hipStream_t s, int op, int groups, const Params& a, __bf16* planes, int width) {
+    if (op != QR_RMS_NORM && op != QR_ADD_RMS_NORM && op != QR_RMS_NORM_GATE) return int(hipErrorNotSupported);
+    if (a.n[0] < 1 || width < a.n[0] || width % a.n[0] != 0 || (long(groups) * a.n[0]) % width != 0)
+        return int(hipErrorNotSupported);
+    if (!launch_rms_rows_any(s, op, groups, a, planes, width)) return int(hipErrorNotSupported);
     return int(hipGetLastError());
 }
 
 int run_rms_family(hipStream_t s, int op, int groups, const Params& a) {
-    if (launch_rms_rows_any(s, op, groups, a, nullptr)) return int(hipGetLastError());
+    if (launch_rms_rows_any(s, op, groups, a, nullptr, a.n[0])) return int(hipGetLastError());
     if (a.n[0] <= 256)
         hipLaunchKernelGGL(rms_family_kernel<true>, dim3(ceil_div(groups, 4)), dim3(256), 0, s, op, groups, a);
     else

@@ -299,6 +299,23 @@ def test_planes_from_producers(gpu):
     W = w_in.read().reshape(2048, h).astype(np.float64)
     bound = np.abs(X) @ np.abs(W.T) * 2e-5 + 1e-30
     assert np.all(np.abs(out.read().reshape(batch, 2048)[:8] - X @ W.T) <= bound)
+    # RmsNormGate (groups of 128, 16 per token) -> a projection of width 2048:
+    # the first pair teaches the bridge the width, the next norm writes planes
+    heads, d = 16, 128
+    core = gpu.upload(rng.standard_normal(batch * heads * d).astype(np.float32))
+    z = gpu.upload(rng.standard_normal(batch * heads * d).astype(np.float32))
+    gw = gpu.upload((rng.standard_normal(d) * 0.1 + 1.0).astype(np.float32))
+    w_o = gpu.upload((rng.standard_normal(h * heads * d) * 0.02).astype(np.float32))
+    gpu.prepare(w_o, h, heads * d)
+    gated, o3 = gpu.alloc(batch * heads * d), gpu.alloc(batch * h)
+    for _ in range(3):
+        gpu.run("RMS_NORM_GATE", batch * heads, [gated, core, gw, z], [d], [1e-6, 0.0])
+        gpu.gemm(o3, w_o, gated, h, heads * d, batch)
+        assert np.array_equal(o3.read(), proj_of_copy(gated, w_o, h, heads * d))
+    G = gated.read().reshape(batch, heads * d)[:8].astype(np.float64)
+    W = w_o.read().reshape(h, heads * d).astype(np.float64)
+    bound = np.abs(G) @ np.abs(W.T) * 2e-5 + 1e-30
+    assert np.all(np.abs(o3.read().reshape(batch, h)[:8] - G @ W.T) <= bound)
 
 
 @pytest.mark.parametrize("kind", ["f32", "bf16", "i8"])
