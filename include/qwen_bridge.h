@@ -111,7 +111,11 @@ int qr_max_op(void);
 int qr_snapshots(void);
 /* 2: ops Argmax and EmbedBf16Picked (bridge.cpp:362-363). */
 int qr_argmax(void);
-/* Engine options; "attention_f16" is refused (RDNA3 WMMA only) (bridge.cpp:412-426). */
+/* Engine options; "attention_f16" is refused (RDNA3 WMMA only) (bridge.cpp:412-426).
+ * "decode_cooperative" (0/1, this bridge's own): one-launch decode plans made after the
+ * call launch their steps cooperatively (the runtime guarantees the 256 blocks are
+ * resident together, about 20 us more per step) instead of as plain launches, which
+ * need a device no other stream or process is using at that moment. */
 int qr_set_option(Context* c, const char* name, int value);
 /* int8 per-row weights: Y[batch, rows] = scale[r] * (X Q^T) (bridge.cpp:620-653). */
 int qr_gemm_i8(Context* c, float* y, const float* packed, const float* x, int rows, int cols, int batch);

@@ -61,6 +61,9 @@ struct Context {
     // after it (its rows span several groups), by group size: from then on such
     // a norm writes its planes in rows of that width.
     std::map<int, int> gate_width;
+    // qr_set_option "decode_cooperative": one-launch decode plans made from
+    // then on launch cooperatively (default: plain launches)
+    bool decode_cooperative = false;
     const float* gate_out = nullptr;
     int gate_d = 0;
     unsigned long gate_serial = 0;
@@ -503,8 +506,12 @@ int qr_create(Context** out) {
 
 int qr_set_option(Context* c, const char* name, int value) {
     ++c->serial;
-    if (std::strcmp(name, "attention_f16") != 0 || (value != 0 && value != 1))
-        return fail(c, "unknown bridge option", -1);
+    if (!name || (value != 0 && value != 1)) return fail(c, "unknown bridge option", -1);
+    if (std::strcmp(name, "decode_cooperative") == 0) {  // this bridge's own: plans made after the call
+        c->decode_cooperative = value != 0;
+        return 0;
+    }
+    if (std::strcmp(name, "attention_f16") != 0) return fail(c, "unknown bridge option", -1);
     if (value) return fail(c, "attention_f16 (16-bit prefill attention) is not offered: attention runs in fp32", -1);
     return 0;
 }
@@ -863,6 +870,11 @@ int qr_decode_plan(Context* c, const QrDecodeDesc* d, QrDecodePlan** out) {
     if (s) {
         std::snprintf(c->error, sizeof(c->error), "%s", why ? why : "one-launch decode unavailable");
         return s;
+    }
+    if (c->decode_cooperative && (s = qr::decode_plan_cooperative(*out, true))) {
+        qr::decode_plan_free(*out);
+        *out = nullptr;
+        return fail(c, "decode_cooperative: the device has no cooperative launch", s);
     }
     return 0;
 }

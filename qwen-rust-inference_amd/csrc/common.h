@@ -149,6 +149,9 @@ size_t attention_scratch_needed(const Params& a);
 const char* decode_unsupported(const QrDecodeDesc& d);
 int decode_plan_create(const QrDecodeDesc& d, QrDecodePlan** out, hipStream_t s, const char** why);
 void decode_plan_free(QrDecodePlan* p);
+// Launch the plan's steps cooperatively (on) or as plain launches (off, the
+// default); hipErrorNotSupported when the device has no cooperative launch.
+int decode_plan_cooperative(QrDecodePlan* p, bool on);
 // token -1: the previous launch's argmax (read on the device). slot >= 0: the
 // step's [argmax, non-finite count] also goes to history slot `slot`.
 // slot >= 0: the chained-steps history slot; row: logits / picks row; snap: snapshot copy (0: none).

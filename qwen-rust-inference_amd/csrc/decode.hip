@@ -7,7 +7,15 @@
 // (each projection needs the whole previous vector). As separate kernels each
 // stage pays a dispatch, a ramp-up and a drain (~2-5 us for the small
 // matrices) and the step cannot approach the HBM roofline. Here 256 blocks of
-// 8 waves stay resident (cooperative launch) and walk the stage list together.
+// 8 waves stay resident and walk the stage list together. The kernel needs
+// all 256 blocks resident at once (one per CU: 256 VGPRs per lane leave room
+// for one 8-wave block per CU). A plain launch gets that on a device no other
+// stream or process is using (the previous step on the same stream has
+// finished, so every CU is free when the grid is dispatched); a cooperative
+// launch has the runtime guarantee it, at about 20 us more per step, and is
+// chosen per plan (decode_plan_cooperative). Either way a block that is not
+// resident makes the others' polls time out: the step then fails (below)
+// instead of hanging.
 //
 // Structure:
 //   * The phase list: per DeltaNet layer in-proj + conv, mixer (+ z rows),
@@ -1497,6 +1505,7 @@ struct QrDecodePlan {
     float* logits = nullptr;    // row 0 of the logits rows ([rows, vocab])
     float* picks = nullptr;     // row 0 of the [argmax, non-finite count] rows
     bool q8 = false;  // int8 matrices and LM head: decode_kernel<true>
+    bool cooperative = false;  // launched with hipLaunchCooperativeKernel instead of a plain launch
     float* hist = nullptr;  // [capacity][argmax, non-finite count] of chained steps
 };
 
@@ -1578,13 +1587,11 @@ int decode_plan_create(const QrDecodeDesc& d, QrDecodePlan** out, hipStream_t s,
     using namespace dec;
     *out = nullptr;
     if ((*why = decode_unsupported(d))) return -1;
-    int dev = 0, cus = 0, per_cu = 0, coop = 0;
+    int dev = 0, cus = 0, per_cu = 0;
     (void)hipGetDevice(&dev);
     (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
-    (void)hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, dev);
     const bool q8 = d.weights == QR_DECODE_INT8;
-    if (!coop ||
-        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, q8 ? decode_kernel<true> : decode_kernel<false>,
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, q8 ? decode_kernel<true> : decode_kernel<false>,
                                                      THREADS, 0) != hipSuccess ||
         per_cu * cus < BLOCKS) {
         *why = "one-launch decode: 256 co-resident blocks do not fit this device";
@@ -1636,6 +1643,17 @@ int decode_plan_create(const QrDecodeDesc& d, QrDecodePlan** out, hipStream_t s,
     return 0;
 }
 
+int decode_plan_cooperative(QrDecodePlan* p, bool on) {
+    if (on) {
+        int dev = 0, coop = 0;
+        (void)hipGetDevice(&dev);
+        (void)hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, dev);
+        if (!coop) return int(hipErrorNotSupported);
+    }
+    p->cooperative = on;
+    return 0;
+}
+
 void decode_plan_free(QrDecodePlan* p) {
     if (!p) return;
     if (p->layers) (void)hipFree(p->layers);
@@ -1672,7 +1690,8 @@ int decode_step(QrDecodePlan* p, int token, int position, int slot, hipStream_t 
     void* args[] = {&a};
     const void* k = p->q8 ? reinterpret_cast<const void*>(decode_kernel<true>)
                           : reinterpret_cast<const void*>(decode_kernel<false>);
-    return int(hipLaunchCooperativeKernel(k, dim3(BLOCKS), dim3(THREADS), args, 0, s));
+    return p->cooperative ? int(hipLaunchCooperativeKernel(k, dim3(BLOCKS), dim3(THREADS), args, 0, s))
+                          : int(hipLaunchKernel(k, dim3(BLOCKS), dim3(THREADS), args, 0, s));
 }
 int decode_history_clear(QrDecodePlan* p, int n, hipStream_t s) {
     if (n < 1 || n > p->capacity) return int(hipErrorInvalidValue);

@@ -29,6 +29,7 @@ NO_F32_FUSIONS, NO_FUSIONS, NO_DELTA_MIXER, NO_FUSED_OPS, NO_ARGMAX, NO_SNAPSHOT
 NO_DECODE_STEP = 64
 NO_EMBED_ROWS = 128
 NO_BLAS_GEMM = 256
+NO_PLAIN_DECODE_LAUNCH = 512  # one-launch decode steps launched cooperatively
 
 # Every entry point of include/qwen_bridge.h.
 BRIDGE_SYMBOLS = [

@@ -396,6 +396,30 @@ def test_qwen08b_chained_greedy_equals_stepwise(qwen08b_models):
             assert np.array_equal(runs[0].state(layer, which), runs[1].state(layer, which)), (layer, which)
 
 
+def test_qwen08b_cooperative_launch_equals_plain(qwen08b, qwen08b_models):
+    """The one-launch step as a cooperative launch (qr_set_option
+    "decode_cooperative") and as the default plain launch: the same kernel on
+    the same inputs, so bitwise the same logits, IDs and states."""
+    c, w = qwen08b
+    plain, _ = qwen08b_models
+    coop = E.Model(w, disable=E.NO_PLAIN_DECODE_LAUNCH)
+    prompt = [int(v) for v in np.random.default_rng(12).integers(0, c.vocab_size, 30)]
+    runs = [m.new_run(64, chunk=32) for m in (plain, coop)]
+    assert all(r.decode_plan for r in runs)
+    first = [O.select_greedy(r.prefill(prompt)) for r in runs]
+    assert first[0] == first[1]
+    logits = [r.step(first[0]) for r in runs]
+    assert np.array_equal(logits[0], logits[1])
+    ids = [r.decode_greedy(O.select_greedy(logits[0]), 9)[0] for r in runs]
+    assert ids[0] == ids[1]
+    for layer in (0, 3, 23):
+        for which in range(4):
+            assert np.array_equal(runs[0].state(layer, which), runs[1].state(layer, which)), (layer, which)
+    for r in runs:
+        r.close()
+    coop.close()
+
+
 @pytest.mark.parametrize("fmt", [E.F32, E.INT8])
 def test_qwen08b_verify_rows_equal_decode_steps(qwen08b, qwen08b_models, fmt):
     """Verify rows on the one-launch path: each row is a launch of the decode
