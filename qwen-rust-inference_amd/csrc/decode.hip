@@ -38,8 +38,11 @@
 //     (The attention split partials are plain stores published by a tagged
 //     (max, sum) pair written after an s_waitcnt.)
 //   * Broadcast vectors are staged once per block in LDS (double-buffered by
-//     phase parity; one s_barrier per phase keeps the block's waves within a
-//     phase of each other, so a buffer is never rewritten while read).
+//     phase parity; the barriers of each phase keep the block's waves within a
+//     phase of each other, so a buffer is never rewritten while read). A
+//     vector stays readable until the block stages into its buffer again, so
+//     later phases take the residual (and MIX its input) from there instead of
+//     polling it.
 //   * Every poll is bounded by the 100 MHz real-time counter; on a time-out a
 //     lane records an error (picks[1] = 1e30, a non-finite count the engine
 //     refuses), the block's waves leave together after their next s_barrier,
@@ -405,18 +408,6 @@ __device__ __forceinline__ void stage_input(const Args& a, Rs rs, int L, int pro
         stage_tagged<H>(a, rs, SOFF(x), tag(a, producer), l.act[par], l, p, mid);
     }
 }
-template <bool Q8>
-__device__ __forceinline__ float input_at(const Args& a, Rs rs, int L, int producer, int i, Lds& l, int p) {
-    if (L == 0) {
-        if (Q8 && a.emb_bf16) {
-            const unsigned e = unsigned(l.token) * unsigned(H) + unsigned(i);
-            const unsigned w = __float_as_uint(ldp(rsrc(a.embedding), e / 2u * 4u));
-            return __uint_as_float((i & 1) ? (w & 0xffff0000u) : (w << 16));
-        }
-        return ldp(rsrc(a.embedding), (unsigned(l.token) * unsigned(H) + unsigned(i)) * 4u);
-    }
-    return wait1(a, rs, SOFF(x) + 8u * unsigned(i), tag(a, producer), l, wall_clock64(), p);
-}
 // The staged H-vector in chunks times its RMSNorm and the staged (1 + w)
 // (reference.h:120-126). fp32 rows: xv[v] holds elements 4 (lane + 64 v) .. +3;
 // int8 rows: elements 16 lane + 4 v .. +3 (the 16 columns of the lane's
@@ -619,10 +610,12 @@ __device__ __forceinline__ void z_row(Rs rs, const f4* wb, const f4 (&xv)[4], in
 }
 template <bool Q8>
 __device__ __forceinline__ bool phase_mix(const Args& a, Rs rs, LayerP w, int L, int p, int u, f4* wb, Lds& l) {
-    const int par = p & 1;
-    stage_norm(w->input_norm, par, l);
-    stage_input<Q8>(a, rs, L, p - 2, par, l, p);
-    if (!bsync(l, p)) return false;
+    // the z rows read the layer input and its norm weights as DIN staged them
+    // (parity of phase p - 1): the block writes that buffer again only after
+    // the barrier that follows this phase, so the phase needs neither a
+    // staging nor a barrier of its own (a time-out of an earlier phase is
+    // acted on at the next phase's barrier)
+    const int par = (p - 1) & 1;
     const unsigned t = tag(a, p);
     if (u >= MIX_WAVES) {
         if ((u - MIX_WAVES) * Z_RPW >= VD) return true;
@@ -657,7 +650,21 @@ __device__ __forceinline__ bool phase_mix(const Args& a, Rs rs, LayerP w, int L,
         mv[k] = raw[k].x;
         ready = ready && __float_as_uint(raw[k].y) == want;
     }
-    if (!ready) wait1n<7>(a, rs, mo, want, mv, l, start, p);
+    while (!ready) {  // every pair again in each round: one round trip serves all late ones
+        if (wall_clock64() - start > kTimeout || failed(l)) {
+            record_failure(a, l, p);
+            break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+        for (int k = 0; k < 7; ++k) raw[k] = ldx2(rs, mo[k]);
+        ready = true;
+#pragma unroll
+        for (int k = 0; k < 7; ++k) {
+            mv[k] = raw[k].x;
+            ready = ready && __float_as_uint(raw[k].y) == want;
+        }
+    }
     const float q0 = mv[0], q1 = mv[1], k0 = mv[2], k1 = mv[3], v = mv[4], av = mv[5], bv = mv[6];
     // L2 norms (reference.h:134-143), q / sqrt(dk)
     const float sq = wave_total(q0 * q0 + q1 * q1);
@@ -719,8 +726,9 @@ __device__ __forceinline__ bool phase_mix(const Args& a, Rs rs, LayerP w, int L,
 
 // ---- T_DOUT: the gated RMSNorm silu(z) * RmsNorm(core) (direct weight,
 // reference.h:201-207) is built once per block in LDS (thread t: elements
-// 4t .. 4t+3, its head's 32 threads reduce the sum of squares), then
-// out_proj row u plus the residual.
+// 4t .. 4t+3, its head's 32 threads reduce the sum of squares; in the upper
+// half of the phase's buffer, whose lower half still holds the layer input as
+// DIN staged it), then out_proj row u plus that residual.
 // PART -1: the whole row; 0 / 1: the first / second half of an fp32 row
 // (int8: part 0 is the whole row).
 template <bool Q8, int COLS, int PART = -1, int AUX = kNT>
@@ -762,7 +770,7 @@ __device__ __forceinline__ bool phase_dout(const Args& a, Rs rs, LayerP w, int L
         const f4 core = f4{c01.x, c01.y, c23.x, c23.y}, sz = f4{z01.x, z01.y, z23.x, z23.y};
         const float ss = lanes_sum<32>(dot4(core, core));
         const float r = 1.f / sqrtf(ss / float(DV) + a.eps);
-        *reinterpret_cast<f4*>(&l.act[par][4 * th]) = sz * ((core * r) * nw);
+        *reinterpret_cast<f4*>(&l.act[par][VD + 4 * th]) = sz * ((core * r) * nw);
     }
     if (!bsync(l, p)) return false;
     if (u >= H) {
@@ -772,8 +780,8 @@ __device__ __forceinline__ bool phase_dout(const Args& a, Rs rs, LayerP w, int L
         }
         return true;
     }
-    const float acc = dot_row_lds<Q8, VD / 256>(wb, l.act[par]);
-    const float res = input_at<Q8>(a, rs, L, p - 3, u, l, p);
+    const float acc = dot_row_lds<Q8, VD / 256>(wb, l.act[par] + VD);
+    const float res = l.act[par][u];  // the layer input as DIN (phase p - 2) staged it
     if (lane_id() == 0) stt(rs, SOFF(after) + 8u * unsigned(u), res + acc, tag(a, p));
     return true;
 }
@@ -847,7 +855,7 @@ __device__ __forceinline__ bool phase_down(const Args& a, Rs rs, LayerP w, Layer
     if (!bsync(l, p)) return false;
     if (u >= H) return true;
     const float acc = dot_row_lds<Q8, I / 256>(wb, l.act[par]);
-    const float res = wait1(a, rs, SOFF(after) + 8u * unsigned(u), tag(a, p - 2), l, wall_clock64(), p);
+    const float res = l.act[par ^ 1][u];  // `after` as GLU (phase p - 1) staged it
     if (lane_id() == 0) stt(rs, SOFF(x) + 8u * unsigned(u), res + acc, tag(a, p));
     return true;
 }
@@ -1187,7 +1195,7 @@ __device__ __forceinline__ bool phase_o(const Args& a, Rs rs, int L, int p, int 
     if (!bsync(l, p)) return false;
     if (u >= H) return true;
     const float acc = dot_row_lds<Q8, NH * HD / 256>(wb, l.act[par]);
-    const float res = input_at<Q8>(a, rs, L, p - 4, u, l, p);
+    const float res = l.act[par ^ 1][u];  // the layer input as AQKV (phase p - 3) staged it
     if (lane_id() == 0) stt(rs, SOFF(after) + 8u * unsigned(u), res + acc, tag(a, p));
     return true;
 }
