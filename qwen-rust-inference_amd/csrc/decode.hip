@@ -105,6 +105,7 @@ struct Scratch {
     f2 pml[NH * SMAX * 2];
     float pacc[NH * SMAX * HD];
     f2 lmpart[NW * 4];  // (max, index, non-finite count, unused) per wave
+    unsigned lmpool[4];  // lm_head chunk counters: [epoch & 1] this launch's, the other reset for the next
 };
 #define SOFF(field) unsigned(offsetof(::qr::dec::Scratch, field))
 
@@ -245,6 +246,8 @@ struct Lds {
     int fail;  // the earliest phase in which a lane of the block timed out (kNoFail: none)
     int token;  // this launch's token
     int lmnext;  // the next lm_head row group of the block's range to hand out
+    int lmchunk;  // the pool chunk the block streams now
+    int lmctr[2];  // the next row group of that chunk, by chunk parity
 };
 constexpr int kNoFail = 0x7fffffff;
 
@@ -338,6 +341,16 @@ __device__ __forceinline__ bool bsync(Lds& l, int p) {
     __builtin_amdgcn_s_barrier();
     compiler_fence();
     return fail_phase(l) >= p;
+}
+
+// Block barrier with no wait on memory counters. After a phase: every wave
+// of the block has issued its outputs before any issues the next phase's
+// loads, which would otherwise queue ahead of a late wave's output stores in
+// the CU's memory pipeline.
+__device__ __forceinline__ void out_barrier() {
+    compiler_fence();
+    __builtin_amdgcn_s_barrier();
+    compiler_fence();
 }
 
 // ---------------------------------------------------------------- staging
@@ -1249,10 +1262,19 @@ __device__ __forceinline__ void lm_rows(Rs lg, const f4* buf, const f4 (&xv)[4],
 // handed out in order by an LDS counter, so the waves of a block finish
 // together (the second wave on each SIMD streams more slowly than the first).
 // Every row is computed the same way whichever wave takes it.
+// The first 85 % of the rows (whole groups, the same count per block) are in
+// fixed block ranges; the rest is a pool of LM_CHUNK-row chunks handed to
+// blocks in order by a device-wide counter once their range is done (the
+// XCDs stream at different rates, by up to 20 %, and which ones are slow
+// differs from GPU to GPU).
+constexpr int LM_CHUNK = 64;
+__device__ __forceinline__ int lm_static_rows(int vocab) {
+    return vocab / 20 * 17 / (BLOCKS * LM_G) * (BLOCKS * LM_G);
+}
 __device__ __forceinline__ void lm_block_range(int u, int vocab, int& first, int& last) {
-    const int rb = (vocab + BLOCKS - 1) / BLOCKS;
-    first = min(vocab, (u % BLOCKS) * rb);
-    last = min(vocab, first + rb);
+    const int rb = lm_static_rows(vocab) / BLOCKS;
+    first = (u % BLOCKS) * rb;
+    last = first + rb;
 }
 template <bool Q8>
 __device__ __forceinline__ void prefetch_lm(const Args& a, int u, f4* wb) {
@@ -1260,10 +1282,34 @@ __device__ __forceinline__ void prefetch_lm(const Args& a, int u, f4* wb) {
     lm_block_range(u, a.vocab, first, last);
     lm_load<Q8>(rsrc(a.lm_head), first + LM_G * (u / BLOCKS), last, a.vocab, wb);
 }
-__device__ __forceinline__ int lm_grab(Lds& l, int first) {
+__device__ __forceinline__ int lm_grab(int* ctr, int first) {
     int g = 0;
-    if (lane_id() == 0) g = __hip_atomic_fetch_add(&l.lmnext, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    if (lane_id() == 0) g = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     return first + LM_G * __builtin_amdgcn_readfirstlane(g);
+}
+// Rows [first, last) in groups of LM_G shared by the block's waves: wave w
+// takes group w first (already in wb when `pre`), the others in order from
+// the LDS counter *ctr (which starts at WAVES). Groups alternate between wb
+// and nb; the counter only grows, so once a grabbed group lies past the range
+// every later one does too.
+template <bool Q8>
+__device__ __forceinline__ void lm_stream(Rs lm, Rs lg, const f4 (&xv)[4], int first, int last, int vocab, int* ctr,
+                                          bool pre, f4* wb, f4* nb, float& best, unsigned& at, unsigned& bad) {
+    int c0 = first + LM_G * int(threadIdx.x >> 6);
+    if (!pre) lm_load<Q8>(lm, c0, last, vocab, wb);
+    int c1 = lm_grab(ctr, first);
+    lm_load<Q8>(lm, c1, last, vocab, nb);
+    for (;;) {
+        if (c0 >= last) break;
+        lm_rows<Q8>(lg, wb, xv, c0, last, best, at, bad);
+        if (c1 >= last) break;
+        c0 = lm_grab(ctr, first);
+        lm_load<Q8>(lm, c0, last, vocab, wb);
+        lm_rows<Q8>(lg, nb, xv, c1, last, best, at, bad);
+        if (c0 >= last) break;
+        c1 = lm_grab(ctr, first);
+        lm_load<Q8>(lm, c1, last, vocab, nb);
+    }
 }
 template <bool Q8>
 __device__ __forceinline__ bool phase_lm(const Args& a, Rs rs, int p, int u, f4* wb, Lds& l) {
@@ -1279,20 +1325,25 @@ __device__ __forceinline__ bool phase_lm(const Args& a, Rs rs, int p, int u, f4*
     float best = -INFINITY;
     unsigned at = 0xffffffffu, bad = 0;
     f4 nb[4 * LM_G];
-    // groups alternate between wb and nb; the counter only grows, so once a
-    // grabbed group lies past the range every later one does too
-    int c0 = first + LM_G * (u / BLOCKS), c1 = lm_grab(l, first);
-    lm_load<Q8>(lm, c1, last, a.vocab, nb);
-    for (;;) {
-        if (c0 >= last) break;
-        lm_rows<Q8>(lg, wb, xv, c0, last, best, at, bad);
-        if (c1 >= last) break;
-        c0 = lm_grab(l, first);
-        lm_load<Q8>(lm, c0, last, a.vocab, wb);
-        lm_rows<Q8>(lg, nb, xv, c1, last, best, at, bad);
-        if (c0 >= last) break;
-        c1 = lm_grab(l, first);
-        lm_load<Q8>(lm, c1, last, a.vocab, nb);
+    lm_stream<Q8>(lm, lg, xv, first, last, a.vocab, &l.lmnext, true, wb, nb, best, at, bad);
+    // then pool chunks, in increasing row order like the range (so a wave's
+    // first maximum is its lowest index): thread 0 takes the block's next
+    // chunk between two block barriers (the waves are done with the previous
+    // chunk's counter); each take returns a larger index, so the loop ends
+    const int srows = lm_static_rows(a.vocab), nchunks = (a.vocab - srows + LM_CHUNK - 1) / LM_CHUNK;
+    for (int round = 0; round <= nchunks; ++round) {
+        out_barrier();
+        if (threadIdx.x == 0) {
+            l.lmchunk = int(__hip_atomic_fetch_add(&a.s->lmpool[a.epoch & 1u], 1u, __ATOMIC_RELAXED,
+                                                   __HIP_MEMORY_SCOPE_AGENT));
+            l.lmctr[round & 1] = WAVES;
+        }
+        out_barrier();
+        const int c = __builtin_amdgcn_readfirstlane(l.lmchunk);
+        if (c >= nchunks) break;
+        const int cf = srows + c * LM_CHUNK;
+        lm_stream<Q8>(lm, lg, xv, cf, min(a.vocab, cf + LM_CHUNK), a.vocab, &l.lmctr[round & 1], false, wb, nb, best,
+                      at, bad);
     }
     if (lane_id() == 0) {
         const unsigned o = SOFF(lmpart) + unsigned(u) * 32u, t = tag(a, p);
@@ -1373,14 +1424,6 @@ __device__ __forceinline__ void phase_arg(const Args& a, Rs rs, int p, Lds& l) {
 }
 
 // ---------------------------------------------------------------- the kernel
-// Every wave of the block has issued its outputs before any issues the next
-// phase's loads, which would otherwise queue ahead of a late wave's output
-// stores in the CU's memory pipeline.
-__device__ __forceinline__ void out_barrier() {
-    compiler_fence();
-    __builtin_amdgcn_s_barrier();
-    compiler_fence();
-}
 // Part 0 of the first phase of layer L, or the LM head's first rows after the
 // last layer.
 // The weights that a phase's first polls queue behind (part 0 of DIN / AQKV /
@@ -1435,6 +1478,8 @@ __global__ __launch_bounds__(THREADS, 1) void decode_kernel(Args a) {
     if (threadIdx.x == 0) {
         l.fail = kNoFail;
         l.lmnext = WAVES;  // groups 0 .. WAVES - 1 are the waves' first, prefetched ones
+        if (blockIdx.x == 0)  // the next launch's lm_head chunk counter (this launch uses the other)
+            stx(rsrc(a.s), SOFF(lmpool) + 4u * ((a.epoch + 1u) & 1u), 0.f);
         int tok = a.token;
         if (a.chain) {  // the previous launch's argmax (kernel boundary: its stores are visible)
             const float f = ldp(rsrc(a.picks), 0);
