@@ -1424,8 +1424,7 @@ __device__ __forceinline__ void phase_arg(const Args& a, Rs rs, int p, Lds& l) {
 }
 
 // ---------------------------------------------------------------- the kernel
-// Part 0 of the first phase of layer L, or the LM head's first rows after the
-// last layer.
+// Part 0 of the first phase of layer L (L < nlayers).
 // The weights that a phase's first polls queue behind (part 0 of DIN / AQKV /
 // GLU / DOWN) are read with allocating loads in the layers of these masks,
 // all other weights non-temporally: that much stays in the 256 MB memory-side
@@ -1446,10 +1445,6 @@ __device__ __forceinline__ bool kept(const Args& a, unsigned long long mask, int
 }
 template <bool Q8>
 __device__ __forceinline__ void prefetch_layer(const Args& a, int L, int u, f4* wb) {
-    if (L >= a.nlayers) {
-        prefetch_lm<Q8>(a, u, wb);
-        return;
-    }
     const LayerP w = layer(a, L);
     if (w->attention) {
         if (kept(a, Q8 ? kKeepAllQ8 : kKeepAqkv, L))
@@ -1490,10 +1485,19 @@ __global__ __launch_bounds__(THREADS, 1) void decode_kernel(Args a) {
     __syncthreads();
     const Rs rs = rsrc(a.s);
     f4 wb[WBUF];
-    prefetch_layer<Q8>(a, 0, unit, wb);
     int p = 0;
     for (int L = 0; L < a.nlayers; ++L) {
         const LayerP w = layer(a, L);
+        // Part 0 of the layer's first phase, issued here rather than before
+        // the loop's back edge: registers with loads in flight across a back
+        // edge (or a join the compiler has to reconcile) are moved there, and
+        // every move waits for its load, i.e. for the whole prefetch, before
+        // the layer's polls can leave. The buffer is cleared first so that no
+        // earlier value has to survive into the layer.
+        if (L > 0) out_barrier();
+#pragma unroll
+        for (int k = 0; k < WBUF; ++k) wb[k] = f4(0.f);
+        prefetch_layer<Q8>(a, L, opaque_uniform(unit), wb);
         if (w->attention) {
             if (!phase_aqkv<Q8>(a, rs, w, L, p, opaque_uniform(unit), wb, l)) return;
             out_barrier();
@@ -1533,10 +1537,10 @@ __global__ __launch_bounds__(THREADS, 1) void decode_kernel(Args a) {
         ++p;
         if (!phase_down<Q8>(a, rs, w, L + 1 < a.nlayers ? layer(a, L + 1) : nullptr, p, opaque_uniform(unit), wb, l))
             return;
-        out_barrier();
-        prefetch_layer<Q8>(a, L + 1, opaque_uniform(unit), wb);
         ++p;
     }
+    out_barrier();
+    prefetch_lm<Q8>(a, opaque_uniform(unit), wb);
     if (!phase_lm<Q8>(a, rs, p, opaque_uniform(unit), wb, l)) return;
     ++p;
     if (blockIdx.x == 0) phase_arg(a, rs, p, l);
