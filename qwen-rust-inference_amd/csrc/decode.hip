@@ -77,11 +77,12 @@ constexpr int SMAX = 256;           // attention splits per KV head
 constexpr int QPG = NH / NKV;       // query heads per KV head: the waves of one attention slot
 constexpr int MAXPH = 6 * 64 + 2;
 constexpr int DIN_RPW = 4, GLU_RPW = 2, AQKV_RPW = 3, Z_RPW = 2;
-// fp32 DeltaNet layers: units >= EARLY_U (waves 4..7 of every block) have no
-// DOUT row; they take GLU rows 0 .. GLU_EARLY_ROWS - 1 and load both of them
-// right after DOUT's barrier, while DOUT's rows are summed (the other GLU rows
-// go to units from 0 on, loaded at the usual time).
-constexpr int EARLY_U = 4 * BLOCKS, GLU_EARLY_ROWS = GLU_RPW * (NW - EARLY_U);
+// fp32 DeltaNet layers: units >= EARLY_U (waves 6 and 7 of every block) have
+// no DOUT row; they take GLU rows 0 .. GLU_EARLY_ROWS - 1 and load both of
+// them right after DOUT's barrier, while DOUT's rows are summed (the other GLU
+// rows go to units from 0 on, loaded at the usual time). Two waves per CU
+// measured best (four: +4 us per token, none: +9).
+constexpr int EARLY_U = 6 * BLOCKS, GLU_EARLY_ROWS = GLU_RPW * (NW - EARLY_U);
 constexpr int MIX_WAVES = VH * 8;  // 16 value columns per wave
 constexpr int COMB_WAVES = NH * (HD / 4);
 static_assert(DIN_RPW * NW >= DIN_ROWS && GLU_RPW * NW >= I && AQKV_RPW * NW >= AQKV_ROWS, "rows per wave");
