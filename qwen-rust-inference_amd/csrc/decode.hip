@@ -77,12 +77,16 @@ constexpr int SMAX = 256;           // attention splits per KV head
 constexpr int QPG = NH / NKV;       // query heads per KV head: the waves of one attention slot
 constexpr int MAXPH = 6 * 64 + 2;
 constexpr int DIN_RPW = 4, GLU_RPW = 2, AQKV_RPW = 3, Z_RPW = 2;
-// fp32 DeltaNet layers: units >= EARLY_U (waves 6 and 7 of every block) have
-// no DOUT row; they take GLU rows 0 .. GLU_EARLY_ROWS - 1 and load both of
-// them right after DOUT's barrier, while DOUT's rows are summed (the other GLU
-// rows go to units from 0 on, loaded at the usual time). Two waves per CU
-// measured best (four: +4 us per token, none: +9).
-constexpr int EARLY_U = 6 * BLOCKS, GLU_EARLY_ROWS = GLU_RPW * (NW - EARLY_U);
+// DeltaNet layers: units >= early_u (fp32: waves 6 and 7 of every block,
+// int8: waves 4-7) have no DOUT row; they take GLU rows 0 .. (NW - early_u)
+// GLU_RPW - 1 and load both of them right after DOUT's barrier, while DOUT's
+// rows are summed (the other GLU rows go to units from 0 on, loaded at the
+// usual time). Measured best: fp32 two waves per CU (four: +4 us per token,
+// none: +9), int8 four (none: +9 us).
+template <bool Q8>
+__device__ __forceinline__ constexpr int early_u() {
+    return Q8 ? 4 * BLOCKS : 6 * BLOCKS;
+}
 constexpr int MIX_WAVES = VH * 8;  // 16 value columns per wave
 constexpr int COMB_WAVES = NH * (HD / 4);
 static_assert(DIN_RPW * NW >= DIN_ROWS && GLU_RPW * NW >= I && AQKV_RPW * NW >= AQKV_ROWS, "rows per wave");
@@ -788,8 +792,8 @@ __device__ __forceinline__ bool phase_dout(const Args& a, Rs rs, LayerP w, int L
     }
     if (!bsync(l, p)) return false;
     if (u >= H) {
-        if (!Q8 && u >= EARLY_U) {  // this unit's GLU rows, both parts, while DOUT's rows are summed
-            glu_load<Q8, 0, kNT>(w, u, wb);
+        if (u >= early_u<Q8>()) {  // this unit's GLU rows, both parts, while DOUT's rows are summed
+            glu_load<Q8, 0, Q8 ? 0 : kNT>(w, u, wb);  // int8: part 0 stays in the memory-side cache
             glu_load<Q8, 1, kNT>(w, u, wb);
         }
         return true;
@@ -804,8 +808,9 @@ __device__ __forceinline__ bool phase_dout(const Args& a, Rs rs, LayerP w, int L
 // The first of unit u's GLU_RPW rows (dn: a DeltaNet layer).
 template <bool Q8>
 __device__ __forceinline__ int glu_first(int u, bool dn) {
-    if (Q8 || !dn) return u * GLU_RPW;
-    return u >= EARLY_U ? (u - EARLY_U) * GLU_RPW : GLU_EARLY_ROWS + u * GLU_RPW;
+    if (!dn) return u * GLU_RPW;
+    constexpr int E = early_u<Q8>(), ER = GLU_RPW * (NW - E);
+    return u >= E ? (u - E) * GLU_RPW : ER + u * GLU_RPW;
 }
 template <bool Q8, int R, int AUX = kNT>
 __device__ __forceinline__ void glu_load(LayerP w, int u, f4* wb) {
@@ -817,7 +822,7 @@ __device__ __forceinline__ void glu_load(LayerP w, int u, f4* wb) {
 }
 template <bool Q8, int AUX = kNT>
 __device__ __forceinline__ void prefetch_glu(LayerP w, int u, f4* wb, int part) {
-    if (!Q8 && !w->attention && u >= EARLY_U) return;  // loaded in DOUT
+    if (!w->attention && u >= early_u<Q8>()) return;  // loaded in DOUT
     if (part == 0)
         glu_load<Q8, 0, AUX>(w, u, wb);
     else
@@ -1268,7 +1273,7 @@ __device__ __forceinline__ void lm_rows(Rs lg, const f4* buf, const f4 (&xv)[4],
 // blocks in order by a device-wide counter once their range is done (the
 // XCDs stream at different rates, by up to 20 %, and which ones are slow
 // differs from GPU to GPU).
-constexpr int LM_CHUNK = 64;
+constexpr int LM_CHUNK = 64, LM_CHUNK_Q8 = 256;  // rows (int8 rows are a quarter of the bytes)
 __device__ __forceinline__ int lm_static_rows(int vocab) {
     return vocab / 20 * 17 / (BLOCKS * LM_G) * (BLOCKS * LM_G);
 }
@@ -1331,7 +1336,8 @@ __device__ __forceinline__ bool phase_lm(const Args& a, Rs rs, int p, int u, f4*
     // first maximum is its lowest index): thread 0 takes the block's next
     // chunk between two block barriers (the waves are done with the previous
     // chunk's counter); each take returns a larger index, so the loop ends
-    const int srows = lm_static_rows(a.vocab), nchunks = (a.vocab - srows + LM_CHUNK - 1) / LM_CHUNK;
+    constexpr int LMC = Q8 ? LM_CHUNK_Q8 : LM_CHUNK;
+    const int srows = lm_static_rows(a.vocab), nchunks = (a.vocab - srows + LMC - 1) / LMC;
     for (int round = 0; round <= nchunks; ++round) {
         out_barrier();
         if (threadIdx.x == 0) {
@@ -1342,8 +1348,8 @@ __device__ __forceinline__ bool phase_lm(const Args& a, Rs rs, int p, int u, f4*
         out_barrier();
         const int c = __builtin_amdgcn_readfirstlane(l.lmchunk);
         if (c >= nchunks) break;
-        const int cf = srows + c * LM_CHUNK;
-        lm_stream<Q8>(lm, lg, xv, cf, min(a.vocab, cf + LM_CHUNK), a.vocab, &l.lmctr[round & 1], false, wb, nb, best,
+        const int cf = srows + c * LMC;
+        lm_stream<Q8>(lm, lg, xv, cf, min(a.vocab, cf + LMC), a.vocab, &l.lmctr[round & 1], false, wb, nb, best,
                       at, bad);
     }
     if (lane_id() == 0) {
@@ -1437,9 +1443,10 @@ __device__ __forceinline__ void phase_arg(const Args& a, Rs rs, int p, Lds& l) {
 // KEEP_MAX_POS on the cache is left to them (ctx 8192: 744 us per step
 // instead of 763 with both).
 constexpr unsigned long long kKeepDin = 0xfffull, kKeepAqkv = ~0ull, kKeepGlu = 0, kKeepDown = 0;
-// int8 weights are a quarter of the bytes: part 0 of every heavy phase in
-// every layer fits (about 210 MB)
-constexpr unsigned long long kKeepAllQ8 = ~0ull;
+// int8 weights are a quarter of the bytes: part 0 of every heavy phase fits
+// for many layers; layers 0-15 measured best (all 24: +7 us per token, 0-11:
+// +3, 0-19: +5)
+constexpr unsigned long long kKeepQ8 = 0xffffull;
 constexpr int KEEP_MAX_POS = 1536;
 __device__ __forceinline__ bool kept(const Args& a, unsigned long long mask, int L) {
     return a.pos < KEEP_MAX_POS && ((mask >> L) & 1ull);
@@ -1448,12 +1455,12 @@ template <bool Q8>
 __device__ __forceinline__ void prefetch_layer(const Args& a, int L, int u, f4* wb) {
     const LayerP w = layer(a, L);
     if (w->attention) {
-        if (kept(a, Q8 ? kKeepAllQ8 : kKeepAqkv, L))
+        if (kept(a, Q8 ? kKeepQ8 : kKeepAqkv, L))
             prefetch_aqkv<Q8, 0>(w, u, wb, 0);
         else
             prefetch_aqkv<Q8>(w, u, wb, 0);
     } else {
-        if (kept(a, Q8 ? kKeepAllQ8 : kKeepDin, L))
+        if (kept(a, Q8 ? kKeepQ8 : kKeepDin, L))
             prefetch_din<Q8, 0>(w, u, wb, 0);
         else
             prefetch_din<Q8>(w, u, wb, 0);
@@ -1524,14 +1531,14 @@ __global__ __launch_bounds__(THREADS, 1) void decode_kernel(Args a) {
             if (!phase_dout<Q8>(a, rs, w, L, p, opaque_uniform(unit), wb, l)) return;
         }
         out_barrier();
-        if (kept(a, Q8 ? kKeepAllQ8 : kKeepGlu, L))
+        if (kept(a, Q8 ? kKeepQ8 : kKeepGlu, L))
             prefetch_glu<Q8, 0>(w, opaque_uniform(unit), wb, 0);
         else
             prefetch_glu<Q8>(w, opaque_uniform(unit), wb, 0);
         ++p;
         if (!phase_glu<Q8>(a, rs, w, p, opaque_uniform(unit), wb, l)) return;
         out_barrier();
-        if (kept(a, Q8 ? kKeepAllQ8 : kKeepDown, L))
+        if (kept(a, Q8 ? kKeepQ8 : kKeepDown, L))
             prefetch_row<Q8, I, 0, 0>(w->down, opaque_uniform(unit), H, wb);
         else
             prefetch_row<Q8, I, 0>(w->down, opaque_uniform(unit), H, wb);
