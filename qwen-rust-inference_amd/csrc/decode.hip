@@ -90,7 +90,7 @@ __device__ __forceinline__ constexpr int early_u() {
 constexpr int MIX_WAVES = VH * 8;  // 16 value columns per wave
 constexpr int COMB_WAVES = NH * (HD / 4);
 static_assert(DIN_RPW * NW >= DIN_ROWS && GLU_RPW * NW >= I && AQKV_RPW * NW >= AQKV_ROWS, "rows per wave");
-static_assert(Z_RPW * (NW - MIX_WAVES) >= VD && COMB_WAVES <= NW && NKV * SMAX * QPG <= NW && SMAX % 64 == 0, "waves");
+static_assert(Z_RPW * WAVES * (BLOCKS - MIX_WAVES) >= VD && MIX_WAVES <= BLOCKS && COMB_WAVES <= NW && NKV * SMAX * QPG <= NW && SMAX % 64 == 0, "waves");
 static_assert(WAVES % QPG == 0 && NKV * SMAX <= BLOCKS * (WAVES / QPG), "attention slots: QPG waves of one block each");
 static_assert(4 * DIN_RPW <= WBUF && 8 * GLU_RPW <= WBUF && 4 * AQKV_RPW <= WBUF && 4 * Z_RPW <= WBUF, "buffer");
 static_assert(I / 256 <= WBUF && VD / 256 <= WBUF && NH * HD / 256 <= WBUF && 8 <= WBUF && KVE <= WBUF, "buffer");
@@ -595,10 +595,18 @@ __device__ __forceinline__ bool phase_din(const Args& a, Rs rs, LayerP w, int L,
 // ---- T_MIX: L2 q/k, gates and the gated delta rule for 16 value columns of
 // one head per wave (units 0..127); silu(z), z = in_proj_z . n, on the other
 // units (only silu(z) is used: the gated norm's gate, reference.h:201-207).
+// z units: every wave of blocks MIX_WAVES .. BLOCKS - 1, so that no z rows
+// queue ahead of the delta-rule waves' polls in their CUs (blocks 0 ..
+// MIX_WAVES - 1, wave 0): 5 us per token less than z rows on units 128 ..
+// 1151 of every block; -1: none
+__device__ __forceinline__ int z_index(int u) {
+    const int b = u % BLOCKS;
+    return b >= MIX_WAVES ? (u / BLOCKS) * (BLOCKS - MIX_WAVES) + (b - MIX_WAVES) : -1;
+}
 template <bool Q8, int R>
 __device__ __forceinline__ void z_load(LayerP w, int u, f4* wb) {
-    const int row = (u - MIX_WAVES) * Z_RPW + R;
-    if (row < VD) load_row_h<Q8, 4 * R>(wb, rsrc(w->z), row, VD);
+    const int zi = z_index(u), row = zi * Z_RPW + R;
+    if (zi >= 0 && row < VD) load_row_h<Q8, 4 * R>(wb, rsrc(w->z), row, VD);
 }
 template <bool Q8>
 __device__ __forceinline__ void prefetch_mix(LayerP w, int u, f4* wb) {
@@ -620,8 +628,8 @@ __device__ __forceinline__ void prefetch_mix(LayerP w, int u, f4* wb) {
 }
 template <bool Q8, int R>
 __device__ __forceinline__ void z_row(Rs rs, const f4* wb, const f4 (&xv)[4], int u, unsigned t) {
-    const int row = (u - MIX_WAVES) * Z_RPW + R;
-    if (row < VD) {
+    const int zi = z_index(u), row = zi * Z_RPW + R;
+    if (zi >= 0 && row < VD) {
         const float acc = dot_row_h<Q8, 4 * R>(wb, xv);
         if (lane_id() == 0) stt(rs, SOFF(z) + 8u * unsigned(row), silu(acc), t);
     }
@@ -636,7 +644,7 @@ __device__ __forceinline__ bool phase_mix(const Args& a, Rs rs, LayerP w, int L,
     const int par = (p - 1) & 1;
     const unsigned t = tag(a, p);
     if (u >= MIX_WAVES) {
-        if ((u - MIX_WAVES) * Z_RPW >= VD) return true;
+        if (z_index(u) < 0) return true;
         f4 xv[4];
         normed_chunks<Q8>(l, par, a.eps, xv);
         z_row<Q8, 0>(rs, wb, xv, u, t);
@@ -644,7 +652,7 @@ __device__ __forceinline__ bool phase_mix(const Args& a, Rs rs, LayerP w, int L,
         return true;
     }
     // the delta rule is the phase's critical path: its wave goes first on its
-    // SIMD (whose other wave streams z rows) until its state is written back
+    // SIMD until its state is written back
     __builtin_amdgcn_s_setprio(3);
     const unsigned lane = lane_id();
     const int wave = int(threadIdx.x >> 6);
