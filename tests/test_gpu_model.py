@@ -232,6 +232,38 @@ def test_qwen08b_short_greedy(qwen08b):
             parity(run.state(layer, which), s.part(layer, which), where=f"0.8B state {layer}/{which}")
 
 
+@pytest.mark.parametrize("vocab", [1000, 3001])
+@pytest.mark.parametrize("fmt", [E.F32, E.INT8])
+def test_one_launch_small_vocabulary(vocab, fmt):
+    """The one-launch decode on the 0.8B geometry with 4 layers and a small
+    vocabulary: 1000 rows all go to the lm_head chunk pool (no block range),
+    3001 leave 2048 rows in the block ranges and a ragged last chunk. Every
+    step's logits against the oracle (fp32 bound; int8 against the oracle on
+    the dequantised weights), identical greedy IDs."""
+    c = M.make_config(hidden=1024, intermediate=3584, vocab=vocab,
+                      layer_types=["linear_attention"] * 3 + ["full_attention"], heads=8, kv_heads=2, head_dim=256,
+                      rotary_dim=64, key_heads=16, value_heads=16, key_dim=128, value_dim=128, conv_kernel=4,
+                      max_positions=256, eps=1e-6, theta=1e7)
+    w = M.synthetic_weights(c, seed=3)
+    prompt = [int(v) for v in np.random.default_rng(9).integers(0, vocab, 6)]
+    run = E.Model(w, fmt=fmt).new_run(32, chunk=8)
+    assert run.decode_plan
+    st = (O.Oracle(w) if fmt == E.F32 else dequantised(c, w)).new_state()
+    for t in prompt:
+        want = st.step(t, O.VECTOR)
+    rtol = {} if fmt == E.F32 else {"rtol": INT8_RTOL}
+    parity(run.prefill(prompt), want, where=f"vocab {vocab} prefill", **rtol)
+    tok = O.select_greedy(want)
+    for i in range(5):
+        print(f"vocab {vocab} fmt {fmt} one-launch step {i}", flush=True)
+        got = run.step(tok)
+        want = st.step(tok, O.VECTOR)
+        parity(got, want, where=f"vocab {vocab} step {i}", **rtol)
+        if fmt == E.F32:
+            assert O.select_greedy(got) == O.select_greedy(want)
+        tok = O.select_greedy(want)
+
+
 def test_qwen08b_decode_step_logits_against_oracle(qwen08b, qwen08b_models):
     """Each one-launch step's full logits against the oracle (fp32 bound)."""
     c, w = qwen08b
