@@ -56,6 +56,13 @@ def test_gemm_f32(gpu, rows, cols, batch):
     assert np.all(np.abs(got - want) <= bound)
 
 
+@pytest.mark.parametrize("batch", [1, 4])
+def test_gemm_f32_lm_head_shape(gpu, batch):
+    """The tied lm_head (248,320 x 1024, 1 GB of fp32) as the op path runs it:
+    one logit row (GEMV) and the 4 rows of a verify pass, against fp64."""
+    test_gemm_f32(gpu, 248320, 1024, batch)
+
+
 @pytest.mark.parametrize("rows,cols", SHAPES_08B + [(33, 20), (7, 12), (3, 260)])
 @pytest.mark.parametrize("batch", [127, 130, 257])
 def test_gemm_f32_prefill_tiles(gpu, rows, cols, batch):
