@@ -155,25 +155,42 @@ __global__ __launch_bounds__(256) void attention_read_kernel(ReadArgs a) {
     }
 }
 
-// Merge the split partials: one thread per (row, head, dim).
+// Merge the split partials: one thread per (row, head, 4 dims), the partial
+// sums read as 8-byte pairs (a partial is d + 2 floats: even, not a multiple
+// of 4); every output element sums its splits in order, as one thread per
+// element would.
 __global__ __launch_bounds__(256) void attention_combine_kernel(ReadArgs a) {
+    typedef float f2v __attribute__((ext_vector_type(2)));
+    typedef float f4v __attribute__((ext_vector_type(4)));
     const long idx = blockIdx.x * long(blockDim.x) + threadIdx.x;
-    const long total = long(a.rows) * a.heads * a.d;
+    const int q = a.d / 4;
+    const long total = long(a.rows) * a.heads * q;
     if (idx >= total) return;
-    const int i = int(idx % a.d);
-    const long rh = idx / a.d;  // row * heads + head
+    const int i = 4 * int(idx % q);
+    const long rh = idx / q;  // row * heads + head
     const float* parts = a.parts + size_t(rh) * a.splits * (a.d + 2);
     float mm = -INFINITY;
     for (int s = 0; s < a.splits; ++s) mm = fmaxf(mm, parts[size_t(s) * (a.d + 2)]);
-    float den = 0.f, num = 0.f;
+    float den = 0.f;
+    f4v num = {0.f, 0.f, 0.f, 0.f};
     for (int s = 0; s < a.splits; ++s) {
         const float* p = parts + size_t(s) * (a.d + 2);
         const float c = p[0] == -INFINITY ? 0.f : expf(p[0] - mm);
         den += p[1] * c;
-        num += p[2 + i] * c;
+        const f2v lo = *reinterpret_cast<const f2v*>(p + 2 + i), hi = *reinterpret_cast<const f2v*>(p + 4 + i);
+        num.x += lo.x * c;
+        num.y += lo.y * c;
+        num.z += hi.x * c;
+        num.w += hi.y * c;
     }
     const size_t o = size_t(rh) * a.d + i;
-    a.out[o] = (num / den) * sigmoidf_(a.gate[o]);
+    const f4v g = *reinterpret_cast<const f4v*>(a.gate + o);
+    f4v r;
+    r.x = (num.x / den) * sigmoidf_(g.x);
+    r.y = (num.y / den) * sigmoidf_(g.y);
+    r.z = (num.z / den) * sigmoidf_(g.z);
+    r.w = (num.w / den) * sigmoidf_(g.w);
+    *reinterpret_cast<f4v*>(a.out + o) = r;
 }
 
 // ---------------------------------------------------------------- prefill
@@ -679,7 +696,7 @@ int launch_prefill_g(hipStream_t s, const ReadArgs& a) {
             hipLaunchKernelGGL((attention_prefill_kernel<D, G>), grid, dim3(64 * G), 0, s, a);
         if (a.splits == 1) return int(hipGetLastError());
         if (hipError_t e = hipGetLastError()) return int(e);
-        const long total = long(a.rows) * a.heads * a.d;
+        const long total = long(a.rows) * a.heads * (a.d / 4);
         hipLaunchKernelGGL(attention_combine_kernel, dim3(ceil_div(total, 256)), dim3(256), 0, s, a);
         return int(hipGetLastError());
     }
@@ -812,7 +829,7 @@ int run_attention_read(hipStream_t s, int heads_count, const Params& p, float* s
     default: return int(hipErrorInvalidValue);
     }
     if (e || a.splits == 1) return e;
-    const long total = long(a.rows) * a.heads * a.d;
+    const long total = long(a.rows) * a.heads * (a.d / 4);
     hipLaunchKernelGGL(attention_combine_kernel, dim3(ceil_div(total, 256)), dim3(256), 0, s, a);
     return int(hipGetLastError());
 }
