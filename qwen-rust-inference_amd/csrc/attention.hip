@@ -155,33 +155,38 @@ __global__ __launch_bounds__(256) void attention_read_kernel(ReadArgs a) {
     }
 }
 
-// Merge the split partials: the four lanes of a quad per (row, head, 4 dims),
-// lane q of the quad taking splits q, q + 4, ... (a decode row has tens of
-// splits: a lane's loads are then in flight together), the quad's (max, sum,
-// weighted sums) combined by two xor shuffles; the partial sums are read as
-// 8-byte pairs (a partial is d + 2 floats: even, not a multiple of 4). The
-// order of every sum is fixed, so the result is the same in every run.
+// Merge the split partials: LANES lanes (1, or the 4 of a quad) per (row,
+// head, 4 dims), lane q taking splits q, q + LANES, ... and a quad's (max,
+// sum, weighted sums) combined by two xor shuffles. Quads for a decode row
+// (tens of splits: each lane's loads in flight together), one lane for a
+// prefill chunk (a few shares: more lanes only add shuffles). The partial
+// sums are read as 8-byte pairs (a partial is d + 2 floats: even, not a
+// multiple of 4). The order of every sum is fixed for a given split count.
+template <int LANES>
 __global__ __launch_bounds__(256) void attention_combine_kernel(ReadArgs a) {
     typedef float f2v __attribute__((ext_vector_type(2)));
     typedef float f4v __attribute__((ext_vector_type(4)));
+    static_assert(LANES == 1 || LANES == 4, "one lane or a quad");
     const long idx = blockIdx.x * long(blockDim.x) + threadIdx.x;
     const int q = a.d / 4;
-    const long total = long(a.rows) * a.heads * q * 4;  // whole quads: the shuffles see only live lanes
+    const long total = long(a.rows) * a.heads * q * LANES;  // whole quads: the shuffles see only live lanes
     if (idx >= total) return;
-    const int lq = int(idx & 3);
-    const long e = idx >> 2;
+    const int lq = int(idx % LANES);
+    const long e = idx / LANES;
     const int i = 4 * int(e % q);
     const long rh = e / q;  // row * heads + head
     const float* parts = a.parts + size_t(rh) * a.splits * (a.d + 2);
     float mm = -INFINITY;
 #pragma unroll 8
-    for (int s = lq; s < a.splits; s += 4) mm = fmaxf(mm, parts[size_t(s) * (a.d + 2)]);
-    mm = fmaxf(mm, __shfl_xor(mm, 1, 64));
-    mm = fmaxf(mm, __shfl_xor(mm, 2, 64));
+    for (int s = lq; s < a.splits; s += LANES) mm = fmaxf(mm, parts[size_t(s) * (a.d + 2)]);
+    if constexpr (LANES == 4) {
+        mm = fmaxf(mm, __shfl_xor(mm, 1, 64));
+        mm = fmaxf(mm, __shfl_xor(mm, 2, 64));
+    }
     float den = 0.f;
     f4v num = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll 8
-    for (int s = lq; s < a.splits; s += 4) {
+    for (int s = lq; s < a.splits; s += LANES) {
         const float* p = parts + size_t(s) * (a.d + 2);
         const float c = p[0] == -INFINITY ? 0.f : expf(p[0] - mm);
         den += p[1] * c;
@@ -191,15 +196,17 @@ __global__ __launch_bounds__(256) void attention_combine_kernel(ReadArgs a) {
         num.z += hi.x * c;
         num.w += hi.y * c;
     }
+    if constexpr (LANES == 4) {
 #pragma unroll
-    for (int o = 1; o <= 2; o <<= 1) {
-        den += __shfl_xor(den, o, 64);
-        num.x += __shfl_xor(num.x, o, 64);
-        num.y += __shfl_xor(num.y, o, 64);
-        num.z += __shfl_xor(num.z, o, 64);
-        num.w += __shfl_xor(num.w, o, 64);
+        for (int o = 1; o <= 2; o <<= 1) {
+            den += __shfl_xor(den, o, 64);
+            num.x += __shfl_xor(num.x, o, 64);
+            num.y += __shfl_xor(num.y, o, 64);
+            num.z += __shfl_xor(num.z, o, 64);
+            num.w += __shfl_xor(num.w, o, 64);
+        }
+        if (lq != 0) return;
     }
-    if (lq != 0) return;
     const size_t o = size_t(rh) * a.d + i;
     const f4v g = *reinterpret_cast<const f4v*>(a.gate + o);
     f4v r;
@@ -208,6 +215,15 @@ __global__ __launch_bounds__(256) void attention_combine_kernel(ReadArgs a) {
     r.z = (num.z / den) * sigmoidf_(g.z);
     r.w = (num.w / den) * sigmoidf_(g.w);
     *reinterpret_cast<f4v*>(a.out + o) = r;
+}
+// Launch of the merge: quads from 16 splits on.
+int launch_combine(hipStream_t s, const ReadArgs& a) {
+    const long groups = long(a.rows) * a.heads * (a.d / 4);
+    if (a.splits >= 16)
+        hipLaunchKernelGGL(attention_combine_kernel<4>, dim3(ceil_div(groups * 4, 256)), dim3(256), 0, s, a);
+    else
+        hipLaunchKernelGGL(attention_combine_kernel<1>, dim3(ceil_div(groups, 256)), dim3(256), 0, s, a);
+    return int(hipGetLastError());
 }
 
 // ---------------------------------------------------------------- prefill
@@ -713,9 +729,7 @@ int launch_prefill_g(hipStream_t s, const ReadArgs& a) {
             hipLaunchKernelGGL((attention_prefill_kernel<D, G>), grid, dim3(64 * G), 0, s, a);
         if (a.splits == 1) return int(hipGetLastError());
         if (hipError_t e = hipGetLastError()) return int(e);
-        const long total = long(a.rows) * a.heads * a.d;  // four lanes per 4 dims
-        hipLaunchKernelGGL(attention_combine_kernel, dim3(ceil_div(total, 256)), dim3(256), 0, s, a);
-        return int(hipGetLastError());
+        return launch_combine(s, a);
     }
     return int(hipErrorInvalidValue);
 }
@@ -846,9 +860,7 @@ int run_attention_read(hipStream_t s, int heads_count, const Params& p, float* s
     default: return int(hipErrorInvalidValue);
     }
     if (e || a.splits == 1) return e;
-    const long total = long(a.rows) * a.heads * a.d;  // four lanes per 4 dims
-    hipLaunchKernelGGL(attention_combine_kernel, dim3(ceil_div(total, 256)), dim3(256), 0, s, a);
-    return int(hipGetLastError());
+    return launch_combine(s, a);
 }
 
 }  // namespace qr
