@@ -348,7 +348,7 @@ def main():
         # fp32 call sequence (one qr_gemv per matrix plus separate norm ops, no
         # one-launch step, a per-token embedding copy) and 128-token prefill
         # chunks (src/device.rs PREFILL_CHUNK).
-        md = E.Model(w, disable=E.NO_DECODE_STEP | E.NO_F32_FUSIONS | E.NO_EMBED_ROWS | E.NO_BLAS_GEMM)
+        md = E.Model(w, disable=E.NO_DECODE_STEP | E.NO_F32_FUSIONS | E.NO_EMBED_ROWS | E.NO_PREPARED_GEMM)
         rd = md.new_run(args.prompt + 64, chunk=PREFILL_CHUNK)
         tok = int(np.argmax(rd.prefill(prompt)))
         for _ in range(3):

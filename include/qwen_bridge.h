@@ -150,15 +150,17 @@ int qr_gemm_f32_add_norm(Context* c, float* y, const float* a, const float* x, i
 
 /* Prepared fp32 matrices (no counterpart in the reference's ABI; optional:
  * an engine may call qr_gemm_f32_prepare once after uploading an fp32 matrix
- * `a` of rows x cols, cols % 4 == 0, 16-byte aligned). The bridge then keeps
- * the matrix's three-way BF16 split planes (12 bytes per element) and runs
- * every qr_gemm / qr_gemm_f32_group / qr_gemm_f32_glu projection of `a` over
- * at least 64 tokens as one BF16 GEMM with K' = 6 cols on hipBLASLt (fp32
- * accumulation and output; the same six part products as the split-BF16
- * kernel, hence fp32 accuracy; the GLU then writes gate_y and up_y). The
- * planes are dropped by qr_gemm_f32_release(a), by qr_free(a), and by any
- * qr_write / qr_copy into the matrix's range; unprepared matrices take the
- * split-BF16 kernel. */
+ * `a` of rows x cols, 16-byte aligned). When cols % 32 == 0 the bridge keeps
+ * the matrix's three-way BF16 split planes in MFMA fragment order (6 bytes per
+ * element) and runs every qr_gemm / qr_gemm_f32_group / qr_gemm_f32_glu
+ * projection of `a` over at least 64 tokens on its own BF16-MFMA kernel over
+ * them (gemm_p3.hip: the six part products of the split, fp32 accumulation and
+ * output, hence fp32 accuracy; a GLU of two prepared matrices with rows % 128
+ * == 0 runs gate, up and the silu product as one kernel, gate_y and up_y
+ * untouched). Other column counts prepare nothing (returns 0). The planes are
+ * dropped by qr_gemm_f32_release(a), by qr_free(a), and by any qr_write /
+ * qr_copy into the matrix's range; unprepared matrices take the split-BF16
+ * kernel. */
 int qr_gemm_f32_prepare(Context* c, const float* a, int rows, int cols);
 int qr_gemm_f32_release(Context* c, const float* a);
 

@@ -27,36 +27,36 @@ struct Context {
     size_t rule_chunks_len = 0;
     float* gemm_work = nullptr;  // K-split partial sums of prefill GEMMs
     size_t gemm_work_len = 0;
-    // Prepared fp32 matrices (qr_gemm_f32_prepare): the K'-concatenated BF16
-    // planes of each, by the matrix's device address, for the hipBLASLt path
-    // of prefill projections; dropped when the matrix is freed or written.
+    // Prepared fp32 matrices (qr_gemm_f32_prepare): the P3 planes of each
+    // (common.h), by the matrix's device address, for the prefill projections
+    // of gemm_p3.hip; dropped when the matrix is freed or written.
     struct Prepared {
         int rows, cols;
-        __bf16* w6;
+        __bf16* w3;
     };
     std::map<const float*, Prepared> prepared;
-    // A prepared GLU's gate and up planes side by side ([gate; up]: 2 rows x 6
-    // cols), made on the pair's first prefill GLU, so both projections run as one
-    // GEMM into glu_tmp ([batch][2 rows]); dropped with either matrix's planes.
+    // A prepared GLU's combined gate / up planes (p3_glu_interleave), made on
+    // the pair's first prefill GLU, so both projections and the silu product
+    // run as one kernel; dropped with either matrix's planes.
     struct GluPair {
         int rows, cols;
-        __bf16* w6;
+        __bf16* w3;
     };
     std::map<std::pair<const float*, const float*>, GluPair> glu_pairs;
-    float* glu_tmp = nullptr;
-    size_t glu_tmp_len = 0;
-    qr::Blas* blas = nullptr;
-    __bf16* x6 = nullptr;  // the split planes of a projection's input
-    size_t x6_len = 0;     // in BF16 elements
-    // A producer (a norm, or a GLU's product, over at least kBlasMinBatch rows
-    // of a width some prepared matrix takes) may leave its output's planes in
-    // x6 as it writes the output: they stand for x6_src (x6_rows x x6_cols)
-    // during the very next bridge call only (serial == x6_serial + 1), so
+    // The P3 planes of a projection's input (xp), and a second buffer the GLU
+    // writes its product's planes into while it reads xp (then they swap).
+    __bf16* xp = nullptr;
+    __bf16* xp_alt = nullptr;
+    size_t xp_len = 0, xp_alt_len = 0;  // in BF16 elements
+    // A producer (a norm, or a GLU's product, over at least kPlanesMinBatch
+    // rows of a width some prepared matrix takes) may leave its output's planes
+    // in xp as it writes the output: they stand for xp_src (xp_rows x xp_cols)
+    // during the very next bridge call only (serial == xp_serial + 1), so
     // nothing written in between can make them stale. Every entry point
     // advances the serial.
-    const float* x6_src = nullptr;
-    int x6_rows = 0, x6_cols = 0;
-    unsigned long serial = 0, x6_serial = 0;
+    const float* xp_src = nullptr;
+    int xp_rows = 0, xp_cols = 0;
+    unsigned long serial = 0, xp_serial = 0;
     // The width of the projection that took the last RmsNormGate output right
     // after it (its rows span several groups), by group size: from then on such
     // a norm writes its planes in rows of that width.
@@ -168,76 +168,83 @@ int ensure(Context* c, float** buf, size_t* len, size_t need, const char* what) 
 
 const void* i8_packed(const float* packed) { return packed; }
 
-// ---- prepared fp32 matrices on hipBLASLt (csrc/blas.cpp)
-// Projections of at least this many tokens take the hipBLASLt path when their
+// ---- prepared fp32 matrices (csrc/gemm_p3.hip)
+// Projections of at least this many tokens take the P3 planes when their
 // matrix is prepared (fewer tokens: the split-BF16 kernel, whose tiles the
 // small batches fill as well).
-constexpr int kBlasMinBatch = 64;
+constexpr int kPlanesMinBatch = 64;
 
 const Context::Prepared* prepared_for(Context* c, const void* a, int rows, int cols, int batch) {
-    if (batch < kBlasMinBatch || rows <= 16) return nullptr;
+    if (batch < kPlanesMinBatch || rows <= 16) return nullptr;
     auto it = c->prepared.find(static_cast<const float*>(a));
     if (it == c->prepared.end() || it->second.rows != rows || it->second.cols != cols) return nullptr;
     return &it->second;
 }
-// c->x6 large enough for batch x 6 cols planes (queued work on the old buffer
-// drains first).
-int grow_x6(Context* c, int cols, int batch) {
-    const size_t need = size_t(batch) * 6 * size_t(cols);
-    if (need <= c->x6_len) return 0;
-    c->x6_src = nullptr;
-    if (c->x6) {
+// A planes buffer large enough for batch rows of cols (queued work on the old
+// buffer drains first).
+int grow_planes(Context* c, __bf16** buf, size_t* len, int cols, int batch) {
+    const size_t need = qr::p3_elements(batch, cols);
+    if (need <= *len) return 0;
+    if (*buf) {
         (void)hipStreamSynchronize(c->stream);
-        (void)hipFree(c->x6);
-        c->x6 = nullptr;
-        c->x6_len = 0;
+        (void)hipFree(*buf);
+        *buf = nullptr;
+        *len = 0;
     }
-    auto st = hipMalloc(reinterpret_cast<void**>(&c->x6), need * sizeof(__bf16));
+    auto st = hipMalloc(reinterpret_cast<void**>(buf), need * sizeof(__bf16));
     if (st != hipSuccess) return fail(c, "hipMalloc split input", int(st));
-    c->x6_len = need;
+    *len = need;
     return 0;
 }
-// x's split planes into c->x6: already there when the previous bridge call
+int grow_xp(Context* c, int cols, int batch) {
+    if (qr::p3_elements(batch, cols) > c->xp_len) c->xp_src = nullptr;
+    return grow_planes(c, &c->xp, &c->xp_len, cols, batch);
+}
+// x's P3 planes into c->xp: already there when the previous bridge call
 // produced x with them, else split now.
 int split_input(Context* c, const float* x, int cols, int batch) {
     if (c->gate_out == x && c->gate_serial + 1 == c->serial && cols % c->gate_d == 0)
         c->gate_width[c->gate_d] = cols;  // a gated norm's output projected: its row width
-    if (c->x6_src == x && c->x6_rows == batch && c->x6_cols == cols && c->x6_serial + 1 == c->serial) return 0;
-    c->x6_src = nullptr;
-    if (int st = grow_x6(c, cols, batch)) return st;
-    auto s = scope(c, [&] { return std::string("split6 ") + shape(batch, cols, 1); });
-    return launched(c, "split6", qr::split6(c->stream, c->x6, x, batch, cols, false));
+    if (c->xp_src == x && c->xp_rows == batch && c->xp_cols == cols && c->xp_serial + 1 == c->serial) return 0;
+    c->xp_src = nullptr;
+    if (int st = grow_xp(c, cols, batch)) return st;
+    auto s = scope(c, [&] { return std::string("p3_split ") + shape(batch, cols, 1); });
+    return launched(c, "p3_split", qr::p3_split(c->stream, c->xp, x, batch, cols));
 }
 // Whether a producer of `rows` rows of width `cols` should also write the
-// planes: enough rows for the hipBLASLt path and a prepared matrix of that width.
+// planes: enough rows for the planes path and a prepared matrix of that width.
 bool planes_wanted(Context* c, int cols, int rows) {
-    if (rows < kBlasMinBatch || !c->blas) return false;
+    if (rows < kPlanesMinBatch || !qr::p3_cols_ok(cols)) return false;
     for (auto& kv : c->prepared)
         if (kv.second.cols == cols && kv.second.rows > 16) return true;
     return false;
 }
-// Records that c->x6 now holds src's planes (for the next bridge call).
+// Records that c->xp now holds src's planes (for the next bridge call).
 void planes_made(Context* c, const float* src, int rows, int cols) {
-    c->x6_src = src;
-    c->x6_rows = rows;
-    c->x6_cols = cols;
-    c->x6_serial = c->serial;
+    c->xp_src = src;
+    c->xp_rows = rows;
+    c->xp_cols = cols;
+    c->xp_serial = c->serial;
 }
-int blas_project(Context* c, float* y, const Context::Prepared& p, int batch) {
-    auto s = scope(c, [&] { return std::string("gemm_f32_blas ") + shape(p.rows, p.cols, batch); });
-    return launched(c, "hipBLASLt GEMM", qr::blas_gemm6(c->blas, c->stream, y, p.w6, c->x6, p.rows, p.cols, batch));
+int p3_project(Context* c, float* y, const Context::Prepared& p, int batch) {
+    if (int st = ensure(c, &c->gemm_work, &c->gemm_work_len, qr::p3_gemm_scratch(batch, p.rows, p.cols),
+                        "hipMalloc GEMM split"))
+        return st;
+    auto s = scope(c, [&] { return std::string("gemm_f32_p3 ") + shape(p.rows, p.cols, batch); });
+    return launched(c, "gemm_p3", qr::p3_gemm(c->stream, y, c->xp, p.w3, batch, p.rows, p.cols, c->gemm_work,
+                                               c->gemm_work_len));
 }
 void drop_prepared(Context* c, std::map<const float*, Context::Prepared>::iterator it) {
     (void)hipStreamSynchronize(c->stream);  // queued GEMMs may still read the planes
     for (auto p = c->glu_pairs.begin(); p != c->glu_pairs.end();) {  // pairs holding a copy of them
         auto next = std::next(p);
         if (p->first.first == it->first || p->first.second == it->first) {
-            (void)hipFree(p->second.w6);
+            (void)hipFree(p->second.w3);
             c->glu_pairs.erase(p);
         }
         p = next;
     }
-    (void)hipFree(it->second.w6);
+    (void)hipFree(it->second.w3);
     c->prepared.erase(it);
 }
 // Drops the planes of every prepared matrix that [p, p + n) overlaps.
@@ -281,7 +288,7 @@ int project(Context* c, qr::WeightType t, float* y, const void* a, const float* 
     if (t == qr::WeightType::F32) {
         if (const Context::Prepared* p = prepared_for(c, a, rows, cols, batch)) {
             if (int st = split_input(c, x, cols, batch)) return st;
-            return blas_project(c, y, *p, batch);
+            return p3_project(c, y, *p, batch);
         }
     }
     if (!qr::gemm_preferred(t, rows, cols, batch)) {
@@ -309,7 +316,7 @@ int group(Context* c, qr::WeightType t, int n, const QrProjection* items, const 
                         if (int st = split_input(c, x, cols, batch)) return st;
                         split = true;
                     }
-                    if (int st = blas_project(c, items[i].y, *p, batch)) return st;
+                    if (int st = p3_project(c, items[i].y, *p, batch)) return st;
                     continue;
                 }
             }
@@ -354,50 +361,43 @@ int glu(Context* c, qr::WeightType t, float* product, float* gate_y, float* up_y
     if (t == qr::WeightType::F32) {
         const Context::Prepared* pg = prepared_for(c, gate, rows, cols, batch);
         const Context::Prepared* pu = prepared_for(c, up, rows, cols, batch);
-        if (pg && pu && rows % 8 == 0) {
-            // gate and up as ONE hipBLASLt GEMM over their planes side by side into glu_tmp
-            // (gate_y / up_y untouched, as the fused GLU), then silu(gate) * up from it
+        if (pg && pu && rows % 128 == 0) {
+            // gate, up and the silu product as ONE kernel over the combined planes (gate_y / up_y
+            // untouched, as the fused GLU), the product's planes for the next call (down)
             auto key = std::make_pair(gate, up);
             auto it = c->glu_pairs.find(key);
             if (it == c->glu_pairs.end()) {
-                const size_t half = size_t(rows) * 6 * size_t(cols);
                 Context::GluPair pair{rows, cols, nullptr};
-                auto st = hipMalloc(reinterpret_cast<void**>(&pair.w6), 2 * half * sizeof(__bf16));
+                auto st = hipMalloc(reinterpret_cast<void**>(&pair.w3), qr::p3_elements(2 * rows, cols) * sizeof(__bf16));
                 if (st != hipSuccess) return fail(c, "hipMalloc GLU planes", int(st));
-                st = hipMemcpyAsync(pair.w6, pg->w6, half * sizeof(__bf16), hipMemcpyDeviceToDevice, c->stream);
-                if (st == hipSuccess)
-                    st = hipMemcpyAsync(pair.w6 + half, pu->w6, half * sizeof(__bf16), hipMemcpyDeviceToDevice,
-                                        c->stream);
-                if (st != hipSuccess) {
+                if (int e = qr::p3_glu_interleave(c->stream, pair.w3, pg->w3, pu->w3, rows, cols)) {
                     (void)hipStreamSynchronize(c->stream);
-                    (void)hipFree(pair.w6);
-                    return fail(c, "GLU planes copy", int(st));
+                    (void)hipFree(pair.w3);
+                    return fail(c, "GLU planes", e);
                 }
                 it = c->glu_pairs.emplace(key, pair).first;
             }
             if (int st = split_input(c, x, cols, batch)) return st;
-            if (int st = ensure(c, &c->glu_tmp, &c->glu_tmp_len, size_t(batch) * 2 * size_t(rows), "hipMalloc GLU"))
+            if (int st = ensure(c, &c->gemm_work, &c->gemm_work_len, qr::p3_glu_scratch(batch, rows, cols),
+                                "hipMalloc GEMM split"))
                 return st;
-            {
-                auto s = scope(c, [&] { return std::string("gemm_f32_blas_glu 2x") + shape(rows, cols, batch); });
-                if (int st = launched(c, "hipBLASLt GEMM", qr::blas_gemm6(c->blas, c->stream, c->glu_tmp,
-                                                                            it->second.w6, c->x6, 2 * rows, cols,
-                                                                            batch)))
-                    return st;
-            }
-            const bool planes = planes_wanted(c, rows, batch);  // the product's planes for the next call (down)
+            const bool planes = planes_wanted(c, rows, batch);
             if (planes)
-                if (int st = grow_x6(c, rows, batch)) return st;
-            auto s = scope(c, [&] { return std::string("silu_split6 ") + shape(rows, batch, 1); });
-            const int st = qr::silu_split6(c->stream, product, c->glu_tmp, c->glu_tmp + rows, 2 * rows,
-                                           planes ? c->x6 : nullptr, batch, rows);
-            if (st == 0 && planes) planes_made(c, product, batch, rows);
-            return launched(c, "silu_split6", st);
+                if (int st = grow_planes(c, &c->xp_alt, &c->xp_alt_len, rows, batch)) return st;
+            auto s = scope(c, [&] { return std::string("gemm_f32_p3_glu 2x") + shape(rows, cols, batch); });
+            const int st = qr::p3_gemm_glu(c->stream, product, planes ? c->xp_alt : nullptr, c->xp, it->second.w3,
+                                           batch, rows, cols, c->gemm_work, c->gemm_work_len);
+            if (st == 0 && planes) {
+                std::swap(c->xp, c->xp_alt);
+                std::swap(c->xp_len, c->xp_alt_len);
+                planes_made(c, product, batch, rows);
+            }
+            return launched(c, "gemm_p3_glu", st);
         }
-        if (pg && pu) {  // gate and up on hipBLASLt into gate_y / up_y, then silu(gate_y) * up_y
+        if (pg && pu) {  // gate and up into gate_y / up_y, then silu(gate_y) * up_y
             if (int st = split_input(c, x, cols, batch)) return st;
-            if (int st = blas_project(c, gate_y, *pg, batch)) return st;
-            if (int st = blas_project(c, up_y, *pu, batch)) return st;
+            if (int st = p3_project(c, gate_y, *pg, batch)) return st;
+            if (int st = p3_project(c, up_y, *pu, batch)) return st;
             Params p{};
             p.p[0] = product;
             p.p[1] = gate_y;
@@ -577,11 +577,10 @@ void qr_destroy(Context* c) {
     if (c->attn_parts) (void)hipFree(c->attn_parts);
     if (c->rule_chunks) (void)hipFree(c->rule_chunks);
     if (c->gemm_work) (void)hipFree(c->gemm_work);
-    for (auto& kv : c->prepared) (void)hipFree(kv.second.w6);
-    for (auto& kv : c->glu_pairs) (void)hipFree(kv.second.w6);
-    if (c->glu_tmp) (void)hipFree(c->glu_tmp);
-    if (c->x6) (void)hipFree(c->x6);
-    qr::blas_destroy(c->blas);
+    for (auto& kv : c->prepared) (void)hipFree(kv.second.w3);
+    for (auto& kv : c->glu_pairs) (void)hipFree(kv.second.w3);
+    if (c->xp) (void)hipFree(c->xp);
+    if (c->xp_alt) (void)hipFree(c->xp_alt);
     (void)hipStreamDestroy(c->stream);
     delete c;
 }
@@ -655,8 +654,8 @@ int qr_run(Context* c, int op, int count, const Params* ap) {
             const long total = long(count) * a.n[0];
             if (width > 0 && total % width == 0 && planes_wanted(c, width, int(total / width))) {
                 const int rows = int(total / width);
-                if (int st = grow_x6(c, width, rows)) return st;
-                const int st = qr::run_rms_family_planes(s, op, count, a, c->x6, width);
+                if (int st = grow_xp(c, width, rows)) return st;
+                const int st = qr::run_rms_family_planes(s, op, count, a, c->xp, width);
                 if (st == 0) {
                     planes_made(c, op == QR_ADD_RMS_NORM ? a.p[3] : a.p[0], rows, width);
                     return launched(c, "rms_norm", 0);
@@ -745,23 +744,22 @@ int qr_gemm_f32_glu(Context* c, float* product, float* gate_y, float* up_y, cons
 }
 int qr_gemm_f32_prepare(Context* c, const float* a, int rows, int cols) {
     ++c->serial;
-    if (!a || rows < 1 || cols < 4 || cols % 4 != 0 || reinterpret_cast<uintptr_t>(a) % 16 != 0)
+    if (!a || rows < 1 || cols < 1 || reinterpret_cast<uintptr_t>(a) % 16 != 0)
         return fail(c, "GEMM prepare shape", -1);
+    if (!qr::p3_cols_ok(cols)) return 0;  // no planes: its projections keep the split-BF16 kernel
     auto it = c->prepared.find(a);
     if (it != c->prepared.end()) {
         if (it->second.rows == rows && it->second.cols == cols) return 0;
         drop_prepared(c, it);
     }
-    if (!c->blas)
-        if (int st = qr::blas_create(&c->blas)) return fail(c, "hipBLASLt context", st);
-    __bf16* w6 = nullptr;
-    auto st = hipMalloc(reinterpret_cast<void**>(&w6), size_t(rows) * 6 * size_t(cols) * sizeof(__bf16));
+    __bf16* w3 = nullptr;
+    auto st = hipMalloc(reinterpret_cast<void**>(&w3), qr::p3_elements(rows, cols) * sizeof(__bf16));
     if (st != hipSuccess) return fail(c, "hipMalloc GEMM planes", int(st));
-    if (int e = qr::split6(c->stream, w6, a, rows, cols, true)) {
-        (void)hipFree(w6);
-        return fail(c, "split6", e);
+    if (int e = qr::p3_split(c->stream, w3, a, rows, cols)) {
+        (void)hipFree(w3);
+        return fail(c, "p3_split", e);
     }
-    c->prepared[a] = Context::Prepared{rows, cols, w6};
+    c->prepared[a] = Context::Prepared{rows, cols, w3};
     return 0;
 }
 int qr_gemm_f32_release(Context* c, const float* a) {

@@ -84,23 +84,36 @@ int gemm(hipStream_t s, WeightType t, float* y, const void* a, const float* x, i
          float* work, size_t work_len);
 size_t gemm_scratch(WeightType t, int rows, int cols, int batch);
 bool gemm_preferred(WeightType t, int rows, int cols, int batch);
-// [rows, cols] fp32 -> [rows, 6 cols] BF16: the three-way split planes of
-// every row laid out for one BF16 GEMM with K' = 6 K (weight: the W order
-// [w0 w1 w2 w0 w1 w0], else the X order [x2 x1 x0 x1 x0 x0]); cols % 4 == 0.
-int split6(hipStream_t s, __bf16* out, const float* in, int rows, int cols, bool weight);
-// prod = silu(g) * u (rows x cols; g and u rows ld apart) and, when out is not
-// null, prod's split6 planes (activation order), in one pass;
-// hipErrorNotSupported (nothing launched) unless cols % 8 == 0, ld % 4 == 0
-// and every pointer is 16-byte aligned.
-int silu_split6(hipStream_t s, float* prod, const float* g, const float* u, int ld, __bf16* out, int rows, int cols);
-// Y[batch, rows] = X6 W6^T on hipBLASLt (BF16 inputs, fp32 accumulation and
-// output) for K'-concatenated planes of split6: the fp32 product X W^T to
-// fp32 accuracy. One Blas per bridge context; the algorithm of each shape is
-// chosen once per process by timing hipBLASLt's candidates.
-struct Blas;
-int blas_create(Blas** out);
-void blas_destroy(Blas* b);
-int blas_gemm6(Blas* b, hipStream_t s, float* y, const __bf16* w6, const __bf16* x6, int rows, int cols, int batch);
+// gemm_p3.hip -----------------------------------------------------------------
+// P3 planes: the three BF16 split planes (x = x0 + x1 + x2) of a [rows, cols]
+// fp32 matrix in MFMA fragment order, rows padded to a multiple of 256 (pad
+// rows zero): the 32 x 16 fragment (rows 32 rt.., k 16 kt..) of plane p is
+// 512 contiguous BF16 at ((rt cols/16 + kt) 3 + p) 512, element (row, k) at
+// lane (row % 32) + 32 ((k / 8) % 2), position k % 8.
+__host__ __device__ inline int p3_rows(int rows) { return (rows + 255) / 256 * 256; }
+__host__ __device__ inline bool p3_cols_ok(int cols) { return cols >= 32 && cols % 32 == 0; }
+__host__ __device__ inline size_t p3_index(int row, int k, int plane, int kt) {
+    return ((size_t(row >> 5) * size_t(kt) + size_t(k >> 4)) * 3 + size_t(plane)) * 512 +
+           size_t((row & 31) + 32 * ((k >> 3) & 1)) * 8 + size_t(k & 7);
+}
+size_t p3_elements(int rows, int cols);
+// fp32 [rows, cols] -> P3 planes (cols % 32 == 0, 16-byte aligned pointers).
+int p3_split(hipStream_t s, __bf16* out, const float* in, int rows, int cols);
+// Y[M, N] = X W^T from the P3 planes of X (M rows) and W (N rows), K % 32 ==
+// 0; `work` holds at least p3_gemm_scratch(M, N, K) floats (K-chunk partials).
+int p3_gemm(hipStream_t s, float* y, const __bf16* xp, const __bf16* wp, int M, int N, int K, float* work,
+            size_t work_len);
+size_t p3_gemm_scratch(int M, int N, int K);
+// The combined planes of a GLU (2 rows x cols; rows % 128 == 0) from the P3
+// planes of gate and up: 64 gate rows, then the same 64 up rows, and so on.
+int p3_glu_interleave(hipStream_t s, __bf16* out, const __bf16* gate, const __bf16* up, int rows, int cols);
+// product[M, rows] = silu(X G^T) * (X U^T) from X's P3 planes and the combined
+// planes; when `planes` is set, the product's P3 planes too (rows / 16 k
+// tiles). `work`: at least p3_glu_scratch(M, rows, K) floats.
+int p3_gemm_glu(hipStream_t s, float* product, __bf16* planes, const __bf16* xp, const __bf16* wglu, int M, int rows,
+                int K, float* work, size_t work_len);
+size_t p3_glu_scratch(int M, int rows, int K);
+
 // Y1 = X A1^T and (rows2 > 0) Y2 = X A2^T in one launch for fp32 matrices of
 // at most 16 rows and 1024 columns (the DeltaNet a / b projections of
 // prefill), when gemm_ab_ok holds for each.
@@ -115,11 +128,10 @@ int gemm_glu(hipStream_t s, WeightType t, float* product, const void* gate, cons
 // ops.hip --------------------------------------------------------------------
 int run_elementwise(hipStream_t s, int op, int count, const Params& a);
 int run_rms_family(hipStream_t s, int op, int groups, const Params& a);
-// RmsNorm / AddRmsNorm / RmsNormGate whose output is also written as split6
-// planes (activation order) of rows of `width` values (a multiple of the
-// group size that divides the output: groups * d / width rows of 6 width
-// BF16); hipErrorNotSupported (nothing launched) when the op, width or
-// alignment has no such form.
+// RmsNorm / AddRmsNorm / RmsNormGate whose output is also written as the P3
+// planes of rows of `width` values (a multiple of the group size and of 32
+// that divides the output: groups * d / width rows); hipErrorNotSupported
+// (nothing launched) when the op, width or alignment has no such form.
 int run_rms_family_planes(hipStream_t s, int op, int groups, const Params& a, __bf16* planes, int width);
 int run_conv_silu(hipStream_t s, int count, const Params& a);
 int run_delta_qk(hipStream_t s, int count, const Params& a);

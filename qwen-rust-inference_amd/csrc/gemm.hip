@@ -423,38 +423,6 @@ __global__ __launch_bounds__(512) void gemm_ab_kernel(AbMats m, const float* x, 
 }
 
 
-// The K'-concatenated BF16 planes of an fp32 matrix for one BF16 GEMM with
-// K' = 6 K whose products are the six part products of the three-way split:
-// row r of a matrix becomes [x2 | x1 | x0 | x1 | x0 | x0] (the activations X)
-// or [w0 | w1 | w2 | w0 | w1 | w0] (the weights W), so block b of K' pairs
-// x_{P[b]} with w_{Q[b]} for (P, Q) = (2,0) (1,1) (0,2) (1,0) (0,1) (0,0);
-// every BF16 x BF16 product is exact in fp32. When cols % 8 == 0 (every
-// plane then starts 16-byte aligned) one thread splits 8 consecutive values
-// of a row with a 16-byte store per plane, the grid over all rows
-// (split6_flat_kernel); else one block per row, 4 values per thread step with
-// 8-byte stores (cols % 4 == 0); each plane's stores coalesced.
-__device__ __forceinline__ void split3_4(f4v v, bf16x4 (&h)[3]) {
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        h[0][e] = __bf16(v[e]);
-        const float r1 = v[e] - float(h[0][e]);
-        h[1][e] = __bf16(r1);
-        h[2][e] = __bf16(r1 - float(h[1][e]));
-    }
-}
-constexpr int SPLIT6_THREADS = 128;
-__global__ __launch_bounds__(SPLIT6_THREADS) void split6_kernel(__bf16* out, const float* in, int cols, int weight) {
-    constexpr int XP[6] = {2, 1, 0, 1, 0, 0}, WQ[6] = {0, 1, 2, 0, 1, 0};
-    const float* src = in + size_t(blockIdx.x) * cols;
-    __bf16* row = out + size_t(blockIdx.x) * 6 * cols;
-    for (int k = 4 * int(threadIdx.x); k < cols; k += 4 * SPLIT6_THREADS) {
-        bf16x4 h[3];
-        split3_4(*reinterpret_cast<const f4v*>(src + k), h);
-#pragma unroll
-        for (int b = 0; b < 6; ++b) *reinterpret_cast<bf16x4*>(row + size_t(b) * cols + k) = h[weight ? WQ[b] : XP[b]];
-    }
-}
-
 }  // namespace
 
 bool gemm_preferred(WeightType, int, int, int batch) { return batch > 4; }
@@ -471,84 +439,6 @@ size_t gemm_scratch(WeightType t, int rows, int cols, int batch) {
     int kchunk;
     const int splits = mfma_splits(rows, cols, batch, kchunk);
     return splits > 1 ? size_t(splits) * size_t(rows) * size_t(batch) : 0;
-}
-
-// SiluProduct (reference.h SILU_PRODUCT) of a prefill GLU from the rows of the
-// gate and up outputs (row stride ld), one thread per 8 consecutive elements
-// of a row (cols % 8 == 0), the grid over all rows; when `out` is set, the
-// product's split6 planes (activation order) too, for the projection after.
-__global__ __launch_bounds__(256) void silu_split6_kernel(float* prod, const float* g, const float* u, int ld,
-                                                          __bf16* out, int cols, long chunks) {
-    constexpr int XP[6] = {2, 1, 0, 1, 0, 0};
-    const int per_row = cols / 8;
-    for (long c = blockIdx.x * long(blockDim.x) + threadIdx.x; c < chunks; c += long(gridDim.x) * blockDim.x) {
-        const size_t r = size_t(c / per_row), k = size_t(c % per_row) * 8, e0 = r * cols + k, i0 = r * ld + k;
-        f4v v[2];
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            const f4v gv = *reinterpret_cast<const f4v*>(g + i0 + 4 * h);
-            const f4v uv = *reinterpret_cast<const f4v*>(u + i0 + 4 * h);
-#pragma unroll
-            for (int e = 0; e < 4; ++e) v[h][e] = siluf_(gv[e]) * uv[e];
-            *reinterpret_cast<f4v*>(prod + e0 + 4 * h) = v[h];
-        }
-        if (!out) continue;
-        bf16x4 lo[3], hi[3];
-        split3_4(v[0], lo);
-        split3_4(v[1], hi);
-        __bf16* row = out + r * 6 * cols + k;
-#pragma unroll
-        for (int b = 0; b < 6; ++b)
-            *reinterpret_cast<bf16x8*>(row + size_t(b) * cols) =
-                __builtin_shufflevector(lo[XP[b]], hi[XP[b]], 0, 1, 2, 3, 4, 5, 6, 7);
-    }
-}
-
-int silu_split6(hipStream_t s, float* prod, const float* g, const float* u, int ld, __bf16* out, int rows, int cols) {
-    if (rows < 1 || cols < 8 || cols % 8 != 0 || ld % 4 != 0 || ld < cols ||
-        (reinterpret_cast<uintptr_t>(prod) | reinterpret_cast<uintptr_t>(g) | reinterpret_cast<uintptr_t>(u) |
-         reinterpret_cast<uintptr_t>(out)) % 16 != 0)
-        return int(hipErrorNotSupported);
-    const long chunks = long(rows) * (cols / 8);
-    const long blocks = (chunks + 255) / 256;
-    hipLaunchKernelGGL(silu_split6_kernel, dim3(unsigned(blocks < 65536 ? blocks : 65536)), dim3(256), 0, s, prod, g,
-                       u, ld, out, cols, chunks);
-    return int(hipGetLastError());
-}
-
-// split6 for cols % 8 == 0: one thread per 8 consecutive elements of a row,
-// the grid over all rows.
-__global__ __launch_bounds__(256) void split6_flat_kernel(__bf16* out, const float* in, int cols, long chunks,
-                                                          int weight) {
-    constexpr int XP[6] = {2, 1, 0, 1, 0, 0}, WQ[6] = {0, 1, 2, 0, 1, 0};
-    const int per_row = cols / 8;
-    for (long c = blockIdx.x * long(blockDim.x) + threadIdx.x; c < chunks; c += long(gridDim.x) * blockDim.x) {
-        const size_t r = size_t(c / per_row), k = size_t(c % per_row) * 8;
-        bf16x4 lo[3], hi[3];
-        split3_4(*reinterpret_cast<const f4v*>(in + r * cols + k), lo);
-        split3_4(*reinterpret_cast<const f4v*>(in + r * cols + k + 4), hi);
-        __bf16* row = out + r * 6 * cols + k;
-#pragma unroll
-        for (int b = 0; b < 6; ++b) {
-            const int p = weight ? WQ[b] : XP[b];
-            *reinterpret_cast<bf16x8*>(row + size_t(b) * cols) = __builtin_shufflevector(lo[p], hi[p], 0, 1, 2, 3, 4, 5, 6, 7);
-        }
-    }
-}
-
-int split6(hipStream_t s, __bf16* out, const float* in, int rows, int cols, bool weight) {
-    if (rows < 1 || cols < 4 || cols % 4 != 0 || reinterpret_cast<uintptr_t>(in) % 16 != 0 ||
-        reinterpret_cast<uintptr_t>(out) % 16 != 0)
-        return int(hipErrorInvalidValue);
-    if (cols % 8 == 0) {
-        const long chunks = long(rows) * (cols / 8), blocks = (chunks + 255) / 256;
-        hipLaunchKernelGGL(split6_flat_kernel, dim3(unsigned(blocks < 65536 ? blocks : 65536)), dim3(256), 0, s, out, in,
-                           cols, chunks, weight ? 1 : 0);
-    } else {
-        hipLaunchKernelGGL(split6_kernel, dim3(unsigned(rows)), dim3(SPLIT6_THREADS), 0, s, out, in, cols,
-                           weight ? 1 : 0);
-    }
-    return int(hipGetLastError());
 }
 
 bool gemm_ab_ok(WeightType t, const void* a, const float* x, int rows, int cols, int batch) {

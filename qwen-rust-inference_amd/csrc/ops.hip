@@ -103,11 +103,10 @@ __global__ __launch_bounds__(256) void rms_family_kernel(int op, int groups, Par
 // j < PER / V), so every load and store of a wave is one contiguous run and
 // each input is read once (the block form above reads a group twice and
 // waits on two block barriers).
-// planes (may be null): the output also as the K'-concatenated BF16 planes a
-// prepared projection takes, the output read as rows of `width` values (a
-// multiple of d: consecutive groups form a row): row r holds 6 segments of
-// width, segment b the split part {2, 1, 0, 1, 0, 0}[b] of x = x0 + x1 + x2
-// (as split6 of gemm.hip).
+// planes (may be null): the output also as the P3 planes a prepared
+// projection takes (common.h), the output read as rows of `width` values (a
+// multiple of d and of 32: consecutive groups form a row); the V consecutive
+// values of a lane are V consecutive BF16 of each plane.
 template <int PER>
 __global__ __launch_bounds__(256) void rms_rows_kernel(int op, int groups, Params a, __bf16* planes, int width) {
     constexpr int V = PER >= 4 ? 4 : PER, NV = PER / V;
@@ -157,11 +156,10 @@ __global__ __launch_bounds__(256) void rms_rows_kernel(int op, int groups, Param
                 h[1][e] = __bf16(r1);
                 h[2][e] = __bf16(r1 - float(h[1][e]));
             }
-            constexpr int XP[6] = {2, 1, 0, 1, 0, 0};
             const unsigned pe = unsigned(off) + unsigned(c), pr = pe / unsigned(width);  // element, plane row
-            __bf16* row = planes + size_t(pr) * 6 * width + (pe - pr * unsigned(width));
+            const int k = int(pe - pr * unsigned(width));
 #pragma unroll
-            for (int b = 0; b < 6; ++b) *reinterpret_cast<hv*>(row + size_t(b) * width) = h[XP[b]];
+            for (int q = 0; q < 3; ++q) *reinterpret_cast<hv*>(planes + p3_index(int(pr), k, q, width / 16)) = h[q];
         }
     }
 }
@@ -596,7 +594,8 @@ bool launch_rms_rows_any(hipStream_t s, int op, int groups, const Params& a, __b
 
 int run_rms_family_planes(hipStream_t s, int op, int groups, const Params& a, __bf16* planes, int width) {
     if (op != QR_RMS_NORM && op != QR_ADD_RMS_NORM && op != QR_RMS_NORM_GATE) return int(hipErrorNotSupported);
-    if (a.n[0] < 1 || width < a.n[0] || width % a.n[0] != 0 || (long(groups) * a.n[0]) % width != 0)
+    if (a.n[0] < 1 || width < a.n[0] || width % a.n[0] != 0 || !p3_cols_ok(width) ||
+        (long(groups) * a.n[0]) % width != 0)
         return int(hipErrorNotSupported);
     if (!launch_rms_rows_any(s, op, groups, a, planes, width)) return int(hipErrorNotSupported);
     return int(hipGetLastError());

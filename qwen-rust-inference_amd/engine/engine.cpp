@@ -179,7 +179,7 @@ struct Api {
             if (!decode_plan || !decode_step || !decode_free) decode_plan = nullptr;
         }
         if (!(disable & QE_NO_EMBED_ROWS)) embed_rows = symbol<decltype(embed_rows)>("qr_embed_rows", false);
-        if (!(disable & QE_NO_BLAS_GEMM))
+        if (!(disable & QE_NO_PREPARED_GEMM))
             gemm_f32_prepare = symbol<decltype(gemm_f32_prepare)>("qr_gemm_f32_prepare", false);
         profile = symbol<decltype(profile)>("qr_profile", false);
         profile_read = symbol<decltype(profile_read)>("qr_profile_read", false);

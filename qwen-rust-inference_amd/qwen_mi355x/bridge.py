@@ -157,7 +157,7 @@ class Bridge:
                        batch))
 
     def prepare(self, a: Buffer, rows: int, cols: int):
-        """qr_gemm_f32_prepare: keep a's split planes for the hipBLASLt prefill path."""
+        """qr_gemm_f32_prepare: keep a's split planes for the prefill projections."""
         self._check(self.L.qr_gemm_f32_prepare(self.ctx, ctypes.c_void_p(a.ptr), rows, cols))
 
     def release(self, a: Buffer):

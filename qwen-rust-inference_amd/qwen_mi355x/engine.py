@@ -28,7 +28,7 @@ F32, BF16_EXACT, INT8 = 0, 1, 2
 NO_F32_FUSIONS, NO_FUSIONS, NO_DELTA_MIXER, NO_FUSED_OPS, NO_ARGMAX, NO_SNAPSHOTS = 1, 2, 4, 8, 16, 32
 NO_DECODE_STEP = 64
 NO_EMBED_ROWS = 128
-NO_BLAS_GEMM = 256
+NO_PREPARED_GEMM = 256
 NO_PLAIN_DECODE_LAUNCH = 512  # one-launch decode steps launched cooperatively
 
 # Every entry point of include/qwen_bridge.h.

@@ -23,6 +23,11 @@ the tests draw the same ones (`sample`). Workloads:
   c5  int8 per-row weights: the oracle on the dequantised weights, 454-token
       prompt (ids seed 4), then the 4 draft tokens (seed 6) as sequential steps
       (what each verify row must equal) and 16 greedy tokens
+  c2l the c2 prompt and greedy tokens with every layer's output (the hidden
+      state after each block, the reference's per-layer `validate_device`
+      record, src/device/cli.rs:229-366) sampled at every checkpoint and at
+      greedy steps 1, 2, 4, ..., 64, 127
+  c3l 10,240-token prompt (ids seed 2), checkpoints and layer outputs
 
 Weights: `synthetic_weights(config_qwen08b(), seed=0)` (the engine library's
 counter-based normal generator, thread-count independent).
@@ -48,12 +53,17 @@ WORKLOADS = {
     "c3": dict(prompt=2644, seed=2, greedy=0, int8=False),
     "c4": dict(prompt=8192, seed=5, greedy=64, int8=False),
     "c5": dict(prompt=454, seed=4, greedy=16, int8=True, draft_seed=6, draft=4),
+    "c2l": dict(prompt=454, seed=4, greedy=128, int8=False, layers=True),
+    "c3l": dict(prompt=10240, seed=2, greedy=0, int8=False, layers=True),
 }
 LOGIT_SAMPLES = 1024
 TOP = 16
 STATE_SAMPLES = 64
 FINAL_STATE_SAMPLES = 1024
-WORKLOAD_ID = {"c2": 2, "c3": 3, "c4": 4, "c5": 5}
+LAYER_SAMPLES = 256
+LAYER_PART = 7  # sample key of a layer output, beside the state parts 0-3
+GREEDY_LAYER_STEPS = (1, 2, 4, 8, 16, 32, 64, 127)
+WORKLOAD_ID = {"c2": 2, "c3": 3, "c4": 4, "c5": 5, "c2l": 2, "c3l": 3}
 
 
 def prompt_ids(name: str) -> list[int]:
@@ -107,6 +117,18 @@ def state_summary(name: str, point: int, read, num_layers: int, k: int) -> np.nd
     return np.concatenate(out).astype(np.float32)
 
 
+def layer_summary(name: str, point: int, records, hidden: int) -> np.ndarray:
+    """[layers, LAYER_SAMPLES]: each layer's output ("layer" in the oracle's
+    trace, "output" in the engine's capture) at the sampled indices."""
+    out = [v[sample(name, (point, layer, LAYER_PART, LAYER_SAMPLES), hidden, LAYER_SAMPLES)]
+           for layer, v in records]
+    return np.stack(out).astype(np.float32)
+
+
+def oracle_layers(records) -> list:
+    return [(layer, v) for layer, nm, v in records if nm == "layer"]
+
+
 def load(name: str) -> dict:
     with np.load(HERE / f"qwen08b_{name}.npz", allow_pickle=False) as z:
         return {k: z[k] for k in z.files}
@@ -137,8 +159,13 @@ def make(name: str, threads: int = 8) -> Path:
     rec = {"points": np.array(points, np.int32), "prompt": np.array(ids, np.int32)}
     t0 = time.time()
     logits = None
+    layers = spec.get("layers", False)
     for p, tok in enumerate(ids, start=1):
-        logits = s.step(tok, O.VECTOR)
+        if layers and p in points:
+            logits, records = s.step(tok, O.VECTOR, trace=True)
+            rec[f"p{p}_layers"] = layer_summary(name, p, oracle_layers(records), c.hidden_size)
+        else:
+            logits = s.step(tok, O.VECTOR)
         if p in points:
             summ = logits_summary(name, (p,), logits)
             for k, v in summ.items():
@@ -160,7 +187,10 @@ def make(name: str, threads: int = 8) -> Path:
         rec["draft_picks"] = np.array(rows, np.int32)
     greedy = []
     for i in range(spec["greedy"]):
-        if i:
+        if i and layers and i in GREEDY_LAYER_STEPS:
+            logits, records = s.step(greedy[-1], O.VECTOR, trace=True)
+            rec[f"g{i}_layers"] = layer_summary(name, 2_000_000 + i, oracle_layers(records), c.hidden_size)
+        elif i:
             logits = s.step(greedy[-1], O.VECTOR)
         summ = logits_summary(name, (2_000_000 + i,), logits)
         for k, v in summ.items():

@@ -163,13 +163,17 @@ def test_group_glu_equal_separate_calls(gpu, kind, batch):
 
 
 @pytest.mark.parametrize("rows,cols,batch", [(6144, 1024, 2644), (1024, 2048, 130), (1024, 3584, 64), (512, 1024, 454),
-                                            (4096, 1024, 10240), (40, 12, 65), (2048, 1024, 63)])
+                                            (4096, 1024, 10240), (40, 12, 65), (2048, 1024, 63),
+                                            (4096, 1024, 2644), (1024, 3584, 2644), (3584, 1024, 2644),
+                                            (1024, 2048, 10240), (256, 64, 300), (48, 1024, 200)])
 def test_gemm_f32_prepared(gpu, rows, cols, batch):
-    """qr_gemm_f32_prepare: the projection of a prepared matrix (one BF16 GEMM
-    with K' = 6 cols on hipBLASLt from 64 tokens, the split-BF16 kernel below)
-    against fp64 with the fp32 dot-product bound on sampled rows, twice
-    bitwise-equal (the algorithm of a shape is fixed), and within the bound of
-    the unprepared kernel's result."""
+    """qr_gemm_f32_prepare: the projection of a prepared matrix (the P3 GEMM of
+    gemm_p3.hip from 64 tokens: whole tiles, and the tiles past the last whole
+    round of 256 blocks split along K and summed in chunk order; the
+    split-BF16 kernel below 64 tokens or for cols % 32 != 0) against fp64 with
+    the fp32 dot-product bound on sampled rows (the last row always among
+    them), twice bitwise-equal, and within the bound of the unprepared
+    kernel's result."""
     print(f"gemm f32 prepared {rows}x{cols} batch {batch}", flush=True)
     rng = np.random.default_rng(rows + 3 * cols + batch)
     w = (rng.standard_normal(rows * cols) * 0.02).astype(np.float32)
@@ -182,7 +186,7 @@ def test_gemm_f32_prepared(gpu, rows, cols, batch):
     gpu.gemm(y2, a, xb, rows, cols, batch)
     got = y1.read().reshape(batch, rows)
     assert np.array_equal(got, y2.read().reshape(batch, rows))
-    idx = np.unique(np.random.default_rng(0).integers(0, batch, 64))
+    idx = np.unique(np.append(np.random.default_rng(0).integers(0, batch, 64), batch - 1))
     X, W = x.reshape(batch, cols)[idx].astype(np.float64), w.reshape(rows, cols).astype(np.float64)
     want = X @ W.T
     bound = np.abs(X) @ np.abs(W.T) * 2e-5 + 1e-30
@@ -245,6 +249,35 @@ def test_prepared_group_glu_and_invalidation(gpu):
     assert np.all(np.abs(y.read().reshape(batch, shapes[0])[:16] - X @ W.T) <= bound)
     gpu.release(mats[1])
     gpu.release(mats[1])  # releasing twice (or an unprepared matrix) is accepted
+
+
+@pytest.mark.parametrize("rows,batch", [(3584, 2644), (3584, 64), (256, 300), (384, 130), (320, 130)])
+def test_prepared_glu_shapes(gpu, rows, batch):
+    """A GLU of two prepared matrices (rows % 128 == 0: gate, up and the silu
+    product in one P3 kernel, whole tiles and K-split tiles; else two prepared
+    projections and the silu product) against the silu product of the
+    prepared projections in float64, gate_y / up_y untouched by the fused
+    form, twice bitwise-equal."""
+    print(f"prepared glu {rows} rows batch {batch}", flush=True)
+    rng = np.random.default_rng(rows + batch)
+    cols = 1024
+    g = gpu.upload((rng.standard_normal(rows * cols) * 0.02).astype(np.float32))
+    u = gpu.upload((rng.standard_normal(rows * cols) * 0.02).astype(np.float32))
+    x = gpu.upload(rng.standard_normal(batch * cols).astype(np.float32))
+    gpu.prepare(g, rows, cols)
+    gpu.prepare(u, rows, cols)
+    prod, gy, uy = gpu.alloc(batch * rows), gpu.alloc(batch * rows), gpu.alloc(batch * rows)
+    gpu.glu(prod, gy, uy, g, u, x, rows, cols, batch)
+    first = prod.read()
+    gpu.glu(prod, gy, uy, g, u, x, rows, cols, batch)
+    assert np.array_equal(first, prod.read())
+    if rows % 128 == 0:
+        assert not gy.read().any() and not uy.read().any()
+    g1, u1 = gpu.alloc(batch * rows), gpu.alloc(batch * rows)
+    gpu.gemm(g1, g, x, rows, cols, batch)
+    gpu.gemm(u1, u, x, rows, cols, batch)
+    gv, uv = g1.read().astype(np.float64), u1.read().astype(np.float64)
+    parity(first, gv / (1 + np.exp(-gv)) * uv, where=f"prepared glu {rows}x{batch}")
 
 
 def test_planes_from_producers(gpu):
