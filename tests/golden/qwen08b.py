@@ -26,7 +26,7 @@ the tests draw the same ones (`sample`). Workloads:
   c2l the c2 prompt and greedy tokens with every layer's output (the hidden
       state after each block, the reference's per-layer `validate_device`
       record, src/device/cli.rs:229-366) sampled at every checkpoint and at
-      greedy steps 1, 2, 4, ..., 64, 127
+      greedy steps 1, 2, 4, ..., 64, 127 (only those: the rest is c2's)
   c3l 10,240-token prompt (ids seed 2), checkpoints and layer outputs
 
 Weights: `synthetic_weights(config_qwen08b(), seed=0)` (the engine library's
@@ -53,7 +53,7 @@ WORKLOADS = {
     "c3": dict(prompt=2644, seed=2, greedy=0, int8=False),
     "c4": dict(prompt=8192, seed=5, greedy=64, int8=False),
     "c5": dict(prompt=454, seed=4, greedy=16, int8=True, draft_seed=6, draft=4),
-    "c2l": dict(prompt=454, seed=4, greedy=128, int8=False, layers=True),
+    "c2l": dict(prompt=454, seed=4, greedy=128, int8=False, layers=True, layers_only=True),
     "c3l": dict(prompt=10240, seed=2, greedy=0, int8=False, layers=True),
 }
 LOGIT_SAMPLES = 1024
@@ -200,6 +200,9 @@ def make(name: str, threads: int = 8) -> Path:
         rec["greedy"] = np.array(greedy, np.int32)
         rec["greedy_state"] = state_summary(name, 3_000_000, s.part, c.num_layers, FINAL_STATE_SAMPLES)
         print(f"{name}: {len(greedy)} greedy tokens ({time.time() - t0:.0f} s)", flush=True)
+    if spec.get("layers_only"):  # the rest is c2's fixture
+        keep = ("points", "prompt", "greedy")
+        rec = {k: v for k, v in rec.items() if k in keep or k.endswith("_layers")}
     out = HERE / f"qwen08b_{name}.npz"
     np.savez_compressed(out, **rec)
     return out

@@ -12,7 +12,10 @@ unless the oracle's top-2 margin is inside the bound. Greedy decode after the
 prompt must pick the oracle's tokens (same near-tie rule, which ends the id
 comparison); the logits of every decode step are compared teacher-forced.
 
-  C2  454-token prompt + 128 greedy tokens (the bench workload)
+  C2  454-token prompt + 128 greedy tokens (the bench workload); every
+      layer's output (the hidden state after each block) at every checkpoint
+      and at greedy steps 1, 2, 4, ..., 64, 127 (the reference's per-layer
+      validate_device, src/device/cli.rs:229-366)
   C3  2644-token prefill: one chunk, the checkpoint walk, 128-token chunks
       (the reference's PREFILL_CHUNK); 10,240 tokens in one chunk against
       the same prompt in 128-token chunks
@@ -157,6 +160,48 @@ def test_c2_prompt_checkpoints_and_greedy(weights, fast):
     walk_checkpoints("c2", run, c, rec)
     greedy_against_fixture("c2", run, rec)
     check_state("c2", 3_000_000, run, c, rec, "greedy_state", FP32_RTOL, "c2 after greedy")
+
+
+def check_layers(name, key, records, want, c, rtol, where):
+    """The captured "output" record of every layer (the engine's capture of
+    forward_body) against the fixture's samples of the oracle's "layer"."""
+    outs = {layer: v for layer, nm, v in records if nm == "output"}
+    assert sorted(outs) == list(range(c.num_layers)), sorted(outs)
+    for layer in range(c.num_layers):
+        idx = G.sample(name, (key, layer, G.LAYER_PART, G.LAYER_SAMPLES), c.hidden_size, G.LAYER_SAMPLES)
+        parity(outs[layer][idx], want[layer], rtol=rtol, where=f"{where} layer {layer} output")
+
+
+def test_c2_layer_outputs(weights, fast):
+    """Config 2's prompt: at every checkpoint p the tokens before p in one
+    prefill chunk and token p as a captured step (the engine's op path records
+    every layer's output), each layer's hidden state and the logits against
+    the oracle; then the greedy tokens, with steps 1, 2, 4, ..., 64 and 127
+    captured, the others on the one-launch decode."""
+    c, _ = weights
+    rec, full = G.load("c2l"), G.load("c2")
+    ids = [int(v) for v in rec["prompt"]]
+    run = fast.new_run(454 + 136, chunk=454)
+    assert run.decode_plan
+    done = 0
+    for p in [int(v) for v in rec["points"]]:
+        if p - 1 > done:
+            run.prefill(ids[done:p - 1])
+        logits, records = run.step(ids[p - 1], capture=True)
+        done = p
+        check_layers("c2", p, records, rec[f"p{p}_layers"], c, FP32_RTOL, f"c2 checkpoint {p}")
+        check_logits("c2", (p,), logits, full, f"p{p}_", FP32_RTOL, f"c2 checkpoint {p} (captured)")
+        print(f"c2: checkpoint {p}: {c.num_layers} layer outputs ok", flush=True)
+    greedy = [int(v) for v in rec["greedy"]]
+    for i in range(1, len(greedy)):
+        if i in G.GREEDY_LAYER_STEPS:
+            logits, records = run.step(greedy[i - 1], capture=True)
+            check_layers("c2", 2_000_000 + i, records, rec[f"g{i}_layers"], c, FP32_RTOL, f"c2 greedy step {i}")
+        else:
+            logits = run.step(greedy[i - 1])
+        check_logits("c2", (2_000_000 + i,), logits, full, f"g{i}_", FP32_RTOL, f"c2 greedy step {i}")
+    print(f"c2: layer outputs at {len(rec['points'])} checkpoints and {len(G.GREEDY_LAYER_STEPS)} greedy steps ok",
+          flush=True)
 
 
 def test_c3_prefill_2644_one_chunk(weights, fast):
