@@ -229,6 +229,19 @@ int qr_decode_steps(Context* c, QrDecodePlan* p, int first_token, int position, 
  * verify rows, native/rocm/bridge.cpp:197-215, src/device.rs:1514-1531). No
  * counterpart in the reference's ABI. */
 int qr_decode_step_row(Context* c, QrDecodePlan* p, int token, int position, int row, int snap);
+/* Part of a verify pass, n = 1..4 consecutive tokens in ONE launch, the
+ * weights read once for all rows: row r is tokens[r] at position + r (logits
+ * row first + r, [argmax, non-finite count] in picks row first + r), and when
+ * first + r < snaps its DeltaNet states also go to snapshot copy first + r + 1.
+ * Every row is computed with the per-lane arithmetic of qr_decode_step at its
+ * position (the delta rule walks the rows in order, row r's attention is split
+ * as a one-row step at position + r would be and sees the new keys / values
+ * of rows <= r), so a row is bit for bit the decode step of its position, as
+ * the reference's fixed-count verify GEMV keeps each row's order
+ * (native/rocm/kernels.h:124-170, native/rocm/bridge.cpp:197-215).
+ * first + n <= the plan's rows, snaps <= its snapshots. No counterpart in the
+ * reference's ABI. */
+int qr_decode_rows(Context* c, QrDecodePlan* p, const int32_t* tokens, int n, int position, int first, int snaps);
 void qr_decode_plan_free(Context* c, QrDecodePlan* p);
 
 /* Op 16 (Argmax) without any allocation: the same slot meanings and result

@@ -40,8 +40,9 @@ enum QeDisable {
     QE_NO_DECODE_STEP = 64,  /* qr_decode_plan / qr_decode_step */
     QE_NO_EMBED_ROWS = 128,  /* qr_embed_rows */
     QE_NO_PREPARED_GEMM = 256, /* qr_gemm_f32_prepare (prefill projections over split planes) */
-    QE_NO_PLAIN_DECODE_LAUNCH = 512 /* one-launch decode steps launched cooperatively
+    QE_NO_PLAIN_DECODE_LAUNCH = 512, /* one-launch decode steps launched cooperatively
                                         (qr_set_option "decode_cooperative"; without it: no plan) */
+    QE_NO_DECODE_ROWS = 1024 /* qr_decode_rows (verify rows: one launch per row instead) */
 };
 
 /* Record callback of a captured step: (layer, name, values, n). Names follow

@@ -883,6 +883,14 @@ int qr_decode_step(Context* c, QrDecodePlan* p, int token, int position) {
     if (token < 0) return fail(c, "decode step token", -1);
     return launched(c, "decode step", qr::decode_step(p, token, position, -1, c->stream));
 }
+int qr_decode_rows(Context* c, QrDecodePlan* p, const int32_t* tokens, int n, int position, int first, int snaps) {
+    ++c->serial;
+    if (!p || !tokens) return fail(c, "decode rows without a plan", -1);
+    auto sc = scope(c, [&] { return std::string("decode_rows ") + std::to_string(n); });
+    const int st = qr::decode_rows(p, tokens, n, position, first, snaps, c->stream);
+    if (st == int(hipErrorNotSupported)) return fail(c, "decode rows: the multi-row kernel does not fit this device", st);
+    return launched(c, "decode rows", st);
+}
 int qr_decode_step_row(Context* c, QrDecodePlan* p, int token, int position, int row, int snap) {
     ++c->serial;
     if (!p) return fail(c, "decode step without a plan", -1);

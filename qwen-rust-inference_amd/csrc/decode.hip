@@ -76,6 +76,9 @@ constexpr int KVE = 2 * SPAN;       // 16-byte entries per lane of one K/V chunk
 constexpr int SMAX = 256;           // attention splits per KV head
 constexpr int QPG = NH / NKV;       // query heads per KV head: the waves of one attention slot
 constexpr int MAXPH = 6 * 64 + 2;
+// Rows of a multi-row step (decode_rows_kernel: a verify pass of up to NRMAX
+// consecutive tokens with the weights read once).
+constexpr int NRMAX = 4;
 constexpr int DIN_RPW = 4, GLU_RPW = 2, AQKV_RPW = 3, Z_RPW = 2;
 // DeltaNet layers: units >= early_u (fp32: waves 6 and 7 of every block,
 // int8: waves 4-7) have no DOUT row; they take GLU rows 0 .. (NW - early_u)
@@ -101,18 +104,21 @@ enum : uint8_t { T_DIN, T_MIX, T_DOUT, T_GLU, T_DOWN, T_AQKV, T_ATTN, T_COMB, T_
 typedef float f4 __attribute__((ext_vector_type(4)));
 typedef float f2 __attribute__((ext_vector_type(2)));
 
-// Cross-block activations of one step, as (value, tag) pairs. pml: the
-// attention splits' (max score, tag), (exp sum, tag) per (query head, split);
-// pacc: their weighted value sums, plain floats published by the pml pair.
+// Cross-block activations of one step, as (value, tag) pairs, per row of a
+// multi-row step (a one-row step uses row 0). pml: the attention splits' (max
+// score, tag), (exp sum, tag) per (query head, split); pacc: their weighted
+// value sums, plain floats published by the pml pair.
 struct Scratch {
-    f2 x[H], after[H], proj[CH], z[VD], ab[2 * VH], core[VD];
-    f2 mixed[QROWS], key[KVR], value[KVR], ctx[NH * HD], product[I];
-    f2 pml[NH * SMAX * 2];
-    float pacc[NH * SMAX * HD];
-    f2 lmpart[NW * 4];  // (max, index, non-finite count, unused) per wave
+    f2 x[NRMAX][H], after[NRMAX][H], proj[NRMAX][CH], z[NRMAX][VD], ab[NRMAX][2 * VH], core[NRMAX][VD];
+    f2 mixed[NRMAX][QROWS], key[NRMAX][KVR], value[NRMAX][KVR], ctx[NRMAX][NH * HD], product[NRMAX][I];
+    f2 pml[NRMAX][NH * SMAX * 2];
+    float pacc[NRMAX][NH * SMAX * HD];
+    f2 lmpart[NRMAX][NW * 4];  // (max, index, non-finite count, unused) per wave
     unsigned lmpool[4];  // lm_head chunk counters: [epoch & 1] this launch's, the other reset for the next
 };
 #define SOFF(field) unsigned(offsetof(::qr::dec::Scratch, field))
+// Row t of a scratch field.
+#define SROW(field, t) (SOFF(field) + unsigned(t) * unsigned(sizeof(::qr::dec::Scratch::field[0])))
 
 struct Args {
     const QrDecodeLayer* layers;
@@ -129,7 +135,11 @@ struct Args {
     int snap;      // > 0: the updated DeltaNet conv and recurrent states are also written to this snapshot copy
     unsigned epoch;
     float eps;
-    float rope_cs[ROT / 2], rope_sn[ROT / 2];  // cos / sin of pos / theta^(2i / rot)
+    // multi-row steps: rows t < nrows are tokens[t] at positions pos + t;
+    // rows t < snaps also write their DeltaNet states to snapshot copy snap0 + t + 1
+    int nrows, snaps, snap0;
+    int tokens[NRMAX];
+    float rope_cs[NRMAX][ROT / 2], rope_sn[NRMAX][ROT / 2];  // cos / sin of (pos + t) / theta^(2i / rot)
 };
 // The layer table read through the constant address space: uniform indices
 // make scalar loads, so the weight pointers stay wave-uniform (in SGPRs).
@@ -244,12 +254,23 @@ __device__ __forceinline__ float wave_maximum(float v) {
 }
 
 // ---------------------------------------------------------------- LDS, waits
+// Staged vectors of a phase: one row's [input | gated vector] (2 VD), or the
+// rows of a multi-row step: NRMAX x (the DOWN input I, the DOUT input and
+// gated vector H + VD, the attention's new q / k / v (NH + 2 NKV) HD).
+constexpr int ACT = NRMAX * I > NRMAX * (H + VD) ? NRMAX * I : NRMAX * (H + VD);
+static_assert(ACT >= 2 * VD && ACT >= NRMAX * (NH + 2 * NKV) * HD, "staging");
+// Where a phase's rows sit in l.act: the layer input (row t at t H), DOUT's
+// gated vector (row t at gated_off + t VD), ATTN's new q / k / v of row t at
+// t (NH + 2 NKV) HD.
+template <int NR>
+constexpr int gated_off() { return NR == 1 ? VD : NR * H; }
+constexpr int ATTN_ROW = (NH + 2 * NKV) * HD;
 struct Lds {
-    alignas(16) float act[2][2 * VD];       // staged broadcast vector, by phase parity
+    alignas(16) float act[2][ACT];          // staged broadcast vectors, by phase parity
     alignas(16) float nw[2][H];             // staged (1 + w) norm weights, by phase parity
     alignas(16) float wave[WAVES][2 * HD];  // wave-private scratch
     int fail;  // the earliest phase in which a lane of the block timed out (kNoFail: none)
-    int token;  // this launch's token
+    int token[NRMAX];  // this launch's tokens (one per row)
     int lmnext;  // the next lm_head row group of the block's range to hand out
     int lmchunk;  // the pool chunk the block streams now
     int lmctr[2];  // the next row group of that chunk, by chunk parity
@@ -369,9 +390,11 @@ __device__ __forceinline__ float silu(float x) { return x * sigmoidf_(x); }
 struct NoMid {
     __device__ void operator()() const {}
 };
+// `pairs`: how many of the N / 2 pairs are polled (the rows of a multi-row
+// step that take part), the rest skipped.
 template <int N, class Mid = NoMid>
 __device__ __forceinline__ void stage_tagged(const Args& a, Rs rs, unsigned off, unsigned want, float* dst, Lds& l,
-                                             int p, Mid&& mid = Mid()) {
+                                             int p, Mid&& mid = Mid(), int pairs = N / 2) {
     constexpr int PAIRS = N / 2, K = (PAIRS + THREADS - 1) / THREADS;
     const unsigned long long start = wall_clock64();
     unsigned o[K];
@@ -381,7 +404,7 @@ __device__ __forceinline__ void stage_tagged(const Args& a, Rs rs, unsigned off,
 #pragma unroll
     for (int k = 0; k < K; ++k) {
         const int i = int(threadIdx.x) + THREADS * k;
-        live[k] = i < PAIRS;
+        live[k] = i < PAIRS && i < pairs;
         o[k] = off + 16u * unsigned(i);
         if (live[k]) first[k] = ldx4(rs, o[k]);
     }
@@ -402,28 +425,33 @@ __device__ __forceinline__ void stage_norm(const float* w, int par, Lds& l) {
 // The layer's input residual into l.act[par]: the token's embedding row for
 // layer 0 (BF16 tables only with int8 matrices, as the reference's int8
 // upload keeps the embedding BF16), else x as written by phase `producer`.
-template <bool Q8, class Mid = NoMid>
-__device__ __forceinline__ void stage_input(const Args& a, Rs rs, int L, int producer, int par, Lds& l, int p,
+template <bool Q8, int NR, class Mid = NoMid>
+__device__ __forceinline__ void stage_input(const Args& a, Rs rs, int L, int producer, int par, Lds& l, int p, int nr,
                                             Mid&& mid = Mid()) {
     if (L == 0) {
         mid();
-        const int t = int(threadIdx.x);
-        if (Q8 && a.emb_bf16) {
-            if (t < H / 8) {
-                const f4 wv = ldp4(rsrc(a.embedding), unsigned(l.token) * unsigned(H * 2) + 16u * unsigned(t), 0);
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const unsigned w = __float_as_uint(wv[j]);
-                    l.act[par][8 * t + 2 * j] = __uint_as_float(w << 16);
-                    l.act[par][8 * t + 2 * j + 1] = __uint_as_float(w & 0xffff0000u);
+        for (int r = 0; r < NR; ++r) {
+            if (r >= nr) break;
+            const int t = int(threadIdx.x);
+            float* dst = &l.act[par][r * H];
+            if (Q8 && a.emb_bf16) {
+                if (t < H / 8) {
+                    const f4 wv = ldp4(rsrc(a.embedding), unsigned(l.token[r]) * unsigned(H * 2) + 16u * unsigned(t), 0);
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        const unsigned w = __float_as_uint(wv[j]);
+                        dst[8 * t + 2 * j] = __uint_as_float(w << 16);
+                        dst[8 * t + 2 * j + 1] = __uint_as_float(w & 0xffff0000u);
+                    }
                 }
+            } else if (t < H / 4) {
+                *reinterpret_cast<f4*>(dst + 4 * t) =
+                    ldp4(rsrc(a.embedding), unsigned(l.token[r]) * unsigned(H * 4) + 16u * unsigned(t), 0);
             }
-        } else if (t < H / 4) {
-            *reinterpret_cast<f4*>(&l.act[par][4 * t]) =
-                ldp4(rsrc(a.embedding), unsigned(l.token) * unsigned(H * 4) + 16u * unsigned(t), 0);
         }
     } else {
-        stage_tagged<H>(a, rs, SOFF(x), tag(a, producer), l.act[par], l, p, mid);
+        stage_tagged<NR * H>(a, rs, SOFF(x), tag(a, producer), l.act[par], l, p, mid, nr * (H / 2));
     }
 }
 // The staged H-vector in chunks times its RMSNorm and the staged (1 + w)
@@ -431,12 +459,12 @@ __device__ __forceinline__ void stage_input(const Args& a, Rs rs, int L, int pro
 // int8 rows: elements 16 lane + 4 v .. +3 (the 16 columns of the lane's
 // 16-byte weight entry).
 template <bool Q8>
-__device__ __forceinline__ void normed_chunks(const Lds& l, int par, float eps, f4 (&xv)[4]) {
+__device__ __forceinline__ void normed_chunks(const Lds& l, int par, float eps, f4 (&xv)[4], int row = 0) {
     const unsigned lane = lane_id();
     float ss = 0.f;
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
-        xv[v] = lds4(&l.act[par][Q8 ? 16 * lane + 4 * v : 4 * (lane + 64 * v)]);
+        xv[v] = lds4(&l.act[par][row * H + (Q8 ? 16 * lane + 4 * v : 4 * (lane + 64 * v))]);
         ss += dot4(xv[v], xv[v]);
     }
     ss = wave_total(ss);
@@ -542,8 +570,10 @@ __device__ __forceinline__ void din_row(const f4* wb, const f4 (&xv)[4], int u, 
         if (lane_id() == R) mine = acc;
     }
 }
-template <bool Q8>
-__device__ __forceinline__ bool phase_din(const Args& a, Rs rs, LayerP w, int L, int p, int u, f4* wb, Lds& l) {
+// The rows of a multi-row step run through the channel's history in order
+// (the history after row r is row r's snapshot).
+template <bool Q8, int NR>
+__device__ __forceinline__ bool phase_din(const Args& a, Rs rs, LayerP w, int L, int p, int u, f4* wb, Lds& l, int nr) {
     const int par = p & 1;
     const int lane = int(lane_id()), row = u * DIN_RPW + lane;
     const bool conv = lane < DIN_RPW && row < CH;
@@ -557,37 +587,64 @@ __device__ __forceinline__ bool phase_din(const Args& a, Rs rs, LayerP w, int L,
         c0 = ldp(cw, co), c1 = ldp(cw, co + 4), c2 = ldp(cw, co + 8), c3 = ldp(cw, co + 12);
     }
     stage_norm(w->input_norm, par, l);
-    stage_input<Q8>(a, rs, L, p - 1, par, l, p, [&] { prefetch_din<Q8>(w, u, wb, 1); });
+    stage_input<Q8, NR>(a, rs, L, p - 1, par, l, p, nr, [&] { prefetch_din<Q8>(w, u, wb, 1); });
     if (!bsync(l, p)) return false;
     if (u * DIN_RPW >= DIN_ROWS) return true;
-    f4 xv[4];
-    normed_chunks<Q8>(l, par, a.eps, xv);
-    float mine = 0.f;  // lane r: the dot product of row u * DIN_RPW + r
-    din_row<Q8, 0>(wb, xv, u, mine);
-    din_row<Q8, 1>(wb, xv, u, mine);
-    din_row<Q8, 2>(wb, xv, u, mine);
-    din_row<Q8, 3>(wb, xv, u, mine);
+    float mine[NR];  // lane r: the dot product of row u * DIN_RPW + r, per step row
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+        mine[r] = 0.f;
+        if (r >= nr) continue;
+        f4 xv[4];
+        normed_chunks<Q8>(l, par, a.eps, xv, r);
+        din_row<Q8, 0>(wb, xv, u, mine[r]);
+        din_row<Q8, 1>(wb, xv, u, mine[r]);
+        din_row<Q8, 2>(wb, xv, u, mine[r]);
+        din_row<Q8, 3>(wb, xv, u, mine[r]);
+    }
     const unsigned t = tag(a, p);
     if (conv) {
-        float sum = 0.f;
-        sum += h0 * c0;
-        sum += h1 * c1;
-        sum += h2 * c2;
-        sum += mine * c3;
-        // the tagged output first: stores leave in order, and a wave's stores
-        // queue behind the memory traffic of its CU
-        stt(rs, SOFF(proj) + 8u * unsigned(row), silu(sum), t);
-        stp(hs, ho, h1);
-        stp(hs, ho + 4, h2);
-        stp(hs, ho + 8, mine);
-        if (a.snap > 0) {  // copy `snap` of the history (the layout of the op path's snapshots)
+        float hist[NR + 3];  // the history then each row's projection: row r sees hist[r .. r + 2]
+        hist[0] = h0;
+        hist[1] = h1;
+        hist[2] = h2;
+#pragma unroll
+        for (int r = 0; r < NR; ++r) {
+            hist[r + 3] = mine[r];
+            if (r >= nr) continue;
+            float sum = 0.f;
+            sum += hist[r] * c0;
+            sum += hist[r + 1] * c1;
+            sum += hist[r + 2] * c2;
+            sum += mine[r] * c3;
+            // the tagged output first: stores leave in order, and a wave's stores
+            // queue behind the memory traffic of its CU
+            stt(rs, SROW(proj, r) + 8u * unsigned(row), silu(sum), t);
+        }
+        const int last = NR == 1 ? 0 : nr - 1;  // the history after the last row
+        stp(hs, ho, hist[last + 1]);
+        stp(hs, ho + 4, hist[last + 2]);
+        stp(hs, ho + 8, hist[last + 3]);
+        if (NR == 1 && a.snap > 0) {  // copy `snap` of the history (the layout of the op path's snapshots)
             const unsigned so = ho + unsigned(a.snap) * unsigned(CH * (CONVK - 1) * 4);
             stp(hs, so, h1);
             stp(hs, so + 4, h2);
-            stp(hs, so + 8, mine);
+            stp(hs, so + 8, mine[0]);
+        }
+        if (NR > 1) {
+#pragma unroll
+            for (int r = 0; r < NR; ++r) {  // row r's history into copy r + 1
+                if (r >= nr || r >= a.snaps) break;
+                const unsigned so = ho + unsigned(a.snap0 + r + 1) * unsigned(CH * (CONVK - 1) * 4);
+                stp(hs, so, hist[r + 1]);
+                stp(hs, so + 4, hist[r + 2]);
+                stp(hs, so + 8, hist[r + 3]);
+            }
         }
     } else if (lane < DIN_RPW && row < DIN_ROWS) {
-        stt(rs, SOFF(ab) + 8u * unsigned(row - CH), mine, t);
+#pragma unroll
+        for (int r = 0; r < NR; ++r)
+            if (r < nr) stt(rs, SROW(ab, r) + 8u * unsigned(row - CH), mine[r], t);
     }
     return true;
 }
@@ -627,15 +684,18 @@ __device__ __forceinline__ void prefetch_mix(LayerP w, int u, f4* wb) {
     }
 }
 template <bool Q8, int R>
-__device__ __forceinline__ void z_row(Rs rs, const f4* wb, const f4 (&xv)[4], int u, unsigned t) {
+__device__ __forceinline__ void z_row(Rs rs, const f4* wb, const f4 (&xv)[4], int u, unsigned t, int r) {
     const int zi = z_index(u), row = zi * Z_RPW + R;
     if (zi >= 0 && row < VD) {
         const float acc = dot_row_h<Q8, 4 * R>(wb, xv);
-        if (lane_id() == 0) stt(rs, SOFF(z) + 8u * unsigned(row), silu(acc), t);
+        if (lane_id() == 0) stt(rs, SROW(z, r) + 8u * unsigned(row), silu(acc), t);
     }
 }
-template <bool Q8>
-__device__ __forceinline__ bool phase_mix(const Args& a, Rs rs, LayerP w, int L, int p, int u, f4* wb, Lds& l) {
+// The delta-rule waves walk the rows of a multi-row step in order, the state
+// staying in their registers (row r's state is its snapshot).
+template <bool Q8, int NR>
+__device__ __forceinline__ bool phase_mix(const Args& a, Rs rs, LayerP w, int L, int p, int u, f4* wb, Lds& l,
+                                          int nr) {
     // the z rows read the layer input and its norm weights as DIN staged them
     // (parity of phase p - 1): the block writes that buffer again only after
     // the barrier that follows this phase, so the phase needs neither a
@@ -645,10 +705,14 @@ __device__ __forceinline__ bool phase_mix(const Args& a, Rs rs, LayerP w, int L,
     const unsigned t = tag(a, p);
     if (u >= MIX_WAVES) {
         if (z_index(u) < 0) return true;
-        f4 xv[4];
-        normed_chunks<Q8>(l, par, a.eps, xv);
-        z_row<Q8, 0>(rs, wb, xv, u, t);
-        z_row<Q8, 1>(rs, wb, xv, u, t);
+#pragma unroll
+        for (int r = 0; r < NR; ++r) {
+            if (r >= nr) break;
+            f4 xv[4];
+            normed_chunks<Q8>(l, par, a.eps, xv, r);
+            z_row<Q8, 0>(rs, wb, xv, u, t, r);
+            z_row<Q8, 1>(rs, wb, xv, u, t, r);
+        }
         return true;
     }
     // the delta rule is the phase's critical path: its wave goes first on its
@@ -660,73 +724,109 @@ __device__ __forceinline__ bool phase_mix(const Args& a, Rs rs, LayerP w, int L,
     // convolved q and k of head h (lane: q[lane], q[lane + 64], k[lane], k[lane + 64]), v of column j
     const unsigned want = tag(a, p - 1);
     const unsigned long long start = wall_clock64();
-    const unsigned qo = SOFF(proj) + (unsigned(h) * DK + lane) * 8u, ko = qo + KD * 8u;
-    const unsigned mo[7] = {qo, qo + 512u, ko, ko + 512u, SOFF(proj) + unsigned(2 * KD + h * DV + j) * 8u,
-                            SOFF(ab) + 8u * unsigned(h), SOFF(ab) + 8u * unsigned(VH + h)};
-    f2 raw[7];
+    // every row's inputs polled at once: row r's q, k (this lane's two of
+    // each), v of column j, a and b of head h
+    unsigned mo[NR][7];
+    f2 raw[NR][7];
 #pragma unroll
-    for (int k = 0; k < 7; ++k) raw[k] = ldx2(rs, mo[k]);
+    for (int r = 0; r < NR; ++r) {
+        const unsigned qo = SROW(proj, r) + (unsigned(h) * DK + lane) * 8u, ko = qo + KD * 8u;
+        mo[r][0] = qo;
+        mo[r][1] = qo + 512u;
+        mo[r][2] = ko;
+        mo[r][3] = ko + 512u;
+        mo[r][4] = SROW(proj, r) + unsigned(2 * KD + h * DV + j) * 8u;
+        mo[r][5] = SROW(ab, r) + 8u * unsigned(h);
+        mo[r][6] = SROW(ab, r) + 8u * unsigned(VH + h);
+        if (r < nr)
+#pragma unroll
+            for (int k = 0; k < 7; ++k) raw[r][k] = ldx2(rs, mo[r][k]);
+    }
     // the gate parameters while the polls are in flight
     float dt = w->gates[h], alog = w->gates[VH + h];
     asm volatile("" : "+v"(dt), "+v"(alog));
-    float mv[7];
+    float mv[NR][7];
     bool ready = true;
 #pragma unroll
-    for (int k = 0; k < 7; ++k) {
-        mv[k] = raw[k].x;
-        ready = ready && __float_as_uint(raw[k].y) == want;
-    }
+    for (int r = 0; r < NR; ++r)
+        if (r < nr)
+#pragma unroll
+            for (int k = 0; k < 7; ++k) {
+                mv[r][k] = raw[r][k].x;
+                ready = ready && __float_as_uint(raw[r][k].y) == want;
+            }
     while (!ready) {  // every pair again in each round: one round trip serves all late ones
         if (wall_clock64() - start > kTimeout || failed(l)) {
             record_failure(a, l, p);
             break;
         }
         __builtin_amdgcn_s_sleep(1);
-#pragma unroll
-        for (int k = 0; k < 7; ++k) raw[k] = ldx2(rs, mo[k]);
         ready = true;
 #pragma unroll
-        for (int k = 0; k < 7; ++k) {
-            mv[k] = raw[k].x;
-            ready = ready && __float_as_uint(raw[k].y) == want;
-        }
+        for (int r = 0; r < NR; ++r)
+            if (r < nr) {
+#pragma unroll
+                for (int k = 0; k < 7; ++k) raw[r][k] = ldx2(rs, mo[r][k]);
+#pragma unroll
+                for (int k = 0; k < 7; ++k) {
+                    mv[r][k] = raw[r][k].x;
+                    ready = ready && __float_as_uint(raw[r][k].y) == want;
+                }
+            }
     }
-    const float q0 = mv[0], q1 = mv[1], k0 = mv[2], k1 = mv[3], v = mv[4], av = mv[5], bv = mv[6];
-    // L2 norms (reference.h:134-143), q / sqrt(dk)
-    const float sq = wave_total(q0 * q0 + q1 * q1);
-    const float sk = wave_total(k0 * k0 + k1 * k1);
-    const float rq = 1.f / sqrtf(sq + 1e-6f), rk = 1.f / sqrtf(sk + 1e-6f), sd = sqrtf(float(DK));
     float* lw = l.wave[wave];
-    lw[lane] = (q0 * rq) / sd;
-    lw[lane + 64] = (q1 * rq) / sd;
-    lw[128 + lane] = k0 * rk;
-    lw[192 + lane] = k1 * rk;
-    compiler_fence();
     const float* qq = lw + pr * 32;        // this lane's 32 key rows of q / sqrt(dk)
     const float* kk = lw + 128 + pr * 32;  // and of k
-    // gates (reference.h:48-60, 144-148)
-    const float log_decay = -expf(alog) * softplusf_(av + dt);
-    const float beta = sigmoidf_(bv);
-    const float decay = expf(log_decay);
-    // the rule (reference.h:149-170) on rows pr*32 .. pr*32+31 of column j, in place in wb[0..7]
-    float m = 0.f;
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-        wb[k] *= decay;
-        m = fdot4(wb[k], lds4(kk + 4 * k), m);
-    }
-    m = column_sum(m);
-    const float delta = (v - m) * beta;
-    float o = 0.f;
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-        wb[k] += lds4(kk + 4 * k) * delta;
-        o = fdot4(wb[k], lds4(qq + 4 * k), o);
-    }
-    o = column_sum(o);
-    if (pr == 0) stt(rs, SOFF(core) + unsigned(h * DV + j) * 8u, o, t);  // the consumers' value first
     const Rs S = rsrc(w->recurrent);
     const unsigned base = ((unsigned(h) * DK + unsigned(pr) * 32u) * DV + unsigned(j)) * 4u;
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+        if (r >= nr) break;
+        const float q0 = mv[r][0], q1 = mv[r][1], k0 = mv[r][2], k1 = mv[r][3], v = mv[r][4], av = mv[r][5],
+                    bv = mv[r][6];
+        // L2 norms (reference.h:134-143), q / sqrt(dk)
+        const float sq = wave_total(q0 * q0 + q1 * q1);
+        const float sk = wave_total(k0 * k0 + k1 * k1);
+        const float rq = 1.f / sqrtf(sq + 1e-6f), rk = 1.f / sqrtf(sk + 1e-6f), sd = sqrtf(float(DK));
+        lw[lane] = (q0 * rq) / sd;
+        lw[lane + 64] = (q1 * rq) / sd;
+        lw[128 + lane] = k0 * rk;
+        lw[192 + lane] = k1 * rk;
+        compiler_fence();
+        // gates (reference.h:48-60, 144-148)
+        const float log_decay = -expf(alog) * softplusf_(av + dt);
+        const float beta = sigmoidf_(bv);
+        const float decay = expf(log_decay);
+        // the rule (reference.h:149-170) on rows pr*32 .. pr*32+31 of column j, in place in wb[0..7]
+        float m = 0.f;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            wb[k] *= decay;
+            m = fdot4(wb[k], lds4(kk + 4 * k), m);
+        }
+        m = column_sum(m);
+        const float delta = (v - m) * beta;
+        float o = 0.f;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            wb[k] += lds4(kk + 4 * k) * delta;
+            o = fdot4(wb[k], lds4(qq + 4 * k), o);
+        }
+        o = column_sum(o);
+        if (pr == 0) stt(rs, SROW(core, r) + unsigned(h * DV + j) * 8u, o, t);  // the consumers' value first
+        if (NR > 1 && r < a.snaps) {  // row r's state into snapshot copy snap0 + r + 1
+            const unsigned sb = base + unsigned(a.snap0 + r + 1) * unsigned(VH * DK * DV * 4);
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                const unsigned so = sb + unsigned(4 * k) * DV * 4u;
+                stp(S, so, wb[k].x);
+                stp(S, so + DV * 4u, wb[k].y);
+                stp(S, so + 2u * DV * 4u, wb[k].z);
+                stp(S, so + 3u * DV * 4u, wb[k].w);
+            }
+        }
+        compiler_fence();  // the next row's q / k replace this row's in the wave's scratch
+    }
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
         const unsigned so = base + unsigned(4 * k) * DV * 4u;
@@ -735,7 +835,7 @@ __device__ __forceinline__ bool phase_mix(const Args& a, Rs rs, LayerP w, int L,
         stp(S, so + 2u * DV * 4u, wb[k].z);
         stp(S, so + 3u * DV * 4u, wb[k].w);
     }
-    if (a.snap > 0) {  // the same state into snapshot copy `snap` (one [VH][DK][DV] state per copy)
+    if (NR == 1 && a.snap > 0) {  // the same state into snapshot copy `snap` (one [VH][DK][DV] state per copy)
         const unsigned sb = base + unsigned(a.snap) * unsigned(VH * DK * DV * 4);
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
@@ -779,24 +879,37 @@ __device__ __forceinline__ void prefetch_row(const float* m, int row, int rows, 
 }
 template <bool Q8, int R, int AUX>
 __device__ __forceinline__ void glu_load(LayerP w, int u, f4* wb);
-template <bool Q8>
-__device__ __forceinline__ bool phase_dout(const Args& a, Rs rs, LayerP w, int L, int p, int u, f4* wb, Lds& l) {
+template <bool Q8, int NR>
+__device__ __forceinline__ bool phase_dout(const Args& a, Rs rs, LayerP w, int L, int p, int u, f4* wb, Lds& l,
+                                           int nr) {
     const int par = p & 1;
     {
         const unsigned th = threadIdx.x;
         const f4 nw = ldp4(rsrc(w->norm_w), 16u * (th & 31), 0);
         const unsigned want = tag(a, p - 1);
         const unsigned long long start = wall_clock64();
-        const unsigned co[4] = {SOFF(core) + 32u * th, SOFF(core) + 32u * th + 16u, SOFF(z) + 32u * th,
-                                SOFF(z) + 32u * th + 16u};
-        const bool all[4] = {true, true, true, true};
-        f2 cz[4];
-        wait2n<4>(a, rs, co, all, want, cz, l, start, p);
-        const f2 c01 = cz[0], c23 = cz[1], z01 = cz[2], z23 = cz[3];
-        const f4 core = f4{c01.x, c01.y, c23.x, c23.y}, sz = f4{z01.x, z01.y, z23.x, z23.y};
-        const float ss = lanes_sum<32>(dot4(core, core));
-        const float r = 1.f / sqrtf(ss / float(DV) + a.eps);
-        *reinterpret_cast<f4*>(&l.act[par][VD + 4 * th]) = sz * ((core * r) * nw);
+        unsigned co[4 * NR];
+        bool live[4 * NR];
+#pragma unroll
+        for (int r = 0; r < NR; ++r) {
+            co[4 * r] = SROW(core, r) + 32u * th;
+            co[4 * r + 1] = SROW(core, r) + 32u * th + 16u;
+            co[4 * r + 2] = SROW(z, r) + 32u * th;
+            co[4 * r + 3] = SROW(z, r) + 32u * th + 16u;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) live[4 * r + k] = r < nr;
+        }
+        f2 cz[4 * NR];
+        wait2n<4 * NR>(a, rs, co, live, want, cz, l, start, p);
+#pragma unroll
+        for (int r = 0; r < NR; ++r) {
+            if (r >= nr) break;
+            const f2 c01 = cz[4 * r], c23 = cz[4 * r + 1], z01 = cz[4 * r + 2], z23 = cz[4 * r + 3];
+            const f4 core = f4{c01.x, c01.y, c23.x, c23.y}, sz = f4{z01.x, z01.y, z23.x, z23.y};
+            const float ss = lanes_sum<32>(dot4(core, core));
+            const float rn = 1.f / sqrtf(ss / float(DV) + a.eps);
+            *reinterpret_cast<f4*>(&l.act[par][gated_off<NR>() + r * VD + 4 * th]) = sz * ((core * rn) * nw);
+        }
     }
     if (!bsync(l, p)) return false;
     if (u >= H) {
@@ -806,9 +919,13 @@ __device__ __forceinline__ bool phase_dout(const Args& a, Rs rs, LayerP w, int L
         }
         return true;
     }
-    const float acc = dot_row_lds<Q8, VD / 256>(wb, l.act[par] + VD);
-    const float res = l.act[par][u];  // the layer input as DIN (phase p - 2) staged it
-    if (lane_id() == 0) stt(rs, SOFF(after) + 8u * unsigned(u), res + acc, tag(a, p));
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+        if (r >= nr) break;
+        const float acc = dot_row_lds<Q8, VD / 256>(wb, l.act[par] + gated_off<NR>() + r * VD);
+        const float res = l.act[par][r * H + u];  // the layer input as DIN (phase p - 2) staged it
+        if (lane_id() == 0) stt(rs, SROW(after, r) + 8u * unsigned(u), res + acc, tag(a, p));
+    }
     return true;
 }
 
@@ -837,25 +954,30 @@ __device__ __forceinline__ void prefetch_glu(LayerP w, int u, f4* wb, int part) 
         glu_load<Q8, 1>(w, u, wb);
 }
 template <bool Q8, int R>
-__device__ __forceinline__ void glu_row(Rs rs, const f4* wb, const f4 (&xv)[4], int row0, unsigned t) {
+__device__ __forceinline__ void glu_row(Rs rs, const f4* wb, const f4 (&xv)[4], int row0, unsigned t, int r) {
     const int row = row0 + R;
     if (row < I) {
         const float g = dot_row_h<Q8, 8 * R>(wb, xv), up = dot_row_h<Q8, 8 * R + 4>(wb, xv);
-        if (lane_id() == 0) stt(rs, SOFF(product) + 8u * unsigned(row), silu(g) * up, t);
+        if (lane_id() == 0) stt(rs, SROW(product, r) + 8u * unsigned(row), silu(g) * up, t);
     }
 }
-template <bool Q8>
-__device__ __forceinline__ bool phase_glu(const Args& a, Rs rs, LayerP w, int p, int u, f4* wb, Lds& l) {
+template <bool Q8, int NR>
+__device__ __forceinline__ bool phase_glu(const Args& a, Rs rs, LayerP w, int p, int u, f4* wb, Lds& l, int nr) {
     const int par = p & 1;
     stage_norm(w->post_norm, par, l);
-    stage_tagged<H>(a, rs, SOFF(after), tag(a, p - 1), l.act[par], l, p, [&] { prefetch_glu<Q8>(w, u, wb, 1); });
+    stage_tagged<NR * H>(a, rs, SOFF(after), tag(a, p - 1), l.act[par], l, p, [&] { prefetch_glu<Q8>(w, u, wb, 1); },
+                         nr * (H / 2));
     if (!bsync(l, p)) return false;
     const int row0 = glu_first<Q8>(u, !w->attention);
     if (row0 >= I) return true;
-    f4 xv[4];
-    normed_chunks<Q8>(l, par, a.eps, xv);
-    glu_row<Q8, 0>(rs, wb, xv, row0, tag(a, p));
-    glu_row<Q8, 1>(rs, wb, xv, row0, tag(a, p));
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+        if (r >= nr) break;
+        f4 xv[4];
+        normed_chunks<Q8>(l, par, a.eps, xv, r);
+        glu_row<Q8, 0>(rs, wb, xv, row0, tag(a, p), r);
+        glu_row<Q8, 1>(rs, wb, xv, row0, tag(a, p), r);
+    }
     return true;
 }
 
@@ -871,19 +993,26 @@ __device__ __forceinline__ void touch_record(LayerP w) {
     asm volatile("" ::"s"(x0), "s"(x1), "s"(x2), "s"(x3));
 }
 // ---- T_DOWN: x = after + down . product
-template <bool Q8>
-__device__ __forceinline__ bool phase_down(const Args& a, Rs rs, LayerP w, LayerP next, int p, int u, f4* wb,
-                                           Lds& l) {
+template <bool Q8, int NR>
+__device__ __forceinline__ bool phase_down(const Args& a, Rs rs, LayerP w, LayerP next, int p, int u, f4* wb, Lds& l,
+                                           int nr) {
     const int par = p & 1;
-    stage_tagged<I>(a, rs, SOFF(product), tag(a, p - 1), l.act[par], l, p, [&] {
-        prefetch_row<Q8, I, 1>(w->down, u, H, wb);
-        if (next) touch_record(next);
-    });
+    stage_tagged<NR * I>(
+        a, rs, SOFF(product), tag(a, p - 1), l.act[par], l, p,
+        [&] {
+            prefetch_row<Q8, I, 1>(w->down, u, H, wb);
+            if (next) touch_record(next);
+        },
+        nr * (I / 2));
     if (!bsync(l, p)) return false;
     if (u >= H) return true;
-    const float acc = dot_row_lds<Q8, I / 256>(wb, l.act[par]);
-    const float res = l.act[par ^ 1][u];  // `after` as GLU (phase p - 1) staged it
-    if (lane_id() == 0) stt(rs, SOFF(x) + 8u * unsigned(u), res + acc, tag(a, p));
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+        if (r >= nr) break;
+        const float acc = dot_row_lds<Q8, I / 256>(wb, l.act[par] + r * I);
+        const float res = l.act[par ^ 1][r * H + u];  // `after` as GLU (phase p - 1) staged it
+        if (lane_id() == 0) stt(rs, SROW(x, r) + 8u * unsigned(u), res + acc, tag(a, p));
+    }
     return true;
 }
 
@@ -908,30 +1037,35 @@ __device__ __forceinline__ void prefetch_aqkv(LayerP w, int u, f4* wb, int part)
     }
 }
 template <bool Q8, int R>
-__device__ __forceinline__ void aqkv_row(Rs rs, const f4* wb, const f4 (&xv)[4], int u, unsigned t) {
+__device__ __forceinline__ void aqkv_row(Rs rs, const f4* wb, const f4 (&xv)[4], int u, unsigned t, int r) {
     const int row = u * AQKV_RPW + R;
     if (row < AQKV_ROWS) {
         const float acc = dot_row_h<Q8, 4 * R>(wb, xv);
         if (lane_id() == 0) {
-            const unsigned dst = row < QROWS ? SOFF(mixed) + 8u * unsigned(row)
-                                 : row < QROWS + KVR ? SOFF(key) + 8u * unsigned(row - QROWS)
-                                                     : SOFF(value) + 8u * unsigned(row - QROWS - KVR);
+            const unsigned dst = row < QROWS ? SROW(mixed, r) + 8u * unsigned(row)
+                                 : row < QROWS + KVR ? SROW(key, r) + 8u * unsigned(row - QROWS)
+                                                     : SROW(value, r) + 8u * unsigned(row - QROWS - KVR);
             stt(rs, dst, acc, t);
         }
     }
 }
-template <bool Q8>
-__device__ __forceinline__ bool phase_aqkv(const Args& a, Rs rs, LayerP w, int L, int p, int u, f4* wb, Lds& l) {
+template <bool Q8, int NR>
+__device__ __forceinline__ bool phase_aqkv(const Args& a, Rs rs, LayerP w, int L, int p, int u, f4* wb, Lds& l,
+                                           int nr) {
     const int par = p & 1;
     stage_norm(w->input_norm, par, l);
-    stage_input<Q8>(a, rs, L, p - 1, par, l, p, [&] { prefetch_aqkv<Q8>(w, u, wb, 1); });
+    stage_input<Q8, NR>(a, rs, L, p - 1, par, l, p, nr, [&] { prefetch_aqkv<Q8>(w, u, wb, 1); });
     if (!bsync(l, p)) return false;
     if (u * AQKV_RPW >= AQKV_ROWS) return true;
-    f4 xv[4];
-    normed_chunks<Q8>(l, par, a.eps, xv);
-    aqkv_row<Q8, 0>(rs, wb, xv, u, tag(a, p));
-    aqkv_row<Q8, 1>(rs, wb, xv, u, tag(a, p));
-    aqkv_row<Q8, 2>(rs, wb, xv, u, tag(a, p));
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+        if (r >= nr) break;
+        f4 xv[4];
+        normed_chunks<Q8>(l, par, a.eps, xv, r);
+        aqkv_row<Q8, 0>(rs, wb, xv, u, tag(a, p), r);
+        aqkv_row<Q8, 1>(rs, wb, xv, u, tag(a, p), r);
+        aqkv_row<Q8, 2>(rs, wb, xv, u, tag(a, p), r);
+    }
     return true;
 }
 
@@ -986,15 +1120,64 @@ __device__ __forceinline__ void patch_new(f4* buf, const float* kn, const float*
         }
     }
 }
-__device__ __forceinline__ void prefetch_attn(LayerP w, int u, int pos, f4* wb) {
-    const int len = pos + 1, span = attn_span(len), splits = (len + span - 1) / span;
-    const AttnUnit au = attn_unit(u, splits);
-    if (au.busy) load_kv_chunk(w, au.kvh, au.sp * span, pos, wb);
+// Multi-row steps: row r (position pos + r) is split as a one-row step at
+// its position would be; the rows' (KV head, split) slots are numbered row
+// after row, and slot gs of the list goes to block gs % BLOCKS, wave pair
+// (gs / BLOCKS) % (WAVES / QPG), round gs / (BLOCKS WAVES / QPG). False past
+// the last slot.
+constexpr int ATTN_PER_ROUND = BLOCKS * (WAVES / QPG);
+__device__ __forceinline__ bool attn_slot(int pos, int nr, int gs, int& r, int& kvh, int& sp, int& span) {
+#pragma unroll
+    for (r = 0; r < NRMAX; ++r) {
+        if (r >= nr) return false;
+        const int len = pos + r + 1;
+        span = attn_span(len);
+        const int splits = (len + span - 1) / span;
+        if (gs < NKV * splits) {
+            kvh = gs / splits;
+            sp = gs % splits;
+            return true;
+        }
+        gs -= NKV * splits;
+    }
+    return false;
+}
+// The lanes whose position of the chunk at `first` is one of the step's new
+// positions pos .. newest take that row's key / value from LDS (row q at
+// rows + q ATTN_ROW).
+__device__ __forceinline__ void patch_rows(f4* buf, const float* rows, int kvh, int first, int pos, int newest) {
+    const unsigned lane = lane_id(), sub = lane & 15, slot = lane >> 4;
+#pragma unroll
+    for (int step = 0; step < SPAN / 4; ++step) {
+        const int pp = first + 4 * step + int(slot);
+        if (pp >= pos && pp <= newest) {
+            const float* kn = rows + (pp - pos) * ATTN_ROW + NH * HD + kvh * HD;
+            const float* vn = rows + (pp - pos) * ATTN_ROW + (NH + NKV) * HD + kvh * HD;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                buf[step * 8 + e] = lds4(kn + sub * 4 + 64 * e);
+                buf[step * 8 + 4 + e] = lds4(vn + sub * 4 + 64 * e);
+            }
+        }
+    }
+}
+template <int NR>
+__device__ __forceinline__ void prefetch_attn(const Args& a, LayerP w, int u, f4* wb) {
+    const int pos = a.pos;
+    if (NR == 1) {
+        const int len = pos + 1, span = attn_span(len), splits = (len + span - 1) / span;
+        const AttnUnit au = attn_unit(u, splits);
+        if (au.busy) load_kv_chunk(w, au.kvh, au.sp * span, pos, wb);
+        return;
+    }
+    int r, kvh, sp, span;
+    if (attn_slot(pos, a.nrows, (u / BLOCKS / QPG) * BLOCKS + u % BLOCKS, r, kvh, sp, span))
+        load_kv_chunk(w, kvh, sp * span, pos, wb);
 }
 // RMSNorm (1 + w) of one head's 256 dims held 4 per lane by a whole wave,
 // then rotate-half RoPE of the first 64 dims (the partner of dim d < 32 is
 // d + 32, on lane + 8), into LDS (reference.h:75-95, 41-47).
-__device__ __forceinline__ void norm_rope_head(f4 x, f4 wplus, const Args& a, float* out) {
+__device__ __forceinline__ void norm_rope_head(f4 x, f4 wplus, const Args& a, float* out, int row = 0) {
     const unsigned lane = lane_id();
     const float ss = wave_total(dot4(x, x));
     const float r = 1.f / sqrtf(ss / float(HD) + a.eps);
@@ -1006,8 +1189,8 @@ __device__ __forceinline__ void norm_rope_head(f4 x, f4 wplus, const Args& a, fl
     other.w = dpp<kRowRor8>(x.w);
     if (lane < ROT / 4) {  // dims 4 lane .. 4 lane + 3 < 64
         const int i = int(4 * (lane & 7));
-        const f4 cs = f4{a.rope_cs[i], a.rope_cs[i + 1], a.rope_cs[i + 2], a.rope_cs[i + 3]};
-        const f4 sn = f4{a.rope_sn[i], a.rope_sn[i + 1], a.rope_sn[i + 2], a.rope_sn[i + 3]};
+        const f4 cs = f4{a.rope_cs[row][i], a.rope_cs[row][i + 1], a.rope_cs[row][i + 2], a.rope_cs[row][i + 3]};
+        const f4 sn = f4{a.rope_sn[row][i], a.rope_sn[row][i + 1], a.rope_sn[row][i + 2], a.rope_sn[row][i + 3]};
         x = lane < 8 ? x * cs - other * sn : x * cs + other * sn;
     }
     *reinterpret_cast<f4*>(out + 4 * lane) = x;
@@ -1046,58 +1229,41 @@ __device__ __forceinline__ void attn_chunk(const f4* kv, const f4 (&q)[4], int f
     }
     m = mn;
 }
-__device__ __forceinline__ bool phase_attn(const Args& a, Rs rs, LayerP w, int p, int u, f4* wb, Lds& l) {
-    const int par = p & 1;
-    const int pos = a.pos, len = pos + 1, span = attn_span(len), splits = (len + span - 1) / span;
-    const bool block_busy = int(blockIdx.x) < NKV * splits;  // waves 0 .. QPG-1 hold the block's first slot
-    const int wave = int(threadIdx.x >> 6);
-    const unsigned want = tag(a, p - 1);
-    if (block_busy) {
-        // normalised, rotated q of the 8 heads (wave h: head h), new k of the 2
-        // KV heads (waves 0, 1) and their new v (waves 2, 3) into LDS: q at
-        // act[h * HD], k at act[NH * HD + kvh * HD], v at act[(NH + NKV) * HD + kvh * HD]
-        const unsigned lane = lane_id();
-        const Rs rn = rsrc(w->qk_norm);
-        const f4 wq = f4(1.f) + ldp4(rn, 16u * lane, 0), wk = f4(1.f) + ldp4(rn, HD * 4u + 16u * lane, 0);
-        const unsigned long long start = wall_clock64();
-        const bool hask = wave < NKV, hasv = wave >= NKV && wave < 2 * NKV;
-        const unsigned qo = SOFF(mixed) + (unsigned(wave) * 2u * HD + 4u * lane) * 8u;
-        const unsigned ko = hask   ? SOFF(key) + (unsigned(wave) * HD + 4u * lane) * 8u
-                            : hasv ? SOFF(value) + (unsigned(wave - NKV) * HD + 4u * lane) * 8u
-                                   : qo;
-        const unsigned qk[4] = {qo, qo + 16u, ko, ko + 16u};
-        const bool live[4] = {true, true, hask || hasv, hask || hasv};
-        f2 qkv[4];
-        wait2n<4>(a, rs, qk, live, want, qkv, l, start, p);
-        norm_rope_head(f4{qkv[0].x, qkv[0].y, qkv[1].x, qkv[1].y}, wq, a, &l.act[par][wave * HD]);
-        if (hask) norm_rope_head(f4{qkv[2].x, qkv[2].y, qkv[3].x, qkv[3].y}, wk, a, &l.act[par][NH * HD + wave * HD]);
-        if (hasv)
-            *reinterpret_cast<f4*>(&l.act[par][(NH + NKV) * HD + (wave - NKV) * HD + 4 * int(lane)]) =
-                f4{qkv[2].x, qkv[2].y, qkv[3].x, qkv[3].y};
-    }
-    if (!bsync(l, p)) return false;
-    const AttnUnit au = attn_unit(u, splits);
-    if (!au.busy) return true;
+// One (row, KV head, split, query head) unit: `pre`: its first chunk is in
+// wb already (else loaded here).
+template <int NR>
+__device__ __forceinline__ void attn_run(const Args& a, Rs rs, LayerP w, int p, int par, Lds& l, int row, int kvh,
+                                         int sp, int g, int span, bool pre, f4* wb) {
     const unsigned lane = lane_id(), sub = lane & 15, slot = lane >> 4;
-    const int kvh = au.kvh, sp = au.sp, h = kvh * QPG + au.g, begin = sp * span, end = min(len, begin + span);
-    const float* kn = &l.act[par][NH * HD + kvh * HD];
-    const float* vn = &l.act[par][(NH + NKV) * HD + kvh * HD];
-    const bool has_new = pos >= begin && pos < end;
-    if (has_new) {
-        if (slot == 0 && au.g == 0) {  // one wave of the slot appends the row to the caches
-            const Rs rk = rsrc(w->keys), rv = rsrc(w->values);
-            const unsigned co = ((unsigned(pos) * NKV + unsigned(kvh)) * HD + sub * 4u) * 4u;
+    const int pos = a.pos, newest = pos + row, len = newest + 1;
+    const int h = kvh * QPG + g, begin = sp * span, end = min(len, begin + span);
+    const float* rows = &l.act[par][0];
+    const float* kn = &l.act[par][row * ATTN_ROW + NH * HD + kvh * HD];
+    const float* vn = &l.act[par][row * ATTN_ROW + (NH + NKV) * HD + kvh * HD];
+    // the new positions pos .. newest that fall in [begin, end), and whether
+    // this row's own position does (its unit appends it to the caches)
+    const bool has_new = NR == 1 ? (pos >= begin && pos < end) : (newest >= begin && pos < end);
+    const bool appends = newest >= begin && newest < end;
+    if (!pre) load_kv_chunk(w, kvh, begin, pos, wb);
+    if (appends && slot == 0 && g == 0) {  // one wave of the slot appends the row to the caches
+        const Rs rk = rsrc(w->keys), rv = rsrc(w->values);
+        const unsigned co = ((unsigned(newest) * NKV + unsigned(kvh)) * HD + sub * 4u) * 4u;
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                stp4(rk, co + 256u * e, lds4(kn + sub * 4 + 64 * e));
-                stp4(rv, co + 256u * e, lds4(vn + sub * 4 + 64 * e));
-            }
+        for (int e = 0; e < 4; ++e) {
+            stp4(rk, co + 256u * e, lds4(kn + sub * 4 + 64 * e));
+            stp4(rv, co + 256u * e, lds4(vn + sub * 4 + 64 * e));
         }
-        patch_new(wb, kn, vn, begin, pos);
     }
+    auto patch = [&](f4* buf, int first) {
+        if (NR == 1)
+            patch_new(buf, kn, vn, first, pos);
+        else
+            patch_rows(buf, rows, kvh, first, pos, newest);
+    };
+    if (has_new) patch(wb, begin);
     f4 q[4];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) q[e] = lds4(&l.act[par][h * HD + sub * 4 + 64 * e]);
+    for (int e = 0; e < 4; ++e) q[e] = lds4(&l.act[par][row * ATTN_ROW + h * HD + sub * 4 + 64 * e]);
     float m = -INFINITY, lsum = 0.f;
     f4 acc[4] = {f4(0.f), f4(0.f), f4(0.f), f4(0.f)};
     // chunks alternate between wb and nb: the next chunk's loads are in
@@ -1109,10 +1275,10 @@ __device__ __forceinline__ bool phase_attn(const Args& a, Rs rs, LayerP w, int p
         if (c1 < end) load_kv_chunk(w, kvh, c1, pos, nb);
         attn_chunk(wb, q, first, end, m, lsum, acc);
         if (c1 >= end) break;
-        if (has_new) patch_new(nb, kn, vn, c1, pos);
+        if (has_new) patch(nb, c1);
         if (c2 < end) load_kv_chunk(w, kvh, c2, pos, wb);
         attn_chunk(nb, q, c1, end, m, lsum, acc);
-        if (c2 < end && has_new) patch_new(wb, kn, vn, c2, pos);
+        if (c2 < end && has_new) patch(wb, c2);
     }
     // merge the 4 position slots
 #pragma unroll
@@ -1135,7 +1301,7 @@ __device__ __forceinline__ bool phase_attn(const Args& a, Rs rs, LayerP w, int p
     }
     const unsigned slotix = unsigned(h) * SMAX + unsigned(sp);
     if (slot == 0) {
-        const unsigned ao = SOFF(pacc) + (slotix * HD + sub * 4u) * 4u;
+        const unsigned ao = SROW(pacc, row) + (slotix * HD + sub * 4u) * 4u;
 #pragma unroll
         for (int e = 0; e < 4; ++e) stx4(rs, ao + 256u * e, acc[e]);
     }
@@ -1144,8 +1310,70 @@ __device__ __forceinline__ bool phase_attn(const Args& a, Rs rs, LayerP w, int p
     compiler_fence();
     if (lane == 0) {
         const unsigned t = tag(a, p);
-        stt(rs, SOFF(pml) + slotix * 16u, m, t);
-        stt(rs, SOFF(pml) + slotix * 16u + 8u, lsum, t);
+        stt(rs, SROW(pml, row) + slotix * 16u, m, t);
+        stt(rs, SROW(pml, row) + slotix * 16u + 8u, lsum, t);
+    }
+}
+
+
+template <int NR>
+__device__ __forceinline__ bool phase_attn(const Args& a, Rs rs, LayerP w, int p, int u, f4* wb, Lds& l, int nr) {
+    const int par = p & 1;
+    const int pos = a.pos, len = pos + 1, span = attn_span(len), splits = (len + span - 1) / span;
+    // waves 0 .. QPG-1 hold the block's first slot (a multi-row step: every block takes part)
+    const bool block_busy = NR > 1 || int(blockIdx.x) < NKV * splits;
+    const int wave = int(threadIdx.x >> 6);
+    const unsigned want = tag(a, p - 1);
+    if (block_busy) {
+        // normalised, rotated q of the 8 heads (wave h: head h), new k of the 2
+        // KV heads (waves 0, 1) and their new v (waves 2, 3) into LDS, per row r
+        // at r ATTN_ROW: q at + h HD, k at + NH HD + kvh HD, v at + (NH + NKV) HD + kvh HD
+        const unsigned lane = lane_id();
+        const Rs rn = rsrc(w->qk_norm);
+        const f4 wq = f4(1.f) + ldp4(rn, 16u * lane, 0), wk = f4(1.f) + ldp4(rn, HD * 4u + 16u * lane, 0);
+        const unsigned long long start = wall_clock64();
+        const bool hask = wave < NKV, hasv = wave >= NKV && wave < 2 * NKV;
+        unsigned qk[4 * NR];
+        bool live[4 * NR];
+#pragma unroll
+        for (int r = 0; r < NR; ++r) {
+            const unsigned qo = SROW(mixed, r) + (unsigned(wave) * 2u * HD + 4u * lane) * 8u;
+            const unsigned ko = hask   ? SROW(key, r) + (unsigned(wave) * HD + 4u * lane) * 8u
+                                : hasv ? SROW(value, r) + (unsigned(wave - NKV) * HD + 4u * lane) * 8u
+                                       : qo;
+            qk[4 * r] = qo;
+            qk[4 * r + 1] = qo + 16u;
+            qk[4 * r + 2] = ko;
+            qk[4 * r + 3] = ko + 16u;
+            live[4 * r] = live[4 * r + 1] = r < nr;
+            live[4 * r + 2] = live[4 * r + 3] = r < nr && (hask || hasv);
+        }
+        f2 qkv[4 * NR];
+        wait2n<4 * NR>(a, rs, qk, live, want, qkv, l, start, p);
+#pragma unroll
+        for (int r = 0; r < NR; ++r) {
+            if (r >= nr) break;
+            float* rowp = &l.act[par][r * ATTN_ROW];
+            norm_rope_head(f4{qkv[4 * r].x, qkv[4 * r].y, qkv[4 * r + 1].x, qkv[4 * r + 1].y}, wq, a, rowp + wave * HD, r);
+            if (hask)
+                norm_rope_head(f4{qkv[4 * r + 2].x, qkv[4 * r + 2].y, qkv[4 * r + 3].x, qkv[4 * r + 3].y}, wk, a,
+                               rowp + NH * HD + wave * HD, r);
+            if (hasv)
+                *reinterpret_cast<f4*>(rowp + (NH + NKV) * HD + (wave - NKV) * HD + 4 * int(lane)) =
+                    f4{qkv[4 * r + 2].x, qkv[4 * r + 2].y, qkv[4 * r + 3].x, qkv[4 * r + 3].y};
+        }
+    }
+    if (!bsync(l, p)) return false;
+    if (NR == 1) {
+        const AttnUnit au = attn_unit(u, splits);
+        if (au.busy) attn_run<NR>(a, rs, w, p, par, l, 0, au.kvh, au.sp, au.g, span, true, wb);
+        return true;
+    }
+    const int block = u % BLOCKS, wv = u / BLOCKS;
+    for (int round = 0;; ++round) {
+        int r, kvh, sp, rspan;
+        if (!attn_slot(pos, nr, round * ATTN_PER_ROUND + (wv / QPG) * BLOCKS + block, r, kvh, sp, rspan)) break;
+        attn_run<NR>(a, rs, w, p, par, l, r, kvh, sp, wv % QPG, rspan, round == 0, wb);
     }
     return true;
 }
@@ -1153,16 +1381,21 @@ __device__ __forceinline__ bool phase_attn(const Args& a, Rs rs, LayerP w, int p
 // ---- T_COMB: merge the splits (log-sum-exp) and apply the sigmoid gate
 // (reference.h:171-200); one wave per (head, 4 dims), lanes over splits.
 constexpr int COMB_PER_LANE = SMAX / 64;
-__device__ __forceinline__ bool phase_comb(const Args& a, Rs rs, int p, int u, Lds& l) {
+// Multi-row steps: units r COMB_WAVES .. take row r.
+template <int NR>
+__device__ __forceinline__ bool phase_comb(const Args& a, Rs rs, int p, int u, Lds& l, int nr) {
+    static_assert(NR * COMB_WAVES <= NW, "one combine unit per wave");
     if (!bsync(l, p)) return false;
-    if (u >= COMB_WAVES) return true;
+    const int row = NR == 1 ? 0 : u / COMB_WAVES;
+    if (NR == 1 ? u >= COMB_WAVES : row >= nr) return true;
+    const int uu = NR == 1 ? u : u % COMB_WAVES;
     const unsigned lane = lane_id();
-    const int len = a.pos + 1, span = attn_span(len), splits = (len + span - 1) / span;
-    const int h = u / (HD / 4), c4 = u % (HD / 4);
+    const int len = a.pos + row + 1, span = attn_span(len), splits = (len + span - 1) / span;
+    const int h = uu / (HD / 4), c4 = uu % (HD / 4);
     const unsigned want = tag(a, p - 1);
     const unsigned long long start = wall_clock64();
     // the gate (q_proj's second half, written two phases back) in flight with the polls
-    const unsigned go = SOFF(mixed) + unsigned(h * 2 * HD + HD + 4 * c4 + int(lane & 3)) * 8u;
+    const unsigned go = SROW(mixed, row) + unsigned(h * 2 * HD + HD + 4 * c4 + int(lane & 3)) * 8u;
     const f2 gpair = ldx2(rs, go);
     float mv[COMB_PER_LANE], lv[COMB_PER_LANE];
     float mm = -INFINITY;
@@ -1174,7 +1407,7 @@ __device__ __forceinline__ bool phase_comb(const Args& a, Rs rs, int p, int u, L
         for (int k = 0; k < COMB_PER_LANE; ++k) {
             const int s = int(lane) + 64 * k;
             live[k] = s < splits;
-            po[k] = SOFF(pml) + (unsigned(h) * SMAX + unsigned(s)) * 16u;
+            po[k] = SROW(pml, row) + (unsigned(h) * SMAX + unsigned(s)) * 16u;
         }
         wait2n<COMB_PER_LANE>(a, rs, po, live, want, ml, l, start, p);
 #pragma unroll
@@ -1190,7 +1423,7 @@ __device__ __forceinline__ bool phase_comb(const Args& a, Rs rs, int p, int u, L
 #pragma unroll
     for (int k = 0; k < COMB_PER_LANE; ++k) {
         const unsigned ix = unsigned(h) * SMAX + (live[k] ? unsigned(lane) + 64u * k : 0u);
-        pv[k] = ldx4(rs, SOFF(pacc) + (ix * HD + unsigned(4 * c4)) * 4u);
+        pv[k] = ldx4(rs, SROW(pacc, row) + (ix * HD + unsigned(4 * c4)) * 4u);
     }
     float den = 0.f;
     f4 num = f4(0.f);
@@ -1209,21 +1442,25 @@ __device__ __forceinline__ bool phase_comb(const Args& a, Rs rs, int p, int u, L
         const float val = lane == 0 ? num.x : lane == 1 ? num.y : lane == 2 ? num.z : num.w;
         const int d = 4 * c4 + int(lane);
         const float gate = __float_as_uint(gpair.y) == tag(a, p - 2) ? gpair.x : wait1(a, rs, go, tag(a, p - 2), l, start, p);
-        stt(rs, SOFF(ctx) + unsigned(h * HD + d) * 8u, (val / den) * sigmoidf_(gate), tag(a, p));
+        stt(rs, SROW(ctx, row) + unsigned(h * HD + d) * 8u, (val / den) * sigmoidf_(gate), tag(a, p));
     }
     return true;
 }
 
 // ---- T_O: after = x + o . ctx
-template <bool Q8>
-__device__ __forceinline__ bool phase_o(const Args& a, Rs rs, int L, int p, int u, const f4* wb, Lds& l) {
+template <bool Q8, int NR>
+__device__ __forceinline__ bool phase_o(const Args& a, Rs rs, int L, int p, int u, const f4* wb, Lds& l, int nr) {
     const int par = p & 1;
-    stage_tagged<NH * HD>(a, rs, SOFF(ctx), tag(a, p - 1), l.act[par], l, p);
+    stage_tagged<NR * NH * HD>(a, rs, SOFF(ctx), tag(a, p - 1), l.act[par], l, p, NoMid(), nr * (NH * HD / 2));
     if (!bsync(l, p)) return false;
     if (u >= H) return true;
-    const float acc = dot_row_lds<Q8, NH * HD / 256>(wb, l.act[par]);
-    const float res = l.act[par ^ 1][u];  // the layer input as AQKV (phase p - 3) staged it
-    if (lane_id() == 0) stt(rs, SOFF(after) + 8u * unsigned(u), res + acc, tag(a, p));
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+        if (r >= nr) break;
+        const float acc = dot_row_lds<Q8, NH * HD / 256>(wb, l.act[par] + r * NH * HD);
+        const float res = l.act[par ^ 1][r * H + u];  // the layer input as AQKV (phase p - 3) staged it
+        if (lane_id() == 0) stt(rs, SROW(after, r) + 8u * unsigned(u), res + acc, tag(a, p));
+    }
     return true;
 }
 
@@ -1246,27 +1483,33 @@ __device__ __forceinline__ void lm_load(Rs lm, int row0, int row_end, int vocab,
             }
         }
 }
-template <bool Q8>
-__device__ __forceinline__ void lm_rows(Rs lg, const f4* buf, const f4 (&xv)[4], int row0, int row_end, float& best,
-                                        unsigned& at, unsigned& bad) {
+// Multi-row steps: each row of the group against every step row's input
+// (row t's logits at t vocab).
+template <bool Q8, int NR>
+__device__ __forceinline__ void lm_rows(Rs lg, const f4* buf, const f4 (&xv)[NR][4], int row0, int row_end, int vocab,
+                                        int nr, float (&best)[NR], unsigned (&at)[NR], unsigned (&bad)[NR]) {
 #pragma unroll
     for (int r = 0; r < LM_G; ++r) {
         const int row = row0 + r;
         if (row < row_end) {
-            float acc = 0.f;
-            if constexpr (Q8) {
-                acc = buf[r * 4 + 1].x * wave_total(q8dot(buf[r * 4], xv, acc));
-            } else {
 #pragma unroll
-                for (int v = 0; v < 4; ++v) acc = fdot4(buf[r * 4 + v], xv[v], acc);
-                acc = wave_total(acc);
-            }
-            if (lane_id() == 0) stp(lg, 4u * unsigned(row), acc);
-            if (!isfinite(acc)) {
-                ++bad;
-            } else if (acc > best) {
-                best = acc;
-                at = unsigned(row);
+            for (int t = 0; t < NR; ++t) {
+                if (t >= nr) break;
+                float acc = 0.f;
+                if constexpr (Q8) {
+                    acc = buf[r * 4 + 1].x * wave_total(q8dot(buf[r * 4], xv[t], acc));
+                } else {
+#pragma unroll
+                    for (int v = 0; v < 4; ++v) acc = fdot4(buf[r * 4 + v], xv[t][v], acc);
+                    acc = wave_total(acc);
+                }
+                if (lane_id() == 0) stp(lg, 4u * (unsigned(t) * unsigned(vocab) + unsigned(row)), acc);
+                if (!isfinite(acc)) {
+                    ++bad[t];
+                } else if (acc > best[t]) {
+                    best[t] = acc;
+                    at[t] = unsigned(row);
+                }
             }
         }
     }
@@ -1306,40 +1549,49 @@ __device__ __forceinline__ int lm_grab(int* ctr, int first) {
 // the LDS counter *ctr (which starts at WAVES). Groups alternate between wb
 // and nb; the counter only grows, so once a grabbed group lies past the range
 // every later one does too.
-template <bool Q8>
-__device__ __forceinline__ void lm_stream(Rs lm, Rs lg, const f4 (&xv)[4], int first, int last, int vocab, int* ctr,
-                                          bool pre, f4* wb, f4* nb, float& best, unsigned& at, unsigned& bad) {
+template <bool Q8, int NR>
+__device__ __forceinline__ void lm_stream(Rs lm, Rs lg, const f4 (&xv)[NR][4], int first, int last, int vocab, int nr,
+                                          int* ctr, bool pre, f4* wb, f4* nb, float (&best)[NR], unsigned (&at)[NR],
+                                          unsigned (&bad)[NR]) {
     int c0 = first + LM_G * int(threadIdx.x >> 6);
     if (!pre) lm_load<Q8>(lm, c0, last, vocab, wb);
     int c1 = lm_grab(ctr, first);
     lm_load<Q8>(lm, c1, last, vocab, nb);
     for (;;) {
         if (c0 >= last) break;
-        lm_rows<Q8>(lg, wb, xv, c0, last, best, at, bad);
+        lm_rows<Q8, NR>(lg, wb, xv, c0, last, vocab, nr, best, at, bad);
         if (c1 >= last) break;
         c0 = lm_grab(ctr, first);
         lm_load<Q8>(lm, c0, last, vocab, wb);
-        lm_rows<Q8>(lg, nb, xv, c1, last, best, at, bad);
+        lm_rows<Q8, NR>(lg, nb, xv, c1, last, vocab, nr, best, at, bad);
         if (c0 >= last) break;
         c1 = lm_grab(ctr, first);
         lm_load<Q8>(lm, c1, last, vocab, nb);
     }
 }
-template <bool Q8>
-__device__ __forceinline__ bool phase_lm(const Args& a, Rs rs, int p, int u, f4* wb, Lds& l) {
+template <bool Q8, int NR>
+__device__ __forceinline__ bool phase_lm(const Args& a, Rs rs, int p, int u, f4* wb, Lds& l, int nr) {
     const int par = p & 1;
     stage_norm(a.final_norm, par, l);
-    stage_tagged<H>(a, rs, SOFF(x), tag(a, p - 1), l.act[par], l, p);
+    stage_tagged<NR * H>(a, rs, SOFF(x), tag(a, p - 1), l.act[par], l, p, NoMid(), nr * (H / 2));
     if (!bsync(l, p)) return false;
-    f4 xv[4];
-    normed_chunks<Q8>(l, par, a.eps, xv);
+    f4 xv[NR][4];
+#pragma unroll
+    for (int t = 0; t < NR; ++t)
+        if (t < nr) normed_chunks<Q8>(l, par, a.eps, xv[t], t);
     int first, last;
     lm_block_range(u, a.vocab, first, last);
     const Rs lm = rsrc(a.lm_head), lg = rsrc(a.logits);
-    float best = -INFINITY;
-    unsigned at = 0xffffffffu, bad = 0;
+    float best[NR];
+    unsigned at[NR], bad[NR];
+#pragma unroll
+    for (int t = 0; t < NR; ++t) {
+        best[t] = -INFINITY;
+        at[t] = 0xffffffffu;
+        bad[t] = 0;
+    }
     f4 nb[4 * LM_G];
-    lm_stream<Q8>(lm, lg, xv, first, last, a.vocab, &l.lmnext, true, wb, nb, best, at, bad);
+    lm_stream<Q8, NR>(lm, lg, xv, first, last, a.vocab, nr, &l.lmnext, true, wb, nb, best, at, bad);
     // then pool chunks, in increasing row order like the range (so a wave's
     // first maximum is its lowest index): thread 0 takes the block's next
     // chunk between two block barriers (the waves are done with the previous
@@ -1357,14 +1609,18 @@ __device__ __forceinline__ bool phase_lm(const Args& a, Rs rs, int p, int u, f4*
         const int c = __builtin_amdgcn_readfirstlane(l.lmchunk);
         if (c >= nchunks) break;
         const int cf = srows + c * LMC;
-        lm_stream<Q8>(lm, lg, xv, cf, min(a.vocab, cf + LMC), a.vocab, &l.lmctr[round & 1], false, wb, nb, best,
-                      at, bad);
+        lm_stream<Q8, NR>(lm, lg, xv, cf, min(a.vocab, cf + LMC), a.vocab, nr, &l.lmctr[round & 1], false, wb, nb,
+                          best, at, bad);
     }
     if (lane_id() == 0) {
-        const unsigned o = SOFF(lmpart) + unsigned(u) * 32u, t = tag(a, p);
-        stt(rs, o, best, t);
-        stt(rs, o + 8, __uint_as_float(at), t);
-        stt(rs, o + 16, __uint_as_float(bad), t);
+#pragma unroll
+        for (int r = 0; r < NR; ++r) {
+            if (r >= nr) break;
+            const unsigned o = SROW(lmpart, r) + unsigned(u) * 32u, t = tag(a, p);
+            stt(rs, o, best[r], t);
+            stt(rs, o + 8, __uint_as_float(at[r]), t);
+            stt(rs, o + 16, __uint_as_float(bad[r]), t);
+        }
     }
     return true;
 }
@@ -1372,7 +1628,8 @@ __device__ __forceinline__ bool phase_lm(const Args& a, Rs rs, int p, int u, f4*
 // ---- T_ARG (block 0): merge the per-wave maxima (first index of the
 // maximum, non-finite count; reference.h:222-230). Each of the block's
 // threads polls NW / THREADS parts at once; the waves' results meet in LDS.
-__device__ __forceinline__ void phase_arg(const Args& a, Rs rs, int p, Lds& l) {
+// Row `row` of a multi-row step (block `row` runs it).
+__device__ __forceinline__ void phase_arg(const Args& a, Rs rs, int p, Lds& l, int row = 0) {
     constexpr int K = NW / THREADS;
     static_assert(NW % THREADS == 0, "argmax parts per thread");
     const unsigned lane = lane_id(), wave = threadIdx.x >> 6;
@@ -1383,7 +1640,7 @@ __device__ __forceinline__ void phase_arg(const Args& a, Rs rs, int p, Lds& l) {
     f2 vi[K], b2[K];
 #pragma unroll
     for (int k = 0; k < K; ++k) {
-        po[k] = SOFF(lmpart) + unsigned(int(threadIdx.x) + THREADS * k) * 32u;
+        po[k] = SROW(lmpart, row) + unsigned(int(threadIdx.x) + THREADS * k) * 32u;
         live[k] = true;
         b2[k] = ldx2(rs, po[k] + 16u);
     }
@@ -1428,8 +1685,8 @@ __device__ __forceinline__ void phase_arg(const Args& a, Rs rs, int p, Lds& l) {
     }
     if (!failed(l)) {
         const Rs pk = rsrc(a.picks);
-        stp(pk, 0, float(at));
-        stp(pk, 4, float(bad));
+        stp(pk, 8u * unsigned(row), float(at));
+        stp(pk, 8u * unsigned(row) + 4u, float(bad));
         if (a.hist) {
             const Rs hs = rsrc(a.hist);
             stp(hs, 0, float(at));
@@ -1479,9 +1736,14 @@ __device__ __forceinline__ void prefetch_layer(const Args& a, int L, int u, f4* 
 // per attention layer, AQKV ATTN COMB O GLU DOWN, then LM and ARG: per layer
 // straight-line code, so the prefetch buffer flows from each phase into the
 // next without a dispatch between them.
-template <bool Q8>
+// NR > 1: a multi-row step (rows 0 .. a.nrows - 1: tokens[r] at positions
+// pos + r), every phase over its rows with the weights read once; each row is
+// computed exactly as a one-row step at its position (the same per-lane
+// arithmetic), so row r equals that step bit for bit.
+template <bool Q8, int NR>
 __global__ __launch_bounds__(THREADS, 1) void decode_kernel(Args a) {
     __shared__ Lds l;
+    const int nr = NR == 1 ? 1 : a.nrows;
     // wave-uniform (readfirstlane lets the compiler keep indices and buffer
     // descriptors derived from it in SGPRs)
     const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x >> 6));
@@ -1491,12 +1753,17 @@ __global__ __launch_bounds__(THREADS, 1) void decode_kernel(Args a) {
         l.lmnext = WAVES;  // groups 0 .. WAVES - 1 are the waves' first, prefetched ones
         if (blockIdx.x == 0)  // the next launch's lm_head chunk counter (this launch uses the other)
             stx(rsrc(a.s), SOFF(lmpool) + 4u * ((a.epoch + 1u) & 1u), 0.f);
-        int tok = a.token;
-        if (a.chain) {  // the previous launch's argmax (kernel boundary: its stores are visible)
-            const float f = ldp(rsrc(a.picks), 0);
-            tok = f >= 0.f && f < float(a.vocab) ? int(f) : 0;  // a bad step is reported by its own slot
+        if (NR == 1) {
+            int tok = a.token;
+            if (a.chain) {  // the previous launch's argmax (kernel boundary: its stores are visible)
+                const float f = ldp(rsrc(a.picks), 0);
+                tok = f >= 0.f && f < float(a.vocab) ? int(f) : 0;  // a bad step is reported by its own slot
+            }
+            l.token[0] = tok;
+        } else {
+#pragma unroll
+            for (int r = 0; r < NR; ++r) l.token[r] = a.tokens[r];
         }
-        l.token = tok;
     }
     __syncthreads();
     const Rs rs = rsrc(a.s);
@@ -1515,28 +1782,28 @@ __global__ __launch_bounds__(THREADS, 1) void decode_kernel(Args a) {
         for (int k = 0; k < WBUF; ++k) wb[k] = f4(0.f);
         prefetch_layer<Q8>(a, L, opaque_uniform(unit), wb);
         if (w->attention) {
-            if (!phase_aqkv<Q8>(a, rs, w, L, p, opaque_uniform(unit), wb, l)) return;
+            if (!phase_aqkv<Q8, NR>(a, rs, w, L, p, opaque_uniform(unit), wb, l, nr)) return;
             out_barrier();
-            prefetch_attn(w, opaque_uniform(unit), a.pos, wb);
+            prefetch_attn<NR>(a, w, opaque_uniform(unit), wb);
             ++p;
-            if (!phase_attn(a, rs, w, p, opaque_uniform(unit), wb, l)) return;
+            if (!phase_attn<NR>(a, rs, w, p, opaque_uniform(unit), wb, l, nr)) return;
             out_barrier();
             prefetch_row<Q8, NH * HD>(w->o, opaque_uniform(unit), H, wb);  // T_COMB reads no weights
             ++p;
-            if (!phase_comb(a, rs, p, opaque_uniform(unit), l)) return;
+            if (!phase_comb<NR>(a, rs, p, opaque_uniform(unit), l, nr)) return;
             out_barrier();
             ++p;
-            if (!phase_o<Q8>(a, rs, L, p, opaque_uniform(unit), wb, l)) return;
+            if (!phase_o<Q8, NR>(a, rs, L, p, opaque_uniform(unit), wb, l, nr)) return;
         } else {
-            if (!phase_din<Q8>(a, rs, w, L, p, opaque_uniform(unit), wb, l)) return;
+            if (!phase_din<Q8, NR>(a, rs, w, L, p, opaque_uniform(unit), wb, l, nr)) return;
             out_barrier();
             prefetch_mix<Q8>(w, opaque_uniform(unit), wb);
             ++p;
-            if (!phase_mix<Q8>(a, rs, w, L, p, opaque_uniform(unit), wb, l)) return;
+            if (!phase_mix<Q8, NR>(a, rs, w, L, p, opaque_uniform(unit), wb, l, nr)) return;
             out_barrier();
             prefetch_row<Q8, VD>(w->out, opaque_uniform(unit), H, wb);
             ++p;
-            if (!phase_dout<Q8>(a, rs, w, L, p, opaque_uniform(unit), wb, l)) return;
+            if (!phase_dout<Q8, NR>(a, rs, w, L, p, opaque_uniform(unit), wb, l, nr)) return;
         }
         out_barrier();
         if (kept(a, Q8 ? kKeepQ8 : kKeepGlu, L))
@@ -1544,22 +1811,27 @@ __global__ __launch_bounds__(THREADS, 1) void decode_kernel(Args a) {
         else
             prefetch_glu<Q8>(w, opaque_uniform(unit), wb, 0);
         ++p;
-        if (!phase_glu<Q8>(a, rs, w, p, opaque_uniform(unit), wb, l)) return;
+        if (!phase_glu<Q8, NR>(a, rs, w, p, opaque_uniform(unit), wb, l, nr)) return;
         out_barrier();
         if (kept(a, Q8 ? kKeepQ8 : kKeepDown, L))
             prefetch_row<Q8, I, 0, 0>(w->down, opaque_uniform(unit), H, wb);
         else
             prefetch_row<Q8, I, 0>(w->down, opaque_uniform(unit), H, wb);
         ++p;
-        if (!phase_down<Q8>(a, rs, w, L + 1 < a.nlayers ? layer(a, L + 1) : nullptr, p, opaque_uniform(unit), wb, l))
+        if (!phase_down<Q8, NR>(a, rs, w, L + 1 < a.nlayers ? layer(a, L + 1) : nullptr, p, opaque_uniform(unit), wb, l,
+                                nr))
             return;
         ++p;
     }
     out_barrier();
     prefetch_lm<Q8>(a, opaque_uniform(unit), wb);
-    if (!phase_lm<Q8>(a, rs, p, opaque_uniform(unit), wb, l)) return;
+    if (!phase_lm<Q8, NR>(a, rs, p, opaque_uniform(unit), wb, l, nr)) return;
     ++p;
-    if (blockIdx.x == 0) phase_arg(a, rs, p, l);
+    if (NR == 1) {
+        if (blockIdx.x == 0) phase_arg(a, rs, p, l);
+    } else if (int(blockIdx.x) < nr) {
+        phase_arg(a, rs, p, l, int(blockIdx.x));
+    }
 }
 
 }  // namespace dec
@@ -1577,7 +1849,8 @@ struct QrDecodePlan {
     int rows = 1;               // logits / picks rows (desc.rows)
     float* logits = nullptr;    // row 0 of the logits rows ([rows, vocab])
     float* picks = nullptr;     // row 0 of the [argmax, non-finite count] rows
-    bool q8 = false;  // int8 matrices and LM head: decode_kernel<true>
+    bool q8 = false;  // int8 matrices and LM head: decode_kernel<true, *>
+    bool rows_ok = false;  // the multi-row kernel fits the device (decode_rows)
     bool cooperative = false;  // launched with hipLaunchCooperativeKernel instead of a plain launch
     float* hist = nullptr;  // [capacity][argmax, non-finite count] of chained steps
 };
@@ -1664,12 +1937,17 @@ int decode_plan_create(const QrDecodeDesc& d, QrDecodePlan** out, hipStream_t s,
     (void)hipGetDevice(&dev);
     (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
     const bool q8 = d.weights == QR_DECODE_INT8;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, q8 ? decode_kernel<true> : decode_kernel<false>,
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, q8 ? decode_kernel<true, 1> : decode_kernel<false, 1>,
                                                      THREADS, 0) != hipSuccess ||
         per_cu * cus < BLOCKS) {
         *why = "one-launch decode: 256 co-resident blocks do not fit this device";
         return -1;
     }
+    int rows_per_cu = 0;
+    const bool rows_fit =
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&rows_per_cu, q8 ? decode_kernel<true, NRMAX> : decode_kernel<false, NRMAX>,
+                                                     THREADS, 0) == hipSuccess &&
+        rows_per_cu * cus >= BLOCKS;
     auto* p = new QrDecodePlan;
     std::memset(&p->args, 0, sizeof(p->args));
     p->capacity = d.capacity;
@@ -1678,6 +1956,7 @@ int decode_plan_create(const QrDecodeDesc& d, QrDecodePlan** out, hipStream_t s,
     p->logits = d.logits;
     p->picks = d.picks;
     p->q8 = q8;
+    p->rows_ok = rows_fit;
     p->device = dev;
     unsigned epoch = 0;
     hipError_t e = hipMalloc(reinterpret_cast<void**>(&p->layers), sizeof(QrDecodeLayer) * size_t(d.layers));
@@ -1735,6 +2014,33 @@ void decode_plan_free(QrDecodePlan* p) {
     delete p;
 }
 
+// RoPE angle pos / theta^(2i / rot) and its cos / sin on the host for row r
+// (reference: src/attention.rs:49-55, the same f32 expressions).
+static void set_rope(const QrDecodePlan* p, dec::Args& a, int r, int position) {
+    for (int i = 0; i < dec::ROT / 2; ++i) {
+        const float angle = float(position) / p->host_denom[size_t(i)];
+        a.rope_cs[r][i] = cosf(angle);
+        a.rope_sn[r][i] = sinf(angle);
+    }
+}
+// Advances the launch epoch and launches the one-row or the multi-row kernel.
+static int launch(QrDecodePlan* p, hipStream_t s, bool rows) {
+    using namespace dec;
+    Args& a = p->args;
+    a.epoch = (a.epoch + 1) & 0x3fffffu;
+    if (a.epoch == 0) {  // tags repeat after 2^22 steps: clear every pair first
+        a.epoch = 1;
+        if (hipError_t e = hipMemsetAsync(p->scratch, 0, sizeof(Scratch), s)) return int(e);
+    }
+    void* args[] = {&a};
+    const void* k = rows ? (p->q8 ? reinterpret_cast<const void*>(decode_kernel<true, NRMAX>)
+                                  : reinterpret_cast<const void*>(decode_kernel<false, NRMAX>))
+                         : (p->q8 ? reinterpret_cast<const void*>(decode_kernel<true, 1>)
+                                  : reinterpret_cast<const void*>(decode_kernel<false, 1>));
+    return p->cooperative ? int(hipLaunchCooperativeKernel(k, dim3(BLOCKS), dim3(THREADS), args, 0, s))
+                          : int(hipLaunchKernel(k, dim3(BLOCKS), dim3(THREADS), args, 0, s));
+}
+
 int decode_step(QrDecodePlan* p, int token, int position, int slot, hipStream_t s, int row, int snap) {
     using namespace dec;
     Args& a = p->args;
@@ -1750,21 +2056,42 @@ int decode_step(QrDecodePlan* p, int token, int position, int slot, hipStream_t 
     a.pos = position;
     // RoPE angle pos / theta^(2i / rot) and its cos / sin on the host
     // (reference: src/attention.rs:49-55, the same f32 expressions)
-    for (int i = 0; i < ROT / 2; ++i) {
-        const float angle = float(position) / p->host_denom[size_t(i)];
-        a.rope_cs[i] = cosf(angle);
-        a.rope_sn[i] = sinf(angle);
+    set_rope(p, a, 0, position);
+    a.nrows = 1;
+    a.snaps = 0;
+    a.snap0 = 0;
+    return launch(p, s, false);
+}
+
+// One launch of up to NRMAX consecutive tokens (part of a verify pass): row
+// r is tokens[r] at position + r, its logits in logits row first + r and
+// [argmax, count] in picks row first + r; when first + r < snaps its DeltaNet
+// states also go to snapshot copy first + r + 1. Each row equals the one-row
+// step of its position.
+int decode_rows(QrDecodePlan* p, const int* tokens, int n, int position, int first, int snaps, hipStream_t s) {
+    using namespace dec;
+    Args& a = p->args;
+    if (!p->rows_ok) return int(hipErrorNotSupported);
+    if (n < 1 || n > NRMAX || first < 0 || first + n > p->rows || position < 0 || position + n > p->capacity ||
+        snaps < 0 || snaps > p->snapshots)
+        return int(hipErrorInvalidValue);
+    for (int r = 0; r < n; ++r)
+        if (tokens[r] < 0 || tokens[r] >= a.vocab) return int(hipErrorInvalidValue);
+    a.logits = p->logits + size_t(first) * size_t(a.vocab);
+    a.picks = p->picks + 2 * first;
+    a.snap0 = first;
+    a.snap = 0;
+    a.chain = 0;
+    a.token = tokens[0];
+    a.hist = nullptr;
+    a.pos = position;
+    a.nrows = n;
+    a.snaps = snaps > first ? snaps - first : 0;
+    for (int r = 0; r < NRMAX; ++r) {
+        a.tokens[r] = r < n ? tokens[r] : 0;
+        set_rope(p, a, r, position + (r < n ? r : 0));
     }
-    a.epoch = (a.epoch + 1) & 0x3fffffu;
-    if (a.epoch == 0) {  // tags repeat after 2^22 steps: clear every pair first
-        a.epoch = 1;
-        if (hipError_t e = hipMemsetAsync(p->scratch, 0, sizeof(Scratch), s)) return int(e);
-    }
-    void* args[] = {&a};
-    const void* k = p->q8 ? reinterpret_cast<const void*>(decode_kernel<true>)
-                          : reinterpret_cast<const void*>(decode_kernel<false>);
-    return p->cooperative ? int(hipLaunchCooperativeKernel(k, dim3(BLOCKS), dim3(THREADS), args, 0, s))
-                          : int(hipLaunchKernel(k, dim3(BLOCKS), dim3(THREADS), args, 0, s));
+    return launch(p, s, true);
 }
 int decode_history_clear(QrDecodePlan* p, int n, hipStream_t s) {
     if (n < 1 || n > p->capacity) return int(hipErrorInvalidValue);

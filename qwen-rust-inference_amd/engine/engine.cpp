@@ -68,6 +68,7 @@ constexpr size_t kAttentionSplit = 32;  // ATTENTION_SPLIT (src/device.rs:192)
 constexpr size_t kKvBlock = 64;         // KV_BLOCK (src/device.rs:201)
 constexpr size_t kPrefillFlush = 32;    // PREFILL_FLUSH_INTERVAL (src/device.rs:858)
 constexpr size_t kVerifyRows = 8;       // VERIFY_ROWS (src/device.rs:865)
+constexpr size_t kDecodeRowsMax = 4;    // rows of one qr_decode_rows launch
 size_t kv_rows(size_t capacity) { return (capacity + kKvBlock - 1) / kKvBlock * kKvBlock; }
 size_t score_row(size_t capacity, size_t head_dim) {
     size_t splits = (capacity + kAttentionSplit - 1) / kAttentionSplit;
@@ -102,6 +103,7 @@ struct Api {
     int (*decode_plan)(Context*, const QrDecodeDesc*, QrDecodePlan**) = nullptr;
     int (*decode_step)(Context*, QrDecodePlan*, int, int) = nullptr;
     int (*decode_step_row)(Context*, QrDecodePlan*, int, int, int, int) = nullptr;
+    int (*decode_rows)(Context*, QrDecodePlan*, const int32_t*, int, int, int, int) = nullptr;
     int (*decode_steps)(Context*, QrDecodePlan*, int, int, int, int32_t*, float*) = nullptr;
     void (*decode_free)(Context*, QrDecodePlan*) = nullptr;
     int (*embed_rows)(Context*, float*, const float*, int, int, int, const int32_t*, int) = nullptr;
@@ -176,6 +178,7 @@ struct Api {
             decode_free = symbol<decltype(decode_free)>("qr_decode_plan_free", false);
             decode_steps = symbol<decltype(decode_steps)>("qr_decode_steps", false);
             decode_step_row = symbol<decltype(decode_step_row)>("qr_decode_step_row", false);
+            if (!(disable & QE_NO_DECODE_ROWS)) decode_rows = symbol<decltype(decode_rows)>("qr_decode_rows", false);
             if (!decode_plan || !decode_step || !decode_free) decode_plan = nullptr;
         }
         if (!(disable & QE_NO_EMBED_ROWS)) embed_rows = symbol<decltype(embed_rows)>("qr_embed_rows", false);
@@ -676,11 +679,24 @@ struct QeRun {
     // buffers, the DeltaNet states after row r in snapshot copy r + 1 for
     // r < snapshot_rows (what accept restores). The launches are queued back
     // to back; the host reads once at the end.
+    // Verify rows: up to four per launch with the weights read once
+    // (qr_decode_rows), else one launch per row; either way each row is the
+    // decode step of its position bit for bit.
     std::vector<float> forward_planned_rows(const uint32_t* ids, size_t t) {
         const Api* a = api();
-        for (size_t r = 0; r < t; ++r)
-            a->check(a->decode_step_row(a->ctx, plan, int(ids[r]), int(position + r), int(r),
-                                        r < snapshot_rows ? int(r + 1) : 0));
+        for (size_t r = 0; r < t;) {
+            const size_t n = std::min<size_t>(kDecodeRowsMax, t - r);
+            if (a->decode_rows && n > 1) {
+                int32_t tok[kDecodeRowsMax];
+                for (size_t k = 0; k < n; ++k) tok[k] = int32_t(ids[r + k]);
+                a->check(a->decode_rows(a->ctx, plan, tok, int(n), int(position + r), int(r), int(snapshot_rows)));
+                r += n;
+            } else {
+                a->check(a->decode_step_row(a->ctx, plan, int(ids[r]), int(position + r), int(r),
+                                            r < snapshot_rows ? int(r + 1) : 0));
+                ++r;
+            }
+        }
         std::vector<float> out;
         std::vector<float> pk(2 * t);
         a->check(a->read(a->ctx, pk.data(), picks.p, pk.size()));

@@ -30,6 +30,7 @@ NO_DECODE_STEP = 64
 NO_EMBED_ROWS = 128
 NO_PREPARED_GEMM = 256
 NO_PLAIN_DECODE_LAUNCH = 512  # one-launch decode steps launched cooperatively
+NO_DECODE_ROWS = 1024  # verify rows one launch each instead of qr_decode_rows
 
 # Every entry point of include/qwen_bridge.h.
 BRIDGE_SYMBOLS = [
@@ -39,7 +40,7 @@ BRIDGE_SYMBOLS = [
     "qr_gemm_bf16_glu", "qr_gemm_i8_glu", "qr_gemm_bf16_add_norm", "qr_gemm_i8_add_norm", "qr_delta_mixer",
     "qr_gemm_f32_group", "qr_gemm_f32_glu", "qr_gemm_f32_add_norm", "qr_profile", "qr_profile_read",
     "qr_decode_plan", "qr_decode_step", "qr_decode_steps", "qr_decode_step_row", "qr_decode_plan_free",
-    "qr_embed_rows", "qr_argmax_fixed", "qr_gemm_f32_prepare", "qr_gemm_f32_release",
+    "qr_embed_rows", "qr_argmax_fixed", "qr_gemm_f32_prepare", "qr_gemm_f32_release", "qr_decode_rows",
 ]
 
 _F = ctypes.POINTER(ctypes.c_float)

@@ -472,6 +472,34 @@ def test_qwen08b_verify_rows_equal_decode_steps(qwen08b, qwen08b_models, fmt):
         m.close()
 
 
+@pytest.mark.parametrize("fmt", [E.F32, E.INT8])
+@pytest.mark.parametrize("prompt_len,n", [(200, 2), (200, 3), (200, 6), (2046, 4), (2046, 6)])
+def test_qwen08b_verify_rows_multi(qwen08b, qwen08b_models, fmt, prompt_len, n):
+    """Verify passes through qr_decode_rows (up to four rows per launch, the
+    weights read once: 2 and 3 rows, 6 = a 4-row and a 2-row launch), rows
+    straddling position 2048 (where a one-row step's attention splits grow
+    from 8 to 16 positions, so consecutive rows are split differently): every
+    row, accepted state and pick equals sequential decode steps bit for bit,
+    and the rows equal the per-row launches (QE_NO_DECODE_ROWS)."""
+    c, w = qwen08b
+    m = qwen08b_models[0] if fmt == E.F32 else E.Model(w, fmt=E.INT8)
+    prompt = [int(v) for v in np.random.default_rng(prompt_len + n).integers(0, c.vocab_size, prompt_len)]
+    draft = [int(v) for v in np.random.default_rng(n).integers(0, c.vocab_size, n)]
+    cap, chunk = prompt_len + 16, 256
+    print(f"multi-row verify: format {fmt}, prompt {prompt_len}, {n} rows", flush=True)
+    verify_rows_equal_steps(c, m, prompt, draft, cap, chunk)
+    per_row = E.Model(w, fmt=fmt, disable=E.NO_DECODE_ROWS)
+    a, b = m.new_run(cap, chunk=chunk, snapshots=n - 1), per_row.new_run(cap, chunk=chunk, snapshots=n - 1)
+    assert a.decode_plan and b.decode_plan
+    a.prefill(prompt)
+    b.prefill(prompt)
+    for ra, rb in zip(a.verify_rollback(draft), b.verify_rollback(draft)):
+        assert np.array_equal(ra, rb)
+    per_row.close()
+    if fmt != E.F32:
+        m.close()
+
+
 @pytest.mark.parametrize("depth", [1, 2, 3])
 def test_qwen08b_speculative_equals_greedy(qwen08b, qwen08b_models, depth):
     """generate (reference src/device/speculative.rs:53-160) on the 0.8B model
