@@ -196,6 +196,13 @@ __device__ __forceinline__ unsigned lane_id() {
     asm volatile("" : "+v"(l));
     return l;
 }
+// The thread index, re-materialised the same way (so the per-thread offsets
+// of a phase's polls are computed in the phase, not kept live across all).
+__device__ __forceinline__ int thread_id() {
+    int t = int(threadIdx.x);
+    asm volatile("" : "+v"(t));
+    return t;
+}
 __device__ __forceinline__ int opaque_uniform(int v) {
     asm volatile("" : "+s"(v));
     return v;
@@ -336,14 +343,7 @@ __device__ __forceinline__ void wait2n(const Args& a, Rs r, const unsigned (&off
 #pragma unroll
     for (int k = 0; k < N; ++k)
         if (live[k]) v[k] = ldx4(r, off[k]);
-#pragma unroll
-    for (int k = 0; k < N; ++k) {
-        if (!live[k]) continue;
-        if (__float_as_uint(v[k].y) == want && __float_as_uint(v[k].w) == want)
-            out[k] = f2{v[k].x, v[k].z};
-        else
-            out[k] = wait2(a, r, off[k], want, l, start, p);
-    }
+    wait2n_from<N>(a, r, off, live, want, v, out, l, start, p);
 }
 template <int N>
 __device__ __forceinline__ void wait1n(const Args& a, Rs r, const unsigned (&off)[N], unsigned want, float (&out)[N],
@@ -397,13 +397,14 @@ __device__ __forceinline__ void stage_tagged(const Args& a, Rs rs, unsigned off,
                                              int p, Mid&& mid = Mid(), int pairs = N / 2) {
     constexpr int PAIRS = N / 2, K = (PAIRS + THREADS - 1) / THREADS;
     const unsigned long long start = wall_clock64();
+    const int tid = thread_id();
     unsigned o[K];
     bool live[K];
     f4 first[K];
     f2 v[K];
 #pragma unroll
     for (int k = 0; k < K; ++k) {
-        const int i = int(threadIdx.x) + THREADS * k;
+        const int i = tid + THREADS * k;
         live[k] = i < PAIRS && i < pairs;
         o[k] = off + 16u * unsigned(i);
         if (live[k]) first[k] = ldx4(rs, o[k]);
@@ -414,7 +415,7 @@ __device__ __forceinline__ void stage_tagged(const Args& a, Rs rs, unsigned off,
     wait2n_from<K>(a, rs, o, live, want, first, v, l, start, p);
 #pragma unroll
     for (int k = 0; k < K; ++k)
-        if (live[k]) *reinterpret_cast<f2*>(dst + 2 * (int(threadIdx.x) + THREADS * k)) = v[k];
+        if (live[k]) *reinterpret_cast<f2*>(dst + 2 * (tid + THREADS * k)) = v[k];
 }
 // (1 + w) of an H-long norm weight into l.nw[par] (plain loads, issued before
 // the tagged polls so their latency overlaps).
@@ -592,9 +593,8 @@ __device__ __forceinline__ bool phase_din(const Args& a, Rs rs, LayerP w, int L,
     if (u * DIN_RPW >= DIN_ROWS) return true;
     float mine[NR];  // lane r: the dot product of row u * DIN_RPW + r, per step row
 #pragma unroll
-    for (int r = 0; r < NR; ++r) {
+    for (int r = 0; r < NR; ++r) {  // every row computed (rows >= nr unused): no branch between the rows' chains
         mine[r] = 0.f;
-        if (r >= nr) continue;
         f4 xv[4];
         normed_chunks<Q8>(l, par, a.eps, xv, r);
         din_row<Q8, 0>(wb, xv, u, mine[r]);
@@ -684,11 +684,11 @@ __device__ __forceinline__ void prefetch_mix(LayerP w, int u, f4* wb) {
     }
 }
 template <bool Q8, int R>
-__device__ __forceinline__ void z_row(Rs rs, const f4* wb, const f4 (&xv)[4], int u, unsigned t, int r) {
+__device__ __forceinline__ void z_row(Rs rs, const f4* wb, const f4 (&xv)[4], int u, unsigned t, int r, bool live) {
     const int zi = z_index(u), row = zi * Z_RPW + R;
     if (zi >= 0 && row < VD) {
         const float acc = dot_row_h<Q8, 4 * R>(wb, xv);
-        if (lane_id() == 0) stt(rs, SROW(z, r) + 8u * unsigned(row), silu(acc), t);
+        if (lane_id() == 0 && live) stt(rs, SROW(z, r) + 8u * unsigned(row), silu(acc), t);
     }
 }
 // The delta-rule waves walk the rows of a multi-row step in order, the state
@@ -707,11 +707,10 @@ __device__ __forceinline__ bool phase_mix(const Args& a, Rs rs, LayerP w, int L,
         if (z_index(u) < 0) return true;
 #pragma unroll
         for (int r = 0; r < NR; ++r) {
-            if (r >= nr) break;
             f4 xv[4];
             normed_chunks<Q8>(l, par, a.eps, xv, r);
-            z_row<Q8, 0>(rs, wb, xv, u, t, r);
-            z_row<Q8, 1>(rs, wb, xv, u, t, r);
+            z_row<Q8, 0>(rs, wb, xv, u, t, r, r < nr);
+            z_row<Q8, 1>(rs, wb, xv, u, t, r, r < nr);
         }
         return true;
     }
@@ -779,24 +778,32 @@ __device__ __forceinline__ bool phase_mix(const Args& a, Rs rs, LayerP w, int L,
     const float* kk = lw + 128 + pr * 32;  // and of k
     const Rs S = rsrc(w->recurrent);
     const unsigned base = ((unsigned(h) * DK + unsigned(pr) * 32u) * DV + unsigned(j)) * 4u;
+    // every row's L2 norms (reference.h:134-143) and gates (reference.h:48-60,
+    // 144-148) first, with no branch between the rows' chains (rows >= nr
+    // unused); then the rule walks the rows in order
+    float rq[NR], rk[NR], beta_r[NR], decay_r[NR];
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+        const float q0 = mv[r][0], q1 = mv[r][1], k0 = mv[r][2], k1 = mv[r][3], av = mv[r][5], bv = mv[r][6];
+        const float sq = wave_total(q0 * q0 + q1 * q1);
+        const float sk = wave_total(k0 * k0 + k1 * k1);
+        rq[r] = 1.f / sqrtf(sq + 1e-6f);
+        rk[r] = 1.f / sqrtf(sk + 1e-6f);
+        const float log_decay = -expf(alog) * softplusf_(av + dt);
+        beta_r[r] = sigmoidf_(bv);
+        decay_r[r] = expf(log_decay);
+    }
 #pragma unroll
     for (int r = 0; r < NR; ++r) {
         if (r >= nr) break;
-        const float q0 = mv[r][0], q1 = mv[r][1], k0 = mv[r][2], k1 = mv[r][3], v = mv[r][4], av = mv[r][5],
-                    bv = mv[r][6];
-        // L2 norms (reference.h:134-143), q / sqrt(dk)
-        const float sq = wave_total(q0 * q0 + q1 * q1);
-        const float sk = wave_total(k0 * k0 + k1 * k1);
-        const float rq = 1.f / sqrtf(sq + 1e-6f), rk = 1.f / sqrtf(sk + 1e-6f), sd = sqrtf(float(DK));
-        lw[lane] = (q0 * rq) / sd;
-        lw[lane + 64] = (q1 * rq) / sd;
-        lw[128 + lane] = k0 * rk;
-        lw[192 + lane] = k1 * rk;
+        const float q0 = mv[r][0], q1 = mv[r][1], k0 = mv[r][2], k1 = mv[r][3], v = mv[r][4];
+        const float sd = sqrtf(float(DK));
+        lw[lane] = (q0 * rq[r]) / sd;
+        lw[lane + 64] = (q1 * rq[r]) / sd;
+        lw[128 + lane] = k0 * rk[r];
+        lw[192 + lane] = k1 * rk[r];
         compiler_fence();
-        // gates (reference.h:48-60, 144-148)
-        const float log_decay = -expf(alog) * softplusf_(av + dt);
-        const float beta = sigmoidf_(bv);
-        const float decay = expf(log_decay);
+        const float beta = beta_r[r], decay = decay_r[r];
         // the rule (reference.h:149-170) on rows pr*32 .. pr*32+31 of column j, in place in wb[0..7]
         float m = 0.f;
 #pragma unroll
@@ -884,7 +891,7 @@ __device__ __forceinline__ bool phase_dout(const Args& a, Rs rs, LayerP w, int L
                                            int nr) {
     const int par = p & 1;
     {
-        const unsigned th = threadIdx.x;
+        const unsigned th = unsigned(thread_id());
         const f4 nw = ldp4(rsrc(w->norm_w), 16u * (th & 31), 0);
         const unsigned want = tag(a, p - 1);
         const unsigned long long start = wall_clock64();
@@ -902,8 +909,7 @@ __device__ __forceinline__ bool phase_dout(const Args& a, Rs rs, LayerP w, int L
         f2 cz[4 * NR];
         wait2n<4 * NR>(a, rs, co, live, want, cz, l, start, p);
 #pragma unroll
-        for (int r = 0; r < NR; ++r) {
-            if (r >= nr) break;
+        for (int r = 0; r < NR; ++r) {  // rows >= nr: unused values, no branch between the rows
             const f2 c01 = cz[4 * r], c23 = cz[4 * r + 1], z01 = cz[4 * r + 2], z23 = cz[4 * r + 3];
             const f4 core = f4{c01.x, c01.y, c23.x, c23.y}, sz = f4{z01.x, z01.y, z23.x, z23.y};
             const float ss = lanes_sum<32>(dot4(core, core));
@@ -921,10 +927,9 @@ __device__ __forceinline__ bool phase_dout(const Args& a, Rs rs, LayerP w, int L
     }
 #pragma unroll
     for (int r = 0; r < NR; ++r) {
-        if (r >= nr) break;
         const float acc = dot_row_lds<Q8, VD / 256>(wb, l.act[par] + gated_off<NR>() + r * VD);
         const float res = l.act[par][r * H + u];  // the layer input as DIN (phase p - 2) staged it
-        if (lane_id() == 0) stt(rs, SROW(after, r) + 8u * unsigned(u), res + acc, tag(a, p));
+        if (lane_id() == 0 && r < nr) stt(rs, SROW(after, r) + 8u * unsigned(u), res + acc, tag(a, p));
     }
     return true;
 }
@@ -954,29 +959,30 @@ __device__ __forceinline__ void prefetch_glu(LayerP w, int u, f4* wb, int part) 
         glu_load<Q8, 1>(w, u, wb);
 }
 template <bool Q8, int R>
-__device__ __forceinline__ void glu_row(Rs rs, const f4* wb, const f4 (&xv)[4], int row0, unsigned t, int r) {
+__device__ __forceinline__ void glu_row(Rs rs, const f4* wb, const f4 (&xv)[4], int row0, unsigned t, int r,
+                                        bool live = true) {
     const int row = row0 + R;
     if (row < I) {
         const float g = dot_row_h<Q8, 8 * R>(wb, xv), up = dot_row_h<Q8, 8 * R + 4>(wb, xv);
-        if (lane_id() == 0) stt(rs, SROW(product, r) + 8u * unsigned(row), silu(g) * up, t);
+        if (lane_id() == 0 && live) stt(rs, SROW(product, r) + 8u * unsigned(row), silu(g) * up, t);
     }
 }
 template <bool Q8, int NR>
 __device__ __forceinline__ bool phase_glu(const Args& a, Rs rs, LayerP w, int p, int u, f4* wb, Lds& l, int nr) {
     const int par = p & 1;
     stage_norm(w->post_norm, par, l);
-    stage_tagged<NR * H>(a, rs, SOFF(after), tag(a, p - 1), l.act[par], l, p, [&] { prefetch_glu<Q8>(w, u, wb, 1); },
+    stage_tagged<NR * H>(a, rs, SOFF(after), tag(a, p - 1), l.act[par], l, p,
+                                   [&] { prefetch_glu<Q8>(w, u, wb, 1); },
                          nr * (H / 2));
     if (!bsync(l, p)) return false;
     const int row0 = glu_first<Q8>(u, !w->attention);
     if (row0 >= I) return true;
 #pragma unroll
     for (int r = 0; r < NR; ++r) {
-        if (r >= nr) break;
         f4 xv[4];
         normed_chunks<Q8>(l, par, a.eps, xv, r);
-        glu_row<Q8, 0>(rs, wb, xv, row0, tag(a, p), r);
-        glu_row<Q8, 1>(rs, wb, xv, row0, tag(a, p), r);
+        glu_row<Q8, 0>(rs, wb, xv, row0, tag(a, p), r, r < nr);
+        glu_row<Q8, 1>(rs, wb, xv, row0, tag(a, p), r, r < nr);
     }
     return true;
 }
@@ -1008,10 +1014,9 @@ __device__ __forceinline__ bool phase_down(const Args& a, Rs rs, LayerP w, Layer
     if (u >= H) return true;
 #pragma unroll
     for (int r = 0; r < NR; ++r) {
-        if (r >= nr) break;
         const float acc = dot_row_lds<Q8, I / 256>(wb, l.act[par] + r * I);
         const float res = l.act[par ^ 1][r * H + u];  // `after` as GLU (phase p - 1) staged it
-        if (lane_id() == 0) stt(rs, SROW(x, r) + 8u * unsigned(u), res + acc, tag(a, p));
+        if (lane_id() == 0 && r < nr) stt(rs, SROW(x, r) + 8u * unsigned(u), res + acc, tag(a, p));
     }
     return true;
 }
@@ -1037,11 +1042,12 @@ __device__ __forceinline__ void prefetch_aqkv(LayerP w, int u, f4* wb, int part)
     }
 }
 template <bool Q8, int R>
-__device__ __forceinline__ void aqkv_row(Rs rs, const f4* wb, const f4 (&xv)[4], int u, unsigned t, int r) {
+__device__ __forceinline__ void aqkv_row(Rs rs, const f4* wb, const f4 (&xv)[4], int u, unsigned t, int r,
+                                         bool live = true) {
     const int row = u * AQKV_RPW + R;
     if (row < AQKV_ROWS) {
         const float acc = dot_row_h<Q8, 4 * R>(wb, xv);
-        if (lane_id() == 0) {
+        if (lane_id() == 0 && live) {
             const unsigned dst = row < QROWS ? SROW(mixed, r) + 8u * unsigned(row)
                                  : row < QROWS + KVR ? SROW(key, r) + 8u * unsigned(row - QROWS)
                                                      : SROW(value, r) + 8u * unsigned(row - QROWS - KVR);
@@ -1059,12 +1065,11 @@ __device__ __forceinline__ bool phase_aqkv(const Args& a, Rs rs, LayerP w, int L
     if (u * AQKV_RPW >= AQKV_ROWS) return true;
 #pragma unroll
     for (int r = 0; r < NR; ++r) {
-        if (r >= nr) break;
         f4 xv[4];
         normed_chunks<Q8>(l, par, a.eps, xv, r);
-        aqkv_row<Q8, 0>(rs, wb, xv, u, tag(a, p), r);
-        aqkv_row<Q8, 1>(rs, wb, xv, u, tag(a, p), r);
-        aqkv_row<Q8, 2>(rs, wb, xv, u, tag(a, p), r);
+        aqkv_row<Q8, 0>(rs, wb, xv, u, tag(a, p), r, r < nr);
+        aqkv_row<Q8, 1>(rs, wb, xv, u, tag(a, p), r, r < nr);
+        aqkv_row<Q8, 2>(rs, wb, xv, u, tag(a, p), r, r < nr);
     }
     return true;
 }
@@ -1351,8 +1356,7 @@ __device__ __forceinline__ bool phase_attn(const Args& a, Rs rs, LayerP w, int p
         f2 qkv[4 * NR];
         wait2n<4 * NR>(a, rs, qk, live, want, qkv, l, start, p);
 #pragma unroll
-        for (int r = 0; r < NR; ++r) {
-            if (r >= nr) break;
+        for (int r = 0; r < NR; ++r) {  // rows >= nr: unused values
             float* rowp = &l.act[par][r * ATTN_ROW];
             norm_rope_head(f4{qkv[4 * r].x, qkv[4 * r].y, qkv[4 * r + 1].x, qkv[4 * r + 1].y}, wq, a, rowp + wave * HD, r);
             if (hask)
@@ -1451,15 +1455,15 @@ __device__ __forceinline__ bool phase_comb(const Args& a, Rs rs, int p, int u, L
 template <bool Q8, int NR>
 __device__ __forceinline__ bool phase_o(const Args& a, Rs rs, int L, int p, int u, const f4* wb, Lds& l, int nr) {
     const int par = p & 1;
-    stage_tagged<NR * NH * HD>(a, rs, SOFF(ctx), tag(a, p - 1), l.act[par], l, p, NoMid(), nr * (NH * HD / 2));
+    stage_tagged<NR * NH * HD>(a, rs, SOFF(ctx), tag(a, p - 1), l.act[par], l, p, NoMid(),
+                                         nr * (NH * HD / 2));
     if (!bsync(l, p)) return false;
     if (u >= H) return true;
 #pragma unroll
     for (int r = 0; r < NR; ++r) {
-        if (r >= nr) break;
         const float acc = dot_row_lds<Q8, NH * HD / 256>(wb, l.act[par] + r * NH * HD);
         const float res = l.act[par ^ 1][r * H + u];  // the layer input as AQKV (phase p - 3) staged it
-        if (lane_id() == 0) stt(rs, SROW(after, r) + 8u * unsigned(u), res + acc, tag(a, p));
+        if (lane_id() == 0 && r < nr) stt(rs, SROW(after, r) + 8u * unsigned(u), res + acc, tag(a, p));
     }
     return true;
 }
@@ -1483,34 +1487,81 @@ __device__ __forceinline__ void lm_load(Rs lm, int row0, int row_end, int vocab,
             }
         }
 }
-// Multi-row steps: each row of the group against every step row's input
-// (row t's logits at t vocab).
-template <bool Q8, int NR>
-__device__ __forceinline__ void lm_rows(Rs lg, const f4* buf, const f4 (&xv)[NR][4], int row0, int row_end, int vocab,
-                                        int nr, float (&best)[NR], unsigned (&at)[NR], unsigned (&bad)[NR]) {
+// One lm_head row's logit from its dot-product partial: stored for rows
+// t < nr, folded into row t's running (max, first index, non-finite count).
+template <int NR>
+__device__ __forceinline__ void lm_take(Rs lg, float acc, int t, int row, int vocab, int nr, float (&best)[NR],
+                                        unsigned (&at)[NR], unsigned (&bad)[NR]) {
+    if (lane_id() == 0 && t < nr) stp(lg, 4u * (unsigned(t) * unsigned(vocab) + unsigned(row)), acc);
+    if (!isfinite(acc)) {
+        ++bad[t];
+    } else if (acc > best[t]) {
+        best[t] = acc;
+        at[t] = unsigned(row);
+    }
+}
+// The LM_G rows of a group against the step's inputs (row t's logits at
+// t vocab; rows >= nr computed, not stored), in the per-lane order of the
+// one-row step: one-row steps with the input in registers; multi-row int8
+// steps unpack each weight row once and take the NR inputs from registers
+// (xv[t]); multi-row fp32 steps walk the inputs in the outer loop, each read
+// once per group from LDS (xn: row t at t H, in the lane layout of
+// normed_chunks). Each input row's maxima are taken in row order.
+template <bool Q8, int NR, int NX>
+__device__ __forceinline__ void lm_rows(Rs lg, const f4* buf, const f4 (&xv)[NX][4], const float* xn, int row0,
+                                        int row_end, int vocab, int nr, float (&best)[NR], unsigned (&at)[NR],
+                                        unsigned (&bad)[NR]) {
+    if constexpr (NR > 1 && Q8) {
 #pragma unroll
-    for (int r = 0; r < LM_G; ++r) {
-        const int row = row0 + r;
-        if (row < row_end) {
+        for (int r = 0; r < LM_G; ++r) {
+            const int row = row0 + r;
+            if (row >= row_end) continue;
+            float wf[16];
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) wf[4 * j + e] = q8v(__float_as_uint(buf[r * 4][j]), e);
 #pragma unroll
             for (int t = 0; t < NR; ++t) {
-                if (t >= nr) break;
                 float acc = 0.f;
-                if constexpr (Q8) {
-                    acc = buf[r * 4 + 1].x * wave_total(q8dot(buf[r * 4], xv[t], acc));
-                } else {
 #pragma unroll
-                    for (int v = 0; v < 4; ++v) acc = fdot4(buf[r * 4 + v], xv[t][v], acc);
-                    acc = wave_total(acc);
-                }
-                if (lane_id() == 0) stp(lg, 4u * (unsigned(t) * unsigned(vocab) + unsigned(row)), acc);
-                if (!isfinite(acc)) {
-                    ++bad[t];
-                } else if (acc > best[t]) {
-                    best[t] = acc;
-                    at[t] = unsigned(row);
-                }
+                for (int j = 0; j < 4; ++j)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) acc = fmaf(wf[4 * j + e], xv[t][j][e], acc);
+                lm_take<NR>(lg, buf[r * 4 + 1].x * wave_total(acc), t, row, vocab, nr, best, at, bad);
             }
+        }
+    } else if constexpr (NR > 1) {
+        const unsigned lane = lane_id();
+#pragma unroll
+        for (int t = 0; t < NR; ++t) {
+            f4 x[4];
+#pragma unroll
+            for (int v = 0; v < 4; ++v) x[v] = lds4(xn + t * H + 4 * (lane + 64 * v));
+#pragma unroll
+            for (int r = 0; r < LM_G; ++r) {
+                const int row = row0 + r;
+                if (row >= row_end) continue;
+                float acc = 0.f;
+#pragma unroll
+                for (int v = 0; v < 4; ++v) acc = fdot4(buf[r * 4 + v], x[v], acc);
+                lm_take<NR>(lg, wave_total(acc), t, row, vocab, nr, best, at, bad);
+            }
+        }
+    } else {
+#pragma unroll
+        for (int r = 0; r < LM_G; ++r) {
+            const int row = row0 + r;
+            if (row >= row_end) continue;
+            float acc = 0.f;
+            if constexpr (Q8) {
+                acc = buf[r * 4 + 1].x * wave_total(q8dot(buf[r * 4], xv[0], acc));
+            } else {
+#pragma unroll
+                for (int v = 0; v < 4; ++v) acc = fdot4(buf[r * 4 + v], xv[0][v], acc);
+                acc = wave_total(acc);
+            }
+            lm_take<NR>(lg, acc, 0, row, vocab, nr, best, at, bad);
         }
     }
 }
@@ -1549,21 +1600,21 @@ __device__ __forceinline__ int lm_grab(int* ctr, int first) {
 // the LDS counter *ctr (which starts at WAVES). Groups alternate between wb
 // and nb; the counter only grows, so once a grabbed group lies past the range
 // every later one does too.
-template <bool Q8, int NR>
-__device__ __forceinline__ void lm_stream(Rs lm, Rs lg, const f4 (&xv)[NR][4], int first, int last, int vocab, int nr,
-                                          int* ctr, bool pre, f4* wb, f4* nb, float (&best)[NR], unsigned (&at)[NR],
-                                          unsigned (&bad)[NR]) {
+template <bool Q8, int NR, int NX>
+__device__ __forceinline__ void lm_stream(Rs lm, Rs lg, const f4 (&xv)[NX][4], const float* xn, int first, int last,
+                                          int vocab, int nr, int* ctr, bool pre, f4* wb, f4* nb, float (&best)[NR],
+                                          unsigned (&at)[NR], unsigned (&bad)[NR]) {
     int c0 = first + LM_G * int(threadIdx.x >> 6);
     if (!pre) lm_load<Q8>(lm, c0, last, vocab, wb);
     int c1 = lm_grab(ctr, first);
     lm_load<Q8>(lm, c1, last, vocab, nb);
     for (;;) {
         if (c0 >= last) break;
-        lm_rows<Q8, NR>(lg, wb, xv, c0, last, vocab, nr, best, at, bad);
+        lm_rows<Q8, NR, NX>(lg, wb, xv, xn, c0, last, vocab, nr, best, at, bad);
         if (c1 >= last) break;
         c0 = lm_grab(ctr, first);
         lm_load<Q8>(lm, c0, last, vocab, wb);
-        lm_rows<Q8, NR>(lg, nb, xv, c1, last, vocab, nr, best, at, bad);
+        lm_rows<Q8, NR, NX>(lg, nb, xv, xn, c1, last, vocab, nr, best, at, bad);
         if (c0 >= last) break;
         c1 = lm_grab(ctr, first);
         lm_load<Q8>(lm, c1, last, vocab, nb);
@@ -1575,10 +1626,32 @@ __device__ __forceinline__ bool phase_lm(const Args& a, Rs rs, int p, int u, f4*
     stage_norm(a.final_norm, par, l);
     stage_tagged<NR * H>(a, rs, SOFF(x), tag(a, p - 1), l.act[par], l, p, NoMid(), nr * (H / 2));
     if (!bsync(l, p)) return false;
-    f4 xv[NR][4];
+    // the normalised input(s): registers (one-row steps, and the rows of
+    // int8 multi-row steps), else LDS (xn, row t normalised once by wave t)
+    constexpr int NX = (NR == 1 || Q8) ? NR : 1;
+    f4 xv[NX][4];
+    float* xn = &l.act[par][NR * H];
+    if (NR == 1) {
+        normed_chunks<Q8>(l, par, a.eps, xv[0]);
+    } else {
+        const int wave = int(threadIdx.x >> 6);
+        if (wave < NR) {
+            const unsigned lane = lane_id();
+            f4 x[4];
+            normed_chunks<Q8>(l, par, a.eps, x, wave);
 #pragma unroll
-    for (int t = 0; t < NR; ++t)
-        if (t < nr) normed_chunks<Q8>(l, par, a.eps, xv[t], t);
+            for (int v = 0; v < 4; ++v)
+                *reinterpret_cast<f4*>(xn + wave * H + (Q8 ? 16 * lane + 4 * v : 4 * (lane + 64 * v))) = x[v];
+        }
+        if (!bsync(l, p)) return false;
+        if constexpr (Q8) {
+            const unsigned lane = lane_id();
+#pragma unroll
+            for (int t = 0; t < NX; ++t)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) xv[t][v] = lds4(xn + t * H + 16 * lane + 4 * v);
+        }
+    }
     int first, last;
     lm_block_range(u, a.vocab, first, last);
     const Rs lm = rsrc(a.lm_head), lg = rsrc(a.logits);
@@ -1591,7 +1664,7 @@ __device__ __forceinline__ bool phase_lm(const Args& a, Rs rs, int p, int u, f4*
         bad[t] = 0;
     }
     f4 nb[4 * LM_G];
-    lm_stream<Q8, NR>(lm, lg, xv, first, last, a.vocab, nr, &l.lmnext, true, wb, nb, best, at, bad);
+    lm_stream<Q8, NR, NX>(lm, lg, xv, xn, first, last, a.vocab, nr, &l.lmnext, true, wb, nb, best, at, bad);
     // then pool chunks, in increasing row order like the range (so a wave's
     // first maximum is its lowest index): thread 0 takes the block's next
     // chunk between two block barriers (the waves are done with the previous
@@ -1609,8 +1682,8 @@ __device__ __forceinline__ bool phase_lm(const Args& a, Rs rs, int p, int u, f4*
         const int c = __builtin_amdgcn_readfirstlane(l.lmchunk);
         if (c >= nchunks) break;
         const int cf = srows + c * LMC;
-        lm_stream<Q8, NR>(lm, lg, xv, cf, min(a.vocab, cf + LMC), a.vocab, nr, &l.lmctr[round & 1], false, wb, nb,
-                          best, at, bad);
+        lm_stream<Q8, NR, NX>(lm, lg, xv, xn, cf, min(a.vocab, cf + LMC), a.vocab, nr, &l.lmctr[round & 1], false,
+                              wb, nb, best, at, bad);
     }
     if (lane_id() == 0) {
 #pragma unroll
@@ -1640,7 +1713,7 @@ __device__ __forceinline__ void phase_arg(const Args& a, Rs rs, int p, Lds& l, i
     f2 vi[K], b2[K];
 #pragma unroll
     for (int k = 0; k < K; ++k) {
-        po[k] = SROW(lmpart, row) + unsigned(int(threadIdx.x) + THREADS * k) * 32u;
+        po[k] = SROW(lmpart, row) + unsigned(thread_id() + THREADS * k) * 32u;
         live[k] = true;
         b2[k] = ldx2(rs, po[k] + 16u);
     }
