@@ -10,10 +10,14 @@ stream synchronisation on both sides. value = decode tokens/s at ctx 454.
 
 Also reported: weight-read HBM GB/s of the decode step; the prefill rate of
 the prompt; the 2644- and 10,240-token prefills (config 3: median of timed
-runs, tok/s and FLOP rate against the fp32 MFMA peak; --no-prefill skips);
-decode at ctx 8192 after a real 8192-token prefill (config 4; --no-long
-skips); int8 decode at ctx 454 and a 4-row verify with snapshots (config 5;
---no-int8 skips); the drop-in rates (an unmodified reference engine: the op
+runs, tok/s, the fp32-equivalent FLOP rate, the BF16 part products it
+executes and the fraction of the prefill time the work would take at the
+peaks of the instructions executed; --no-prefill skips); the 4-row verify
+and speculative generation (n-gram and known-continuation drafts) against
+plain greedy (--no-spec skips); decode at ctx 8192 after a real 8192-token
+prefill (config 4; --no-long skips); int8 decode at ctx 454, its 4-row
+verify with snapshots and speculative rates (config 5; --no-int8 skips);
+the drop-in rates (an unmodified reference engine: the op
 sequence of bridge calls, no one-launch step or fp32 fusions, prefill in
 128-token chunks; --no-dropin skips). roofline: the one-launch decode kernel
 (decode_kernel: every layer, lm_head and argmax of a step), timed with a
@@ -22,9 +26,10 @@ the same decode; achieved = the step's algorithmic HBM bytes (every matrix
 once, DeltaNet recurrent and conv states read and written, K/V rows of the
 context read and the new row written, logits written) / launch duration.
 cpu_baseline: the CPU oracle (restatement of the reference's Backend::Vector
-path) on this host, decode steps at ctx 454 from the GPU run's state after
-the prompt: one warmup step and --cpu-steps timed steps, at the reference's
-default thread count min(cores, 8) (the value) and at every core of this
+path) on this host: decode steps at ctx 454 from the GPU run's state after
+the prompt (the value), and token-by-token prefill steps near ctx 2644; one
+warmup step, then --cpu-runs runs of --cpu-steps steps each, at the
+reference's default thread count min(cores, 8) and at every core of this
 job's CPU share (at most 16 on a one-GPU box).
 """
 import argparse
@@ -123,6 +128,11 @@ def prefill_flops(c, n: int, weight_params: int) -> float:
     n(n+1)/2 pairs per head), and the chunked DeltaRule (per chunk and head:
     the Gram products, the triangular solve, U / W, and the three scan
     products)."""
+    return sum(prefill_flop_parts(c, n, weight_params))
+
+
+def prefill_flop_parts(c, n: int, weight_params: int):
+    """(projections, attention, DeltaRule) FLOPs of prefill_flops."""
     vocab_params = c.vocab_size * c.hidden_size
     proj = 2.0 * (weight_params - vocab_params) * n + 2.0 * vocab_params
     attn_layers = sum(1 for t in c.layer_types if t == "full_attention")
@@ -130,7 +140,68 @@ def prefill_flops(c, n: int, weight_params: int) -> float:
     dk, dv, ch = c.key_dim, c.value_dim, 64
     per_chunk = 2.0 * (2 * ch * ch * dk + ch * ch * (dk + dv) / 2 + 2 * ch * dk * dv + ch * ch * dv + dk * ch * dv)
     rule = (len(c.layer_types) - attn_layers) * c.value_heads * -(-n // ch) * per_chunk
-    return proj + attn + rule
+    return proj, attn, rule
+
+
+# Part products per fp32 multiply-add on the BF16 MFMA (x = x0 + x1 + x2 for
+# both operands, the six products with p + q <= 2): the prefill projections
+# (csrc/gemm_p3.hip) and prefill attention (attention_prefill_bf3_kernel) run
+# on v_mfma_f32_32x32x16_bf16 at this multiple of the fp32-equivalent FLOPs;
+# the chunked DeltaRule runs on fp32 MFMA (v_mfma_f32_16x16x4_f32).
+BF16_PARTS = 6
+MFMA_BF16_PEAK_TFLOPS = 2500.0
+
+
+class KnownDraft:
+    """A draft that proposes the true greedy continuation (known from a plain
+    greedy run of the same model): every drafted token is accepted, so a
+    speculative pass of depth k emits k + 1 tokens. The upper bound of what
+    the one-pass verify gives a draft model."""
+
+    def __init__(self, prompt, continuation):
+        self.seq = list(prompt[1:]) + list(continuation)
+        self.n = 0
+
+    def absorb(self, tokens):
+        self.n += len(tokens)
+
+    def draft(self, k):
+        return self.seq[self.n:self.n + k]
+
+
+def speculative_rates(E, model, prompt, depth: int, n_new: int, snapshots: int):
+    """Plain greedy and speculative (n-gram and known-continuation drafts)
+    generation of n_new tokens after `prompt` on fresh runs: tok/s of the
+    decode part (prefill excluded), the verify pass cost and acceptance."""
+    out = {}
+    r = model.new_run(len(prompt) + n_new + 8, chunk=len(prompt), snapshots=snapshots)
+    tok = int(__import__("numpy").argmax(r.prefill(prompt)))
+    model.sync()
+    ids, _ = r.decode_greedy(tok, 2)  # warm
+    r.close()
+    r = model.new_run(len(prompt) + n_new + 8, chunk=len(prompt), snapshots=snapshots)
+    tok = int(__import__("numpy").argmax(r.prefill(prompt)))
+    model.sync()
+    t = time.perf_counter()
+    ids, _ = r.decode_greedy(tok, n_new)
+    model.sync()
+    out["greedy_tok_s"] = round((n_new - 1) / (time.perf_counter() - t), 1)
+    r.close()
+    for name, draft in (("ngram", "ngram"), ("known", KnownDraft(prompt, ids))):
+        for rep in range(2):  # the first pass warms the verify code path
+            if name == "known":
+                draft.n = 0
+            r = model.new_run(len(prompt) + n_new + 8, chunk=len(prompt), snapshots=snapshots)
+            model.sync()
+            t = time.perf_counter()
+            got, st = r.speculative_generate(prompt, n_new, depth, draft=draft)
+            model.sync()
+            wall = time.perf_counter() - t
+            r.close()
+        same = got == ids
+        out[name] = {"tok_s": round((len(got) - 1) / (wall - st["prefill_s"]), 1), "passes": st["passes"],
+                     "accepted": st["accepted"], "offered": st["offered"], "equals_greedy": same}
+    return out
 
 
 def main():
@@ -144,10 +215,13 @@ def main():
     ap.add_argument("--no-long", dest="long", action="store_false", help="skip decode at ctx 8192 (config 4)")
     ap.add_argument("--no-int8", dest="int8", action="store_false",
                     help="skip the int8 decode and 4-row verify at ctx 454 (config 5)")
+    ap.add_argument("--no-spec", dest="spec", action="store_false",
+                    help="skip the speculative-generation rates (fp32, and int8 with config 5)")
     ap.add_argument("--no-dropin", dest="dropin", action="store_false",
                     help="skip the drop-in (unmodified reference engine call sequence) rates")
-    ap.add_argument("--cpu-steps", type=int, default=3,
-                    help="timed oracle decode steps per thread count of the CPU baseline (0: skip)")
+    ap.add_argument("--cpu-steps", type=int, default=4,
+                    help="timed oracle steps per run of the CPU baseline (0: skip)")
+    ap.add_argument("--cpu-runs", type=int, default=2, help="timed runs per CPU baseline measurement")
     ap.add_argument("--profile-steps", type=int, default=16)
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="also run one device copy of MIB MiB (a plain copy kernel of known size, the scale "
@@ -283,6 +357,39 @@ def main():
         else:
             log(f"stream read failed: {r.stderr.strip()[-200:]}")
 
+    def verify4_ms(m, fmt_prompt):
+        """A 4-row verify with per-row snapshots + accept(1) (the rows' logits
+        rolled back but the first), after one untimed pass."""
+        rv = m.new_run(len(fmt_prompt) + 160, chunk=len(fmt_prompt), snapshots=3)
+        tk = int(np.argmax(rv.prefill(fmt_prompt)))
+        idv, _ = rv.decode_greedy(tk, 3)
+        draft = [int(v) for v in np.random.default_rng(6).integers(0, c.vocab_size, 4)]
+        rv.verify_rollback_greedy(draft)
+        rv.accept(1)
+        m.sync()
+        reps = 16
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            rv.verify_rollback_greedy(draft)
+            rv.accept(1)
+        m.sync()
+        dt = (time.perf_counter() - t0) / reps
+        rv.close()
+        return dt * 1e3
+
+    if args.spec:
+        # Speculative generation (the reference's generate loop, depth 3: one
+        # 4-row verify pass per step) against plain greedy on the same model:
+        # the engine's n-gram prompt-lookup draft, and a draft that knows the
+        # greedy continuation (every token accepted: the one-pass verify's
+        # upper bound for a real draft model).
+        out["verify4_ms"] = round(verify4_ms(model, prompt), 3)
+        spec = speculative_rates(E, model, prompt, 3, 64, 3)
+        out["speculative_454"] = spec
+        log(f"fp32 4-row verify + accept(1): {out['verify4_ms']:.3f} ms; speculative depth 3 over 64 tokens: "
+            f"greedy {spec['greedy_tok_s']} tok/s, n-gram draft {spec['ngram']['tok_s']} tok/s "
+            f"(accepted {spec['ngram']['accepted']}), known draft {spec['known']['tok_s']} tok/s")
+
     if args.long:
         # Decode at ctx 8192 (config 4): a real prefill of 8192 uniform random
         # ids (seed 5, one chunk), then 2 untimed and 64 timed greedy steps.
@@ -326,21 +433,14 @@ def main():
         out["int8_weight_bytes_per_token"] = int8_bytes
         out["int8_hbm_weight_read_frac"] = round(int8_bytes * 64 / dt / 1e9 / HBM_PEAK_GBS, 4)
         log(f"int8 decode @454: {dt / 64 * 1e3:.3f} ms/token, {int8_bytes * 64 / dt / 1e9:.0f} GB/s of int8 weights")
-        tok = ids8[-1]
-        draft = [int(v) for v in np.random.default_rng(6).integers(0, c.vocab_size, 4)]
-        r8.verify_rollback_greedy(draft)
-        r8.accept(1)
-        m8.sync()
-        reps = 16
-        t = time.perf_counter()
-        for _ in range(reps):
-            r8.verify_rollback_greedy(draft)
-            r8.accept(1)
-        m8.sync()
-        dt = (time.perf_counter() - t) / reps
-        out["int8_verify4_ms"] = round(dt * 1e3, 3)
-        log(f"int8 4-row verify with snapshots + accept(1): {dt * 1e3:.3f} ms")
         r8.close()
+        out["int8_verify4_ms"] = round(verify4_ms(m8, prompt), 3)
+        log(f"int8 4-row verify with snapshots + accept(1): {out['int8_verify4_ms']:.3f} ms")
+        if args.spec:
+            spec = speculative_rates(E, m8, prompt, 3, 64, 3)
+            out["int8_speculative_454"] = spec
+            log(f"int8 speculative depth 3: greedy {spec['greedy_tok_s']} tok/s, n-gram {spec['ngram']['tok_s']} "
+                f"tok/s, known draft {spec['known']['tok_s']} tok/s")
         m8.close()
 
     if args.dropin:
@@ -398,13 +498,23 @@ def main():
                     times.append(dt)
                 r2.close()
             dt = float(np.median(times))
-            tflops = prefill_flops(c, n, weight_bytes // 4) / dt / 1e12
+            proj, attn, rule = prefill_flop_parts(c, n, weight_bytes // 4)
+            tflops = (proj + attn + rule) / dt / 1e12
+            # the instructions executed: BF16 part products for the
+            # projections and attention, fp32 MFMA for the DeltaRule; the
+            # fraction of the prefill's time the whole job would take at
+            # those peaks
+            executed = BF16_PARTS * (proj + attn) / dt / 1e12
+            at_peak = BF16_PARTS * (proj + attn) / (MFMA_BF16_PEAK_TFLOPS * 1e12) + rule / (MFMA_F32_PEAK_TFLOPS * 1e12)
             out[f"prefill_{n}_tok_s"] = round(n / dt, 1)
             out[f"prefill_{n}_ms"] = round(dt * 1e3, 2)
             out[f"prefill_{n}_tflops"] = round(tflops, 2)
+            out[f"prefill_{n}_bf16_executed_tflops"] = round(executed, 1)
+            out[f"prefill_{n}_executed_peak_frac"] = round(at_peak / dt, 4)
             out[f"prefill_{n}_mfma_frac"] = round(tflops / MFMA_F32_PEAK_TFLOPS, 4)
             log(f"prefill {n}: {dt * 1e3:.1f} ms (median of {reps}), {n / dt:.0f} tok/s, "
-                f"{tflops:.1f} TFLOP/s algorithmic ({tflops / MFMA_F32_PEAK_TFLOPS:.1%} of fp32 MFMA peak)")
+                f"{tflops:.1f} TFLOP/s algorithmic fp32; executed {executed:.0f} TFLOP/s of BF16 part products; "
+                f"{at_peak / dt:.1%} of the executed instructions' peak time")
     if args.copy_calibration > 0:
         from qwen_mi355x.bridge import Bridge
         br = Bridge()
@@ -418,36 +528,74 @@ def main():
 
     if args.cpu_steps > 0:
         # The oracle (C++ restatement of the reference's Backend::Vector CPU
-        # decode) from the GPU run's state after the 454-token prompt, on the
-        # same greedy tokens: decode steps at ctx 454.
+        # path, one step_compact per token with its logits) on this host, as
+        # the reference's benchmark times it (src/benchmark.rs:93-154: one
+        # warmup, then measured runs; tok/s = steps / summed step time):
+        #   decode: steps at ctx 454 on the config-2 greedy tokens, from the
+        #     GPU run's state after the prompt;
+        #   prefill: token-by-token steps of the 2644-token prompt (seed 2)
+        #     from position 2640, from the GPU's state after its first 2640
+        #     tokens (the reference's CPU prefill is one such step per token).
+        # Each run starts from a fresh copy of the loaded state.
         import oracle as O
         cpu = host_cpu()
         share = min(cpu["affinity"], 16)
-        rc = model.new_run(args.prompt + 8, chunk=args.prompt)
-        rc.prefill(prompt)
-        parts = {(layer, which): rc.state(layer, which) for layer in range(c.num_layers) for which in range(4)}
-        rc.close()
+        n2 = 2644
+        ids2 = [int(v) for v in np.random.default_rng(2).integers(0, c.vocab_size, n2)]
+        start2 = n2 - args.cpu_steps
+        loads = {}
+        for name, pre in (("decode", prompt), ("prefill", ids2[:start2])):
+            rc = model.new_run(len(pre) + 8, chunk=len(pre))
+            rc.prefill(pre)
+            loads[name] = (len(pre), {(layer, which): rc.state(layer, which)
+                                      for layer in range(c.num_layers) for which in range(4)})
+            rc.close()
         oracle = O.Oracle(w)
+        samples = {"decode": ids[1:1 + args.cpu_steps], "prefill": ids2[start2:start2 + args.cpu_steps]}
+        warm_tok = {"decode": ids[0], "prefill": ids2[start2 - 1]}
         rates = {}
         for threads in sorted({min(share, 8), share}):
             O.set_threads(threads)
-            s = oracle.new_state()
-            s.load(args.prompt, lambda layer, which: parts[(layer, which)])
-            s.step(ids[0], O.VECTOR)  # warmup
-            t = time.perf_counter()
-            for tok in ids[1:1 + args.cpu_steps]:
-                s.step(tok, O.VECTOR)
-            rates[threads] = args.cpu_steps / (time.perf_counter() - t)
-            log(f"cpu baseline: {1e3 / rates[threads]:.1f} ms/token on {threads} threads")
-            del s
+            for name in ("decode", "prefill"):
+                pos, parts = loads[name]
+                base = oracle.new_state()
+                base.load(pos, lambda layer, which: parts[(layer, which)])
+                w0 = base.clone()
+                w0.step(warm_tok[name], O.VECTOR)  # warmup (pages the weights in)
+                del w0
+                runs = []
+                for _ in range(args.cpu_runs):
+                    st = base.clone()
+                    t = time.perf_counter()
+                    for tok in samples[name]:
+                        st.step(tok, O.VECTOR)
+                    runs.append(time.perf_counter() - t)
+                    del st
+                rates[(name, threads)] = (len(samples[name]) * len(runs) / sum(runs),
+                                          [round(len(samples[name]) / r, 3) for r in runs])
+                log(f"cpu baseline {name}: {1e3 * sum(runs) / (len(runs) * len(samples[name])):.1f} ms/token on "
+                    f"{threads} threads (runs: {rates[(name, threads)][1]} tok/s)")
+                del base
         default = min(share, 8)
-        out["cpu_baseline"] = {"value": round(rates[default], 3), "unit": "tok/s", "cores": default, "kind": "port",
-                               "sample": f"{args.cpu_steps} decode steps at ctx {args.prompt + 2}.."
-                                         f"{args.prompt + 1 + args.cpu_steps} (after one warmup step) of the config-2 "
-                                         "greedy tokens, from the GPU run's state after the prompt, through the CPU "
-                                         "oracle's Backend::Vector path (C++ restatement of the reference's Rust CPU "
-                                         f"decode); {default} threads = the reference default min(cores, 8)",
-                               "all_cores": {"value": round(rates[share], 3), "cores": share},
+        out["cpu_baseline"] = {"value": round(rates[("decode", default)][0], 3), "unit": "tok/s", "cores": default,
+                               "kind": "port",
+                               "sample": f"{args.cpu_runs} runs x {args.cpu_steps} decode steps at ctx {args.prompt + 2}"
+                                         f"..{args.prompt + 1 + args.cpu_steps} after one warmup step (config-2 greedy "
+                                         "tokens, from the GPU run's state after the prompt), through the CPU oracle's "
+                                         "Backend::Vector path (C++ restatement of the reference's Rust CPU decode); "
+                                         f"{default} threads = the reference default min(cores, 8); tok/s = steps / "
+                                         "summed step time",
+                               "runs": rates[("decode", default)][1],
+                               "all_cores": {"value": round(rates[("decode", share)][0], 3), "cores": share,
+                                             "runs": rates[("decode", share)][1]},
+                               "prefill_2644": {"value": round(rates[("prefill", default)][0], 3), "unit": "tok/s",
+                                                "cores": default, "runs": rates[("prefill", default)][1],
+                                                "all_cores": round(rates[("prefill", share)][0], 3),
+                                                "sample": f"{args.cpu_runs} runs x token-by-token steps at positions "
+                                                          f"{start2}..{n2 - 1} of the 2644-token prompt (seed 2) "
+                                                          "after one warmup step, from the GPU's state after the "
+                                                          f"first {start2} tokens (the reference's CPU prefill: one "
+                                                          "step with logits per token)"},
                                "host": cpu}
 
     run.close()

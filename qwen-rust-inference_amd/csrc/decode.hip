@@ -196,11 +196,14 @@ __device__ __forceinline__ unsigned lane_id() {
     asm volatile("" : "+v"(l));
     return l;
 }
-// The thread index, re-materialised the same way (so the per-thread offsets
-// of a phase's polls are computed in the phase, not kept live across all).
+// The thread index, re-materialised the same way in multi-row kernels (NR >
+// 1: there the per-thread offsets of a phase's polls kept live across all
+// phases spill); one-row kernels have the registers, and are faster with the
+// offsets computed once.
+template <int NR>
 __device__ __forceinline__ int thread_id() {
     int t = int(threadIdx.x);
-    asm volatile("" : "+v"(t));
+    if constexpr (NR > 1) asm volatile("" : "+v"(t));
     return t;
 }
 __device__ __forceinline__ int opaque_uniform(int v) {
@@ -392,12 +395,12 @@ struct NoMid {
 };
 // `pairs`: how many of the N / 2 pairs are polled (the rows of a multi-row
 // step that take part), the rest skipped.
-template <int N, class Mid = NoMid>
+template <int N, int NR, class Mid = NoMid>
 __device__ __forceinline__ void stage_tagged(const Args& a, Rs rs, unsigned off, unsigned want, float* dst, Lds& l,
                                              int p, Mid&& mid = Mid(), int pairs = N / 2) {
     constexpr int PAIRS = N / 2, K = (PAIRS + THREADS - 1) / THREADS;
     const unsigned long long start = wall_clock64();
-    const int tid = thread_id();
+    const int tid = thread_id<NR>();
     unsigned o[K];
     bool live[K];
     f4 first[K];
@@ -452,7 +455,7 @@ __device__ __forceinline__ void stage_input(const Args& a, Rs rs, int L, int pro
             }
         }
     } else {
-        stage_tagged<NR * H>(a, rs, SOFF(x), tag(a, producer), l.act[par], l, p, mid, nr * (H / 2));
+        stage_tagged<NR * H, NR>(a, rs, SOFF(x), tag(a, producer), l.act[par], l, p, mid, nr * (H / 2));
     }
 }
 // The staged H-vector in chunks times its RMSNorm and the staged (1 + w)
@@ -685,6 +688,7 @@ __device__ __forceinline__ void prefetch_mix(LayerP w, int u, f4* wb) {
 }
 template <bool Q8, int R>
 __device__ __forceinline__ void z_row(Rs rs, const f4* wb, const f4 (&xv)[4], int u, unsigned t, int r, bool live) {
+#pragma clang fp contract(on)
     const int zi = z_index(u), row = zi * Z_RPW + R;
     if (zi >= 0 && row < VD) {
         const float acc = dot_row_h<Q8, 4 * R>(wb, xv);
@@ -696,6 +700,11 @@ __device__ __forceinline__ void z_row(Rs rs, const f4* wb, const f4 (&xv)[4], in
 template <bool Q8, int NR>
 __device__ __forceinline__ bool phase_mix(const Args& a, Rs rs, LayerP w, int L, int p, int u, f4* wb, Lds& l,
                                           int nr) {
+    // Multiply-adds contracted only within one expression: the default also
+    // fuses across statements of a basic block, and the blocks of the
+    // one-row and multi-row mixers differ, so their rounding would too
+    // (every row must equal the one-row step bit for bit).
+#pragma clang fp contract(on)
     // the z rows read the layer input and its norm weights as DIN staged them
     // (parity of phase p - 1): the block writes that buffer again only after
     // the barrier that follows this phase, so the phase needs neither a
@@ -891,7 +900,7 @@ __device__ __forceinline__ bool phase_dout(const Args& a, Rs rs, LayerP w, int L
                                            int nr) {
     const int par = p & 1;
     {
-        const unsigned th = unsigned(thread_id());
+        const unsigned th = unsigned(thread_id<NR>());
         const f4 nw = ldp4(rsrc(w->norm_w), 16u * (th & 31), 0);
         const unsigned want = tag(a, p - 1);
         const unsigned long long start = wall_clock64();
@@ -971,9 +980,8 @@ template <bool Q8, int NR>
 __device__ __forceinline__ bool phase_glu(const Args& a, Rs rs, LayerP w, int p, int u, f4* wb, Lds& l, int nr) {
     const int par = p & 1;
     stage_norm(w->post_norm, par, l);
-    stage_tagged<NR * H>(a, rs, SOFF(after), tag(a, p - 1), l.act[par], l, p,
-                                   [&] { prefetch_glu<Q8>(w, u, wb, 1); },
-                         nr * (H / 2));
+    stage_tagged<NR * H, NR>(a, rs, SOFF(after), tag(a, p - 1), l.act[par], l, p,
+                             [&] { prefetch_glu<Q8>(w, u, wb, 1); }, nr * (H / 2));
     if (!bsync(l, p)) return false;
     const int row0 = glu_first<Q8>(u, !w->attention);
     if (row0 >= I) return true;
@@ -1003,7 +1011,7 @@ template <bool Q8, int NR>
 __device__ __forceinline__ bool phase_down(const Args& a, Rs rs, LayerP w, LayerP next, int p, int u, f4* wb, Lds& l,
                                            int nr) {
     const int par = p & 1;
-    stage_tagged<NR * I>(
+    stage_tagged<NR * I, NR>(
         a, rs, SOFF(product), tag(a, p - 1), l.act[par], l, p,
         [&] {
             prefetch_row<Q8, I, 1>(w->down, u, H, wb);
@@ -1455,8 +1463,7 @@ __device__ __forceinline__ bool phase_comb(const Args& a, Rs rs, int p, int u, L
 template <bool Q8, int NR>
 __device__ __forceinline__ bool phase_o(const Args& a, Rs rs, int L, int p, int u, const f4* wb, Lds& l, int nr) {
     const int par = p & 1;
-    stage_tagged<NR * NH * HD>(a, rs, SOFF(ctx), tag(a, p - 1), l.act[par], l, p, NoMid(),
-                                         nr * (NH * HD / 2));
+    stage_tagged<NR * NH * HD, NR>(a, rs, SOFF(ctx), tag(a, p - 1), l.act[par], l, p, NoMid(), nr * (NH * HD / 2));
     if (!bsync(l, p)) return false;
     if (u >= H) return true;
 #pragma unroll
@@ -1624,7 +1631,7 @@ template <bool Q8, int NR>
 __device__ __forceinline__ bool phase_lm(const Args& a, Rs rs, int p, int u, f4* wb, Lds& l, int nr) {
     const int par = p & 1;
     stage_norm(a.final_norm, par, l);
-    stage_tagged<NR * H>(a, rs, SOFF(x), tag(a, p - 1), l.act[par], l, p, NoMid(), nr * (H / 2));
+    stage_tagged<NR * H, NR>(a, rs, SOFF(x), tag(a, p - 1), l.act[par], l, p, NoMid(), nr * (H / 2));
     if (!bsync(l, p)) return false;
     // the normalised input(s): registers (one-row steps, and the rows of
     // int8 multi-row steps), else LDS (xn, row t normalised once by wave t)
@@ -1713,7 +1720,7 @@ __device__ __forceinline__ void phase_arg(const Args& a, Rs rs, int p, Lds& l, i
     f2 vi[K], b2[K];
 #pragma unroll
     for (int k = 0; k < K; ++k) {
-        po[k] = SROW(lmpart, row) + unsigned(thread_id() + THREADS * k) * 32u;
+        po[k] = SROW(lmpart, row) + unsigned(int(threadIdx.x) + THREADS * k) * 32u;
         live[k] = true;
         b2[k] = ldx2(rs, po[k] + 16u);
     }
