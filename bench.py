@@ -17,6 +17,7 @@ and speculative generation (n-gram and known-continuation drafts) against
 plain greedy (--no-spec skips); decode at ctx 8192 after a real 8192-token
 prefill (config 4; --no-long skips); int8 decode at ctx 454, its 4-row
 verify with snapshots and speculative rates (config 5; --no-int8 skips);
+BF16 decode at ctx 454 on the BF16-rounded weights (--no-bf16 skips);
 the drop-in rates (an unmodified reference engine: the op
 sequence of bridge calls, no one-launch step or fp32 fusions, prefill in
 128-token chunks; --no-dropin skips). roofline: the one-launch decode kernel
@@ -217,6 +218,8 @@ def main():
                     help="skip the int8 decode and 4-row verify at ctx 454 (config 5)")
     ap.add_argument("--no-spec", dest="spec", action="store_false",
                     help="skip the speculative-generation rates (fp32, and int8 with config 5)")
+    ap.add_argument("--no-bf16", dest="bf16", action="store_false",
+                    help="skip the BF16 decode (the model's weights rounded to BF16, every matrix uploaded as BF16)")
     ap.add_argument("--no-dropin", dest="dropin", action="store_false",
                     help="skip the drop-in (unmodified reference engine call sequence) rates")
     ap.add_argument("--cpu-steps", type=int, default=4,
@@ -410,6 +413,33 @@ def main():
         out["decode_8192_weight_read_frac"] = round(weight_bytes * 64 / dt / 1e9 / HBM_PEAK_GBS, 4)
         log(f"decode @8192: {dt / 64 * 1e3:.3f} ms/token, {long_bytes * 64 / dt / 1e9:.0f} GB/s algorithmic")
         r3.close()
+
+    if args.bf16:
+        # The reference's deployed precision: the same model with every tensor
+        # rounded to BF16 and every matrix (the tied LM head included) uploaded
+        # as packed BF16, decode at ctx 454 (the one-launch step when the
+        # bridge accepts the all-BF16 plan).
+        wb = M.bf16_weights(w)
+        mb = E.Model(wb, fmt=E.BF16_EXACT)
+        mb.set_run_budget(64 << 30)
+        rb = mb.new_run(args.prompt + 80, chunk=args.prompt)
+        tok = int(np.argmax(rb.prefill(prompt)))
+        for _ in range(2):
+            tok = rb.step_greedy(tok)
+        mb.sync()
+        t = time.perf_counter()
+        rb.decode_greedy(tok, 65)
+        dt = time.perf_counter() - t
+        bf16_bytes = weight_bytes // 2
+        out["bf16_decode_454_tok_s"] = round(64 / dt, 2)
+        out["bf16_decode_one_launch"] = bool(rb.decode_plan)
+        out["bf16_weight_bytes_per_token"] = bf16_bytes
+        out["bf16_hbm_weight_read_frac"] = round(bf16_bytes * 64 / dt / 1e9 / HBM_PEAK_GBS, 4)
+        log(f"BF16 decode @454: {dt / 64 * 1e3:.3f} ms/token, {bf16_bytes * 64 / dt / 1e9:.0f} GB/s of BF16 weights "
+            f"(one-launch: {rb.decode_plan})")
+        rb.close()
+        mb.close()
+        del wb
 
     if args.int8:
         # Config 5: int8 per-row weights (quantised on the host by the engine, as the

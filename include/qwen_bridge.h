@@ -196,9 +196,12 @@ typedef struct QrDecodeDesc {
     float* logits;           /* [vocab] */
     float* picks;            /* [2] */
     const QrDecodeLayer* layer;
-    /* Matrix format of every layer matrix and of lm_head: QR_DECODE_F32 or
-     * QR_DECODE_INT8 (the reference's upload_int8 packing, src/device.rs:550-561:
-     * rows fp32 scales, then the int8 values row-major, four to a word). */
+    /* Matrix format of every layer matrix and of lm_head: QR_DECODE_F32,
+     * QR_DECODE_BF16 (the reference's upload_bf16_bits packing,
+     * src/device.rs:535-549: two to a word, element 2i in the low half; a
+     * tied LM head is the BF16 embedding table) or QR_DECODE_INT8 (the
+     * reference's upload_int8 packing, src/device.rs:550-561: rows fp32
+     * scales, then the int8 values row-major, four to a word). */
     int32_t weights;
     int32_t embedding_bf16;  /* embedding is packed BF16 (element 2i in the low half of word i) */
     /* Rows of `logits` ([rows, vocab]) and `picks` ([rows, 2]) a launch may
@@ -207,7 +210,7 @@ typedef struct QrDecodeDesc {
      * state + s * n, the layout of the ops' snapshot mode). */
     int32_t rows, snapshots;
 } QrDecodeDesc;
-enum { QR_DECODE_F32 = 0, QR_DECODE_INT8 = 2 };
+enum { QR_DECODE_F32 = 0, QR_DECODE_BF16 = 1, QR_DECODE_INT8 = 2 };
 typedef struct QrDecodePlan QrDecodePlan;
 /* Non-zero (with qr_error set) when this bridge has no one-launch decode for the shape. */
 int qr_decode_plan(Context* c, const QrDecodeDesc* d, QrDecodePlan** out);

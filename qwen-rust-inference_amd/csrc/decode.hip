@@ -79,6 +79,11 @@ constexpr int MAXPH = 6 * 64 + 2;
 // Rows of a multi-row step (decode_rows_kernel: a verify pass of up to NRMAX
 // consecutive tokens with the weights read once).
 constexpr int NRMAX = 4;
+// Matrix formats (the W template parameter): fp32; BF16 packed two to a word
+// (element 2i in the low half, the reference's upload_bf16_bits,
+// src/device.rs:535-549); int8 per-row (the reference's upload_int8,
+// src/device.rs:550-561).
+constexpr int WF32 = 0, WB16 = 1, WQ8 = 2;
 constexpr int DIN_RPW = 4, GLU_RPW = 2, AQKV_RPW = 3, Z_RPW = 2;
 // DeltaNet layers: units >= early_u (fp32: waves 6 and 7 of every block,
 // int8: waves 4-7) have no DOUT row; they take GLU rows 0 .. (NW - early_u)
@@ -86,9 +91,9 @@ constexpr int DIN_RPW = 4, GLU_RPW = 2, AQKV_RPW = 3, Z_RPW = 2;
 // rows are summed (the other GLU rows go to units from 0 on, loaded at the
 // usual time). Measured best: fp32 two waves per CU (four: +4 us per token,
 // none: +9), int8 four (none: +9 us).
-template <bool Q8>
+template <int W>
 __device__ __forceinline__ constexpr int early_u() {
-    return Q8 ? 4 * BLOCKS : 6 * BLOCKS;
+    return W == WF32 ? 6 * BLOCKS : 4 * BLOCKS;
 }
 constexpr int MIX_WAVES = VH * 8;  // 16 value columns per wave
 constexpr int COMB_WAVES = NH * (HD / 4);
@@ -429,7 +434,7 @@ __device__ __forceinline__ void stage_norm(const float* w, int par, Lds& l) {
 // The layer's input residual into l.act[par]: the token's embedding row for
 // layer 0 (BF16 tables only with int8 matrices, as the reference's int8
 // upload keeps the embedding BF16), else x as written by phase `producer`.
-template <bool Q8, int NR, class Mid = NoMid>
+template <int W, int NR, class Mid = NoMid>
 __device__ __forceinline__ void stage_input(const Args& a, Rs rs, int L, int producer, int par, Lds& l, int p, int nr,
                                             Mid&& mid = Mid()) {
     if (L == 0) {
@@ -439,7 +444,7 @@ __device__ __forceinline__ void stage_input(const Args& a, Rs rs, int L, int pro
             if (r >= nr) break;
             const int t = int(threadIdx.x);
             float* dst = &l.act[par][r * H];
-            if (Q8 && a.emb_bf16) {
+            if (W != WF32 && a.emb_bf16) {
                 if (t < H / 8) {
                     const f4 wv = ldp4(rsrc(a.embedding), unsigned(l.token[r]) * unsigned(H * 2) + 16u * unsigned(t), 0);
 #pragma unroll
@@ -462,19 +467,29 @@ __device__ __forceinline__ void stage_input(const Args& a, Rs rs, int L, int pro
 // (reference.h:120-126). fp32 rows: xv[v] holds elements 4 (lane + 64 v) .. +3;
 // int8 rows: elements 16 lane + 4 v .. +3 (the 16 columns of the lane's
 // 16-byte weight entry).
-template <bool Q8>
+// Staged-vector element of chunk v (0..3) of `lane`: the columns a lane's
+// 16-byte weight entries cover, in entry order (fp32: 4 columns per entry,
+// entry v at 4 (lane + 64 v); BF16: 8 per entry, entry e at 8 (lane + 64 e),
+// chunks 2e and 2e + 1 its halves; int8: one entry of 16 at 16 lane).
+template <int W>
+__device__ __forceinline__ constexpr unsigned xcol(unsigned lane, int v) {
+    return W == WQ8    ? 16 * lane + 4 * v
+           : W == WB16 ? 8 * (lane + 64 * unsigned(v >> 1)) + 4 * unsigned(v & 1)
+                       : 4 * (lane + 64 * v);
+}
+template <int W>
 __device__ __forceinline__ void normed_chunks(const Lds& l, int par, float eps, f4 (&xv)[4], int row = 0) {
     const unsigned lane = lane_id();
     float ss = 0.f;
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
-        xv[v] = lds4(&l.act[par][row * H + (Q8 ? 16 * lane + 4 * v : 4 * (lane + 64 * v))]);
+        xv[v] = lds4(&l.act[par][row * H + xcol<W>(lane, v)]);
         ss += dot4(xv[v], xv[v]);
     }
     ss = wave_total(ss);
     const float r = 1.f / sqrtf(ss / float(H) + eps);
 #pragma unroll
-    for (int v = 0; v < 4; ++v) xv[v] = (xv[v] * r) * lds4(&l.nw[par][Q8 ? 16 * lane + 4 * v : 4 * (lane + 64 * v)]);
+    for (int v = 0; v < 4; ++v) xv[v] = (xv[v] * r) * lds4(&l.nw[par][xcol<W>(lane, v)]);
 }
 // Value e (0..3) of a word of packed int8.
 __device__ __forceinline__ float q8v(unsigned w, int e) { return float(int(w << (24 - 8 * e)) >> 24); }
@@ -488,16 +503,35 @@ __device__ __forceinline__ float q8dot(f4 w, const f4 (&x)[4], float acc) {
     }
     return acc;
 }
-// Row `r` of an [rows, H] matrix into wb[AT .. AT + 3]. int8 (packed as the
-// reference's upload_int8, src/device.rs:550-561: `rows` fp32 scales, then the
-// values row-major): the row's 1 KiB in wb[AT] (columns 16 lane .. +15) and
-// its scale in wb[AT + 1].x.
-template <bool Q8, int AT, int AUX = kNT>
+// The two BF16 halves of a packed word (element 2i low) as fp32.
+__device__ __forceinline__ float b16lo(unsigned w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float b16hi(unsigned w) { return __uint_as_float(w & 0xffff0000u); }
+// 8 BF16 weights (one 16-byte entry) times 8 activations (x0: the first 4).
+__device__ __forceinline__ float b16dot(f4 w, f4 x0, f4 x1, float acc) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const unsigned wj = __float_as_uint(w[j]);
+        const f4& x = j < 2 ? x0 : x1;
+        acc = fmaf(b16lo(wj), x[2 * (j & 1)], acc);
+        acc = fmaf(b16hi(wj), x[2 * (j & 1) + 1], acc);
+    }
+    return acc;
+}
+// Row `r` of an [rows, H] matrix into wb[AT .. AT + 3]. BF16: the row's 2 KiB
+// in wb[AT], wb[AT + 1] (columns 8 (lane + 64 e) .. +7 in entry e). int8
+// (packed as the reference's upload_int8, src/device.rs:550-561: `rows` fp32
+// scales, then the values row-major): the row's 1 KiB in wb[AT] (columns
+// 16 lane .. +15) and its scale in wb[AT + 1].x.
+template <int W, int AT, int AUX = kNT>
 __device__ __forceinline__ void load_row_h(f4* wb, Rs m, int r, int rows) {
     const unsigned lo = 16u * lane_id();
-    if constexpr (Q8) {
+    if constexpr (W == WQ8) {
         wb[AT] = buffer_load_f4(m, lo, unsigned(rows) * 4u + unsigned(r) * unsigned(H), AUX);
         wb[AT + 1] = f4{ldp(m, unsigned(r) * 4u), 0.f, 0.f, 0.f};
+    } else if constexpr (W == WB16) {
+        const unsigned row = unsigned(r) * unsigned(H * 2);
+#pragma unroll
+        for (int e = 0; e < 2; ++e) wb[AT + e] = buffer_load_f4(m, lo + 1024u * e, row, AUX);
     } else {
         const unsigned row = unsigned(r) * unsigned(H * 4);
 #pragma unroll
@@ -505,21 +539,32 @@ __device__ __forceinline__ void load_row_h(f4* wb, Rs m, int r, int rows) {
     }
 }
 // int8: scale * sum(q x), the scale after the sum (reference bridge.cpp:620-653).
-template <bool Q8, int AT>
+template <int W, int AT>
 __device__ __forceinline__ float dot_row_h(const f4* wb, const f4 (&xv)[4]) {
     float acc = 0.f;
-    if constexpr (Q8) return wb[AT + 1].x * wave_total(q8dot(wb[AT], xv, acc));
+    if constexpr (W == WQ8) return wb[AT + 1].x * wave_total(q8dot(wb[AT], xv, acc));
+    if constexpr (W == WB16) return wave_total(b16dot(wb[AT + 1], xv[2], xv[3], b16dot(wb[AT], xv[0], xv[1], acc)));
 #pragma unroll
     for (int v = 0; v < 4; ++v) acc = fdot4(wb[AT + v], xv[v], acc);
     return wave_total(acc);
 }
-// Dot of a prefetched row of K * 256 columns with the staged vector (int8: the
+// Dot of a prefetched row of K * 256 columns with the staged vector (BF16:
+// K / 2 entries of 8 columns per lane, entry v at 512 v + 8 lane; int8: the
 // row in ceil(K / 4) entries of 16 columns per lane, its scale after them).
-template <bool Q8, int K>
+template <int W, int K>
 __device__ __forceinline__ float dot_row_lds(const f4* wb, const float* act) {
     const unsigned lane = lane_id();
     float acc = 0.f;
-    if constexpr (Q8) {
+    if constexpr (W == WB16) {
+        static_assert(K % 2 == 0, "BF16 rows: whole 512-column entries");
+#pragma unroll
+        for (int v = 0; v < K / 2; ++v) {
+            const unsigned c0 = 512u * v + 8u * lane;
+            acc = b16dot(wb[v], lds4(act + c0), lds4(act + c0 + 4), acc);
+        }
+        return wave_total(acc);
+    }
+    if constexpr (W == WQ8) {
         constexpr int NV = (K + 3) / 4;
 #pragma unroll
         for (int v = 0; v < NV; ++v) {
@@ -544,39 +589,39 @@ __device__ __forceinline__ float dot_row_lds(const f4* wb, const float* act) {
 // ---- T_DIN: qkv | a | b rows of a DeltaNet layer (z rows: phase T_MIX), then
 // the causal conv + SiLU of each qkv channel (reference.h:96-116): the wave
 // computing a channel's row is the only one touching its history.
-template <bool Q8, int R, int AUX = kNT>
+template <int W, int R, int AUX = kNT>
 __device__ __forceinline__ void din_load(LayerP w, int u, f4* wb) {
     const int row = u * DIN_RPW + R;
     if (row < CH)
-        load_row_h<Q8, 4 * R, AUX>(wb, rsrc(w->qkv), row, CH);
+        load_row_h<W, 4 * R, AUX>(wb, rsrc(w->qkv), row, CH);
     else if (row < CH + VH)
-        load_row_h<Q8, 4 * R, AUX>(wb, rsrc(w->a), row - CH, VH);
+        load_row_h<W, 4 * R, AUX>(wb, rsrc(w->a), row - CH, VH);
     else if (row < DIN_ROWS)
-        load_row_h<Q8, 4 * R, AUX>(wb, rsrc(w->b), row - CH - VH, VH);
+        load_row_h<W, 4 * R, AUX>(wb, rsrc(w->b), row - CH - VH, VH);
 }
 // Weights of the heavier phases are fetched in two parts: part 0 after the
 // previous phase, part 1 after the phase's own first polls (so the polls are
 // not queued behind all of it).
-template <bool Q8, int AUX = kNT>
+template <int W, int AUX = kNT>
 __device__ __forceinline__ void prefetch_din(LayerP w, int u, f4* wb, int part) {
     if (part == 0) {
-        din_load<Q8, 0, AUX>(w, u, wb);
-        din_load<Q8, 1, AUX>(w, u, wb);
+        din_load<W, 0, AUX>(w, u, wb);
+        din_load<W, 1, AUX>(w, u, wb);
     } else {
-        din_load<Q8, 2>(w, u, wb);
-        din_load<Q8, 3>(w, u, wb);
+        din_load<W, 2>(w, u, wb);
+        din_load<W, 3>(w, u, wb);
     }
 }
-template <bool Q8, int R>
+template <int W, int R>
 __device__ __forceinline__ void din_row(const f4* wb, const f4 (&xv)[4], int u, float& mine) {
     if (u * DIN_RPW + R < DIN_ROWS) {
-        const float acc = dot_row_h<Q8, 4 * R>(wb, xv);
+        const float acc = dot_row_h<W, 4 * R>(wb, xv);
         if (lane_id() == R) mine = acc;
     }
 }
 // The rows of a multi-row step run through the channel's history in order
 // (the history after row r is row r's snapshot).
-template <bool Q8, int NR>
+template <int W, int NR>
 __device__ __forceinline__ bool phase_din(const Args& a, Rs rs, LayerP w, int L, int p, int u, f4* wb, Lds& l, int nr) {
     const int par = p & 1;
     const int lane = int(lane_id()), row = u * DIN_RPW + lane;
@@ -591,7 +636,7 @@ __device__ __forceinline__ bool phase_din(const Args& a, Rs rs, LayerP w, int L,
         c0 = ldp(cw, co), c1 = ldp(cw, co + 4), c2 = ldp(cw, co + 8), c3 = ldp(cw, co + 12);
     }
     stage_norm(w->input_norm, par, l);
-    stage_input<Q8, NR>(a, rs, L, p - 1, par, l, p, nr, [&] { prefetch_din<Q8>(w, u, wb, 1); });
+    stage_input<W, NR>(a, rs, L, p - 1, par, l, p, nr, [&] { prefetch_din<W>(w, u, wb, 1); });
     if (!bsync(l, p)) return false;
     if (u * DIN_RPW >= DIN_ROWS) return true;
     float mine[NR];  // lane r: the dot product of row u * DIN_RPW + r, per step row
@@ -599,11 +644,11 @@ __device__ __forceinline__ bool phase_din(const Args& a, Rs rs, LayerP w, int L,
     for (int r = 0; r < NR; ++r) {  // every row computed (rows >= nr unused): no branch between the rows' chains
         mine[r] = 0.f;
         f4 xv[4];
-        normed_chunks<Q8>(l, par, a.eps, xv, r);
-        din_row<Q8, 0>(wb, xv, u, mine[r]);
-        din_row<Q8, 1>(wb, xv, u, mine[r]);
-        din_row<Q8, 2>(wb, xv, u, mine[r]);
-        din_row<Q8, 3>(wb, xv, u, mine[r]);
+        normed_chunks<W>(l, par, a.eps, xv, r);
+        din_row<W, 0>(wb, xv, u, mine[r]);
+        din_row<W, 1>(wb, xv, u, mine[r]);
+        din_row<W, 2>(wb, xv, u, mine[r]);
+        din_row<W, 3>(wb, xv, u, mine[r]);
     }
     const unsigned t = tag(a, p);
     if (conv) {
@@ -663,16 +708,16 @@ __device__ __forceinline__ int z_index(int u) {
     const int b = u % BLOCKS;
     return b >= MIX_WAVES ? (u / BLOCKS) * (BLOCKS - MIX_WAVES) + (b - MIX_WAVES) : -1;
 }
-template <bool Q8, int R>
+template <int W, int R>
 __device__ __forceinline__ void z_load(LayerP w, int u, f4* wb) {
     const int zi = z_index(u), row = zi * Z_RPW + R;
-    if (zi >= 0 && row < VD) load_row_h<Q8, 4 * R>(wb, rsrc(w->z), row, VD);
+    if (zi >= 0 && row < VD) load_row_h<W, 4 * R>(wb, rsrc(w->z), row, VD);
 }
-template <bool Q8>
+template <int W>
 __device__ __forceinline__ void prefetch_mix(LayerP w, int u, f4* wb) {
     if (u >= MIX_WAVES) {
-        z_load<Q8, 0>(w, u, wb);
-        z_load<Q8, 1>(w, u, wb);
+        z_load<W, 0>(w, u, wb);
+        z_load<W, 1>(w, u, wb);
         return;
     }
     // state S[h][i][j] (key row i, value column j), rows p*32 .. p*32+31 of column j
@@ -686,18 +731,18 @@ __device__ __forceinline__ void prefetch_mix(LayerP w, int u, f4* wb) {
         wb[k] = f4{ldp(S, o), ldp(S, o + DV * 4u), ldp(S, o + 2u * DV * 4u), ldp(S, o + 3u * DV * 4u)};
     }
 }
-template <bool Q8, int R>
+template <int W, int R>
 __device__ __forceinline__ void z_row(Rs rs, const f4* wb, const f4 (&xv)[4], int u, unsigned t, int r, bool live) {
 #pragma clang fp contract(on)
     const int zi = z_index(u), row = zi * Z_RPW + R;
     if (zi >= 0 && row < VD) {
-        const float acc = dot_row_h<Q8, 4 * R>(wb, xv);
+        const float acc = dot_row_h<W, 4 * R>(wb, xv);
         if (lane_id() == 0 && live) stt(rs, SROW(z, r) + 8u * unsigned(row), silu(acc), t);
     }
 }
 // The delta-rule waves walk the rows of a multi-row step in order, the state
 // staying in their registers (row r's state is its snapshot).
-template <bool Q8, int NR>
+template <int W, int NR>
 __device__ __forceinline__ bool phase_mix(const Args& a, Rs rs, LayerP w, int L, int p, int u, f4* wb, Lds& l,
                                           int nr) {
     // Multiply-adds contracted only within one expression: the default also
@@ -717,9 +762,9 @@ __device__ __forceinline__ bool phase_mix(const Args& a, Rs rs, LayerP w, int L,
 #pragma unroll
         for (int r = 0; r < NR; ++r) {
             f4 xv[4];
-            normed_chunks<Q8>(l, par, a.eps, xv, r);
-            z_row<Q8, 0>(rs, wb, xv, u, t, r, r < nr);
-            z_row<Q8, 1>(rs, wb, xv, u, t, r, r < nr);
+            normed_chunks<W>(l, par, a.eps, xv, r);
+            z_row<W, 0>(rs, wb, xv, u, t, r, r < nr);
+            z_row<W, 1>(rs, wb, xv, u, t, r, r < nr);
         }
         return true;
     }
@@ -871,14 +916,20 @@ __device__ __forceinline__ bool phase_mix(const Args& a, Rs rs, LayerP w, int L,
 // 4t .. 4t+3, its head's 32 threads reduce the sum of squares; in the upper
 // half of the phase's buffer, whose lower half still holds the layer input as
 // DIN staged it), then out_proj row u plus that residual.
-// PART -1: the whole row; 0 / 1: the first / second half of an fp32 row
-// (int8: part 0 is the whole row).
-template <bool Q8, int COLS, int PART = -1, int AUX = kNT>
+// PART -1: the whole row; 0 / 1: the first / second half of an fp32 or BF16
+// row's entries (int8: part 0 is the whole row).
+template <int W, int COLS, int PART = -1, int AUX = kNT>
 __device__ __forceinline__ void prefetch_row(const float* m, int row, int rows, f4* wb) {
     if (row >= rows) return;
     const Rs r = rsrc(m);
     const unsigned lo = 16u * lane_id();
-    if constexpr (Q8) {
+    if constexpr (W == WB16) {
+        static_assert(COLS % 512 == 0, "BF16 rows: whole 512-column entries");
+        constexpr int NB = COLS / 512, V0 = PART == 1 ? NB / 2 : 0, V1 = PART == 0 ? NB / 2 : NB;
+        const unsigned ro = unsigned(row) * unsigned(COLS * 2);
+#pragma unroll
+        for (int v = V0; v < V1; ++v) wb[v] = buffer_load_f4(r, lo + 1024u * v, ro, AUX);
+    } else if constexpr (W == WQ8) {
         if (PART == 1) return;
         constexpr int NV = (COLS + 1023) / 1024;
         const unsigned ro = unsigned(rows) * 4u + unsigned(row) * unsigned(COLS);
@@ -893,9 +944,9 @@ __device__ __forceinline__ void prefetch_row(const float* m, int row, int rows, 
         for (int v = V0; v < V1; ++v) wb[v] = buffer_load_f4(r, lo + 1024u * v, ro, AUX);
     }
 }
-template <bool Q8, int R, int AUX>
+template <int W, int R, int AUX>
 __device__ __forceinline__ void glu_load(LayerP w, int u, f4* wb);
-template <bool Q8, int NR>
+template <int W, int NR>
 __device__ __forceinline__ bool phase_dout(const Args& a, Rs rs, LayerP w, int L, int p, int u, f4* wb, Lds& l,
                                            int nr) {
     const int par = p & 1;
@@ -928,15 +979,15 @@ __device__ __forceinline__ bool phase_dout(const Args& a, Rs rs, LayerP w, int L
     }
     if (!bsync(l, p)) return false;
     if (u >= H) {
-        if (u >= early_u<Q8>()) {  // this unit's GLU rows, both parts, while DOUT's rows are summed
-            glu_load<Q8, 0, Q8 ? 0 : kNT>(w, u, wb);  // int8: part 0 stays in the memory-side cache
-            glu_load<Q8, 1, kNT>(w, u, wb);
+        if (u >= early_u<W>()) {  // this unit's GLU rows, both parts, while DOUT's rows are summed
+            glu_load<W, 0, W == WQ8 ? 0 : kNT>(w, u, wb);  // int8: part 0 stays in the memory-side cache
+            glu_load<W, 1, kNT>(w, u, wb);
         }
         return true;
     }
 #pragma unroll
     for (int r = 0; r < NR; ++r) {
-        const float acc = dot_row_lds<Q8, VD / 256>(wb, l.act[par] + gated_off<NR>() + r * VD);
+        const float acc = dot_row_lds<W, VD / 256>(wb, l.act[par] + gated_off<NR>() + r * VD);
         const float res = l.act[par][r * H + u];  // the layer input as DIN (phase p - 2) staged it
         if (lane_id() == 0 && r < nr) stt(rs, SROW(after, r) + 8u * unsigned(u), res + acc, tag(a, p));
     }
@@ -945,52 +996,52 @@ __device__ __forceinline__ bool phase_dout(const Args& a, Rs rs, LayerP w, int L
 
 // ---- T_GLU: product = silu(gate . n) * (up . n), n = post RMSNorm of `after`
 // The first of unit u's GLU_RPW rows (dn: a DeltaNet layer).
-template <bool Q8>
+template <int W>
 __device__ __forceinline__ int glu_first(int u, bool dn) {
     if (!dn) return u * GLU_RPW;
-    constexpr int E = early_u<Q8>(), ER = GLU_RPW * (NW - E);
+    constexpr int E = early_u<W>(), ER = GLU_RPW * (NW - E);
     return u >= E ? (u - E) * GLU_RPW : ER + u * GLU_RPW;
 }
-template <bool Q8, int R, int AUX = kNT>
+template <int W, int R, int AUX = kNT>
 __device__ __forceinline__ void glu_load(LayerP w, int u, f4* wb) {
-    const int row = glu_first<Q8>(u, !w->attention) + R;
+    const int row = glu_first<W>(u, !w->attention) + R;
     if (row < I) {
-        load_row_h<Q8, 8 * R, AUX>(wb, rsrc(w->gate), row, I);
-        load_row_h<Q8, 8 * R + 4, AUX>(wb, rsrc(w->up), row, I);
+        load_row_h<W, 8 * R, AUX>(wb, rsrc(w->gate), row, I);
+        load_row_h<W, 8 * R + 4, AUX>(wb, rsrc(w->up), row, I);
     }
 }
-template <bool Q8, int AUX = kNT>
+template <int W, int AUX = kNT>
 __device__ __forceinline__ void prefetch_glu(LayerP w, int u, f4* wb, int part) {
-    if (!w->attention && u >= early_u<Q8>()) return;  // loaded in DOUT
+    if (!w->attention && u >= early_u<W>()) return;  // loaded in DOUT
     if (part == 0)
-        glu_load<Q8, 0, AUX>(w, u, wb);
+        glu_load<W, 0, AUX>(w, u, wb);
     else
-        glu_load<Q8, 1>(w, u, wb);
+        glu_load<W, 1>(w, u, wb);
 }
-template <bool Q8, int R>
+template <int W, int R>
 __device__ __forceinline__ void glu_row(Rs rs, const f4* wb, const f4 (&xv)[4], int row0, unsigned t, int r,
                                         bool live = true) {
     const int row = row0 + R;
     if (row < I) {
-        const float g = dot_row_h<Q8, 8 * R>(wb, xv), up = dot_row_h<Q8, 8 * R + 4>(wb, xv);
+        const float g = dot_row_h<W, 8 * R>(wb, xv), up = dot_row_h<W, 8 * R + 4>(wb, xv);
         if (lane_id() == 0 && live) stt(rs, SROW(product, r) + 8u * unsigned(row), silu(g) * up, t);
     }
 }
-template <bool Q8, int NR>
+template <int W, int NR>
 __device__ __forceinline__ bool phase_glu(const Args& a, Rs rs, LayerP w, int p, int u, f4* wb, Lds& l, int nr) {
     const int par = p & 1;
     stage_norm(w->post_norm, par, l);
     stage_tagged<NR * H, NR>(a, rs, SOFF(after), tag(a, p - 1), l.act[par], l, p,
-                             [&] { prefetch_glu<Q8>(w, u, wb, 1); }, nr * (H / 2));
+                             [&] { prefetch_glu<W>(w, u, wb, 1); }, nr * (H / 2));
     if (!bsync(l, p)) return false;
-    const int row0 = glu_first<Q8>(u, !w->attention);
+    const int row0 = glu_first<W>(u, !w->attention);
     if (row0 >= I) return true;
 #pragma unroll
     for (int r = 0; r < NR; ++r) {
         f4 xv[4];
-        normed_chunks<Q8>(l, par, a.eps, xv, r);
-        glu_row<Q8, 0>(rs, wb, xv, row0, tag(a, p), r, r < nr);
-        glu_row<Q8, 1>(rs, wb, xv, row0, tag(a, p), r, r < nr);
+        normed_chunks<W>(l, par, a.eps, xv, r);
+        glu_row<W, 0>(rs, wb, xv, row0, tag(a, p), r, r < nr);
+        glu_row<W, 1>(rs, wb, xv, row0, tag(a, p), r, r < nr);
     }
     return true;
 }
@@ -1007,14 +1058,14 @@ __device__ __forceinline__ void touch_record(LayerP w) {
     asm volatile("" ::"s"(x0), "s"(x1), "s"(x2), "s"(x3));
 }
 // ---- T_DOWN: x = after + down . product
-template <bool Q8, int NR>
+template <int W, int NR>
 __device__ __forceinline__ bool phase_down(const Args& a, Rs rs, LayerP w, LayerP next, int p, int u, f4* wb, Lds& l,
                                            int nr) {
     const int par = p & 1;
     stage_tagged<NR * I, NR>(
         a, rs, SOFF(product), tag(a, p - 1), l.act[par], l, p,
         [&] {
-            prefetch_row<Q8, I, 1>(w->down, u, H, wb);
+            prefetch_row<W, I, 1>(w->down, u, H, wb);
             if (next) touch_record(next);
         },
         nr * (I / 2));
@@ -1022,7 +1073,7 @@ __device__ __forceinline__ bool phase_down(const Args& a, Rs rs, LayerP w, Layer
     if (u >= H) return true;
 #pragma unroll
     for (int r = 0; r < NR; ++r) {
-        const float acc = dot_row_lds<Q8, I / 256>(wb, l.act[par] + r * I);
+        const float acc = dot_row_lds<W, I / 256>(wb, l.act[par] + r * I);
         const float res = l.act[par ^ 1][r * H + u];  // `after` as GLU (phase p - 1) staged it
         if (lane_id() == 0 && r < nr) stt(rs, SROW(x, r) + 8u * unsigned(u), res + acc, tag(a, p));
     }
@@ -1030,31 +1081,31 @@ __device__ __forceinline__ bool phase_down(const Args& a, Rs rs, LayerP w, Layer
 }
 
 // ---- T_AQKV: q ([Q | gate] per head), k, v rows of an attention layer
-template <bool Q8, int R, int AUX = kNT>
+template <int W, int R, int AUX = kNT>
 __device__ __forceinline__ void aqkv_load(LayerP w, int u, f4* wb) {
     const int row = u * AQKV_RPW + R;
     if (row < QROWS)
-        load_row_h<Q8, 4 * R, AUX>(wb, rsrc(w->q), row, QROWS);
+        load_row_h<W, 4 * R, AUX>(wb, rsrc(w->q), row, QROWS);
     else if (row < QROWS + KVR)
-        load_row_h<Q8, 4 * R, AUX>(wb, rsrc(w->k), row - QROWS, KVR);
+        load_row_h<W, 4 * R, AUX>(wb, rsrc(w->k), row - QROWS, KVR);
     else if (row < AQKV_ROWS)
-        load_row_h<Q8, 4 * R, AUX>(wb, rsrc(w->v), row - QROWS - KVR, KVR);
+        load_row_h<W, 4 * R, AUX>(wb, rsrc(w->v), row - QROWS - KVR, KVR);
 }
-template <bool Q8, int AUX = kNT>
+template <int W, int AUX = kNT>
 __device__ __forceinline__ void prefetch_aqkv(LayerP w, int u, f4* wb, int part) {
     if (part == 0) {
-        aqkv_load<Q8, 0, AUX>(w, u, wb);
-        aqkv_load<Q8, 1, AUX>(w, u, wb);
+        aqkv_load<W, 0, AUX>(w, u, wb);
+        aqkv_load<W, 1, AUX>(w, u, wb);
     } else {
-        aqkv_load<Q8, 2>(w, u, wb);
+        aqkv_load<W, 2>(w, u, wb);
     }
 }
-template <bool Q8, int R>
+template <int W, int R>
 __device__ __forceinline__ void aqkv_row(Rs rs, const f4* wb, const f4 (&xv)[4], int u, unsigned t, int r,
                                          bool live = true) {
     const int row = u * AQKV_RPW + R;
     if (row < AQKV_ROWS) {
-        const float acc = dot_row_h<Q8, 4 * R>(wb, xv);
+        const float acc = dot_row_h<W, 4 * R>(wb, xv);
         if (lane_id() == 0 && live) {
             const unsigned dst = row < QROWS ? SROW(mixed, r) + 8u * unsigned(row)
                                  : row < QROWS + KVR ? SROW(key, r) + 8u * unsigned(row - QROWS)
@@ -1063,21 +1114,21 @@ __device__ __forceinline__ void aqkv_row(Rs rs, const f4* wb, const f4 (&xv)[4],
         }
     }
 }
-template <bool Q8, int NR>
+template <int W, int NR>
 __device__ __forceinline__ bool phase_aqkv(const Args& a, Rs rs, LayerP w, int L, int p, int u, f4* wb, Lds& l,
                                            int nr) {
     const int par = p & 1;
     stage_norm(w->input_norm, par, l);
-    stage_input<Q8, NR>(a, rs, L, p - 1, par, l, p, nr, [&] { prefetch_aqkv<Q8>(w, u, wb, 1); });
+    stage_input<W, NR>(a, rs, L, p - 1, par, l, p, nr, [&] { prefetch_aqkv<W>(w, u, wb, 1); });
     if (!bsync(l, p)) return false;
     if (u * AQKV_RPW >= AQKV_ROWS) return true;
 #pragma unroll
     for (int r = 0; r < NR; ++r) {
         f4 xv[4];
-        normed_chunks<Q8>(l, par, a.eps, xv, r);
-        aqkv_row<Q8, 0>(rs, wb, xv, u, tag(a, p), r, r < nr);
-        aqkv_row<Q8, 1>(rs, wb, xv, u, tag(a, p), r, r < nr);
-        aqkv_row<Q8, 2>(rs, wb, xv, u, tag(a, p), r, r < nr);
+        normed_chunks<W>(l, par, a.eps, xv, r);
+        aqkv_row<W, 0>(rs, wb, xv, u, tag(a, p), r, r < nr);
+        aqkv_row<W, 1>(rs, wb, xv, u, tag(a, p), r, r < nr);
+        aqkv_row<W, 2>(rs, wb, xv, u, tag(a, p), r, r < nr);
     }
     return true;
 }
@@ -1460,7 +1511,7 @@ __device__ __forceinline__ bool phase_comb(const Args& a, Rs rs, int p, int u, L
 }
 
 // ---- T_O: after = x + o . ctx
-template <bool Q8, int NR>
+template <int W, int NR>
 __device__ __forceinline__ bool phase_o(const Args& a, Rs rs, int L, int p, int u, const f4* wb, Lds& l, int nr) {
     const int par = p & 1;
     stage_tagged<NR * NH * HD, NR>(a, rs, SOFF(ctx), tag(a, p - 1), l.act[par], l, p, NoMid(), nr * (NH * HD / 2));
@@ -1468,7 +1519,7 @@ __device__ __forceinline__ bool phase_o(const Args& a, Rs rs, int L, int p, int 
     if (u >= H) return true;
 #pragma unroll
     for (int r = 0; r < NR; ++r) {
-        const float acc = dot_row_lds<Q8, NH * HD / 256>(wb, l.act[par] + r * NH * HD);
+        const float acc = dot_row_lds<W, NH * HD / 256>(wb, l.act[par] + r * NH * HD);
         const float res = l.act[par ^ 1][r * H + u];  // the layer input as AQKV (phase p - 3) staged it
         if (lane_id() == 0 && r < nr) stt(rs, SROW(after, r) + 8u * unsigned(u), res + acc, tag(a, p));
     }
@@ -1479,14 +1530,18 @@ __device__ __forceinline__ bool phase_o(const Args& a, Rs rs, int L, int p, int 
 // at a time with the next 4 in flight; per-wave (max, first index,
 // non-finite count).
 constexpr int LM_G = 4;
-template <bool Q8>
+template <int W>
 __device__ __forceinline__ void lm_load(Rs lm, int row0, int row_end, int vocab, f4* buf) {
 #pragma unroll
     for (int r = 0; r < LM_G; ++r)
         if (row0 + r < row_end) {
-            if constexpr (Q8) {
+            if constexpr (W == WQ8) {
                 buf[r * 4] = ldw(lm, 16u * lane_id(), unsigned(vocab) * 4u + unsigned(row0 + r) * unsigned(H));
                 buf[r * 4 + 1] = f4{ldp(lm, unsigned(row0 + r) * 4u), 0.f, 0.f, 0.f};
+            } else if constexpr (W == WB16) {
+                const unsigned lo = 16u * lane_id(), ro = unsigned(row0 + r) * unsigned(H * 2);
+#pragma unroll
+                for (int e = 0; e < 2; ++e) buf[r * 4 + e] = ldw(lm, lo + 1024u * e, ro);
             } else {
                 const unsigned lo = 16u * lane_id(), ro = unsigned(row0 + r) * unsigned(H * 4);
 #pragma unroll
@@ -1514,20 +1569,30 @@ __device__ __forceinline__ void lm_take(Rs lg, float acc, int t, int row, int vo
 // (xv[t]); multi-row fp32 steps walk the inputs in the outer loop, each read
 // once per group from LDS (xn: row t at t H, in the lane layout of
 // normed_chunks). Each input row's maxima are taken in row order.
-template <bool Q8, int NR, int NX>
+template <int W, int NR, int NX>
 __device__ __forceinline__ void lm_rows(Rs lg, const f4* buf, const f4 (&xv)[NX][4], const float* xn, int row0,
                                         int row_end, int vocab, int nr, float (&best)[NR], unsigned (&at)[NR],
                                         unsigned (&bad)[NR]) {
-    if constexpr (NR > 1 && Q8) {
+    if constexpr (NR > 1 && W != WF32) {
 #pragma unroll
         for (int r = 0; r < LM_G; ++r) {
             const int row = row0 + r;
             if (row >= row_end) continue;
-            float wf[16];
+            float wf[16];  // the row's 16 weights of this lane, in the one-row step's order
+            if constexpr (W == WQ8) {
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
+                for (int j = 0; j < 4; ++j)
 #pragma unroll
-                for (int e = 0; e < 4; ++e) wf[4 * j + e] = q8v(__float_as_uint(buf[r * 4][j]), e);
+                    for (int e = 0; e < 4; ++e) wf[4 * j + e] = q8v(__float_as_uint(buf[r * 4][j]), e);
+            } else {
+#pragma unroll
+                for (int e = 0; e < 2; ++e)
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        wf[8 * e + 2 * j] = b16lo(__float_as_uint(buf[r * 4 + e][j]));
+                        wf[8 * e + 2 * j + 1] = b16hi(__float_as_uint(buf[r * 4 + e][j]));
+                    }
+            }
 #pragma unroll
             for (int t = 0; t < NR; ++t) {
                 float acc = 0.f;
@@ -1535,7 +1600,9 @@ __device__ __forceinline__ void lm_rows(Rs lg, const f4* buf, const f4 (&xv)[NX]
                 for (int j = 0; j < 4; ++j)
 #pragma unroll
                     for (int e = 0; e < 4; ++e) acc = fmaf(wf[4 * j + e], xv[t][j][e], acc);
-                lm_take<NR>(lg, buf[r * 4 + 1].x * wave_total(acc), t, row, vocab, nr, best, at, bad);
+                acc = wave_total(acc);
+                if constexpr (W == WQ8) acc = buf[r * 4 + 1].x * acc;
+                lm_take<NR>(lg, acc, t, row, vocab, nr, best, at, bad);
             }
         }
     } else if constexpr (NR > 1) {
@@ -1561,8 +1628,10 @@ __device__ __forceinline__ void lm_rows(Rs lg, const f4* buf, const f4 (&xv)[NX]
             const int row = row0 + r;
             if (row >= row_end) continue;
             float acc = 0.f;
-            if constexpr (Q8) {
+            if constexpr (W == WQ8) {
                 acc = buf[r * 4 + 1].x * wave_total(q8dot(buf[r * 4], xv[0], acc));
+            } else if constexpr (W == WB16) {
+                acc = wave_total(b16dot(buf[r * 4 + 1], xv[0][2], xv[0][3], b16dot(buf[r * 4], xv[0][0], xv[0][1], acc)));
             } else {
 #pragma unroll
                 for (int v = 0; v < 4; ++v) acc = fdot4(buf[r * 4 + v], xv[0][v], acc);
@@ -1582,7 +1651,7 @@ __device__ __forceinline__ void lm_rows(Rs lg, const f4* buf, const f4 (&xv)[NX]
 // blocks in order by a device-wide counter once their range is done (the
 // XCDs stream at different rates, by up to 20 %, and which ones are slow
 // differs from GPU to GPU).
-constexpr int LM_CHUNK = 64, LM_CHUNK_Q8 = 256;  // rows (int8 rows are a quarter of the bytes)
+constexpr int LM_CHUNK = 64, LM_CHUNK_B16 = 128, LM_CHUNK_Q8 = 256;  // rows (BF16 / int8 rows: a half / quarter of the bytes)
 __device__ __forceinline__ int lm_static_rows(int vocab) {
     return vocab / 20 * 17 / (BLOCKS * LM_G) * (BLOCKS * LM_G);
 }
@@ -1591,11 +1660,11 @@ __device__ __forceinline__ void lm_block_range(int u, int vocab, int& first, int
     first = (u % BLOCKS) * rb;
     last = first + rb;
 }
-template <bool Q8>
+template <int W>
 __device__ __forceinline__ void prefetch_lm(const Args& a, int u, f4* wb) {
     int first, last;
     lm_block_range(u, a.vocab, first, last);
-    lm_load<Q8>(rsrc(a.lm_head), first + LM_G * (u / BLOCKS), last, a.vocab, wb);
+    lm_load<W>(rsrc(a.lm_head), first + LM_G * (u / BLOCKS), last, a.vocab, wb);
 }
 __device__ __forceinline__ int lm_grab(int* ctr, int first) {
     int g = 0;
@@ -1607,56 +1676,57 @@ __device__ __forceinline__ int lm_grab(int* ctr, int first) {
 // the LDS counter *ctr (which starts at WAVES). Groups alternate between wb
 // and nb; the counter only grows, so once a grabbed group lies past the range
 // every later one does too.
-template <bool Q8, int NR, int NX>
+template <int W, int NR, int NX>
 __device__ __forceinline__ void lm_stream(Rs lm, Rs lg, const f4 (&xv)[NX][4], const float* xn, int first, int last,
                                           int vocab, int nr, int* ctr, bool pre, f4* wb, f4* nb, float (&best)[NR],
                                           unsigned (&at)[NR], unsigned (&bad)[NR]) {
     int c0 = first + LM_G * int(threadIdx.x >> 6);
-    if (!pre) lm_load<Q8>(lm, c0, last, vocab, wb);
+    if (!pre) lm_load<W>(lm, c0, last, vocab, wb);
     int c1 = lm_grab(ctr, first);
-    lm_load<Q8>(lm, c1, last, vocab, nb);
+    lm_load<W>(lm, c1, last, vocab, nb);
     for (;;) {
         if (c0 >= last) break;
-        lm_rows<Q8, NR, NX>(lg, wb, xv, xn, c0, last, vocab, nr, best, at, bad);
+        lm_rows<W, NR, NX>(lg, wb, xv, xn, c0, last, vocab, nr, best, at, bad);
         if (c1 >= last) break;
         c0 = lm_grab(ctr, first);
-        lm_load<Q8>(lm, c0, last, vocab, wb);
-        lm_rows<Q8, NR, NX>(lg, nb, xv, xn, c1, last, vocab, nr, best, at, bad);
+        lm_load<W>(lm, c0, last, vocab, wb);
+        lm_rows<W, NR, NX>(lg, nb, xv, xn, c1, last, vocab, nr, best, at, bad);
         if (c0 >= last) break;
         c1 = lm_grab(ctr, first);
-        lm_load<Q8>(lm, c1, last, vocab, nb);
+        lm_load<W>(lm, c1, last, vocab, nb);
     }
 }
-template <bool Q8, int NR>
+template <int W, int NR>
 __device__ __forceinline__ bool phase_lm(const Args& a, Rs rs, int p, int u, f4* wb, Lds& l, int nr) {
     const int par = p & 1;
     stage_norm(a.final_norm, par, l);
     stage_tagged<NR * H, NR>(a, rs, SOFF(x), tag(a, p - 1), l.act[par], l, p, NoMid(), nr * (H / 2));
     if (!bsync(l, p)) return false;
     // the normalised input(s): registers (one-row steps, and the rows of
-    // int8 multi-row steps), else LDS (xn, row t normalised once by wave t)
-    constexpr int NX = (NR == 1 || Q8) ? NR : 1;
+    // BF16 / int8 multi-row steps), else LDS (xn, row t normalised once by
+    // wave t)
+    constexpr int NX = (NR == 1 || W != WF32) ? NR : 1;
     f4 xv[NX][4];
     float* xn = &l.act[par][NR * H];
     if (NR == 1) {
-        normed_chunks<Q8>(l, par, a.eps, xv[0]);
+        normed_chunks<W>(l, par, a.eps, xv[0]);
     } else {
         const int wave = int(threadIdx.x >> 6);
         if (wave < NR) {
             const unsigned lane = lane_id();
             f4 x[4];
-            normed_chunks<Q8>(l, par, a.eps, x, wave);
+            normed_chunks<W>(l, par, a.eps, x, wave);
 #pragma unroll
             for (int v = 0; v < 4; ++v)
-                *reinterpret_cast<f4*>(xn + wave * H + (Q8 ? 16 * lane + 4 * v : 4 * (lane + 64 * v))) = x[v];
+                *reinterpret_cast<f4*>(xn + wave * H + xcol<W>(lane, v)) = x[v];
         }
         if (!bsync(l, p)) return false;
-        if constexpr (Q8) {
+        if constexpr (W != WF32) {
             const unsigned lane = lane_id();
 #pragma unroll
             for (int t = 0; t < NX; ++t)
 #pragma unroll
-                for (int v = 0; v < 4; ++v) xv[t][v] = lds4(xn + t * H + 16 * lane + 4 * v);
+                for (int v = 0; v < 4; ++v) xv[t][v] = lds4(xn + t * H + xcol<W>(lane, v));
         }
     }
     int first, last;
@@ -1671,12 +1741,12 @@ __device__ __forceinline__ bool phase_lm(const Args& a, Rs rs, int p, int u, f4*
         bad[t] = 0;
     }
     f4 nb[4 * LM_G];
-    lm_stream<Q8, NR, NX>(lm, lg, xv, xn, first, last, a.vocab, nr, &l.lmnext, true, wb, nb, best, at, bad);
+    lm_stream<W, NR, NX>(lm, lg, xv, xn, first, last, a.vocab, nr, &l.lmnext, true, wb, nb, best, at, bad);
     // then pool chunks, in increasing row order like the range (so a wave's
     // first maximum is its lowest index): thread 0 takes the block's next
     // chunk between two block barriers (the waves are done with the previous
     // chunk's counter); each take returns a larger index, so the loop ends
-    constexpr int LMC = Q8 ? LM_CHUNK_Q8 : LM_CHUNK;
+    constexpr int LMC = W == WQ8 ? LM_CHUNK_Q8 : W == WB16 ? LM_CHUNK_B16 : LM_CHUNK;
     const int srows = lm_static_rows(a.vocab), nchunks = (a.vocab - srows + LMC - 1) / LMC;
     for (int round = 0; round <= nchunks; ++round) {
         out_barrier();
@@ -1689,7 +1759,7 @@ __device__ __forceinline__ bool phase_lm(const Args& a, Rs rs, int p, int u, f4*
         const int c = __builtin_amdgcn_readfirstlane(l.lmchunk);
         if (c >= nchunks) break;
         const int cf = srows + c * LMC;
-        lm_stream<Q8, NR, NX>(lm, lg, xv, xn, cf, min(a.vocab, cf + LMC), a.vocab, nr, &l.lmctr[round & 1], false,
+        lm_stream<W, NR, NX>(lm, lg, xv, xn, cf, min(a.vocab, cf + LMC), a.vocab, nr, &l.lmctr[round & 1], false,
                               wb, nb, best, at, bad);
     }
     if (lane_id() == 0) {
@@ -1796,19 +1866,19 @@ constexpr int KEEP_MAX_POS = 1536;
 __device__ __forceinline__ bool kept(const Args& a, unsigned long long mask, int L) {
     return a.pos < KEEP_MAX_POS && ((mask >> L) & 1ull);
 }
-template <bool Q8>
+template <int W>
 __device__ __forceinline__ void prefetch_layer(const Args& a, int L, int u, f4* wb) {
     const LayerP w = layer(a, L);
     if (w->attention) {
-        if (kept(a, Q8 ? kKeepQ8 : kKeepAqkv, L))
-            prefetch_aqkv<Q8, 0>(w, u, wb, 0);
+        if (kept(a, W == WQ8 ? kKeepQ8 : kKeepAqkv, L))
+            prefetch_aqkv<W, 0>(w, u, wb, 0);
         else
-            prefetch_aqkv<Q8>(w, u, wb, 0);
+            prefetch_aqkv<W>(w, u, wb, 0);
     } else {
-        if (kept(a, Q8 ? kKeepQ8 : kKeepDin, L))
-            prefetch_din<Q8, 0>(w, u, wb, 0);
+        if (kept(a, W == WQ8 ? kKeepQ8 : kKeepDin, L))
+            prefetch_din<W, 0>(w, u, wb, 0);
         else
-            prefetch_din<Q8>(w, u, wb, 0);
+            prefetch_din<W>(w, u, wb, 0);
     }
 }
 
@@ -1820,7 +1890,7 @@ __device__ __forceinline__ void prefetch_layer(const Args& a, int L, int u, f4* 
 // pos + r), every phase over its rows with the weights read once; each row is
 // computed exactly as a one-row step at its position (the same per-lane
 // arithmetic), so row r equals that step bit for bit.
-template <bool Q8, int NR>
+template <int W, int NR>
 __global__ __launch_bounds__(THREADS, 1) void decode_kernel(Args a) {
     __shared__ Lds l;
     const int nr = NR == 1 ? 1 : a.nrows;
@@ -1860,52 +1930,52 @@ __global__ __launch_bounds__(THREADS, 1) void decode_kernel(Args a) {
         if (L > 0) out_barrier();
 #pragma unroll
         for (int k = 0; k < WBUF; ++k) wb[k] = f4(0.f);
-        prefetch_layer<Q8>(a, L, opaque_uniform(unit), wb);
+        prefetch_layer<W>(a, L, opaque_uniform(unit), wb);
         if (w->attention) {
-            if (!phase_aqkv<Q8, NR>(a, rs, w, L, p, opaque_uniform(unit), wb, l, nr)) return;
+            if (!phase_aqkv<W, NR>(a, rs, w, L, p, opaque_uniform(unit), wb, l, nr)) return;
             out_barrier();
             prefetch_attn<NR>(a, w, opaque_uniform(unit), wb);
             ++p;
             if (!phase_attn<NR>(a, rs, w, p, opaque_uniform(unit), wb, l, nr)) return;
             out_barrier();
-            prefetch_row<Q8, NH * HD>(w->o, opaque_uniform(unit), H, wb);  // T_COMB reads no weights
+            prefetch_row<W, NH * HD>(w->o, opaque_uniform(unit), H, wb);  // T_COMB reads no weights
             ++p;
             if (!phase_comb<NR>(a, rs, p, opaque_uniform(unit), l, nr)) return;
             out_barrier();
             ++p;
-            if (!phase_o<Q8, NR>(a, rs, L, p, opaque_uniform(unit), wb, l, nr)) return;
+            if (!phase_o<W, NR>(a, rs, L, p, opaque_uniform(unit), wb, l, nr)) return;
         } else {
-            if (!phase_din<Q8, NR>(a, rs, w, L, p, opaque_uniform(unit), wb, l, nr)) return;
+            if (!phase_din<W, NR>(a, rs, w, L, p, opaque_uniform(unit), wb, l, nr)) return;
             out_barrier();
-            prefetch_mix<Q8>(w, opaque_uniform(unit), wb);
+            prefetch_mix<W>(w, opaque_uniform(unit), wb);
             ++p;
-            if (!phase_mix<Q8, NR>(a, rs, w, L, p, opaque_uniform(unit), wb, l, nr)) return;
+            if (!phase_mix<W, NR>(a, rs, w, L, p, opaque_uniform(unit), wb, l, nr)) return;
             out_barrier();
-            prefetch_row<Q8, VD>(w->out, opaque_uniform(unit), H, wb);
+            prefetch_row<W, VD>(w->out, opaque_uniform(unit), H, wb);
             ++p;
-            if (!phase_dout<Q8, NR>(a, rs, w, L, p, opaque_uniform(unit), wb, l, nr)) return;
+            if (!phase_dout<W, NR>(a, rs, w, L, p, opaque_uniform(unit), wb, l, nr)) return;
         }
         out_barrier();
-        if (kept(a, Q8 ? kKeepQ8 : kKeepGlu, L))
-            prefetch_glu<Q8, 0>(w, opaque_uniform(unit), wb, 0);
+        if (kept(a, W == WQ8 ? kKeepQ8 : kKeepGlu, L))
+            prefetch_glu<W, 0>(w, opaque_uniform(unit), wb, 0);
         else
-            prefetch_glu<Q8>(w, opaque_uniform(unit), wb, 0);
+            prefetch_glu<W>(w, opaque_uniform(unit), wb, 0);
         ++p;
-        if (!phase_glu<Q8, NR>(a, rs, w, p, opaque_uniform(unit), wb, l, nr)) return;
+        if (!phase_glu<W, NR>(a, rs, w, p, opaque_uniform(unit), wb, l, nr)) return;
         out_barrier();
-        if (kept(a, Q8 ? kKeepQ8 : kKeepDown, L))
-            prefetch_row<Q8, I, 0, 0>(w->down, opaque_uniform(unit), H, wb);
+        if (kept(a, W == WQ8 ? kKeepQ8 : kKeepDown, L))
+            prefetch_row<W, I, 0, 0>(w->down, opaque_uniform(unit), H, wb);
         else
-            prefetch_row<Q8, I, 0>(w->down, opaque_uniform(unit), H, wb);
+            prefetch_row<W, I, 0>(w->down, opaque_uniform(unit), H, wb);
         ++p;
-        if (!phase_down<Q8, NR>(a, rs, w, L + 1 < a.nlayers ? layer(a, L + 1) : nullptr, p, opaque_uniform(unit), wb, l,
+        if (!phase_down<W, NR>(a, rs, w, L + 1 < a.nlayers ? layer(a, L + 1) : nullptr, p, opaque_uniform(unit), wb, l,
                                 nr))
             return;
         ++p;
     }
     out_barrier();
-    prefetch_lm<Q8>(a, opaque_uniform(unit), wb);
-    if (!phase_lm<Q8, NR>(a, rs, p, opaque_uniform(unit), wb, l, nr)) return;
+    prefetch_lm<W>(a, opaque_uniform(unit), wb);
+    if (!phase_lm<W, NR>(a, rs, p, opaque_uniform(unit), wb, l, nr)) return;
     ++p;
     if (NR == 1) {
         if (blockIdx.x == 0) phase_arg(a, rs, p, l);
@@ -1929,7 +1999,7 @@ struct QrDecodePlan {
     int rows = 1;               // logits / picks rows (desc.rows)
     float* logits = nullptr;    // row 0 of the logits rows ([rows, vocab])
     float* picks = nullptr;     // row 0 of the [argmax, non-finite count] rows
-    bool q8 = false;  // int8 matrices and LM head: decode_kernel<true, *>
+    int fmt = 0;  // matrix format of every layer matrix and the LM head: decode_kernel<fmt, *> (dec::WF32 / WB16 / WQ8)
     bool rows_ok = false;  // the multi-row kernel fits the device (decode_rows)
     bool cooperative = false;  // launched with hipLaunchCooperativeKernel instead of a plain launch
     float* hist = nullptr;  // [capacity][argmax, non-finite count] of chained steps
@@ -1952,9 +2022,10 @@ const char* decode_unsupported(const QrDecodeDesc& d) {
         return "one-launch decode: vocabulary or capacity beyond 32-bit offsets";
     if (!d.embedding || !d.final_norm || !d.logits || !d.picks || !d.layer)
         return "one-launch decode: missing buffer";
-    if (d.weights != QR_DECODE_F32 && d.weights != QR_DECODE_INT8)
-        return "one-launch decode: matrices must be all fp32 or all int8";
-    if (d.weights == QR_DECODE_INT8 && !d.lm_head) return "one-launch decode: int8 needs its own int8 LM head";
+    if (d.weights != QR_DECODE_F32 && d.weights != QR_DECODE_BF16 && d.weights != QR_DECODE_INT8)
+        return "one-launch decode: matrices must be all fp32, all BF16 or all int8";
+    if (d.weights != QR_DECODE_F32 && !d.lm_head)
+        return "one-launch decode: BF16 and int8 matrices need an LM head in the same format";
     int phases = 2;
     for (int l = 0; l < d.layers; ++l) phases += d.layer[l].attention ? 6 : 5;
     if (phases > MAXPH || phases >= 1023) return "one-launch decode: too many phases";
@@ -2009,6 +2080,14 @@ void scratch_release(int dev, qr::dec::Scratch* p, unsigned epoch) {
 }
 }  // namespace
 
+// The kernel of a matrix format (dec::WF32 / WB16 / WQ8), one-row or multi-row.
+void (*decode_kernel_for(int fmt, bool rows))(dec::Args) {
+    using namespace dec;
+    if (fmt == WQ8) return rows ? decode_kernel<WQ8, NRMAX> : decode_kernel<WQ8, 1>;
+    if (fmt == WB16) return rows ? decode_kernel<WB16, NRMAX> : decode_kernel<WB16, 1>;
+    return rows ? decode_kernel<WF32, NRMAX> : decode_kernel<WF32, 1>;
+}
+
 int decode_plan_create(const QrDecodeDesc& d, QrDecodePlan** out, hipStream_t s, const char** why) {
     using namespace dec;
     *out = nullptr;
@@ -2016,17 +2095,16 @@ int decode_plan_create(const QrDecodeDesc& d, QrDecodePlan** out, hipStream_t s,
     int dev = 0, cus = 0, per_cu = 0;
     (void)hipGetDevice(&dev);
     (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
-    const bool q8 = d.weights == QR_DECODE_INT8;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, q8 ? decode_kernel<true, 1> : decode_kernel<false, 1>,
-                                                     THREADS, 0) != hipSuccess ||
+    const int fmt = d.weights == QR_DECODE_INT8 ? WQ8 : d.weights == QR_DECODE_BF16 ? WB16 : WF32;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, decode_kernel_for(fmt, false), THREADS, 0) != hipSuccess ||
         per_cu * cus < BLOCKS) {
         *why = "one-launch decode: 256 co-resident blocks do not fit this device";
         return -1;
     }
     int rows_per_cu = 0;
     const bool rows_fit =
-        hipOccupancyMaxActiveBlocksPerMultiprocessor(&rows_per_cu, q8 ? decode_kernel<true, NRMAX> : decode_kernel<false, NRMAX>,
-                                                     THREADS, 0) == hipSuccess &&
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&rows_per_cu, decode_kernel_for(fmt, true), THREADS, 0) ==
+            hipSuccess &&
         rows_per_cu * cus >= BLOCKS;
     auto* p = new QrDecodePlan;
     std::memset(&p->args, 0, sizeof(p->args));
@@ -2035,7 +2113,7 @@ int decode_plan_create(const QrDecodeDesc& d, QrDecodePlan** out, hipStream_t s,
     p->rows = d.rows;
     p->logits = d.logits;
     p->picks = d.picks;
-    p->q8 = q8;
+    p->fmt = fmt;
     p->rows_ok = rows_fit;
     p->device = dev;
     unsigned epoch = 0;
@@ -2113,10 +2191,7 @@ static int launch(QrDecodePlan* p, hipStream_t s, bool rows) {
         if (hipError_t e = hipMemsetAsync(p->scratch, 0, sizeof(Scratch), s)) return int(e);
     }
     void* args[] = {&a};
-    const void* k = rows ? (p->q8 ? reinterpret_cast<const void*>(decode_kernel<true, NRMAX>)
-                                  : reinterpret_cast<const void*>(decode_kernel<false, NRMAX>))
-                         : (p->q8 ? reinterpret_cast<const void*>(decode_kernel<true, 1>)
-                                  : reinterpret_cast<const void*>(decode_kernel<false, 1>));
+    const void* k = reinterpret_cast<const void*>(decode_kernel_for(p->fmt, rows));
     return p->cooperative ? int(hipLaunchCooperativeKernel(k, dim3(BLOCKS), dim3(THREADS), args, 0, s))
                           : int(hipLaunchKernel(k, dim3(BLOCKS), dim3(THREADS), args, 0, s));
 }

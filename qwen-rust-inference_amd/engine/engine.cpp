@@ -534,9 +534,11 @@ struct QeRun {
         const Api* a = api();
         const QwConfig& c = model->config;
         if (!a->decode_plan || model->embedding.int8) return;
-        // all matrices fp32, or all int8 (the int8 model's LM head is int8 too)
-        const bool q8 = model->output().int8;
-        auto ok = [q8](const DeviceMatrix& m) { return q8 ? m.int8 : m.f32(); };
+        // all matrices fp32, all BF16 (a BF16-exact model: the tied LM head is
+        // the BF16 embedding table), or all int8 (the int8 model's LM head is
+        // int8 too)
+        const bool q8 = model->output().int8, b16 = model->output().bf16;
+        auto ok = [q8, b16](const DeviceMatrix& m) { return q8 ? m.int8 : b16 ? m.bf16 : m.f32(); };
         if (!ok(model->output())) return;
         std::vector<QrDecodeLayer> layers;
         const DeviceBlock* attn = nullptr;
@@ -620,7 +622,7 @@ struct QeRun {
         desc.logits = logits.p;
         desc.picks = picks.p;
         desc.layer = layers.data();
-        desc.weights = q8 ? QR_DECODE_INT8 : QR_DECODE_F32;
+        desc.weights = q8 ? QR_DECODE_INT8 : b16 ? QR_DECODE_BF16 : QR_DECODE_F32;
         desc.embedding_bf16 = model->embedding.bf16 ? 1 : 0;
         desc.rows = int32(std::min(kVerifyRows, chunk));
         desc.snapshots = int32(snapshots);

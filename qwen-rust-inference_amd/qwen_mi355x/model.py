@@ -213,6 +213,17 @@ def synthetic_weights(c: QwConfig, seed: int = 0, std: float = 0.02, fill=None) 
     return Weights(c, tensors)
 
 
+def bf16_weights(w: Weights) -> Weights:
+    """The tensors rounded to BF16 (nearest, ties to even), kept as fp32: a
+    BF16-exact model whose matrices the engine uploads as packed BF16 under
+    fmt=BF16_EXACT (the reference's deployed precision, src/device.rs:535-549)."""
+    out = {}
+    for i, t in w.tensors.items():
+        u = np.ascontiguousarray(t, dtype=np.float32).view(np.uint32)
+        out[i] = ((u + 0x7FFF + ((u >> 16) & 1)) & 0xFFFF0000).astype(np.uint32).view(np.float32)
+    return Weights(w.config, out)
+
+
 def load_fixture(path) -> dict:
     with open(path) as f:
         return json.load(f)

@@ -30,3 +30,18 @@ def parity(actual, expected, rtol=FP32_RTOL, where=""):
 def dot_bound(w, x, rel=2e-5):
     """Error bound of an fp32 dot product against fp64: rel * sum |w_j x_j|."""
     return rel * (np.abs(w.astype(np.float64)) @ np.abs(x.astype(np.float64))) + 1e-30
+
+
+def bf16_round(a):
+    """Round-to-nearest-even float32 -> BF16, returned widened to float32."""
+    u = np.ascontiguousarray(a, dtype=np.float32).view(np.uint32)
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) & 0xFFFF0000).astype(np.uint32)
+    return r.view(np.float32)
+
+
+def bf16_weights(c, w):
+    """The weights with every tensor rounded to BF16 (a BF16-exact model: every
+    matrix uploads as BF16 under fmt=BF16_EXACT, the embedding and tied LM head
+    included)."""
+    from qwen_mi355x import model as M
+    return M.bf16_weights(w)

@@ -333,3 +333,20 @@ def test_edit_overlay_matches_oracle(fixture, bridge, fmt):
         run.set_edit([dict(edits[0], columns=[3, 3])])
     with pytest.raises(E.EngineError, match="direction"):
         run.set_edit([dict(edits[1], direction=np.zeros(c.hidden_size, np.float32))])
+
+
+def test_bf16_weights_round_like_torch(tiny):
+    """model.bf16_weights (the BF16-exact model of the BF16 decode tests and
+    the bench) rounds every tensor as torch's float32 -> bfloat16 conversion
+    does (nearest, ties to even), including values exactly halfway."""
+    import torch
+    c, w = tiny
+    b = M.bf16_weights(w)
+    for i, t in w.tensors.items():
+        want = torch.from_numpy(t).to(torch.bfloat16).to(torch.float32).numpy()
+        assert np.array_equal(b.tensors[i].view(np.uint32), want.view(np.uint32)), i
+    ties = np.array([1.0 + 2.0 ** -8, 1.0 + 3 * 2.0 ** -8, -(1.0 + 2.0 ** -8), 2.0 ** -130 * 3], dtype=np.float32)
+    tw = M.Weights(c, {**w.tensors, 0: np.resize(ties, w.tensors[0].size).astype(np.float32)})
+    got = M.bf16_weights(tw).tensors[0][:4]
+    want = torch.from_numpy(ties).to(torch.bfloat16).to(torch.float32).numpy()
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))

@@ -7,7 +7,7 @@ import numpy as np
 import pytest
 
 from conftest import GOLDEN
-from parity import INT8_RTOL, parity
+from parity import INT8_RTOL, bf16_weights, parity
 from qwen_mi355x import engine as E
 from qwen_mi355x import model as M
 from test_engine_cpu import dequantised
@@ -232,26 +232,72 @@ def test_qwen08b_short_greedy(qwen08b):
             parity(run.state(layer, which), s.part(layer, which), where=f"0.8B state {layer}/{which}")
 
 
+def test_qwen08b_bf16_one_launch(qwen08b):
+    """The 0.8B-shaped model with BF16-exact weights (every matrix, the
+    embedding and the tied LM head uploaded as BF16, the reference's deployed
+    format) on the one-launch decode: identical greedy IDs and every step's
+    logits within the fp32 bound against the oracle on the same weights, the
+    op sequence's BF16 kernels within the bound, and verify rows (one
+    multi-row launch) equal to decode steps bit for bit."""
+    c, w0 = qwen08b
+    w = bf16_weights(c, w0)
+    prompt = [int(v) for v in np.random.default_rng(3).integers(0, c.vocab_size, 12)]
+    print("oracle on the BF16-exact 0.8B", flush=True)
+    want, want_logits, s = oracle_greedy(O.Oracle(w), prompt, 6)
+    m = E.Model(w, fmt=E.BF16_EXACT)
+    nb, nm, _ = m.weight_summary()
+    assert nb == nm, "every matrix uploads as BF16"
+    run = m.new_run(64, chunk=8)
+    assert run.decode_plan, "all-BF16 steps should take the one-launch decode"
+    logits = run.prefill(prompt)
+    parity(logits, want_logits[0], where="BF16 0.8B prefill logits")
+    tok = O.select_greedy(logits)
+    ops = E.Model(w, fmt=E.BF16_EXACT, disable=E.NO_DECODE_STEP)
+    ref = ops.new_run(64, chunk=8)
+    ref.prefill(prompt)
+    for i in range(5):
+        print(f"BF16 one-launch step {i}", flush=True)
+        got = run.step(tok)
+        parity(got, want_logits[i + 1], where=f"BF16 0.8B step {i}")
+        parity(got, ref.step(tok), where=f"BF16 0.8B step {i} against the op sequence")
+        assert O.select_greedy(got) == want[i + 1]
+        tok = want[i + 1]
+    for layer in (0, 3):
+        for which in range(4):
+            parity(run.state(layer, which), s.part(layer, which), where=f"BF16 0.8B state {layer}/{which}")
+    ops.close()
+    draft = [int(v) for v in np.random.default_rng(13).integers(0, c.vocab_size, 4)]
+    print("BF16 verify rows vs decode steps", flush=True)
+    verify_rows_equal_steps(c, m, prompt, draft, 64, 8)
+    m.close()
+
+
 @pytest.mark.parametrize("vocab", [1000, 3001])
-@pytest.mark.parametrize("fmt", [E.F32, E.INT8])
+@pytest.mark.parametrize("fmt", [E.F32, E.BF16_EXACT, E.INT8])
 def test_one_launch_small_vocabulary(vocab, fmt):
     """The one-launch decode on the 0.8B geometry with 4 layers and a small
     vocabulary: 1000 rows all go to the lm_head chunk pool (no block range),
     3001 leave 2048 rows in the block ranges and a ragged last chunk. Every
-    step's logits against the oracle (fp32 bound; int8 against the oracle on
-    the dequantised weights), identical greedy IDs."""
+    step's logits against the oracle (fp32 bound, also for BF16 matrices on
+    BF16-exact weights; int8 against the oracle on the dequantised weights),
+    identical greedy IDs."""
     c = M.make_config(hidden=1024, intermediate=3584, vocab=vocab,
                       layer_types=["linear_attention"] * 3 + ["full_attention"], heads=8, kv_heads=2, head_dim=256,
                       rotary_dim=64, key_heads=16, value_heads=16, key_dim=128, value_dim=128, conv_kernel=4,
                       max_positions=256, eps=1e-6, theta=1e7)
     w = M.synthetic_weights(c, seed=3)
+    if fmt == E.BF16_EXACT:
+        w = bf16_weights(c, w)
     prompt = [int(v) for v in np.random.default_rng(9).integers(0, vocab, 6)]
-    run = E.Model(w, fmt=fmt).new_run(32, chunk=8)
+    m = E.Model(w, fmt=fmt)
+    if fmt == E.BF16_EXACT:
+        assert m.weight_summary()[0] == m.weight_summary()[1], "every matrix uploads as BF16"
+    run = m.new_run(32, chunk=8)
     assert run.decode_plan
-    st = (O.Oracle(w) if fmt == E.F32 else dequantised(c, w)).new_state()
+    st = (dequantised(c, w) if fmt == E.INT8 else O.Oracle(w)).new_state()
     for t in prompt:
         want = st.step(t, O.VECTOR)
-    rtol = {} if fmt == E.F32 else {"rtol": INT8_RTOL}
+    rtol = {"rtol": INT8_RTOL} if fmt == E.INT8 else {}
     parity(run.prefill(prompt), want, where=f"vocab {vocab} prefill", **rtol)
     tok = O.select_greedy(want)
     for i in range(5):
@@ -259,7 +305,7 @@ def test_one_launch_small_vocabulary(vocab, fmt):
         got = run.step(tok)
         want = st.step(tok, O.VECTOR)
         parity(got, want, where=f"vocab {vocab} step {i}", **rtol)
-        if fmt == E.F32:
+        if fmt != E.INT8:
             assert O.select_greedy(got) == O.select_greedy(want)
         tok = O.select_greedy(want)
 
