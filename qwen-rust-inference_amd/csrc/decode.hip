@@ -1862,6 +1862,15 @@ constexpr unsigned long long kKeepDin = 0xfffull, kKeepAqkv = ~0ull, kKeepGlu = 
 // for many layers; layers 0-15 measured best (all 24: +7 us per token, 0-11:
 // +3, 0-19: +5)
 constexpr unsigned long long kKeepQ8 = 0xffffull;
+// BF16 weights are half the bytes: part 0 of DIN and AQKV in every layer and
+// of GLU in layers 0-5 measured best (the fp32 choice: +5 us per token; part 0
+// of DOWN too: +2; int8's: +5)
+constexpr unsigned long long kKeepB16Din = ~0ull, kKeepB16Aqkv = ~0ull, kKeepB16Glu = 0x3full, kKeepB16Down = 0;
+// The mask of a phase's part-0 weights read with allocating loads.
+template <int W>
+__device__ __forceinline__ unsigned long long keep_mask(unsigned long long f32, unsigned long long b16) {
+    return W == WQ8 ? kKeepQ8 : W == WB16 ? b16 : f32;
+}
 constexpr int KEEP_MAX_POS = 1536;
 __device__ __forceinline__ bool kept(const Args& a, unsigned long long mask, int L) {
     return a.pos < KEEP_MAX_POS && ((mask >> L) & 1ull);
@@ -1870,12 +1879,12 @@ template <int W>
 __device__ __forceinline__ void prefetch_layer(const Args& a, int L, int u, f4* wb) {
     const LayerP w = layer(a, L);
     if (w->attention) {
-        if (kept(a, W == WQ8 ? kKeepQ8 : kKeepAqkv, L))
+        if (kept(a, keep_mask<W>(kKeepAqkv, kKeepB16Aqkv), L))
             prefetch_aqkv<W, 0>(w, u, wb, 0);
         else
             prefetch_aqkv<W>(w, u, wb, 0);
     } else {
-        if (kept(a, W == WQ8 ? kKeepQ8 : kKeepDin, L))
+        if (kept(a, keep_mask<W>(kKeepDin, kKeepB16Din), L))
             prefetch_din<W, 0>(w, u, wb, 0);
         else
             prefetch_din<W>(w, u, wb, 0);
@@ -1956,14 +1965,14 @@ __global__ __launch_bounds__(THREADS, 1) void decode_kernel(Args a) {
             if (!phase_dout<W, NR>(a, rs, w, L, p, opaque_uniform(unit), wb, l, nr)) return;
         }
         out_barrier();
-        if (kept(a, W == WQ8 ? kKeepQ8 : kKeepGlu, L))
+        if (kept(a, keep_mask<W>(kKeepGlu, kKeepB16Glu), L))
             prefetch_glu<W, 0>(w, opaque_uniform(unit), wb, 0);
         else
             prefetch_glu<W>(w, opaque_uniform(unit), wb, 0);
         ++p;
         if (!phase_glu<W, NR>(a, rs, w, p, opaque_uniform(unit), wb, l, nr)) return;
         out_barrier();
-        if (kept(a, W == WQ8 ? kKeepQ8 : kKeepDown, L))
+        if (kept(a, keep_mask<W>(kKeepDown, kKeepB16Down), L))
             prefetch_row<W, I, 0, 0>(w->down, opaque_uniform(unit), H, wb);
         else
             prefetch_row<W, I, 0>(w->down, opaque_uniform(unit), H, wb);
