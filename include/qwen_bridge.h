@@ -232,6 +232,17 @@ int qr_decode_steps(Context* c, QrDecodePlan* p, int first_token, int position, 
  * verify rows, native/rocm/bridge.cpp:197-215, src/device.rs:1514-1531). No
  * counterpart in the reference's ABI. */
 int qr_decode_step_row(Context* c, QrDecodePlan* p, int token, int position, int row, int snap);
+/* qr_decode_step with the per-layer records of a captured forward also
+ * written to `capture` (device memory of len floats, at least layers *
+ * (6 hidden + intermediate) + hidden): layer L's records at capture +
+ * L (6 hidden + intermediate), in the order of src/device.rs:1748-1761's
+ * records (input_norm, mixed, after_mixer, post_norm [hidden each],
+ * ffn_product [intermediate], ffn, output [hidden each]), then the final norm
+ * [hidden]. The engine reads them back and reports them as the op sequence's
+ * capture would (the same values up to fp32 summation order), so a captured
+ * step keeps the one-launch kernel. No counterpart in the reference's ABI,
+ * which captures on the op sequence. */
+int qr_decode_step_capture(Context* c, QrDecodePlan* p, int token, int position, float* capture, int64_t len);
 /* Part of a verify pass, n = 1..4 consecutive tokens in ONE launch, the
  * weights read once for all rows: row r is tokens[r] at position + r (logits
  * row first + r, [argmax, non-finite count] in picks row first + r), and when

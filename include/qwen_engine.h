@@ -42,7 +42,8 @@ enum QeDisable {
     QE_NO_PREPARED_GEMM = 256, /* qr_gemm_f32_prepare (prefill projections over split planes) */
     QE_NO_PLAIN_DECODE_LAUNCH = 512, /* one-launch decode steps launched cooperatively
                                         (qr_set_option "decode_cooperative"; without it: no plan) */
-    QE_NO_DECODE_ROWS = 1024 /* qr_decode_rows (verify rows: one launch per row instead) */
+    QE_NO_DECODE_ROWS = 1024, /* qr_decode_rows (verify rows: one launch per row instead) */
+    QE_NO_DECODE_CAPTURE = 2048 /* qr_decode_step_capture (captured steps: the op sequence instead) */
 };
 
 /* Record callback of a captured step: (layer, name, values, n). Names follow

@@ -883,6 +883,14 @@ int qr_decode_step(Context* c, QrDecodePlan* p, int token, int position) {
     if (token < 0) return fail(c, "decode step token", -1);
     return launched(c, "decode step", qr::decode_step(p, token, position, -1, c->stream));
 }
+int qr_decode_step_capture(Context* c, QrDecodePlan* p, int token, int position, float* capture, int64_t len) {
+    ++c->serial;
+    if (!p || !capture) return fail(c, "decode step capture without a plan or buffer", -1);
+    if (len < int64_t(qr::decode_capture_floats(p))) return fail(c, "decode step capture buffer too short", -1);
+    auto sc = scope(c, [&] { return std::string("decode_step_capture"); });
+    if (token < 0) return fail(c, "decode step token", -1);
+    return launched(c, "decode step", qr::decode_step(p, token, position, -1, c->stream, 0, 0, capture));
+}
 int qr_decode_rows(Context* c, QrDecodePlan* p, const int32_t* tokens, int n, int position, int first, int snaps) {
     ++c->serial;
     if (!p || !tokens) return fail(c, "decode rows without a plan", -1);

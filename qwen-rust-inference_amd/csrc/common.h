@@ -167,7 +167,10 @@ int decode_plan_cooperative(QrDecodePlan* p, bool on);
 // token -1: the previous launch's argmax (read on the device). slot >= 0: the
 // step's [argmax, non-finite count] also goes to history slot `slot`.
 // slot >= 0: the chained-steps history slot; row: logits / picks row; snap: snapshot copy (0: none).
-int decode_step(QrDecodePlan* p, int token, int position, int slot, hipStream_t s, int row = 0, int snap = 0);
+// cap: when set, the step's per-layer records (decode_capture_floats(layers) floats).
+int decode_step(QrDecodePlan* p, int token, int position, int slot, hipStream_t s, int row = 0, int snap = 0,
+                float* cap = nullptr);
+size_t decode_capture_floats(const QrDecodePlan* p);
 // Up to 4 consecutive tokens in one launch (qr_decode_rows).
 int decode_rows(QrDecodePlan* p, const int* tokens, int n, int position, int first, int snaps, hipStream_t s);
 int decode_history_clear(QrDecodePlan* p, int n, hipStream_t s);

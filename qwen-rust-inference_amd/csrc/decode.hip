@@ -137,6 +137,7 @@ struct Args {
     int emb_bf16;  // the embedding table is packed BF16 (two per word, element 2i low)
     int chain;     // 1: the token is the previous launch's argmax (picks[0]), not `token`
     float* hist;   // when set: this launch's [argmax, non-finite count] also lands here
+    float* cap;    // when set (one-row steps): the step's per-layer records land here (capture layout below)
     int snap;      // > 0: the updated DeltaNet conv and recurrent states are also written to this snapshot copy
     unsigned epoch;
     float eps;
@@ -491,6 +492,21 @@ __device__ __forceinline__ void normed_chunks(const Lds& l, int par, float eps, 
 #pragma unroll
     for (int v = 0; v < 4; ++v) xv[v] = (xv[v] * r) * lds4(&l.nw[par][xcol<W>(lane, v)]);
 }
+// ---- capture: with a.cap set, a one-row step also writes the records of the
+// engine's captured forward (src/device.rs:1748-1761 records: per layer the
+// input norm, the mixer output, the residual after it, the post norm, the FFN
+// product, the FFN output and the layer output) as plain stores, layer L's at
+// a.cap + L CAPL, then the final norm at a.cap + nlayers CAPL.
+constexpr int CAP_IN = 0, CAP_MIXED = H, CAP_AFTER = 2 * H, CAP_POST = 3 * H, CAP_PROD = 4 * H, CAP_FFN = 4 * H + I,
+              CAP_OUT = 5 * H + I, CAPL = 6 * H + I;
+__device__ __forceinline__ float* cap_at(const Args& a, int L, int off) { return a.cap + size_t(L) * CAPL + off; }
+// A normalised vector held in normed_chunks' lane layout (one wave writes it).
+template <int W>
+__device__ __forceinline__ void capture_normed(float* dst, const f4 (&xv)[4]) {
+    const unsigned lane = lane_id();
+#pragma unroll
+    for (int v = 0; v < 4; ++v) *reinterpret_cast<f4*>(dst + xcol<W>(lane, v)) = xv[v];
+}
 // Value e (0..3) of a word of packed int8.
 __device__ __forceinline__ float q8v(unsigned w, int e) { return float(int(w << (24 - 8 * e)) >> 24); }
 // 16 int8 weights (one 16-byte entry) times 16 activations.
@@ -645,6 +661,7 @@ __device__ __forceinline__ bool phase_din(const Args& a, Rs rs, LayerP w, int L,
         mine[r] = 0.f;
         f4 xv[4];
         normed_chunks<W>(l, par, a.eps, xv, r);
+        if (NR == 1 && a.cap && u == 0) capture_normed<W>(cap_at(a, L, CAP_IN), xv);
         din_row<W, 0>(wb, xv, u, mine[r]);
         din_row<W, 1>(wb, xv, u, mine[r]);
         din_row<W, 2>(wb, xv, u, mine[r]);
@@ -990,6 +1007,10 @@ __device__ __forceinline__ bool phase_dout(const Args& a, Rs rs, LayerP w, int L
         const float acc = dot_row_lds<W, VD / 256>(wb, l.act[par] + gated_off<NR>() + r * VD);
         const float res = l.act[par][r * H + u];  // the layer input as DIN (phase p - 2) staged it
         if (lane_id() == 0 && r < nr) stt(rs, SROW(after, r) + 8u * unsigned(u), res + acc, tag(a, p));
+        if (NR == 1 && a.cap && lane_id() == 0) {
+            cap_at(a, L, CAP_MIXED)[u] = acc;
+            cap_at(a, L, CAP_AFTER)[u] = res + acc;
+        }
     }
     return true;
 }
@@ -1020,15 +1041,17 @@ __device__ __forceinline__ void prefetch_glu(LayerP w, int u, f4* wb, int part) 
 }
 template <int W, int R>
 __device__ __forceinline__ void glu_row(Rs rs, const f4* wb, const f4 (&xv)[4], int row0, unsigned t, int r,
-                                        bool live = true) {
+                                        bool live = true, float* cap = nullptr) {
     const int row = row0 + R;
     if (row < I) {
         const float g = dot_row_h<W, 8 * R>(wb, xv), up = dot_row_h<W, 8 * R + 4>(wb, xv);
         if (lane_id() == 0 && live) stt(rs, SROW(product, r) + 8u * unsigned(row), silu(g) * up, t);
+        if (cap && lane_id() == 0) cap[row] = silu(g) * up;
     }
 }
 template <int W, int NR>
-__device__ __forceinline__ bool phase_glu(const Args& a, Rs rs, LayerP w, int p, int u, f4* wb, Lds& l, int nr) {
+__device__ __forceinline__ bool phase_glu(const Args& a, Rs rs, LayerP w, int L, int p, int u, f4* wb, Lds& l,
+                                          int nr) {
     const int par = p & 1;
     stage_norm(w->post_norm, par, l);
     stage_tagged<NR * H, NR>(a, rs, SOFF(after), tag(a, p - 1), l.act[par], l, p,
@@ -1040,8 +1063,13 @@ __device__ __forceinline__ bool phase_glu(const Args& a, Rs rs, LayerP w, int p,
     for (int r = 0; r < NR; ++r) {
         f4 xv[4];
         normed_chunks<W>(l, par, a.eps, xv, r);
-        glu_row<W, 0>(rs, wb, xv, row0, tag(a, p), r, r < nr);
-        glu_row<W, 1>(rs, wb, xv, row0, tag(a, p), r, r < nr);
+        float* cap = nullptr;
+        if (NR == 1 && a.cap) {
+            if (u == 0) capture_normed<W>(cap_at(a, L, CAP_POST), xv);
+            cap = cap_at(a, L, CAP_PROD);
+        }
+        glu_row<W, 0>(rs, wb, xv, row0, tag(a, p), r, r < nr, cap);
+        glu_row<W, 1>(rs, wb, xv, row0, tag(a, p), r, r < nr, cap);
     }
     return true;
 }
@@ -1059,8 +1087,8 @@ __device__ __forceinline__ void touch_record(LayerP w) {
 }
 // ---- T_DOWN: x = after + down . product
 template <int W, int NR>
-__device__ __forceinline__ bool phase_down(const Args& a, Rs rs, LayerP w, LayerP next, int p, int u, f4* wb, Lds& l,
-                                           int nr) {
+__device__ __forceinline__ bool phase_down(const Args& a, Rs rs, LayerP w, LayerP next, int L, int p, int u, f4* wb,
+                                           Lds& l, int nr) {
     const int par = p & 1;
     stage_tagged<NR * I, NR>(
         a, rs, SOFF(product), tag(a, p - 1), l.act[par], l, p,
@@ -1076,6 +1104,10 @@ __device__ __forceinline__ bool phase_down(const Args& a, Rs rs, LayerP w, Layer
         const float acc = dot_row_lds<W, I / 256>(wb, l.act[par] + r * I);
         const float res = l.act[par ^ 1][r * H + u];  // `after` as GLU (phase p - 1) staged it
         if (lane_id() == 0 && r < nr) stt(rs, SROW(x, r) + 8u * unsigned(u), res + acc, tag(a, p));
+        if (NR == 1 && a.cap && lane_id() == 0) {
+            cap_at(a, L, CAP_FFN)[u] = acc;
+            cap_at(a, L, CAP_OUT)[u] = res + acc;
+        }
     }
     return true;
 }
@@ -1126,6 +1158,7 @@ __device__ __forceinline__ bool phase_aqkv(const Args& a, Rs rs, LayerP w, int L
     for (int r = 0; r < NR; ++r) {
         f4 xv[4];
         normed_chunks<W>(l, par, a.eps, xv, r);
+        if (NR == 1 && a.cap && u == 0) capture_normed<W>(cap_at(a, L, CAP_IN), xv);
         aqkv_row<W, 0>(rs, wb, xv, u, tag(a, p), r, r < nr);
         aqkv_row<W, 1>(rs, wb, xv, u, tag(a, p), r, r < nr);
         aqkv_row<W, 2>(rs, wb, xv, u, tag(a, p), r, r < nr);
@@ -1522,6 +1555,10 @@ __device__ __forceinline__ bool phase_o(const Args& a, Rs rs, int L, int p, int 
         const float acc = dot_row_lds<W, NH * HD / 256>(wb, l.act[par] + r * NH * HD);
         const float res = l.act[par ^ 1][r * H + u];  // the layer input as AQKV (phase p - 3) staged it
         if (lane_id() == 0 && r < nr) stt(rs, SROW(after, r) + 8u * unsigned(u), res + acc, tag(a, p));
+        if (NR == 1 && a.cap && lane_id() == 0) {
+            cap_at(a, L, CAP_MIXED)[u] = acc;
+            cap_at(a, L, CAP_AFTER)[u] = res + acc;
+        }
     }
     return true;
 }
@@ -1710,6 +1747,7 @@ __device__ __forceinline__ bool phase_lm(const Args& a, Rs rs, int p, int u, f4*
     float* xn = &l.act[par][NR * H];
     if (NR == 1) {
         normed_chunks<W>(l, par, a.eps, xv[0]);
+        if (a.cap && u == 0) capture_normed<W>(cap_at(a, a.nlayers, 0), xv[0]);
     } else {
         const int wave = int(threadIdx.x >> 6);
         if (wave < NR) {
@@ -1970,15 +2008,15 @@ __global__ __launch_bounds__(THREADS, 1) void decode_kernel(Args a) {
         else
             prefetch_glu<W>(w, opaque_uniform(unit), wb, 0);
         ++p;
-        if (!phase_glu<W, NR>(a, rs, w, p, opaque_uniform(unit), wb, l, nr)) return;
+        if (!phase_glu<W, NR>(a, rs, w, L, p, opaque_uniform(unit), wb, l, nr)) return;
         out_barrier();
         if (kept(a, keep_mask<W>(kKeepDown, kKeepB16Down), L))
             prefetch_row<W, I, 0, 0>(w->down, opaque_uniform(unit), H, wb);
         else
             prefetch_row<W, I, 0>(w->down, opaque_uniform(unit), H, wb);
         ++p;
-        if (!phase_down<W, NR>(a, rs, w, L + 1 < a.nlayers ? layer(a, L + 1) : nullptr, p, opaque_uniform(unit), wb, l,
-                                nr))
+        if (!phase_down<W, NR>(a, rs, w, L + 1 < a.nlayers ? layer(a, L + 1) : nullptr, L, p, opaque_uniform(unit), wb,
+                                l, nr))
             return;
         ++p;
     }
@@ -2205,7 +2243,7 @@ static int launch(QrDecodePlan* p, hipStream_t s, bool rows) {
                           : int(hipLaunchKernel(k, dim3(BLOCKS), dim3(THREADS), args, 0, s));
 }
 
-int decode_step(QrDecodePlan* p, int token, int position, int slot, hipStream_t s, int row, int snap) {
+int decode_step(QrDecodePlan* p, int token, int position, int slot, hipStream_t s, int row, int snap, float* cap) {
     using namespace dec;
     Args& a = p->args;
     if (token < -1 || token >= a.vocab || position < 0 || position >= p->capacity || slot >= p->capacity ||
@@ -2217,6 +2255,7 @@ int decode_step(QrDecodePlan* p, int token, int position, int slot, hipStream_t 
     a.chain = token < 0 ? 1 : 0;
     a.token = token < 0 ? 0 : token;
     a.hist = slot < 0 ? nullptr : p->hist + 2 * slot;
+    a.cap = cap;
     a.pos = position;
     // RoPE angle pos / theta^(2i / rot) and its cos / sin on the host
     // (reference: src/attention.rs:49-55, the same f32 expressions)
@@ -2248,6 +2287,7 @@ int decode_rows(QrDecodePlan* p, const int* tokens, int n, int position, int fir
     a.chain = 0;
     a.token = tokens[0];
     a.hist = nullptr;
+    a.cap = nullptr;
     a.pos = position;
     a.nrows = n;
     a.snaps = snaps > first ? snaps - first : 0;
@@ -2256,6 +2296,9 @@ int decode_rows(QrDecodePlan* p, const int* tokens, int n, int position, int fir
         set_rope(p, a, r, position + (r < n ? r : 0));
     }
     return launch(p, s, true);
+}
+size_t decode_capture_floats(const QrDecodePlan* p) {
+    return size_t(p->args.nlayers) * dec::CAPL + dec::H;
 }
 int decode_history_clear(QrDecodePlan* p, int n, hipStream_t s) {
     if (n < 1 || n > p->capacity) return int(hipErrorInvalidValue);

@@ -103,6 +103,7 @@ struct Api {
     int (*decode_plan)(Context*, const QrDecodeDesc*, QrDecodePlan**) = nullptr;
     int (*decode_step)(Context*, QrDecodePlan*, int, int) = nullptr;
     int (*decode_step_row)(Context*, QrDecodePlan*, int, int, int, int) = nullptr;
+    int (*decode_step_capture)(Context*, QrDecodePlan*, int, int, float*, int64_t) = nullptr;
     int (*decode_rows)(Context*, QrDecodePlan*, const int32_t*, int, int, int, int) = nullptr;
     int (*decode_steps)(Context*, QrDecodePlan*, int, int, int, int32_t*, float*) = nullptr;
     void (*decode_free)(Context*, QrDecodePlan*) = nullptr;
@@ -178,6 +179,8 @@ struct Api {
             decode_free = symbol<decltype(decode_free)>("qr_decode_plan_free", false);
             decode_steps = symbol<decltype(decode_steps)>("qr_decode_steps", false);
             decode_step_row = symbol<decltype(decode_step_row)>("qr_decode_step_row", false);
+            if (!(disable & QE_NO_DECODE_CAPTURE))
+                decode_step_capture = symbol<decltype(decode_step_capture)>("qr_decode_step_capture", false);
             if (!(disable & QE_NO_DECODE_ROWS)) decode_rows = symbol<decltype(decode_rows)>("qr_decode_rows", false);
             if (!decode_plan || !decode_step || !decode_free) decode_plan = nullptr;
         }
@@ -501,6 +504,7 @@ struct QeRun {
     bool failed = false;
     std::vector<MixerRun> mixers;
     Buffer x, norm, mixed, residual, gate, up, product, ffn, logits, picks;
+    Buffer captured;  // the one-launch step's per-layer records (qr_decode_step_capture), made on first use
     bool greedy_rows = false;
     std::vector<uint32_t> picked;
     size_t pick_slot = 0;
@@ -671,6 +675,35 @@ struct QeRun {
         } else {
             out = logits.read(size_t(model->config.vocab_size));
         }
+        position += 1;
+        return out;
+    }
+    // One captured token through the plan (qr_decode_step_capture): the
+    // records forward_body would report, in its order (src/device.rs:1748-1761),
+    // from one read of the step's record buffer.
+    std::vector<float> forward_planned_capture(uint32_t id, const Record* rec) {
+        const Api* a = api();
+        const size_t h = size_t(model->config.hidden_size), i_size = size_t(model->config.intermediate_size);
+        const size_t layers = model->blocks.size(), per = 6 * h + i_size, n = layers * per + h;
+        if (captured.len < n) captured = Buffer(a, n);
+        a->check(a->decode_step_capture(a->ctx, plan, int(id), int(position), captured.p, int64_t(captured.len)));
+        std::vector<float> pk(2);
+        a->check(a->read(a->ctx, pk.data(), picks.p, 2));
+        require(pk[1] < 1e30f, "one-launch decode step timed out at a stage barrier");
+        const std::vector<float> v = captured.read(n);
+        static const char* names[] = {"input_norm", "mixed", "after_mixer", "post_norm", "ffn_product", "ffn", "output"};
+        const size_t off[] = {0, h, 2 * h, 3 * h, 4 * h, 4 * h + i_size, 5 * h + i_size};
+        const size_t len[] = {h, h, h, h, i_size, h, h};
+        for (size_t l = 0; l < layers; ++l)
+            for (int k = 0; k < 7; ++k) rec->fn(rec->user, int(l), names[k], v.data() + l * per + off[k], int64_t(len[k]));
+        std::vector<float> out;
+        if (greedy_rows) {
+            picked = read_picks(0, 1);
+        } else {
+            out = logits.read(size_t(model->config.vocab_size));
+        }
+        rec->fn(rec->user, int(layers) - 1, "normalized", v.data() + layers * per, int64_t(h));
+        if (!out.empty()) rec->fn(rec->user, int(layers) - 1, "logits", out.data(), int64_t(out.size()));
         position += 1;
         return out;
     }
@@ -941,6 +974,12 @@ struct QeRun {
         const Api* a = api();
         if (plan && edits.empty() && t == 1 && !rec && logit_rows == 1 && snapshot_rows == 0 && pick_slot == 0) {
             auto out = forward_planned(ids[0]);
+            logits_unread = greedy_rows;
+            return out;
+        }
+        if (plan && edits.empty() && a->decode_step_capture && t == 1 && rec && logit_rows == 1 &&
+            snapshot_rows == 0 && pick_slot == 0) {
+            auto out = forward_planned_capture(ids[0], rec);
             logits_unread = greedy_rows;
             return out;
         }

@@ -31,6 +31,7 @@ NO_EMBED_ROWS = 128
 NO_PREPARED_GEMM = 256
 NO_PLAIN_DECODE_LAUNCH = 512  # one-launch decode steps launched cooperatively
 NO_DECODE_ROWS = 1024  # verify rows one launch each instead of qr_decode_rows
+NO_DECODE_CAPTURE = 2048  # captured steps on the op sequence instead of qr_decode_step_capture
 
 # Every entry point of include/qwen_bridge.h.
 BRIDGE_SYMBOLS = [
@@ -41,6 +42,7 @@ BRIDGE_SYMBOLS = [
     "qr_gemm_f32_group", "qr_gemm_f32_glu", "qr_gemm_f32_add_norm", "qr_profile", "qr_profile_read",
     "qr_decode_plan", "qr_decode_step", "qr_decode_steps", "qr_decode_step_row", "qr_decode_plan_free",
     "qr_embed_rows", "qr_argmax_fixed", "qr_gemm_f32_prepare", "qr_gemm_f32_release", "qr_decode_rows",
+    "qr_decode_step_capture",
 ]
 
 _F = ctypes.POINTER(ctypes.c_float)

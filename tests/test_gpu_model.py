@@ -232,6 +232,49 @@ def test_qwen08b_short_greedy(qwen08b):
             parity(run.state(layer, which), s.part(layer, which), where=f"0.8B state {layer}/{which}")
 
 
+@pytest.mark.parametrize("fmt", [E.F32, E.BF16_EXACT])
+def test_qwen08b_capture_on_the_one_launch_step(qwen08b, qwen08b_models, fmt):
+    """A captured step keeps the one-launch kernel (qr_decode_step_capture):
+    every per-layer record of the 0.8B shape (input norm, mixer output,
+    residual, post norm, FFN product, FFN output, layer output) and the final
+    norm against the oracle's trace of the same step and against the op
+    sequence's capture, within the fp32 bound, in the op sequence's order; the
+    logits equal the uncaptured step's bit for bit (the records are extra
+    stores of the same kernel)."""
+    c, w0 = qwen08b
+    w = w0 if fmt == E.F32 else bf16_weights(c, w0)
+    fast = qwen08b_models[0] if fmt == E.F32 else E.Model(w, fmt=fmt)
+    ops = E.Model(w, fmt=fmt, disable=E.NO_DECODE_STEP)
+    prompt = [int(v) for v in np.random.default_rng(21).integers(0, c.vocab_size, 5)]
+    s = O.Oracle(w).new_state()
+    for t in prompt:
+        s.step(t, O.VECTOR)
+    run, ref, plain = (m.new_run(32, chunk=8) for m in (fast, ops, fast))
+    assert run.decode_plan
+    for r in (run, ref, plain):
+        r.prefill(prompt)
+    for i, tok in enumerate((7, 123456)):
+        print(f"captured one-launch step {i}, format {fmt}", flush=True)
+        fast.profile(True)
+        logits, rec = run.step(tok, capture=True)
+        stats = fast.profile_read()
+        fast.profile(False)
+        assert "decode_step_capture" in stats, stats
+        want, orec = s.step(tok, O.VECTOR, trace=True)
+        _, rrec = ref.step(tok, capture=True)
+        assert [(l, n) for (l, n, _) in rec] == [(l, n) for (l, n, _) in rrec]
+        omap = {(l, n): v for (l, n, v) in orec}
+        names = dict(NAMES, normalized="final_norm", logits="logits")
+        for (layer, name, v), (_, _, rv) in zip(rec, rrec):
+            parity(v, omap[(layer, names[name])], where=f"step {i} {layer}.{name} vs oracle")
+            parity(v, rv, where=f"step {i} {layer}.{name} vs op sequence")
+        assert np.array_equal(logits, plain.step(tok))
+        parity(logits, want, where=f"step {i} logits")
+    ops.close()
+    if fmt != E.F32:
+        fast.close()
+
+
 def test_qwen08b_bf16_one_launch(qwen08b):
     """The 0.8B-shaped model with BF16-exact weights (every matrix, the
     embedding and the tied LM head uploaded as BF16, the reference's deployed
