@@ -43,7 +43,10 @@ enum QeDisable {
     QE_NO_PLAIN_DECODE_LAUNCH = 512, /* one-launch decode steps launched cooperatively
                                         (qr_set_option "decode_cooperative"; without it: no plan) */
     QE_NO_DECODE_ROWS = 1024, /* qr_decode_rows (verify rows: one launch per row instead) */
-    QE_NO_DECODE_CAPTURE = 2048 /* qr_decode_step_capture (captured steps: the op sequence instead) */
+    QE_NO_DECODE_CAPTURE = 2048, /* qr_decode_step_capture (captured steps: the op sequence instead) */
+    QE_DECODE_RESIDENCY_TEST = 4096 /* qr_set_option "decode_residency_test": every plain one-launch step
+                                       counts as one with a non-resident block, so the plan switches to
+                                       cooperative launches after its first step (the switch, tested) */
 };
 
 /* Record callback of a captured step: (layer, name, values, n). Names follow

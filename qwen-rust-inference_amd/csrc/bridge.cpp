@@ -64,6 +64,11 @@ struct Context {
     // qr_set_option "decode_cooperative": one-launch decode plans made from
     // then on launch cooperatively (default: plain launches)
     bool decode_cooperative = false;
+    // "decode_residency_check" (default 1): a plain-launched plan whose
+    // blocks were not all resident at dispatch switches itself to
+    // cooperative launches; "decode_residency_test" 1: every launch counts
+    // as such (the switch exercised on an idle device)
+    bool decode_residency_auto = true, decode_residency_test = false;
     const float* gate_out = nullptr;
     int gate_d = 0;
     unsigned long gate_serial = 0;
@@ -511,6 +516,14 @@ int qr_set_option(Context* c, const char* name, int value) {
         c->decode_cooperative = value != 0;
         return 0;
     }
+    if (std::strcmp(name, "decode_residency_check") == 0) {
+        c->decode_residency_auto = value != 0;
+        return 0;
+    }
+    if (std::strcmp(name, "decode_residency_test") == 0) {
+        c->decode_residency_test = value != 0;
+        return 0;
+    }
     if (std::strcmp(name, "attention_f16") != 0) return fail(c, "unknown bridge option", -1);
     if (value) return fail(c, "attention_f16 (16-bit prefill attention) is not offered: attention runs in fp32", -1);
     return 0;
@@ -874,12 +887,18 @@ int qr_decode_plan(Context* c, const QrDecodeDesc* d, QrDecodePlan** out) {
         *out = nullptr;
         return fail(c, "decode_cooperative: the device has no cooperative launch", s);
     }
+    qr::decode_plan_residency(*out, c->decode_residency_test ? 0 : -1, c->decode_residency_auto);
     return 0;
+}
+// The profile label of a plan's launches.
+static std::string step_label(QrDecodePlan* p, const char* what) {
+    qr::decode_plan_refresh(p);
+    return std::string(what) + (qr::decode_plan_is_cooperative(p) ? " cooperative" : "");
 }
 int qr_decode_step(Context* c, QrDecodePlan* p, int token, int position) {
     ++c->serial;
     if (!p) return fail(c, "decode step without a plan", -1);
-    auto sc = scope(c, [&] { return std::string("decode_step"); });
+    auto sc = scope(c, [&] { return step_label(p, "decode_step"); });
     if (token < 0) return fail(c, "decode step token", -1);
     return launched(c, "decode step", qr::decode_step(p, token, position, -1, c->stream));
 }
@@ -887,7 +906,7 @@ int qr_decode_step_capture(Context* c, QrDecodePlan* p, int token, int position,
     ++c->serial;
     if (!p || !capture) return fail(c, "decode step capture without a plan or buffer", -1);
     if (len < int64_t(qr::decode_capture_floats(p))) return fail(c, "decode step capture buffer too short", -1);
-    auto sc = scope(c, [&] { return std::string("decode_step_capture"); });
+    auto sc = scope(c, [&] { return step_label(p, "decode_step_capture"); });
     if (token < 0) return fail(c, "decode step token", -1);
     return launched(c, "decode step", qr::decode_step(p, token, position, -1, c->stream, 0, 0, capture));
 }
@@ -902,7 +921,7 @@ int qr_decode_rows(Context* c, QrDecodePlan* p, const int32_t* tokens, int n, in
 int qr_decode_step_row(Context* c, QrDecodePlan* p, int token, int position, int row, int snap) {
     ++c->serial;
     if (!p) return fail(c, "decode step without a plan", -1);
-    auto sc = scope(c, [&] { return std::string("decode_step"); });
+    auto sc = scope(c, [&] { return step_label(p, "decode_step"); });
     if (token < 0 || row < 0 || snap < 0) return fail(c, "decode step token / row / snapshot", -1);
     return launched(c, "decode step", qr::decode_step(p, token, position, -1, c->stream, row, snap));
 }
@@ -912,7 +931,7 @@ int qr_decode_steps(Context* c, QrDecodePlan* p, int first_token, int position, 
     int e = qr::decode_history_clear(p, n, c->stream);
     if (e) return launched(c, "decode steps", e);
     for (int k = 0; k < n; ++k) {
-        auto sc = scope(c, [&] { return std::string("decode_step"); });
+        auto sc = scope(c, [&] { return step_label(p, "decode_step"); });
         e = qr::decode_step(p, k == 0 ? first_token : -1, position + k, k, c->stream);
         if (e) return launched(c, "decode steps", e);
     }

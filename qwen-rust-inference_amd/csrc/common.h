@@ -164,6 +164,17 @@ void decode_plan_free(QrDecodePlan* p);
 // Launch the plan's steps cooperatively (on) or as plain launches (off, the
 // default); hipErrorNotSupported when the device has no cooperative launch.
 int decode_plan_cooperative(QrDecodePlan* p, bool on);
+// The residency check of plain launches: a launch whose blocks start `ticks`
+// (100 MHz; < 0: unchanged, default 5000) or more apart sets the plan's
+// flag, and with `automatic` (default) the plan launches cooperatively from
+// its next step on.
+void decode_plan_residency(QrDecodePlan* p, int ticks, bool automatic);
+// True when the plan's steps launch cooperatively (chosen, or switched to by
+// the residency check).
+bool decode_plan_is_cooperative(const QrDecodePlan* p);
+// Applies a set residency flag (the switch to cooperative launches); every
+// launch does this first.
+void decode_plan_refresh(QrDecodePlan* p);
 // token -1: the previous launch's argmax (read on the device). slot >= 0: the
 // step's [argmax, non-finite count] also goes to history slot `slot`.
 // slot >= 0: the chained-steps history slot; row: logits / picks row; snap: snapshot copy (0: none).

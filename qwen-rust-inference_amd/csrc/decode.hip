@@ -119,6 +119,7 @@ struct Scratch {
     f2 pml[NRMAX][NH * SMAX * 2];
     float pacc[NRMAX][NH * SMAX * HD];
     f2 lmpart[NRMAX][NW * 4];  // (max, index, non-finite count, unused) per wave
+    f2 start[BLOCKS];  // (low word of the block's start time, tag) of this launch
     unsigned lmpool[4];  // lm_head chunk counters: [epoch & 1] this launch's, the other reset for the next
 };
 #define SOFF(field) unsigned(offsetof(::qr::dec::Scratch, field))
@@ -138,6 +139,9 @@ struct Args {
     int chain;     // 1: the token is the previous launch's argmax (picks[0]), not `token`
     float* hist;   // when set: this launch's [argmax, non-finite count] also lands here
     float* cap;    // when set (one-row steps): the step's per-layer records land here (capture layout below)
+    unsigned* late;        // host-mapped flag: set when the blocks' start times spread by >= late_ticks
+    unsigned late_ticks;   // (100 MHz ticks: a block that was not resident when the grid was dispatched)
+    unsigned late_mask;    // launches with (epoch & late_mask) == 0 check (the check costs ~7 us)
     int snap;      // > 0: the updated DeltaNet conv and recurrent states are also written to this snapshot copy
     unsigned epoch;
     float eps;
@@ -290,10 +294,15 @@ struct Lds {
     int lmnext;  // the next lm_head row group of the block's range to hand out
     int lmchunk;  // the pool chunk the block streams now
     int lmctr[2];  // the next row group of that chunk, by chunk parity
+    unsigned start;  // low word of this block's start time
 };
 constexpr int kNoFail = 0x7fffffff;
 
 constexpr unsigned long long kTimeout = 50000000ull;  // 0.5 s at 100 MHz
+// Start-time spread of a launch's blocks that marks a block as not resident
+// at dispatch (a whole grid starts within a few us on an idle device).
+constexpr unsigned kLateTicks = 5000;  // 50 us at 100 MHz
+constexpr unsigned kLateEvery = 16;    // launches per check (power of two)
 
 __device__ void record_failure(const Args& a, Lds& l, int p) {
     stx(rsrc(a.picks), 4, 1e30f);
@@ -966,6 +975,10 @@ __device__ __forceinline__ void glu_load(LayerP w, int u, f4* wb);
 template <int W, int NR>
 __device__ __forceinline__ bool phase_dout(const Args& a, Rs rs, LayerP w, int L, int p, int u, f4* wb, Lds& l,
                                            int nr) {
+    // the residual add is not fused with an int8 row's scale multiply: the
+    // one-row and multi-row kernels must round it alike whatever else reads
+    // the product
+#pragma clang fp contract(on)
     const int par = p & 1;
     {
         const unsigned th = unsigned(thread_id<NR>());
@@ -1089,6 +1102,10 @@ __device__ __forceinline__ void touch_record(LayerP w) {
 template <int W, int NR>
 __device__ __forceinline__ bool phase_down(const Args& a, Rs rs, LayerP w, LayerP next, int L, int p, int u, f4* wb,
                                            Lds& l, int nr) {
+    // the residual add is not fused with an int8 row's scale multiply: the
+    // one-row and multi-row kernels must round it alike whatever else reads
+    // the product
+#pragma clang fp contract(on)
     const int par = p & 1;
     stage_tagged<NR * I, NR>(
         a, rs, SOFF(product), tag(a, p - 1), l.act[par], l, p,
@@ -1546,6 +1563,10 @@ __device__ __forceinline__ bool phase_comb(const Args& a, Rs rs, int p, int u, L
 // ---- T_O: after = x + o . ctx
 template <int W, int NR>
 __device__ __forceinline__ bool phase_o(const Args& a, Rs rs, int L, int p, int u, const f4* wb, Lds& l, int nr) {
+    // the residual add is not fused with an int8 row's scale multiply: the
+    // one-row and multi-row kernels must round it alike whatever else reads
+    // the product
+#pragma clang fp contract(on)
     const int par = p & 1;
     stage_tagged<NR * NH * HD, NR>(a, rs, SOFF(ctx), tag(a, p - 1), l.act[par], l, p, NoMid(), nr * (NH * HD / 2));
     if (!bsync(l, p)) return false;
@@ -1929,6 +1950,23 @@ __device__ __forceinline__ void prefetch_layer(const Args& a, int L, int u, f4* 
     }
 }
 
+// Residency check (the last block, after its lm_head rows): every block
+// stamped its start time (tag of phase -1) on entry; a block that started
+// late_ticks or more away from this one was not resident when the grid was
+// dispatched (another kernel held its CU: the others' polls waited for it).
+// The host-mapped flag then tells the host to launch this plan's next steps
+// cooperatively, where the runtime guarantees residency. Each stamp was
+// written before its block's first output, which this block has since read,
+// so the stamps are visible (a tag that does not match is skipped).
+__device__ __forceinline__ void check_residency(const Args& a, Rs rs, Lds& l) {
+    const int t = int(threadIdx.x);
+    if (t >= BLOCKS) return;
+    const f2 v = ldx2(rs, SOFF(start) + 8u * unsigned(t));
+    if (__float_as_uint(v.y) != tag(a, -1)) return;
+    const int d = int(__float_as_uint(v.x) - l.start);
+    if (unsigned(d < 0 ? -d : d) >= a.late_ticks) buffer_store_f32(__uint_as_float(1u), rsrc(a.late), 0, 0, kSys);
+}
+
 // Phase p (the tag index) runs, per DeltaNet layer, DIN MIX DOUT GLU DOWN and,
 // per attention layer, AQKV ATTN COMB O GLU DOWN, then LM and ARG: per layer
 // straight-line code, so the prefetch buffer flows from each phase into the
@@ -1945,7 +1983,13 @@ __global__ __launch_bounds__(THREADS, 1) void decode_kernel(Args a) {
     // descriptors derived from it in SGPRs)
     const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x >> 6));
     const int unit = wave * BLOCKS + int(blockIdx.x);  // rows spread wave-major over blocks
+    const bool residency = a.late && (a.epoch & a.late_mask) == 0;
     if (threadIdx.x == 0) {
+        if (residency) {
+            const unsigned t0 = unsigned(wall_clock64());
+            l.start = t0;
+            stt(rsrc(a.s), SOFF(start) + 8u * blockIdx.x, __uint_as_float(t0), tag(a, -1));
+        }
         l.fail = kNoFail;
         l.lmnext = WAVES;  // groups 0 .. WAVES - 1 are the waves' first, prefetched ones
         if (blockIdx.x == 0)  // the next launch's lm_head chunk counter (this launch uses the other)
@@ -2023,6 +2067,8 @@ __global__ __launch_bounds__(THREADS, 1) void decode_kernel(Args a) {
     out_barrier();
     prefetch_lm<W>(a, opaque_uniform(unit), wb);
     if (!phase_lm<W, NR>(a, rs, p, opaque_uniform(unit), wb, l, nr)) return;
+    // the last block takes no argmax row: its check runs beside the argmax
+    if (blockIdx.x == BLOCKS - 1 && residency) check_residency(a, rs, l);
     ++p;
     if (NR == 1) {
         if (blockIdx.x == 0) phase_arg(a, rs, p, l);
@@ -2049,6 +2095,8 @@ struct QrDecodePlan {
     int fmt = 0;  // matrix format of every layer matrix and the LM head: decode_kernel<fmt, *> (dec::WF32 / WB16 / WQ8)
     bool rows_ok = false;  // the multi-row kernel fits the device (decode_rows)
     bool cooperative = false;  // launched with hipLaunchCooperativeKernel instead of a plain launch
+    unsigned* late_host = nullptr;  // host-mapped residency flag (set by a launch whose blocks started apart)
+    bool auto_cooperative = true;   // a set flag switches the plan to cooperative launches
     float* hist = nullptr;  // [capacity][argmax, non-finite count] of chained steps
 };
 
@@ -2167,6 +2215,14 @@ int decode_plan_create(const QrDecodeDesc& d, QrDecodePlan** out, hipStream_t s,
     hipError_t e = hipMalloc(reinterpret_cast<void**>(&p->layers), sizeof(QrDecodeLayer) * size_t(d.layers));
     if (e == hipSuccess) e = scratch_acquire(dev, s, &p->scratch, &epoch);
     if (e == hipSuccess) e = hipMalloc(reinterpret_cast<void**>(&p->hist), sizeof(float) * 2 * size_t(d.capacity));
+    // the residency flag: pinned, mapped host memory the kernel writes and the
+    // host reads before the next launch
+    unsigned* late_dev = nullptr;
+    if (e == hipSuccess) e = hipHostMalloc(reinterpret_cast<void**>(&p->late_host), sizeof(unsigned), hipHostMallocMapped);
+    if (e == hipSuccess) {
+        *p->late_host = 0;
+        e = hipHostGetDevicePointer(reinterpret_cast<void**>(&late_dev), p->late_host, 0);
+    }
     p->args.epoch = epoch;  // what decode_plan_free hands back with the buffer
     // RoPE denominators theta^(2i / rot) by the host libm (the reference's
     // expression, src/attention.rs:49-50), as the op path's table
@@ -2192,6 +2248,9 @@ int decode_plan_create(const QrDecodeDesc& d, QrDecodePlan** out, hipStream_t s,
     a.emb_bf16 = d.embedding_bf16 ? 1 : 0;
     a.eps = d.eps;
     a.epoch = epoch;
+    a.late = late_dev;
+    a.late_ticks = kLateTicks;
+    a.late_mask = kLateEvery - 1;
     // the phase list the kernel walks (tags are phase indices): per DeltaNet
     // layer DIN MIX DOUT GLU DOWN, per attention layer AQKV ATTN COMB O GLU
     // DOWN, then LM and ARG
@@ -2200,6 +2259,21 @@ int decode_plan_create(const QrDecodeDesc& d, QrDecodePlan** out, hipStream_t s,
     return 0;
 }
 
+bool decode_plan_is_cooperative(const QrDecodePlan* p) { return p->cooperative; }
+void decode_plan_refresh(QrDecodePlan* p) {
+    // a previous launch found a block that was not resident: the device is
+    // shared, so residency is left to the runtime from now on
+    if (!p->cooperative && p->auto_cooperative && p->late_host && __atomic_load_n(p->late_host, __ATOMIC_RELAXED) &&
+        decode_plan_cooperative(p, true) != 0)
+        p->auto_cooperative = false;  // no cooperative launch on this device: stay plain
+}
+void decode_plan_residency(QrDecodePlan* p, int ticks, bool automatic) {
+    if (ticks >= 0) {
+        p->args.late_ticks = unsigned(ticks);
+        p->args.late_mask = ticks == 0 ? 0u : dec::kLateEvery - 1;  // the test setting checks every launch
+    }
+    p->auto_cooperative = automatic;
+}
 int decode_plan_cooperative(QrDecodePlan* p, bool on) {
     if (on) {
         int dev = 0, coop = 0;
@@ -2213,6 +2287,7 @@ int decode_plan_cooperative(QrDecodePlan* p, bool on) {
 
 void decode_plan_free(QrDecodePlan* p) {
     if (!p) return;
+    if (p->late_host) (void)hipHostFree(p->late_host);
     if (p->layers) (void)hipFree(p->layers);
     if (p->hist) (void)hipFree(p->hist);
     if (p->scratch) scratch_release(p->device, p->scratch, p->args.epoch);
@@ -2237,6 +2312,7 @@ static int launch(QrDecodePlan* p, hipStream_t s, bool rows) {
         a.epoch = 1;
         if (hipError_t e = hipMemsetAsync(p->scratch, 0, sizeof(Scratch), s)) return int(e);
     }
+    decode_plan_refresh(p);
     void* args[] = {&a};
     const void* k = reinterpret_cast<const void*>(decode_kernel_for(p->fmt, rows));
     return p->cooperative ? int(hipLaunchCooperativeKernel(k, dim3(BLOCKS), dim3(THREADS), args, 0, s))

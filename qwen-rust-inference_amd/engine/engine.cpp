@@ -205,6 +205,10 @@ struct Api {
         int status = create(&c);
         require(status == 0 && c, "bridge context creation failed, status=" + std::to_string(status));
         ctx = c;
+        if ((disable & QE_DECODE_RESIDENCY_TEST) && decode_plan) {
+            auto set_option = symbol<int (*)(Context*, const char*, int)>("qr_set_option", false);
+            if (!set_option || set_option(ctx, "decode_residency_test", 1) != 0) decode_plan = nullptr;
+        }
         if ((disable & QE_NO_PLAIN_DECODE_LAUNCH) && decode_plan) {
             auto set_option = symbol<int (*)(Context*, const char*, int)>("qr_set_option", false);
             if (!set_option || set_option(ctx, "decode_cooperative", 1) != 0) decode_plan = nullptr;

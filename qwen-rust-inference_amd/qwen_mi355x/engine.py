@@ -32,6 +32,7 @@ NO_PREPARED_GEMM = 256
 NO_PLAIN_DECODE_LAUNCH = 512  # one-launch decode steps launched cooperatively
 NO_DECODE_ROWS = 1024  # verify rows one launch each instead of qr_decode_rows
 NO_DECODE_CAPTURE = 2048  # captured steps on the op sequence instead of qr_decode_step_capture
+DECODE_RESIDENCY_TEST = 4096  # every plain one-launch step reads as non-resident: cooperative from the second on
 
 # Every entry point of include/qwen_bridge.h.
 BRIDGE_SYMBOLS = [

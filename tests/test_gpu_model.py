@@ -541,6 +541,39 @@ def test_qwen08b_cooperative_launch_equals_plain(qwen08b, qwen08b_models):
     coop.close()
 
 
+def test_qwen08b_residency_check_switches_to_cooperative(qwen08b, qwen08b_models):
+    """The plain launch's residency check: a step whose blocks did not all
+    start together (forced here from the host: qr_set_option
+    "decode_residency_test" makes every start spread count) sets the plan's
+    flag, and its next steps launch cooperatively, where the runtime
+    guarantees residency. The switch changes no result: logits, IDs and states
+    equal the plain plan's bit for bit."""
+    c, w = qwen08b
+    plain, _ = qwen08b_models
+    test = E.Model(w, disable=E.DECODE_RESIDENCY_TEST)
+    prompt = [int(v) for v in np.random.default_rng(17).integers(0, c.vocab_size, 20)]
+    runs = [m.new_run(64, chunk=32) for m in (plain, test)]
+    assert all(r.decode_plan for r in runs)
+    first = [O.select_greedy(r.prefill(prompt)) for r in runs]
+    assert first[0] == first[1]
+    test.profile(True)
+    logits = [r.step(first[0]) for r in runs]
+    after = [r.step(7) for r in runs]
+    stats = test.profile_read()
+    test.profile(False)
+    assert stats.get("decode_step", (0, 0))[0] == 1, stats
+    assert stats.get("decode_step cooperative", (0, 0))[0] == 1, stats
+    assert np.array_equal(logits[0], logits[1]) and np.array_equal(after[0], after[1])
+    ids = [r.decode_greedy(O.select_greedy(after[0]), 6)[0] for r in runs]
+    assert ids[0] == ids[1]
+    for layer in (0, 3, 23):
+        for which in range(4):
+            assert np.array_equal(runs[0].state(layer, which), runs[1].state(layer, which)), (layer, which)
+    for r in runs:
+        r.close()
+    test.close()
+
+
 @pytest.mark.parametrize("fmt", [E.F32, E.INT8])
 def test_qwen08b_verify_rows_equal_decode_steps(qwen08b, qwen08b_models, fmt):
     """Verify rows on the one-launch path: each row is a launch of the decode
