@@ -48,7 +48,7 @@ for p in (str(ROOT / "qwen-rust-inference_amd"), str(ROOT / "oracle")):
 HBM_PEAK_GBS = 8000.0
 # HBM bytes per decode_kernel launch at ctx ~475 from the rocprofv3 FETCH_SIZE / WRITE_SIZE passes
 # (FETCH_SIZE x 2.0, WRITE_SIZE x 1.0, calibrated on a 512 MiB copy; profiles/decode_kernel_config2.md).
-DECODE_TRAFFIC_BYTES = 3_154_417_600
+DECODE_TRAFFIC_BYTES = 3_154_785_217
 PREFILL_CHUNK = 128  # the reference engine's prefill chunk (src/device.rs)
 
 
