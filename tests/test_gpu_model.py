@@ -89,6 +89,28 @@ def test_tiny_config1_greedy_bit_exact(tiny):
             parity(run.state(layer, which), s.part(layer, which), where=f"state {layer}/{which}")
 
 
+def test_tiny_teacher_forced_walk(tiny):
+    """Config 1 fed 48 random ids after its prompt (its greedy continuation is
+    a fixed point for every prompt, so greedy ids alone discriminate little):
+    every step's logits within the fp32 bound of the oracle's and the same
+    pick (near-tie rule: none of the walk's steps is within twice the bound)."""
+    c, w = tiny
+    ids = tiny_prompt()
+    walk = [int(v) for v in np.random.default_rng(101).integers(0, c.vocab_size, 48)]
+    s = O.Oracle(w).new_state()
+    for t in ids:
+        s.step(t, O.VECTOR)
+    run = E.Model(w).new_run(96, chunk=16)
+    run.prefill(ids)
+    for i, t in enumerate(walk):
+        want = s.step(t, O.VECTOR)
+        got = run.step(t)
+        parity(got, want, where=f"walk step {i}")
+        top = np.sort(want)[-2:]
+        if top[1] - top[0] > 2e-4 * (abs(top[1]) + float(np.sqrt(np.mean(want * want)))):
+            assert O.select_greedy(got) == O.select_greedy(want), i
+
+
 def test_tiny_fused_and_unfused_paths_agree(tiny):
     """Every optional symbol switched off gives the same results (the
     reference's fallbacks, src/device.rs:368-441)."""
