@@ -264,6 +264,16 @@ __device__ __forceinline__ float lanes_sum(float v) {
 __device__ __forceinline__ float wave_total(float v) { return lanes_sum<64>(v); }
 // Sum over the four lanes of equal lane % 16.
 __device__ __forceinline__ float column_sum(float v) { return xor_sum<32>(xor_sum<16>(v)); }
+__device__ __forceinline__ unsigned min_u32_from(unsigned v, float other) { return min(v, __float_as_uint(other)); }
+// Minimum of an unsigned over the wave (every lane gets it).
+__device__ __forceinline__ unsigned wave_min_u32(unsigned v) {
+    v = min_u32_from(v, dpp<kQuadXor1>(__uint_as_float(v)));
+    v = min_u32_from(v, dpp<kQuadXor2>(__uint_as_float(v)));
+    v = min_u32_from(v, dpp<kRowHalfMirror>(__uint_as_float(v)));
+    v = min_u32_from(v, dpp<kRowMirror>(__uint_as_float(v)));
+    v = min_u32_from(v, lane_xor<16>(__uint_as_float(v)));
+    return min_u32_from(v, lane_xor<32>(__uint_as_float(v)));
+}
 __device__ __forceinline__ float wave_maximum(float v) {
     v = fmaxf(v, dpp<kQuadXor1>(v));
     v = fmaxf(v, dpp<kQuadXor2>(v));
@@ -1607,35 +1617,104 @@ __device__ __forceinline__ void lm_load(Rs lm, int row0, int row_end, int vocab,
             }
         }
 }
-// One lm_head row's logit from its dot-product partial: stored for rows
-// t < nr, folded into row t's running (max, first index, non-finite count).
-template <int NR>
-__device__ __forceinline__ void lm_take(Rs lg, float acc, int t, int row, int vocab, int nr, float (&best)[NR],
-                                        unsigned (&at)[NR], unsigned (&bad)[NR]) {
-    if (lane_id() == 0 && t < nr) stp(lg, 4u * (unsigned(t) * unsigned(vocab) + unsigned(row)), acc);
-    if (!isfinite(acc)) {
-        ++bad[t];
-    } else if (acc > best[t]) {
-        best[t] = acc;
-        at[t] = unsigned(row);
-    }
+// The lm_head rows of a group are summed transposed: a lane holds V = LM_G NR
+// partial dot products (value j = t LM_G + r: row r of the group against
+// input row t), and the wave sums all of them at once with a butterfly whose
+// first steps halve the values a lane holds (partners l ^ 32 and l ^ 16 by
+// the permlane swaps, then the row mirror l ^ 15 and the half mirror l ^ 7 by
+// DPP) and whose last steps are plain sums (l ^ 2, l ^ 1; and the mirrors
+// when V < 16). Every value meets its partners in the same order whatever V
+// is (a + b = b + a in IEEE arithmetic), so a one-row and a multi-row step sum
+// each logit alike; against one wave sum per value (8 VALU operations each)
+// this takes 10 operations for 4 values and 35 for 16. Afterwards lane l
+// holds the total of value lm_vidx(l).
+template <int V>
+__device__ __forceinline__ unsigned lm_vidx(unsigned lane) {
+    unsigned j = 0;
+    if constexpr (V >= 2) j += (lane >> 5 & 1) * (V / 2);
+    if constexpr (V >= 4) j += (lane >> 4 & 1) * (V / 4);
+    if constexpr (V >= 8) j += (lane >> 3 & 1) * (V / 8);
+    if constexpr (V >= 16) j += (lane >> 2 & 1) * (V / 16);
+    return j;
 }
+// Lanes whose total is the one they report: one per value (the lowest lane
+// of each group that holds it).
+template <int V>
+__device__ __forceinline__ bool lm_owner(unsigned lane) {
+    return V >= 16 ? (lane & 3) == 0 : (lane & 15) == 0;
+}
+template <int V>
+__device__ __forceinline__ float lm_sums(float (&v)[V]) {
+    static_assert(V == 4 || V == 16, "4 or 16 values per lane");
+    const unsigned lane = lane_id();
+#pragma unroll
+    for (int i = 0; i < V / 2; ++i) {  // l ^ 32: lanes < 32 keep values i, the others i + V / 2
+        const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v[i]), __float_as_uint(v[i + V / 2]), false,
+                                                        false);
+        v[i] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    }
+#pragma unroll
+    for (int i = 0; i < V / 4; ++i) {  // l ^ 16: even 16-lane rows keep i, odd ones i + V / 4
+        const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v[i]), __float_as_uint(v[i + V / 4]), false,
+                                                        false);
+        v[i] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    }
+    if constexpr (V >= 16) {
+        const bool b3 = (lane & 8) != 0, b2 = (lane & 4) != 0;
+#pragma unroll
+        for (int i = 0; i < V / 8; ++i) {  // l ^ 15: lanes 0-7 of a row keep i, 8-15 i + V / 8
+            const float src = b3 ? v[i] : v[i + V / 8], keep = b3 ? v[i + V / 8] : v[i];
+            v[i] = keep + dpp<kRowMirror>(src);
+        }
+        {  // l ^ 7: lanes 0-3 of each 8 keep value 0, 4-7 value 1
+            const float src = b2 ? v[0] : v[1], keep = b2 ? v[1] : v[0];
+            v[0] = keep + dpp<kRowHalfMirror>(src);
+        }
+    } else {
+        v[0] += dpp<kRowMirror>(v[0]);
+        v[0] += dpp<kRowHalfMirror>(v[0]);
+    }
+    v[0] += dpp<kQuadXor2>(v[0]);
+    v[0] += dpp<kQuadXor1>(v[0]);
+    return v[0];
+}
+// A lane's running (max, first row of it, non-finite count) over the values it
+// reports, for its input row (lm_vidx(lane) / LM_G).
+struct LmBest {
+    float best;
+    unsigned at, bad;
+};
 // The LM_G rows of a group against the step's inputs (row t's logits at
-// t vocab; rows >= nr computed, not stored), in the per-lane order of the
-// one-row step: one-row steps with the input in registers; multi-row int8
-// steps unpack each weight row once and take the NR inputs from registers
-// (xv[t]); multi-row fp32 steps walk the inputs in the outer loop, each read
-// once per group from LDS (xn: row t at t H, in the lane layout of
-// normed_chunks). Each input row's maxima are taken in row order.
+// t vocab; rows >= nr computed, not stored), each lane's partial sums in the
+// per-lane order of the one-row step: one-row steps with the input in
+// registers; multi-row BF16 / int8 steps unpack each weight row once and take
+// the NR inputs from registers (xv[t]); multi-row fp32 steps walk the inputs
+// in the outer loop, each read once per group from LDS (xn: row t at t H, in
+// the lane layout of normed_chunks). Then the transposed sums, the int8 row
+// scale after the sum, one store per value and the lane's running maximum.
 template <int W, int NR, int NX>
 __device__ __forceinline__ void lm_rows(Rs lg, const f4* buf, const f4 (&xv)[NX][4], const float* xn, int row0,
-                                        int row_end, int vocab, int nr, float (&best)[NR], unsigned (&at)[NR],
-                                        unsigned (&bad)[NR]) {
-    if constexpr (NR > 1 && W != WF32) {
+                                        int row_end, int vocab, int nr, LmBest& lb) {
+    constexpr int V = LM_G * NR;
+    const unsigned lane = lane_id();
+    float v[V];
+    if constexpr (W == WF32) {
+#pragma unroll
+        for (int t = 0; t < NR; ++t) {
+            f4 x[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) x[q] = NR == 1 ? xv[0][q] : lds4(xn + t * H + 4 * (lane + 64 * q));
+#pragma unroll
+            for (int r = 0; r < LM_G; ++r) {
+                float acc = 0.f;
+#pragma unroll
+                for (int q = 0; q < 4; ++q) acc = fdot4(buf[r * 4 + q], x[q], acc);
+                v[t * LM_G + r] = acc;
+            }
+        }
+    } else {
 #pragma unroll
         for (int r = 0; r < LM_G; ++r) {
-            const int row = row0 + r;
-            if (row >= row_end) continue;
             float wf[16];  // the row's 16 weights of this lane, in the one-row step's order
             if constexpr (W == WQ8) {
 #pragma unroll
@@ -1657,45 +1736,25 @@ __device__ __forceinline__ void lm_rows(Rs lg, const f4* buf, const f4 (&xv)[NX]
 #pragma unroll
                 for (int j = 0; j < 4; ++j)
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) acc = fmaf(wf[4 * j + e], xv[t][j][e], acc);
-                acc = wave_total(acc);
-                if constexpr (W == WQ8) acc = buf[r * 4 + 1].x * acc;
-                lm_take<NR>(lg, acc, t, row, vocab, nr, best, at, bad);
+                    for (int e = 0; e < 4; ++e) acc = fmaf(wf[4 * j + e], xv[NX == 1 ? 0 : t][j][e], acc);
+                v[t * LM_G + r] = acc;
             }
         }
-    } else if constexpr (NR > 1) {
-        const unsigned lane = lane_id();
-#pragma unroll
-        for (int t = 0; t < NR; ++t) {
-            f4 x[4];
-#pragma unroll
-            for (int v = 0; v < 4; ++v) x[v] = lds4(xn + t * H + 4 * (lane + 64 * v));
-#pragma unroll
-            for (int r = 0; r < LM_G; ++r) {
-                const int row = row0 + r;
-                if (row >= row_end) continue;
-                float acc = 0.f;
-#pragma unroll
-                for (int v = 0; v < 4; ++v) acc = fdot4(buf[r * 4 + v], x[v], acc);
-                lm_take<NR>(lg, wave_total(acc), t, row, vocab, nr, best, at, bad);
-            }
-        }
-    } else {
-#pragma unroll
-        for (int r = 0; r < LM_G; ++r) {
-            const int row = row0 + r;
-            if (row >= row_end) continue;
-            float acc = 0.f;
-            if constexpr (W == WQ8) {
-                acc = buf[r * 4 + 1].x * wave_total(q8dot(buf[r * 4], xv[0], acc));
-            } else if constexpr (W == WB16) {
-                acc = wave_total(b16dot(buf[r * 4 + 1], xv[0][2], xv[0][3], b16dot(buf[r * 4], xv[0][0], xv[0][1], acc)));
-            } else {
-#pragma unroll
-                for (int v = 0; v < 4; ++v) acc = fdot4(buf[r * 4 + v], xv[0][v], acc);
-                acc = wave_total(acc);
-            }
-            lm_take<NR>(lg, acc, 0, row, vocab, nr, best, at, bad);
+    }
+    float acc = lm_sums<V>(v);
+    const unsigned j = lm_vidx<V>(lane);
+    const int r = int(j % LM_G), t = int(j / LM_G), row = row0 + r;
+    if constexpr (W == WQ8) {
+        const float s0 = buf[1].x, s1 = buf[5].x, s2 = buf[9].x, s3 = buf[13].x;
+        acc = (r == 0 ? s0 : r == 1 ? s1 : r == 2 ? s2 : s3) * acc;
+    }
+    if (lm_owner<V>(lane) && row < row_end) {
+        if (t < nr) stp(lg, 4u * (unsigned(t) * unsigned(vocab) + unsigned(row)), acc);
+        if (!isfinite(acc)) {
+            ++lb.bad;
+        } else if (acc > lb.best) {
+            lb.best = acc;
+            lb.at = unsigned(row);
         }
     }
 }
@@ -1736,19 +1795,18 @@ __device__ __forceinline__ int lm_grab(int* ctr, int first) {
 // every later one does too.
 template <int W, int NR, int NX>
 __device__ __forceinline__ void lm_stream(Rs lm, Rs lg, const f4 (&xv)[NX][4], const float* xn, int first, int last,
-                                          int vocab, int nr, int* ctr, bool pre, f4* wb, f4* nb, float (&best)[NR],
-                                          unsigned (&at)[NR], unsigned (&bad)[NR]) {
+                                          int vocab, int nr, int* ctr, bool pre, f4* wb, f4* nb, LmBest& lb) {
     int c0 = first + LM_G * int(threadIdx.x >> 6);
     if (!pre) lm_load<W>(lm, c0, last, vocab, wb);
     int c1 = lm_grab(ctr, first);
     lm_load<W>(lm, c1, last, vocab, nb);
     for (;;) {
         if (c0 >= last) break;
-        lm_rows<W, NR, NX>(lg, wb, xv, xn, c0, last, vocab, nr, best, at, bad);
+        lm_rows<W, NR, NX>(lg, wb, xv, xn, c0, last, vocab, nr, lb);
         if (c1 >= last) break;
         c0 = lm_grab(ctr, first);
         lm_load<W>(lm, c0, last, vocab, wb);
-        lm_rows<W, NR, NX>(lg, nb, xv, xn, c1, last, vocab, nr, best, at, bad);
+        lm_rows<W, NR, NX>(lg, nb, xv, xn, c1, last, vocab, nr, lb);
         if (c0 >= last) break;
         c1 = lm_grab(ctr, first);
         lm_load<W>(lm, c1, last, vocab, nb);
@@ -1791,16 +1849,9 @@ __device__ __forceinline__ bool phase_lm(const Args& a, Rs rs, int p, int u, f4*
     int first, last;
     lm_block_range(u, a.vocab, first, last);
     const Rs lm = rsrc(a.lm_head), lg = rsrc(a.logits);
-    float best[NR];
-    unsigned at[NR], bad[NR];
-#pragma unroll
-    for (int t = 0; t < NR; ++t) {
-        best[t] = -INFINITY;
-        at[t] = 0xffffffffu;
-        bad[t] = 0;
-    }
+    LmBest lb{-INFINITY, 0xffffffffu, 0u};
     f4 nb[4 * LM_G];
-    lm_stream<W, NR, NX>(lm, lg, xv, xn, first, last, a.vocab, nr, &l.lmnext, true, wb, nb, best, at, bad);
+    lm_stream<W, NR, NX>(lm, lg, xv, xn, first, last, a.vocab, nr, &l.lmnext, true, wb, nb, lb);
     // then pool chunks, in increasing row order like the range (so a wave's
     // first maximum is its lowest index): thread 0 takes the block's next
     // chunk between two block barriers (the waves are done with the previous
@@ -1819,16 +1870,22 @@ __device__ __forceinline__ bool phase_lm(const Args& a, Rs rs, int p, int u, f4*
         if (c >= nchunks) break;
         const int cf = srows + c * LMC;
         lm_stream<W, NR, NX>(lm, lg, xv, xn, cf, min(a.vocab, cf + LMC), a.vocab, nr, &l.lmctr[round & 1], false,
-                              wb, nb, best, at, bad);
+                              wb, nb, lb);
     }
-    if (lane_id() == 0) {
+    // the wave's (max, first row of it, non-finite count) per input row from
+    // the lanes that report its values
+    const unsigned lane = lane_id(), mine = lm_vidx<LM_G * NR>(lane) / LM_G;
 #pragma unroll
-        for (int r = 0; r < NR; ++r) {
-            if (r >= nr) break;
+    for (int r = 0; r < NR; ++r) {
+        const bool in = mine == unsigned(r);
+        const float m = wave_maximum(in ? lb.best : -INFINITY);
+        const unsigned at = wave_min_u32(in && lb.best == m ? lb.at : 0xffffffffu);
+        const float bad = wave_total(in ? float(lb.bad) : 0.f);
+        if (lane == 0 && r < nr) {
             const unsigned o = SROW(lmpart, r) + unsigned(u) * 32u, t = tag(a, p);
-            stt(rs, o, best[r], t);
-            stt(rs, o + 8, __uint_as_float(at[r]), t);
-            stt(rs, o + 16, __uint_as_float(bad[r]), t);
+            stt(rs, o, m, t);
+            stt(rs, o + 8, __uint_as_float(at), t);
+            stt(rs, o + 16, __uint_as_float(unsigned(bad)), t);
         }
     }
     return true;
