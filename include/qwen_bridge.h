@@ -256,6 +256,12 @@ int qr_decode_step_capture(Context* c, QrDecodePlan* p, int token, int position,
  * first + n <= the plan's rows, snaps <= its snapshots. No counterpart in the
  * reference's ABI. */
 int qr_decode_rows(Context* c, QrDecodePlan* p, const int32_t* tokens, int n, int position, int first, int snaps);
+/* accept (src/device.rs:1626-1662) of a verify pass in one launch: for every
+ * DeltaNet layer of the plan, snapshot copy `rows` (1..snapshots) of the
+ * recurrent state and of the conv history replaces copy 0, as the engine's
+ * two qr_copy calls per layer would (36 calls at the 0.8B shape). No
+ * counterpart in the reference's ABI. */
+int qr_decode_accept(Context* c, QrDecodePlan* p, int rows);
 void qr_decode_plan_free(Context* c, QrDecodePlan* p);
 
 /* Op 16 (Argmax) without any allocation: the same slot meanings and result

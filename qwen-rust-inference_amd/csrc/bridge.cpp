@@ -918,6 +918,14 @@ int qr_decode_rows(Context* c, QrDecodePlan* p, const int32_t* tokens, int n, in
     if (st == int(hipErrorNotSupported)) return fail(c, "decode rows: the multi-row kernel does not fit this device", st);
     return launched(c, "decode rows", st);
 }
+int qr_decode_accept(Context* c, QrDecodePlan* p, int rows) {
+    ++c->serial;
+    if (!p) return fail(c, "decode accept without a plan", -1);
+    auto sc = scope(c, [&] { return std::string("decode_accept"); });
+    const int st = qr::decode_accept(p, rows, c->stream);
+    if (st == int(hipErrorInvalidValue)) return fail(c, "decode accept: rows beyond the plan's snapshots", st);
+    return launched(c, "decode accept", st);
+}
 int qr_decode_step_row(Context* c, QrDecodePlan* p, int token, int position, int row, int snap) {
     ++c->serial;
     if (!p) return fail(c, "decode step without a plan", -1);

@@ -185,6 +185,9 @@ size_t decode_capture_floats(const QrDecodePlan* p);
 // Up to 4 consecutive tokens in one launch (qr_decode_rows).
 int decode_rows(QrDecodePlan* p, const int* tokens, int n, int position, int first, int snaps, hipStream_t s);
 int decode_history_clear(QrDecodePlan* p, int n, hipStream_t s);
+// accept for every DeltaNet layer of the plan in one launch: snapshot copy
+// `rows` (1..snapshots) of each recurrent state and conv history becomes copy 0.
+int decode_accept(QrDecodePlan* p, int rows, hipStream_t s);
 int decode_history_read(QrDecodePlan* p, int n, float* out, hipStream_t s);
 
 // delta_chunk.hip ------------------------------------------------------------

@@ -2134,6 +2134,24 @@ __global__ __launch_bounds__(THREADS, 1) void decode_kernel(Args a) {
     }
 }
 
+// accept (src/device.rs:1626-1662) for every DeltaNet layer at once: the
+// recurrent state and conv history of snapshot copy `rows` become the current
+// ones (copy 0). Block (x, y) copies float4s x, x + gridDim.x, ... of layer
+// y's two states (attention layers have none).
+constexpr int ACCEPT_THREADS = 256, ACCEPT_BLOCKS = 64;
+__global__ __launch_bounds__(ACCEPT_THREADS) void accept_kernel(const QrDecodeLayer* layers, int rows) {
+    const QrDecodeLayer& w = layers[blockIdx.y];
+    if (w.attention) return;
+    constexpr int REC = VH * DK * DV / 4, CONV = CH * (CONVK - 1) / 4;  // float4s
+    f4* rec = reinterpret_cast<f4*>(w.recurrent);
+    f4* conv = reinterpret_cast<f4*>(w.conv_state);
+    for (int i = int(blockIdx.x * ACCEPT_THREADS + threadIdx.x); i < REC; i += ACCEPT_BLOCKS * ACCEPT_THREADS)
+        rec[i] = rec[size_t(rows) * REC + i];
+    for (int i = int(blockIdx.x * ACCEPT_THREADS + threadIdx.x); i < CONV; i += ACCEPT_BLOCKS * ACCEPT_THREADS)
+        conv[i] = conv[size_t(rows) * CONV + i];
+}
+static_assert((VH * DK * DV) % 4 == 0 && (CH * (CONVK - 1)) % 4 == 0, "float4 copies");
+
 }  // namespace dec
 }  // namespace qr
 
@@ -2429,6 +2447,13 @@ int decode_rows(QrDecodePlan* p, const int* tokens, int n, int position, int fir
         set_rope(p, a, r, position + (r < n ? r : 0));
     }
     return launch(p, s, true);
+}
+int decode_accept(QrDecodePlan* p, int rows, hipStream_t s) {
+    using namespace dec;
+    if (rows < 1 || rows > p->snapshots) return int(hipErrorInvalidValue);
+    hipLaunchKernelGGL(accept_kernel, dim3(ACCEPT_BLOCKS, unsigned(p->args.nlayers)), dim3(ACCEPT_THREADS), 0, s,
+                       static_cast<const QrDecodeLayer*>(p->layers), rows);
+    return int(hipGetLastError());
 }
 size_t decode_capture_floats(const QrDecodePlan* p) {
     return size_t(p->args.nlayers) * dec::CAPL + dec::H;

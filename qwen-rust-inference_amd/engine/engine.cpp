@@ -104,6 +104,7 @@ struct Api {
     int (*decode_step)(Context*, QrDecodePlan*, int, int) = nullptr;
     int (*decode_step_row)(Context*, QrDecodePlan*, int, int, int, int) = nullptr;
     int (*decode_step_capture)(Context*, QrDecodePlan*, int, int, float*, int64_t) = nullptr;
+    int (*decode_accept)(Context*, QrDecodePlan*, int) = nullptr;
     int (*decode_rows)(Context*, QrDecodePlan*, const int32_t*, int, int, int, int) = nullptr;
     int (*decode_steps)(Context*, QrDecodePlan*, int, int, int, int32_t*, float*) = nullptr;
     void (*decode_free)(Context*, QrDecodePlan*) = nullptr;
@@ -182,6 +183,7 @@ struct Api {
             if (!(disable & QE_NO_DECODE_CAPTURE))
                 decode_step_capture = symbol<decltype(decode_step_capture)>("qr_decode_step_capture", false);
             if (!(disable & QE_NO_DECODE_ROWS)) decode_rows = symbol<decltype(decode_rows)>("qr_decode_rows", false);
+            decode_accept = symbol<decltype(decode_accept)>("qr_decode_accept", false);
             if (!decode_plan || !decode_step || !decode_free) decode_plan = nullptr;
         }
         if (!(disable & QE_NO_EMBED_ROWS)) embed_rows = symbol<decltype(embed_rows)>("qr_embed_rows", false);
@@ -958,6 +960,11 @@ struct QeRun {
         require(rows >= 1 && rows <= t, "accept rows out of range");
         if (rows == t) return;
         const Api* a = api();
+        if (plan && a->decode_accept && rows <= snapshots) {  // the same copies in one launch
+            a->check(a->decode_accept(a->ctx, plan, int(rows)));
+            position = start + rows;
+            return;
+        }
         for (size_t l = 0; l < model->blocks.size(); ++l) {
             const DeviceBlock& b = model->blocks[l];
             if (b.attention) continue;

@@ -249,6 +249,55 @@ def test_c3_prefill_10240_one_chunk_vs_chunks(weights, fast):
     print(f"10240 one chunk vs 128-token chunks: largest relative difference {max(worst):.3e}", flush=True)
 
 
+def test_c3_prefill_10240_one_chunk_against_oracle(weights, fast):
+    """BASELINE config 3's second size against the oracle (fixture c3l): the
+    10,240-token prompt in one prefill chunk (the bench's call), last-row
+    logits, pick and 1024 samples of every state part; then the same prompt
+    as one chunk of 10,239 tokens and token 10,240 as a captured one-launch
+    step: its logits and every layer's output against the oracle's trace."""
+    c, _ = weights
+    rec = G.load("c3l")
+    ids = [int(v) for v in rec["prompt"]]
+    n = len(ids)
+    run = fast.new_run(n, chunk=n)
+    logits = run.prefill(ids)
+    margin, bound = check_logits("c3l", (n,), logits, rec, f"p{n}_", FP32_RTOL, "c3 10240 one chunk")
+    check_pick(int(np.argmax(logits)), int(rec[f"p{n}_pick"]), margin, bound, "c3 10240 one chunk")
+    check_state("c3l", n, run, c, rec, f"p{n}_state", FP32_RTOL, "c3 10240 one chunk",
+                recurrent_rtol=LONG_RECURRENT_RTOL)
+    run.close()
+    run = fast.new_run(n, chunk=n - 1)
+    assert run.decode_plan
+    run.prefill(ids[:n - 1])
+    logits, records = run.step(ids[n - 1], capture=True)
+    check_layers("c3l", n, records, rec[f"p{n}_layers"], c, FP32_RTOL, "c3 10240 captured step")
+    check_logits("c3l", (n,), logits, rec, f"p{n}_", FP32_RTOL, "c3 10240 captured step")
+    print("c3: 10240 one chunk and captured last step against the oracle ok", flush=True)
+
+
+def test_c3_prefill_10240_checkpoints(weights, fast):
+    """validate_long on the 10,240-token prompt: every checkpoint (1 .. 8193,
+    10,240) as one prefill call from the previous one, logits, pick and every
+    state part against the oracle; at the checkpoints up to 8193 the captured
+    step's layer outputs too (a second run: the tokens before the point in
+    one chunk, the point's token captured)."""
+    c, _ = weights
+    rec = G.load("c3l")
+    walk_checkpoints("c3l", fast.new_run(10240, chunk=10240), c, rec)
+    ids = [int(v) for v in rec["prompt"]]
+    run = fast.new_run(10240, chunk=10240)
+    done = 0
+    for p in [int(v) for v in rec["points"]]:
+        if f"p{p}_layers" not in rec:
+            continue
+        if p - 1 > done:
+            run.prefill(ids[done:p - 1])
+        _, records = run.step(ids[p - 1], capture=True)
+        done = p
+        check_layers("c3l", p, records, rec[f"p{p}_layers"], c, FP32_RTOL, f"c3 checkpoint {p}")
+    print("c3: 10240 checkpoint walk and layer outputs ok", flush=True)
+
+
 def test_c4_prefill_8192_one_chunk(weights, fast):
     """The whole 8192-token prompt in one prefill chunk against the oracle:
     last-row logits, pick and 1024 samples of every state part."""
