@@ -134,24 +134,30 @@ __device__ __forceinline__ bool block_work(const Plan& p, int b, int& tm, int& t
 }
 
 // One K step (two 16-deep k tiles) of the wave's 2 x TNW MFMA tiles from the
-// stage at `st` (already offset by lane * 16). Both k tiles' fragments sit in
-// their own registers: k tile 1's reads are interleaved with k tile 0's MFMAs.
-template <int TNW>
-__device__ __forceinline__ void step_mfma(f16v (&acc)[2][TNW], const char* st, int wm, int wn) {
+// stage at `st` (already offset by lane * 16). k tile 0's fragments are read
+// first; k tile 1's reads go one each before the first MFMAs. With DMA, the
+// wave's fragments of the next step (dma(i), i < DMA_PER_WAVE) are issued
+// spread over the MFMA stream, one every few MFMAs: a burst of them after the
+// barrier stalls the wave (the CU's vector memory path takes ~16 cycles per
+// KiB, and the wave issues in order), while spread out they cost the MFMA
+// stream nothing. sched_barrier(0) around each DMA keeps the scheduler from
+// moving anything across it (it cannot classify the inline assembly).
+template <int TNW, bool DMA, class F>
+__device__ __forceinline__ void step_mfma(f16v (&acc)[2][TNW], const char* st, int wm, int wn, F&& dma) {
     using G = Geo<TNW>;
+    constexpr int R = 3 * (2 + TNW), MF = 12 * TNW, ND = G::DMA_PER_WAVE, EVERY = 2 * MF / ND;
+    static_assert(R <= MF && EVERY >= 1 && ND * EVERY <= 2 * MF, "reads and DMAs fit the MFMA stream");
     bf16x8 a[2][2][3], b[2][TNW][3];
+    // read r of k tile k, in the order the products first use them: (x2, w0) (x1, w1) (x0, w2)
+    auto read = [&](int k, int r) {
+        const int f = r / (2 + TNW), t = r % (2 + TNW);
+        if (t < 2)
+            a[k][t][2 - f] = *reinterpret_cast<const bf16x8*>(st + ((2 * wm + t) * 6 + 3 * k + 2 - f) * FRAG);
+        else
+            b[k][t - 2][f] = *reinterpret_cast<const bf16x8*>(st + (6 * G::XRT + (TNW * wn + t - 2) * 6 + 3 * k + f) * FRAG);
+    };
 #pragma unroll
-    for (int k = 0; k < 2; ++k)
-#pragma unroll
-        for (int f = 0; f < 3; ++f) {  // in the order the products first use them: (x2, w0) (x1, w1) (x0, w2)
-            const int p = 2 - f, q = f;
-#pragma unroll
-            for (int i = 0; i < 2; ++i)
-                a[k][i][p] = *reinterpret_cast<const bf16x8*>(st + ((2 * wm + i) * 6 + 3 * k + p) * FRAG);
-#pragma unroll
-            for (int j = 0; j < TNW; ++j)
-                b[k][j][q] = *reinterpret_cast<const bf16x8*>(st + (6 * G::XRT + (TNW * wn + j) * 6 + 3 * k + q) * FRAG);
-        }
+    for (int r = 0; r < R; ++r) read(0, r);
     // the part products, smallest first; the tiles interleaved
     constexpr int P[6] = {2, 1, 0, 1, 0, 0}, Q[6] = {0, 1, 2, 0, 1, 0};
 #pragma unroll
@@ -161,22 +167,17 @@ __device__ __forceinline__ void step_mfma(f16v (&acc)[2][TNW], const char* st, i
 #pragma unroll
             for (int i = 0; i < 2; ++i)
 #pragma unroll
-                for (int j = 0; j < TNW; ++j)
+                for (int j = 0; j < TNW; ++j) {
+                    const int n = ((k * 6 + pq) * 2 + i) * TNW + j;
+                    if (k == 0 && n < R) read(1, n);
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[k][i][P[pq]], b[k][j][Q[pq]], acc[i][j], 0,
                                                                        0, 0);
-    // schedule: k tile 0's reads, then its MFMAs each followed by one of k
-    // tile 1's reads, then the rest of the MFMAs
-    constexpr int R = 3 * (2 + TNW), MF = 12 * TNW;
-    static_assert(R <= MF, "reads interleave with MFMAs");
-#pragma unroll
-    for (int i = 0; i < R; ++i) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-#pragma unroll
-    for (int i = 0; i < R; ++i) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-    }
-#pragma unroll
-    for (int i = R; i < 2 * MF; ++i) __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                    if (DMA && n % EVERY == EVERY / 2 && n / EVERY < ND) {
+                        __builtin_amdgcn_sched_barrier(0);
+                        dma(n / EVERY);
+                        __builtin_amdgcn_sched_barrier(0);
+                    }
+                }
 }
 
 // The K loop of one block: steps [s0, s0 + ns) of tile (tm, tn) into acc.
@@ -184,7 +185,9 @@ __device__ __forceinline__ void step_mfma(f16v (&acc)[2][TNW], const char* st, i
 // operand, row tile r = c' / 6, then k tile and plane (c' % 6 = 3 k + p), the
 // order of the global layout, so fragment c of step s is at
 // r rt_bytes + (6 s + c' % 6) KiB of its operand. Wave w moves fragments
-// w DMA_PER_WAVE .. + DMA_PER_WAVE - 1.
+// w DMA_PER_WAVE .. + DMA_PER_WAVE - 1: those of step s + 1 during step s's
+// MFMAs, into the other stage (every wave finished reading it before the
+// barrier of step s).
 template <int TNW>
 __device__ __forceinline__ void k_loop(f16v (&acc)[2][TNW], char* lds, const __bf16* xp, const __bf16* wp, int kt,
                                        int tm, int tn, int s0, int ns, int w, int lane) {
@@ -195,15 +198,12 @@ __device__ __forceinline__ void k_loop(f16v (&acc)[2][TNW], char* lds, const __b
     const unsigned lds0 = unsigned(reinterpret_cast<size_t>((__attribute__((address_space(3))) char*)lds));
     const unsigned voff = unsigned(lane) * 16u;
     const int wm = w & 1, wn = w >> 1;
-    auto issue = [&](int s, int stage) {
-#pragma unroll
-        for (int i = 0; i < G::DMA_PER_WAVE; ++i) {
-            const int c = w * G::DMA_PER_WAVE + i;
-            const bool isw = c >= 6 * G::XRT;
-            const int cc = isw ? c - 6 * G::XRT : c;
-            const char* src = (isw ? wb : xb) + size_t(cc / 6) * rt_bytes + size_t(6 * s + cc % 6) * FRAG;
-            dma_frag(src, lds0 + unsigned(stage * G::STAGE + c * FRAG), voff);
-        }
+    auto dma_one = [&](int s, int stage, int i) {
+        const int c = w * G::DMA_PER_WAVE + i;
+        const bool isw = c >= 6 * G::XRT;
+        const int cc = isw ? c - 6 * G::XRT : c;
+        const char* src = (isw ? wb : xb) + size_t(cc / 6) * rt_bytes + size_t(6 * s + cc % 6) * FRAG;
+        dma_frag(src, lds0 + unsigned(stage * G::STAGE + c * FRAG), voff);
     };
 #pragma unroll
     for (int i = 0; i < 2; ++i)
@@ -211,13 +211,18 @@ __device__ __forceinline__ void k_loop(f16v (&acc)[2][TNW], char* lds, const __b
         for (int j = 0; j < TNW; ++j)
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
-    issue(0, 0);
-    for (int s = 0; s < ns; ++s) {
+#pragma unroll
+    for (int i = 0; i < G::DMA_PER_WAVE; ++i) dma_one(0, 0, i);
+    int s = 0;
+    for (; s + 1 < ns; ++s) {
         vm_wait0();     // this wave's fragments of step s landed
         lds_barrier();  // ... every wave's; and every wave is past its reads of step s - 1
-        if (s + 1 < ns) issue(s + 1, (s + 1) & 1);
-        step_mfma<TNW>(acc, lds + (s & 1) * G::STAGE + lane * 16, wm, wn);
+        step_mfma<TNW, true>(acc, lds + (s & 1) * G::STAGE + lane * 16, wm, wn,
+                             [&](int i) { dma_one(s + 1, (s + 1) & 1, i); });
     }
+    vm_wait0();
+    lds_barrier();
+    step_mfma<TNW, false>(acc, lds + (s & 1) * G::STAGE + lane * 16, wm, wn, [](int) {});
 }
 
 // Accumulator register e of lane l in MFMA tile (i, j) of wave (wm, wn): tile
