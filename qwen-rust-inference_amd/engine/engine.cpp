@@ -677,7 +677,7 @@ struct QeRun {
         a->check(a->read(a->ctx, pk.data(), picks.p, 2));
         require(pk[1] < 1e30f, "one-launch decode step timed out at a stage barrier");
         if (greedy_rows) {
-            picked = read_picks(0, 1);
+            picked = picks_of(pk, 0, 1);  // the pick is in the read just made
         } else {
             out = logits.read(size_t(model->config.vocab_size));
         }
@@ -704,7 +704,7 @@ struct QeRun {
             for (int k = 0; k < 7; ++k) rec->fn(rec->user, int(l), names[k], v.data() + l * per + off[k], int64_t(len[k]));
         std::vector<float> out;
         if (greedy_rows) {
-            picked = read_picks(0, 1);
+            picked = picks_of(pk, 0, 1);
         } else {
             out = logits.read(size_t(model->config.vocab_size));
         }
@@ -743,7 +743,7 @@ struct QeRun {
         a->check(a->read(a->ctx, pk.data(), picks.p, pk.size()));
         for (size_t r = 0; r < t; ++r) require(pk[2 * r + 1] < 1e30f, "one-launch decode step timed out at a stage barrier");
         if (greedy_rows) {
-            picked = read_picks(0, t);
+            picked = picks_of(pk, 0, t);
         } else {
             out = logits.read(size_t(model->config.vocab_size) * t);
         }
@@ -895,9 +895,13 @@ struct QeRun {
         picked = read_picks(pick_slot, rows);
     }
     std::vector<uint32_t> read_picks(size_t slot, size_t rows) const {
-        size_t v = size_t(model->config.vocab_size);
         std::vector<float> all(2 * (slot + rows));
         api()->check(api()->read(api()->ctx, all.data(), picks.p, all.size()));
+        return picks_of(all, slot, rows);
+    }
+    // rows slot .. slot + rows - 1 of the picks buffer's (index, flag) pairs
+    std::vector<uint32_t> picks_of(const std::vector<float>& all, size_t slot, size_t rows) const {
+        size_t v = size_t(model->config.vocab_size);
         std::vector<uint32_t> out;
         for (size_t r = slot; r < slot + rows; ++r) {
             float idx = all[2 * r], bad = all[2 * r + 1];
