@@ -636,22 +636,33 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         b3_lds_barrier();  // scores exchanged; every wave is past its K reads
         if (more) b3_dma<B3_KDMA>(kblk + size_t(t + 1) * B3_KBLK, ks, w, lane);
         float mx = -INFINITY;
+        if (t * 32 + 31 < a.length0 + q0) {  // every key of the tile visible to every query of the block
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const float full = sc[r] + xch[w ^ 4][r][lane];  // the two halves' dims (addition commutes: same on both)
-            const float v = t * 32 + acc_row(r, hl) < len ? full * scale : -INFINITY;
-            sc[r] = v;
-            mx = fmaxf(mx, v);
+            for (int r = 0; r < 16; ++r) {
+                sc[r] = (sc[r] + xch[w ^ 4][r][lane]) * scale;  // the two halves' dims (addition commutes: same on both)
+                mx = fmaxf(mx, sc[r]);
+            }
+        } else {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const float full = sc[r] + xch[w ^ 4][r][lane];
+                const float v = t * 32 + acc_row(r, hl) < len ? full * scale : -INFINITY;
+                sc[r] = v;
+                mx = fmaxf(mx, v);
+            }
         }
         mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
         // -inf while a row has seen no visible position (a KV share past its length)
         const float mn = fmaxf(m, mx), mref = mn == -INFINITY ? 0.f : mn;
-        const float corr = expf(m - mref);
+        // the hardware exponential (v_exp_f32 of x log2 e): arguments are <= 0,
+        // where its error (a few ulp, plus |x| 2^-24 from the scaling) stays far
+        // below the fp32 bound the outputs are held to; exp(-inf) = 0
+        const float corr = __expf(m - mref);
         m = mn;
         float ps = 0.f;
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-            sc[r] = expf(sc[r] - mref);
+            sc[r] = __expf(sc[r] - mref);
             ps += sc[r];
         }
         l = l * corr + ps;
