@@ -607,19 +607,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         }
     }
     constexpr int P[6] = {2, 1, 0, 1, 0, 0}, Q[6] = {0, 1, 2, 0, 1, 0};  // part products, smallest first
-    b3_dma<B3_KDMA>(kblk + size_t(t_begin) * B3_KBLK, ks, w, lane);
-    b3_dma<B3_VDMA>(vblk + size_t(t_begin) * B3_VBLK, vt, w, lane);
-    b3_vm_wait<B3_VDMA>();  // this wave's K instructions done
-    b3_lds_barrier();
-    f16v o[DT];
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) o[dt][r] = 0.f;
-    float m = -INFINITY, l = 0.f;
-    for (int t = t_begin; t < t_end; ++t) {
-        const bool more = t + 1 < t_end;
-        f16v sc;
+    // this wave's partial scores of the tile in ks (its half of the dims)
+    auto scores = [&](f16v& sc) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) sc[r] = 0.f;
 #pragma unroll
@@ -631,26 +620,53 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
             for (int pq = 0; pq < 6; ++pq) sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka[P[pq]], qb[Q[pq]][s], sc, 0, 0, 0);
         }
-#pragma unroll
-        for (int r = 0; r < 16; ++r) xch[w][r][lane] = sc[r];
-        b3_lds_barrier();  // scores exchanged; every wave is past its K reads
-        if (more) b3_dma<B3_KDMA>(kblk + size_t(t + 1) * B3_KBLK, ks, w, lane);
-        float mx = -INFINITY;
+    };
+    // partial + the partner's (exchanged in xch) = the tile's scaled scores,
+    // -inf at positions this lane's query does not see
+    auto finish = [&](f16v& sc, int t) {
         if (t * 32 + 31 < a.length0 + q0) {  // every key of the tile visible to every query of the block
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                sc[r] = (sc[r] + xch[w ^ 4][r][lane]) * scale;  // the two halves' dims (addition commutes: same on both)
-                mx = fmaxf(mx, sc[r]);
-            }
+            for (int r = 0; r < 16; ++r) sc[r] = (sc[r] + xch[w ^ 4][r][lane]) * scale;  // (addition commutes: same on both)
         } else {
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const float full = sc[r] + xch[w ^ 4][r][lane];
-                const float v = t * 32 + acc_row(r, hl) < len ? full * scale : -INFINITY;
-                sc[r] = v;
-                mx = fmaxf(mx, v);
+                sc[r] = t * 32 + acc_row(r, hl) < len ? full * scale : -INFINITY;
             }
         }
+    };
+    b3_dma<B3_KDMA>(kblk + size_t(t_begin) * B3_KBLK, ks, w, lane);
+    b3_dma<B3_VDMA>(vblk + size_t(t_begin) * B3_VBLK, vt, w, lane);
+    b3_vm_wait<B3_VDMA>();  // this wave's K instructions done
+    b3_lds_barrier();
+    f16v sc, scn;
+    scores(sc);
+#pragma unroll
+    for (int r = 0; r < 16; ++r) xch[w][r][lane] = sc[r];
+    b3_lds_barrier();  // scores exchanged; every wave is past its K reads
+    if (t_begin + 1 < t_end) b3_dma<B3_KDMA>(kblk + size_t(t_begin + 1) * B3_KBLK, ks, w, lane);
+    finish(sc, t_begin);
+    if (t_begin + 1 < t_end) {
+        b3_vm_wait<0>();   // tile t_begin + 1's K (and t_begin's V) landed
+        b3_lds_barrier();  // ... for every wave; every wave past its xch reads
+    }
+    f16v o[DT];
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[dt][r] = 0.f;
+    float m = -INFINITY, l = 0.f;
+    // Software-pipelined by one tile: at the top of iteration t, sc holds tile
+    // t's scores, tile t + 1's K is in ks (if any), tile t's V is in flight to
+    // vt. Tile t + 1's score product (MFMA) and tile t's softmax (VALU) are
+    // independent and share one basic block, so they issue interleaved.
+    for (int t = t_begin; t < t_end; ++t) {
+        const bool more = t + 1 < t_end;
+        // tile t + 1's partial scores (the last tile multiplies stale K: unused)
+        scores(scn);
+        float mx = -INFINITY;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sc[r]);
         mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
         // -inf while a row has seen no visible position (a KV share past its length)
         const float mn = fmaxf(m, mx), mref = mn == -INFINITY ? 0.f : mn;
@@ -666,16 +682,18 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
             ps += sc[r];
         }
         l = l * corr + ps;
-        if (__any(corr != 1.f)) {  // a running maximum moved (scaling by 1 is exact: skipped)
 #pragma unroll
-            for (int dt = 0; dt < DT; ++dt) o[dt] *= corr;
-        }
-        // V of this tile landed (the next tile's K may still be in flight)
+        for (int dt = 0; dt < DT; ++dt) o[dt] *= corr;  // exact when the maximum did not move (corr = 1)
+        // the softmax is computed here, beside the score product's MFMAs (the
+        // compiler would otherwise sink it to the PV product after the barrier)
+        asm volatile("" : "+v"(sc), "+v"(o[0]), "+v"(o[1]), "+v"(o[2]), "+v"(o[3]), "+v"(l));
         if (more)
-            b3_vm_wait<B3_KDMA>();
-        else
-            b3_vm_wait<0>();
-        b3_lds_barrier();
+#pragma unroll
+            for (int r = 0; r < 16; ++r) xch[w][r][lane] = scn[r];
+        b3_vm_wait<0>();   // tile t's V landed (the only load in flight)
+        b3_lds_barrier();  // ... for every wave; tile t + 1's partials exchanged; every wave past its K reads
+        if (t + 2 < t_end) b3_dma<B3_KDMA>(kblk + size_t(t + 2) * B3_KBLK, ks, w, lane);
+        if (more) finish(scn, t + 1);
         // key steps outermost, so one step's P^T planes are live at a time
         // (each accumulator still takes step 0's products, then step 1's)
 #pragma unroll
@@ -700,9 +718,10 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
             }
         }
         if (more) {
-            b3_vm_wait<0>();   // the next tile's K landed
-            b3_lds_barrier();  // ... for every wave, and every wave is past its V reads
+            b3_vm_wait<0>();   // tile t + 2's K landed (if it was issued)
+            b3_lds_barrier();  // ... for every wave, and every wave is past its V reads and xch reads
             b3_dma<B3_VDMA>(vblk + size_t(t + 1) * B3_VBLK, vt, w, lane);
+            sc = scn;
         }
     }
     const float den = l + __shfl_xor(l, 32, 64);
