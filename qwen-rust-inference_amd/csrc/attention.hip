@@ -437,12 +437,13 @@ __global__ __launch_bounds__(64 * G) void attention_prefill_kernel(ReadArgs a) {
 // to whole 8 KiB rounds of 16-byte LDS DMA (56 and 64 KiB). The attention
 // kernel stages a tile by LDS DMA (global_load_lds_dwordx4: 64 lanes x 16 B
 // straight into LDS, no registers): each of the 8 waves issues 7 K and 8 V
-// instructions. K of tile t + 1 is loaded while tile t's softmax and PV
-// product run (K is not read after the score product), and V of tile t + 1
-// while tile t + 1's score product runs (V is not read before the PV
-// product), so one K buffer and one V buffer suffice (56 + 64 + 32 KiB score
-// exchange = 152 KiB) and the barriers wait for LDS only, never for loads in
-// flight.
+// instructions. The loop runs one tile ahead on the score product: tile t + 1's
+// scores are multiplied while tile t's softmax runs, then tile t's PV product;
+// K of tile t + 2 is loaded during that PV product (every wave is past its
+// reads of tile t + 1's K), and V of tile t + 1 during the next score product
+// (every wave is past its reads of tile t's V), so one K buffer and one V
+// buffer suffice (56 + 64 + 32 KiB score exchange = 152 KiB) and the barriers
+// wait for LDS only, never for loads in flight.
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 constexpr int B3_KROW = 256 + 8, B3_VROW = 40;
