@@ -165,11 +165,14 @@ def test_group_glu_equal_separate_calls(gpu, kind, batch):
 @pytest.mark.parametrize("rows,cols,batch", [(6144, 1024, 2644), (1024, 2048, 130), (1024, 3584, 64), (512, 1024, 454),
                                             (4096, 1024, 10240), (40, 12, 65), (2048, 1024, 63),
                                             (4096, 1024, 2644), (1024, 3584, 2644), (3584, 1024, 2644),
-                                            (1024, 2048, 10240), (256, 64, 300), (48, 1024, 200)])
+                                            (1024, 2048, 10240), (256, 64, 300), (48, 1024, 200),
+                                            (96, 32, 130), (320, 96, 257)])
 def test_gemm_f32_prepared(gpu, rows, cols, batch):
     """qr_gemm_f32_prepare: the projection of a prepared matrix (the P3 GEMM of
     gemm_p3.hip from 64 tokens: whole tiles, and the tiles past the last whole
-    round of 256 blocks split along K and summed in chunk order; the
+    round of 256 blocks split along K and summed in chunk order; K loops of
+    one step (cols 32: only the last step, which issues no DMA) and of three;
+    the
     split-BF16 kernel below 64 tokens or for cols % 32 != 0) against fp64 with
     the fp32 dot-product bound on sampled rows (the last row always among
     them), twice bitwise-equal, and within the bound of the unprepared
