@@ -13,9 +13,12 @@
 //   S_C = e^{G_63} S0 + (e^{G_63 - G} K)^T D.
 // Everything but S0 depends on the chunk's own inputs only:
 // rule_chunk_prep_kernel builds U, -W, e^G Q, (e^{G_63-G} K)^T and L for all
-// (chunk, head) pairs at once (8 waves; the triangular solve by 16-row blocks
-// on MFMA with the inverses of the diagonal blocks); rule_chunk_scan_kernel then walks the chunks in
-// order, one block per (head, 16-column slice of S) with the slice in LDS.
+// (chunk, head) pairs of a group of chunks at once (8 waves; the triangular
+// solve by 16-row blocks on MFMA with the inverses of the diagonal blocks);
+// rule_chunk_scan_kernel then walks the group's chunks in order, one block per
+// (head, 16-column slice of S) with the slice in LDS. With several groups,
+// rule_chunk_scan_prep_kernel scans group g on half the CUs while the other
+// half makes group g + 1's records (two record buffers).
 // Tokens past the end of the last chunk are zero with g = 0 and beta = 0,
 // which leaves D, O and S unchanged. G is summed in double so that
 // G_t - G_s keeps its precision when G itself is large.
@@ -31,7 +34,6 @@ constexpr int kSlices = kD / kSlice;
 // One (chunk, head) record, in floats: -W, U, e^G Q, (e^{G_63-G} K)^T, L, e^{G_63}.
 constexpr int kW = 0, kU = kW + kC * kD, kQ = kU + kC * kD, kK = kQ + kC * kD, kL = kK + kD * kC,
               kG = kL + kC * kC, kRec = kG + 64;
-constexpr int kGroupChunks = 64;  // chunks per prep + scan pair
 
 typedef float f4v __attribute__((ext_vector_type(4)));
 
@@ -50,21 +52,36 @@ typedef float f4v __attribute__((ext_vector_type(4)));
 constexpr int kPrep = 512;              // threads of a prep block (8 waves)
 constexpr int kPrepLoads = kC * kD / 4 / kPrep;  // float4 of q (of k, of V) per thread
 
-__global__ __launch_bounds__(kPrep) void rule_chunk_prep_kernel(Params a, int gated, int c0, float* scratch) {
+struct PrepLds {
     // row stride 132 (4 mod 64 banks): the Gram products' MFMA operand reads
     // (16 rows x 4 interleaved k per step) hit 64 distinct banks
-    __shared__ float ks[kC][kD + 4], qs[kC][kD + 4];
+    float ks[kC][kD + 4], qs[kC][kD + 4];
     // am holds A transposed: am[s][t] = A_ts (s < t), so the solve's column
     // sweeps read rows
-    __shared__ float am[kC][kC + 4], lm[kC][kC + 4];
+    float am[kC][kC + 4], lm[kC][kC + 4];
     // inverses of the four 16 x 16 diagonal blocks of I + A: li[i][t][s] = ((I + A)_ii^-1)_ts
-    __shared__ float li[kC / 16][16][16];
-    __shared__ double gd[kC];
-    __shared__ float bs[kC], eg[kC], el[kC];
-    const int tid = threadIdx.x, h = blockIdx.y, c = c0 + int(blockIdx.x);
+    float li[kC / 16][16][16];
+    double gd[kC];
+    float bs[kC], eg[kC], el[kC];
+};
+
+// The record of chunk c0 + xi of head h, into slot xi of `scratch`; every
+// thread of a kPrep-thread block takes part.
+__device__ __forceinline__ void prep_task(const Params& a, int gated, int c0, float* scratch, int xi, int h,
+                                          PrepLds& P) {
+    auto& ks = P.ks;
+    auto& qs = P.qs;
+    auto& am = P.am;
+    auto& lm = P.lm;
+    auto& li = P.li;
+    auto& gd = P.gd;
+    auto& bs = P.bs;
+    auto& eg = P.eg;
+    auto& el = P.el;
+    const int tid = threadIdx.x, c = c0 + xi;
     const int kh = a.n[2], vh = a.n[3], tokens = a.n[4] > 0 ? a.n[4] : 1, stride = a.n[5];
     const int t0 = c * kC, n = min(kC, tokens - t0);
-    float* rec = scratch + (size_t(blockIdx.x) * vh + h) * kRec;
+    float* rec = scratch + (size_t(xi) * vh + h) * kRec;
     f4v* rec4 = reinterpret_cast<f4v*>(rec);
     // Every global input of the block is requested up front: the gate inputs
     // (wave 0), q and k rows, and the V rows, held in registers until the
@@ -263,6 +280,11 @@ __global__ __launch_bounds__(kPrep) void rule_chunk_prep_kernel(Params a, int ga
     if (tid == 0) rec[kG] = eg[kC - 1];
 }
 
+__global__ __launch_bounds__(kPrep) void rule_chunk_prep_kernel(Params a, int gated, int c0, float* scratch) {
+    __shared__ PrepLds P;
+    prep_task(a, gated, c0, scratch, int(blockIdx.x), int(blockIdx.y), P);
+}
+
 __device__ __forceinline__ f4v mfma16(float x, float y, f4v acc) {
     return __builtin_amdgcn_mfma_f32_16x16x4f32(x, y, acc, 0, 0, 0);
 }
@@ -323,87 +345,138 @@ __device__ __forceinline__ void scan_load2(const float* rec, int w, int l, f4v (
         k1[m] = Kp[(w + 4) * 256 + m * 64];
     }
 }
-__global__ __launch_bounds__(256) void rule_chunk_scan_kernel(Params a, int c0, int chunks,
-                                                              const float* __restrict__ scratch) {
-    __shared__ __attribute__((aligned(16))) float sl[64][kSRow];
-    __shared__ __attribute__((aligned(16))) float dl[64][kDRow];
-    const int nb = int(gridDim.x), b = int(blockIdx.x);
-    const int i = nb % kXcds == 0 ? (b % kXcds) * (nb / kXcds) + b / kXcds : b;
+struct ScanLds {
+    alignas(16) float sl[64][kSRow];
+    alignas(16) float dl[64][kDRow];
+};
+// Block b of nb scan blocks -> its (head, slice) index: the 8 slices of a
+// head on one XCD.
+__device__ __forceinline__ int scan_index(int b, int nb) {
+    return nb % kXcds == 0 ? (b % kXcds) * (nb / kXcds) + b / kXcds : b;
+}
+// The scan of chunks [c0, c0 + chunks) by the (head, slice) of index i over
+// the records in `scratch`. With ALL false the block is larger than 256
+// threads: the threads past 256 only take part in the barriers.
+template <bool ALL>
+__device__ __forceinline__ void scan_group(const Params& a, int c0, int chunks, const float* __restrict__ scratch,
+                                           int i, ScanLds& S) {
+    auto& sl = S.sl;
+    auto& dl = S.dl;
+    const bool active = ALL || threadIdx.x < 256;
     const int h = i / kSlices, js = i % kSlices;
-    const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, lc = l & 15, q = l >> 4;
+    const int tid = threadIdx.x, w = (tid >> 6) & 3, l = tid & 63, lc = l & 15, q = l >> 4;
     const int vh = a.n[3], tokens = a.n[4] > 0 ? a.n[4] : 1;
     float* state = a.p[4] + size_t(h) * kD * kD + js * kSlice;
     // the output as a buffer of exactly tokens x vh x kD floats (its size is
     // checked below 2^31 bytes on the host): stores past it are dropped, so
     // the ragged last chunk needs no per-lane branch around its stores
     const Rs out_rs = __builtin_amdgcn_make_buffer_rsrc(a.p[0], 0, tokens * vh * kD * 4, 0x00020000);
-    for (int e = tid; e < kD * kSlice; e += 256) {  // S row k, column j -> [16 (k % 4) + j][k / 4]
-        const int k = e / kSlice, j = e % kSlice;
-        sl[16 * (k & 3) + j][k >> 2] = state[size_t(k) * kD + j];
-    }
     f4v wv[8], qv[8], uv, lv[4], k0[4], k1[4];
-    scan_load1(scan_rec(scratch, 0, vh, h), w, js, l, wv, qv, uv);
-    scan_load2(scan_rec(scratch, 0, vh, h), w, l, lv, k0, k1);
+    if (active) {
+        for (int e = tid; e < kD * kSlice; e += 256) {  // S row k, column j -> [16 (k % 4) + j][k / 4]
+            const int k = e / kSlice, j = e % kSlice;
+            sl[16 * (k & 3) + j][k >> 2] = state[size_t(k) * kD + j];
+        }
+        scan_load1(scan_rec(scratch, 0, vh, h), w, js, l, wv, qv, uv);
+        scan_load2(scan_rec(scratch, 0, vh, h), w, l, lv, k0, k1);
+    }
     __syncthreads();
     for (int c = 0; c < chunks; ++c) {
         const int t0 = (c0 + c) * kC;
         const int cn = c + 1 < chunks ? c + 1 : c;  // the last chunk reloads itself
         const float decay = scan_rec(scratch, c, vh, h)[kG];
-        f4v sb[8];  // S in B-operand order: step s = 4 m + e is sb[m][e]
-#pragma unroll
-        for (int m = 0; m < 8; ++m) sb[m] = *reinterpret_cast<const f4v*>(&sl[l][4 * m]);
-        f4v dacc = uv, oacc = {0.f, 0.f, 0.f, 0.f};
         const float* recn = scan_rec(scratch, cn, vh, h);
+        f4v oacc = {0.f, 0.f, 0.f, 0.f};
+        if (active) {
+            f4v sb[8];  // S in B-operand order: step s = 4 m + e is sb[m][e]
 #pragma unroll
-        for (int m = 0; m < 8; ++m) {
+            for (int m = 0; m < 8; ++m) sb[m] = *reinterpret_cast<const f4v*>(&sl[l][4 * m]);
+            f4v dacc = uv;
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                dacc = mfma16(wv[m][e], sb[m][e], dacc);
-                oacc = mfma16(qv[m][e], sb[m][e], oacc);
+            for (int m = 0; m < 8; ++m) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    dacc = mfma16(wv[m][e], sb[m][e], dacc);
+                    oacc = mfma16(qv[m][e], sb[m][e], oacc);
+                }
+                // float4 m is consumed: chunk cn's goes out while the MFMAs run
+                wv[m] = reinterpret_cast<const f4v*>(recn + kW)[w * 512 + m * 64 + l];
+                qv[m] = reinterpret_cast<const f4v*>(recn + kQ)[w * 512 + m * 64 + l];
             }
-            // float4 m is consumed: chunk cn's goes out while the MFMAs run
-            wv[m] = reinterpret_cast<const f4v*>(recn + kW)[w * 512 + m * 64 + l];
-            qv[m] = reinterpret_cast<const f4v*>(recn + kQ)[w * 512 + m * 64 + l];
-        }
-        uv = reinterpret_cast<const f4v*>(recn + kU)[(w * kSlices + js) * 64 + l];
+            uv = reinterpret_cast<const f4v*>(recn + kU)[(w * kSlices + js) * 64 + l];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) dl[16 * r + lc][4 * w + q] = dacc[r];  // D row 16 w + 4 q + r
+            for (int r = 0; r < 4; ++r) dl[16 * r + lc][4 * w + q] = dacc[r];  // D row 16 w + 4 q + r
+        }
         lds_barrier();
-        f4v s0, s1;
+        if (active) {
+            f4v s0, s1;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {  // S rows 16 w + 4 q + r and 16 (w + 4) + 4 q + r
-            s0[r] = decay * sl[16 * r + lc][4 * w + q];
-            s1[r] = decay * sl[16 * r + lc][4 * w + 16 + q];
-        }
-        f4v db[4];
-#pragma unroll
-        for (int m = 0; m < 4; ++m) db[m] = *reinterpret_cast<const f4v*>(&dl[l][4 * m]);
-#pragma unroll
-        for (int m = 0; m < 4; ++m) {
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                if (m <= w) oacc = mfma16(lv[m][e], db[m][e], oacc);  // L is zero past the tile's last token
-                s0 = mfma16(k0[m][e], db[m][e], s0);
-                s1 = mfma16(k1[m][e], db[m][e], s1);
+            for (int r = 0; r < 4; ++r) {  // S rows 16 w + 4 q + r and 16 (w + 4) + 4 q + r
+                s0[r] = decay * sl[16 * r + lc][4 * w + q];
+                s1[r] = decay * sl[16 * r + lc][4 * w + 16 + q];
             }
-            const f4v* Kp = reinterpret_cast<const f4v*>(recn + kK) + l;
-            lv[m] = reinterpret_cast<const f4v*>(recn + kL)[w * 256 + m * 64 + l];
-            k0[m] = Kp[w * 256 + m * 64];
-            k1[m] = Kp[(w + 4) * 256 + m * 64];
-        }
+            f4v db[4];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int t = t0 + 16 * w + 4 * q + r;  // rows t >= tokens fall outside out_rs: dropped
-            buffer_store_f32(oacc[r], out_rs, unsigned(((t * vh + h) * kD + js * kSlice + lc) * 4), 0, 0);
-            sl[16 * r + lc][4 * w + q] = s0[r];
-            sl[16 * r + lc][4 * w + 16 + q] = s1[r];
+            for (int m = 0; m < 4; ++m) db[m] = *reinterpret_cast<const f4v*>(&dl[l][4 * m]);
+#pragma unroll
+            for (int m = 0; m < 4; ++m) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    if (m <= w) oacc = mfma16(lv[m][e], db[m][e], oacc);  // L is zero past the tile's last token
+                    s0 = mfma16(k0[m][e], db[m][e], s0);
+                    s1 = mfma16(k1[m][e], db[m][e], s1);
+                }
+                const f4v* Kp = reinterpret_cast<const f4v*>(recn + kK) + l;
+                lv[m] = reinterpret_cast<const f4v*>(recn + kL)[w * 256 + m * 64 + l];
+                k0[m] = Kp[w * 256 + m * 64];
+                k1[m] = Kp[(w + 4) * 256 + m * 64];
+            }
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int t = t0 + 16 * w + 4 * q + r;  // rows t >= tokens fall outside out_rs: dropped
+                buffer_store_f32(oacc[r], out_rs, unsigned(((t * vh + h) * kD + js * kSlice + lc) * 4), 0, 0);
+                sl[16 * r + lc][4 * w + q] = s0[r];
+                sl[16 * r + lc][4 * w + 16 + q] = s1[r];
+            }
         }
         lds_barrier();
     }
     __syncthreads();
-    for (int e = tid; e < kD * kSlice; e += 256) {
-        const int k = e / kSlice, j = e % kSlice;
-        state[size_t(k) * kD + j] = sl[16 * (k & 3) + j][k >> 2];
+    if (active)
+        for (int e = tid; e < kD * kSlice; e += 256) {
+            const int k = e / kSlice, j = e % kSlice;
+            state[size_t(k) * kD + j] = sl[16 * (k & 3) + j][k >> 2];
+        }
+}
+
+__global__ __launch_bounds__(256) void rule_chunk_scan_kernel(Params a, int c0, int chunks,
+                                                              const float* __restrict__ scratch) {
+    __shared__ ScanLds S;
+    scan_group<true>(a, c0, chunks, scratch, scan_index(int(blockIdx.x), int(gridDim.x)), S);
+}
+
+// One launch, two jobs on separate CUs: blocks [0, nscan) scan the chunks
+// [sc0, sc0 + schunks) from the records in `srec` (as rule_chunk_scan_kernel,
+// on 4 of their 8 waves); the others make the records of the next group's
+// chunks [pc0, pc0 + pchunks) into `prec`, the (chunk, head) tasks dealt
+// round-robin. The two record buffers are disjoint and neither job waits for
+// the other. Their LDS together (~122 KiB) leaves room for one block per CU,
+// so on an idle device the blocks take one CU each and the prep work never
+// shares a CU with the latency-bound scan.
+__global__ __launch_bounds__(kPrep) void rule_chunk_scan_prep_kernel(Params a, int gated, int nscan, int sc0,
+                                                                     int schunks, const float* __restrict__ srec,
+                                                                     int pc0, int pchunks, float* prec) {
+    __shared__ ScanLds S;
+    __shared__ PrepLds P;
+    const int b = int(blockIdx.x), vh = a.n[3];
+    if (b < nscan) {
+        scan_group<false>(a, sc0, schunks, srec, scan_index(b, nscan), S);
+        return;
+    }
+    const int nprep = int(gridDim.x) - nscan;
+    for (int task = b - nscan; task < pchunks * vh; task += nprep) {
+        if (task != b - nscan) __syncthreads();  // every thread past the previous task's LDS reads
+        prep_task(a, gated, pc0, prec, task / vh, task % vh, P);
     }
 }
 
@@ -418,23 +491,46 @@ bool delta_rule_chunked_ok(const Params& a, int count) {
            int64_t(tokens) * a.n[3] * kD * 4 < (int64_t(1) << 31);  // the scan's output buffer resource
 }
 
+// Chunks per group. Up to kOneGroup chunks: one group (the prep on every CU,
+// then the scan). Beyond: groups of about kGroupTarget chunks, equal in size,
+// the scan of group g and the prep of group g + 1 in one launch; at that size
+// the prep of a group on the CUs the scan leaves free takes about as long as
+// its scan (measured at 10,240 tokens of the 0.8B shape: 633 -> 608 us per
+// layer for prep + scan; 8-chunk groups 668 us, the launches' fixed cost; at
+// 2644 tokens three overlapped groups measured no faster than one).
+constexpr int kOneGroup = 64, kGroupTarget = 16;
+int group_chunks(int chunks) {
+    if (chunks <= kOneGroup) return chunks;
+    const int groups = (chunks + kGroupTarget - 1) / kGroupTarget;
+    return (chunks + groups - 1) / groups;
+}
+
 size_t delta_rule_chunked_scratch(const Params& a) {
     const int tokens = a.n[4] > 0 ? a.n[4] : 1;
-    const int chunks = int(ceil_div(tokens, kC));
-    return size_t(chunks < kGroupChunks ? chunks : kGroupChunks) * size_t(a.n[3]) * kRec;
+    const int chunks = int(ceil_div(tokens, kC)), g = group_chunks(chunks);
+    return size_t(chunks > g ? 2 : 1) * size_t(g) * size_t(a.n[3]) * kRec;
 }
 
 int run_delta_rule_chunked(hipStream_t s, bool gated, const Params& a, float* scratch, size_t len) {
     if (len < delta_rule_chunked_scratch(a)) return int(hipErrorInvalidValue);
     const int tokens = a.n[4] > 0 ? a.n[4] : 1, vh = a.n[3];
-    const int chunks = int(ceil_div(tokens, kC));
-    for (int c0 = 0; c0 < chunks; c0 += kGroupChunks) {
-        const int group = chunks - c0 < kGroupChunks ? chunks - c0 : kGroupChunks;
-        hipLaunchKernelGGL(rule_chunk_prep_kernel, dim3(unsigned(group), unsigned(vh)), dim3(kPrep), 0, s, a,
-                           gated ? 1 : 0, c0, scratch);
-        if (hipError_t e = hipGetLastError()) return int(e);
-        hipLaunchKernelGGL(rule_chunk_scan_kernel, dim3(unsigned(vh * kSlices)), dim3(256), 0, s, a, c0, group,
-                           static_cast<const float*>(scratch));
+    const int chunks = int(ceil_div(tokens, kC)), g = group_chunks(chunks);
+    float* buf[2] = {scratch, scratch + size_t(g) * size_t(vh) * kRec};
+    const int nscan = vh * kSlices, nprep = nscan < 256 - 64 ? 256 - nscan : 64;
+    hipLaunchKernelGGL(rule_chunk_prep_kernel, dim3(unsigned(g), unsigned(vh)), dim3(kPrep), 0, s, a, gated ? 1 : 0, 0,
+                       buf[0]);
+    if (hipError_t e = hipGetLastError()) return int(e);
+    for (int c0 = 0, k = 0; c0 < chunks; c0 += g, ++k) {
+        const int n = chunks - c0 < g ? chunks - c0 : g, c1 = c0 + n;
+        if (c1 < chunks) {  // this group's scan beside the next group's prep
+            const int n1 = chunks - c1 < g ? chunks - c1 : g;
+            hipLaunchKernelGGL(rule_chunk_scan_prep_kernel, dim3(unsigned(nscan + nprep)), dim3(kPrep), 0, s, a,
+                               gated ? 1 : 0, nscan, c0, n, static_cast<const float*>(buf[k & 1]), c1, n1,
+                               buf[(k + 1) & 1]);
+        } else {
+            hipLaunchKernelGGL(rule_chunk_scan_kernel, dim3(unsigned(nscan)), dim3(256), 0, s, a, c0, n,
+                               static_cast<const float*>(buf[k & 1]));
+        }
         if (hipError_t e = hipGetLastError()) return int(e);
     }
     return 0;
