@@ -562,19 +562,20 @@ def _unit_rows(rng, rows, d, scale=1.0):
     return (x / np.linalg.norm(x, axis=1, keepdims=True) * scale).astype(np.float32).ravel()
 
 
-@pytest.mark.parametrize("tokens,gated,a_log", [(16, True, 0.0), (63, True, 0.0), (64, True, 0.0), (65, False, 0.0),
-                                                (130, True, 0.0), (300, False, 0.0), (200, True, 3.0),
-                                                (64 * 64 + 37, True, 0.0), (64 * 70 + 5, False, 0.0)])
-def test_delta_rule_chunked(gpu, cpu, tokens, gated, a_log):
+@pytest.mark.parametrize("tokens,gated,a_log,heads", [(16, True, 0.0, 16), (63, True, 0.0, 16), (64, True, 0.0, 16),
+                                                      (65, False, 0.0, 16), (130, True, 0.0, 16), (300, False, 0.0, 16),
+                                                      (200, True, 3.0, 16), (64 * 64 + 37, True, 0.0, 16),
+                                                      (64 * 70 + 5, False, 0.0, 16), (64 * 66 + 3, True, 0.0, 4)])
+def test_delta_rule_chunked(gpu, cpu, tokens, gated, a_log, heads):
     """Prefill lengths take the chunked (WY form, MFMA) path: 64-token chunks,
     ragged last chunks, heavy decay (A_log 3: g ~ -14 per token), and past 64
     chunks the grouped walk (65 chunks: five groups of 13; 71: four of 15 and
-    one of 11), each group's scan beside the next group's prep in one launch.
-    q and k are unit rows (q also / sqrt(dk)) as DeltaQk hands them to the
-    rule; the CPU side is the token-by-token recurrence."""
+    one of 11), each group's scan beside the next group's prep in one launch
+    (with 4 heads: 32 scan blocks beside 224 prep blocks). q and k are unit
+    rows (q also / sqrt(dk)) as DeltaQk hands them to the rule; the CPU side
+    is the token-by-token recurrence."""
     kd = vd = 128
-    heads = 16
-    print(f"delta_rule_chunked tokens={tokens} gated={gated} a_log={a_log}", flush=True)
+    print(f"delta_rule_chunked tokens={tokens} gated={gated} a_log={a_log} heads={heads}", flush=True)
     rng = np.random.default_rng(tokens + 7 * gated)
     stride = 2 * heads * kd + heads * vd
     q = _unit_rows(rng, tokens * heads, kd, 1 / np.sqrt(kd))
