@@ -18,9 +18,10 @@
 // The GEMM (gemm_p3_kernel): a block tile of 128 tokens x 128 or 256 weight
 // rows, 4 waves (2 x 2 waves of 64 x 64 or 64 x 128). K steps of 32 are copied
 // global -> LDS by LDS DMA (global_load_lds_dwordx4: each instruction moves one
-// fragment, 64 lanes x 16 bytes, straight into LDS) into two stages: the DMA of
-// step s + 1 is issued right after the barrier of step s and lands while step
-// s is multiplied. Per 16-deep k tile a wave reads 3 planes x its row tiles of
+// fragment, 64 lanes x 16 bytes, straight into LDS) into two stages: the DMAs
+// of step s + 1 are issued spread over step s's MFMAs (one every few) into the
+// other stage and land while step s is multiplied. Per 16-deep k tile a wave
+// reads 3 planes x its row tiles of
 // X and of W and issues six MFMAs per (X tile, W tile) pair, so each operand
 // read from LDS feeds six MFMAs: half the operand traffic of the same products
 // laid out along K (a BF16 GEMM with K' = 6K reads a plane pair per product).
