@@ -392,12 +392,18 @@ __global__ __launch_bounds__(256) void p3_glu_sum_kernel(float* product, __bf16*
     glu_store8(product, planes, p.N / 2, m, tn * 128 + c8, v);
 }
 
-// fp32 [rows, cols] -> P3 planes of p3_rows(rows) rows (the pad rows zero):
-// one thread per 8 consecutive values of a row, a 16-byte store per plane.
+// fp32 [rows, cols] -> P3 planes of p3_rows(rows) rows (the pad rows zero).
+// Work item c is lane c % 64 of fragment c / 64 (32 rows x 16 k, row tile
+// major): its 8 values (row 32 rt + lane % 32, k 16 kt + 8 (lane / 32)) are
+// read as two 16-byte loads, and each wave writes whole 1 KiB fragments of
+// the three planes, so the stores are contiguous (a row-major walk would
+// scatter them 16 bytes per cache line).
 __global__ __launch_bounds__(256) void p3_split_kernel(__bf16* out, const float* in, int rows, int cols, long chunks) {
-    const int per_row = cols / 8, kt = cols / 16;
+    const int kt = cols / 16;
     for (long c = blockIdx.x * long(blockDim.x) + threadIdx.x; c < chunks; c += long(gridDim.x) * blockDim.x) {
-        const int r = int(c / per_row), k = int(c % per_row) * 8;
+        const long f = c >> 6;
+        const int l = int(c & 63), rt = int(f / kt), kk = int(f % kt);
+        const int r = 32 * rt + (l & 31), k = 16 * kk + 8 * (l >> 5);
         bf16x8 h[3];
         if (r < rows) {
             const f4v lo = *reinterpret_cast<const f4v*>(in + size_t(r) * cols + k);

@@ -467,6 +467,104 @@ __global__ __launch_bounds__(256) void attention_qkv_kernel(int op, int count, P
     (void)count;
 }
 
+// The same items with one wave each (four per 256-thread block) when d = 64
+// NJ and rot <= 64: lane l holds elements l + 64 j, the rotary partner of
+// element i < rot / 2 (i + rot / 2) sits in lane l + rot / 2 of the same
+// register, so no block barrier or LDS round trip is needed (the block form
+// spends most of its time on those at d = 256: 102,400 blocks at 10,240
+// tokens). The sum of squares is formed exactly as block_sum forms it for a
+// 256-thread block (thread 64 w + l accumulates elements 64 w + l + 256 m in m
+// order, one butterfly per wave, the wave sums added in order), so the
+// results equal the block form's.
+template <int NJ>
+__device__ __forceinline__ void qkv_item_wave(bool query, int t, const Params& a, const float* denom, int l) {
+    constexpr int d = 64 * NJ;
+    const int rot = a.n[1], half = rot / 2;
+    int pos;
+    const float* x;
+    float* out;
+    size_t dest = 0;
+    if (query) {
+        pos = a.n[2] + (a.n[3] > 0 ? t / a.n[3] : 0);
+        x = a.p[1] + size_t(t) * 2 * d;
+        out = a.p[0] + size_t(t) * d;
+    } else {
+        const int kv = a.n[3];
+        pos = a.n[2] + t / kv;
+        x = a.p[1] + size_t(t) * d;
+        dest = (size_t(pos) * kv + t % kv) * d;
+        out = a.p[0] + dest;
+    }
+    float v[NJ];
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) v[j] = x[l + 64 * j];
+    float ss = 0.f;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+        float part = 0.f;
+#pragma unroll
+        for (int j = w; j < NJ; j += 4) part += v[j] * v[j];
+        ss += wave_sum(part);
+    }
+    const float r = 1.f / sqrtf(ss / float(d) + a.f[0]);
+    float y[NJ];
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+        const int e = l + 64 * j;
+        y[j] = (v[j] * r) * (1.f + a.p[2][e]);
+        if (query)
+            a.p[3][size_t(t) * d + e] = x[d + e];
+        else
+            a.p[4][dest + e] = a.p[3][size_t(t) * d + e];
+    }
+    // rope_lds on element pairs (i, i + half), i < half, all in j = 0
+    const int partner = l < half ? l + half : l < rot ? l - half : l;
+    const float pv = __shfl(y[0], partner, kWave);
+    if (l < rot) {
+        const int i = l < half ? l : l - half;
+        const float angle = float(pos) / denom[i];
+        const float sn = sinf(angle), cs = cosf(angle);
+        y[0] = l < half ? y[0] * cs - pv * sn : y[0] * cs + pv * sn;
+    }
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) out[l + 64 * j] = y[j];
+}
+
+template <int NJ>
+__global__ __launch_bounds__(256) void attention_qkv_wave_kernel(int op, int count, Params a, const float* denom) {
+    const int item = int(blockIdx.x) * 4 + int(threadIdx.x >> 6), l = int(threadIdx.x & 63);
+    if (item >= count) return;  // whole waves only: no block barrier
+    if (op == QR_ATTENTION_QUERY) {
+        qkv_item_wave<NJ>(true, item, a, denom, l);
+    } else if (op == QR_ATTENTION_KV) {
+        qkv_item_wave<NJ>(false, item, a, denom, l);
+    } else {  // AttentionQueryKv: the items split as attention_qkv_kernel splits them
+        const int queries = a.n[3] * a.n[5];
+        Params part{};
+        part.n[0] = a.n[0];
+        part.n[1] = a.n[1];
+        part.n[2] = a.n[2];
+        part.f[0] = a.f[0];
+        part.f[1] = a.f[1];
+        if (item < queries) {
+            part.p[0] = a.p[0];
+            part.p[1] = a.p[1];
+            part.p[2] = a.p[2];
+            part.p[3] = a.p[3];
+            part.n[3] = a.n[3];
+            qkv_item_wave<NJ>(true, item, part, denom, l);
+        } else {
+            part.p[0] = a.p[4];
+            part.p[1] = a.p[5];
+            part.p[2] = a.p[2] + a.n[0];
+            part.p[3] = a.p[6];
+            part.p[4] = a.p[7];
+            part.n[3] = a.n[4];
+            qkv_item_wave<NJ>(false, item - queries, part, denom, l);
+        }
+    }
+}
+
 // ---------------------------------------------------------------- Argmax (16)
 // reference.h:222-230: per row [first index of the maximum over finite values
 // (0xffffffff if none), non-finite count]. Pass 1: one block per (slice, row)
@@ -661,6 +759,17 @@ int run_delta_rule(hipStream_t s, bool gated, int count, const Params& a) {
 
 int run_attention_qkv(hipStream_t s, int op, int count, const Params& a, const float* denom) {
     if (a.n[0] > kAttnMaxHeadDim || a.n[1] > a.n[0] || a.n[1] % 2 != 0) return int(hipErrorInvalidValue);
+    const dim3 waves(unsigned((count + 3) / 4));
+    if (a.n[1] <= 64) {
+        switch (a.n[0]) {
+        case 64: hipLaunchKernelGGL(attention_qkv_wave_kernel<1>, waves, dim3(256), 0, s, op, count, a, denom); break;
+        case 128: hipLaunchKernelGGL(attention_qkv_wave_kernel<2>, waves, dim3(256), 0, s, op, count, a, denom); break;
+        case 256: hipLaunchKernelGGL(attention_qkv_wave_kernel<4>, waves, dim3(256), 0, s, op, count, a, denom); break;
+        case 512: hipLaunchKernelGGL(attention_qkv_wave_kernel<8>, waves, dim3(256), 0, s, op, count, a, denom); break;
+        default: hipLaunchKernelGGL(attention_qkv_kernel, dim3(unsigned(count)), dim3(256), 0, s, op, count, a, denom);
+        }
+        return int(hipGetLastError());
+    }
     hipLaunchKernelGGL(attention_qkv_kernel, dim3(unsigned(count)), dim3(256), 0, s, op, count, a, denom);
     return int(hipGetLastError());
 }
