@@ -164,6 +164,65 @@ __global__ __launch_bounds__(256) void rms_rows_kernel(int op, int groups, Param
     }
 }
 
+// RmsNormGate with the output's P3 planes for groups of 128 (the DeltaNet
+// gated norm before out_proj): one block per (32 rows of the planes, one
+// group column h of the width); wave w normalizes rows 8 w .. 8 w + 7 of the
+// tile exactly as rms_rows_kernel<2> does (lane l: elements 2 l, 2 l + 1; the
+// same sums and products), stores the fp32 output, and stages it in LDS; then
+// each wave writes whole 1 KiB plane fragments (rows of the tile x 16 k) for
+// two of the group's 8 k tiles. rms_rows_kernel writes a row's planes 4 bytes
+// per lane, one cache line each. Rows past `rows` get zero planes.
+__global__ __launch_bounds__(256) void rms_gate_planes_kernel(int rows, Params a, __bf16* planes, int width) {
+    constexpr int D = 128, KT = D / 16;
+    typedef float f2v __attribute__((ext_vector_type(2)));
+    typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+    __shared__ float ys[32][D + 4];
+    const int rt = int(blockIdx.x), h = int(blockIdx.y), hc = width / D;
+    const int w = int(threadIdx.x >> 6), lane = int(threadIdx.x & 63);
+    const float eps = a.f[0], offset = a.f[1];
+    const f2v wv = *reinterpret_cast<const f2v*>(a.p[2] + 2 * lane);
+    for (int i = 0; i < 8; ++i) {
+        const int rr = 8 * w + i, row = 32 * rt + rr;
+        f2v y = {0.f, 0.f};
+        if (row < rows) {  // wave-uniform
+            const size_t off = (size_t(row) * hc + h) * D + 2 * lane;
+            const f2v x = *reinterpret_cast<const f2v*>(a.p[1] + off);
+            float ss = 0.f;
+            ss += x[0] * x[0];
+            ss += x[1] * x[1];
+            ss = wave_sum(ss);
+            const float r = 1.f / sqrtf(ss / float(D) + eps);
+            const f2v z = *reinterpret_cast<const f2v*>(a.p[3] + off);
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                y[e] = (x[e] * r) * (wv[e] + offset);
+                y[e] = siluf_(z[e]) * y[e];
+            }
+            *reinterpret_cast<f2v*>(a.p[0] + off) = y;
+        }
+        ys[rr][2 * lane] = y[0];
+        ys[rr][2 * lane + 1] = y[1];
+    }
+    __syncthreads();
+    const int rl = lane & 31, k8 = 8 * (lane >> 5);
+    for (int kk = w; kk < KT; kk += 4) {
+        bf16x8 hp[3];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const float v = ys[rl][16 * kk + k8 + e];
+            const __bf16 h0 = __bf16(v);
+            const float r1 = v - float(h0);
+            const __bf16 h1 = __bf16(r1);
+            hp[0][e] = h0;
+            hp[1][e] = h1;
+            hp[2][e] = __bf16(r1 - float(h1));
+        }
+#pragma unroll
+        for (int q = 0; q < 3; ++q)
+            *reinterpret_cast<bf16x8*>(planes + p3_index(32 * rt + rl, h * D + 16 * kk + k8, q, width / 16)) = hp[q];
+    }
+}
+
 // ---------------------------------------------------------------- ConvSilu (4)
 // reference.h:96-116: one channel per thread, tokens in order through the
 // channel's history (oldest -> newest); with n3 = S > 0 the history after
@@ -695,6 +754,12 @@ int run_rms_family_planes(hipStream_t s, int op, int groups, const Params& a, __
     if (a.n[0] < 1 || width < a.n[0] || width % a.n[0] != 0 || !p3_cols_ok(width) ||
         (long(groups) * a.n[0]) % width != 0)
         return int(hipErrorNotSupported);
+    if (op == QR_RMS_NORM_GATE && a.n[0] == 128) {
+        const int hc = width / 128, rows = int(long(groups) / hc);
+        hipLaunchKernelGGL(rms_gate_planes_kernel, dim3(unsigned((rows + 31) / 32), unsigned(hc)), dim3(256), 0, s, rows,
+                           a, planes, width);
+        return int(hipGetLastError());
+    }
     if (!launch_rms_rows_any(s, op, groups, a, planes, width)) return int(hipErrorNotSupported);
     return int(hipGetLastError());
 }
