@@ -817,7 +817,8 @@ int qr_delta_mixer(Context* c, const QrDelta* d) {
         return launched(c, "delta_mixer", qr::delta_mixer_decode(c->stream, *d));
     }
     // Otherwise the four ops with the slots the engine gives them
-    // (reference native/rocm/bridge.cpp:743-761).
+    // (reference native/rocm/bridge.cpp:743-761), DeltaQk inside the chunked
+    // rule at prefill lengths.
     const int vh = d->value_heads, vd = vh * d->value_dim, t = d->tokens;
     Params conv{}, qk{}, rule{}, gate{};
     conv.p[0] = d->convolved;
@@ -856,8 +857,21 @@ int qr_delta_mixer(Context* c, const QrDelta* d) {
     gate.f[0] = d->eps;
     gate.f[1] = 0.f;
     if (int s = qr_run(c, QR_CONV_SILU, d->channels, &conv)) return s;
-    if (int s = qr_run(c, QR_DELTA_QK, vh * t, &qk)) return s;
-    if (int s = qr_run(c, QR_DELTA_RULE_GATED, vd, &rule)) return s;
+    if (qr::delta_rule_chunked_ok(rule, vd)) {
+        // the chunked rule's prep normalises the convolution's q / k rows
+        // itself and stores them to query / key, as DeltaQk would
+        ++c->serial;
+        auto sc = scope(c, [&] { return std::string("delta_qk+delta_rule_gated chunked"); });
+        if (int st = ensure(c, &c->rule_chunks, &c->rule_chunks_len, qr::delta_rule_chunked_scratch(rule),
+                            "hipMalloc delta rule chunks"))
+            return st;
+        if (int st = launched(c, "delta_rule_chunked",
+                              qr::run_delta_rule_chunked(c->stream, true, rule, c->rule_chunks, c->rule_chunks_len, true)))
+            return st;
+    } else {
+        if (int s = qr_run(c, QR_DELTA_QK, vh * t, &qk)) return s;
+        if (int s = qr_run(c, QR_DELTA_RULE_GATED, vd, &rule)) return s;
+    }
     return qr_run(c, QR_RMS_NORM_GATE, vh * t, &gate);
 }
 

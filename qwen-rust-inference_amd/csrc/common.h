@@ -196,7 +196,9 @@ int decode_history_read(QrDecodePlan* p, int n, float* out, hipStream_t s);
 constexpr int kChunkMinTokens = 16;
 bool delta_rule_chunked_ok(const Params& a, int count);
 size_t delta_rule_chunked_scratch(const Params& a);  // floats
-int run_delta_rule_chunked(hipStream_t s, bool gated, const Params& a, float* scratch, size_t len);
+// qkn: q and k taken from the convolution output (slot 3) and normalised as
+// DeltaQk does, the normalised rows also stored to slots 1 and 2.
+int run_delta_rule_chunked(hipStream_t s, bool gated, const Params& a, float* scratch, size_t len, bool qkn = false);
 
 // deltanet.hip ---------------------------------------------------------------
 // qr_delta_mixer for one token (decode) when the shape allows; returns -1 if not handled.

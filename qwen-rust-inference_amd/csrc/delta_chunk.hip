@@ -67,7 +67,7 @@ struct PrepLds {
 
 // The record of chunk c0 + xi of head h, into slot xi of `scratch`; every
 // thread of a kPrep-thread block takes part.
-__device__ __forceinline__ void prep_task(const Params& a, int gated, int c0, float* scratch, int xi, int h,
+__device__ __forceinline__ void prep_task(const Params& a, int gated, int qkn, int c0, float* scratch, int xi, int h,
                                           PrepLds& P) {
     auto& ks = P.ks;
     auto& qs = P.qs;
@@ -99,13 +99,20 @@ __device__ __forceinline__ void prep_task(const Params& a, int gated, int c0, fl
     f4v vv[kPrepLoads];
     {  // q and k rows: every thread's float4 loads in flight together
         f4v kv[kPrepLoads], qv[kPrepLoads];
+        // qkn: the rows are the convolution's q and k of the head's key head,
+        // L2-normalised here as DeltaQk does (reference.h:134-143) and stored
+        // to the query / key outputs too; else DeltaQk's outputs
+        const int hk = qkn ? h / (vh / kh) : 0;  // the host checks kh >= 1 and vh % kh == 0 for qkn
+        const float* qsrc = qkn ? a.p[3] + size_t(hk) * kD : a.p[1] + size_t(h) * kD;
+        const float* ksrc = qkn ? a.p[3] + size_t(kh + hk) * kD : a.p[2] + size_t(h) * kD;
+        const size_t rs = qkn ? size_t(stride) : size_t(vh) * kD;
 #pragma unroll
         for (int j = 0; j < kPrepLoads; ++j) {
             const int e = tid + kPrep * j, r = e >> 5, i = (e & 31) * 4;
-            const size_t off = size_t(t0 + r) * vh * kD + size_t(h) * kD + i;
+            const size_t off = size_t(t0 + r) * rs + i;
             const f4v z = {0.f, 0.f, 0.f, 0.f};
-            kv[j] = r < n ? *reinterpret_cast<const f4v*>(a.p[2] + off) : z;
-            qv[j] = r < n ? *reinterpret_cast<const f4v*>(a.p[1] + off) : z;
+            kv[j] = r < n ? *reinterpret_cast<const f4v*>(ksrc + off) : z;
+            qv[j] = r < n ? *reinterpret_cast<const f4v*>(qsrc + off) : z;
         }
 #pragma unroll
         for (int j = 0; j < kPrepLoads; ++j) {
@@ -114,6 +121,28 @@ __device__ __forceinline__ void prep_task(const Params& a, int gated, int c0, fl
             vv[j] = t < n ? *reinterpret_cast<const f4v*>(a.p[3] + size_t(t0 + t) * stride + 2 * size_t(kh) * kD +
                                                           size_t(h) * kD + i)
                           : z;
+        }
+        if (qkn) {  // a row is one half-wave (32 lanes x 4 elements): its sums by xor shuffles
+            const float sd = sqrtf(float(kD));
+#pragma unroll
+            for (int j = 0; j < kPrepLoads; ++j) {
+                const int e = tid + kPrep * j, r = e >> 5, i = (e & 31) * 4;
+                float sq = qv[j].x * qv[j].x + qv[j].y * qv[j].y + qv[j].z * qv[j].z + qv[j].w * qv[j].w;
+                float sk = kv[j].x * kv[j].x + kv[j].y * kv[j].y + kv[j].z * kv[j].z + kv[j].w * kv[j].w;
+#pragma unroll
+                for (int o = 16; o > 0; o >>= 1) {
+                    sq += __shfl_xor(sq, o, kWave);
+                    sk += __shfl_xor(sk, o, kWave);
+                }
+                const float rq = 1.f / sqrtf(sq + 1e-6f), rk = 1.f / sqrtf(sk + 1e-6f);
+                qv[j] = f4v{(qv[j].x * rq) / sd, (qv[j].y * rq) / sd, (qv[j].z * rq) / sd, (qv[j].w * rq) / sd};
+                kv[j] = f4v{kv[j].x * rk, kv[j].y * rk, kv[j].z * rk, kv[j].w * rk};
+                if (r < n) {
+                    const size_t off = size_t(t0 + r) * vh * kD + size_t(h) * kD + i;
+                    *reinterpret_cast<f4v*>(a.p[1] + off) = qv[j];
+                    *reinterpret_cast<f4v*>(a.p[2] + off) = kv[j];
+                }
+            }
         }
 #pragma unroll
         for (int j = 0; j < kPrepLoads; ++j) {
@@ -280,9 +309,9 @@ __device__ __forceinline__ void prep_task(const Params& a, int gated, int c0, fl
     if (tid == 0) rec[kG] = eg[kC - 1];
 }
 
-__global__ __launch_bounds__(kPrep) void rule_chunk_prep_kernel(Params a, int gated, int c0, float* scratch) {
+__global__ __launch_bounds__(kPrep) void rule_chunk_prep_kernel(Params a, int gated, int qkn, int c0, float* scratch) {
     __shared__ PrepLds P;
-    prep_task(a, gated, c0, scratch, int(blockIdx.x), int(blockIdx.y), P);
+    prep_task(a, gated, qkn, c0, scratch, int(blockIdx.x), int(blockIdx.y), P);
 }
 
 __device__ __forceinline__ f4v mfma16(float x, float y, f4v acc) {
@@ -463,7 +492,7 @@ __global__ __launch_bounds__(256) void rule_chunk_scan_kernel(Params a, int c0, 
 // the other. Their LDS together (~122 KiB) leaves room for one block per CU,
 // so on an idle device the blocks take one CU each and the prep work never
 // shares a CU with the latency-bound scan.
-__global__ __launch_bounds__(kPrep) void rule_chunk_scan_prep_kernel(Params a, int gated, int nscan, int sc0,
+__global__ __launch_bounds__(kPrep) void rule_chunk_scan_prep_kernel(Params a, int gated, int qkn, int nscan, int sc0,
                                                                      int schunks, const float* __restrict__ srec,
                                                                      int pc0, int pchunks, float* prec) {
     __shared__ ScanLds S;
@@ -476,7 +505,7 @@ __global__ __launch_bounds__(kPrep) void rule_chunk_scan_prep_kernel(Params a, i
     const int nprep = int(gridDim.x) - nscan;
     for (int task = b - nscan; task < pchunks * vh; task += nprep) {
         if (task != b - nscan) __syncthreads();  // every thread past the previous task's LDS reads
-        prep_task(a, gated, pc0, prec, task / vh, task % vh, P);
+        prep_task(a, gated, qkn, pc0, prec, task / vh, task % vh, P);
     }
 }
 
@@ -511,21 +540,22 @@ size_t delta_rule_chunked_scratch(const Params& a) {
     return size_t(chunks > g ? 2 : 1) * size_t(g) * size_t(a.n[3]) * kRec;
 }
 
-int run_delta_rule_chunked(hipStream_t s, bool gated, const Params& a, float* scratch, size_t len) {
+int run_delta_rule_chunked(hipStream_t s, bool gated, const Params& a, float* scratch, size_t len, bool qkn) {
     if (len < delta_rule_chunked_scratch(a)) return int(hipErrorInvalidValue);
     const int tokens = a.n[4] > 0 ? a.n[4] : 1, vh = a.n[3];
+    if (qkn && (a.n[2] < 1 || vh % a.n[2] != 0)) return int(hipErrorInvalidValue);
     const int chunks = int(ceil_div(tokens, kC)), g = group_chunks(chunks);
     float* buf[2] = {scratch, scratch + size_t(g) * size_t(vh) * kRec};
     const int nscan = vh * kSlices, nprep = nscan < 256 - 64 ? 256 - nscan : 64;
-    hipLaunchKernelGGL(rule_chunk_prep_kernel, dim3(unsigned(g), unsigned(vh)), dim3(kPrep), 0, s, a, gated ? 1 : 0, 0,
-                       buf[0]);
+    hipLaunchKernelGGL(rule_chunk_prep_kernel, dim3(unsigned(g), unsigned(vh)), dim3(kPrep), 0, s, a, gated ? 1 : 0,
+                       qkn ? 1 : 0, 0, buf[0]);
     if (hipError_t e = hipGetLastError()) return int(e);
     for (int c0 = 0, k = 0; c0 < chunks; c0 += g, ++k) {
         const int n = chunks - c0 < g ? chunks - c0 : g, c1 = c0 + n;
         if (c1 < chunks) {  // this group's scan beside the next group's prep
             const int n1 = chunks - c1 < g ? chunks - c1 : g;
             hipLaunchKernelGGL(rule_chunk_scan_prep_kernel, dim3(unsigned(nscan + nprep)), dim3(kPrep), 0, s, a,
-                               gated ? 1 : 0, nscan, c0, n, static_cast<const float*>(buf[k & 1]), c1, n1,
+                               gated ? 1 : 0, qkn ? 1 : 0, nscan, c0, n, static_cast<const float*>(buf[k & 1]), c1, n1,
                                buf[(k + 1) & 1]);
         } else {
             hipLaunchKernelGGL(rule_chunk_scan_kernel, dim3(unsigned(nscan)), dim3(256), 0, s, a, c0, n,

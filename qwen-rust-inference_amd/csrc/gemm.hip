@@ -8,8 +8,9 @@
 // tiles each); K in steps of 32 through LDS; the next K step's global loads are
 // in flight (registers) while the current one is multiplied.
 // fp32 weights with at most 16 rows (the DeltaNet a / b projections):
-// gemm_ab_kernel, two such matrices per launch (x read once), up to 1024
-// columns; wider rows: gemm_skinny_kernel (lanes over columns).
+// two such matrices per launch (x read once), up to 1024 columns, on fp32
+// MFMA (gemm_ab_mfma_kernel) for cols % 16 == 0, else gemm_ab_kernel; wider
+// rows: gemm_skinny_kernel (lanes over columns).
 // Fewer 128 x 128 tiles than CUs: K split into chunks (partials + an ordered
 // sum). The prefill GLU: gate and up in one MFMA kernel with silu(g) * u in
 // the epilogue.
@@ -422,6 +423,53 @@ __global__ __launch_bounds__(512) void gemm_ab_kernel(AbMats m, const float* x, 
     }
 }
 
+// The same two matrices (each up to 16 rows) on fp32 MFMA
+// (v_mfma_f32_16x16x4_f32) when cols % 16 == 0: a block = 16 tokens x both
+// matrices' rows, 8 waves, each with one accumulator tile per matrix (A = the
+// weight rows, B = x^T) over the K steps m = w, w + 8, ... of 16 columns;
+// step 4 m + e takes k = 16 m + 4 (lane / 16) + e, so every operand is one
+// float4 load per m (at 1024 columns a wave's 8 loads per operand go out
+// together, then its 64 MFMAs). The waves' partial tiles are added in wave
+// order through LDS. The FMA kernel above streams x through LDS with one
+// 16-byte LDS read per four FMAs; here the products run on the matrix cores.
+constexpr int AB_WAVES = 8;
+__global__ __launch_bounds__(64 * AB_WAVES) void gemm_ab_mfma_kernel(AbMats m, const float* x, int cols, int batch) {
+    __shared__ f4v part[AB_WAVES][2][64];
+    const int lane = int(threadIdx.x & 63), w = int(threadIdx.x >> 6), lr = lane & 15, g = lane >> 4;
+    const int tok = int(blockIdx.x) * 16 + lr, nm = cols / 16;
+    const f4v z = {0.f, 0.f, 0.f, 0.f};
+    f4v acc0 = z, acc1 = z;
+    constexpr int B = 8;  // float4 of each operand in flight
+    for (int mb = w; mb < nm; mb += AB_WAVES * B) {
+        f4v xv[B], w0[B], w1[B];
+#pragma unroll
+        for (int j = 0; j < B; ++j) {
+            const int mm = mb + AB_WAVES * j, k = 16 * mm + 4 * g;
+            const bool in = mm < nm;
+            xv[j] = in && tok < batch ? *reinterpret_cast<const f4v*>(x + size_t(tok) * cols + k) : z;
+            w0[j] = in && lr < m.rows[0] ? *reinterpret_cast<const f4v*>(m.a[0] + size_t(lr) * cols + k) : z;
+            w1[j] = in && lr < m.rows[1] ? *reinterpret_cast<const f4v*>(m.a[1] + size_t(lr) * cols + k) : z;
+        }
+#pragma unroll
+        for (int j = 0; j < B; ++j)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                acc0 = __builtin_amdgcn_mfma_f32_16x16x4f32(w0[j][e], xv[j][e], acc0, 0, 0, 0);
+                acc1 = __builtin_amdgcn_mfma_f32_16x16x4f32(w1[j][e], xv[j][e], acc1, 0, 0, 0);
+            }
+    }
+    part[w][0][lane] = acc0;
+    part[w][1][lane] = acc1;
+    __syncthreads();
+    if (w < 2 && tok < batch) {  // wave t sums matrix t: lane (lr, g) holds rows 4 g + r of token lr
+        f4v sum = part[0][w][lane];
+#pragma unroll
+        for (int v = 1; v < AB_WAVES; ++v) sum += part[v][w][lane];
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+            if (4 * g + r < m.rows[w]) m.y[w][size_t(tok) * m.rows[w] + 4 * g + r] = sum[r];
+    }
+}
 
 }  // namespace
 
@@ -451,6 +499,11 @@ int gemm_ab(hipStream_t s, float* y1, const float* a1, int rows1, float* y2, con
         cols > AB_COLS || batch < 1)
         return int(hipErrorInvalidValue);
     const AbMats m{{y1, rows2 > 0 ? y2 : y1}, {a1, rows2 > 0 ? a2 : a1}, {rows1, rows2}};
+    if (cols % 16 == 0 && rows1 <= 16 && rows2 <= 16) {
+        hipLaunchKernelGGL(gemm_ab_mfma_kernel, dim3(unsigned(ceil_div(batch, 16))), dim3(64 * AB_WAVES), 0, s, m, x,
+                           cols, batch);
+        return int(hipGetLastError());
+    }
     const int groups = int(ceil_div(batch, AB_TOK));
     hipLaunchKernelGGL(gemm_ab_kernel, dim3(unsigned(groups < 256 ? groups : 256)), dim3(512), 0, s, m, x, cols, batch);
     return int(hipGetLastError());

@@ -106,13 +106,21 @@ __global__ __launch_bounds__(256) void rms_family_kernel(int op, int groups, Par
 // planes (may be null): the output also as the P3 planes a prepared
 // projection takes (common.h), the output read as rows of `width` values (a
 // multiple of d and of 32: consecutive groups form a row); the V consecutive
-// values of a lane are V consecutive BF16 of each plane.
+// values of a lane are V consecutive BF16 of each plane. A plane's 128-byte
+// lines hold 8 rows: with planes, the blocks are renumbered so that each XCD
+// (blocks are dealt to the 8 XCDs round-robin) takes one contiguous range of
+// rows, and the rows that share a line are written through one L2.
+__device__ __forceinline__ int xcd_contiguous(int b, int nb) {
+    const int x = b % 8, per = nb / 8, extra = nb % 8;
+    return x * per + (x < extra ? x : extra) + b / 8;
+}
 template <int PER>
 __global__ __launch_bounds__(256) void rms_rows_kernel(int op, int groups, Params a, __bf16* planes, int width) {
     constexpr int V = PER >= 4 ? 4 : PER, NV = PER / V;
     typedef float fv __attribute__((ext_vector_type(V)));
     typedef __bf16 hv __attribute__((ext_vector_type(V)));
-    const int g = int(blockIdx.x) * 4 + int(threadIdx.x >> 6);
+    const int b = planes ? xcd_contiguous(int(blockIdx.x), int(gridDim.x)) : int(blockIdx.x);
+    const int g = b * 4 + int(threadIdx.x >> 6);
     if (g >= groups) return;  // whole waves only: no block barrier
     const int lane = int(threadIdx.x & 63), d = 64 * PER;
     const size_t off = size_t(g) * d;

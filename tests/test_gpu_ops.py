@@ -63,10 +63,12 @@ def test_gemm_f32_lm_head_shape(gpu, batch):
     test_gemm_f32(gpu, 248320, 1024, batch)
 
 
-@pytest.mark.parametrize("rows,cols", SHAPES_08B + [(33, 20), (7, 12), (3, 260)])
+@pytest.mark.parametrize("rows,cols", SHAPES_08B + [(33, 20), (7, 12), (3, 260), (12, 64), (5, 192)])
 @pytest.mark.parametrize("batch", [127, 130, 257])
 def test_gemm_f32_prefill_tiles(gpu, rows, cols, batch):
-    """Prefill batches across the 128-token MFMA tile edge (and odd widths on the FMA kernel)."""
+    """Prefill batches across the 128-token MFMA tile edge (and odd widths on
+    the FMA kernel; few-row matrices on the 16-token MFMA tiles with their
+    rows past the matrix masked)."""
     test_gemm_f32(gpu, rows, cols, batch)
 
 
@@ -639,31 +641,38 @@ def test_attention_read(gpu, cpu, d, heads, kv, length, tokens):
     parity(g[0], c[0], where="attention")
 
 
-def test_delta_mixer_matches_four_ops(gpu, cpu):
-    """qr_delta_mixer for one token equals ConvSilu, DeltaQk, DeltaRuleGated,
-    RmsNormGate (reference native/rocm/bridge.cpp:730-796)."""
-    rng = np.random.default_rng(99)
-    h, k = 16, 4
-    ch = 3 * h * 128
-    data = dict(projected=rnd(rng, ch), conv_w=rnd(rng, ch * k, 0.3), conv_state=rnd(rng, ch * (k - 1)),
-                recurrent=rnd(rng, h * 128 * 128, 0.5), a=rnd(rng, h), b=rnd(rng, h), gates=rnd(rng, 2 * h, 0.3),
-                norm_w=(1 + rnd(rng, 128, 0.1)).astype(np.float32), z=rnd(rng, h * 128))
-    outs = dict(convolved=ch, query=h * 128, key=h * 128, core=h * 128, gated=h * 128)
+@pytest.mark.parametrize("tokens,kh,vh", [(1, 16, 16), (150, 16, 16), (70, 4, 8)])
+def test_delta_mixer_matches_four_ops(gpu, cpu, tokens, kh, vh):
+    """qr_delta_mixer equals ConvSilu, DeltaQk, DeltaRuleGated, RmsNormGate
+    (reference native/rocm/bridge.cpp:730-796): one token (the fused decode
+    mixer) and prefill lengths, where the chunked rule normalises the
+    convolution's q / k rows itself and stores them to query / key (key
+    heads shared by two value heads in the last case)."""
+    print(f"delta_mixer tokens={tokens} kh={kh} vh={vh}", flush=True)
+    rng = np.random.default_rng(99 + tokens)
+    k, t = 4, tokens
+    ch = (2 * kh + vh) * 128
+    data = dict(projected=rnd(rng, t * ch), conv_w=rnd(rng, ch * k, 0.3), conv_state=rnd(rng, ch * (k - 1)),
+                recurrent=rnd(rng, vh * 128 * 128, 0.5), a=rnd(rng, t * vh), b=rnd(rng, t * vh),
+                gates=rnd(rng, 2 * vh, 0.3), norm_w=(1 + rnd(rng, 128, 0.1)).astype(np.float32),
+                z=rnd(rng, t * vh * 128))
+    outs = dict(convolved=t * ch, query=t * vh * 128, key=t * vh * 128, core=t * vh * 128, gated=t * vh * 128)
     res = []
     for br in (gpu, cpu):
         bufs = {n: br.upload(v) for n, v in data.items()}
         bufs.update({n: br.alloc(s) for n, s in outs.items()})
         if br is gpu:
-            br.delta_mixer(**bufs, key_heads=h, value_heads=h, key_dim=128, value_dim=128, kernel=k, tokens=1,
+            br.delta_mixer(**bufs, key_heads=kh, value_heads=vh, key_dim=128, value_dim=128, kernel=k, tokens=t,
                            channels=ch, eps=1e-6)
         else:
             br.run("CONV_SILU", ch, [bufs["convolved"], bufs["projected"], bufs["conv_w"], bufs["conv_state"]],
-                   [k, 1, ch])
-            br.run("DELTA_QK", h, [bufs["query"], bufs["convolved"], bufs["key"]], [h, h, 128, ch])
-            br.run("DELTA_RULE_GATED", h * 128, [bufs["core"], bufs["query"], bufs["key"], bufs["convolved"],
-                                                 bufs["recurrent"], bufs["a"], bufs["b"], bufs["gates"]],
-                   [128, 128, h, h, 1, ch])
-            br.run("RMS_NORM_GATE", h, [bufs["gated"], bufs["core"], bufs["norm_w"], bufs["z"]], [128], [1e-6, 0.0])
+                   [k, t, ch])
+            br.run("DELTA_QK", vh * t, [bufs["query"], bufs["convolved"], bufs["key"]], [kh, vh, 128, ch])
+            br.run("DELTA_RULE_GATED", vh * 128, [bufs["core"], bufs["query"], bufs["key"], bufs["convolved"],
+                                                  bufs["recurrent"], bufs["a"], bufs["b"], bufs["gates"]],
+                   [128, 128, kh, vh, t, ch])
+            br.run("RMS_NORM_GATE", vh * t, [bufs["gated"], bufs["core"], bufs["norm_w"], bufs["z"]], [128],
+                   [1e-6, 0.0])
         res.append({n: bufs[n].read() for n in list(outs) + ["conv_state", "recurrent"]})
     for n in res[0]:
         parity(res[0][n], res[1][n], where=n)
