@@ -641,13 +641,14 @@ def test_attention_read(gpu, cpu, d, heads, kv, length, tokens):
     parity(g[0], c[0], where="attention")
 
 
-@pytest.mark.parametrize("tokens,kh,vh", [(1, 16, 16), (150, 16, 16), (70, 4, 8)])
+@pytest.mark.parametrize("tokens,kh,vh", [(1, 16, 16), (150, 16, 16), (70, 4, 8), (64 * 66 + 3, 4, 4)])
 def test_delta_mixer_matches_four_ops(gpu, cpu, tokens, kh, vh):
     """qr_delta_mixer equals ConvSilu, DeltaQk, DeltaRuleGated, RmsNormGate
     (reference native/rocm/bridge.cpp:730-796): one token (the fused decode
     mixer) and prefill lengths, where the chunked rule normalises the
     convolution's q / k rows itself and stores them to query / key (key
-    heads shared by two value heads in the last case)."""
+    heads shared by two value heads; past 64 chunks the grouped walk, whose
+    later groups' preps run beside the scan)."""
     print(f"delta_mixer tokens={tokens} kh={kh} vh={vh}", flush=True)
     rng = np.random.default_rng(99 + tokens)
     k, t = 4, tokens
