@@ -236,13 +236,16 @@ __global__ __launch_bounds__(256) void split_sum_kernel(float* y, const float* p
 }
 
 // K splits of an fp32 MFMA GEMM: fewer 128 x 128 tiles than CUs leave CUs
-// idle, so K is cut into up to 4 chunks (multiples of the 32-deep step) until
-// there are about two blocks per CU.
+// idle, so K is cut into up to 16 chunks (multiples of the 32-deep step, at
+// least two steps each) until there are about two blocks per CU. A block's K
+// steps are latency-bound (one step of loads in flight), so a 128-token chunk
+// wants many short K chunks: qkv 6144 x 1024 at 128 tokens, 48 tiles, takes
+// 11 chunks of 3 steps.
 int mfma_splits(int rows, int cols, int batch, int& kchunk) {
     const long tiles = long(ceil_div(rows, MN)) * long(ceil_div(batch, MM));
     int splits = 1;
     if (rows % 4 == 0)
-        while (splits < 4 && tiles * splits < 2 * 256 && cols / (splits + 1) >= 2 * B3K) ++splits;
+        while (splits < 16 && tiles * splits < 2 * 256 && cols / (splits + 1) >= 2 * B3K) ++splits;
     kchunk = int(ceil_div(ceil_div(cols, splits), B3K)) * B3K;
     return int(ceil_div(cols, kchunk));
 }
