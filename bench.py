@@ -438,6 +438,23 @@ def main():
         log(f"BF16 decode @454: {dt / 64 * 1e3:.3f} ms/token, {bf16_bytes * 64 / dt / 1e9:.0f} GB/s of BF16 weights "
             f"(one-launch: {rb.decode_plan})")
         rb.close()
+        # BF16 prefill of the config-3 prompt (one chunk; the engine prepares the
+        # BF16 matrices' planes when the bridge offers qr_gemm_bf16_prepare)
+        n = 2644
+        ids2 = [int(v) for v in np.random.default_rng(2).integers(0, c.vocab_size, n)]
+        times = []
+        for rep in range(4):
+            r2 = mb.new_run(n + 1, chunk=n)
+            mb.sync()
+            t = time.perf_counter()
+            r2.prefill(ids2)
+            if rep:
+                times.append(time.perf_counter() - t)
+            r2.close()
+        dt = float(np.median(times))
+        out["bf16_prefill_2644_ms"] = round(dt * 1e3, 2)
+        out["bf16_prefill_2644_tok_s"] = round(n / dt, 1)
+        log(f"BF16 prefill 2644: {dt * 1e3:.1f} ms (median of {len(times)})")
         mb.close()
         del wb
 

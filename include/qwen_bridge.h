@@ -163,6 +163,16 @@ int qr_gemm_f32_add_norm(Context* c, float* y, const float* a, const float* x, i
  * kernel. */
 int qr_gemm_f32_prepare(Context* c, const float* a, int rows, int cols);
 int qr_gemm_f32_release(Context* c, const float* a);
+/* Prepared BF16 matrices (no counterpart in the reference's ABI; optional,
+ * as qr_gemm_f32_prepare): `packed` is a rows x cols matrix in the words of
+ * the reference's upload_bf16 (src/device.rs:535-549; element 2i in the low
+ * half of word i), 16-byte aligned. When cols % 32 == 0 the bridge keeps its
+ * one plane in the same fragment order (2 bytes per element) and runs every
+ * qr_gemm_bf16 / qr_gemm_bf16_group / qr_gemm_bf16_glu projection of it over
+ * at least 64 tokens on the same kernels with three part products (x's three
+ * planes times the exact BF16 weight). Released and invalidated as prepared
+ * fp32 matrices (qr_gemm_f32_release takes either). */
+int qr_gemm_bf16_prepare(Context* c, const float* packed, int rows, int cols);
 
 /* One decode token in one launch (no counterpart in the reference's ABI; the
  * engine calls it from `forward` when t == 1, nothing is captured, the

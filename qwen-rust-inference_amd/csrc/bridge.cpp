@@ -27,12 +27,16 @@ struct Context {
     size_t rule_chunks_len = 0;
     float* gemm_work = nullptr;  // K-split partial sums of prefill GEMMs
     size_t gemm_work_len = 0;
-    // Prepared fp32 matrices (qr_gemm_f32_prepare): the P3 planes of each
-    // (common.h), by the matrix's device address, for the prefill projections
-    // of gemm_p3.hip; dropped when the matrix is freed or written.
+    // Prepared matrices, by the matrix's device address, for the prefill
+    // projections of gemm_p3.hip: the three P3 planes of an fp32 matrix
+    // (qr_gemm_f32_prepare), or the one P1 plane of a packed BF16 matrix
+    // (qr_gemm_bf16_prepare); dropped when the matrix is freed or written.
     struct Prepared {
         int rows, cols;
         __bf16* w3;
+        int planes;  // 3 (fp32) or 1 (BF16)
+        // the matrix's extent in 32-bit words (BF16: two values per word)
+        size_t words() const { return planes == 3 ? size_t(rows) * cols : (size_t(rows) * cols + 1) / 2; }
     };
     std::map<const float*, Prepared> prepared;
     // A prepared GLU's combined gate / up planes (p3_glu_interleave), made on
@@ -41,6 +45,7 @@ struct Context {
     struct GluPair {
         int rows, cols;
         __bf16* w3;
+        int planes;
     };
     std::map<std::pair<const float*, const float*>, GluPair> glu_pairs;
     // The P3 planes of a projection's input (xp), and a second buffer the GLU
@@ -173,16 +178,19 @@ int ensure(Context* c, float** buf, size_t* len, size_t need, const char* what) 
 
 const void* i8_packed(const float* packed) { return packed; }
 
-// ---- prepared fp32 matrices (csrc/gemm_p3.hip)
+// ---- prepared fp32 and BF16 matrices (csrc/gemm_p3.hip)
 // Projections of at least this many tokens take the P3 planes when their
 // matrix is prepared (fewer tokens: the split-BF16 kernel, whose tiles the
 // small batches fill as well).
 constexpr int kPlanesMinBatch = 64;
 
-const Context::Prepared* prepared_for(Context* c, const void* a, int rows, int cols, int batch) {
-    if (batch < kPlanesMinBatch || rows <= 16) return nullptr;
+// The prepared planes of matrix a of format t (fp32: three planes, BF16: one).
+const Context::Prepared* prepared_for(Context* c, qr::WeightType t, const void* a, int rows, int cols, int batch) {
+    if (batch < kPlanesMinBatch || rows <= 16 || (t != qr::WeightType::F32 && t != qr::WeightType::BF16)) return nullptr;
     auto it = c->prepared.find(static_cast<const float*>(a));
-    if (it == c->prepared.end() || it->second.rows != rows || it->second.cols != cols) return nullptr;
+    if (it == c->prepared.end() || it->second.rows != rows || it->second.cols != cols ||
+        it->second.planes != (t == qr::WeightType::F32 ? 3 : 1))
+        return nullptr;
     return &it->second;
 }
 // A planes buffer large enough for batch rows of cols (queued work on the old
@@ -232,12 +240,14 @@ void planes_made(Context* c, const float* src, int rows, int cols) {
     c->xp_serial = c->serial;
 }
 int p3_project(Context* c, float* y, const Context::Prepared& p, int batch) {
-    if (int st = ensure(c, &c->gemm_work, &c->gemm_work_len, qr::p3_gemm_scratch(batch, p.rows, p.cols),
+    if (int st = ensure(c, &c->gemm_work, &c->gemm_work_len, qr::p3_gemm_scratch(batch, p.rows, p.cols, p.planes),
                         "hipMalloc GEMM split"))
         return st;
-    auto s = scope(c, [&] { return std::string("gemm_f32_p3 ") + shape(p.rows, p.cols, batch); });
+    auto s = scope(c, [&] {
+        return std::string(p.planes == 3 ? "gemm_f32_p3 " : "gemm_bf16_p1 ") + shape(p.rows, p.cols, batch);
+    });
     return launched(c, "gemm_p3", qr::p3_gemm(c->stream, y, c->xp, p.w3, batch, p.rows, p.cols, c->gemm_work,
-                                               c->gemm_work_len));
+                                               c->gemm_work_len, p.planes));
 }
 void drop_prepared(Context* c, std::map<const float*, Context::Prepared>::iterator it) {
     (void)hipStreamSynchronize(c->stream);  // queued GEMMs may still read the planes
@@ -256,7 +266,7 @@ void drop_prepared(Context* c, std::map<const float*, Context::Prepared>::iterat
 void invalidate_prepared(Context* c, const float* p, size_t n) {
     for (auto it = c->prepared.begin(); it != c->prepared.end();) {
         const float* a = it->first;
-        const size_t len = size_t(it->second.rows) * size_t(it->second.cols);
+        const size_t len = it->second.words();
         auto next = std::next(it);
         if (p < a + len && a < p + n) drop_prepared(c, it);
         it = next;
@@ -290,11 +300,9 @@ int rope_table(Context* c, float theta, int rot, const float** out) {
 
 int project(Context* c, qr::WeightType t, float* y, const void* a, const float* x, int rows, int cols, int batch) {
     if (rows < 1 || cols < 1 || batch < 1) return fail(c, "projection shape", -1);
-    if (t == qr::WeightType::F32) {
-        if (const Context::Prepared* p = prepared_for(c, a, rows, cols, batch)) {
-            if (int st = split_input(c, x, cols, batch)) return st;
-            return p3_project(c, y, *p, batch);
-        }
+    if (const Context::Prepared* p = prepared_for(c, t, a, rows, cols, batch)) {
+        if (int st = split_input(c, x, cols, batch)) return st;
+        return p3_project(c, y, *p, batch);
     }
     if (!qr::gemm_preferred(t, rows, cols, batch)) {
         auto s = scope(c, [&] { return std::string("gemv_") + wname(t) + " " + shape(rows, cols, batch); });
@@ -315,15 +323,13 @@ int group(Context* c, qr::WeightType t, int n, const QrProjection* items, const 
     if (qr::gemm_preferred(t, items[0].rows, cols, batch)) {
         bool split = false;  // x's planes, made at the group's first prepared matrix
         for (int i = 0; i < n; ++i) {
-            if (t == qr::WeightType::F32) {
-                if (const Context::Prepared* p = prepared_for(c, items[i].a, items[i].rows, cols, batch)) {
-                    if (!split) {
-                        if (int st = split_input(c, x, cols, batch)) return st;
-                        split = true;
-                    }
-                    if (int st = p3_project(c, items[i].y, *p, batch)) return st;
-                    continue;
+            if (const Context::Prepared* p = prepared_for(c, t, items[i].a, items[i].rows, cols, batch)) {
+                if (!split) {
+                    if (int st = split_input(c, x, cols, batch)) return st;
+                    split = true;
                 }
+                if (int st = p3_project(c, items[i].y, *p, batch)) return st;
+                continue;
             }
             // two consecutive few-row fp32 matrices (the DeltaNet a / b) in one launch
             if (i + 1 < n && qr::gemm_ab_ok(t, items[i].a, x, items[i].rows, cols, batch) &&
@@ -363,19 +369,20 @@ int glu(Context* c, qr::WeightType t, float* product, float* gate_y, float* up_y
         auto s = scope(c, [&] { return std::string("gemv_") + wname(t) + "_glu 2x" + shape(rows, cols, batch); });
         return launched(c, "gemv_glu", qr::gemv_glu(c->stream, t, product, gate, up, x, rows, cols, batch));
     }
-    if (t == qr::WeightType::F32) {
-        const Context::Prepared* pg = prepared_for(c, gate, rows, cols, batch);
-        const Context::Prepared* pu = prepared_for(c, up, rows, cols, batch);
+    {
+        const Context::Prepared* pg = prepared_for(c, t, gate, rows, cols, batch);
+        const Context::Prepared* pu = prepared_for(c, t, up, rows, cols, batch);
         if (pg && pu && rows % 128 == 0) {
             // gate, up and the silu product as ONE kernel over the combined planes (gate_y / up_y
             // untouched, as the fused GLU), the product's planes for the next call (down)
             auto key = std::make_pair(gate, up);
             auto it = c->glu_pairs.find(key);
             if (it == c->glu_pairs.end()) {
-                Context::GluPair pair{rows, cols, nullptr};
-                auto st = hipMalloc(reinterpret_cast<void**>(&pair.w3), qr::p3_elements(2 * rows, cols) * sizeof(__bf16));
+                Context::GluPair pair{rows, cols, nullptr, pg->planes};
+                const size_t elems = pg->planes == 3 ? qr::p3_elements(2 * rows, cols) : qr::p1_elements(2 * rows, cols);
+                auto st = hipMalloc(reinterpret_cast<void**>(&pair.w3), elems * sizeof(__bf16));
                 if (st != hipSuccess) return fail(c, "hipMalloc GLU planes", int(st));
-                if (int e = qr::p3_glu_interleave(c->stream, pair.w3, pg->w3, pu->w3, rows, cols)) {
+                if (int e = qr::p3_glu_interleave(c->stream, pair.w3, pg->w3, pu->w3, rows, cols, pg->planes)) {
                     (void)hipStreamSynchronize(c->stream);
                     (void)hipFree(pair.w3);
                     return fail(c, "GLU planes", e);
@@ -383,15 +390,18 @@ int glu(Context* c, qr::WeightType t, float* product, float* gate_y, float* up_y
                 it = c->glu_pairs.emplace(key, pair).first;
             }
             if (int st = split_input(c, x, cols, batch)) return st;
-            if (int st = ensure(c, &c->gemm_work, &c->gemm_work_len, qr::p3_glu_scratch(batch, rows, cols),
-                                "hipMalloc GEMM split"))
+            if (int st = ensure(c, &c->gemm_work, &c->gemm_work_len,
+                                qr::p3_glu_scratch(batch, rows, cols, it->second.planes), "hipMalloc GEMM split"))
                 return st;
             const bool planes = planes_wanted(c, rows, batch);
             if (planes)
                 if (int st = grow_planes(c, &c->xp_alt, &c->xp_alt_len, rows, batch)) return st;
-            auto s = scope(c, [&] { return std::string("gemm_f32_p3_glu 2x") + shape(rows, cols, batch); });
+            auto s = scope(c, [&] {
+                return std::string(it->second.planes == 3 ? "gemm_f32_p3_glu 2x" : "gemm_bf16_p1_glu 2x") +
+                       shape(rows, cols, batch);
+            });
             const int st = qr::p3_gemm_glu(c->stream, product, planes ? c->xp_alt : nullptr, c->xp, it->second.w3,
-                                           batch, rows, cols, c->gemm_work, c->gemm_work_len);
+                                           batch, rows, cols, c->gemm_work, c->gemm_work_len, it->second.planes);
             if (st == 0 && planes) {
                 std::swap(c->xp, c->xp_alt);
                 std::swap(c->xp_len, c->xp_alt_len);
@@ -772,7 +782,27 @@ int qr_gemm_f32_prepare(Context* c, const float* a, int rows, int cols) {
         (void)hipFree(w3);
         return fail(c, "p3_split", e);
     }
-    c->prepared[a] = Context::Prepared{rows, cols, w3};
+    c->prepared[a] = Context::Prepared{rows, cols, w3, 3};
+    return 0;
+}
+int qr_gemm_bf16_prepare(Context* c, const float* packed, int rows, int cols) {
+    ++c->serial;
+    if (!packed || rows < 1 || cols < 1 || reinterpret_cast<uintptr_t>(packed) % 16 != 0)
+        return fail(c, "GEMM prepare shape", -1);
+    if (!qr::p3_cols_ok(cols)) return 0;  // no plane: its projections keep the split-BF16 kernel
+    auto it = c->prepared.find(packed);
+    if (it != c->prepared.end()) {
+        if (it->second.rows == rows && it->second.cols == cols && it->second.planes == 1) return 0;
+        drop_prepared(c, it);
+    }
+    __bf16* w1 = nullptr;
+    auto st = hipMalloc(reinterpret_cast<void**>(&w1), qr::p1_elements(rows, cols) * sizeof(__bf16));
+    if (st != hipSuccess) return fail(c, "hipMalloc GEMM plane", int(st));
+    if (int e = qr::p1_from_bf16(c->stream, w1, packed, rows, cols)) {
+        (void)hipFree(w1);
+        return fail(c, "p1_from_bf16", e);
+    }
+    c->prepared[packed] = Context::Prepared{rows, cols, w1, 1};
     return 0;
 }
 int qr_gemm_f32_release(Context* c, const float* a) {

@@ -99,20 +99,29 @@ __host__ __device__ inline size_t p3_index(int row, int k, int plane, int kt) {
 size_t p3_elements(int rows, int cols);
 // fp32 [rows, cols] -> P3 planes (cols % 32 == 0, 16-byte aligned pointers).
 int p3_split(hipStream_t s, __bf16* out, const float* in, int rows, int cols);
-// Y[M, N] = X W^T from the P3 planes of X (M rows) and W (N rows), K % 32 ==
-// 0; `work` holds at least p3_gemm_scratch(M, N, K) floats (K-chunk partials).
+// A matrix exact in BF16 as ONE plane in the same fragment order ("P1":
+// element (row, k) at p3_index(row, k, 0, kt) with one plane per fragment
+// slot, i.e. ((row / 32) kt + k / 16) 512 + ...), from the packed BF16 words
+// of the reference's upload_bf16; p1_elements(rows, cols) BF16.
+size_t p1_elements(int rows, int cols);
+int p1_from_bf16(hipStream_t s, __bf16* out, const void* packed, int rows, int cols);
+// Y[M, N] = X W^T from the P3 planes of X (M rows) and W's planes (N rows; 3,
+// or wplanes = 1 for P1), K % 32 == 0; `work` holds at least
+// p3_gemm_scratch(M, N, K, wplanes) floats (K-chunk partials).
 int p3_gemm(hipStream_t s, float* y, const __bf16* xp, const __bf16* wp, int M, int N, int K, float* work,
-            size_t work_len);
-size_t p3_gemm_scratch(int M, int N, int K);
-// The combined planes of a GLU (2 rows x cols; rows % 128 == 0) from the P3
-// planes of gate and up: 64 gate rows, then the same 64 up rows, and so on.
-int p3_glu_interleave(hipStream_t s, __bf16* out, const __bf16* gate, const __bf16* up, int rows, int cols);
+            size_t work_len, int wplanes = 3);
+size_t p3_gemm_scratch(int M, int N, int K, int wplanes = 3);
+// The combined planes of a GLU (2 rows x cols; rows % 128 == 0) from the
+// planes (3, or 1 for P1) of gate and up: 64 gate rows, then the same 64 up
+// rows, and so on.
+int p3_glu_interleave(hipStream_t s, __bf16* out, const __bf16* gate, const __bf16* up, int rows, int cols,
+                      int planes = 3);
 // product[M, rows] = silu(X G^T) * (X U^T) from X's P3 planes and the combined
 // planes; when `planes` is set, the product's P3 planes too (rows / 16 k
-// tiles). `work`: at least p3_glu_scratch(M, rows, K) floats.
+// tiles). `work`: at least p3_glu_scratch(M, rows, K, wplanes) floats.
 int p3_gemm_glu(hipStream_t s, float* product, __bf16* planes, const __bf16* xp, const __bf16* wglu, int M, int rows,
-                int K, float* work, size_t work_len);
-size_t p3_glu_scratch(int M, int rows, int K);
+                int K, float* work, size_t work_len, int wplanes = 3);
+size_t p3_glu_scratch(int M, int rows, int K, int wplanes = 3);
 
 // Y1 = X A1^T and (rows2 > 0) Y2 = X A2^T in one launch for fp32 matrices of
 // at most 16 rows and 1024 columns (the DeltaNet a / b projections of

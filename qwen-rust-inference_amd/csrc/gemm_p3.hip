@@ -35,6 +35,11 @@
 // range of the tile order, which walks groups of 8 tile rows column by column,
 // so the blocks resident on one XCD share X rows and W rows in its L2.
 //
+// Prepared BF16 matrices ("P1": the one plane of a matrix whose values are
+// exact in BF16, in the same fragment order) take the same kernels with one
+// weight plane: three part products per step, x2 w, x1 w and x0 w, each
+// operand read from LDS feeding three MFMAs.
+//
 // The prefill GLU (gemm_p3_glu_kernel): gate and up as one GEMM over planes
 // that interleave them by 64 rows ([gate 64 | up 64] per 128 combined rows,
 // p3_glu_interleave), so a wave's gate value and its up partner sit in the
@@ -55,14 +60,18 @@ constexpr int BM = 128;     // block tile rows (tokens)
 
 // A block tile of 128 tokens x (64 TNW) weight rows: 2 x 2 waves, each
 // 64 x (32 TNW) = 2 x TNW MFMA tiles. One K step (32 deep) of one 32-row tile
-// is 6 fragments; a stage holds the step's X fragments then its W fragments.
-template <int TNW>
+// is 6 fragments of X (2 k tiles x 3 planes) and 2 WP of W (WP weight planes:
+// 3, or 1 for BF16 weights); a stage holds the step's X fragments then its W
+// fragments.
+template <int TNW, int WP = 3>
 struct Geo {
     static constexpr int BN = 64 * TNW;
     static constexpr int XRT = BM / 32, WRT = BN / 32;  // 32-row tiles per operand
-    static constexpr int FRAGS = 6 * (XRT + WRT);        // per stage
+    static constexpr int WF = 2 * WP;                   // W fragments per row tile and step
+    static constexpr int FRAGS = 6 * XRT + WF * WRT;    // per stage
     static constexpr int STAGE = FRAGS * FRAG;
     static constexpr int DMA_PER_WAVE = FRAGS / 4;
+    static_assert(FRAGS % 4 == 0, "the stage's DMAs split over 4 waves");
 };
 
 __device__ __forceinline__ void split3(float v, bf16x8 (&h)[3], int e) {
@@ -143,36 +152,57 @@ __device__ __forceinline__ bool block_work(const Plan& p, int b, int& tm, int& t
 // KiB, and the wave issues in order), while spread out they cost the MFMA
 // stream nothing. sched_barrier(0) around each DMA keeps the scheduler from
 // moving anything across it (it cannot classify the inline assembly).
-template <int TNW, bool DMA, class F>
+template <int TNW, int WP, bool DMA, class F>
 __device__ __forceinline__ void step_mfma(f16v (&acc)[2][TNW], const char* st, int wm, int wn, F&& dma) {
-    using G = Geo<TNW>;
-    constexpr int R = 3 * (2 + TNW), MF = 12 * TNW, ND = G::DMA_PER_WAVE, EVERY = 2 * MF / ND;
+    using G = Geo<TNW, WP>;
+    constexpr int NPQ = WP == 3 ? 6 : 3;              // part products per (X tile, W tile)
+    constexpr int R = WP == 3 ? 3 * (2 + TNW) : 6 + TNW;  // fragment reads per k tile
+    constexpr int MF = 2 * NPQ * TNW;                 // MFMAs per k tile
+    constexpr int ND = G::DMA_PER_WAVE, EVERY = 2 * MF / ND;
     static_assert(R <= MF && EVERY >= 1 && ND * EVERY <= 2 * MF, "reads and DMAs fit the MFMA stream");
-    bf16x8 a[2][2][3], b[2][TNW][3];
-    // read r of k tile k, in the order the products first use them: (x2, w0) (x1, w1) (x0, w2)
+    bf16x8 a[2][2][3], b[2][TNW][WP];
+    auto xfrag = [&](int k, int t, int pl) {
+        return *reinterpret_cast<const bf16x8*>(st + ((2 * wm + t) * 6 + 3 * k + pl) * FRAG);
+    };
+    auto wfrag = [&](int k, int j, int pl) {
+        return *reinterpret_cast<const bf16x8*>(st + (6 * G::XRT + (TNW * wn + j) * G::WF + WP * k + pl) * FRAG);
+    };
+    // read r of k tile k, in the order the products first use them: (x2, w0) (x1, w1) (x0, w2), or
+    // with one weight plane (x2, w) then the x1 and x0 tiles
     auto read = [&](int k, int r) {
-        const int f = r / (2 + TNW), t = r % (2 + TNW);
-        if (t < 2)
-            a[k][t][2 - f] = *reinterpret_cast<const bf16x8*>(st + ((2 * wm + t) * 6 + 3 * k + 2 - f) * FRAG);
-        else
-            b[k][t - 2][f] = *reinterpret_cast<const bf16x8*>(st + (6 * G::XRT + (TNW * wn + t - 2) * 6 + 3 * k + f) * FRAG);
+        if constexpr (WP == 3) {
+            const int f = r / (2 + TNW), t = r % (2 + TNW);
+            if (t < 2)
+                a[k][t][2 - f] = xfrag(k, t, 2 - f);
+            else
+                b[k][t - 2][f] = wfrag(k, t - 2, f);
+        } else if (r < 2 + TNW) {
+            if (r < 2)
+                a[k][r][2] = xfrag(k, r, 2);
+            else
+                b[k][r - 2][0] = wfrag(k, r - 2, 0);
+        } else {
+            const int rr = r - (2 + TNW), f = 1 + rr / 2, t = rr % 2;
+            a[k][t][2 - f] = xfrag(k, t, 2 - f);
+        }
     };
 #pragma unroll
     for (int r = 0; r < R; ++r) read(0, r);
     // the part products, smallest first; the tiles interleaved
     constexpr int P[6] = {2, 1, 0, 1, 0, 0}, Q[6] = {0, 1, 2, 0, 1, 0};
+    constexpr int P1[3] = {2, 1, 0};
 #pragma unroll
     for (int k = 0; k < 2; ++k)
 #pragma unroll
-        for (int pq = 0; pq < 6; ++pq)
+        for (int pq = 0; pq < NPQ; ++pq)
 #pragma unroll
             for (int i = 0; i < 2; ++i)
 #pragma unroll
                 for (int j = 0; j < TNW; ++j) {
-                    const int n = ((k * 6 + pq) * 2 + i) * TNW + j;
+                    const int n = ((k * NPQ + pq) * 2 + i) * TNW + j;
                     if (k == 0 && n < R) read(1, n);
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[k][i][P[pq]], b[k][j][Q[pq]], acc[i][j], 0,
-                                                                       0, 0);
+                    const int pa = WP == 3 ? P[pq] : P1[pq], pb = WP == 3 ? Q[pq] : 0;
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[k][i][pa], b[k][j][pb], acc[i][j], 0, 0, 0);
                     if (DMA && n % EVERY == EVERY / 2 && n / EVERY < ND) {
                         __builtin_amdgcn_sched_barrier(0);
                         dma(n / EVERY);
@@ -183,19 +213,20 @@ __device__ __forceinline__ void step_mfma(f16v (&acc)[2][TNW], const char* st, i
 
 // The K loop of one block: steps [s0, s0 + ns) of tile (tm, tn) into acc.
 // Fragment c of a stage sits at c KiB: c < 6 XRT from X, else W; within an
-// operand, row tile r = c' / 6, then k tile and plane (c' % 6 = 3 k + p), the
-// order of the global layout, so fragment c of step s is at
-// r rt_bytes + (6 s + c' % 6) KiB of its operand. Wave w moves fragments
+// operand of F fragments per row tile and step (6, or 2 WP for W), row tile
+// r = c' / F, then k tile and plane (c' % F = planes k + p), the order of the
+// global layout, so fragment c of step s is at r rt_bytes + (F s + c' % F) KiB
+// of its operand. Wave w moves fragments
 // w DMA_PER_WAVE .. + DMA_PER_WAVE - 1: those of step s + 1 during step s's
 // MFMAs, into the other stage (every wave finished reading it before the
 // barrier of step s).
-template <int TNW>
+template <int TNW, int WP>
 __device__ __forceinline__ void k_loop(f16v (&acc)[2][TNW], char* lds, const __bf16* xp, const __bf16* wp, int kt,
                                        int tm, int tn, int s0, int ns, int w, int lane) {
-    using G = Geo<TNW>;
-    const size_t rt_bytes = size_t(kt) * 3 * FRAG;  // one 32-row tile of a P3 plane set
-    const char* xb = reinterpret_cast<const char*>(xp) + size_t(tm) * G::XRT * rt_bytes + size_t(s0) * 6 * FRAG;
-    const char* wb = reinterpret_cast<const char*>(wp) + size_t(tn) * G::WRT * rt_bytes + size_t(s0) * 6 * FRAG;
+    using G = Geo<TNW, WP>;
+    const size_t rt_x = size_t(kt) * 3 * FRAG, rt_w = size_t(kt) * WP * FRAG;  // one 32-row tile of a plane set
+    const char* xb = reinterpret_cast<const char*>(xp) + size_t(tm) * G::XRT * rt_x + size_t(s0) * 6 * FRAG;
+    const char* wb = reinterpret_cast<const char*>(wp) + size_t(tn) * G::WRT * rt_w + size_t(s0) * G::WF * FRAG;
     const unsigned lds0 = unsigned(reinterpret_cast<size_t>((__attribute__((address_space(3))) char*)lds));
     const unsigned voff = unsigned(lane) * 16u;
     const int wm = w & 1, wn = w >> 1;
@@ -203,7 +234,12 @@ __device__ __forceinline__ void k_loop(f16v (&acc)[2][TNW], char* lds, const __b
         const int c = w * G::DMA_PER_WAVE + i;
         const bool isw = c >= 6 * G::XRT;
         const int cc = isw ? c - 6 * G::XRT : c;
-        const char* src = (isw ? wb : xb) + size_t(cc / 6) * rt_bytes + size_t(6 * s + cc % 6) * FRAG;
+        const char* src;
+        if constexpr (WP == 3)  // both operands 6 fragments per row tile and step
+            src = (isw ? wb : xb) + size_t(cc / 6) * rt_x + size_t(6 * s + cc % 6) * FRAG;
+        else
+            src = isw ? wb + size_t(cc / G::WF) * rt_w + size_t(G::WF * s + cc % G::WF) * FRAG
+                      : xb + size_t(cc / 6) * rt_x + size_t(6 * s + cc % 6) * FRAG;
         dma_frag(src, lds0 + unsigned(stage * G::STAGE + c * FRAG), voff);
     };
 #pragma unroll
@@ -218,12 +254,12 @@ __device__ __forceinline__ void k_loop(f16v (&acc)[2][TNW], char* lds, const __b
     for (; s + 1 < ns; ++s) {
         vm_wait0();     // this wave's fragments of step s landed
         lds_barrier();  // ... every wave's; and every wave is past its reads of step s - 1
-        step_mfma<TNW, true>(acc, lds + (s & 1) * G::STAGE + lane * 16, wm, wn,
-                             [&](int i) { dma_one(s + 1, (s + 1) & 1, i); });
+        step_mfma<TNW, WP, true>(acc, lds + (s & 1) * G::STAGE + lane * 16, wm, wn,
+                                 [&](int i) { dma_one(s + 1, (s + 1) & 1, i); });
     }
     vm_wait0();
     lds_barrier();
-    step_mfma<TNW, false>(acc, lds + (s & 1) * G::STAGE + lane * 16, wm, wn, [](int) {});
+    step_mfma<TNW, WP, false>(acc, lds + (s & 1) * G::STAGE + lane * 16, wm, wn, [](int) {});
 }
 
 // Accumulator register e of lane l in MFMA tile (i, j) of wave (wm, wn): tile
@@ -248,10 +284,10 @@ __device__ __forceinline__ void store_part(float* work, const Plan& p, int kc, i
 }
 
 // Y = X W^T: whole tiles into y, chunks of split tiles into `work`.
-template <int TNW>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void gemm_p3_kernel(
+template <int TNW, int WP>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WP == 3 ? 1 : 2, WP == 3 ? 1 : 2))) void gemm_p3_kernel(
     float* y, float* work, const __bf16* xp, const __bf16* wp, Plan p) {
-    using G = Geo<TNW>;
+    using G = Geo<TNW, WP>;
     __shared__ __attribute__((aligned(1024))) char lds[2 * G::STAGE];
     int tm, tn, kc, r;
     if (!block_work(p, int(blockIdx.x), tm, tn, kc, r)) return;
@@ -259,7 +295,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     const int wm = w & 1, wn = w >> 1;
     const int s0 = kc < 0 ? 0 : kc * p.spc, ns = kc < 0 ? p.kt / 2 : min(p.kt / 2 - s0, p.spc);
     f16v acc[2][TNW];
-    k_loop<TNW>(acc, lds, xp, wp, p.kt, tm, tn, s0, ns, w, lane);
+    k_loop<TNW, WP>(acc, lds, xp, wp, p.kt, tm, tn, s0, ns, w, lane);
     if (kc >= 0) {
         store_part<TNW>(work, p, kc, r, acc, wm, wn, lane);
         return;
@@ -316,9 +352,10 @@ __device__ __forceinline__ void glu_store8(float* product, __bf16* planes, int I
     for (int q = 0; q < 3; ++q) *reinterpret_cast<bf16x8*>(planes + p3_index(m, n, q, I / 16)) = h[q];
 }
 
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void gemm_p3_glu_kernel(
+template <int WP>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WP == 3 ? 1 : 2, WP == 3 ? 1 : 2))) void gemm_p3_glu_kernel(
     float* product, __bf16* planes, float* work, const __bf16* xp, const __bf16* wp, Plan p) {
-    using G = Geo<4>;
+    using G = Geo<4, WP>;
     __shared__ __attribute__((aligned(1024))) char lds[2 * G::STAGE];
     int tm, tn, kc, r;
     if (!block_work(p, int(blockIdx.x), tm, tn, kc, r)) return;
@@ -326,7 +363,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     const int wm = w & 1, wn = w >> 1;
     const int s0 = kc < 0 ? 0 : kc * p.spc, ns = kc < 0 ? p.kt / 2 : min(p.kt / 2 - s0, p.spc);
     f16v acc[2][4];
-    k_loop<4>(acc, lds, xp, wp, p.kt, tm, tn, s0, ns, w, lane);
+    k_loop<4, WP>(acc, lds, xp, wp, p.kt, tm, tn, s0, ns, w, lane);
     if (kc >= 0) {  // raw gate / up sums of a chunk (p3_glu_sum_kernel finishes them)
         store_part<4>(work, p, kc, r, acc, wm, wn, lane);
         return;
@@ -419,9 +456,27 @@ __global__ __launch_bounds__(256) void p3_split_kernel(__bf16* out, const float*
     }
 }
 
+// Packed BF16 [rows, cols] (the reference's upload_bf16 words: element 2 i in
+// the low half of word i) -> the one P1 plane of p3_rows(rows) rows (pad rows
+// zero), in the fragment order of the P3 planes: work item c is lane c % 64 of
+// fragment c / 64, 8 consecutive BF16 of one row, one 16-byte copy.
+__global__ __launch_bounds__(256) void p1_from_bf16_kernel(__bf16* out, const uint16_t* in, int rows, int cols,
+                                                           long chunks) {
+    const int kt = cols / 16;
+    for (long c = blockIdx.x * long(blockDim.x) + threadIdx.x; c < chunks; c += long(gridDim.x) * blockDim.x) {
+        const long f = c >> 6;
+        const int l = int(c & 63), rt = int(f / kt), kk = int(f % kt);
+        const int r = 32 * rt + (l & 31), k = 16 * kk + 8 * (l >> 5);
+        uint4 v = {0u, 0u, 0u, 0u};
+        if (r < rows) v = *reinterpret_cast<const uint4*>(in + size_t(r) * cols + k);
+        *reinterpret_cast<uint4*>(out + size_t(c) * 8) = v;
+    }
+}
+
 // The GLU's combined planes from gate's and up's (each rows x cols, rows %
-// 128 == 0): combined 32-row tile 4 g + t is gate tile 2 g + t (t < 2), else up
-// tile 2 g + t - 2; a tile is contiguous, so this is a copy, 16 bytes per thread.
+// 128 == 0, 3 planes or BF16's 1): combined 32-row tile 4 g + t is gate tile
+// 2 g + t (t < 2), else up tile 2 g + t - 2; a tile is contiguous, so this is
+// a copy, 16 bytes per thread.
 __global__ __launch_bounds__(256) void p3_glu_interleave_kernel(__bf16* out, const __bf16* gate, const __bf16* up,
                                                                 int tiles, size_t tile_elems) {
     const size_t per_tile = tile_elems / 8, total = size_t(tiles) * per_tile;
@@ -434,14 +489,18 @@ __global__ __launch_bounds__(256) void p3_glu_interleave_kernel(__bf16* out, con
 }
 
 // Microseconds of one 32-deep K step of a 128 x bn block tile at the rate the
-// kernels reach on the prefill shapes (0.8B model, 2644 tokens).
-double step_us(int bn) { return bn == 256 ? 2.9 : 1.66; }
+// kernels reach on the prefill shapes (0.8B model, 2644 tokens); one weight
+// plane: half the MFMAs.
+double step_us(int bn, int wp) { return (bn == 256 ? 2.9 : 1.66) * (wp == 3 ? 1.0 : 1.1); }
+// Blocks per round: one per CU (three weight planes: 144 KiB of LDS), two
+// (one plane: 80 KiB each).
+int round_blocks(int wp) { return wp == 3 ? 256 : 512; }
 
 // The plan of an M x N (x K) product with bn-row W tiles: whole rounds of 256
 // blocks take whole tiles; the tiles past them (all, when there are fewer than
 // 256) are split into K chunks when that is estimated faster: the split
 // round's time, plus the partials' sum (their bytes at ~4 TB/s plus ~4 us).
-Plan make_plan(int M, int N, int K, int bn) {
+Plan make_plan(int M, int N, int K, int bn, int wp) {
     Plan p{};
     p.M = M;
     p.N = N;
@@ -449,12 +508,12 @@ Plan make_plan(int M, int N, int K, int bn) {
     p.tiles_m = int(ceil_div(M, BM));
     p.tiles_n = int(ceil_div(N, bn));
     const int tiles = p.tiles_m * p.tiles_n, steps = K / 32;
-    const int whole = tiles / 256, rest = tiles - 256 * whole;
+    const int slots = round_blocks(wp), whole = tiles / slots, rest = tiles - slots * whole;
     int best_c = 1;
-    double best = double(ceil_div(tiles, 256)) * steps * step_us(bn);
+    double best = double(ceil_div(tiles, slots)) * steps * step_us(bn, wp);
     for (int c = 2; c <= 8 && steps / c >= 4 && rest > 0; ++c) {
         const double t =
-            (double(whole) * steps + double(ceil_div(long(rest) * c, 256)) * ceil_div(steps, c)) * step_us(bn) +
+            (double(whole) * steps + double(ceil_div(long(rest) * c, slots)) * ceil_div(steps, c)) * step_us(bn, wp) +
             double(rest) * BM * bn * 4.0 * (c + 1) / 4e6 + 4.0;
         if (t < best) {
             best = t;
@@ -467,7 +526,7 @@ Plan make_plan(int M, int N, int K, int bn) {
         p.chunks = 1;
         p.spc = steps;
     } else {
-        p.full = 256 * whole;
+        p.full = slots * whole;
         p.rem = rest;
         p.spc = int(ceil_div(steps, best_c));
         p.chunks = int(ceil_div(steps, p.spc));
@@ -477,23 +536,35 @@ Plan make_plan(int M, int N, int K, int bn) {
 }
 
 // The estimated time of a plan.
-double plan_us(const Plan& p, int K, int bn) {
-    return (double(ceil_div(p.full, 256)) * (K / 32) + double(ceil_div(long(p.rem) * p.chunks, 256)) * p.spc) *
-               step_us(bn) +
+double plan_us(const Plan& p, int K, int bn, int wp) {
+    const int slots = round_blocks(wp);
+    return (double(ceil_div(p.full, slots)) * (K / 32) + double(ceil_div(long(p.rem) * p.chunks, slots)) * p.spc) *
+               step_us(bn, wp) +
            (p.rem ? double(p.rem) * BM * bn * 4.0 * (p.chunks + 1) / 4e6 + 4.0 : 0.0);
 }
 
 // The W tile width of a plain product: 256 rows unless 128-row tiles are
 // estimated faster.
-int plain_bn(int M, int N, int K) {
-    return plan_us(make_plan(M, N, K, 128), K, 128) < plan_us(make_plan(M, N, K, 256), K, 256) ? 128 : 256;
+int plain_bn(int M, int N, int K, int wp) {
+    return plan_us(make_plan(M, N, K, 128, wp), K, 128, wp) < plan_us(make_plan(M, N, K, 256, wp), K, 256, wp) ? 128
+                                                                                                              : 256;
 }
 
 size_t scratch_of(const Plan& p, int bn) { return size_t(p.rem) * size_t(p.chunks) * BM * size_t(bn); }
 
+template <int WP>
+void launch_gemm(hipStream_t s, int bn, dim3 grid, float* y, float* work, const __bf16* xp, const __bf16* wp,
+                 const Plan& p) {
+    if (bn == 256)
+        hipLaunchKernelGGL((gemm_p3_kernel<4, WP>), grid, dim3(256), 0, s, y, work, xp, wp, p);
+    else
+        hipLaunchKernelGGL((gemm_p3_kernel<2, WP>), grid, dim3(256), 0, s, y, work, xp, wp, p);
+}
+
 }  // namespace
 
 size_t p3_elements(int rows, int cols) { return size_t(p3_rows(rows)) * size_t(cols) * 3; }
+size_t p1_elements(int rows, int cols) { return size_t(p3_rows(rows)) * size_t(cols); }
 
 int p3_split(hipStream_t s, __bf16* out, const float* in, int rows, int cols) {
     if (rows < 1 || !p3_cols_ok(cols) || reinterpret_cast<uintptr_t>(in) % 16 != 0 ||
@@ -505,11 +576,22 @@ int p3_split(hipStream_t s, __bf16* out, const float* in, int rows, int cols) {
     return int(hipGetLastError());
 }
 
-int p3_glu_interleave(hipStream_t s, __bf16* out, const __bf16* gate, const __bf16* up, int rows, int cols) {
-    if (rows < 128 || rows % 128 != 0 || !p3_cols_ok(cols) ||
+int p1_from_bf16(hipStream_t s, __bf16* out, const void* packed, int rows, int cols) {
+    if (rows < 1 || !p3_cols_ok(cols) || reinterpret_cast<uintptr_t>(packed) % 16 != 0 ||
+        reinterpret_cast<uintptr_t>(out) % 16 != 0)
+        return int(hipErrorInvalidValue);
+    const long chunks = long(p3_rows(rows)) * (cols / 8), blocks = (chunks + 255) / 256;
+    hipLaunchKernelGGL(p1_from_bf16_kernel, dim3(unsigned(blocks < 65536 ? blocks : 65536)), dim3(256), 0, s, out,
+                       static_cast<const uint16_t*>(packed), rows, cols, chunks);
+    return int(hipGetLastError());
+}
+
+int p3_glu_interleave(hipStream_t s, __bf16* out, const __bf16* gate, const __bf16* up, int rows, int cols,
+                      int planes) {
+    if (rows < 128 || rows % 128 != 0 || !p3_cols_ok(cols) || (planes != 3 && planes != 1) ||
         ((reinterpret_cast<uintptr_t>(out) | reinterpret_cast<uintptr_t>(gate) | reinterpret_cast<uintptr_t>(up)) % 16))
         return int(hipErrorInvalidValue);
-    const size_t tile = size_t(32) * size_t(cols) * 3;
+    const size_t tile = size_t(32) * size_t(cols) * size_t(planes);
     const int tiles = 2 * rows / 32;
     const size_t total = size_t(tiles) * tile / 8, blocks = (total + 255) / 256;
     hipLaunchKernelGGL(p3_glu_interleave_kernel, dim3(unsigned(blocks < 65536 ? blocks : 65536)), dim3(256), 0, s,
@@ -517,28 +599,29 @@ int p3_glu_interleave(hipStream_t s, __bf16* out, const __bf16* gate, const __bf
     return int(hipGetLastError());
 }
 
-size_t p3_gemm_scratch(int M, int N, int K) {
+size_t p3_gemm_scratch(int M, int N, int K, int wplanes) {
     if (M < 1 || N < 1 || !p3_cols_ok(K)) return 0;
-    const int bn = plain_bn(M, N, K);
-    return scratch_of(make_plan(M, N, K, bn), bn);
+    const int bn = plain_bn(M, N, K, wplanes);
+    return scratch_of(make_plan(M, N, K, bn, wplanes), bn);
 }
-size_t p3_glu_scratch(int M, int rows, int K) {
+size_t p3_glu_scratch(int M, int rows, int K, int wplanes) {
     if (M < 1 || rows < 1 || !p3_cols_ok(K)) return 0;
-    return scratch_of(make_plan(M, 2 * rows, K, 256), 256);
+    return scratch_of(make_plan(M, 2 * rows, K, 256, wplanes), 256);
 }
 
 int p3_gemm(hipStream_t s, float* y, const __bf16* xp, const __bf16* wp, int M, int N, int K, float* work,
-            size_t work_len) {
-    if (M < 1 || N < 1 || !p3_cols_ok(K) || ((reinterpret_cast<uintptr_t>(xp) | reinterpret_cast<uintptr_t>(wp)) % 16))
+            size_t work_len, int wplanes) {
+    if (M < 1 || N < 1 || !p3_cols_ok(K) || (wplanes != 3 && wplanes != 1) ||
+        ((reinterpret_cast<uintptr_t>(xp) | reinterpret_cast<uintptr_t>(wp)) % 16))
         return int(hipErrorInvalidValue);
-    const int bn = plain_bn(M, N, K);
-    const Plan p = make_plan(M, N, K, bn);
+    const int bn = plain_bn(M, N, K, wplanes);
+    const Plan p = make_plan(M, N, K, bn, wplanes);
     if (p.rem > 0 && (!work || work_len < scratch_of(p, bn))) return int(hipErrorInvalidValue);
     const dim3 grid{unsigned(p.full_grid + p.rem * p.chunks)}, block{256u};
-    if (bn == 256)
-        hipLaunchKernelGGL(gemm_p3_kernel<4>, grid, block, 0, s, y, work, xp, wp, p);
+    if (wplanes == 3)
+        launch_gemm<3>(s, bn, grid, y, work, xp, wp, p);
     else
-        hipLaunchKernelGGL(gemm_p3_kernel<2>, grid, block, 0, s, y, work, xp, wp, p);
+        launch_gemm<1>(s, bn, grid, y, work, xp, wp, p);
     if (p.rem > 0) {
         const long n = long(p.rem) * BM * bn / 4;
         if (bn == 256)
@@ -550,16 +633,18 @@ int p3_gemm(hipStream_t s, float* y, const __bf16* xp, const __bf16* wp, int M, 
 }
 
 int p3_gemm_glu(hipStream_t s, float* product, __bf16* planes, const __bf16* xp, const __bf16* wglu, int M, int rows,
-                int K, float* work, size_t work_len) {
-    if (M < 1 || rows < 128 || rows % 128 != 0 || !p3_cols_ok(K) ||
+                int K, float* work, size_t work_len, int wplanes) {
+    if (M < 1 || rows < 128 || rows % 128 != 0 || !p3_cols_ok(K) || (wplanes != 3 && wplanes != 1) ||
         ((reinterpret_cast<uintptr_t>(xp) | reinterpret_cast<uintptr_t>(wglu) | reinterpret_cast<uintptr_t>(product) |
           reinterpret_cast<uintptr_t>(planes)) % 16))
         return int(hipErrorInvalidValue);
-    const Plan p = make_plan(M, 2 * rows, K, 256);
+    const Plan p = make_plan(M, 2 * rows, K, 256, wplanes);
     if (p.rem > 0 && (!work || work_len < scratch_of(p, 256))) return int(hipErrorInvalidValue);
-    const dim3 block{256u};
-    hipLaunchKernelGGL(gemm_p3_glu_kernel, dim3(unsigned(p.full_grid + p.rem * p.chunks)), block, 0, s, product,
-                       planes, work, xp, wglu, p);
+    const dim3 grid{unsigned(p.full_grid + p.rem * p.chunks)}, block{256u};
+    if (wplanes == 3)
+        hipLaunchKernelGGL(gemm_p3_glu_kernel<3>, grid, block, 0, s, product, planes, work, xp, wglu, p);
+    else
+        hipLaunchKernelGGL(gemm_p3_glu_kernel<1>, grid, block, 0, s, product, planes, work, xp, wglu, p);
     if (p.rem > 0) {
         const long n = long(p.rem) * BM * 16;
         hipLaunchKernelGGL(p3_glu_sum_kernel, dim3(unsigned((n + 255) / 256)), block, 0, s, product, planes, work, p);

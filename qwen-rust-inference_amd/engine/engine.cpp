@@ -110,6 +110,7 @@ struct Api {
     void (*decode_free)(Context*, QrDecodePlan*) = nullptr;
     int (*embed_rows)(Context*, float*, const float*, int, int, int, const int32_t*, int) = nullptr;
     int (*gemm_f32_prepare)(Context*, const float*, int, int) = nullptr;
+    int (*gemm_bf16_prepare)(Context*, const float*, int, int) = nullptr;
     int (*profile)(Context*, int) = nullptr;
     long (*profile_read)(Context*, char*, size_t) = nullptr;
     int (*sync_)(Context*) = nullptr;
@@ -187,8 +188,10 @@ struct Api {
             if (!decode_plan || !decode_step || !decode_free) decode_plan = nullptr;
         }
         if (!(disable & QE_NO_EMBED_ROWS)) embed_rows = symbol<decltype(embed_rows)>("qr_embed_rows", false);
-        if (!(disable & QE_NO_PREPARED_GEMM))
+        if (!(disable & QE_NO_PREPARED_GEMM)) {
             gemm_f32_prepare = symbol<decltype(gemm_f32_prepare)>("qr_gemm_f32_prepare", false);
+            gemm_bf16_prepare = symbol<decltype(gemm_bf16_prepare)>("qr_gemm_bf16_prepare", false);
+        }
         profile = symbol<decltype(profile)>("qr_profile", false);
         profile_read = symbol<decltype(profile_read)>("qr_profile_read", false);
         if (!(disable & QE_NO_SNAPSHOTS)) {
@@ -1295,13 +1298,16 @@ QeModel* qe_model_load(const char* bridge_path, int expect_kind, const QwConfig*
             b.gate = DeviceMatrix::make(a, t[QW_GATE], I, H, format);
             b.up = DeviceMatrix::make(a, t[QW_UP], I, H, format);
             b.down = DeviceMatrix::make(a, t[QW_DOWN], H, I, format);
-            // the prefill projections' split planes (optional bridge symbol):
-            // every fp32 block matrix of more than 16 rows with 4-aligned
+            // the prefill projections' planes (optional bridge symbols): every
+            // fp32 or BF16 block matrix of more than 16 rows with 4-aligned
             // columns (the a / b rows have a kernel of their own)
-            if (a->gemm_f32_prepare)
-                for (const DeviceMatrix* dm : {&b.q, &b.k, &b.v, &b.o, &b.qkv, &b.z, &b.out, &b.gate, &b.up, &b.down})
-                    if (dm->buffer.p && dm->f32() && dm->rows > 16 && dm->cols % 4 == 0)
-                        a->check(a->gemm_f32_prepare(a->ctx, dm->buffer.p, int32(dm->rows), int32(dm->cols)));
+            for (const DeviceMatrix* dm : {&b.q, &b.k, &b.v, &b.o, &b.qkv, &b.z, &b.out, &b.gate, &b.up, &b.down}) {
+                if (!dm->buffer.p || dm->rows <= 16 || dm->cols % 4 != 0) continue;
+                if (dm->f32() && a->gemm_f32_prepare)
+                    a->check(a->gemm_f32_prepare(a->ctx, dm->buffer.p, int32(dm->rows), int32(dm->cols)));
+                else if (dm->bf16 && a->gemm_bf16_prepare)
+                    a->check(a->gemm_bf16_prepare(a->ctx, dm->buffer.p, int32(dm->rows), int32(dm->cols)));
+            }
             m->blocks.push_back(std::move(b));
         }
         a->sync();

@@ -156,9 +156,11 @@ class Bridge:
         self._check(fn(self.ctx, ctypes.c_void_p(y.ptr), ctypes.c_void_p(a.ptr), ctypes.c_void_p(x.ptr), rows, cols,
                        batch))
 
-    def prepare(self, a: Buffer, rows: int, cols: int):
-        """qr_gemm_f32_prepare: keep a's split planes for the prefill projections."""
-        self._check(self.L.qr_gemm_f32_prepare(self.ctx, ctypes.c_void_p(a.ptr), rows, cols))
+    def prepare(self, a: Buffer, rows: int, cols: int, kind: str = "f32"):
+        """qr_gemm_f32_prepare (qr_gemm_bf16_prepare for kind "bf16"): keep a's
+        planes for the prefill projections."""
+        fn = self.L.qr_gemm_f32_prepare if kind == "f32" else self.L.qr_gemm_bf16_prepare
+        self._check(fn(self.ctx, ctypes.c_void_p(a.ptr), rows, cols))
 
     def release(self, a: Buffer):
         self._check(self.L.qr_gemm_f32_release(self.ctx, ctypes.c_void_p(a.ptr)))

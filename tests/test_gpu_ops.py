@@ -256,6 +256,87 @@ def test_prepared_group_glu_and_invalidation(gpu):
     gpu.release(mats[1])  # releasing twice (or an unprepared matrix) is accepted
 
 
+@pytest.mark.parametrize("rows,cols,batch", [(6144, 1024, 2644), (1024, 3584, 130), (3584, 1024, 257),
+                                            (512, 1024, 454), (1024, 2048, 64), (48, 1024, 200), (96, 32, 130),
+                                            (4096, 1024, 10240)])
+def test_gemm_bf16_prepared(gpu, rows, cols, batch):
+    """qr_gemm_bf16_prepare: the projection of a prepared BF16 matrix (its one
+    plane in fragment order, three part products x_p w on the P3 kernels:
+    whole tiles, K-split tiles, 128- and 256-row weight tiles) against fp64
+    over the matrix's BF16 values with the fp32 dot-product bound on sampled
+    rows (the last among them), twice bitwise-equal, and within the bound of
+    the unprepared split-BF16 kernel's result."""
+    print(f"gemm bf16 prepared {rows}x{cols} batch {batch}", flush=True)
+    rng = np.random.default_rng(rows + 5 * cols + batch)
+    w = (rng.standard_normal(rows * cols) * 0.02).astype(np.float32)
+    dense = ((w.view(np.uint32) >> 16) << 16).view(np.float32)  # the values pack_bf16 keeps
+    x = rng.standard_normal(batch * cols).astype(np.float32)
+    a, xb = gpu.upload(pack_bf16(w)), gpu.upload(x)
+    plain, y1, y2 = gpu.alloc(batch * rows), gpu.alloc(batch * rows), gpu.alloc(batch * rows)
+    gpu.gemm(plain, a, xb, rows, cols, batch, kind="bf16")
+    gpu.prepare(a, rows, cols, kind="bf16")
+    gpu.gemm(y1, a, xb, rows, cols, batch, kind="bf16")
+    gpu.gemm(y2, a, xb, rows, cols, batch, kind="bf16")
+    got = y1.read().reshape(batch, rows)
+    assert np.array_equal(got, y2.read().reshape(batch, rows))
+    idx = np.unique(np.append(np.random.default_rng(0).integers(0, batch, 64), batch - 1))
+    X, W = x.reshape(batch, cols)[idx].astype(np.float64), dense.reshape(rows, cols).astype(np.float64)
+    want = X @ W.T
+    bound = np.abs(X) @ np.abs(W.T) * 2e-5 + 1e-30
+    assert np.all(np.abs(got[idx] - want) <= bound), np.max(np.abs(got[idx] - want) / bound)
+    other = plain.read().reshape(batch, rows)[idx]
+    assert np.all(np.abs(got[idx] - other) <= 2 * bound)
+
+
+def test_prepared_bf16_group_glu_and_invalidation(gpu):
+    """Prepared BF16 matrices in a group equal their separate prepared
+    projections bitwise (the 16-row a / b matrices unprepared beside them); a
+    prepared BF16 GLU (gate and up in one kernel over their interleaved planes
+    with the silu product; rows % 128 != 0: two prepared projections and the
+    silu product) follows the separate projections to the fp32 bound, gate_y /
+    up_y untouched by the fused form; a qr_write into a prepared matrix drops
+    its plane, so the next projection follows the new values."""
+    rng = np.random.default_rng(15)
+    cols, batch = 1024, 300
+    shapes = [6144, 2048, 16, 16]
+    ws = [(rng.standard_normal(r * cols) * 0.02).astype(np.float32) for r in shapes]
+    mats = [gpu.upload(pack_bf16(w)) for w in ws]
+    for m, r in zip(mats, shapes):
+        if r > 16:
+            gpu.prepare(m, r, cols, kind="bf16")
+    x = gpu.upload(rng.standard_normal(batch * cols).astype(np.float32))
+    ys = [gpu.alloc(batch * r) for r in shapes]
+    gpu.group(list(zip(ys, mats, shapes)), x, cols, batch, kind="bf16")
+    for y, m, r in zip(ys, mats, shapes):
+        one = gpu.alloc(batch * r)
+        gpu.gemm(one, m, x, r, cols, batch, kind="bf16")
+        assert np.array_equal(y.read(), one.read()), r
+    for rows in (3584, 320):
+        gw, uw = [(rng.standard_normal(rows * cols) * 0.02).astype(np.float32) for _ in range(2)]
+        g, u = gpu.upload(pack_bf16(gw)), gpu.upload(pack_bf16(uw))
+        gpu.prepare(g, rows, cols, kind="bf16")
+        gpu.prepare(u, rows, cols, kind="bf16")
+        prod, gy, uy = gpu.alloc(batch * rows), gpu.alloc(batch * rows), gpu.alloc(batch * rows)
+        gpu.glu(prod, gy, uy, g, u, x, rows, cols, batch, kind="bf16")
+        g1, u1 = gpu.alloc(batch * rows), gpu.alloc(batch * rows)
+        gpu.gemm(g1, g, x, rows, cols, batch, kind="bf16")
+        gpu.gemm(u1, u, x, rows, cols, batch, kind="bf16")
+        if rows % 128 == 0:
+            assert not gy.read().any() and not uy.read().any()  # untouched
+        gv, uv = g1.read().astype(np.float64), u1.read().astype(np.float64)
+        parity(prod.read(), gv / (1 + np.exp(-gv)) * uv, where=f"prepared bf16 glu {rows}")
+    # rewrite the first matrix: its plane is dropped, the projection follows the new weights
+    new = (rng.standard_normal(shapes[0] * cols) * 0.02).astype(np.float32)
+    mats[0].write(pack_bf16(new))
+    y = gpu.alloc(batch * shapes[0])
+    gpu.gemm(y, mats[0], x, shapes[0], cols, batch, kind="bf16")
+    X = x.read().reshape(batch, cols)[:16].astype(np.float64)
+    W = ((new.view(np.uint32) >> 16) << 16).view(np.float32).reshape(shapes[0], cols).astype(np.float64)
+    bound = np.abs(X) @ np.abs(W.T) * 2e-5 + 1e-30
+    assert np.all(np.abs(y.read().reshape(batch, shapes[0])[:16] - X @ W.T) <= bound)
+    gpu.release(mats[1])
+
+
 @pytest.mark.parametrize("rows,batch", [(3584, 2644), (3584, 64), (256, 300), (384, 130), (320, 130)])
 def test_prepared_glu_shapes(gpu, rows, batch):
     """A GLU of two prepared matrices (rows % 128 == 0: gate, up and the silu
