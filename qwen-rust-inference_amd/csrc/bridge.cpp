@@ -331,18 +331,18 @@ int group(Context* c, qr::WeightType t, int n, const QrProjection* items, const 
                 if (int st = p3_project(c, items[i].y, *p, batch)) return st;
                 continue;
             }
-            // two consecutive few-row fp32 matrices (the DeltaNet a / b) in one launch
+            // two consecutive few-row fp32 or BF16 matrices (the DeltaNet a / b) in one launch
             if (i + 1 < n && qr::gemm_ab_ok(t, items[i].a, x, items[i].rows, cols, batch) &&
                 qr::gemm_ab_ok(t, items[i + 1].a, x, items[i + 1].rows, cols, batch)) {
                 auto sc = scope(c, [&] {
-                    return std::string("gemm_f32_ab ") + shape(items[i].rows, cols, batch) + "+" +
+                    return std::string("gemm_") + wname(t) + "_ab " + shape(items[i].rows, cols, batch) + "+" +
                            shape(items[i + 1].rows, cols, batch);
                 });
                 if (int st = launched(c, "gemm_ab",
                                       qr::gemm_ab(c->stream, items[i].y, static_cast<const float*>(items[i].a),
                                                   items[i].rows, items[i + 1].y,
                                                   static_cast<const float*>(items[i + 1].a), items[i + 1].rows, x,
-                                                  cols, batch)))
+                                                  cols, batch, t)))
                     return st;
                 ++i;
                 continue;

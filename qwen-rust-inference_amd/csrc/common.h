@@ -123,12 +123,12 @@ int p3_gemm_glu(hipStream_t s, float* product, __bf16* planes, const __bf16* xp,
                 int K, float* work, size_t work_len, int wplanes = 3);
 size_t p3_glu_scratch(int M, int rows, int K, int wplanes = 3);
 
-// Y1 = X A1^T and (rows2 > 0) Y2 = X A2^T in one launch for fp32 matrices of
-// at most 16 rows and 1024 columns (the DeltaNet a / b projections of
-// prefill), when gemm_ab_ok holds for each.
+// Y1 = X A1^T and (rows2 > 0) Y2 = X A2^T in one launch for fp32 (or packed
+// BF16, cols % 16 == 0) matrices of at most 16 rows and 1024 columns (the
+// DeltaNet a / b projections of prefill), when gemm_ab_ok holds for each.
 bool gemm_ab_ok(WeightType t, const void* a, const float* x, int rows, int cols, int batch);
 int gemm_ab(hipStream_t s, float* y1, const float* a1, int rows1, float* y2, const float* a2, int rows2,
-            const float* x, int cols, int batch);
+            const float* x, int cols, int batch, WeightType t = WeightType::F32);
 // product[batch, rows] = silu(X G^T) * (X U^T) in one kernel (prefill, any weight format).
 bool gemm_glu_fused(WeightType t, const void* gate, const void* up, const float* x, int rows, int cols, int batch);
 int gemm_glu(hipStream_t s, WeightType t, float* product, const void* gate, const void* up, const float* x, int rows,
