@@ -337,6 +337,35 @@ def test_qwen08b_bf16_one_launch(qwen08b):
     m.close()
 
 
+def test_qwen08b_bf16_prepared_prefill(qwen08b):
+    """BF16-exact 0.8B prefill of a 96-token prompt as one chunk: every block
+    projection over its prepared BF16 plane (qr_gemm_bf16_prepare: three part
+    products on the plane kernels, the fused GLU, the BF16 a / b on the MFMA
+    a / b kernel), the chunked DeltaRule with a ragged second chunk and
+    prefill attention, against the oracle on the same weights fed token by
+    token: the last row's logits and every state part of a DeltaNet and an
+    attention layer within the fp32 bound, the greedy pick equal; the op
+    sequence without prepared planes within the bound of it."""
+    c, w0 = qwen08b
+    w = bf16_weights(c, w0)
+    prompt = [int(v) for v in np.random.default_rng(23).integers(0, c.vocab_size, 96)]
+    print("oracle on the BF16-exact 0.8B, 96 tokens", flush=True)
+    want, want_logits, s = oracle_greedy(O.Oracle(w), prompt, 1)
+    m = E.Model(w, fmt=E.BF16_EXACT)
+    run = m.new_run(128, chunk=96)
+    logits = run.prefill(prompt)
+    parity(logits, want_logits[0], where="BF16 0.8B prepared prefill logits")
+    assert O.select_greedy(logits) == want[0]
+    for layer in (0, 3):
+        for which in range(4):
+            parity(run.state(layer, which), s.part(layer, which), where=f"BF16 prepared prefill state {layer}/{which}")
+    m.close()
+    plain = E.Model(w, fmt=E.BF16_EXACT, disable=E.NO_PREPARED_GEMM)
+    r2 = plain.new_run(128, chunk=96)
+    parity(r2.prefill(prompt), logits, where="BF16 prefill without planes")
+    plain.close()
+
+
 @pytest.mark.parametrize("vocab", [1000, 3001])
 @pytest.mark.parametrize("fmt", [E.F32, E.BF16_EXACT, E.INT8])
 def test_one_launch_small_vocabulary(vocab, fmt):
