@@ -481,6 +481,22 @@ def main():
         out["int8_hbm_weight_read_frac"] = round(int8_bytes * 64 / dt / 1e9 / HBM_PEAK_GBS, 4)
         log(f"int8 decode @454: {dt / 64 * 1e3:.3f} ms/token, {int8_bytes * 64 / dt / 1e9:.0f} GB/s of int8 weights")
         r8.close()
+        # int8 prefill of the config-3 prompt (one chunk; the engine prepares the
+        # int8 matrices' planes when the bridge offers qr_gemm_i8_prepare)
+        n = 2644
+        ids2 = [int(v) for v in np.random.default_rng(2).integers(0, c.vocab_size, n)]
+        times = []
+        for rep in range(4):
+            r2 = m8.new_run(n + 1, chunk=n)
+            m8.sync()
+            t = time.perf_counter()
+            r2.prefill(ids2)
+            if rep:
+                times.append(time.perf_counter() - t)
+            r2.close()
+        dt = float(np.median(times))
+        out["int8_prefill_2644_ms"] = round(dt * 1e3, 2)
+        log(f"int8 prefill 2644: {dt * 1e3:.1f} ms (median of {len(times)})")
         out["int8_verify4_ms"] = round(verify4_ms(m8, prompt), 3)
         log(f"int8 4-row verify with snapshots + accept(1): {out['int8_verify4_ms']:.3f} ms")
         if args.spec:

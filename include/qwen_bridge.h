@@ -173,6 +173,14 @@ int qr_gemm_f32_release(Context* c, const float* a);
  * planes times the exact BF16 weight). Released and invalidated as prepared
  * fp32 matrices (qr_gemm_f32_release takes either). */
 int qr_gemm_bf16_prepare(Context* c, const float* packed, int rows, int cols);
+/* Prepared int8 matrices (no counterpart in the reference's ABI; optional, as
+ * qr_gemm_bf16_prepare): `packed` is the reference's upload_int8 layout
+ * (src/device.rs:550-561: rows fp32 scales, then the int8 values four per
+ * word). The bridge keeps the values' one plane (integers are exact in BF16);
+ * qr_gemm_i8 / qr_gemm_i8_group / qr_gemm_i8_glu over at least 64 tokens run
+ * the plane kernels and scale each output by its row's scale after the sum
+ * (scale * sum(q x), as qr_gemm_i8). Released and invalidated as above. */
+int qr_gemm_i8_prepare(Context* c, const float* packed, int rows, int cols);
 
 /* One decode token in one launch (no counterpart in the reference's ABI; the
  * engine calls it from `forward` when t == 1, nothing is captured, the

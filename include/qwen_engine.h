@@ -39,7 +39,7 @@ enum QeDisable {
     QE_NO_SNAPSHOTS = 32,    /* qr_snapshots */
     QE_NO_DECODE_STEP = 64,  /* qr_decode_plan / qr_decode_step */
     QE_NO_EMBED_ROWS = 128,  /* qr_embed_rows */
-    QE_NO_PREPARED_GEMM = 256, /* qr_gemm_f32_prepare / qr_gemm_bf16_prepare (prefill projections over planes) */
+    QE_NO_PREPARED_GEMM = 256, /* qr_gemm_{f32,bf16,i8}_prepare (prefill projections over planes) */
     QE_NO_PLAIN_DECODE_LAUNCH = 512, /* one-launch decode steps launched cooperatively
                                         (qr_set_option "decode_cooperative"; without it: no plan) */
     QE_NO_DECODE_ROWS = 1024, /* qr_decode_rows (verify rows: one launch per row instead) */

@@ -30,13 +30,21 @@ struct Context {
     // Prepared matrices, by the matrix's device address, for the prefill
     // projections of gemm_p3.hip: the three P3 planes of an fp32 matrix
     // (qr_gemm_f32_prepare), or the one P1 plane of a packed BF16 matrix
-    // (qr_gemm_bf16_prepare); dropped when the matrix is freed or written.
+    // (qr_gemm_bf16_prepare) or of an int8 matrix's values (qr_gemm_i8_prepare;
+    // its row scales stay in the matrix); dropped when the matrix is freed or
+    // written.
     struct Prepared {
         int rows, cols;
         __bf16* w3;
-        int planes;  // 3 (fp32) or 1 (BF16)
-        // the matrix's extent in 32-bit words (BF16: two values per word)
-        size_t words() const { return planes == 3 ? size_t(rows) * cols : (size_t(rows) * cols + 1) / 2; }
+        int planes;  // 3 (fp32) or 1 (BF16, int8)
+        qr::WeightType kind;
+        // int8: the rows' scales (the matrix's first `rows` words)
+        const float* scales;
+        // the matrix's extent in 32-bit words
+        size_t words() const {
+            const size_t n = size_t(rows) * size_t(cols);
+            return kind == qr::WeightType::F32 ? n : kind == qr::WeightType::BF16 ? (n + 1) / 2 : rows + (n + 3) / 4;
+        }
     };
     std::map<const float*, Prepared> prepared;
     // A prepared GLU's combined gate / up planes (p3_glu_interleave), made on
@@ -184,12 +192,12 @@ const void* i8_packed(const float* packed) { return packed; }
 // small batches fill as well).
 constexpr int kPlanesMinBatch = 64;
 
-// The prepared planes of matrix a of format t (fp32: three planes, BF16: one).
+// The prepared planes of matrix a of format t (fp32: three planes; BF16 and
+// int8: one).
 const Context::Prepared* prepared_for(Context* c, qr::WeightType t, const void* a, int rows, int cols, int batch) {
-    if (batch < kPlanesMinBatch || rows <= 16 || (t != qr::WeightType::F32 && t != qr::WeightType::BF16)) return nullptr;
+    if (batch < kPlanesMinBatch || rows <= 16) return nullptr;
     auto it = c->prepared.find(static_cast<const float*>(a));
-    if (it == c->prepared.end() || it->second.rows != rows || it->second.cols != cols ||
-        it->second.planes != (t == qr::WeightType::F32 ? 3 : 1))
+    if (it == c->prepared.end() || it->second.rows != rows || it->second.cols != cols || it->second.kind != t)
         return nullptr;
     return &it->second;
 }
@@ -244,10 +252,10 @@ int p3_project(Context* c, float* y, const Context::Prepared& p, int batch) {
                         "hipMalloc GEMM split"))
         return st;
     auto s = scope(c, [&] {
-        return std::string(p.planes == 3 ? "gemm_f32_p3 " : "gemm_bf16_p1 ") + shape(p.rows, p.cols, batch);
+        return std::string("gemm_") + wname(p.kind) + (p.planes == 3 ? "_p3 " : "_p1 ") + shape(p.rows, p.cols, batch);
     });
     return launched(c, "gemm_p3", qr::p3_gemm(c->stream, y, c->xp, p.w3, batch, p.rows, p.cols, c->gemm_work,
-                                               c->gemm_work_len, p.planes));
+                                               c->gemm_work_len, p.planes, p.scales));
 }
 void drop_prepared(Context* c, std::map<const float*, Context::Prepared>::iterator it) {
     (void)hipStreamSynchronize(c->stream);  // queued GEMMs may still read the planes
@@ -397,11 +405,12 @@ int glu(Context* c, qr::WeightType t, float* product, float* gate_y, float* up_y
             if (planes)
                 if (int st = grow_planes(c, &c->xp_alt, &c->xp_alt_len, rows, batch)) return st;
             auto s = scope(c, [&] {
-                return std::string(it->second.planes == 3 ? "gemm_f32_p3_glu 2x" : "gemm_bf16_p1_glu 2x") +
+                return std::string("gemm_") + wname(t) + (it->second.planes == 3 ? "_p3_glu 2x" : "_p1_glu 2x") +
                        shape(rows, cols, batch);
             });
             const int st = qr::p3_gemm_glu(c->stream, product, planes ? c->xp_alt : nullptr, c->xp, it->second.w3,
-                                           batch, rows, cols, c->gemm_work, c->gemm_work_len, it->second.planes);
+                                           batch, rows, cols, c->gemm_work, c->gemm_work_len, it->second.planes,
+                                           pg->scales, pu->scales);
             if (st == 0 && planes) {
                 std::swap(c->xp, c->xp_alt);
                 std::swap(c->xp_len, c->xp_alt_len);
@@ -782,28 +791,38 @@ int qr_gemm_f32_prepare(Context* c, const float* a, int rows, int cols) {
         (void)hipFree(w3);
         return fail(c, "p3_split", e);
     }
-    c->prepared[a] = Context::Prepared{rows, cols, w3, 3};
+    c->prepared[a] = Context::Prepared{rows, cols, w3, 3, qr::WeightType::F32, nullptr};
     return 0;
 }
-int qr_gemm_bf16_prepare(Context* c, const float* packed, int rows, int cols) {
+// The one plane of a BF16 or int8 matrix (qr_gemm_bf16_prepare / qr_gemm_i8_prepare).
+static int prepare_p1(Context* c, qr::WeightType t, const float* packed, int rows, int cols) {
     ++c->serial;
     if (!packed || rows < 1 || cols < 1 || reinterpret_cast<uintptr_t>(packed) % 16 != 0)
         return fail(c, "GEMM prepare shape", -1);
     if (!qr::p3_cols_ok(cols)) return 0;  // no plane: its projections keep the split-BF16 kernel
     auto it = c->prepared.find(packed);
     if (it != c->prepared.end()) {
-        if (it->second.rows == rows && it->second.cols == cols && it->second.planes == 1) return 0;
+        if (it->second.rows == rows && it->second.cols == cols && it->second.kind == t) return 0;
         drop_prepared(c, it);
     }
     __bf16* w1 = nullptr;
     auto st = hipMalloc(reinterpret_cast<void**>(&w1), qr::p1_elements(rows, cols) * sizeof(__bf16));
     if (st != hipSuccess) return fail(c, "hipMalloc GEMM plane", int(st));
-    if (int e = qr::p1_from_bf16(c->stream, w1, packed, rows, cols)) {
+    const int e = t == qr::WeightType::BF16 ? qr::p1_from_bf16(c->stream, w1, packed, rows, cols)
+                                            : qr::p1_from_i8(c->stream, w1, packed, rows, cols);
+    if (e) {
         (void)hipFree(w1);
-        return fail(c, "p1_from_bf16", e);
+        return fail(c, "GEMM plane", e);
     }
-    c->prepared[packed] = Context::Prepared{rows, cols, w1, 1};
+    c->prepared[packed] =
+        Context::Prepared{rows, cols, w1, 1, t, t == qr::WeightType::I8 ? packed : nullptr};
     return 0;
+}
+int qr_gemm_bf16_prepare(Context* c, const float* packed, int rows, int cols) {
+    return prepare_p1(c, qr::WeightType::BF16, packed, rows, cols);
+}
+int qr_gemm_i8_prepare(Context* c, const float* packed, int rows, int cols) {
+    return prepare_p1(c, qr::WeightType::I8, packed, rows, cols);
 }
 int qr_gemm_f32_release(Context* c, const float* a) {
     ++c->serial;

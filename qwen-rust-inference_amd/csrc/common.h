@@ -105,11 +105,15 @@ int p3_split(hipStream_t s, __bf16* out, const float* in, int rows, int cols);
 // of the reference's upload_bf16; p1_elements(rows, cols) BF16.
 size_t p1_elements(int rows, int cols);
 int p1_from_bf16(hipStream_t s, __bf16* out, const void* packed, int rows, int cols);
+// The same plane from the int8 values of a [rows fp32 scales | int8 values]
+// matrix (the reference's upload_int8); the scales are applied after the sum.
+int p1_from_i8(hipStream_t s, __bf16* out, const void* packed, int rows, int cols);
 // Y[M, N] = X W^T from the P3 planes of X (M rows) and W's planes (N rows; 3,
-// or wplanes = 1 for P1), K % 32 == 0; `work` holds at least
+// or wplanes = 1 for P1), K % 32 == 0, each column times scale[n] after the
+// sum when `scale` is set (int8 weights, P1 only); `work` holds at least
 // p3_gemm_scratch(M, N, K, wplanes) floats (K-chunk partials).
 int p3_gemm(hipStream_t s, float* y, const __bf16* xp, const __bf16* wp, int M, int N, int K, float* work,
-            size_t work_len, int wplanes = 3);
+            size_t work_len, int wplanes = 3, const float* scale = nullptr);
 size_t p3_gemm_scratch(int M, int N, int K, int wplanes = 3);
 // The combined planes of a GLU (2 rows x cols; rows % 128 == 0) from the
 // planes (3, or 1 for P1) of gate and up: 64 gate rows, then the same 64 up
@@ -120,12 +124,13 @@ int p3_glu_interleave(hipStream_t s, __bf16* out, const __bf16* gate, const __bf
 // planes; when `planes` is set, the product's P3 planes too (rows / 16 k
 // tiles). `work`: at least p3_glu_scratch(M, rows, K, wplanes) floats.
 int p3_gemm_glu(hipStream_t s, float* product, __bf16* planes, const __bf16* xp, const __bf16* wglu, int M, int rows,
-                int K, float* work, size_t work_len, int wplanes = 3);
+                int K, float* work, size_t work_len, int wplanes = 3, const float* scale_gate = nullptr,
+                const float* scale_up = nullptr);
 size_t p3_glu_scratch(int M, int rows, int K, int wplanes = 3);
 
 // Y1 = X A1^T and (rows2 > 0) Y2 = X A2^T in one launch for fp32 (or packed
-// BF16, cols % 16 == 0) matrices of at most 16 rows and 1024 columns (the
-// DeltaNet a / b projections of prefill), when gemm_ab_ok holds for each.
+// BF16 / int8, cols % 16 == 0) matrices of at most 16 rows and 1024 columns
+// (the DeltaNet a / b projections of prefill), when gemm_ab_ok holds for each.
 bool gemm_ab_ok(WeightType t, const void* a, const float* x, int rows, int cols, int batch);
 int gemm_ab(hipStream_t s, float* y1, const float* a1, int rows1, float* y2, const float* a2, int rows2,
             const float* x, int cols, int batch, WeightType t = WeightType::F32);

@@ -10,8 +10,8 @@
 // fp32 weights with at most 16 rows (the DeltaNet a / b projections):
 // two such matrices per launch (x read once), up to 1024 columns, on fp32
 // MFMA (gemm_ab_mfma_kernel) for cols % 16 == 0, else gemm_ab_kernel; wider
-// rows: gemm_skinny_kernel (lanes over columns). BF16 weights of that shape
-// (cols % 16 == 0) take gemm_ab_mfma_kernel too.
+// rows: gemm_skinny_kernel (lanes over columns). BF16 and int8 weights of
+// that shape (cols % 16 == 0) take gemm_ab_mfma_kernel too.
 // Fewer 128 x 128 tiles than CUs: K split into chunks (partials + an ordered
 // sum). The prefill GLU: gate and up in one MFMA kernel with silu(g) * u in
 // the epilogue.
@@ -436,10 +436,11 @@ __global__ __launch_bounds__(512) void gemm_ab_kernel(AbMats m, const float* x, 
 // together, then its 64 MFMAs). The waves' partial tiles are added in wave
 // order through LDS. The FMA kernel above streams x through LDS with one
 // 16-byte LDS read per four FMAs; here the products run on the matrix cores.
-// BF: the matrices are packed BF16 (their values widened exactly to fp32 as
-// they load, 8 bytes per 4 values).
+// T: fp32, packed BF16 (values widened exactly to fp32 as they load, 8 bytes
+// per 4 values) or int8 ([rows scales | values], 4 bytes per 4 values; each
+// output scaled by its row's scale after the sum, as qr_gemm_i8).
 constexpr int AB_WAVES = 8;
-template <bool BF>
+template <WeightType T>
 __global__ __launch_bounds__(64 * AB_WAVES) void gemm_ab_mfma_kernel(AbMats m, const float* x, int cols, int batch) {
     __shared__ f4v part[AB_WAVES][2][64];
     const int lane = int(threadIdx.x & 63), w = int(threadIdx.x >> 6), lr = lane & 15, g = lane >> 4;
@@ -455,11 +456,16 @@ __global__ __launch_bounds__(64 * AB_WAVES) void gemm_ab_mfma_kernel(AbMats m, c
             const bool in = mm < nm;
             auto wload = [&](int mi) -> f4v {
                 if (!(in && lr < m.rows[mi])) return z;
-                if constexpr (BF) {
+                if constexpr (T == WeightType::BF16) {
                     const uint2 v = *reinterpret_cast<const uint2*>(reinterpret_cast<const uint16_t*>(m.a[mi]) +
                                                                     size_t(lr) * cols + k);
                     return f4v{__uint_as_float(v.x << 16), __uint_as_float(v.x & 0xffff0000u),
                                __uint_as_float(v.y << 16), __uint_as_float(v.y & 0xffff0000u)};
+                } else if constexpr (T == WeightType::I8) {
+                    const unsigned v = *reinterpret_cast<const unsigned*>(
+                        reinterpret_cast<const int8_t*>(m.a[mi] + m.rows[mi]) + size_t(lr) * cols + k);
+                    return f4v{float(int(v << 24) >> 24), float(int(v << 16) >> 24), float(int(v << 8) >> 24),
+                               float(int(v) >> 24)};
                 } else {
                     return *reinterpret_cast<const f4v*>(m.a[mi] + size_t(lr) * cols + k);
                 }
@@ -485,7 +491,11 @@ __global__ __launch_bounds__(64 * AB_WAVES) void gemm_ab_mfma_kernel(AbMats m, c
         for (int v = 1; v < AB_WAVES; ++v) sum += part[v][w][lane];
 #pragma unroll
         for (int r = 0; r < 4; ++r)
-            if (4 * g + r < m.rows[w]) m.y[w][size_t(tok) * m.rows[w] + 4 * g + r] = sum[r];
+            if (4 * g + r < m.rows[w]) {
+                float v = sum[r];
+                if constexpr (T == WeightType::I8) v = m.a[w][4 * g + r] * v;
+                m.y[w][size_t(tok) * m.rows[w] + 4 * g + r] = v;
+            }
     }
 }
 
@@ -508,22 +518,23 @@ size_t gemm_scratch(WeightType t, int rows, int cols, int batch) {
 }
 
 bool gemm_ab_ok(WeightType t, const void* a, const float* x, int rows, int cols, int batch) {
-    return (t == WeightType::F32 || (t == WeightType::BF16 && cols % 16 == 0)) && gemm_preferred(t, rows, cols, batch) &&
-           rows >= 1 && rows <= AB_ROWS / 2 && cols <= AB_COLS && mfma_ok(t, a, x, cols);
+    return (t == WeightType::F32 || cols % 16 == 0) && gemm_preferred(t, rows, cols, batch) && rows >= 1 &&
+           rows <= AB_ROWS / 2 && cols <= AB_COLS && mfma_ok(t, a, x, cols);
 }
 int gemm_ab(hipStream_t s, float* y1, const float* a1, int rows1, float* y2, const float* a2, int rows2,
             const float* x, int cols, int batch, WeightType t) {
     if (rows1 < 1 || rows2 < 0 || rows1 + rows2 > AB_ROWS || (rows2 > 0 && (!y2 || !a2)) || cols % 4 != 0 ||
-        cols > AB_COLS || batch < 1 || (t != WeightType::F32 && (t != WeightType::BF16 || cols % 16 != 0)))
+        cols > AB_COLS || batch < 1 || (t != WeightType::F32 && cols % 16 != 0))
         return int(hipErrorInvalidValue);
     const AbMats m{{y1, rows2 > 0 ? y2 : y1}, {a1, rows2 > 0 ? a2 : a1}, {rows1, rows2}};
     if (cols % 16 == 0 && rows1 <= 16 && rows2 <= 16) {
+        const dim3 grid{unsigned(ceil_div(batch, 16))}, block{64u * AB_WAVES};
         if (t == WeightType::BF16)
-            hipLaunchKernelGGL(gemm_ab_mfma_kernel<true>, dim3(unsigned(ceil_div(batch, 16))), dim3(64 * AB_WAVES), 0,
-                               s, m, x, cols, batch);
+            hipLaunchKernelGGL(gemm_ab_mfma_kernel<WeightType::BF16>, grid, block, 0, s, m, x, cols, batch);
+        else if (t == WeightType::I8)
+            hipLaunchKernelGGL(gemm_ab_mfma_kernel<WeightType::I8>, grid, block, 0, s, m, x, cols, batch);
         else
-            hipLaunchKernelGGL(gemm_ab_mfma_kernel<false>, dim3(unsigned(ceil_div(batch, 16))), dim3(64 * AB_WAVES), 0,
-                               s, m, x, cols, batch);
+            hipLaunchKernelGGL(gemm_ab_mfma_kernel<WeightType::F32>, grid, block, 0, s, m, x, cols, batch);
         return int(hipGetLastError());
     }
     const int groups = int(ceil_div(batch, AB_TOK));
@@ -556,7 +567,7 @@ int gemm(hipStream_t s, WeightType t, float* y, const void* a, const float* x, i
          float* work, size_t work_len) {
     dim3 grid(ceil_div(rows, BN), ceil_div(batch, BM));
     if (mfma_ok(t, a, x, cols)) {
-        if (t == WeightType::BF16 && rows <= AB_ROWS / 2 && cols <= AB_COLS && cols % 16 == 0)
+        if (t != WeightType::F32 && rows <= AB_ROWS / 2 && cols <= AB_COLS && cols % 16 == 0)
             return gemm_ab(s, y, static_cast<const float*>(a), rows, nullptr, nullptr, 0, x, cols, batch, t);
         if (t == WeightType::F32 && rows <= SK_ROWS) {
             if (cols <= AB_COLS) return gemm_ab(s, y, static_cast<const float*>(a), rows, nullptr, nullptr, 0, x, cols, batch);

@@ -115,6 +115,10 @@ struct Plan {
     int full_grid;         // blocks of those: 8 ceil(full / 8)
     int rem;               // tiles split along K (the rest)
     int chunks, spc;       // K chunks of a split tile, 32-deep steps per chunk
+    // int8 weights: the row scales (the GLU: gate's, and up's in scale_up),
+    // applied after the sum; null otherwise
+    const float* scale;
+    const float* scale_up;
 };
 
 // Tile t of the grouped order: groups of 8 tile rows, column by column.
@@ -283,8 +287,9 @@ __device__ __forceinline__ void store_part(float* work, const Plan& p, int kc, i
                 part[acc_row(wm, i, e, lane) * BN + 32 * (TNW * wn + j) + (lane & 31)] = acc[i][j][e];
 }
 
-// Y = X W^T: whole tiles into y, chunks of split tiles into `work`.
-template <int TNW, int WP>
+// Y = X W^T: whole tiles into y, chunks of split tiles into `work`. SC: each
+// output column scaled by its weight row's p.scale after the sum (int8).
+template <int TNW, int WP, bool SC = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WP == 3 ? 1 : 2, WP == 3 ? 1 : 2))) void gemm_p3_kernel(
     float* y, float* work, const __bf16* xp, const __bf16* wp, Plan p) {
     using G = Geo<TNW, WP>;
@@ -304,12 +309,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WP == 3 ? 1
     for (int j = 0; j < TNW; ++j) {
         const int n = tn * G::BN + 32 * (TNW * wn + j) + (lane & 31);
         if (n >= p.N) continue;
+        float sc = 1.f;
+        if constexpr (SC) sc = p.scale[n];
 #pragma unroll
         for (int i = 0; i < 2; ++i)
 #pragma unroll
             for (int e = 0; e < 16; ++e) {
                 const int m = tm * BM + acc_row(wm, i, e, lane);
-                if (m < p.M) y[size_t(m) * p.N + n] = acc[i][j][e];
+                if (m < p.M) y[size_t(m) * p.N + n] = SC ? sc * acc[i][j][e] : acc[i][j][e];
             }
     }
 }
@@ -332,7 +339,7 @@ __global__ __launch_bounds__(256) void p3_sum_kernel(float* y, const float* work
     for (int k = 1; k < p.chunks; ++k) s += *reinterpret_cast<const f4v*>(src + size_t(k) * stride);
 #pragma unroll
     for (int q = 0; q < 4; ++q)
-        if (n + q < p.N) y[size_t(m) * p.N + n + q] = s[q];
+        if (n + q < p.N) y[size_t(m) * p.N + n + q] = p.scale ? p.scale[n + q] * s[q] : s[q];
 }
 
 // ---- GLU: combined rows 128 g + [0, 64) are gate rows 64 g + .., 128 g +
@@ -352,7 +359,7 @@ __device__ __forceinline__ void glu_store8(float* product, __bf16* planes, int I
     for (int q = 0; q < 3; ++q) *reinterpret_cast<bf16x8*>(planes + p3_index(m, n, q, I / 16)) = h[q];
 }
 
-template <int WP>
+template <int WP, bool SC = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WP == 3 ? 1 : 2, WP == 3 ? 1 : 2))) void gemm_p3_glu_kernel(
     float* product, __bf16* planes, float* work, const __bf16* xp, const __bf16* wp, Plan p) {
     using G = Geo<4, WP>;
@@ -377,11 +384,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WP == 3 ? 1
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
+        for (int j = 0; j < 2; ++j) {
+            float sg = 1.f, su = 1.f;  // int8: the gate and up rows' scales of this product column
+            if constexpr (SC) {
+                const int n = tn * 128 + 64 * wn + 32 * j + (lane & 31);
+                sg = p.scale[n];
+                su = p.scale_up[n];
+            }
 #pragma unroll
             for (int e = 0; e < 16; ++e)
                 pt[acc_row(wm, i, e, lane) * PITCH + 64 * wn + 32 * j + (lane & 31)] =
-                    siluf_(acc[i][j][e]) * acc[i][j + 2][e];
+                    SC ? siluf_(sg * acc[i][j][e]) * (su * acc[i][j + 2][e]) : siluf_(acc[i][j][e]) * acc[i][j + 2][e];
+        }
     lds_barrier();
     const int I = p.N / 2;
 #pragma unroll
@@ -422,6 +436,12 @@ __global__ __launch_bounds__(256) void p3_glu_sum_kernel(float* product, __bf16*
         for (int e = 0; e < 8; ++e) {
             g[e] += src[size_t(k) * stride + gcol + e];
             u[e] += src[size_t(k) * stride + gcol + 64 + e];
+        }
+    if (p.scale)  // int8: the rows' scales after the sums
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            g[e] = p.scale[tn * 128 + c8 + e] * g[e];
+            u[e] = p.scale_up[tn * 128 + c8 + e] * u[e];
         }
     float v[8];
 #pragma unroll
@@ -470,6 +490,30 @@ __global__ __launch_bounds__(256) void p1_from_bf16_kernel(__bf16* out, const ui
         uint4 v = {0u, 0u, 0u, 0u};
         if (r < rows) v = *reinterpret_cast<const uint4*>(in + size_t(r) * cols + k);
         *reinterpret_cast<uint4*>(out + size_t(c) * 8) = v;
+    }
+}
+
+// The int8 values of a [rows fp32 scales | rows x cols int8] matrix (the
+// reference's upload_int8) -> their one P1 plane (integers of magnitude <= 128
+// are exact in BF16; the scales stay in the matrix and are applied after the
+// sum): 8 values, one 16-byte store, per work item as p1_from_bf16_kernel.
+__global__ __launch_bounds__(256) void p1_from_i8_kernel(__bf16* out, const int8_t* in, int rows, int cols,
+                                                         long chunks) {
+    typedef __bf16 bf16x8v __attribute__((ext_vector_type(8)));
+    const int kt = cols / 16;
+    for (long c = blockIdx.x * long(blockDim.x) + threadIdx.x; c < chunks; c += long(gridDim.x) * blockDim.x) {
+        const long f = c >> 6;
+        const int l = int(c & 63), rt = int(f / kt), kk = int(f % kt);
+        const int r = 32 * rt + (l & 31), k = 16 * kk + 8 * (l >> 5);
+        bf16x8v h;
+        uint2 v = {0u, 0u};
+        if (r < rows) v = *reinterpret_cast<const uint2*>(in + size_t(r) * cols + k);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const unsigned w = e < 4 ? v.x : v.y;
+            h[e] = __bf16(float(int(w << (24 - 8 * (e & 3))) >> 24));
+        }
+        *reinterpret_cast<bf16x8v*>(out + size_t(c) * 8) = h;
     }
 }
 
@@ -552,13 +596,13 @@ int plain_bn(int M, int N, int K, int wp) {
 
 size_t scratch_of(const Plan& p, int bn) { return size_t(p.rem) * size_t(p.chunks) * BM * size_t(bn); }
 
-template <int WP>
+template <int WP, bool SC>
 void launch_gemm(hipStream_t s, int bn, dim3 grid, float* y, float* work, const __bf16* xp, const __bf16* wp,
                  const Plan& p) {
     if (bn == 256)
-        hipLaunchKernelGGL((gemm_p3_kernel<4, WP>), grid, dim3(256), 0, s, y, work, xp, wp, p);
+        hipLaunchKernelGGL((gemm_p3_kernel<4, WP, SC>), grid, dim3(256), 0, s, y, work, xp, wp, p);
     else
-        hipLaunchKernelGGL((gemm_p3_kernel<2, WP>), grid, dim3(256), 0, s, y, work, xp, wp, p);
+        hipLaunchKernelGGL((gemm_p3_kernel<2, WP, SC>), grid, dim3(256), 0, s, y, work, xp, wp, p);
 }
 
 }  // namespace
@@ -586,6 +630,17 @@ int p1_from_bf16(hipStream_t s, __bf16* out, const void* packed, int rows, int c
     return int(hipGetLastError());
 }
 
+int p1_from_i8(hipStream_t s, __bf16* out, const void* packed, int rows, int cols) {
+    const int8_t* values = reinterpret_cast<const int8_t*>(static_cast<const float*>(packed) + rows);
+    if (rows < 1 || !p3_cols_ok(cols) || reinterpret_cast<uintptr_t>(values) % 8 != 0 ||
+        reinterpret_cast<uintptr_t>(out) % 16 != 0)
+        return int(hipErrorInvalidValue);
+    const long chunks = long(p3_rows(rows)) * (cols / 8), blocks = (chunks + 255) / 256;
+    hipLaunchKernelGGL(p1_from_i8_kernel, dim3(unsigned(blocks < 65536 ? blocks : 65536)), dim3(256), 0, s, out,
+                       values, rows, cols, chunks);
+    return int(hipGetLastError());
+}
+
 int p3_glu_interleave(hipStream_t s, __bf16* out, const __bf16* gate, const __bf16* up, int rows, int cols,
                       int planes) {
     if (rows < 128 || rows % 128 != 0 || !p3_cols_ok(cols) || (planes != 3 && planes != 1) ||
@@ -610,18 +665,21 @@ size_t p3_glu_scratch(int M, int rows, int K, int wplanes) {
 }
 
 int p3_gemm(hipStream_t s, float* y, const __bf16* xp, const __bf16* wp, int M, int N, int K, float* work,
-            size_t work_len, int wplanes) {
-    if (M < 1 || N < 1 || !p3_cols_ok(K) || (wplanes != 3 && wplanes != 1) ||
+            size_t work_len, int wplanes, const float* scale) {
+    if (M < 1 || N < 1 || !p3_cols_ok(K) || (wplanes != 3 && wplanes != 1) || (scale && wplanes != 1) ||
         ((reinterpret_cast<uintptr_t>(xp) | reinterpret_cast<uintptr_t>(wp)) % 16))
         return int(hipErrorInvalidValue);
     const int bn = plain_bn(M, N, K, wplanes);
-    const Plan p = make_plan(M, N, K, bn, wplanes);
+    Plan p = make_plan(M, N, K, bn, wplanes);
+    p.scale = scale;
     if (p.rem > 0 && (!work || work_len < scratch_of(p, bn))) return int(hipErrorInvalidValue);
     const dim3 grid{unsigned(p.full_grid + p.rem * p.chunks)}, block{256u};
     if (wplanes == 3)
-        launch_gemm<3>(s, bn, grid, y, work, xp, wp, p);
+        launch_gemm<3, false>(s, bn, grid, y, work, xp, wp, p);
+    else if (scale)
+        launch_gemm<1, true>(s, bn, grid, y, work, xp, wp, p);
     else
-        launch_gemm<1>(s, bn, grid, y, work, xp, wp, p);
+        launch_gemm<1, false>(s, bn, grid, y, work, xp, wp, p);
     if (p.rem > 0) {
         const long n = long(p.rem) * BM * bn / 4;
         if (bn == 256)
@@ -633,18 +691,23 @@ int p3_gemm(hipStream_t s, float* y, const __bf16* xp, const __bf16* wp, int M, 
 }
 
 int p3_gemm_glu(hipStream_t s, float* product, __bf16* planes, const __bf16* xp, const __bf16* wglu, int M, int rows,
-                int K, float* work, size_t work_len, int wplanes) {
+                int K, float* work, size_t work_len, int wplanes, const float* scale_gate, const float* scale_up) {
     if (M < 1 || rows < 128 || rows % 128 != 0 || !p3_cols_ok(K) || (wplanes != 3 && wplanes != 1) ||
+        (!scale_gate != !scale_up) || (scale_gate && wplanes != 1) ||
         ((reinterpret_cast<uintptr_t>(xp) | reinterpret_cast<uintptr_t>(wglu) | reinterpret_cast<uintptr_t>(product) |
           reinterpret_cast<uintptr_t>(planes)) % 16))
         return int(hipErrorInvalidValue);
-    const Plan p = make_plan(M, 2 * rows, K, 256, wplanes);
+    Plan p = make_plan(M, 2 * rows, K, 256, wplanes);
+    p.scale = scale_gate;
+    p.scale_up = scale_up;
     if (p.rem > 0 && (!work || work_len < scratch_of(p, 256))) return int(hipErrorInvalidValue);
     const dim3 grid{unsigned(p.full_grid + p.rem * p.chunks)}, block{256u};
     if (wplanes == 3)
-        hipLaunchKernelGGL(gemm_p3_glu_kernel<3>, grid, block, 0, s, product, planes, work, xp, wglu, p);
+        hipLaunchKernelGGL((gemm_p3_glu_kernel<3, false>), grid, block, 0, s, product, planes, work, xp, wglu, p);
+    else if (scale_gate)
+        hipLaunchKernelGGL((gemm_p3_glu_kernel<1, true>), grid, block, 0, s, product, planes, work, xp, wglu, p);
     else
-        hipLaunchKernelGGL(gemm_p3_glu_kernel<1>, grid, block, 0, s, product, planes, work, xp, wglu, p);
+        hipLaunchKernelGGL((gemm_p3_glu_kernel<1, false>), grid, block, 0, s, product, planes, work, xp, wglu, p);
     if (p.rem > 0) {
         const long n = long(p.rem) * BM * 16;
         hipLaunchKernelGGL(p3_glu_sum_kernel, dim3(unsigned((n + 255) / 256)), block, 0, s, product, planes, work, p);

@@ -111,6 +111,7 @@ struct Api {
     int (*embed_rows)(Context*, float*, const float*, int, int, int, const int32_t*, int) = nullptr;
     int (*gemm_f32_prepare)(Context*, const float*, int, int) = nullptr;
     int (*gemm_bf16_prepare)(Context*, const float*, int, int) = nullptr;
+    int (*gemm_i8_prepare)(Context*, const float*, int, int) = nullptr;
     int (*profile)(Context*, int) = nullptr;
     long (*profile_read)(Context*, char*, size_t) = nullptr;
     int (*sync_)(Context*) = nullptr;
@@ -191,6 +192,7 @@ struct Api {
         if (!(disable & QE_NO_PREPARED_GEMM)) {
             gemm_f32_prepare = symbol<decltype(gemm_f32_prepare)>("qr_gemm_f32_prepare", false);
             gemm_bf16_prepare = symbol<decltype(gemm_bf16_prepare)>("qr_gemm_bf16_prepare", false);
+            gemm_i8_prepare = symbol<decltype(gemm_i8_prepare)>("qr_gemm_i8_prepare", false);
         }
         profile = symbol<decltype(profile)>("qr_profile", false);
         profile_read = symbol<decltype(profile_read)>("qr_profile_read", false);
@@ -1299,14 +1301,16 @@ QeModel* qe_model_load(const char* bridge_path, int expect_kind, const QwConfig*
             b.up = DeviceMatrix::make(a, t[QW_UP], I, H, format);
             b.down = DeviceMatrix::make(a, t[QW_DOWN], H, I, format);
             // the prefill projections' planes (optional bridge symbols): every
-            // fp32 or BF16 block matrix of more than 16 rows with 4-aligned
-            // columns (the a / b rows have a kernel of their own)
+            // fp32, BF16 or int8 block matrix of more than 16 rows with
+            // 4-aligned columns (the a / b rows have a kernel of their own)
             for (const DeviceMatrix* dm : {&b.q, &b.k, &b.v, &b.o, &b.qkv, &b.z, &b.out, &b.gate, &b.up, &b.down}) {
                 if (!dm->buffer.p || dm->rows <= 16 || dm->cols % 4 != 0) continue;
                 if (dm->f32() && a->gemm_f32_prepare)
                     a->check(a->gemm_f32_prepare(a->ctx, dm->buffer.p, int32(dm->rows), int32(dm->cols)));
                 else if (dm->bf16 && a->gemm_bf16_prepare)
                     a->check(a->gemm_bf16_prepare(a->ctx, dm->buffer.p, int32(dm->rows), int32(dm->cols)));
+                else if (dm->int8 && a->gemm_i8_prepare)
+                    a->check(a->gemm_i8_prepare(a->ctx, dm->buffer.p, int32(dm->rows), int32(dm->cols)));
             }
             m->blocks.push_back(std::move(b));
         }

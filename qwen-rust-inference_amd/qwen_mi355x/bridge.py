@@ -157,9 +157,10 @@ class Bridge:
                        batch))
 
     def prepare(self, a: Buffer, rows: int, cols: int, kind: str = "f32"):
-        """qr_gemm_f32_prepare (qr_gemm_bf16_prepare for kind "bf16"): keep a's
-        planes for the prefill projections."""
-        fn = self.L.qr_gemm_f32_prepare if kind == "f32" else self.L.qr_gemm_bf16_prepare
+        """qr_gemm_f32_prepare (qr_gemm_bf16_prepare / qr_gemm_i8_prepare for kind
+        "bf16" / "i8"): keep a's planes for the prefill projections."""
+        fn = {"f32": self.L.qr_gemm_f32_prepare, "bf16": self.L.qr_gemm_bf16_prepare,
+              "i8": self.L.qr_gemm_i8_prepare}[kind]
         self._check(fn(self.ctx, ctypes.c_void_p(a.ptr), rows, cols))
 
     def release(self, a: Buffer):

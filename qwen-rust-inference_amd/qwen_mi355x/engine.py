@@ -43,7 +43,7 @@ BRIDGE_SYMBOLS = [
     "qr_gemm_f32_group", "qr_gemm_f32_glu", "qr_gemm_f32_add_norm", "qr_profile", "qr_profile_read",
     "qr_decode_plan", "qr_decode_step", "qr_decode_steps", "qr_decode_step_row", "qr_decode_plan_free",
     "qr_embed_rows", "qr_argmax_fixed", "qr_gemm_f32_prepare", "qr_gemm_f32_release", "qr_decode_rows",
-    "qr_decode_step_capture", "qr_decode_accept", "qr_gemm_bf16_prepare",
+    "qr_decode_step_capture", "qr_decode_accept", "qr_gemm_bf16_prepare", "qr_gemm_i8_prepare",
 ]
 
 _F = ctypes.POINTER(ctypes.c_float)

@@ -256,42 +256,54 @@ def test_prepared_group_glu_and_invalidation(gpu):
     gpu.release(mats[1])  # releasing twice (or an unprepared matrix) is accepted
 
 
+def _bf16_or_i8(kind, w, rows, cols):
+    """(packed upload, exact values as a float64 matrix, per-row scales)."""
+    if kind == "bf16":
+        dense = ((w.view(np.uint32) >> 16) << 16).view(np.float32)  # the values pack_bf16 keeps
+        return pack_bf16(w), dense.reshape(rows, cols).astype(np.float64), np.ones(rows)
+    sc, q = O.quantize_int8_rows(w, rows, cols)
+    return pack_int8(sc, q), q.reshape(rows, cols).astype(np.float64), sc.astype(np.float64)
+
+
+@pytest.mark.parametrize("kind", ["bf16", "i8"])
 @pytest.mark.parametrize("rows,cols,batch", [(6144, 1024, 2644), (1024, 3584, 130), (3584, 1024, 257),
                                             (512, 1024, 454), (1024, 2048, 64), (48, 1024, 200), (96, 32, 130),
                                             (4096, 1024, 10240)])
-def test_gemm_bf16_prepared(gpu, rows, cols, batch):
-    """qr_gemm_bf16_prepare: the projection of a prepared BF16 matrix (its one
-    plane in fragment order, three part products x_p w on the P3 kernels:
-    whole tiles, K-split tiles, 128- and 256-row weight tiles) against fp64
-    over the matrix's BF16 values with the fp32 dot-product bound on sampled
-    rows (the last among them), twice bitwise-equal, and within the bound of
-    the unprepared split-BF16 kernel's result."""
-    print(f"gemm bf16 prepared {rows}x{cols} batch {batch}", flush=True)
+def test_gemm_bf16_prepared(gpu, kind, rows, cols, batch):
+    """qr_gemm_bf16_prepare / qr_gemm_i8_prepare: the projection of a prepared
+    BF16 or int8 matrix (one plane of its exact values in fragment order,
+    three part products x_p w on the plane kernels: whole tiles, K-split
+    tiles, 128- and 256-row weight tiles; int8 rows scaled after the sum)
+    against fp64 over the matrix's values with the fp32 dot-product bound on
+    sampled rows (the last among them), twice bitwise-equal, and within the
+    bound of the unprepared split-BF16 kernel's result."""
+    print(f"gemm {kind} prepared {rows}x{cols} batch {batch}", flush=True)
     rng = np.random.default_rng(rows + 5 * cols + batch)
     w = (rng.standard_normal(rows * cols) * 0.02).astype(np.float32)
-    dense = ((w.view(np.uint32) >> 16) << 16).view(np.float32)  # the values pack_bf16 keeps
+    packed, W, scales = _bf16_or_i8(kind, w, rows, cols)
     x = rng.standard_normal(batch * cols).astype(np.float32)
-    a, xb = gpu.upload(pack_bf16(w)), gpu.upload(x)
+    a, xb = gpu.upload(packed), gpu.upload(x)
     plain, y1, y2 = gpu.alloc(batch * rows), gpu.alloc(batch * rows), gpu.alloc(batch * rows)
-    gpu.gemm(plain, a, xb, rows, cols, batch, kind="bf16")
-    gpu.prepare(a, rows, cols, kind="bf16")
-    gpu.gemm(y1, a, xb, rows, cols, batch, kind="bf16")
-    gpu.gemm(y2, a, xb, rows, cols, batch, kind="bf16")
+    gpu.gemm(plain, a, xb, rows, cols, batch, kind=kind)
+    gpu.prepare(a, rows, cols, kind=kind)
+    gpu.gemm(y1, a, xb, rows, cols, batch, kind=kind)
+    gpu.gemm(y2, a, xb, rows, cols, batch, kind=kind)
     got = y1.read().reshape(batch, rows)
     assert np.array_equal(got, y2.read().reshape(batch, rows))
     idx = np.unique(np.append(np.random.default_rng(0).integers(0, batch, 64), batch - 1))
-    X, W = x.reshape(batch, cols)[idx].astype(np.float64), dense.reshape(rows, cols).astype(np.float64)
-    want = X @ W.T
-    bound = np.abs(X) @ np.abs(W.T) * 2e-5 + 1e-30
+    X = x.reshape(batch, cols)[idx].astype(np.float64)
+    want = (X @ W.T) * scales[None, :]
+    bound = (np.abs(X) @ np.abs(W.T)) * np.abs(scales)[None, :] * 2e-5 + 1e-30
     assert np.all(np.abs(got[idx] - want) <= bound), np.max(np.abs(got[idx] - want) / bound)
     other = plain.read().reshape(batch, rows)[idx]
     assert np.all(np.abs(got[idx] - other) <= 2 * bound)
 
 
-def test_prepared_bf16_group_glu_and_invalidation(gpu):
-    """Prepared BF16 matrices in a group equal their separate prepared
+@pytest.mark.parametrize("kind", ["bf16", "i8"])
+def test_prepared_bf16_group_glu_and_invalidation(gpu, kind):
+    """Prepared BF16 (int8) matrices in a group equal their separate prepared
     projections bitwise (the 16-row a / b matrices unprepared beside them); a
-    prepared BF16 GLU (gate and up in one kernel over their interleaved planes
+    prepared BF16 (int8: the rows' scales after the sums) GLU (gate and up in one kernel over their interleaved planes
     with the silu product; rows % 128 != 0: two prepared projections and the
     silu product) follows the separate projections to the fp32 bound, gate_y /
     up_y untouched by the fused form; a qr_write into a prepared matrix drops
@@ -300,40 +312,40 @@ def test_prepared_bf16_group_glu_and_invalidation(gpu):
     cols, batch = 1024, 300
     shapes = [6144, 2048, 16, 16]
     ws = [(rng.standard_normal(r * cols) * 0.02).astype(np.float32) for r in shapes]
-    mats = [gpu.upload(pack_bf16(w)) for w in ws]
+    mats = [gpu.upload(_bf16_or_i8(kind, w, r, cols)[0]) for w, r in zip(ws, shapes)]
     for m, r in zip(mats, shapes):
         if r > 16:
-            gpu.prepare(m, r, cols, kind="bf16")
+            gpu.prepare(m, r, cols, kind=kind)
     x = gpu.upload(rng.standard_normal(batch * cols).astype(np.float32))
     ys = [gpu.alloc(batch * r) for r in shapes]
-    gpu.group(list(zip(ys, mats, shapes)), x, cols, batch, kind="bf16")
+    gpu.group(list(zip(ys, mats, shapes)), x, cols, batch, kind=kind)
     for y, m, r in zip(ys, mats, shapes):
         one = gpu.alloc(batch * r)
-        gpu.gemm(one, m, x, r, cols, batch, kind="bf16")
+        gpu.gemm(one, m, x, r, cols, batch, kind=kind)
         assert np.array_equal(y.read(), one.read()), r
     for rows in (3584, 320):
         gw, uw = [(rng.standard_normal(rows * cols) * 0.02).astype(np.float32) for _ in range(2)]
-        g, u = gpu.upload(pack_bf16(gw)), gpu.upload(pack_bf16(uw))
-        gpu.prepare(g, rows, cols, kind="bf16")
-        gpu.prepare(u, rows, cols, kind="bf16")
+        g, u = gpu.upload(_bf16_or_i8(kind, gw, rows, cols)[0]), gpu.upload(_bf16_or_i8(kind, uw, rows, cols)[0])
+        gpu.prepare(g, rows, cols, kind=kind)
+        gpu.prepare(u, rows, cols, kind=kind)
         prod, gy, uy = gpu.alloc(batch * rows), gpu.alloc(batch * rows), gpu.alloc(batch * rows)
-        gpu.glu(prod, gy, uy, g, u, x, rows, cols, batch, kind="bf16")
+        gpu.glu(prod, gy, uy, g, u, x, rows, cols, batch, kind=kind)
         g1, u1 = gpu.alloc(batch * rows), gpu.alloc(batch * rows)
-        gpu.gemm(g1, g, x, rows, cols, batch, kind="bf16")
-        gpu.gemm(u1, u, x, rows, cols, batch, kind="bf16")
+        gpu.gemm(g1, g, x, rows, cols, batch, kind=kind)
+        gpu.gemm(u1, u, x, rows, cols, batch, kind=kind)
         if rows % 128 == 0:
             assert not gy.read().any() and not uy.read().any()  # untouched
         gv, uv = g1.read().astype(np.float64), u1.read().astype(np.float64)
-        parity(prod.read(), gv / (1 + np.exp(-gv)) * uv, where=f"prepared bf16 glu {rows}")
+        parity(prod.read(), gv / (1 + np.exp(-gv)) * uv, where=f"prepared {kind} glu {rows}")
     # rewrite the first matrix: its plane is dropped, the projection follows the new weights
     new = (rng.standard_normal(shapes[0] * cols) * 0.02).astype(np.float32)
-    mats[0].write(pack_bf16(new))
+    packed, W, sc = _bf16_or_i8(kind, new, shapes[0], cols)
+    mats[0].write(packed)
     y = gpu.alloc(batch * shapes[0])
-    gpu.gemm(y, mats[0], x, shapes[0], cols, batch, kind="bf16")
+    gpu.gemm(y, mats[0], x, shapes[0], cols, batch, kind=kind)
     X = x.read().reshape(batch, cols)[:16].astype(np.float64)
-    W = ((new.view(np.uint32) >> 16) << 16).view(np.float32).reshape(shapes[0], cols).astype(np.float64)
-    bound = np.abs(X) @ np.abs(W.T) * 2e-5 + 1e-30
-    assert np.all(np.abs(y.read().reshape(batch, shapes[0])[:16] - X @ W.T) <= bound)
+    bound = (np.abs(X) @ np.abs(W.T)) * np.abs(sc)[None, :] * 2e-5 + 1e-30
+    assert np.all(np.abs(y.read().reshape(batch, shapes[0])[:16] - (X @ W.T) * sc[None, :]) <= bound)
     gpu.release(mats[1])
 
 
