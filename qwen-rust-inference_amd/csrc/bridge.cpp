@@ -799,7 +799,9 @@ static int prepare_p1(Context* c, qr::WeightType t, const float* packed, int row
     ++c->serial;
     if (!packed || rows < 1 || cols < 1 || reinterpret_cast<uintptr_t>(packed) % 16 != 0)
         return fail(c, "GEMM prepare shape", -1);
-    if (!qr::p3_cols_ok(cols)) return 0;  // no plane: its projections keep the split-BF16 kernel
+    // no plane (its projections keep the split-BF16 kernel) for other widths, and for int8
+    // values that the odd count of scales before them leaves off 8-byte alignment
+    if (!qr::p3_cols_ok(cols) || (t == qr::WeightType::I8 && rows % 2 != 0)) return 0;
     auto it = c->prepared.find(packed);
     if (it != c->prepared.end()) {
         if (it->second.rows == rows && it->second.cols == cols && it->second.kind == t) return 0;

@@ -268,12 +268,14 @@ def _bf16_or_i8(kind, w, rows, cols):
 @pytest.mark.parametrize("kind", ["bf16", "i8"])
 @pytest.mark.parametrize("rows,cols,batch", [(6144, 1024, 2644), (1024, 3584, 130), (3584, 1024, 257),
                                             (512, 1024, 454), (1024, 2048, 64), (48, 1024, 200), (96, 32, 130),
-                                            (4096, 1024, 10240)])
+                                            (4096, 1024, 10240), (37, 64, 70)])
 def test_gemm_bf16_prepared(gpu, kind, rows, cols, batch):
     """qr_gemm_bf16_prepare / qr_gemm_i8_prepare: the projection of a prepared
     BF16 or int8 matrix (one plane of its exact values in fragment order,
     three part products x_p w on the plane kernels: whole tiles, K-split
-    tiles, 128- and 256-row weight tiles; int8 rows scaled after the sum)
+    tiles, 128- and 256-row weight tiles; int8 rows scaled after the sum; an
+    odd-row int8 matrix, whose values sit off 8-byte alignment, keeps the
+    split-BF16 kernel)
     against fp64 over the matrix's values with the fp32 dot-product bound on
     sampled rows (the last among them), twice bitwise-equal, and within the
     bound of the unprepared split-BF16 kernel's result."""
