@@ -231,6 +231,8 @@ def main():
                          "for rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")
     ap.add_argument("--only-prefill", type=int, default=0, metavar="N",
                     help="profiling mode: only two N-token prefills (one chunk, fresh runs) and a one-line summary")
+    ap.add_argument("--prefill-format", choices=["f32", "bf16", "int8"], default="f32",
+                    help="with --only-prefill: the matrices' format (BF16: every tensor rounded to BF16)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
@@ -249,7 +251,10 @@ def main():
     t0 = time.time()
     w = M.synthetic_weights(c, seed=0)
     log(f"weights synthesised in {time.time() - t0:.1f} s ({w.matrix_bytes() / 1e9:.3f} GB of matrices)")
-    model = E.Model(w)
+    if args.only_prefill > 0 and args.prefill_format != "f32":
+        model = E.Model(M.bf16_weights(w), fmt=E.BF16_EXACT) if args.prefill_format == "bf16" else E.Model(w, fmt=E.INT8)
+    else:
+        model = E.Model(w)
     log(model.info)
     model.set_run_budget(64 << 30)
     weight_bytes = w.matrix_bytes()
@@ -264,8 +269,8 @@ def main():
             r2.prefill(ids2)
             times.append(time.perf_counter() - t)
             r2.close()
-        print(json.dumps({"mode": "only-prefill", "tokens": n, "prefill_ms": [round(x * 1e3, 2) for x in times]}),
-              flush=True)
+        print(json.dumps({"mode": "only-prefill", "format": args.prefill_format, "tokens": n,
+                          "prefill_ms": [round(x * 1e3, 2) for x in times]}), flush=True)
         model.close()
         return
     prompt = [int(v) for v in np.random.default_rng(4).integers(0, c.vocab_size, args.prompt)]
