@@ -602,10 +602,14 @@ def test_embed_rows(gpu, width, n):
 
 
 @pytest.mark.parametrize("k,tokens,snaps", [(4, 1, 0), (4, 5, 0), (4, 4, 3), (3, 2, 1), (1, 1, 0),
-                                             (4, 37, 5), (4, 130, 0), (3, 9, 8), (1, 7, 2), (17, 6, 2), (4, 33, 33)])
+                                             (4, 37, 5), (4, 130, 0), (3, 9, 8), (1, 7, 2), (17, 6, 2), (4, 33, 33),
+                                             (4, 21, 2)])
 def test_conv_silu(gpu, cpu, k, tokens, snaps):
+    """ConvSilu: one thread per channel walking the tokens (<= 4 tokens), the
+    16-token window kernel over prefill chunks (6146 channels: a ragged last
+    block), snapshots of the history per token."""
     rng = np.random.default_rng(k * 10 + tokens)
-    ch = 6144 if k == 4 else 24
+    ch = (6146 if tokens == 21 else 6144) if k == 4 else 24
     x, w, h = rnd(rng, tokens * ch), rnd(rng, ch * k, 0.5), rnd(rng, ch * max(k - 1, 1) * (1 + snaps))
     g, c = both(gpu, cpu, "CONV_SILU", ch, {1: x, 2: w, 3: h}, {0: tokens * ch, 3: h.size}, [k, tokens, ch, snaps])
     parity(g[0], c[0], where="conv out")
