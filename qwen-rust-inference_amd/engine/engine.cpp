@@ -961,6 +961,36 @@ struct QeRun {
         out.swap(picked);
         return out;
     }
+    // Whether greedy steps from the current position can run as chained
+    // one-launch steps (forward's one-launch conditions, nothing pending);
+    // chained_greedy refuses a count past the run's capacity before any launch.
+    bool can_chain() const {
+        return plan && edits.empty() && api()->decode_steps && snapshot_rows == 0 && pick_slot == 0;
+    }
+    // `count` greedy steps from token `first` at the current position, queued
+    // back to back with one read-back: next[i] is the pick after step i (the
+    // token step i + 1 feeds). Seconds of the call.
+    double chained_greedy(uint32_t first, size_t count, uint32_t* next) {
+        const Api* a = api();
+        require(!failed, "device run failed; reset required");
+        require(first < uint32_t(model->config.vocab_size) && position + count <= capacity,
+                "device token/capacity out of bounds");
+        std::vector<int32_t> got(count);
+        float bad = 0.f;
+        pending.reset();
+        auto t0 = std::chrono::steady_clock::now();
+        const int st = a->decode_steps(a->ctx, plan, int(first), int(position), int(count), got.data(), &bad);
+        const double total = std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
+        position += count;
+        logits_unread = true;
+        if (st != 0 || bad != 0.f) failed = true;
+        a->check(st);
+        require(bad < 1e30f, "one-launch decode step timed out at a stage barrier");
+        require(bad == 0.f, "non-finite logits");
+        for (size_t i = 0; i < count; ++i) next[i] = uint32_t(got[i]);
+        picked = {next[count - 1]};
+        return total;
+    }
     // accept (src/device.rs:1626-1662)
     void accept(size_t rows) {
         require(pending.has_value(), "accept needs a verify_rollback pass");
@@ -1583,6 +1613,12 @@ int qe_speculative_generate(QeRun* r, const QeDraft* draft, const uint32_t* prom
         auto is_eos = [&](uint32_t id) { return std::find(eos, eos + std::max<int64_t>(n_eos, 0), id) != eos + std::max<int64_t>(n_eos, 0); };
         int64_t n = 0;
         *n_out = 0;
+        // Empty drafts in a row: with no end-of-sequence token to stop at, the
+        // next pass after one runs a burst of chained greedy steps (2, 4, then
+        // 8 tokens) instead of one verify row, and the draft absorbs them all;
+        // the output is the same greedy sequence, with fewer host reads.
+        int64_t empty = 0;
+        constexpr int64_t kMaxBurst = 8;
         if (max_new > 0) {
             auto t = clock::now();
             auto logits = r->prefill(prompt, size_t(n_prompt));
@@ -1607,6 +1643,25 @@ int qe_speculative_generate(QeRun* r, const QeDraft* draft, const uint32_t* prom
                 const int64_t got = k > 0 ? draft->draft(draft->user, k, rows.data() + 1) : 0;
                 st.draft_s += secs(t);
                 require(got >= 0 && got <= k, "speculative: draft failed");
+                const int64_t burst = n_eos > 0 || got > 0 ? 1 : std::min<int64_t>(kMaxBurst, int64_t(1) << std::min<int64_t>(empty, 3));
+                empty = got > 0 ? 0 : empty + 1;
+                if (burst > 1 && std::min(burst, room) > 1 && r->can_chain()) {
+                    const int64_t b = std::min(burst, room);
+                    std::vector<uint32_t> emitted(static_cast<size_t>(b));
+                    t = clock::now();
+                    r->chained_greedy(cur, size_t(b), emitted.data());
+                    st.verify_s += secs(t);
+                    st.passes += 1;
+                    t = clock::now();
+                    require(draft->absorb(draft->user, emitted.data(), int64_t(emitted.size())) == 0,
+                            "speculative: draft absorb failed");
+                    st.draft_s += secs(t);
+                    for (uint32_t id : emitted) {
+                        out[n++] = id;
+                        cur = id;
+                    }
+                    continue;
+                }
                 for (int64_t j = 1; j <= got; ++j)
                     require(rows[size_t(j)] < uint32_t(r->model->config.vocab_size), "speculative: draft token out of range");
                 rows.resize(size_t(got) + 1);
@@ -1748,27 +1803,9 @@ int qe_decode_greedy(QeRun* r, uint32_t first, int64_t n_new, uint32_t* ids, dou
         uint32_t token = first;
         // the planned steps of step_greedy (forward's one-launch conditions),
         // queued back to back with one read-back
-        if (n_new > 1 && r->plan && r->edits.empty() && r->api()->decode_steps && r->snapshot_rows == 0 &&
-            r->pick_slot == 0) {
-            const Api* a = r->api();
-            require(!r->failed, "device run failed; reset required");
-            require(first < uint32_t(r->model->config.vocab_size) && r->position + size_t(n_new - 1) <= r->capacity,
-                    "device token/capacity out of bounds");
-            std::vector<int32_t> got(size_t(n_new - 1));
-            float bad = 0.f;
-            r->pending.reset();
-            auto t0 = std::chrono::steady_clock::now();
-            const int st = a->decode_steps(a->ctx, r->plan, int(first), int(r->position), int(n_new - 1), got.data(), &bad);
-            total = std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
-            r->position += size_t(n_new - 1);
-            r->logits_unread = true;
-            if (st != 0 || bad != 0.f) r->failed = true;
-            a->check(st);
-            require(bad < 1e30f, "one-launch decode step timed out at a stage barrier");
-            require(bad == 0.f, "non-finite logits");
+        if (n_new > 1 && r->can_chain()) {
             ids[0] = first;
-            for (size_t i = 0; i < got.size(); ++i) ids[i + 1] = uint32_t(got[i]);
-            r->picked = {ids[n_new - 1]};
+            total = r->chained_greedy(first, size_t(n_new - 1), ids + 1);
             if (seconds) *seconds = total;
             return;
         }
