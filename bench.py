@@ -234,6 +234,8 @@ def main():
     ap.add_argument("--prefill-format", choices=["f32", "bf16", "int8"], default="f32",
                     help="with --only-prefill: the matrices' format (BF16: every tensor rounded to BF16)")
     args = ap.parse_args()
+    if args.profile_steps < 1:
+        ap.error("--profile-steps must be at least 1 (the roofline's per-launch time comes from them)")
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
               "the path's sharding is described in DESIGN.md", file=sys.stderr)
