@@ -47,6 +47,9 @@ struct Context {
         }
     };
     std::map<const float*, Prepared> prepared;
+    // Words of each qr_alloc allocation, so that qr_free drops the planes of
+    // any prepared matrix inside the freed range, not only one at its start.
+    std::map<const float*, size_t> allocs;
     // A prepared GLU's combined gate / up planes (p3_glu_interleave), made on
     // the pair's first prefill GLU, so both projections and the silu product
     // run as one kernel; dropped with either matrix's planes.
@@ -628,12 +631,16 @@ int qr_alloc(Context* c, float** p, size_t n) {
         *p = nullptr;
         return fail(c, "hipMemsetAsync", int(s));
     }
+    c->allocs[*p] = n;
     return 0;
 }
 
 void qr_free(Context* c, float* p) {
     ++c->serial;
-    if (!c->prepared.empty()) invalidate_prepared(c, p, 1);
+    auto it = c->allocs.find(p);
+    const size_t n = it != c->allocs.end() ? it->second : 1;
+    if (it != c->allocs.end()) c->allocs.erase(it);
+    if (!c->prepared.empty()) invalidate_prepared(c, p, n);
     (void)hipFree(p);
 }
 

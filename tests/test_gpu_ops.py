@@ -256,6 +256,37 @@ def test_prepared_group_glu_and_invalidation(gpu):
     gpu.release(mats[1])  # releasing twice (or an unprepared matrix) is accepted
 
 
+@pytest.mark.gpu
+def test_prepared_inside_freed_allocation(gpu):
+    """A matrix prepared at an offset inside a larger allocation loses its planes
+    when that allocation is freed: a new allocation of the same size (the
+    runtime usually returns the same address), its values put there by a kernel
+    (an ADD, which drops no planes itself) and prepared again at the same
+    offset, is multiplied with the new values, not the old planes."""
+    import ctypes
+    rng = np.random.default_rng(23)
+    rows, cols, batch = 512, 1024, 128
+    off = rows * cols
+    x = gpu.upload(rng.standard_normal(batch * cols).astype(np.float32))
+    X = x.read().reshape(batch, cols).astype(np.float64)
+    y = gpu.alloc(batch * rows)
+    addrs = []
+    for rep in range(2):
+        w = (rng.standard_normal(rows * cols) * 0.02).astype(np.float32)
+        big = gpu.alloc(2 * off)
+        addrs.append(big.ptr)
+        wb, zero = gpu.upload(w), gpu.alloc(off)
+        gpu.run("ADD", off, p=(big.at(off), wb, zero))
+        inner = ctypes.c_void_p(big.at(off))
+        gpu._check(gpu.L.qr_gemm_f32_prepare(gpu.ctx, inner, rows, cols))
+        gpu._check(gpu.L.qr_gemm(gpu.ctx, ctypes.c_void_p(y.ptr), inner, ctypes.c_void_p(x.ptr), rows, cols, batch))
+        W = w.reshape(rows, cols).astype(np.float64)
+        bound = np.abs(X) @ np.abs(W.T) * 2e-5 + 1e-30
+        assert np.all(np.abs(y.read().reshape(batch, rows) - X @ W.T) <= bound), (rep, addrs)
+        del big  # qr_free of the whole allocation
+    print("allocation addresses", [hex(a) for a in addrs])
+
+
 def _bf16_or_i8(kind, w, rows, cols):
     """(packed upload, exact values as a float64 matrix, per-row scales)."""
     if kind == "bf16":
