@@ -125,34 +125,45 @@ __global__ __launch_bounds__(256) void rms_rows_kernel(int op, int groups, Param
     const int lane = int(threadIdx.x & 63), d = 64 * PER;
     const size_t off = size_t(g) * d;
     const float eps = a.f[0], offset = a.f[1];
-    fv x[NV];
-    float ss = 0.f;
+    // Every load of the row (input, the added input, norm weights, gate) is
+    // issued before the first store: with the stores in between, the compiler
+    // (which cannot rule out aliasing) waited for each 16-byte piece in turn.
+    const float* w = op == QR_ADD_RMS_NORM ? a.p[4] : a.p[2];
+    float* out = op == QR_ADD_RMS_NORM ? a.p[3] : a.p[0];
+    fv x[NV], x2[NV], wv[NV], z[NV];
+    const bool add = op == QR_ADD_RMS_NORM, gate = op == QR_RMS_NORM_GATE;
+    const float* x2p = add ? a.p[2] : a.p[1];  // the added input, else a second read of x (not used)
+    const float* zp = gate ? a.p[3] + off : w;  // the gate's z, else the weights again (not used)
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
         const size_t i = off + size_t(V) * (lane + 64 * j);
+        const int c = V * (lane + 64 * j);
         x[j] = *reinterpret_cast<const fv*>(a.p[1] + i);
-        if (op == QR_ADD_RMS_NORM) {
-            x[j] += *reinterpret_cast<const fv*>(a.p[2] + i);
-            *reinterpret_cast<fv*>(a.p[0] + i) = x[j];
+        x2[j] = *reinterpret_cast<const fv*>(x2p + i);
+        wv[j] = *reinterpret_cast<const fv*>(w + c);
+        z[j] = *reinterpret_cast<const fv*>(zp + c);
+    }
+    float ss = 0.f;
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        if (add) {
+            x[j] += x2[j];
+            *reinterpret_cast<fv*>(a.p[0] + off + size_t(V) * (lane + 64 * j)) = x[j];
         }
 #pragma unroll
         for (int e = 0; e < V; ++e) ss += x[j][e] * x[j][e];
     }
     ss = wave_sum(ss);
     const float r = 1.f / sqrtf(ss / float(d) + eps);
-    const float* w = op == QR_ADD_RMS_NORM ? a.p[4] : a.p[2];
-    float* out = op == QR_ADD_RMS_NORM ? a.p[3] : a.p[0];
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
         const int c = V * (lane + 64 * j);
-        const fv wv = *reinterpret_cast<const fv*>(w + c);
         fv y;
 #pragma unroll
-        for (int e = 0; e < V; ++e) y[e] = (x[j][e] * r) * (wv[e] + offset);
-        if (op == QR_RMS_NORM_GATE) {
-            const fv z = *reinterpret_cast<const fv*>(a.p[3] + off + c);
+        for (int e = 0; e < V; ++e) y[e] = (x[j][e] * r) * (wv[j][e] + offset);
+        if (gate) {
 #pragma unroll
-            for (int e = 0; e < V; ++e) y[e] = siluf_(z[e]) * y[e];
+            for (int e = 0; e < V; ++e) y[e] = siluf_(z[j][e]) * y[e];
         }
         *reinterpret_cast<fv*>(out + off + c) = y;
         if (planes) {
