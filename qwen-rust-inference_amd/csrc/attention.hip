@@ -166,7 +166,7 @@ template <int LANES>
 __global__ __launch_bounds__(256) void attention_combine_kernel(ReadArgs a) {
     typedef float f2v __attribute__((ext_vector_type(2)));
     typedef float f4v __attribute__((ext_vector_type(4)));
-    static_assert(LANES == 1 || LANES == 4, "one lane or a quad");
+    static_assert(LANES == 1 || LANES == 4 || LANES == 16, "one lane, a quad or 16 lanes");
     const long idx = blockIdx.x * long(blockDim.x) + threadIdx.x;
     const int q = a.d / 4;
     const long total = long(a.rows) * a.heads * q * LANES;  // whole quads: the shuffles see only live lanes
@@ -179,10 +179,8 @@ __global__ __launch_bounds__(256) void attention_combine_kernel(ReadArgs a) {
     float mm = -INFINITY;
 #pragma unroll 8
     for (int s = lq; s < a.splits; s += LANES) mm = fmaxf(mm, parts[size_t(s) * (a.d + 2)]);
-    if constexpr (LANES == 4) {
-        mm = fmaxf(mm, __shfl_xor(mm, 1, 64));
-        mm = fmaxf(mm, __shfl_xor(mm, 2, 64));
-    }
+#pragma unroll
+    for (int o = 1; o < LANES; o <<= 1) mm = fmaxf(mm, __shfl_xor(mm, o, 64));
     float den = 0.f;
     f4v num = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll 8
@@ -196,9 +194,9 @@ __global__ __launch_bounds__(256) void attention_combine_kernel(ReadArgs a) {
         num.z += hi.x * c;
         num.w += hi.y * c;
     }
-    if constexpr (LANES == 4) {
+    if constexpr (LANES > 1) {
 #pragma unroll
-        for (int o = 1; o <= 2; o <<= 1) {
+        for (int o = 1; o < LANES; o <<= 1) {
             den += __shfl_xor(den, o, 64);
             num.x += __shfl_xor(num.x, o, 64);
             num.y += __shfl_xor(num.y, o, 64);
@@ -216,10 +214,14 @@ __global__ __launch_bounds__(256) void attention_combine_kernel(ReadArgs a) {
     r.w = (num.w / den) * sigmoidf_(g.w);
     *reinterpret_cast<f4v*>(a.out + o) = r;
 }
-// Launch of the merge: quads from 16 splits on.
+// Launch of the merge: quads from 16 splits on, 16 lanes per group from 64
+// (a decode row has only rows x heads x d / 4 groups: 512 at the 0.8B shape,
+// so with one lane or a quad each lane walks many splits in turn).
 int launch_combine(hipStream_t s, const ReadArgs& a) {
     const long groups = long(a.rows) * a.heads * (a.d / 4);
-    if (a.splits >= 16)
+    if (a.splits >= 64)
+        hipLaunchKernelGGL(attention_combine_kernel<16>, dim3(ceil_div(groups * 16, 256)), dim3(256), 0, s, a);
+    else if (a.splits >= 16)
         hipLaunchKernelGGL(attention_combine_kernel<4>, dim3(ceil_div(groups * 4, 256)), dim3(256), 0, s, a);
     else
         hipLaunchKernelGGL(attention_combine_kernel<1>, dim3(ceil_div(groups, 256)), dim3(256), 0, s, a);
